@@ -1,0 +1,280 @@
+"""Benchmark of MI355X AttnRes routing: achieved HBM GB/s on the 3B prefill sweep.
+
+A step is one forward's routing work at the 3B prefill shape (workload cfg2):
+57 routing calls (S = 1..8 per the block schedule) over bf16 sources with
+B=8, T=4096, D=3072, sources resident in HBM.  ``value`` = algorithmic bytes
+of the step ((S+1) * B*T*D * 2 bytes per call, 68.05 GB) / step time.
+
+Also on the JSON line:
+* ``roofline`` — the dominant kernel (the S=8 routing kernel): its algorithmic
+  bytes per launch / its average launch time from HIP events around every
+  S=8 launch inside the timed region, against MI355X's 8 TB/s HBM peak;
+  ``traffic`` is the measured HBM bytes per launch from rocprofv3 FETCH_SIZE
+  + WRITE_SIZE counters when a committed summary holds them.
+* ``cpu_baseline`` — the reference's CPU routing path (oracle/torch_cpu_path:
+  the einsum-branch op sequence over the padded buffer, fp32) timed on this
+  host on a bounded sample (one call per distinct S at 2048 tokens),
+  extrapolated to the full step.
+
+``--workload cfg3|cfg4|cfg5`` measures the other shapes (cfg4 = 8B decode step,
+65 fused block steps captured in one HIP graph).  ``--gpus`` above 1 exits:
+this build measures one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "AttnRes routing achieved HBM GB/s (% of peak) and tokens/s, 3B/8B shapes"
+WORKLOAD_TEXT = {
+    "cfg2": "3B prefill sweep: D=3072, B=8, T=4096, 28 layers / 8 blocks, 57 routing calls S=1..8 (sum S=281), bf16 in, fp32 accumulate",
+    "cfg3": "8B deepest routing: D=4096, B=4, T=4096, S=9, 8 calls, bf16",
+    "cfg4": "8B decode step: T=1, B=256, D=4096, 65 fused block steps (S=1..9) in one HIP graph, bf16",
+    "cfg5": "3B data-driven blocks {0,3,7,12,18,23}: D=3072, B=2, T=4096, 57 calls S=1..7 (sum S=267), BOS x20, bf16",
+}
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOAD_TEXT))
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-tokens", type=int, default=2048, help="tokens per CPU-baseline sample call")
+    return ap.parse_args()
+
+
+def load_traffic(kernel_tag: str):
+    """Measured HBM bytes per launch of the dominant kernel, if profiled (profiles/traffic.json)."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None, None
+    try:
+        data = json.loads(p.read_text())
+        rec = data.get(kernel_tag)
+        if rec is None:
+            return None, None
+        return float(rec["bytes_per_launch"]), rec.get("source")
+    except (ValueError, KeyError, TypeError):
+        return None, None
+
+
+def cpu_baseline(w, tokens: int) -> dict:
+    """The reference's CPU path on a bounded sample, extrapolated to one step."""
+    import torch
+
+    from oracle import torch_cpu_path as TP
+
+    threads = torch.get_num_threads()
+    max_s = max(w.calls)
+    g = torch.Generator().manual_seed(0)
+    buf = torch.randn((max_s, 1, tokens, w.hidden), generator=g).to(torch.bfloat16).float()
+    qw = (torch.randn(w.hidden, generator=g) * w.w_std).to(w.dtype).float()
+    per_s = {}
+    for s in sorted(set(w.calls)):
+        mask = torch.zeros(max_s, dtype=torch.bool)
+        mask[:s] = True
+        TP.route_static_cpu(buf, qw, w.eps, mask)  # warm-up
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            TP.route_static_cpu(buf, qw, w.eps, mask)
+            ts.append(time.perf_counter() - t0)
+        per_s[s] = statistics.median(ts)
+    scale = w.tokens / tokens
+    step_s = sum(per_s[s] for s in w.calls) * scale
+    gbs = w.step_bytes() / step_s / 1e9
+    return {
+        "value": round(gbs, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"reference CPU op sequence (llama.py:640-644, fp32, padded max_S={max_s} buffer) timed once per "
+            f"distinct S at B=1,T={tokens} (median of 3), extrapolated x{scale:.0f} over the {len(w.calls)}-call "
+            f"schedule; step {step_s:.2f} s, {w.tokens / step_s:.0f} tok/s"
+        ),
+        "tokens_per_s": round(w.tokens / step_s, 1),
+    }
+
+
+def bench_sweep(w, steps: int, warmup: int, dev):
+    """Prefill sweep / single-point configs: one routing call per schedule entry."""
+    import torch
+
+    from kotodama_amd import ops, workloads
+
+    pool = workloads.make_pool(w, dev, seed=2)
+    q, gn = workloads.make_params(w, dev, seed=2, count=len(w.calls))
+    dominant = max(w.calls)
+    calls = list(enumerate(w.calls))
+
+    def step(events=None):
+        for j, s in calls:
+            if events is not None and s == dominant:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                ops.route(pool, s, q[j], gn[j], w.eps, w.dtype, False, False)
+                e1.record()
+                events.append((e0, e1))
+            else:
+                ops.route(pool, s, q[j], gn[j], w.eps, w.dtype, False, False)
+
+    with torch.inference_mode():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        events: list = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(events)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    dom_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in events)
+    return elapsed, dominant, dom_ms, w.call_bytes(dominant)
+
+
+def bench_decode(w, steps: int, warmup: int, dev):
+    """cfg4: one decode step = 65 fused block steps, captured in a HIP graph."""
+    import torch
+
+    from kotodama_amd import workloads
+    from kotodama_amd.engine import AttnResRouter
+
+    sched = w.schedule
+    L = sched.num_layers
+    embed = torch.randn((w.batch, 1, w.hidden), device=dev).to(w.dtype)
+    deltas = workloads.make_deltas(w, dev, 4, 2 * L)
+    q, gn = workloads.make_params(w, dev, 4, sched.num_points)
+    router = AttnResRouter(sched, list(q), list(gn), w.eps)
+    arena = router.new_arena((w.batch, 1), w.hidden, w.dtype, dev)
+    with torch.inference_mode():
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            router.forward(embed, lambda j, h: deltas[j], arena=arena)
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            router.forward(embed, lambda j, h: deltas[j], arena=arena)
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        events = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            graph.replay()
+            e1.record()
+            events.append((e0, e1))
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    step_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in events)
+    # algorithmic bytes of one decode step: (S+3) rows per fused point
+    # (S sources + delta read, partial + out written), 2 rows for the first point
+    rows = 2 + sum(s + 3 for s in sched.active_counts[1:])
+    return elapsed, rows * w.batch * w.hidden * w.elem_bytes, step_ms
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X (routing is "
+            "per-token and shards over B*T with no communication; see the design notes). Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    from kotodama_amd import workloads
+
+    dev = torch.device("cuda", 0)
+    w = workloads.get(args.workload)
+    roofline = None
+    if args.workload == "cfg4":
+        elapsed, step_bytes, graph_ms = bench_decode(w, args.steps, args.warmup, dev)
+        ms_per_step = elapsed * 1e3 / args.steps
+        gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+        tokens = w.batch
+        roofline = {
+            "bound": "hbm",
+            "achieved": round(step_bytes / (graph_ms * 1e-3) / 1e9, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(step_bytes / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "one decode step (65 attnres_route_bf_d2_s*_v1_q1 launches, HIP graph)",
+            "avg_ms": round(graph_ms, 4),
+        }
+    else:
+        elapsed, dominant, dom_ms, dom_bytes = bench_sweep(w, args.steps, args.warmup, dev)
+        ms_per_step = elapsed * 1e3 / args.steps
+        step_bytes = w.step_bytes()
+        gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+        tokens = w.tokens
+        tag = f"{args.workload}_s{dominant}"
+        traffic, traffic_src = load_traffic(tag)
+        achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+        roofline = {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": f"attnres_route_{'bf_d2' if w.dtype == torch.bfloat16 else 'f32_fm'}_s{dominant}_v2_q1",
+            "algorithmic_bytes": dom_bytes,
+            "avg_ms": round(dom_ms, 4),
+        }
+        if traffic_src:
+            roofline["traffic_source"] = traffic_src
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic (seeded N(0,1) sources x per-source log-uniform scales, resident in HBM)",
+        "config": {
+            "workload": WORKLOAD_TEXT[args.workload],
+            "hidden": w.hidden,
+            "batch": w.batch,
+            "seq": w.seq,
+            "routing_calls": len(w.calls),
+            "sum_S": sum(w.calls),
+            "algorithmic_bytes_per_step": step_bytes,
+        },
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "tokens_per_s": round(tokens / (ms_per_step * 1e-3), 1),
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(w, min(args.cpu_tokens, w.tokens)) if args.workload != "cfg4" else \
+            cpu_baseline(w, w.tokens)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

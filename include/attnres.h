@@ -1,0 +1,144 @@
+/*
+ * attnres.h — C ABI of the MI355X (gfx950) Block Attention Residual routing
+ * library, libattnres_hip.so.
+ *
+ * Plain pointers and sizes only: no torch or C++ types cross this boundary.
+ * Every device pointer is a HIP device address on the current HIP device;
+ * `stream` is a hipStream_t (NULL = the null stream).  Calls are asynchronous
+ * on `stream`, allocate nothing, keep no per-call state and never synchronise.
+ *
+ * Return value: ATTNRES_OK (0) or a negative ATTNRES_ERR_* code;
+ * attnres_last_error() then describes the failure (per thread).  Argument
+ * checks run before any HIP call, so a rejected call has no device effects.
+ *
+ * Routing semantics, for each token row t and query q (fp32 arithmetic):
+ *   qw       = query[q] * gain          (rounded to the parameter dtype)
+ *   inv_rms  = rsqrt(mean_d(x_s[t]^2) + eps)
+ *   logit_s  = (x_s[t] . qw) * inv_rms_s
+ *   w        = softmax_s(logit)          (over the S active sources)
+ *   out[q,t] = sum_s w_s * x_s[t]       (raw sources; rounded once to out dtype)
+ *   lse[q,t] = max_s logit_s + log(sum_s exp(logit_s - max))
+ * With S == 0 the softmax is over an empty set and every output is NaN.
+ */
+#ifndef ATTNRES_H
+#define ATTNRES_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+#define ATTNRES_DTYPE_F32 0
+#define ATTNRES_DTYPE_BF16 1
+
+/* status codes */
+#define ATTNRES_OK 0
+#define ATTNRES_ERR_ARG (-1)         /* null pointer, bad size or dtype, inconsistent arguments */
+#define ATTNRES_ERR_UNSUPPORTED (-2) /* shape outside what the kernels handle (S > 16, hidden) */
+#define ATTNRES_ERR_ALIGN (-3)       /* pointer or row stride not 16-byte aligned */
+#define ATTNRES_ERR_HIP (-4)         /* a HIP runtime call failed */
+
+/* Largest number of active sources one routing call accepts. */
+#define ATTNRES_MAX_SOURCES 16
+
+/* Library version, major*10000 + minor*100 + patch. */
+int attnres_version(void);
+
+/* ATTNRES_MAX_SOURCES. */
+int attnres_max_sources(void);
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* attnres_last_error(void);
+
+/*
+ * Load the gfx950 code object on the current HIP device.  Optional: the
+ * launch entry points call it on first use of a device.
+ */
+int attnres_init(void);
+
+/*
+ * One routing point: softmax over depth of S sources for num_tokens rows.
+ *
+ * Replaces LuxiaBaseModel._route_static (src/model/llama.py:605-644) — the
+ * einsum branch llama.py:640-644 and the Triton branch llama.py:633-638 — and
+ * the phase-1 op _phase_1_batched_attention_forward_with_aux
+ * (src/model/flash_attn_res/ops/phase_1.py:11-66, kernel
+ * kernels/phase_1.py:6-101) for num_queries >= 1.
+ *
+ *   sources     host array of num_sources device pointers; source s is a
+ *               (num_tokens, hidden) row block with row stride src_ld elements
+ *               (the reference's buf[s] for s < num_active; no stacked copy)
+ *   src_dtype   ATTNRES_DTYPE_BF16 or ATTNRES_DTYPE_F32
+ *   query       (num_queries, hidden), param_dtype
+ *   gain        (hidden,) RMSNorm gain folded into every query, param_dtype,
+ *               or NULL when `query` is already folded (phase-1 op contract)
+ *   eps         RMSNorm epsilon (norm.eps)
+ *   out         (num_queries, num_tokens, hidden) in out_dtype: row t of query q
+ *               at out + q*out_qstride + t*out_ld elements.  out_dtype is
+ *               either dtype: the einsum branch returns the promoted dtype of
+ *               the sources and qw (llama.py:641-644), the phase-1 op always
+ *               BF16 (ops/phase_1.py:26-30)
+ *   weights     (num_queries, num_sources, num_tokens) fp32, or NULL
+ *   lse         (num_queries, num_tokens) fp32, or NULL (ops/phase_1.py:32-36)
+ *   inv_rms     (num_tokens, num_sources) fp32, or NULL (ops/phase_1.py:38-42)
+ *   logits      (num_queries, num_tokens, num_sources) fp32, or NULL
+ *               (ops/phase_1.py:44-48)
+ * Requirements: 0 <= num_sources <= ATTNRES_MAX_SOURCES; hidden a multiple of
+ * 8 (bf16) or 4 (fp32) and at most 8192 (bf16) / 4096 (fp32); every row start
+ * 16-byte aligned.
+ */
+int attnres_route_fwd(const void* const* sources, int num_sources, int64_t num_tokens, int hidden,
+                      int64_t src_ld, int src_dtype, const void* query, const void* gain, int num_queries,
+                      int param_dtype, float eps, void* out, int out_dtype, int64_t out_ld, int64_t out_qstride,
+                      float* weights, float* lse, float* inv_rms, float* logits, void* stream);
+
+/*
+ * Phase-2 online-softmax merge of the intra-block partial into a phase-1
+ * result (one more source joined to a softmax already taken over the
+ * committed blocks):
+ *   inv_rms = rsqrt(mean(p^2) + eps); logit = (p . query) * inv_rms
+ *   pi = sigmoid(logit - inter_lse);   out = inter + pi * (p - inter)
+ * Replaces _phase_2_online_softmax_merge_forward_with_aux
+ * (src/model/flash_attn_res/ops/phase_2.py:27-71, kernel
+ * kernels/phase_2.py:9-57).  `query` is pre-folded (hidden,) param_dtype;
+ * partial, inter and out are contiguous (num_tokens, hidden); out has
+ * inter_dtype (ops/phase_2.py:41-45); logit and inv_rms (num_tokens,) fp32 or
+ * NULL.
+ */
+int attnres_merge_fwd(const void* partial, int64_t num_tokens, int hidden, int partial_dtype, const void* query,
+                      int param_dtype, const void* inter, int inter_dtype, const float* inter_lse, float eps,
+                      void* out, float* logit, float* inv_rms, void* stream);
+
+/*
+ * One routing point of the block schedule over a preallocated block arena,
+ * with the partial-block update fused in.  The arena holds num_slots slots of
+ * (num_tokens, hidden) rows, slot s at arena + s*slot_stride elements; slots
+ * 0..n_committed-1 are committed block summaries and slot n_committed is the
+ * running partial block.
+ *
+ *   commit == 0: partial := partial + delta (rounded to dtype; delta may be
+ *                NULL for no update); route over slots 0..n_committed.
+ *   commit == 1: the partial slot becomes committed block n_committed and a
+ *                new partial starts in slot n_committed+1 as `delta` (required);
+ *                route over slots 0..n_committed+1.
+ * The updated partial is written back to its slot; `out` (num_tokens, hidden)
+ * gets the routed row in `dtype`; weights/lse as in attnres_route_fwd, or NULL.
+ *
+ * Replaces one iteration step of the caller loops _forward_attn_res and
+ * _forward_attn_res_cached (src/model/llama.py:697-715 and 742-762):
+ * `_pad_and_stack` + `_route_static` + the block commit (`committed.append(
+ * partial.clone()); partial = zero.clone()`) + `partial = partial + out`,
+ * without the per-call stacked copy.  The caller tracks n_committed.
+ */
+int attnres_block_step(void* arena, int num_slots, int64_t slot_stride, int n_committed, int commit,
+                       const void* delta, int64_t num_tokens, int hidden, int dtype, const void* query,
+                       const void* gain, int param_dtype, float eps, void* out, float* weights, float* lse,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATTNRES_H */

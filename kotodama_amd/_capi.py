@@ -1,0 +1,183 @@
+"""ctypes binding of libattnres_hip.so (the C ABI in include/attnres.h).
+
+``torch`` is imported before the library is opened: the library needs
+``libamdhip64.so.7`` and the dynamic linker then binds it to the HIP runtime
+torch has already loaded, so torch streams and device pointers are valid in
+the library.  There is no fallback: if the library is missing, every call
+raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must be loaded first: shares its HIP runtime)
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libattnres_hip.so"
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+OK = 0
+ERR_ARG = -1
+ERR_UNSUPPORTED = -2
+ERR_ALIGN = -3
+ERR_HIP = -4
+
+MAX_SOURCES = 16
+
+_ERR_NAMES = {
+    ERR_ARG: "ATTNRES_ERR_ARG",
+    ERR_UNSUPPORTED: "ATTNRES_ERR_UNSUPPORTED",
+    ERR_ALIGN: "ATTNRES_ERR_ALIGN",
+    ERR_HIP: "ATTNRES_ERR_HIP",
+}
+
+# Exported symbols, in the order include/attnres.h declares them.
+EXPORTS = (
+    "attnres_version",
+    "attnres_max_sources",
+    "attnres_last_error",
+    "attnres_init",
+    "attnres_route_fwd",
+    "attnres_merge_fwd",
+    "attnres_block_step",
+)
+
+_c_vp = ctypes.c_void_p
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_float = ctypes.c_float
+
+_SIGNATURES = {
+    "attnres_version": ([], _c_int),
+    "attnres_max_sources": ([], _c_int),
+    "attnres_last_error": ([], ctypes.c_char_p),
+    "attnres_init": ([], _c_int),
+    "attnres_route_fwd": (
+        [
+            ctypes.POINTER(_c_vp),  # sources
+            _c_int,  # num_sources
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_i64,  # src_ld
+            _c_int,  # src_dtype
+            _c_vp,  # query
+            _c_vp,  # gain
+            _c_int,  # num_queries
+            _c_int,  # param_dtype
+            _c_float,  # eps
+            _c_vp,  # out
+            _c_int,  # out_dtype
+            _c_i64,  # out_ld
+            _c_i64,  # out_qstride
+            _c_vp,  # weights
+            _c_vp,  # lse
+            _c_vp,  # inv_rms
+            _c_vp,  # logits
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
+    "attnres_merge_fwd": (
+        [
+            _c_vp,  # partial
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_int,  # partial_dtype
+            _c_vp,  # query
+            _c_int,  # param_dtype
+            _c_vp,  # inter
+            _c_int,  # inter_dtype
+            _c_vp,  # inter_lse
+            _c_float,  # eps
+            _c_vp,  # out
+            _c_vp,  # logit
+            _c_vp,  # inv_rms
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
+    "attnres_block_step": (
+        [
+            _c_vp,  # arena
+            _c_int,  # num_slots
+            _c_i64,  # slot_stride
+            _c_int,  # n_committed
+            _c_int,  # commit
+            _c_vp,  # delta
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_int,  # dtype
+            _c_vp,  # query
+            _c_vp,  # gain
+            _c_int,  # param_dtype
+            _c_float,  # eps
+            _c_vp,  # out
+            _c_vp,  # weights
+            _c_vp,  # lse
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class AttnResError(RuntimeError):
+    """A C-ABI call returned an error code."""
+
+    def __init__(self, fn: str, code: int, message: str) -> None:
+        super().__init__(f"{fn} -> {_ERR_NAMES.get(code, code)}: {message}")
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: the MI355X routing kernels are not built "
+                    "(run `python -m kotodama_amd.build` or __graft_entry__.build()); "
+                    "there is no CPU fallback"
+                )
+            h = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_LOCAL)
+            for name, (argtypes, restype) in _SIGNATURES.items():
+                fn = getattr(h, name)
+                fn.argtypes = argtypes
+                fn.restype = restype
+            _lib = h
+    return _lib
+
+
+def check(fn: str, code: int) -> None:
+    if code != OK:
+        msg = lib().attnres_last_error()
+        raise AttnResError(fn, code, msg.decode() if msg else "")
+
+
+def pointer_array(ptrs: list[int]):
+    arr = (_c_vp * max(1, len(ptrs)))()
+    for i, p in enumerate(ptrs):
+        arr[i] = p
+    return arr
+
+
+def route_fwd(*args) -> None:
+    check("attnres_route_fwd", lib().attnres_route_fwd(*args))
+
+
+def merge_fwd(*args) -> None:
+    check("attnres_merge_fwd", lib().attnres_merge_fwd(*args))
+
+
+def block_step(*args) -> None:
+    check("attnres_block_step", lib().attnres_block_step(*args))

@@ -1,0 +1,105 @@
+"""Build libattnres_hip.so in-tree: gfx950 code objects + the C-ABI host library.
+
+Steps (all outputs under ``kotodama_amd/lib/``):
+
+1. ``hipcc --genco --offload-arch=gfx950`` compiles ``csrc/attnres_kernels.hip``
+   four times (``-DATTNRES_PART=0..3``, in parallel) into code-object parts.
+2. ``gcc`` assembles ``csrc/attnres_blob.S``, which ``.incbin``s the parts.
+3. ``g++`` builds ``csrc/attnres_capi.cpp`` + the blob into the shared library,
+   linked against ROCm's ``libamdhip64.so.7``.  Loaded after ``import torch``,
+   the dynamic linker binds that soname to the HIP runtime torch already
+   loaded, so streams and device memory are shared with torch.
+
+Run ``python -m kotodama_amd.build`` or call :func:`build`.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIBDIR = PKG / "lib"
+INCLUDE = PKG.parent / "include"
+LIB_NAME = "libattnres_hip.so"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+ARCH = "gfx950"
+NUM_PARTS = 4
+
+# Packed-fp32 VALU ops are disabled for every HIP compile (the kernels are
+# written with scalar fp32 arithmetic).
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "--genco",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def _run(cmd: list[str], cwd: Path | None = None) -> None:
+    res = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"build step failed ({res.returncode}): {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile everything; returns the path of the built shared library."""
+    hipcc = str(ROCM / "bin" / "hipcc")
+    LIBDIR.mkdir(exist_ok=True)
+    with tempfile.TemporaryDirectory(prefix="attnres_build_", dir=LIBDIR) as tmp:
+        tmpd = Path(tmp)
+        procs = []
+        for part in range(NUM_PARTS):
+            out = tmpd / f"attnres_gfx950_part{part}.hsaco"
+            cmd = [hipcc, *HIP_FLAGS, f"-DATTNRES_PART={part}", f"-I{CSRC}", str(CSRC / "attnres_kernels.hip"), "-o", str(out)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+        for cmd, p in procs:
+            so, se = p.communicate()
+            if p.returncode != 0:
+                raise RuntimeError(f"hipcc failed ({p.returncode}): {' '.join(cmd)}\n{so}\n{se}")
+        blob_o = tmpd / "attnres_blob.o"
+        _run(["gcc", "-c", f"-I{tmpd}", str(CSRC / "attnres_blob.S"), "-o", str(blob_o)])
+        so_tmp = tmpd / LIB_NAME
+        _run(
+            [
+                "g++",
+                "-shared",
+                "-fPIC",
+                "-O2",
+                "-std=c++17",
+                "-Wall",
+                "-D__HIP_PLATFORM_AMD__",
+                f"-I{INCLUDE}",
+                f"-I{CSRC}",
+                f"-I{ROCM / 'include'}",
+                str(CSRC / "attnres_capi.cpp"),
+                str(blob_o),
+                f"-L{ROCM / 'lib'}",
+                "-lamdhip64",
+                f"-Wl,-rpath,{ROCM / 'lib'}",
+                "-o",
+                str(so_tmp),
+            ]
+        )
+        for part in range(NUM_PARTS):
+            shutil.copy2(tmpd / f"attnres_gfx950_part{part}.hsaco", LIBDIR / f"attnres_gfx950_part{part}.hsaco")
+        final = LIBDIR / LIB_NAME
+        os.replace(so_tmp, final)  # atomic: a reader never sees a half-written library
+    if verbose:
+        print(f"built {final}", flush=True)
+    return final
+
+
+if __name__ == "__main__":
+    build(verbose="-q" not in sys.argv)

@@ -1,0 +1,20 @@
+/* The four gfx950 code-object parts, linked into libattnres_hip.so as bytes
+ * and loaded with hipModuleLoadData.  The build passes -I<dir of the .hsaco>. */
+    .section .rodata
+    .balign 4096
+    .global attnres_hsaco_part0
+attnres_hsaco_part0:
+    .incbin "attnres_gfx950_part0.hsaco"
+    .balign 4096
+    .global attnres_hsaco_part1
+attnres_hsaco_part1:
+    .incbin "attnres_gfx950_part1.hsaco"
+    .balign 4096
+    .global attnres_hsaco_part2
+attnres_hsaco_part2:
+    .incbin "attnres_gfx950_part2.hsaco"
+    .balign 4096
+    .global attnres_hsaco_part3
+attnres_hsaco_part3:
+    .incbin "attnres_gfx950_part3.hsaco"
+    .section .note.GNU-stack,"",@progbits

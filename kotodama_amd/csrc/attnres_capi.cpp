@@ -1,0 +1,421 @@
+// Host side of libattnres_hip.so: the C ABI declared in include/attnres.h.
+//
+// The gfx950 kernels are compiled ahead of time into code-object parts that
+// are linked into this library as bytes (attnres_blob.S).  On first use of a
+// device the parts are loaded with hipModuleLoadData; every call validates
+// its arguments on the host, fills one kernel-argument block
+// (attnres_params.h) and launches with hipModuleLaunchKernel on the caller's
+// stream.  No allocation, no synchronisation, no state beyond the per-device
+// module and function caches.
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "attnres.h"
+#include "attnres_params.h"
+
+// Code-object parts (attnres_blob.S).
+extern "C" const unsigned char attnres_hsaco_part0[];
+extern "C" const unsigned char attnres_hsaco_part1[];
+extern "C" const unsigned char attnres_hsaco_part2[];
+extern "C" const unsigned char attnres_hsaco_part3[];
+
+namespace {
+
+constexpr int kParts = 4;
+constexpr int kMaxDevices = 64;
+constexpr int kMaxThreads = 512;  // __launch_bounds__ of every kernel
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(ATTNRES_ERR_HIP, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+// Route kernel variants: type combo x S x V x (single/multi query).
+enum TypeCombo { kBfDot2 = 0, kBfFma = 1, kF32Fma = 2, kTypeCombos = 3 };
+constexpr int kNumS = ATTNRES_KMAX_SOURCES + 1;
+constexpr int kRouteFuncs = kTypeCombos * kNumS * 2 * 2;
+constexpr int kMergeFuncs = 4 * 2;
+
+struct DeviceState {
+  std::atomic<bool> loaded{false};
+  hipModule_t mods[kParts] = {};
+  int num_cus = 0;
+  hipFunction_t route[kRouteFuncs] = {};
+  int route_bpc[kRouteFuncs] = {};  // resident workgroups per CU, for the launch block size used
+  int route_bpc_block[kRouteFuncs] = {};
+  hipFunction_t merge[kMergeFuncs] = {};
+  int merge_bpc[kMergeFuncs] = {};
+  int merge_bpc_block[kMergeFuncs] = {};
+};
+
+DeviceState g_dev[kMaxDevices];
+std::mutex g_mu;
+
+// Tuning knobs read once: ATTNRES_V forces chunks per thread (1 or 2),
+// ATTNRES_GRID_MULT scales the resident-workgroup grid.
+struct Tuning {
+  int force_v = 0;
+  double grid_mult = 1.0;
+  Tuning() {
+    if (const char* v = std::getenv("ATTNRES_V")) force_v = std::atoi(v);
+    if (const char* g = std::getenv("ATTNRES_GRID_MULT")) {
+      const double m = std::atof(g);
+      if (m > 0.0) grid_mult = m;
+    }
+  }
+};
+const Tuning& tuning() {
+  static Tuning t;
+  return t;
+}
+
+int ensure_loaded(DeviceState** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(ATTNRES_ERR_HIP, "device ordinal %d out of range", dev);
+  DeviceState& st = g_dev[dev];
+  if (!st.loaded.load(std::memory_order_acquire)) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!st.loaded.load(std::memory_order_relaxed)) {
+      const unsigned char* blobs[kParts] = {attnres_hsaco_part0, attnres_hsaco_part1, attnres_hsaco_part2,
+                                            attnres_hsaco_part3};
+      for (int i = 0; i < kParts; ++i) {
+        e = hipModuleLoadData(&st.mods[i], blobs[i]);
+        if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
+      }
+      e = hipDeviceGetAttribute(&st.num_cus, hipDeviceAttributeMultiprocessorCount, dev);
+      if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
+      st.loaded.store(true, std::memory_order_release);
+    }
+  }
+  *out = &st;
+  return ATTNRES_OK;
+}
+
+// Code-object part holding the route kernels for S sources (the split of the
+// ATTNRES_PART blocks in attnres_kernels.hip); merge kernels live in part 3.
+int part_of_route(int s) { return s <= 5 ? 0 : s <= 9 ? 1 : s <= 13 ? 2 : 3; }
+constexpr int kMergePart = 3;
+
+int find_function(DeviceState& st, int part, const char* name, hipFunction_t* f) {
+  hipError_t e = hipModuleGetFunction(f, st.mods[part], name);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // do not leave a sticky error for the caller's runtime
+    return fail(ATTNRES_ERR_HIP, "kernel %s not found in code-object part %d: %s", name, part, hipGetErrorString(e));
+  }
+  return ATTNRES_OK;
+}
+
+int route_index(int combo, int s, int v, bool multiq) { return ((combo * kNumS + s) * 2 + (v - 1)) * 2 + (multiq ? 1 : 0); }
+
+int get_route(DeviceState& st, int combo, int s, int v, bool multiq, int block, hipFunction_t* f, int* bpc) {
+  const int idx = route_index(combo, s, v, multiq);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!st.route[idx]) {
+    static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
+    char name[96];
+    snprintf(name, sizeof(name), "attnres_route_%s_s%d_v%d_%s", combo_names[combo], s, v, multiq ? "qn" : "q1");
+    int rc = find_function(st, part_of_route(s), name, &st.route[idx]);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  if (st.route_bpc_block[idx] != block) {
+    int nb = 0;
+    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.route[idx], block, 0);
+    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    st.route_bpc[idx] = nb > 0 ? nb : 1;
+    st.route_bpc_block[idx] = block;
+  }
+  *f = st.route[idx];
+  *bpc = st.route_bpc[idx];
+  return ATTNRES_OK;
+}
+
+int get_merge(DeviceState& st, bool pbf, bool ibf, int v, int block, hipFunction_t* f, int* bpc) {
+  const int idx = ((pbf ? 0 : 2) + (ibf ? 0 : 1)) * 2 + (v - 1);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!st.merge[idx]) {
+    char name[96];
+    snprintf(name, sizeof(name), "attnres_merge_%s_%s_v%d", pbf ? "bf" : "f32", ibf ? "bf" : "f32", v);
+    int rc = find_function(st, kMergePart, name, &st.merge[idx]);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  if (st.merge_bpc_block[idx] != block) {
+    int nb = 0;
+    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.merge[idx], block, 0);
+    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    st.merge_bpc[idx] = nb > 0 ? nb : 1;
+    st.merge_bpc_block[idx] = block;
+  }
+  *f = st.merge[idx];
+  *bpc = st.merge_bpc[idx];
+  return ATTNRES_OK;
+}
+
+inline int round64(int64_t t) { return (int)(((t + 63) / 64) * 64); }
+
+// Chunks per thread V and the workgroup size for a row of `nchunk` 16-byte
+// chunks.  Returns 0 when no variant fits in kMaxThreads.
+int pick_v(int64_t n_tokens, int nchunk, int num_cus, int* block) {
+  const int t1 = round64(nchunk);
+  const int t2 = round64((nchunk + 1) / 2);
+  const bool ok1 = t1 <= kMaxThreads, ok2 = t2 <= kMaxThreads;
+  int v = 0;
+  const int force = tuning().force_v;
+  if (force == 1 && ok1) v = 1;
+  else if (force == 2 && ok2) v = 2;
+  else if (!ok1) v = ok2 ? 2 : 0;
+  else if (!ok2) v = 1;
+  else if (n_tokens < 2LL * num_cus) v = 1;  // few rows (decode): more threads per row
+  else v = (t2 >= 128) ? 2 : 1;              // prefill: two chunks per thread if >= 2 waves remain
+  *block = v == 1 ? t1 : t2;
+  return v;
+}
+
+int grid_for(int64_t n_tokens, int num_cus, int bpc) {
+  double g = (double)num_cus * bpc * tuning().grid_mult;
+  int64_t grid = (int64_t)g;
+  if (grid < 1) grid = 1;
+  if (grid > n_tokens) grid = n_tokens;
+  if (grid > 0x7fffffff) grid = 0x7fffffff;
+  return (int)grid;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool valid_dtype(int d) { return d == ATTNRES_DTYPE_F32 || d == ATTNRES_DTYPE_BF16; }
+
+int esize(int d) { return d == ATTNRES_DTYPE_BF16 ? 2 : 4; }
+
+template <typename Params>
+int launch(hipFunction_t f, int grid, int block, Params& P, void* stream) {
+  size_t sz = sizeof(Params);
+  void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &P, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz, HIP_LAUNCH_PARAM_END};
+  hipError_t e = hipModuleLaunchKernel(f, (unsigned)grid, 1, 1, (unsigned)block, 1, 1, 0, (hipStream_t)stream,
+                                       nullptr, cfg);
+  if (e != hipSuccess) return hip_fail(e, "hipModuleLaunchKernel");
+  return ATTNRES_OK;
+}
+
+// Shared validation + launch of the route kernel.  `mode`/`delta` are the
+// fused partial-update inputs of attnres_block_step.
+int route_launch(const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
+                 int src_dtype, const void* query, const void* gain, int num_queries, int param_dtype, float eps,
+                 void* out, int out_dtype, int64_t out_ld, int64_t out_qstride, float* weights, float* lse,
+                 float* inv_rms, float* logits, int mode, const void* delta, int64_t delta_ld, void* stream) {
+  if (num_sources < 0 || num_sources > ATTNRES_MAX_SOURCES)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "num_sources=%d outside [0, %d]", num_sources, ATTNRES_MAX_SOURCES);
+  if (num_sources > 0 && sources == nullptr) return fail(ATTNRES_ERR_ARG, "sources is NULL");
+  if (num_tokens < 0) return fail(ATTNRES_ERR_ARG, "num_tokens=%lld < 0", (long long)num_tokens);
+  if (hidden <= 0) return fail(ATTNRES_ERR_ARG, "hidden=%d <= 0", hidden);
+  if (!valid_dtype(src_dtype) || !valid_dtype(param_dtype) || !valid_dtype(out_dtype))
+    return fail(ATTNRES_ERR_ARG, "unknown dtype code (src=%d param=%d out=%d)", src_dtype, param_dtype, out_dtype);
+  if (query == nullptr) return fail(ATTNRES_ERR_ARG, "query is NULL");
+  if (num_queries < 1) return fail(ATTNRES_ERR_ARG, "num_queries=%d < 1", num_queries);
+  if (out == nullptr) return fail(ATTNRES_ERR_ARG, "out is NULL");
+  if (!std::isfinite(eps)) return fail(ATTNRES_ERR_ARG, "eps is not finite");
+  const bool bf = src_dtype == ATTNRES_DTYPE_BF16;
+  const int vec = bf ? 8 : 4;
+  if (hidden % vec != 0)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d is not a multiple of %d (16-byte chunks)", hidden, vec);
+  const int nchunk = hidden / vec;
+  if (round64((nchunk + 1) / 2) > kMaxThreads)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d exceeds the largest supported row (%d elements)", hidden,
+                2 * kMaxThreads * vec);
+  if (src_ld < hidden) return fail(ATTNRES_ERR_ARG, "src_ld=%lld < hidden=%d", (long long)src_ld, hidden);
+  if ((src_ld * esize(src_dtype)) % 16 != 0) return fail(ATTNRES_ERR_ALIGN, "source row stride not 16-byte aligned");
+  for (int s = 0; s < num_sources; ++s) {
+    if (sources[s] == nullptr) return fail(ATTNRES_ERR_ARG, "sources[%d] is NULL", s);
+    if (!aligned16(sources[s])) return fail(ATTNRES_ERR_ALIGN, "sources[%d] not 16-byte aligned", s);
+  }
+  if (out_ld < hidden) return fail(ATTNRES_ERR_ARG, "out_ld=%lld < hidden=%d", (long long)out_ld, hidden);
+  const int out_es = esize(out_dtype);
+  const int out_chunk_bytes = vec * out_es;  // bytes of one output chunk
+  const int out_align = out_chunk_bytes >= 16 ? 16 : out_chunk_bytes;
+  if (((uintptr_t)out % out_align) != 0 || ((out_ld * out_es) % out_align) != 0)
+    return fail(ATTNRES_ERR_ALIGN, "out rows not %d-byte aligned", out_align);
+  if (num_queries > 1) {
+    if (out_qstride < num_tokens * out_ld)
+      return fail(ATTNRES_ERR_ARG, "out_qstride=%lld overlaps query outputs", (long long)out_qstride);
+    if ((out_qstride * out_es) % out_align != 0) return fail(ATTNRES_ERR_ALIGN, "out_qstride not aligned");
+  }
+  if (mode != ATTNRES_MODE_PLAIN) {
+    if (num_sources < 1 || num_queries != 1) return fail(ATTNRES_ERR_ARG, "partial update needs S >= 1 and one query");
+    if (delta == nullptr) return fail(ATTNRES_ERR_ARG, "delta is NULL");
+    if (!aligned16(delta) || (delta_ld * esize(src_dtype)) % 16 != 0)
+      return fail(ATTNRES_ERR_ALIGN, "delta rows not 16-byte aligned");
+  }
+  if (num_tokens == 0) return ATTNRES_OK;
+
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+
+  int block = 0;
+  const int v = pick_v(num_tokens, nchunk, st->num_cus, &block);
+  if (v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
+
+  const int combo = bf ? (param_dtype == ATTNRES_DTYPE_BF16 ? kBfDot2 : kBfFma) : kF32Fma;
+  const bool multiq = num_queries > 1;
+  hipFunction_t f = nullptr;
+  int bpc = 1;
+  rc = get_route(*st, combo, num_sources, v, multiq, block, &f, &bpc);
+  if (rc != ATTNRES_OK) return rc;
+
+  attnres_route_params P;
+  std::memset(&P, 0, sizeof(P));
+  for (int s = 0; s < num_sources; ++s) P.src[s] = sources[s];
+  P.query = query;
+  P.gain = gain;
+  P.delta = delta;
+  P.out = out;
+  P.weights = weights;
+  P.lse = lse;
+  P.inv_rms = inv_rms;
+  P.logits = logits;
+  P.n_tokens = num_tokens;
+  P.src_ld = src_ld;
+  P.delta_ld = delta_ld;
+  P.out_ld = out_ld;
+  P.out_qstride = out_qstride;
+  P.d = hidden;
+  P.nchunk = nchunk;
+  P.num_queries = num_queries;
+  P.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
+  P.out_bf16 = out_dtype == ATTNRES_DTYPE_BF16;
+  P.mode = mode;
+  P.eps = eps;
+  P.inv_d = 1.0f / (float)hidden;
+  return launch(f, grid_for(num_tokens, st->num_cus, bpc), block, P, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int attnres_version(void) { return 10000; }
+
+int attnres_max_sources(void) { return ATTNRES_MAX_SOURCES; }
+
+const char* attnres_last_error(void) { return g_err.c_str(); }
+
+int attnres_init(void) {
+  DeviceState* st = nullptr;
+  return ensure_loaded(&st);
+}
+
+int attnres_route_fwd(const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
+                      int src_dtype, const void* query, const void* gain, int num_queries, int param_dtype, float eps,
+                      void* out, int out_dtype, int64_t out_ld, int64_t out_qstride, float* weights, float* lse,
+                      float* inv_rms, float* logits, void* stream) {
+  return route_launch(sources, num_sources, num_tokens, hidden, src_ld, src_dtype, query, gain, num_queries,
+                      param_dtype, eps, out, out_dtype, out_ld, out_qstride, weights, lse, inv_rms, logits,
+                      ATTNRES_MODE_PLAIN, nullptr, 0, stream);
+}
+
+int attnres_merge_fwd(const void* partial, int64_t num_tokens, int hidden, int partial_dtype, const void* query,
+                      int param_dtype, const void* inter, int inter_dtype, const float* inter_lse, float eps,
+                      void* out, float* logit, float* inv_rms, void* stream) {
+  if (partial == nullptr || query == nullptr || inter == nullptr || inter_lse == nullptr || out == nullptr)
+    return fail(ATTNRES_ERR_ARG, "merge: partial, query, inter, inter_lse and out are required");
+  if (num_tokens < 0) return fail(ATTNRES_ERR_ARG, "num_tokens=%lld < 0", (long long)num_tokens);
+  if (hidden <= 0) return fail(ATTNRES_ERR_ARG, "hidden=%d <= 0", hidden);
+  if (!valid_dtype(partial_dtype) || !valid_dtype(param_dtype) || !valid_dtype(inter_dtype))
+    return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (!std::isfinite(eps)) return fail(ATTNRES_ERR_ARG, "eps is not finite");
+  const bool pbf = partial_dtype == ATTNRES_DTYPE_BF16;
+  const bool ibf = inter_dtype == ATTNRES_DTYPE_BF16;
+  const int vec = pbf ? 8 : 4;
+  if (hidden % vec != 0)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d is not a multiple of %d (16-byte chunks)", hidden, vec);
+  const int nchunk = hidden / vec;
+  if (round64((nchunk + 1) / 2) > kMaxThreads)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d exceeds the largest supported row", hidden);
+  const int inter_align = (vec * esize(inter_dtype)) >= 16 ? 16 : vec * esize(inter_dtype);
+  if (!aligned16(partial) || ((uintptr_t)inter % inter_align) != 0 || ((uintptr_t)out % inter_align) != 0 ||
+      ((int64_t)hidden * esize(inter_dtype)) % inter_align != 0)
+    return fail(ATTNRES_ERR_ALIGN, "merge rows not aligned");
+  if (num_tokens == 0) return ATTNRES_OK;
+
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  int block = 0;
+  const int v = pick_v(num_tokens, nchunk, st->num_cus, &block);
+  if (v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
+  hipFunction_t f = nullptr;
+  int bpc = 1;
+  rc = get_merge(*st, pbf, ibf, v, block, &f, &bpc);
+  if (rc != ATTNRES_OK) return rc;
+
+  attnres_merge_params P;
+  std::memset(&P, 0, sizeof(P));
+  P.partial = partial;
+  P.query = query;
+  P.inter = inter;
+  P.inter_lse = inter_lse;
+  P.out = out;
+  P.logit = logit;
+  P.inv_rms = inv_rms;
+  P.n_tokens = num_tokens;
+  P.partial_ld = hidden;
+  P.inter_ld = hidden;
+  P.out_ld = hidden;
+  P.d = hidden;
+  P.nchunk = nchunk;
+  P.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
+  P.inter_bf16 = ibf;
+  P.eps = eps;
+  P.inv_d = 1.0f / (float)hidden;
+  return launch(f, grid_for(num_tokens, st->num_cus, bpc), block, P, stream);
+}
+
+int attnres_block_step(void* arena, int num_slots, int64_t slot_stride, int n_committed, int commit,
+                       const void* delta, int64_t num_tokens, int hidden, int dtype, const void* query,
+                       const void* gain, int param_dtype, float eps, void* out, float* weights, float* lse,
+                       void* stream) {
+  if (arena == nullptr) return fail(ATTNRES_ERR_ARG, "arena is NULL");
+  if (num_slots < 1) return fail(ATTNRES_ERR_ARG, "num_slots=%d < 1", num_slots);
+  if (commit != 0 && commit != 1) return fail(ATTNRES_ERR_ARG, "commit=%d is not 0 or 1", commit);
+  if (n_committed < 0) return fail(ATTNRES_ERR_ARG, "n_committed=%d < 0", n_committed);
+  const int S = n_committed + commit + 1;
+  if (S > num_slots)
+    return fail(ATTNRES_ERR_ARG, "partial slot %d outside the arena (%d slots)", S - 1, num_slots);
+  if (S > ATTNRES_MAX_SOURCES)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "%d sources exceed the maximum %d", S, ATTNRES_MAX_SOURCES);
+  if (commit && delta == nullptr) return fail(ATTNRES_ERR_ARG, "a commit needs the new partial block (delta)");
+  if (!valid_dtype(dtype)) return fail(ATTNRES_ERR_ARG, "unknown dtype code %d", dtype);
+  if (num_tokens < 0 || hidden <= 0) return fail(ATTNRES_ERR_ARG, "bad num_tokens/hidden");
+  if (slot_stride < num_tokens * (int64_t)hidden)
+    return fail(ATTNRES_ERR_ARG, "slot_stride=%lld smaller than a slot", (long long)slot_stride);
+  if ((slot_stride * esize(dtype)) % 16 != 0) return fail(ATTNRES_ERR_ALIGN, "slot_stride not 16-byte aligned");
+  const void* srcs[ATTNRES_MAX_SOURCES];
+  const char* base = static_cast<const char*>(arena);
+  for (int s = 0; s < S; ++s) srcs[s] = base + (int64_t)s * slot_stride * esize(dtype);
+  const int mode = commit ? ATTNRES_MODE_SET : (delta ? ATTNRES_MODE_ACCUM : ATTNRES_MODE_PLAIN);
+  return route_launch(srcs, S, num_tokens, hidden, hidden, dtype, query, gain, 1, param_dtype, eps, out, dtype,
+                      hidden, (int64_t)num_tokens * hidden, weights, lse, nullptr, nullptr, mode, delta, hidden,
+                      stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,610 @@
+// Block Attention Residual (AttnRes) routing kernels for gfx950 (CDNA4).
+//
+// One routing point mixes, for every token independently, S depth sources
+// (committed block summaries plus the running partial block) of width d:
+//
+//   qw       = query * gain                            (llama.py:630)
+//   inv_rms  = rsqrt(mean_d(x_s^2) + eps)              (llama.py:640)
+//   logit_s  = (x_s . qw) * inv_rms_s                  (llama.py:641)
+//   w        = softmax over s of logit                 (llama.py:642-643)
+//   out      = sum_s w_s * x_s   (raw, un-normalised)  (llama.py:644)
+//
+// The work is a GEMV per token at ~2 flop/byte, so it is bound by HBM and
+// uses no MFMA.  Layout of the computation:
+//
+//   * One workgroup owns one token row at a time (grid-stride loop over
+//     tokens).  Thread i owns the 16-byte chunks i, i+blockDim, ... of the
+//     row (V chunks), so every wave-wide load is 1 KiB contiguous.
+//   * All S source chunks of the token are loaded into registers up front
+//     (S*V 128-bit loads in flight per thread), so each source byte leaves
+//     HBM exactly once and the softmax can be exact (two-pass over
+//     registers, no online rescaling).
+//   * Per thread: partial sum(x^2) and x.qw per source (bf16 pairs through
+//     v_dot2c_f32_bf16, fp32 accumulation).  Per wave: DPP row reductions
+//     and row broadcasts leave the wave total in lane 63, which writes the
+//     2S totals to LDS.  One barrier per token; every thread then sums the
+//     per-wave totals (broadcast LDS reads), forms the S logits and the
+//     softmax, and writes its chunks of the weighted sum.
+//   * The LDS exchange buffer is double-buffered by round parity, so one
+//     barrier per round is enough.
+//
+// The S sources are separate pointers (no stacked copy is needed), the
+// number of sources S is a template parameter (register arrays stay in
+// VGPRs), and the last slot can be formed in-kernel from a sublayer delta
+// (fused partial accumulate / block commit for the decode and arena paths).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attnres_params.h"
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+namespace {
+
+// ---------------------------------------------------------------- helpers --
+
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __builtin_bit_cast(float, u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __builtin_bit_cast(float, u & 0xffff0000u); }
+
+// Two fp32 -> packed bf16 pair, round-to-nearest-even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  bf16x2 r = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ float round_bf16(float v) { return (float)(__bf16)v; }
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                         false);
+}
+
+template <typename T>
+__device__ __forceinline__ T ldg(const void* p) {
+  return *reinterpret_cast<const T*>(p);
+}
+template <typename T>
+__device__ __forceinline__ void stg(void* p, T v) {
+  *reinterpret_cast<T*>(p) = v;
+}
+
+// One DPP step: v + v[permuted lane], restricted to the rows in ROW_MASK.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+  const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false);
+  return v + __builtin_bit_cast(float, t);
+}
+
+// Sum over the 64 lanes of a wave; the full sum lands in lane 63.
+//   quad_perm[1,0,3,2], quad_perm[2,3,0,1]  -> quad sums
+//   row_half_mirror, row_mirror             -> row (16-lane) sums in every lane
+//   row_bcast:15 (rows 1,3), row_bcast:31 (rows 2,3) -> lane 63 holds the total
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+  v = dpp_add<0xB1, 0xF>(v);
+  v = dpp_add<0x4E, 0xF>(v);
+  v = dpp_add<0x141, 0xF>(v);
+  v = dpp_add<0x140, 0xF>(v);
+  v = dpp_add<0x142, 0xA>(v);
+  v = dpp_add<0x143, 0xC>(v);
+  return v;
+}
+
+// Elements of a 16-byte chunk as fp32.
+template <bool BF16>
+struct Chunk;
+
+template <>
+struct Chunk<true> {  // 8 x bf16
+  static constexpr int VEC = 8;
+  static constexpr int BYTES = 2;
+  __device__ __forceinline__ static float elem(const u32x4& c, int e) {
+    const uint32_t w = c[e >> 1];
+    return (e & 1) ? bf_hi(w) : bf_lo(w);
+  }
+};
+
+template <>
+struct Chunk<false> {  // 4 x fp32
+  static constexpr int VEC = 4;
+  static constexpr int BYTES = 4;
+  __device__ __forceinline__ static float elem(const u32x4& c, int e) { return __builtin_bit_cast(float, c[e]); }
+};
+
+// Load VEC consecutive parameter elements (bf16 or fp32) as fp32.
+template <int VEC>
+__device__ __forceinline__ void load_param(const void* base, int64_t elem_off, bool bf16, float (&v)[VEC]) {
+  if (bf16) {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(base) + elem_off;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) v[e] = __builtin_bit_cast(float, (uint32_t)p[e] << 16);
+  } else {
+    const float* p = reinterpret_cast<const float*>(base) + elem_off;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) v[e] = p[e];
+  }
+}
+
+// qw chunk = query[q] * gain, rounded to the parameter dtype the way the
+// reference's `query * norm.weight` is (llama.py:630; serve.py:89-91).
+template <int VEC>
+__device__ __forceinline__ void load_qw(const attnres_route_params& P, int q, int chunk, float (&qw)[VEC]) {
+  const int64_t off = (int64_t)chunk * VEC;
+  load_param<VEC>(P.query, (int64_t)q * P.d + off, P.param_bf16, qw);
+  if (P.gain != nullptr) {
+    float g[VEC];
+    load_param<VEC>(P.gain, off, P.param_bf16, g);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float prod = qw[e] * g[e];
+      qw[e] = P.param_bf16 ? round_bf16(prod) : prod;
+    }
+  }
+}
+
+// ------------------------------------------------------------ route body --
+
+// S     : number of active sources (0 writes NaN, as softmax over no sources)
+// V     : 16-byte chunks per thread per source row
+// BF16  : sources (and delta) are bf16, else fp32
+// QDOT2 : bf16 sources and bf16-exact qw: the dot uses v_dot2c_f32_bf16
+// MULTIQ: num_queries >= 1 queries share the loaded rows (phase-1 batching)
+template <int S, int V, bool BF16, bool QDOT2, bool MULTIQ>
+__device__ __forceinline__ void route_body(const attnres_route_params& P) {
+  using C = Chunk<BF16>;
+  constexpr int VEC = C::VEC;
+  constexpr int NV = 2 * S;                  // sum(x^2) and x.qw per source
+  constexpr int RLD = ((NV + 3) / 4) * 4;    // row pitch of the LDS exchange
+  __shared__ float red[2][ATTNRES_KMAX_WAVES][RLD > 0 ? RLD : 4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = (blockDim.x + 63) >> 6;
+  const int nq = MULTIQ ? P.num_queries : 1;
+
+  int chunk[V];
+  bool ok[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    chunk[k] = tid + k * (int)blockDim.x;
+    ok[k] = chunk[k] < P.nchunk;
+  }
+
+  // Pseudo-query chunks, kept in registers across the token loop (Q == 1).
+  float qwf[V][VEC];
+  uint32_t qwb[V][VEC / 2];
+  auto fetch_qw = [&](int q) {
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      float t[VEC];
+      if (ok[k]) {
+        load_qw<VEC>(P, q, chunk[k], t);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) t[e] = 0.f;
+      }
+      if constexpr (QDOT2) {
+#pragma unroll
+        for (int e = 0; e < VEC / 2; ++e) qwb[k][e] = pack_bf16(t[2 * e], t[2 * e + 1]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) qwf[k][e] = t[e];
+      }
+    }
+  };
+  if constexpr (!MULTIQ) fetch_qw(0);
+
+  const int64_t row_bytes_ld = P.src_ld * C::BYTES;
+  int ph = 0;
+
+  for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
+    if constexpr (S == 0) {
+      // Softmax over an empty set is NaN everywhere (llama.py:642-644 with an
+      // all-false mask; kernels/phase_1.py:78-101 with num_active == 0).
+      const float nan = __builtin_nanf("");
+      for (int q = 0; q < nq; ++q) {
+        char* orow = reinterpret_cast<char*>(P.out) +
+                     ((int64_t)q * P.out_qstride + tok * P.out_ld) * (P.out_bf16 ? 2 : 4);
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+          if (!ok[k]) continue;
+          if (P.out_bf16) {
+            uint32_t h = pack_bf16(nan, nan);
+            if constexpr (VEC == 8) stg<u32x4>(orow + (int64_t)chunk[k] * 16, u32x4{h, h, h, h});
+            else stg<u32x2>(orow + (int64_t)chunk[k] * 8, u32x2{h, h});
+          } else {
+            const uint32_t f = __builtin_bit_cast(uint32_t, nan);
+            u32x4 v = {f, f, f, f};
+            if constexpr (VEC == 8) {
+              stg<u32x4>(orow + (int64_t)chunk[k] * 32, v);
+              stg<u32x4>(orow + (int64_t)chunk[k] * 32 + 16, v);
+            } else {
+              stg<u32x4>(orow + (int64_t)chunk[k] * 16, v);
+            }
+          }
+        }
+        if (tid == 0 && P.lse) P.lse[(int64_t)q * P.n_tokens + tok] = nan;
+      }
+      continue;
+    } else {
+      // ---- stream the S source chunks of this token into registers ----
+      u32x4 x[S][V];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const char* row = reinterpret_cast<const char*>(P.src[s]) + tok * row_bytes_ld;
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+          if (s == S - 1 && P.mode == ATTNRES_MODE_SET) {
+            x[s][k] = u32x4{0, 0, 0, 0};
+          } else {
+            x[s][k] = ok[k] ? ldg<u32x4>(row + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
+          }
+        }
+      }
+
+      // ---- fused partial update: partial (+)= delta, written back ----
+      if (P.mode != ATTNRES_MODE_PLAIN) {
+        const char* drow = reinterpret_cast<const char*>(P.delta) + tok * P.delta_ld * C::BYTES;
+        char* prow = reinterpret_cast<char*>(const_cast<void*>(P.src[S - 1])) + tok * row_bytes_ld;
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+          if (!ok[k]) continue;
+          const u32x4 dv = ldg<u32x4>(drow + (int64_t)chunk[k] * 16);
+          u32x4 nv = dv;
+          if (P.mode == ATTNRES_MODE_ACCUM) {
+            if constexpr (BF16) {
+#pragma unroll
+              for (int w = 0; w < 4; ++w)
+                nv[w] = pack_bf16(bf_lo(x[S - 1][k][w]) + bf_lo(dv[w]), bf_hi(x[S - 1][k][w]) + bf_hi(dv[w]));
+            } else {
+#pragma unroll
+              for (int w = 0; w < 4; ++w)
+                nv[w] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, x[S - 1][k][w]) +
+                                                         __builtin_bit_cast(float, dv[w]));
+            }
+          }
+          x[S - 1][k] = nv;
+          stg<u32x4>(prow + (int64_t)chunk[k] * 16, nv);
+        }
+      }
+
+      float ss_tot[S];
+      for (int q = 0; q < nq; ++q) {
+        if constexpr (MULTIQ) fetch_qw(q);
+
+        // ---- per-thread partial sums ----
+        float part[NV];
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          float ss = 0.f, dt = 0.f;
+#pragma unroll
+          for (int k = 0; k < V; ++k) {
+            if constexpr (BF16) {
+#pragma unroll
+              for (int w = 0; w < 4; ++w) {
+                ss = dot2_bf16(x[s][k][w], x[s][k][w], ss);
+                if constexpr (QDOT2) {
+                  dt = dot2_bf16(x[s][k][w], qwb[k][w], dt);
+                } else {
+                  dt = __builtin_fmaf(bf_lo(x[s][k][w]), qwf[k][2 * w], dt);
+                  dt = __builtin_fmaf(bf_hi(x[s][k][w]), qwf[k][2 * w + 1], dt);
+                }
+              }
+            } else {
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) {
+                const float v = C::elem(x[s][k], e);
+                ss = __builtin_fmaf(v, v, ss);
+                dt = __builtin_fmaf(v, qwf[k][e], dt);
+              }
+            }
+          }
+          part[s] = ss;
+          part[S + s] = dt;
+        }
+
+        // ---- wave reduce, then one LDS exchange across the waves ----
+#pragma unroll
+        for (int j = 0; j < NV; ++j) part[j] = wave_sum_to_lane63(part[j]);
+        if (lane == 63) {
+#pragma unroll
+          for (int j = 0; j < NV; ++j) red[ph][wave][j] = part[j];
+        }
+        __syncthreads();
+        float tot[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) tot[j] = 0.f;
+        for (int w = 0; w < nwaves; ++w) {
+#pragma unroll
+          for (int j = 0; j < NV; ++j) tot[j] += red[ph][w][j];
+        }
+        ph ^= 1;
+
+        // ---- softmax over depth ----
+        float logit[S], wgt[S];
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          if (q == 0) ss_tot[s] = __builtin_amdgcn_rsqf(tot[s] * P.inv_d + P.eps);
+          logit[s] = tot[S + s] * ss_tot[s];
+          m = __builtin_fmaxf(m, logit[s]);
+        }
+        float sum = 0.f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          wgt[s] = __expf(logit[s] - m);
+          sum += wgt[s];
+        }
+        const float rsum = 1.0f / sum;
+#pragma unroll
+        for (int s = 0; s < S; ++s) wgt[s] *= rsum;
+
+        if (tid == 0) {
+          if (P.weights) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) P.weights[((int64_t)q * S + s) * P.n_tokens + tok] = wgt[s];
+          }
+          if (P.lse) P.lse[(int64_t)q * P.n_tokens + tok] = m + __logf(sum);
+          if (P.logits) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) P.logits[((int64_t)q * P.n_tokens + tok) * S + s] = logit[s];
+          }
+          if (q == 0 && P.inv_rms) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) P.inv_rms[tok * S + s] = ss_tot[s];
+          }
+        }
+
+        // ---- weighted sum of the raw sources, one output row ----
+        // The empty asm makes the rows opaque here, so the compiler re-unpacks
+        // bf16 pairs below instead of keeping the fp32 copies from the dot
+        // phase alive (which doubles register use).
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+#pragma unroll
+          for (int k = 0; k < V; ++k) asm volatile("" : "+v"(x[s][k]));
+        }
+        char* orow = reinterpret_cast<char*>(P.out) +
+                     ((int64_t)q * P.out_qstride + tok * P.out_ld) * (P.out_bf16 ? 2 : 4);
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+          if (!ok[k]) continue;
+          float acc[VEC];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[e] = wgt[0] * C::elem(x[0][k], e);
+#pragma unroll
+          for (int s = 1; s < S; ++s) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(wgt[s], C::elem(x[s][k], e), acc[e]);
+          }
+          if (P.out_bf16) {
+            if constexpr (VEC == 8) {
+              stg<u32x4>(orow + (int64_t)chunk[k] * 16,
+                         u32x4{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3]), pack_bf16(acc[4], acc[5]),
+                               pack_bf16(acc[6], acc[7])});
+            } else {
+              stg<u32x2>(orow + (int64_t)chunk[k] * 8, u32x2{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3])});
+            }
+          } else {
+#pragma unroll
+            for (int h = 0; h < VEC / 4; ++h) {
+              stg<u32x4>(orow + ((int64_t)chunk[k] * VEC + 4 * h) * 4,
+                         u32x4{__builtin_bit_cast(uint32_t, acc[4 * h]), __builtin_bit_cast(uint32_t, acc[4 * h + 1]),
+                               __builtin_bit_cast(uint32_t, acc[4 * h + 2]),
+                               __builtin_bit_cast(uint32_t, acc[4 * h + 3])});
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ merge body --
+
+// Phase-2 merge of the intra-block partial into the phase-1 inter-block
+// result (kernels/phase_2.py:40-57 semantics): one token row per workgroup.
+template <int V, bool PBF16, bool IBF16>
+__device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
+  using C = Chunk<PBF16>;
+  constexpr int VEC = C::VEC;
+  __shared__ float red[2][ATTNRES_KMAX_WAVES][4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = (blockDim.x + 63) >> 6;
+
+  int chunk[V];
+  bool ok[V];
+  float qw[V][VEC];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    chunk[k] = tid + k * (int)blockDim.x;
+    ok[k] = chunk[k] < P.nchunk;
+    if (ok[k]) {
+      load_param<VEC>(P.query, (int64_t)chunk[k] * VEC, P.param_bf16, qw[k]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) qw[k][e] = 0.f;
+    }
+  }
+
+  int ph = 0;
+  for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
+    const char* prow = reinterpret_cast<const char*>(P.partial) + tok * P.partial_ld * C::BYTES;
+    const char* irow = reinterpret_cast<const char*>(P.inter) + tok * P.inter_ld * (IBF16 ? 2 : 4);
+    u32x4 p[V];
+    float iv[V][VEC];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      p[k] = ok[k] ? ldg<u32x4>(prow + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
+      if (ok[k]) {
+        if constexpr (IBF16) {
+#pragma unroll
+          for (int h = 0; h < VEC / 8 + (VEC < 8); ++h) {
+            if constexpr (VEC == 8) {
+              const u32x4 t = ldg<u32x4>(irow + (int64_t)chunk[k] * 16);
+#pragma unroll
+              for (int w = 0; w < 4; ++w) {
+                iv[k][2 * w] = bf_lo(t[w]);
+                iv[k][2 * w + 1] = bf_hi(t[w]);
+              }
+            } else {
+              const u32x2 t = ldg<u32x2>(irow + (int64_t)chunk[k] * 8);
+              iv[k][0] = bf_lo(t[0]);
+              iv[k][1] = bf_hi(t[0]);
+              iv[k][2] = bf_lo(t[1]);
+              iv[k][3] = bf_hi(t[1]);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < VEC / 4; ++h) {
+            const u32x4 t = ldg<u32x4>(irow + ((int64_t)chunk[k] * VEC + 4 * h) * 4);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) iv[k][4 * h + w] = __builtin_bit_cast(float, t[w]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) iv[k][e] = 0.f;
+      }
+    }
+
+    float ss = 0.f, dt = 0.f;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float v = C::elem(p[k], e);
+        ss = __builtin_fmaf(v, v, ss);
+        dt = __builtin_fmaf(v, qw[k][e], dt);
+      }
+    }
+    ss = wave_sum_to_lane63(ss);
+    dt = wave_sum_to_lane63(dt);
+    if (lane == 63) {
+      red[ph][wave][0] = ss;
+      red[ph][wave][1] = dt;
+    }
+    __syncthreads();
+    float tss = 0.f, tdt = 0.f;
+    for (int w = 0; w < nwaves; ++w) {
+      tss += red[ph][w][0];
+      tdt += red[ph][w][1];
+    }
+    ph ^= 1;
+    const float inv = __builtin_amdgcn_rsqf(tss * P.inv_d + P.eps);
+    const float logit = tdt * inv;
+    const float pi = 1.0f / (1.0f + __expf(-(logit - P.inter_lse[tok])));
+    if (tid == 0) {
+      if (P.logit) P.logit[tok] = logit;
+      if (P.inv_rms) P.inv_rms[tok] = inv;
+    }
+
+    char* orow = reinterpret_cast<char*>(P.out) + tok * P.out_ld * (IBF16 ? 2 : 4);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      if (!ok[k]) continue;
+      float o[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[e] = __builtin_fmaf(pi, C::elem(p[k], e) - iv[k][e], iv[k][e]);
+      if constexpr (IBF16) {
+        if constexpr (VEC == 8) {
+          stg<u32x4>(orow + (int64_t)chunk[k] * 16,
+                     u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])});
+        } else {
+          stg<u32x2>(orow + (int64_t)chunk[k] * 8, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < VEC / 4; ++h) {
+          stg<u32x4>(orow + ((int64_t)chunk[k] * VEC + 4 * h) * 4,
+                     u32x4{__builtin_bit_cast(uint32_t, o[4 * h]), __builtin_bit_cast(uint32_t, o[4 * h + 1]),
+                           __builtin_bit_cast(uint32_t, o[4 * h + 2]), __builtin_bit_cast(uint32_t, o[4 * h + 3])});
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+// ------------------------------------------------------- instantiations --
+//
+// Symbol names (looked up by the host launcher with hipModuleGetFunction):
+//   attnres_route_<in>_<qw>_s<S>_v<V>_<q1|qn>
+//     in : bf (bf16 sources) | f32 (fp32 sources)
+//     qw : d2 (bf16-exact query, v_dot2 path) | fm (fp32 FMA path)
+//   attnres_merge_<partial>_<inter>_v<V>
+
+#define ROUTE_LB(V) __launch_bounds__(512)
+
+#define ROUTE_ONE(INNAME, BF, QNAME, QD2, S, V)                                                        \
+  extern "C" __global__ void ROUTE_LB(V) attnres_route_##INNAME##_##QNAME##_s##S##_v##V##_q1(         \
+      attnres_route_params P) {                                                                       \
+    route_body<S, V, BF, QD2, false>(P);                                                              \
+  }                                                                                                   \
+  extern "C" __global__ void ROUTE_LB(V) attnres_route_##INNAME##_##QNAME##_s##S##_v##V##_qn(         \
+      attnres_route_params P) {                                                                       \
+    route_body<S, V, BF, QD2, true>(P);                                                               \
+  }
+
+#define ROUTE_TYPES(S, V)                 \
+  ROUTE_ONE(bf, true, d2, true, S, V)     \
+  ROUTE_ONE(bf, true, fm, false, S, V)    \
+  ROUTE_ONE(f32, false, fm, false, S, V)
+
+#define ROUTE_S(S) \
+  ROUTE_TYPES(S, 1) \
+  ROUTE_TYPES(S, 2)
+
+// The build compiles this file once per module part (ATTNRES_PART = 0..3)
+// so the parts build in parallel; the host searches every part for a symbol.
+#ifndef ATTNRES_PART
+#define ATTNRES_PART 0
+#define ATTNRES_ALL_PARTS 1
+#endif
+
+#if ATTNRES_PART == 0 || defined(ATTNRES_ALL_PARTS)
+ROUTE_S(0)
+ROUTE_S(1)
+ROUTE_S(2)
+ROUTE_S(3)
+ROUTE_S(4)
+ROUTE_S(5)
+#endif
+#if ATTNRES_PART == 1 || defined(ATTNRES_ALL_PARTS)
+ROUTE_S(6)
+ROUTE_S(7)
+ROUTE_S(8)
+ROUTE_S(9)
+#endif
+#if ATTNRES_PART == 2 || defined(ATTNRES_ALL_PARTS)
+ROUTE_S(10)
+ROUTE_S(11)
+ROUTE_S(12)
+ROUTE_S(13)
+#endif
+#if ATTNRES_PART == 3 || defined(ATTNRES_ALL_PARTS)
+ROUTE_S(14)
+ROUTE_S(15)
+ROUTE_S(16)
+
+#define MERGE_ONE(PN, PB, IN, IB, V)                                                                 \
+  extern "C" __global__ void ROUTE_LB(V) attnres_merge_##PN##_##IN##_v##V(attnres_merge_params P) { \
+    merge_body<V, PB, IB>(P);                                                                        \
+  }
+
+#define MERGE_V(V)                   \
+  MERGE_ONE(bf, true, bf, true, V)   \
+  MERGE_ONE(bf, true, f32, false, V) \
+  MERGE_ONE(f32, false, bf, true, V) \
+  MERGE_ONE(f32, false, f32, false, V)
+
+MERGE_V(1)
+MERGE_V(2)
+#endif

@@ -1,0 +1,86 @@
+/*
+ * Kernel-argument blocks shared by the gfx950 code object (attnres_kernels.hip)
+ * and the host launcher (attnres_capi.cpp).  Both sides are compiled from this
+ * one definition, so the byte layout handed to hipModuleLaunchKernel through
+ * HIP_LAUNCH_PARAM_BUFFER_POINTER is the layout the kernels read.
+ *
+ * Plain C types only: this header is included by g++ (host) and by hipcc
+ * (device) alike.
+ */
+#ifndef KOTODAMA_AMD_ATTNRES_PARAMS_H
+#define KOTODAMA_AMD_ATTNRES_PARAMS_H
+
+#include <stdint.h>
+
+#define ATTNRES_KMAX_SOURCES 16   /* S templates instantiated: 0..16 */
+#define ATTNRES_KMAX_WAVES 8      /* 512 threads per workgroup */
+
+/* How the last source slot (the partial block) is formed before routing. */
+#define ATTNRES_MODE_PLAIN 0      /* partial is read as-is */
+#define ATTNRES_MODE_ACCUM 1      /* partial := round(partial + delta), written back */
+#define ATTNRES_MODE_SET 2        /* partial := delta (fresh block after a commit), written */
+
+/*
+ * One routing point over S depth sources for n_tokens token rows.
+ *   src[s]      row block of source s, token t at src[s] + t*src_ld elements
+ *   query       (num_queries, d) pseudo-queries, param dtype
+ *   gain        (d,) RMSNorm gain folded into every query, or NULL (pre-folded)
+ *   delta       (n_tokens, d) sublayer output for MODE_ACCUM / MODE_SET, else NULL
+ *   out         (num_queries, n_tokens, d): query q, token t at
+ *               out + q*out_qstride + t*out_ld elements
+ *   weights     (num_queries, S, n_tokens) fp32 softmax weights, or NULL
+ *   lse         (num_queries, n_tokens) fp32 log-sum-exp of the logits, or NULL
+ *   inv_rms     (n_tokens, S) fp32 rsqrt(mean(x^2)+eps), or NULL
+ *   logits      (num_queries, n_tokens, S) fp32 pre-softmax logits, or NULL
+ */
+typedef struct attnres_route_params {
+  const void* src[ATTNRES_KMAX_SOURCES];
+  const void* query;
+  const void* gain;
+  const void* delta;
+  void* out;
+  float* weights;
+  float* lse;
+  float* inv_rms;
+  float* logits;
+  int64_t n_tokens;
+  int64_t src_ld;
+  int64_t delta_ld;
+  int64_t out_ld;
+  int64_t out_qstride;
+  int32_t d;
+  int32_t nchunk;       /* d / elements-per-16-byte-chunk */
+  int32_t num_queries;
+  int32_t param_bf16;   /* query/gain dtype: 1 bf16, 0 fp32 */
+  int32_t out_bf16;     /* out dtype: 1 bf16, 0 fp32 */
+  int32_t mode;         /* ATTNRES_MODE_* */
+  float eps;
+  float inv_d;
+} attnres_route_params;
+
+/*
+ * Online-softmax merge of one intra-block partial into a phase-1 result:
+ *   inv_rms = rsqrt(mean(p^2)+eps); logit = (p . q) * inv_rms
+ *   pi = sigmoid(logit - inter_lse); out = inter + pi * (p - inter)
+ */
+typedef struct attnres_merge_params {
+  const void* partial;    /* (n_tokens, d), partial dtype */
+  const void* query;      /* (d,) pre-folded, param dtype */
+  const void* inter;      /* (n_tokens, d), inter dtype */
+  const float* inter_lse; /* (n_tokens,) */
+  void* out;              /* (n_tokens, d), inter dtype */
+  float* logit;           /* (n_tokens,) or NULL */
+  float* inv_rms;         /* (n_tokens,) or NULL */
+  int64_t n_tokens;
+  int64_t partial_ld;
+  int64_t inter_ld;
+  int64_t out_ld;
+  int32_t d;
+  int32_t nchunk;
+  int32_t param_bf16;
+  int32_t inter_bf16;
+  float eps;
+  float inv_d;
+} attnres_merge_params;
+
+#endif /* KOTODAMA_AMD_ATTNRES_PARAMS_H */

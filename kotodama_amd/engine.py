@@ -1,0 +1,180 @@
+"""Stack-free routing over a preallocated block arena (prefill and decode).
+
+The reference's caller loops (``_forward_attn_res``, llama.py:666-716, and
+``_forward_attn_res_cached``, llama.py:718-763) keep the committed blocks in a
+Python list and, before each of the 2L+1 routing calls, zero-pad and
+``torch.stack`` them into a fresh ``(max_S, B, T, D)`` buffer; a commit
+clones the partial and starts a zero one; every sublayer output is added to
+the partial out of place.
+
+Here the blocks live in one arena ``(max_S, *batch, D)`` allocated once per
+forward: slots ``0..n_committed-1`` are committed blocks and slot
+``n_committed`` is the running partial.  One ``attnres_hip::block_step``
+call per routing point adds the previous sublayer's output to the partial
+(or, right after a commit, starts the new partial from it), writes it back,
+and routes — a commit is only an index bump.  Per routing point this moves
+(S+3) rows instead of the reference's stack (max_S writes + S reads), route
+and separate add.
+"""
+
+from __future__ import annotations
+
+from typing import Callable, Optional, Sequence
+
+import torch
+from torch import Tensor
+
+from . import ops
+from .schedule import AttnResSchedule
+
+
+class BlockArena:
+    """The committed blocks and the partial block of one forward."""
+
+    def __init__(self, max_sources: int, batch_shape: Sequence[int], hidden: int, dtype: torch.dtype, device) -> None:
+        self.buf = torch.empty((max_sources, *batch_shape, hidden), dtype=dtype, device=device)
+        self.n_committed = 0
+
+    @property
+    def max_sources(self) -> int:
+        return self.buf.shape[0]
+
+    def start(self, embed: Tensor) -> None:
+        """Begin a forward: the embedding is the first partial block."""
+        self.buf[0].copy_(embed)
+        self.n_committed = 0
+
+    @property
+    def partial(self) -> Tensor:
+        return self.buf[self.n_committed]
+
+    @property
+    def committed(self) -> Tensor:
+        return self.buf[: self.n_committed]
+
+    def step(
+        self,
+        query: Tensor,
+        gain: Optional[Tensor],
+        eps: float,
+        delta: Optional[Tensor] = None,
+        commit: bool = False,
+        want_weights: bool = False,
+    ):
+        """One routing point: optional commit, partial update, route.
+
+        Returns the routed ``(*batch, D)`` row block, or ``(out, weights,
+        lse)`` when ``want_weights``.
+        """
+        out, w, lse = ops.block_step(self.buf, self.n_committed, commit, delta, query, gain, eps, want_weights)
+        if commit:
+            self.n_committed += 1
+        return (out, w, lse) if want_weights else out
+
+
+class AttnResRouter:
+    """The routing side of one AttnRes forward over a :class:`BlockArena`.
+
+    ``queries[j]`` / ``gains[j]`` are the pseudo-query and RMSNorm gain of
+    routing point j in the reference's order ``[attn_0, mlp_0, attn_1, ...,
+    final]`` (serve.py:85-92); ``sublayer(j, h)`` returns the residual update
+    of sublayer j (attention for even j, MLP for odd j) given its routed input.
+    """
+
+    def __init__(
+        self,
+        schedule: AttnResSchedule,
+        queries: Sequence[Tensor],
+        gains: Sequence[Optional[Tensor]],
+        eps: float,
+    ) -> None:
+        if len(queries) != schedule.num_points or len(gains) != schedule.num_points:
+            raise ValueError(f"need {schedule.num_points} queries and gains")
+        self.schedule = schedule
+        self.queries = list(queries)
+        self.gains = list(gains)
+        self.eps = float(eps)
+
+    def new_arena(self, batch_shape: Sequence[int], hidden: int, dtype: torch.dtype, device) -> BlockArena:
+        return BlockArena(self.schedule.max_sources, batch_shape, hidden, dtype, device)
+
+    def forward(
+        self,
+        embed: Tensor,
+        sublayer: Callable[[int, Tensor], Tensor],
+        arena: Optional[BlockArena] = None,
+    ) -> Tensor:
+        """Run all 2L+1 routing points; returns the final aggregation (before the final norm)."""
+        if arena is None:
+            arena = self.new_arena(embed.shape[:-1], embed.shape[-1], embed.dtype, embed.device)
+        arena.start(embed)
+        sched = self.schedule
+        delta = None
+        h = embed
+        last = sched.num_points - 1
+        for j in range(sched.num_points):
+            h = arena.step(self.queries[j], self.gains[j], self.eps, delta=delta, commit=sched.commit_before[j])
+            if j < last:
+                delta = sublayer(j, h)
+        return h
+
+
+def _model_router(model) -> AttnResRouter:
+    sched = getattr(model, "_kotodama_amd_schedule", None)
+    if sched is None:
+        sched = AttnResSchedule.build(model.config.num_layers, boundaries=sorted(model._attn_res_boundary_set))
+        model._kotodama_amd_schedule = sched
+    queries, gains = [], []
+    for layer in model.layers:
+        queries += [layer.attn_res_query, layer.mlp_res_query]
+        gains += [layer.attn_res_norm.weight, layer.mlp_res_norm.weight]
+    queries.append(model.final_res_query)
+    gains.append(model.final_res_norm.weight)
+    return AttnResRouter(sched, queries, gains, model.final_res_norm.eps)
+
+
+def forward_attn_res(model, embed: Tensor, mask: Optional[Tensor] = None) -> Tensor:
+    """Drop-in for ``LuxiaBaseModel._forward_attn_res`` (llama.py:666-716), forward only.
+
+    ``model`` has the reference's attributes (``layers[i].attn``, ``attn_norm``,
+    ``ffn``, ``ffn_norm``, the AttnRes queries and norms, ``final_res_*``,
+    ``norm``, ``rope_cos/sin``, ``_attn_res_boundary_set``).  All AttnRes
+    norms are built with the same ``config.norm_eps`` (llama.py:462,464,543),
+    so one eps serves every routing point.
+    """
+    ops.check_forward_only(embed)
+    router = _model_router(model)
+    rope_cos, rope_sin = model.rope_cos, model.rope_sin
+    layers = model.layers
+
+    def sublayer(j: int, h: Tensor) -> Tensor:
+        layer = layers[j // 2]
+        if j % 2 == 0:
+            return layer.attn(layer.attn_norm(h), rope_cos, rope_sin, mask)
+        return layer.ffn(layer.ffn_norm(h))
+
+    return model.norm(router.forward(embed, sublayer))
+
+
+def forward_attn_res_cached(model, embed: Tensor, mask: Optional[Tensor] = None, past_kv=None):
+    """Drop-in for ``_forward_attn_res_cached`` (llama.py:718-763): the KV-cache
+    engine's forward (prefill, and T=1 decode steps), returning
+    ``(hidden, new_kv_list)``."""
+    ops.check_forward_only(embed)
+    router = _model_router(model)
+    rope_cos, rope_sin = model.rope_cos, model.rope_sin
+    layers = model.layers
+    new_kv: list = []
+
+    def sublayer(j: int, h: Tensor) -> Tensor:
+        i = j // 2
+        layer = layers[i]
+        if j % 2 == 0:
+            layer_past = past_kv[i] if past_kv is not None else None
+            out, kv = layer.attn(layer.attn_norm(h), rope_cos, rope_sin, mask, layer_past, use_cache=True)
+            new_kv.append(kv)
+            return out
+        return layer.ffn(layer.ffn_norm(h))
+
+    x = router.forward(embed, sublayer)
+    return model.norm(x), new_kv

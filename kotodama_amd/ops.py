@@ -1,0 +1,384 @@
+"""torch.library registration of the routing ops (namespace ``attnres_hip``).
+
+Each op is a thin shim over the C ABI (``_capi``): it validates tensors,
+allocates outputs on torch's caching allocator, and launches on the current
+HIP stream of the inputs' device.  Fake (meta) implementations give shapes
+for ``torch.compile``.  Inputs must be ROCm device tensors: there is no CPU
+path, and the ops are forward-only (they raise if autograd would need them).
+
+Ops
+---
+``attnres_hip::route(buf, num_sources, query, gain, eps, out_dtype, want_weights, want_aux)``
+    Routing over the first ``num_sources`` slots of a stacked ``(max_S, *batch, D)``
+    buffer (``llama.py:605-644``; phase-1 ``ops/phase_1.py:11-66`` for
+    ``query`` of shape ``(Q, D)``).
+``attnres_hip::route_list(sources, query, gain, eps, out_dtype, want_weights, want_aux)``
+    Same over a list of ``(*batch, D)`` tensors, with no stacked copy.
+``attnres_hip::merge(partial, query, inter, inter_lse, eps)``
+    Phase-2 merge (``ops/phase_2.py:27-71``).
+``attnres_hip::block_step(arena, n_committed, commit, delta, query, gain, eps, want_weights)``
+    One routing point over a block arena with the partial update fused in
+    (the body of ``llama.py:697-715`` / ``742-762``); mutates ``arena``.
+
+Returned tuples always have the same arity; outputs that were not requested
+are empty tensors.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import torch
+from torch import Tensor
+
+from . import _capi
+
+_DTYPE_CODES = {torch.float32: _capi.DTYPE_F32, torch.bfloat16: _capi.DTYPE_BF16}
+_CODE_DTYPES = {v: k for k, v in _DTYPE_CODES.items()}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dt]
+    except KeyError:
+        raise TypeError(f"attnres_hip supports float32 and bfloat16 tensors, got {dt}") from None
+
+
+def _require_device(*tensors: Optional[Tensor]) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"attnres_hip runs on ROCm device tensors only (got a {t.device.type} tensor); there is no CPU path"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"attnres_hip: tensors on different devices ({dev} vs {t.device})")
+    assert dev is not None
+    return dev
+
+
+def _no_grad_needed(*tensors: Optional[Tensor]) -> None:
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise NotImplementedError(
+            "attnres_hip ops are forward-only: backward through AttnRes routing is not implemented "
+            "(run under torch.no_grad()/inference_mode, or detach the inputs)"
+        )
+
+
+class _DeviceStream:
+    """Make ``dev`` current for the C-ABI call and give its current stream."""
+
+    __slots__ = ("dev", "prev")
+
+    def __init__(self, dev: torch.device) -> None:
+        self.dev = dev
+        self.prev = None
+
+    def __enter__(self) -> int:
+        idx = self.dev.index if self.dev.index is not None else torch.cuda.current_device()
+        cur = torch.cuda.current_device()
+        if cur != idx:
+            self.prev = cur
+            torch.cuda.set_device(idx)
+        return torch.cuda.current_stream(idx).cuda_stream
+
+    def __exit__(self, *exc) -> None:
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+
+
+def _fold_query(query: Tensor, gain: Optional[Tensor]) -> tuple[Tensor, Optional[Tensor], int]:
+    """(query, gain, param dtype code) for the kernel.
+
+    The kernel folds ``query * gain`` itself and rounds the product to the
+    parameter dtype; when the two differ in dtype the fold is done here, in
+    the promoted dtype, exactly as ``query * norm.weight`` would be.
+    """
+    if gain is not None and gain.dtype != query.dtype:
+        query = query * gain
+        gain = None
+    query = query.contiguous()
+    if gain is not None:
+        gain = gain.contiguous()
+    return query, gain, dtype_code(query.dtype)
+
+
+def _outputs(
+    device: torch.device,
+    out_dtype: torch.dtype,
+    nq: int,
+    s: int,
+    batch: Sequence[int],
+    d: int,
+    want_weights: bool,
+    want_aux: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    f32 = torch.float32
+    out = torch.empty((nq, *batch, d), device=device, dtype=out_dtype)
+    empty = torch.empty((0,), device=device, dtype=f32)
+    weights = torch.empty((nq, s, *batch), device=device, dtype=f32) if want_weights else empty
+    lse = torch.empty((nq, *batch), device=device, dtype=f32) if want_weights else empty
+    inv_rms = torch.empty((*batch, s), device=device, dtype=f32) if want_aux else empty
+    logits = torch.empty((nq, *batch, s), device=device, dtype=f32) if want_aux else empty
+    return out, weights, lse, inv_rms, logits
+
+
+def _launch_route(
+    ptrs: list[int],
+    src_ld: int,
+    src_dtype: torch.dtype,
+    batch: Sequence[int],
+    d: int,
+    device: torch.device,
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    out_dtype: torch.dtype,
+    want_weights: bool,
+    want_aux: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    if query.dim() == 1:
+        query = query.unsqueeze(0)
+    if query.dim() != 2 or query.shape[1] != d:
+        raise ValueError(f"attnres_hip: query must be (D,) or (Q, D) with D={d}, got {tuple(query.shape)}")
+    if gain is not None and gain.shape != (d,):
+        raise ValueError(f"attnres_hip: gain must be ({d},), got {tuple(gain.shape)}")
+    query, gain, pcode = _fold_query(query, gain)
+    nq = query.shape[0]
+    s = len(ptrs)
+    n = 1
+    for b in batch:
+        n *= b
+    outs = _outputs(device, out_dtype, nq, s, batch, d, want_weights, want_aux)
+    out, weights, lse, inv_rms, logits = outs
+
+    def p(t: Tensor) -> Optional[int]:
+        return t.data_ptr() if t.numel() else None
+
+    with _DeviceStream(device) as stream:
+        _capi.route_fwd(
+            _capi.pointer_array(ptrs),
+            s,
+            n,
+            d,
+            src_ld,
+            dtype_code(src_dtype),
+            query.data_ptr(),
+            gain.data_ptr() if gain is not None else None,
+            nq,
+            pcode,
+            float(eps),
+            out.data_ptr() if out.numel() else None,
+            dtype_code(out_dtype),
+            d,
+            n * d,
+            p(weights),
+            p(lse),
+            p(inv_rms),
+            p(logits),
+            stream,
+        )
+    return outs
+
+
+# ------------------------------------------------------------------ route --
+
+
+@torch.library.custom_op("attnres_hip::route", mutates_args=())
+def route(
+    buf: Tensor,
+    num_sources: int,
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    out_dtype: torch.dtype,
+    want_weights: bool,
+    want_aux: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    device = _require_device(buf, query, gain)
+    if buf.dim() < 2:
+        raise ValueError("attnres_hip::route: buf must be (max_S, *batch, D)")
+    if not 0 <= num_sources <= buf.shape[0]:
+        raise ValueError(f"attnres_hip::route: num_sources={num_sources} outside [0, {buf.shape[0]}]")
+    if not buf.is_contiguous():
+        buf = buf.contiguous()
+    d = buf.shape[-1]
+    batch = tuple(buf.shape[1:-1])
+    slot = buf[0].numel() if buf.shape[0] else 0
+    es = buf.element_size()
+    base = buf.data_ptr()
+    ptrs = [base + i * slot * es for i in range(num_sources)]
+    return _launch_route(ptrs, d, buf.dtype, batch, d, device, query, gain, eps, out_dtype, want_weights, want_aux)
+
+
+@route.register_fake
+def _route_fake(buf, num_sources, query, gain, eps, out_dtype, want_weights, want_aux):
+    nq = 1 if query.dim() == 1 else query.shape[0]
+    return _outputs(buf.device, out_dtype, nq, num_sources, tuple(buf.shape[1:-1]), buf.shape[-1], want_weights, want_aux)
+
+
+@torch.library.custom_op("attnres_hip::route_list", mutates_args=())
+def route_list(
+    sources: list[Tensor],
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    out_dtype: torch.dtype,
+    want_weights: bool,
+    want_aux: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    if len(sources) == 0:
+        raise ValueError("attnres_hip::route_list: empty source list (use route with num_sources=0)")
+    device = _require_device(*sources, query, gain)
+    ref = sources[0]
+    for t in sources[1:]:
+        if t.shape != ref.shape or t.dtype != ref.dtype:
+            raise ValueError("attnres_hip::route_list: sources must share shape and dtype")
+    d = ref.shape[-1]
+    # A temporary made contiguous here is freed on return; the caching
+    # allocator reuses it only for later work on this same stream, which runs
+    # after the kernel has read it.
+    srcs = [t if t.is_contiguous() else t.contiguous() for t in sources]
+    return _launch_route(
+        [t.data_ptr() for t in srcs], d, ref.dtype, tuple(ref.shape[:-1]), d, device, query, gain, eps, out_dtype,
+        want_weights, want_aux,
+    )
+
+
+@route_list.register_fake
+def _route_list_fake(sources, query, gain, eps, out_dtype, want_weights, want_aux):
+    ref = sources[0]
+    nq = 1 if query.dim() == 1 else query.shape[0]
+    return _outputs(ref.device, out_dtype, nq, len(sources), tuple(ref.shape[:-1]), ref.shape[-1], want_weights, want_aux)
+
+
+# ------------------------------------------------------------------ merge --
+
+
+@torch.library.custom_op("attnres_hip::merge", mutates_args=())
+def merge(partial: Tensor, query: Tensor, inter: Tensor, inter_lse: Tensor, eps: float) -> tuple[Tensor, Tensor, Tensor]:
+    device = _require_device(partial, query, inter, inter_lse)
+    d = partial.shape[-1]
+    if inter.shape != partial.shape:
+        raise ValueError("attnres_hip::merge: inter must have the partial's shape")
+    if query.shape != (d,):
+        raise ValueError(f"attnres_hip::merge: query must be ({d},)")
+    if inter_lse.shape != partial.shape[:-1] or inter_lse.dtype != torch.float32:
+        raise ValueError("attnres_hip::merge: inter_lse must be fp32 of shape partial.shape[:-1]")
+    partial = partial.contiguous()
+    inter = inter.contiguous()
+    inter_lse = inter_lse.contiguous()
+    query = query.contiguous()
+    n = partial.numel() // d
+    out = torch.empty_like(inter)
+    logit = torch.empty(partial.shape[:-1], device=device, dtype=torch.float32)
+    inv_rms = torch.empty(partial.shape[:-1], device=device, dtype=torch.float32)
+    with _DeviceStream(device) as stream:
+        _capi.merge_fwd(
+            partial.data_ptr(),
+            n,
+            d,
+            dtype_code(partial.dtype),
+            query.data_ptr(),
+            dtype_code(query.dtype),
+            inter.data_ptr(),
+            dtype_code(inter.dtype),
+            inter_lse.data_ptr(),
+            float(eps),
+            out.data_ptr(),
+            logit.data_ptr() if logit.numel() else None,
+            inv_rms.data_ptr() if inv_rms.numel() else None,
+            stream,
+        )
+    return out, logit, inv_rms
+
+
+@merge.register_fake
+def _merge_fake(partial, query, inter, inter_lse, eps):
+    shp = partial.shape[:-1]
+    return (
+        torch.empty_like(inter),
+        partial.new_empty(shp, dtype=torch.float32),
+        partial.new_empty(shp, dtype=torch.float32),
+    )
+
+
+# ------------------------------------------------------------- block step --
+
+
+@torch.library.custom_op("attnres_hip::block_step", mutates_args=("arena",))
+def block_step(
+    arena: Tensor,
+    n_committed: int,
+    commit: bool,
+    delta: Optional[Tensor],
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    want_weights: bool,
+) -> tuple[Tensor, Tensor, Tensor]:
+    device = _require_device(arena, delta, query, gain)
+    if not arena.is_contiguous():
+        raise ValueError("attnres_hip::block_step: the arena must be contiguous")
+    d = arena.shape[-1]
+    batch = tuple(arena.shape[1:-1])
+    if delta is not None:
+        if delta.shape != arena.shape[1:] or delta.dtype != arena.dtype:
+            raise ValueError("attnres_hip::block_step: delta must match one arena slot in shape and dtype")
+        delta = delta.contiguous()
+    if query.shape != (d,):
+        raise ValueError(f"attnres_hip::block_step: query must be ({d},)")
+    query, gain, pcode = _fold_query(query, gain)
+    s = n_committed + int(commit) + 1
+    n = arena[0].numel() // d if arena.shape[0] else 0
+    out = torch.empty((*batch, d), device=device, dtype=arena.dtype)
+    f32 = torch.float32
+    if want_weights:
+        weights = torch.empty((s, *batch), device=device, dtype=f32)
+        lse = torch.empty(batch, device=device, dtype=f32)
+    else:
+        weights = lse = torch.empty((0,), device=device, dtype=f32)
+    with _DeviceStream(device) as stream:
+        _capi.block_step(
+            arena.data_ptr(),
+            arena.shape[0],
+            n * d,
+            n_committed,
+            int(commit),
+            delta.data_ptr() if delta is not None else None,
+            n,
+            d,
+            dtype_code(arena.dtype),
+            query.data_ptr(),
+            gain.data_ptr() if gain is not None else None,
+            pcode,
+            float(eps),
+            out.data_ptr() if out.numel() else None,
+            weights.data_ptr() if weights.numel() else None,
+            lse.data_ptr() if lse.numel() else None,
+            stream,
+        )
+    return out, weights, lse
+
+
+@block_step.register_fake
+def _block_step_fake(arena, n_committed, commit, delta, query, gain, eps, want_weights):
+    s = n_committed + int(commit) + 1
+    batch = tuple(arena.shape[1:-1])
+    out = arena.new_empty((*batch, arena.shape[-1]))
+    if want_weights:
+        return out, arena.new_empty((s, *batch), dtype=torch.float32), arena.new_empty(batch, dtype=torch.float32)
+    e = arena.new_empty((0,), dtype=torch.float32)
+    return out, e, e
+
+
+def check_forward_only(*tensors: Optional[Tensor]) -> None:
+    """Raise if autograd would have to differentiate through the ops."""
+    _no_grad_needed(*tensors)
+
+
+__all__ = ["route", "route_list", "merge", "block_step", "dtype_code", "check_forward_only"]

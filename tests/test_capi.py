@@ -1,0 +1,96 @@
+"""The C-ABI library: loads, exports every declared symbol, and rejects bad
+arguments on the host before touching the GPU (no compute calls here)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from kotodama_amd import _capi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "attnres.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(attnres_\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_the_bound_symbols():
+    assert declared_symbols() == list(_capi.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _capi.lib()
+    raw = ctypes.CDLL(str(_capi.LIB_PATH))
+    for name in declared_symbols():
+        assert hasattr(raw, name), name
+    assert lib.attnres_version() >= 10000
+    assert lib.attnres_max_sources() == _capi.MAX_SOURCES == 16
+
+
+FAKE = 0x7F0000000000  # never dereferenced: argument checks run first
+
+
+def route(sources, S=None, N=16, D=64, ld=None, sdt=_capi.DTYPE_BF16, query=FAKE, Q=1, pdt=_capi.DTYPE_BF16,
+          eps=1e-5, out=FAKE, odt=_capi.DTYPE_BF16, out_ld=None):
+    S = len(sources) if S is None else S
+    return _capi.lib().attnres_route_fwd(
+        _capi.pointer_array(sources), S, N, D, ld if ld is not None else D, sdt, query, None, Q, pdt, eps, out, odt,
+        out_ld if out_ld is not None else D, N * D, None, None, None, None, None)
+
+
+def test_route_argument_errors():
+    ok_src = [FAKE + 4096 * i for i in range(3)]
+    assert route(ok_src, N=0) == _capi.OK  # empty launch: returns before any HIP call
+    assert route([FAKE] * 17) == _capi.ERR_UNSUPPORTED
+    assert route(ok_src, S=-1) == _capi.ERR_UNSUPPORTED
+    assert route(ok_src, query=None) == _capi.ERR_ARG
+    assert route(ok_src, out=None) == _capi.ERR_ARG
+    assert route(ok_src, Q=0) == _capi.ERR_ARG
+    assert route(ok_src, sdt=7) == _capi.ERR_ARG
+    assert route(ok_src, D=12) == _capi.ERR_UNSUPPORTED  # not a multiple of 8 bf16
+    assert route(ok_src, D=8192 + 8) == _capi.ERR_UNSUPPORTED  # wider than the largest row
+    assert route(ok_src, D=64, ld=32) == _capi.ERR_ARG
+    assert route([FAKE + 2, FAKE]) == _capi.ERR_ALIGN
+    assert route(ok_src, out=FAKE + 4) == _capi.ERR_ALIGN
+    assert route(ok_src, eps=float("nan")) == _capi.ERR_ARG
+    assert route([FAKE, 0]) == _capi.ERR_ARG
+    msg = _capi.lib().attnres_last_error().decode()
+    assert "sources[1]" in msg
+    with pytest.raises(_capi.AttnResError, match="ATTNRES_ERR_UNSUPPORTED"):
+        _capi.check("attnres_route_fwd", route([FAKE] * 17))
+
+
+def step(arena=FAKE, slots=9, stride=16 * 64, nc=0, commit=0, delta=None, N=16, D=64, dt=_capi.DTYPE_BF16):
+    return _capi.lib().attnres_block_step(arena, slots, stride, nc, commit, delta, N, D, dt, FAKE, None,
+                                          _capi.DTYPE_BF16, 1e-5, FAKE, None, None, None)
+
+
+def test_block_step_argument_errors():
+    assert step(N=0) == _capi.OK
+    assert step(arena=None) == _capi.ERR_ARG
+    assert step(commit=1) == _capi.ERR_ARG  # a commit needs the new partial
+    assert step(nc=8, commit=1, delta=FAKE) == _capi.ERR_ARG  # partial slot 9 outside 9 slots
+    assert step(nc=-1) == _capi.ERR_ARG
+    assert step(commit=2) == _capi.ERR_ARG
+    assert step(stride=100) == _capi.ERR_ARG
+    assert step(slots=20, nc=16) == _capi.ERR_UNSUPPORTED
+
+
+def test_merge_argument_errors():
+    lib = _capi.lib()
+    args = [FAKE, 16, 64, _capi.DTYPE_BF16, FAKE, _capi.DTYPE_BF16, FAKE, _capi.DTYPE_BF16, FAKE, 1e-5, FAKE, None,
+            None, None]
+    a = list(args)
+    a[1] = 0
+    assert lib.attnres_merge_fwd(*a) == _capi.OK
+    a = list(args)
+    a[8] = None
+    assert lib.attnres_merge_fwd(*a) == _capi.ERR_ARG
+    a = list(args)
+    a[2] = 60
+    assert lib.attnres_merge_fwd(*a) == _capi.ERR_UNSUPPORTED

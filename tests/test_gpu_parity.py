@@ -1,0 +1,398 @@
+"""Parity of the gfx950 kernels against the float64 oracle (GPU).
+
+Tolerances (stated per the routing contract):
+* fp32 outputs:   |out - ref| <= 1e-5 * |ref| + 1e-6 * max|ref|   (allclose form)
+* routing weights: |w - w_ref| <= 1e-5 absolute (fp32 arithmetic on the same inputs)
+* bf16 outputs:   |out - ref| <= max(2e-2, 1 bf16 ulp of |ref|), ref = float64
+  oracle on the identical bf16 input values.  For |ref| >= 8 one bf16 ulp is
+  already 0.0625 > 2e-2, so a correctly rounded result cannot meet 2e-2 there;
+  the ulp term keeps the bar at "one rounding step", and the fraction of
+  elements equal to the correctly rounded oracle is asserted as well.
+The oracle runs on every row for small shapes and on sampled rows (plus
+token 0 and the last token) at the full BASELINE sizes, where size-independent
+properties (weights sum to 1, output inside the sources' per-element hull)
+are checked on every row.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import kotodama_amd
+from kotodama_amd import _capi, ops, workloads
+from kotodama_amd.engine import AttnResRouter, BlockArena
+from kotodama_amd.flash_attn_res import (
+    phase_1_batched_attention_forward_with_aux,
+    phase_1_batched_attention_triton_op,
+    phase_2_online_softmax_merge_forward_with_aux,
+)
+from kotodama_amd.schedule import AttnResSchedule
+from oracle import attnres_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+class Norm(torch.nn.Module):
+    def __init__(self, weight, eps):
+        super().__init__()
+        self.weight = torch.nn.Parameter(weight, requires_grad=False)
+        self.eps = eps
+
+
+def np64(t):
+    return t.detach().float().cpu().double().numpy()
+
+
+def bf16_ulp(x):
+    a = np.abs(x)
+    e = np.floor(np.log2(np.maximum(a, 2.0**-126)))
+    return 2.0 ** (e - 7)
+
+
+def check_bf16(out, ref, label, exact_frac=0.98):
+    out = np64(out)
+    err = np.abs(out - ref)
+    tol = np.maximum(2e-2, bf16_ulp(ref))
+    bad = err > tol
+    assert not bad.any(), f"{label}: {bad.sum()} elements over tolerance, worst err {err.max():.3e}"
+    same = np.mean(out == O.bf16_round(ref))
+    assert same >= exact_frac, f"{label}: only {same:.4f} of elements equal the correctly rounded oracle"
+
+
+def check_f32(out, ref, label):
+    out = np64(out)
+    err = np.abs(out - ref)
+    tol = 1e-5 * np.abs(ref) + 1e-6 * np.abs(ref).max()
+    assert (err <= tol).all(), f"{label}: worst rel err {(err / (np.abs(ref) + 1e-30)).max():.3e}"
+
+
+def check_weights(w, ref, label, atol=1e-5):
+    err = np.abs(np64(w) - ref).max()
+    assert err <= atol, f"{label}: weights err {err:.3e}"
+
+
+def sample_rows(n, k, seed=0):
+    rng = np.random.default_rng(seed)
+    idx = set(rng.choice(n, size=min(k, n), replace=False).tolist())
+    idx.update([0, n - 1])
+    return torch.tensor(sorted(idx), dtype=torch.long)
+
+
+def oracle_rows(pool, s, rows, qw, eps):
+    """Oracle on selected token rows of the first s slots of a (max_S, B, T, D) pool."""
+    d = pool.shape[-1]
+    src = pool[:s].reshape(s, -1, d)[:, rows.to(pool.device)]
+    return O.route(np64(src), qw, eps)
+
+
+def fold(q, g, dtype):
+    return O.fold_query(np64(q), np64(g), "bf16" if dtype == torch.bfloat16 else "f32")
+
+
+# ------------------------------------------------------------ config 1 --
+
+
+def test_cfg1_fp32_weights_and_outputs(gpu):
+    w = workloads.get("cfg1")
+    g = torch.Generator(device=gpu).manual_seed(1)
+    buf = torch.randn((3, 1, 512, 3072), generator=g, device=gpu, dtype=torch.float32)
+    query = torch.randn((3072,), generator=g, device=gpu) * 0.02
+    gain = torch.ones(3072, device=gpu)
+    out, wts, lse = kotodama_amd.route_weights(buf, 3, query, Norm(gain, w.eps))
+    torch.cuda.synchronize()
+    ref = O.route(np64(buf).reshape(3, 512, 3072), fold(query, gain, torch.float32), w.eps)
+    assert out.dtype == torch.float32 and out.shape == (1, 512, 3072)
+    assert wts.shape == (3, 1, 512)
+    check_weights(wts.reshape(3, 512), ref["weights"][0], "cfg1")
+    check_f32(out.reshape(512, 3072), ref["out"][0], "cfg1")
+    np.testing.assert_allclose(np64(lse).reshape(-1), ref["lse"][0], atol=1e-5)
+    # the drop-in returns the same tensor values
+    h = kotodama_amd.route_static(buf, query, Norm(gain, w.eps), torch.ones(3, dtype=torch.bool, device=gpu), 3)
+    assert torch.equal(h, out)
+
+
+# ------------------------------------------------- route_static, all S --
+
+
+@pytest.mark.parametrize("d", [3072, 4096, 512])
+def test_route_static_every_source_count_bf16(gpu, d):
+    max_s = 9 if d == 4096 else 8
+    g = torch.Generator(device=gpu).manual_seed(d)
+    scales = torch.exp(torch.empty(max_s, device=gpu).uniform_(math.log(0.1), math.log(10), generator=g))
+    buf = (torch.randn((max_s, 2, 96, d), generator=g, device=gpu) * scales.view(-1, 1, 1, 1)).to(torch.bfloat16)
+    query = (torch.randn(d, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    gain = (1 + 0.1 * torch.randn(d, generator=g, device=gpu)).to(torch.bfloat16)
+    norm = Norm(gain, 1e-5)
+    qw = fold(query, gain, torch.bfloat16)
+    for s in range(1, max_s + 1):
+        mask = torch.zeros(max_s, dtype=torch.bool, device=gpu)
+        mask[:s] = True
+        with torch.no_grad():
+            h = kotodama_amd.route_static(buf, query, norm, mask, s)
+            h_mask = kotodama_amd.route_static(buf, query, norm, mask)  # num_active=0: mask read on the host
+        ref = O.route(np64(buf[:s]).reshape(s, -1, d), qw, 1e-5)["out"][0].reshape(2, 96, d)
+        assert h.dtype == torch.bfloat16 and h.shape == (2, 96, d)
+        check_bf16(h, ref, f"d={d} S={s}")
+        assert torch.equal(h, h_mask)
+
+
+def test_route_static_non_prefix_mask_and_list_shim(gpu):
+    d = 3072
+    g = torch.Generator(device=gpu).manual_seed(7)
+    buf = torch.randn((6, 1, 64, d), generator=g, device=gpu).to(torch.bfloat16)
+    query = (torch.randn(d, generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+    norm = Norm(torch.ones(d, device=gpu, dtype=torch.bfloat16), 1e-5)
+    mask = torch.tensor([True, False, True, True, False, True], device=gpu)
+    h = kotodama_amd.route_static(buf, query, norm, mask)
+    sel = [0, 2, 3, 5]
+    ref = O.route(np64(buf[sel]).reshape(4, -1, d), fold(query, norm.weight, torch.bfloat16), 1e-5)["out"][0]
+    check_bf16(h.reshape(-1, d), ref, "non-prefix mask")
+    h2 = kotodama_amd.block_attn_res_from_list([buf[i] for i in sel], query, norm)
+    assert torch.equal(h, h2)
+
+
+# ------------------------------------------------------- edge cases --
+
+
+def test_zero_sources_is_nan_and_one_source_is_exact_copy(gpu):
+    d = 1024
+    buf = torch.randn((4, 3, 5, d), device=gpu).to(torch.bfloat16)
+    q = torch.randn(d, device=gpu).to(torch.bfloat16)
+    out0, _, lse0, _, _ = ops.route(buf, 0, q, None, 1e-5, torch.bfloat16, True, False)
+    assert torch.isnan(out0).all() and torch.isnan(lse0).all()
+    out1, w1, _, _, _ = ops.route(buf, 1, q, None, 1e-5, torch.bfloat16, True, False)
+    assert torch.equal(out1[0], buf[0]) and torch.all(w1 == 1)
+    f = buf.float()
+    out1f, _, _, _, _ = ops.route(f, 1, q.float(), None, 1e-5, torch.float32, False, False)
+    assert torch.equal(out1f[0], f[0])
+
+
+@pytest.mark.parametrize("n,d,s", [(1, 4096, 9), (7, 3072, 5), (1000, 520, 3), (33, 8, 2), (5, 64, 16), (300, 8192, 4)])
+def test_ragged_and_extreme_shapes(gpu, n, d, s):
+    g = torch.Generator(device=gpu).manual_seed(n * 31 + d + s)
+    buf = torch.randn((s, n, d), generator=g, device=gpu).to(torch.bfloat16)
+    q = (torch.randn(d, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    out, w, lse, inv, lg = ops.route(buf, s, q, None, 1e-5, torch.bfloat16, True, True)
+    ref = O.route(np64(buf), np64(q), 1e-5)
+    check_bf16(out[0], ref["out"][0], f"n={n} d={d} s={s}")
+    check_weights(w[0], ref["weights"][0], "ragged")
+    np.testing.assert_allclose(np64(inv), ref["inv_rms"], rtol=2e-6)
+    np.testing.assert_allclose(np64(lg[0]), ref["logits"][0], rtol=1e-4, atol=1e-4)
+
+
+def test_fp32_sources_and_mixed_parameter_dtypes(gpu):
+    d, n = 2048, 64
+    g = torch.Generator(device=gpu).manual_seed(11)
+    buf = torch.randn((4, n, d), generator=g, device=gpu)
+    q32 = torch.randn(d, generator=g, device=gpu) * 0.05
+    g32 = 1 + 0.1 * torch.randn(d, generator=g, device=gpu)
+    # fp32 sources, fp32 params -> fp32 out
+    h = kotodama_amd.route_static(buf, q32, Norm(g32, 1e-5), torch.ones(4, dtype=torch.bool, device=gpu), 4)
+    ref = O.route(np64(buf), fold(q32, g32, torch.float32), 1e-5)["out"][0]
+    check_f32(h, ref, "f32/f32")
+    # bf16 sources with fp32 params (autocast training): the einsum branch promotes to fp32
+    hb = kotodama_amd.route_static(buf.to(torch.bfloat16), q32, Norm(g32, 1e-5),
+                                   torch.ones(4, dtype=torch.bool, device=gpu), 4)
+    assert hb.dtype == torch.float32
+    refb = O.route(np64(buf.to(torch.bfloat16)), fold(q32, g32, torch.float32), 1e-5)["out"][0]
+    check_f32(hb, refb, "bf16 src / f32 params")
+    # fp32 sources with bf16 params: fold in bf16, math in fp32, fp32 out
+    qb, gb = q32.to(torch.bfloat16), g32.to(torch.bfloat16)
+    hf = kotodama_amd.route_static(buf, qb, Norm(gb, 1e-5), torch.ones(4, dtype=torch.bool, device=gpu), 4)
+    assert hf.dtype == torch.float32
+    check_f32(hf, O.route(np64(buf), fold(qb, gb, torch.bfloat16), 1e-5)["out"][0], "f32 src / bf16 params")
+
+
+def test_host_checked_errors_raise(gpu):
+    buf = torch.randn((17, 2, 64), device=gpu).to(torch.bfloat16)
+    q = torch.randn(64, device=gpu).to(torch.bfloat16)
+    with pytest.raises(_capi.AttnResError, match="UNSUPPORTED"):
+        ops.route(buf, 17, q, None, 1e-5, torch.bfloat16, False, False)
+    odd = torch.randn((2, 2, 12), device=gpu).to(torch.bfloat16)
+    with pytest.raises(_capi.AttnResError, match="UNSUPPORTED"):
+        ops.route(odd, 2, torch.randn(12, device=gpu).to(torch.bfloat16), None, 1e-5, torch.bfloat16, False, False)
+    with pytest.raises(TypeError):
+        ops.route(buf.half(), 2, q.half(), None, 1e-5, torch.float16, False, False)
+
+
+def test_forward_only_on_gpu(gpu):
+    buf = torch.randn((2, 1, 4, 64), device=gpu)
+    q = torch.zeros(64, device=gpu, requires_grad=True)
+    with pytest.raises(NotImplementedError):
+        kotodama_amd.route_static(buf, q, Norm(torch.ones(64, device=gpu), 1e-5),
+                                  torch.ones(2, dtype=torch.bool, device=gpu), 2)
+
+
+# ------------------------------------------------ full-size configs --
+
+
+def _full_config_check(gpu, name, seed, calls, rows=384):
+    w = workloads.get(name)
+    pool = workloads.make_pool(w, gpu, seed)
+    q, gn = workloads.make_params(w, gpu, seed, len(calls))
+    n = w.tokens
+    idx = sample_rows(n, rows, seed)
+    for j, s in enumerate(calls):
+        norm = Norm(gn[j], w.eps)
+        out, wts, lse = kotodama_amd.route_weights(pool, s, q[j], norm)
+        # size-independent properties on every row
+        wsum = wts.sum(0)
+        assert torch.allclose(wsum, torch.ones_like(wsum), atol=1e-5), f"{name} S={s}: weights do not sum to 1"
+        lo = pool[:s].float().amin(0)
+        hi = pool[:s].float().amax(0)
+        o = out.float()
+        slack = 1e-2 * torch.maximum(lo.abs(), hi.abs()) + 1e-3
+        assert bool(((o >= lo - slack) & (o <= hi + slack)).all()), f"{name} S={s}: output outside the source hull"
+        del lo, hi, o
+        ref = oracle_rows(pool, s, idx, fold(q[j], gn[j], w.dtype), w.eps)
+        check_bf16(out.reshape(n, -1)[idx.to(gpu)], ref["out"][0], f"{name} S={s}")
+        check_weights(wts.reshape(s, n)[:, idx.to(gpu)], ref["weights"][0], f"{name} S={s}")
+    del pool
+    torch.cuda.empty_cache()
+
+
+def test_cfg3_8b_deepest_routing_full_size(gpu):
+    _full_config_check(gpu, "cfg3", 3, (9, 9))
+
+
+def test_cfg2_3b_every_source_count_full_size(gpu):
+    _full_config_check(gpu, "cfg2", 2, tuple(range(1, 9)), rows=256)
+
+
+def test_cfg5_dd_blocks_bos_sink_full_size(gpu):
+    w = workloads.get("cfg5")
+    assert w.schedule.max_sources == 7 and max(w.calls) == 7 and sum(w.calls) == 267
+    pool = workloads.make_pool(w, gpu, 5)
+    q, gn = workloads.make_params(w, gpu, 5, 2)
+    for j, s in enumerate((4, 7)):
+        out, wts, _ = kotodama_amd.route_weights(pool, s, q[j], Norm(gn[j], w.eps))
+        # every BOS row (token 0 of each sequence, 20x magnitude) checked exactly
+        bos = torch.arange(w.batch, device=gpu) * w.seq
+        ref = O.route(np64(pool[:s].reshape(s, -1, w.hidden)[:, bos]), fold(q[j], gn[j], w.dtype), w.eps)
+        check_bf16(out.reshape(-1, w.hidden)[bos], ref["out"][0], f"cfg5 BOS S={s}")
+        check_weights(wts.reshape(s, -1)[:, bos], ref["weights"][0], f"cfg5 BOS S={s}")
+    del pool
+    _full_config_check(gpu, "cfg5", 5, (7,), rows=256)
+
+
+# ------------------------------------------------ decode / arena path --
+
+
+def test_cfg4_decode_step_block_arena(gpu):
+    w = workloads.get("cfg4")
+    sched = w.schedule
+    L = sched.num_layers
+    g = torch.Generator(device=gpu).manual_seed(4)
+    embed = torch.randn((w.batch, 1, w.hidden), generator=g, device=gpu).to(torch.bfloat16)
+    deltas = workloads.make_deltas(w, gpu, 4, 2 * L)
+    q, gn = workloads.make_params(w, gpu, 4, sched.num_points)
+    router = AttnResRouter(sched, list(q), list(gn), w.eps)
+    outs = []
+
+    def sublayer(j, h):
+        outs.append(h.clone())
+        return deltas[j]
+
+    final = router.forward(embed, sublayer)
+    outs.append(final)
+    torch.cuda.synchronize()
+    qws = [fold(q[j], gn[j], w.dtype) for j in range(sched.num_points)]
+    ref = O.block_forward(
+        np64(embed).reshape(w.batch, w.hidden),
+        [np64(deltas[j]).reshape(w.batch, w.hidden) for j in range(2 * L)],
+        qws, w.eps, L, sched.boundary_set, dtype="bf16",
+    )
+    assert len(outs) == sched.num_points == 65
+    for j in range(sched.num_points):
+        check_bf16(outs[j].reshape(w.batch, w.hidden), ref["outs"][j], f"decode point {j}")
+
+
+def test_block_arena_state_and_fp32(gpu):
+    # fp32 arena, small: the partial written back and the commit bookkeeping
+    d, n = 256, 10
+    sched = AttnResSchedule.build(3, boundaries=[0, 2])
+    g = torch.Generator(device=gpu).manual_seed(12)
+    embed = torch.randn((n, d), generator=g, device=gpu)
+    deltas = torch.randn((6, n, d), generator=g, device=gpu)
+    q = torch.randn((7, d), generator=g, device=gpu) * 0.2
+    arena = BlockArena(sched.max_sources, (n,), d, torch.float32, gpu)
+    router = AttnResRouter(sched, list(q), [None] * 7, 1e-5)
+    outs = []
+
+    def sublayer(j, h):
+        outs.append(h.clone())
+        return deltas[j]
+
+    outs.append(router.forward(embed, sublayer, arena=arena))
+    ref = O.block_forward(np64(embed), [np64(deltas[j]) for j in range(6)], [np64(q[j]) for j in range(7)], 1e-5, 3,
+                          {0, 2}, dtype="f32")
+    assert arena.n_committed == 2
+    check_f32(arena.committed[0], ref["committed"][0], "committed 0")
+    check_f32(arena.committed[1], ref["committed"][1], "committed 1")
+    check_f32(arena.partial, ref["partial"], "partial")
+    for j in range(7):
+        check_f32(outs[j], ref["outs"][j], f"arena point {j}")
+
+
+# ------------------------------------------------- phase 1 / phase 2 --
+
+
+def test_phase1_batched_queries_and_phase2_merge(gpu):
+    d = 4096
+    g = torch.Generator(device=gpu).manual_seed(21)
+    blocks = torch.randn((5, 2, 200, d), generator=g, device=gpu).to(torch.bfloat16)
+    pq = (torch.randn((4, d), generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+    out, lse, inv, lg = phase_1_batched_attention_forward_with_aux(blocks, pq, 1e-5, 5)
+    assert out.shape == (4, 2, 200, d) and out.dtype == torch.bfloat16 and lse.shape == (4, 2, 200)
+    assert inv.shape == (2, 200, 5) and lg.shape == (4, 2, 200, 5)
+    ref = O.route(np64(blocks).reshape(5, -1, d), np64(pq), 1e-5)
+    for i in range(4):
+        check_bf16(out[i].reshape(-1, d), ref["out"][i], f"phase1 q{i}")
+        np.testing.assert_allclose(np64(lse[i]).reshape(-1), ref["lse"][i], atol=2e-5)
+    out2, lse2 = phase_1_batched_attention_triton_op(blocks, pq, 1e-5, num_active=3)
+    ref3 = O.route(np64(blocks[:3]).reshape(3, -1, d), np64(pq), 1e-5)
+    check_bf16(out2[1].reshape(-1, d), ref3["out"][1], "phase1 num_active=3")
+    # phase 2: merge the partial into the committed-blocks result
+    partial = torch.randn((2, 200, d), generator=g, device=gpu).to(torch.bfloat16)
+    merged, logit, inv_p = phase_2_online_softmax_merge_forward_with_aux(partial, pq[2], out2[2], lse2[2], 1e-5)
+    assert merged.dtype == torch.bfloat16
+    mref = O.merge(np64(partial).reshape(-1, d), np64(pq[2]), np64(out2[2]).reshape(-1, d),
+                   np64(lse2[2]).reshape(-1), 1e-5)
+    check_bf16(merged.reshape(-1, d), mref["out"], "phase2")
+    np.testing.assert_allclose(np64(logit).reshape(-1), mref["logit"], rtol=1e-4, atol=1e-4)
+    # identity: merging the partial equals routing over the 4 sources directly
+    full = O.route(np.concatenate([np64(blocks[:3]).reshape(3, -1, d), np64(partial).reshape(1, -1, d)]),
+                   np64(pq[2]), 1e-5)["out"][0]
+    err = np.abs(np64(merged).reshape(-1, d) - full)
+    assert (err <= np.maximum(4e-2, 3 * bf16_ulp(full))).all()
+
+
+# ------------------------------------------------------ HIP graphs --
+
+
+def test_decode_step_graph_replays_match_eager(gpu):
+    w = workloads.get("cfg4")
+    sched = w.schedule
+    L = sched.num_layers
+    embed = torch.randn((w.batch, 1, w.hidden), device=gpu).to(torch.bfloat16)
+    deltas = workloads.make_deltas(w, gpu, 9, 2 * L)
+    q, gn = workloads.make_params(w, gpu, 9, sched.num_points)
+    router = AttnResRouter(sched, list(q), list(gn), w.eps)
+    arena = router.new_arena((w.batch, 1), w.hidden, w.dtype, gpu)
+    eager = router.forward(embed, lambda j, h: deltas[j], arena=arena).clone()
+    static_embed = embed.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        router.forward(static_embed, lambda j, h: deltas[j], arena=arena)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = router.forward(static_embed, lambda j, h: deltas[j], arena=arena)
+    for rep in range(4):
+        arena.buf.normal_()  # eager work between replays; the graph must not depend on arena contents
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), f"replay {rep} differs from eager"

@@ -1,0 +1,194 @@
+"""Pins the float64 oracle (oracle/attnres_oracle.py) without retyping it.
+
+Each check is chosen so a plausible slip in the restatement fails it:
+closed forms (a dropped eps, a sqrt(D) temperature, mean vs sum in the RMS,
+normalised instead of raw sources in the mix), invariants (wrong softmax
+axis, transposed source/token indices, mask handling), a scalar-loop brute
+force, and independent implementations (torch's bf16 cast and multiply, the
+torch CPU op sequence).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attnres_oracle as O
+from oracle import torch_cpu_path as TP
+
+
+def rnd(seed, *shape, scale=1.0):
+    return np.random.default_rng(seed).standard_normal(shape) * scale
+
+
+def test_single_source_is_exact_copy():
+    x = rnd(0, 1, 5, 16)
+    r = O.route(x, rnd(1, 16), 1e-5)
+    assert np.array_equal(r["out"][0], x[0])
+    assert np.array_equal(r["weights"], np.ones((1, 1, 5)))
+
+
+def test_zero_query_gives_uniform_mean_and_log_s_lse():
+    x = rnd(2, 4, 3, 32)
+    r = O.route(x, np.zeros(32), 1e-5)
+    np.testing.assert_allclose(r["weights"], 0.25, rtol=0, atol=1e-15)
+    np.testing.assert_allclose(r["out"][0], x.mean(axis=0), rtol=1e-13, atol=1e-14)
+    np.testing.assert_allclose(r["lse"], math.log(4), rtol=1e-14)
+
+
+@pytest.mark.parametrize("eps", [0.0, 1e-5, 0.3])
+def test_closed_form_sign_vector_construction(eps):
+    # u in {+-1}^D has mean(u^2) = 1; x_s = c_s u, qw = beta u  =>
+    # x_s.qw = c_s beta D, rsqrt(mean(x_s^2)+eps) = 1/sqrt(c_s^2+eps):
+    # logit_s = c_s beta D / sqrt(c_s^2 + eps)   (no 1/sqrt(D) temperature)
+    D = 64
+    u = np.where(np.random.default_rng(3).random(D) < 0.5, -1.0, 1.0)
+    c = np.array([0.5, -2.0, 3.0, 0.25])
+    beta = 0.01
+    x = (c[:, None] * u[None, :])[:, None, :]  # (S, 1, D)
+    r = O.route(x, beta * u, eps)
+    logit = np.array([ci * beta * D / math.sqrt(ci * ci + eps) for ci in c])
+    np.testing.assert_allclose(r["logits"][0, 0], logit, rtol=1e-13)
+    e = np.exp(logit - logit.max())
+    w = e / e.sum()
+    np.testing.assert_allclose(r["weights"][0, :, 0], w, rtol=1e-12)
+    # the mix uses the raw (un-normalised) sources: out = sum_s w_s c_s u
+    np.testing.assert_allclose(r["out"][0, 0], (w * c).sum() * u, rtol=1e-12, atol=1e-15)
+    np.testing.assert_allclose(r["inv_rms"][0], 1 / np.sqrt(c * c + eps), rtol=1e-13)
+    assert abs(r["lse"][0, 0] - (logit.max() + math.log(e.sum()))) < 1e-12
+
+
+def test_logits_invariant_to_positive_source_scaling_when_eps_zero():
+    x = rnd(4, 3, 6, 40)
+    q = rnd(5, 40, scale=0.3)
+    r1 = O.route(x, q, 0.0)
+    y = x.copy()
+    y[1] *= 7.5
+    r2 = O.route(y, q, 0.0)
+    np.testing.assert_allclose(r1["logits"], r2["logits"], rtol=1e-12)
+    np.testing.assert_allclose(r1["weights"], r2["weights"], rtol=1e-12)
+
+
+def test_permutation_equivariance_over_sources():
+    x = rnd(6, 5, 4, 24)
+    q = rnd(7, 24, scale=0.5)
+    perm = [3, 0, 4, 1, 2]
+    r1 = O.route(x, q, 1e-5)
+    r2 = O.route(x[perm], q, 1e-5)
+    np.testing.assert_allclose(r2["weights"][0], r1["weights"][0][perm], rtol=1e-12)
+    np.testing.assert_allclose(r2["out"], r1["out"], rtol=1e-12, atol=1e-14)
+
+
+def test_weights_sum_to_one_and_masked_slots_are_zero():
+    buf = rnd(8, 6, 5, 16)
+    q = rnd(9, 16)
+    mask = np.array([True, True, True, False, False, False])
+    rm = O.route_masked(buf, q, 1e-5, mask)
+    assert np.all(rm["weights"][3:] == 0.0)
+    np.testing.assert_allclose(rm["weights"].sum(axis=0), 1.0, rtol=1e-14)
+    rp = O.route(buf[:3], q, 1e-5)
+    np.testing.assert_allclose(rm["out"], rp["out"][0], rtol=1e-13, atol=1e-15)
+    # a non-prefix mask equals routing over the selected slots
+    mask2 = np.array([False, True, False, True, True, False])
+    rm2 = O.route_masked(buf, q, 1e-5, mask2)
+    rs2 = O.route(buf[mask2], q, 1e-5)
+    np.testing.assert_allclose(rm2["out"], rs2["out"][0], rtol=1e-13, atol=1e-15)
+
+
+def test_all_masked_is_nan_like_the_reference():
+    buf = rnd(10, 3, 2, 8)
+    rm = O.route_masked(buf, rnd(11, 8), 1e-5, np.zeros(3, bool))
+    assert np.isnan(rm["out"]).all()
+    r0 = O.route(np.zeros((0, 2, 8)), rnd(11, 8), 1e-5)
+    assert np.isnan(r0["out"]).all() and np.isnan(r0["lse"]).all()
+
+
+def test_bruteforce_tiny_shapes():
+    for seed in range(5):
+        S, N, D = 1 + seed % 4, 2 + seed, 3 + 2 * seed
+        x = rnd(20 + seed, S, N, D, scale=1 + seed)
+        q = rnd(40 + seed, D, scale=0.7)
+        eps = [1e-6, 1e-5, 0.1, 0.0, 2.0][seed]
+        r = O.route(x, q, eps)
+        b = O.route_bruteforce(x.tolist(), q.tolist(), eps)
+        np.testing.assert_allclose(r["out"][0], np.array(b["out"]), rtol=1e-12, atol=1e-13)
+        np.testing.assert_allclose(r["weights"][0], np.array(b["weights"]), rtol=1e-12, atol=1e-15)
+
+
+def test_multi_query_matches_single_queries():
+    x = rnd(12, 4, 7, 32)
+    q = rnd(13, 3, 32, scale=0.4)
+    r = O.route(x, q, 1e-5)
+    for i in range(3):
+        ri = O.route(x, q[i], 1e-5)
+        np.testing.assert_allclose(r["out"][i], ri["out"][0], rtol=1e-13, atol=1e-15)
+        np.testing.assert_allclose(r["lse"][i], ri["lse"][0], rtol=1e-13)
+
+
+def test_phase2_merge_equals_routing_over_one_more_source():
+    # merge(p, q, phase1(C, q), lse) == route(C u {p}, q)  (the reason phase 2 exists)
+    C = rnd(14, 3, 6, 48, scale=2.0)
+    p = rnd(15, 6, 48, scale=0.5)
+    q = rnd(16, 48, scale=0.2)
+    r1 = O.route(C, q, 1e-5)
+    m = O.merge(p, q, r1["out"][0], r1["lse"][0], 1e-5)
+    full = O.route(np.concatenate([C, p[None]]), q, 1e-5)
+    np.testing.assert_allclose(m["out"], full["out"][0], rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(m["logit"], full["logits"][0, :, 3], rtol=1e-12)
+
+
+def test_bf16_round_ties_and_against_torch():
+    # spacing of bf16 at 1.0 is 2^-7
+    vals = np.array([1.0, 1 + 2**-8, 1 + 3 * 2**-8, -(1 + 2**-8), 3.4e38, np.inf, -0.0], dtype=np.float32)
+    got = O.bf16_round(vals)
+    exp = np.array([1.0, 1.0, 1 + 2**-6, -1.0, np.inf, np.inf, -0.0], dtype=np.float32)
+    assert np.array_equal(got[:4], exp[:4])
+    assert np.isinf(got[4]) and np.isinf(got[5]) and np.signbit(got[6])
+    assert np.isnan(O.bf16_round(np.array([np.nan], np.float32))).all()
+    x = (np.random.default_rng(17).standard_normal(100000) * np.exp(np.random.default_rng(18).uniform(-20, 20, 100000))).astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(O.bf16_round(x), ref)
+
+
+def test_fold_query_matches_torch_parameter_multiply():
+    q = torch.randn(256) * 0.05
+    g = 1 + torch.randn(256) * 0.1
+    for dt, name in [(torch.bfloat16, "bf16"), (torch.float32, "f32")]:
+        qt, gt = q.to(dt), g.to(dt)
+        ref = (qt * gt).double().numpy()
+        got = O.fold_query(qt.double().numpy(), gt.double().numpy(), name)
+        assert np.array_equal(got, ref), name
+
+
+def test_torch_cpu_op_sequence_agrees_with_oracle():
+    buf = torch.randn(8, 2, 16, 96) * torch.tensor([0.5, 1, 2, 4, 1, 1, 1, 1]).view(8, 1, 1, 1)
+    buf[5:] = 0
+    qw = torch.randn(96) * 0.1
+    mask = torch.tensor([True] * 5 + [False] * 3)
+    out = TP.route_static_cpu(buf, qw, 1e-5, mask)
+    w = TP.route_weights_cpu(buf, qw, 1e-5, mask)
+    r = O.route(buf[:5].reshape(5, 32, 96).double().numpy(), qw.double().numpy(), 1e-5)
+    np.testing.assert_allclose(out.reshape(32, 96).numpy(), r["out"][0], rtol=2e-5, atol=2e-6)
+    np.testing.assert_allclose(w[:5].reshape(5, 32).numpy(), r["weights"][0], atol=1e-6)
+    assert torch.all(w[5:] == 0)
+    stacked = TP.pad_and_stack([buf[0], buf[1]], 4)
+    assert stacked.shape == (4, 2, 16, 96) and torch.all(stacked[2:] == 0)
+
+
+def test_block_forward_caller_order():
+    # L=3, boundaries {0, 2}: points see S = [1,2, 2,2, 2,3, 3]
+    L, N, D = 3, 4, 16
+    embed = rnd(30, N, D)
+    deltas = [rnd(31 + j, N, D) for j in range(2 * L)]
+    qws = [rnd(50 + j, D, scale=0.3) for j in range(2 * L + 1)]
+    r = O.block_forward(embed, deltas, qws, 1e-5, L, {0, 2}, want_weights=True)
+    assert [w.shape[0] for w in r["weights"]] == [1, 2, 2, 2, 2, 3, 3]
+    # committed block 0 is the embedding; block 1 is attn0+mlp0+attn1+mlp1
+    assert np.array_equal(r["committed"][0], embed)
+    np.testing.assert_allclose(r["committed"][1], deltas[0] + deltas[1] + deltas[2] + deltas[3], rtol=1e-13)
+    np.testing.assert_allclose(r["partial"], deltas[4] + deltas[5], rtol=1e-13)
+    # point 0 routes the embedding alone; the final point routes everything
+    assert np.array_equal(r["outs"][0], embed)
+    fin = O.route(np.stack([r["committed"][0], r["committed"][1], r["partial"]]), qws[6], 1e-5)
+    np.testing.assert_allclose(r["outs"][6], fin["out"][0], rtol=1e-13)
