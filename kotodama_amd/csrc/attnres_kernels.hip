@@ -46,6 +46,12 @@ namespace {
 
 // ---------------------------------------------------------------- helpers --
 
+// Reinterpret one 32-bit lane as fp32.  Taking the word by value matters:
+// __builtin_bit_cast applied directly to an ext_vector element lvalue
+// (bit_cast<float>(v[i])) is lowered as a cast of element 0 by this compiler.
+__device__ __forceinline__ float as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ uint32_t as_u32(float f) { return __builtin_bit_cast(uint32_t, f); }
+
 __device__ __forceinline__ float bf_lo(uint32_t u) { return __builtin_bit_cast(float, u << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t u) { return __builtin_bit_cast(float, u & 0xffff0000u); }
 
@@ -110,7 +116,7 @@ template <>
 struct Chunk<false> {  // 4 x fp32
   static constexpr int VEC = 4;
   static constexpr int BYTES = 4;
-  __device__ __forceinline__ static float elem(const u32x4& c, int e) { return __builtin_bit_cast(float, c[e]); }
+  __device__ __forceinline__ static float elem(const u32x4& c, int e) { return as_f32(c[e]); }
 };
 
 // Load VEC consecutive parameter elements (bf16 or fp32) as fp32.
@@ -262,8 +268,7 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
             } else {
 #pragma unroll
               for (int w = 0; w < 4; ++w)
-                nv[w] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, x[S - 1][k][w]) +
-                                                         __builtin_bit_cast(float, dv[w]));
+                nv[w] = as_u32(as_f32(x[S - 1][k][w]) + as_f32(dv[w]));
             }
           }
           x[S - 1][k] = nv;
@@ -392,9 +397,9 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
 #pragma unroll
             for (int h = 0; h < VEC / 4; ++h) {
               stg<u32x4>(orow + ((int64_t)chunk[k] * VEC + 4 * h) * 4,
-                         u32x4{__builtin_bit_cast(uint32_t, acc[4 * h]), __builtin_bit_cast(uint32_t, acc[4 * h + 1]),
-                               __builtin_bit_cast(uint32_t, acc[4 * h + 2]),
-                               __builtin_bit_cast(uint32_t, acc[4 * h + 3])});
+                         u32x4{as_u32(acc[4 * h]), as_u32(acc[4 * h + 1]),
+                               as_u32(acc[4 * h + 2]),
+                               as_u32(acc[4 * h + 3])});
             }
           }
         }
@@ -465,7 +470,7 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
           for (int h = 0; h < VEC / 4; ++h) {
             const u32x4 t = ldg<u32x4>(irow + ((int64_t)chunk[k] * VEC + 4 * h) * 4);
 #pragma unroll
-            for (int w = 0; w < 4; ++w) iv[k][4 * h + w] = __builtin_bit_cast(float, t[w]);
+            for (int w = 0; w < 4; ++w) iv[k][4 * h + w] = as_f32(t[w]);
           }
         }
       } else {
@@ -523,8 +528,8 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
 #pragma unroll
         for (int h = 0; h < VEC / 4; ++h) {
           stg<u32x4>(orow + ((int64_t)chunk[k] * VEC + 4 * h) * 4,
-                     u32x4{__builtin_bit_cast(uint32_t, o[4 * h]), __builtin_bit_cast(uint32_t, o[4 * h + 1]),
-                           __builtin_bit_cast(uint32_t, o[4 * h + 2]), __builtin_bit_cast(uint32_t, o[4 * h + 3])});
+                     u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]),
+                           as_u32(o[4 * h + 2]), as_u32(o[4 * h + 3])});
         }
       }
     }

@@ -118,12 +118,15 @@ def _outputs(
     want_aux: bool,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     f32 = torch.float32
+    # every returned tensor is its own allocation: custom ops may not return aliases
+    def alloc(shape, wanted):
+        return torch.empty(shape if wanted else (0,), device=device, dtype=f32)
+
     out = torch.empty((nq, *batch, d), device=device, dtype=out_dtype)
-    empty = torch.empty((0,), device=device, dtype=f32)
-    weights = torch.empty((nq, s, *batch), device=device, dtype=f32) if want_weights else empty
-    lse = torch.empty((nq, *batch), device=device, dtype=f32) if want_weights else empty
-    inv_rms = torch.empty((*batch, s), device=device, dtype=f32) if want_aux else empty
-    logits = torch.empty((nq, *batch, s), device=device, dtype=f32) if want_aux else empty
+    weights = alloc((nq, s, *batch), want_weights)
+    lse = alloc((nq, *batch), want_weights)
+    inv_rms = alloc((*batch, s), want_aux)
+    logits = alloc((nq, *batch, s), want_aux)
     return out, weights, lse, inv_rms, logits
 
 
@@ -341,7 +344,8 @@ def block_step(
         weights = torch.empty((s, *batch), device=device, dtype=f32)
         lse = torch.empty(batch, device=device, dtype=f32)
     else:
-        weights = lse = torch.empty((0,), device=device, dtype=f32)
+        weights = torch.empty((0,), device=device, dtype=f32)
+        lse = torch.empty((0,), device=device, dtype=f32)
     with _DeviceStream(device) as stream:
         _capi.block_step(
             arena.data_ptr(),
@@ -372,8 +376,7 @@ def _block_step_fake(arena, n_committed, commit, delta, query, gain, eps, want_w
     out = arena.new_empty((*batch, arena.shape[-1]))
     if want_weights:
         return out, arena.new_empty((s, *batch), dtype=torch.float32), arena.new_empty(batch, dtype=torch.float32)
-    e = arena.new_empty((0,), dtype=torch.float32)
-    return out, e, e
+    return out, arena.new_empty((0,), dtype=torch.float32), arena.new_empty((0,), dtype=torch.float32)
 
 
 def check_forward_only(*tensors: Optional[Tensor]) -> None:
