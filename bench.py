@@ -41,6 +41,7 @@ WORKLOAD_TEXT = {
     "cfg3": "8B deepest routing: D=4096, B=4, T=4096, S=9, 8 calls, bf16",
     "cfg4": "8B decode step: T=1, B=256, D=4096, 65 fused block steps (S=1..9) in one HIP graph, bf16",
     "cfg5": "3B data-driven blocks {0,3,7,12,18,23}: D=3072, B=2, T=4096, 57 calls S=1..7 (sum S=267), BOS x20, bf16",
+    "copy": "calibration: torch device copy of 1 GiB (bf16), the plain copy kernel that scales rocprof byte counters",
 }
 
 
@@ -68,6 +69,19 @@ def load_traffic(kernel_tag: str):
         return float(rec["bytes_per_launch"]), rec.get("source")
     except (ValueError, KeyError, TypeError):
         return None, None
+
+
+def kernel_name(s: int, tokens: int, hidden: int, dtype) -> str:
+    """The kernel symbol the library launches for one routing call of this shape."""
+    import ctypes
+
+    from kotodama_amd import _capi, ops
+
+    buf = ctypes.create_string_buffer(128)
+    code = ops.dtype_code(dtype)
+    _capi.check("attnres_route_kernel_name",
+                _capi.lib().attnres_route_kernel_name(s, tokens, hidden, code, code, 1, 0, buf, len(buf)))
+    return buf.value.decode()
 
 
 def cpu_baseline(w, tokens: int) -> dict:
@@ -190,6 +204,23 @@ def bench_decode(w, steps: int, warmup: int, dev):
     return elapsed, rows * w.batch * w.hidden * w.elem_bytes, step_ms
 
 
+def bench_copy(steps: int, warmup: int, dev):
+    """A plain 1 GiB device copy: its FETCH_SIZE / WRITE_SIZE counters calibrate the routing kernels' ones."""
+    import torch
+
+    n = (1 << 30) // 2
+    src = torch.randn(n, device=dev).to(torch.bfloat16)
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, 2 * n * 2
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -204,6 +235,12 @@ def main() -> int:
     from kotodama_amd import workloads
 
     dev = torch.device("cuda", 0)
+    if args.workload == "copy":
+        elapsed, nbytes = bench_copy(args.steps, args.warmup, dev)
+        ms = elapsed * 1e3 / args.steps
+        print(json.dumps({"workload": WORKLOAD_TEXT["copy"], "bytes_read": nbytes // 2, "bytes_written": nbytes // 2,
+                          "ms_per_copy": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return 0
     w = workloads.get(args.workload)
     roofline = None
     if args.workload == "cfg4":
@@ -237,7 +274,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": f"attnres_route_{'bf_d2' if w.dtype == torch.bfloat16 else 'f32_fm'}_s{dominant}_v2_q1",
+            "kernel": kernel_name(dominant, w.tokens, w.hidden, w.dtype),
             "algorithmic_bytes": dom_bytes,
             "avg_ms": round(dom_ms, 4),
         }

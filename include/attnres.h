@@ -52,6 +52,28 @@ int attnres_max_sources(void);
 /* Message for the last failed call on this thread ("" if none). */
 const char* attnres_last_error(void);
 
+/* Kernel family used by attnres_route_fwd / attnres_block_step (process-wide). */
+#define ATTNRES_POLICY_AUTO 0      /* streaming kernel for large launches, else workgroup kernel */
+#define ATTNRES_POLICY_WORKGROUP 1 /* one workgroup per token row, sources held in registers */
+#define ATTNRES_POLICY_STREAM 2    /* one wave per token row, sources streamed (where the shape allows) */
+
+/*
+ * Select the kernel family; returns the previous policy (or ATTNRES_ERR_ARG).
+ * Both families compute the same function; AUTO picks by launch size.  A
+ * tuning and testing switch with no counterpart in the reference.
+ */
+int attnres_set_kernel_policy(int policy);
+
+/*
+ * Symbol name of the kernel attnres_route_fwd (fused == 0) or
+ * attnres_block_step (fused == 1) launches for these arguments under the
+ * current policy, for matching profiler output; written NUL-terminated into
+ * buf.  Loads the code object on the current device.  No counterpart in the
+ * reference.
+ */
+int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
+                              int num_queries, int fused, char* buf, int buf_len);
+
 /*
  * Load the gfx950 code object on the current HIP device.  Optional: the
  * launch entry points call it on first use of a device.

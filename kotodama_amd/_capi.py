@@ -28,6 +28,10 @@ ERR_HIP = -4
 
 MAX_SOURCES = 16
 
+POLICY_AUTO = 0
+POLICY_WORKGROUP = 1
+POLICY_STREAM = 2
+
 _ERR_NAMES = {
     ERR_ARG: "ATTNRES_ERR_ARG",
     ERR_UNSUPPORTED: "ATTNRES_ERR_UNSUPPORTED",
@@ -40,6 +44,8 @@ EXPORTS = (
     "attnres_version",
     "attnres_max_sources",
     "attnres_last_error",
+    "attnres_set_kernel_policy",
+    "attnres_route_kernel_name",
     "attnres_init",
     "attnres_route_fwd",
     "attnres_merge_fwd",
@@ -56,6 +62,11 @@ _SIGNATURES = {
     "attnres_max_sources": ([], _c_int),
     "attnres_last_error": ([], ctypes.c_char_p),
     "attnres_init": ([], _c_int),
+    "attnres_set_kernel_policy": ([_c_int], _c_int),
+    "attnres_route_kernel_name": (
+        [_c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.c_char_p, _c_int],
+        _c_int,
+    ),
     "attnres_route_fwd": (
         [
             ctypes.POINTER(_c_vp),  # sources
@@ -181,3 +192,11 @@ def merge_fwd(*args) -> None:
 
 def block_step(*args) -> None:
     check("attnres_block_step", lib().attnres_block_step(*args))
+
+
+def set_kernel_policy(policy: int) -> int:
+    """Select the kernel family (POLICY_*); returns the previous policy."""
+    prev = lib().attnres_set_kernel_policy(policy)
+    if prev < 0:
+        check("attnres_set_kernel_policy", prev)
+    return prev

@@ -16,7 +16,6 @@ Run ``python -m kotodama_amd.build`` or call :func:`build`.
 from __future__ import annotations
 
 import os
-import shutil
 import subprocess
 import sys
 import tempfile
@@ -51,16 +50,23 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
         raise RuntimeError(f"build step failed ({res.returncode}): {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile everything; returns the path of the built shared library."""
+def build(verbose: bool = False, out_dir: Path | None = None, defines: tuple = ()) -> Path:
+    """Compile everything; returns the path of the built shared library.
+
+    ``out_dir`` (default ``kotodama_amd/lib``) and extra ``-D`` ``defines``
+    (e.g. ``("ATTNRES_NT_LOADS=0",)``) allow side-by-side variant builds.
+    """
     hipcc = str(ROCM / "bin" / "hipcc")
-    LIBDIR.mkdir(exist_ok=True)
-    with tempfile.TemporaryDirectory(prefix="attnres_build_", dir=LIBDIR) as tmp:
+    libdir = Path(out_dir) if out_dir is not None else LIBDIR
+    libdir.mkdir(parents=True, exist_ok=True)
+    extra = [f"-D{d}" for d in defines]
+    with tempfile.TemporaryDirectory(prefix="attnres_build_", dir=libdir) as tmp:
         tmpd = Path(tmp)
         procs = []
         for part in range(NUM_PARTS):
             out = tmpd / f"attnres_gfx950_part{part}.hsaco"
-            cmd = [hipcc, *HIP_FLAGS, f"-DATTNRES_PART={part}", f"-I{CSRC}", str(CSRC / "attnres_kernels.hip"), "-o", str(out)]
+            cmd = [hipcc, *HIP_FLAGS, *extra, f"-DATTNRES_PART={part}", f"-I{CSRC}", str(CSRC / "attnres_kernels.hip"),
+                   "-o", str(out)]
             if verbose:
                 print(" ".join(cmd), flush=True)
             procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
@@ -92,9 +98,7 @@ def build(verbose: bool = False) -> Path:
                 str(so_tmp),
             ]
         )
-        for part in range(NUM_PARTS):
-            shutil.copy2(tmpd / f"attnres_gfx950_part{part}.hsaco", LIBDIR / f"attnres_gfx950_part{part}.hsaco")
-        final = LIBDIR / LIB_NAME
+        final = libdir / LIB_NAME
         os.replace(so_tmp, final)  # atomic: a reader never sees a half-written library
     if verbose:
         print(f"built {final}", flush=True)

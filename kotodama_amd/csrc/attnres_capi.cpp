@@ -55,6 +55,9 @@ enum TypeCombo { kBfDot2 = 0, kBfFma = 1, kF32Fma = 2, kTypeCombos = 3 };
 constexpr int kNumS = ATTNRES_KMAX_SOURCES + 1;
 constexpr int kRouteFuncs = kTypeCombos * kNumS * 2 * 2;
 constexpr int kMergeFuncs = 4 * 2;
+constexpr int kStreamMaxChunks = 8;  // rows of up to 8 KiB
+constexpr int kStreamWaves = 4;      // waves per workgroup of the streaming kernels
+constexpr int kStreamFuncs = kTypeCombos * kStreamMaxChunks * 2;
 
 struct DeviceState {
   std::atomic<bool> loaded{false};
@@ -63,6 +66,8 @@ struct DeviceState {
   hipFunction_t route[kRouteFuncs] = {};
   int route_bpc[kRouteFuncs] = {};  // resident workgroups per CU, for the launch block size used
   int route_bpc_block[kRouteFuncs] = {};
+  hipFunction_t stream[kStreamFuncs] = {};
+  int stream_bpc[kStreamFuncs] = {};
   hipFunction_t merge[kMergeFuncs] = {};
   int merge_bpc[kMergeFuncs] = {};
   int merge_bpc_block[kMergeFuncs] = {};
@@ -70,14 +75,21 @@ struct DeviceState {
 
 DeviceState g_dev[kMaxDevices];
 std::mutex g_mu;
+std::atomic<int> g_policy{ATTNRES_POLICY_AUTO};
 
-// Tuning knobs read once: ATTNRES_V forces chunks per thread (1 or 2),
-// ATTNRES_GRID_MULT scales the resident-workgroup grid.
+// Tuning knobs read once: ATTNRES_V forces chunks per thread (1 or 2) of the
+// row-per-workgroup kernels, ATTNRES_STREAM / ATTNRES_STREAM_MIN_TOKENS choose
+// when the row-per-wave streaming kernels run, ATTNRES_GRID_MULT scales the
+// resident-workgroup grid.
 struct Tuning {
   int force_v = 0;
+  int stream = -1;  // -1: by size, 0: never, 1: whenever the shape allows
+  int64_t stream_min_tokens = 2048;
   double grid_mult = 1.0;
   Tuning() {
     if (const char* v = std::getenv("ATTNRES_V")) force_v = std::atoi(v);
+    if (const char* v = std::getenv("ATTNRES_STREAM")) stream = std::atoi(v);
+    if (const char* v = std::getenv("ATTNRES_STREAM_MIN_TOKENS")) stream_min_tokens = std::atoll(v);
     if (const char* g = std::getenv("ATTNRES_GRID_MULT")) {
       const double m = std::atof(g);
       if (m > 0.0) grid_mult = m;
@@ -124,6 +136,27 @@ int find_function(DeviceState& st, int part, const char* name, hipFunction_t* f)
     (void)hipGetLastError();  // do not leave a sticky error for the caller's runtime
     return fail(ATTNRES_ERR_HIP, "kernel %s not found in code-object part %d: %s", name, part, hipGetErrorString(e));
   }
+  return ATTNRES_OK;
+}
+
+int part_of_stream(int nch) { return nch <= 4 ? 2 : 1; }
+
+int get_stream(DeviceState& st, int combo, int nch, bool fused, hipFunction_t* f, int* bpc) {
+  const int idx = (combo * kStreamMaxChunks + (nch - 1)) * 2 + (fused ? 1 : 0);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!st.stream[idx]) {
+    static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
+    char name[96];
+    snprintf(name, sizeof(name), "attnres_stream_%s_c%d_%s", combo_names[combo], nch, fused ? "fused" : "plain");
+    int rc = find_function(st, part_of_stream(nch), name, &st.stream[idx]);
+    if (rc != ATTNRES_OK) return rc;
+    int nb = 0;
+    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.stream[idx], 64 * kStreamWaves, 0);
+    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    st.stream_bpc[idx] = nb > 0 ? nb : 1;
+  }
+  *f = st.stream[idx];
+  *bpc = st.stream_bpc[idx];
   return ATTNRES_OK;
 }
 
@@ -217,6 +250,50 @@ int launch(hipFunction_t f, int grid, int block, Params& P, void* stream) {
   return ATTNRES_OK;
 }
 
+// Which kernel a routing call runs: the row-per-wave streaming kernel (one
+// query, S >= 1, a row of whole KiB up to 8 KiB, enough rows to give every
+// wave of the chip several, or forced by the policy) or the row-per-workgroup
+// kernel with V chunks per thread.
+struct RouteChoice {
+  bool stream = false;
+  int combo = 0;
+  int nch = 0;    // streaming: KiB per row
+  int v = 0;      // workgroup: chunks per thread (0: no shape fits)
+  int block = 0;  // threads per workgroup
+};
+
+RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
+                         int num_queries, int num_cus) {
+  RouteChoice ch;
+  const bool bf = src_dtype == ATTNRES_DTYPE_BF16;
+  ch.combo = bf ? (param_dtype == ATTNRES_DTYPE_BF16 ? kBfDot2 : kBfFma) : kF32Fma;
+  const int64_t row_bytes = (int64_t)hidden * esize(src_dtype);
+  ch.nch = (int)(row_bytes / 1024);
+  const bool stream_shape = num_queries == 1 && num_sources >= 1 && row_bytes % 1024 == 0 && ch.nch >= 1 &&
+                            ch.nch <= kStreamMaxChunks;
+  const int policy = g_policy.load(std::memory_order_relaxed);
+  const int want_stream = policy == ATTNRES_POLICY_STREAM      ? 1
+                          : policy == ATTNRES_POLICY_WORKGROUP ? 0
+                                                               : tuning().stream;
+  ch.stream = stream_shape && (want_stream == 1 || (want_stream < 0 && num_tokens >= tuning().stream_min_tokens));
+  if (ch.stream) {
+    ch.block = 64 * kStreamWaves;
+  } else {
+    ch.v = pick_v(num_tokens, hidden / (bf ? 8 : 4), num_cus, &ch.block);
+  }
+  return ch;
+}
+
+void kernel_name_of(const RouteChoice& ch, int num_sources, int num_queries, bool fused, char* buf, size_t n) {
+  static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
+  if (ch.stream) {
+    snprintf(buf, n, "attnres_stream_%s_c%d_%s", combo_names[ch.combo], ch.nch, fused ? "fused" : "plain");
+  } else {
+    snprintf(buf, n, "attnres_route_%s_s%d_v%d_%s", combo_names[ch.combo], num_sources, ch.v,
+             num_queries > 1 ? "qn" : "q1");
+  }
+}
+
 // Shared validation + launch of the route kernel.  `mode`/`delta` are the
 // fused partial-update inputs of attnres_block_step.
 int route_launch(const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
@@ -271,16 +348,21 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
 
-  int block = 0;
-  const int v = pick_v(num_tokens, nchunk, st->num_cus, &block);
-  if (v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
+  const RouteChoice ch = choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus);
+  if (!ch.stream && ch.v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
 
-  const int combo = bf ? (param_dtype == ATTNRES_DTYPE_BF16 ? kBfDot2 : kBfFma) : kF32Fma;
-  const bool multiq = num_queries > 1;
   hipFunction_t f = nullptr;
   int bpc = 1;
-  rc = get_route(*st, combo, num_sources, v, multiq, block, &f, &bpc);
-  if (rc != ATTNRES_OK) return rc;
+  int block = ch.block;
+  int64_t work_units = num_tokens;  // rows per workgroup-slot of the grid
+  if (ch.stream) {
+    rc = get_stream(*st, ch.combo, ch.nch, mode != ATTNRES_MODE_PLAIN, &f, &bpc);
+    if (rc != ATTNRES_OK) return rc;
+    work_units = (num_tokens + kStreamWaves - 1) / kStreamWaves;
+  } else {
+    rc = get_route(*st, ch.combo, num_sources, ch.v, num_queries > 1, block, &f, &bpc);
+    if (rc != ATTNRES_OK) return rc;
+  }
 
   attnres_route_params P;
   std::memset(&P, 0, sizeof(P));
@@ -304,9 +386,10 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   P.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
   P.out_bf16 = out_dtype == ATTNRES_DTYPE_BF16;
   P.mode = mode;
+  P.num_sources = num_sources;
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
-  return launch(f, grid_for(num_tokens, st->num_cus, bpc), block, P, stream);
+  return launch(f, grid_for(work_units, st->num_cus, bpc), block, P, stream);
 }
 
 }  // namespace
@@ -318,6 +401,26 @@ int attnres_version(void) { return 10000; }
 int attnres_max_sources(void) { return ATTNRES_MAX_SOURCES; }
 
 const char* attnres_last_error(void) { return g_err.c_str(); }
+
+int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
+                              int num_queries, int fused, char* buf, int buf_len) {
+  if (buf == nullptr || buf_len < 1) return fail(ATTNRES_ERR_ARG, "no output buffer");
+  if (!valid_dtype(src_dtype) || !valid_dtype(param_dtype)) return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (num_sources < 0 || num_sources > ATTNRES_MAX_SOURCES || hidden <= 0 || num_queries < 1)
+    return fail(ATTNRES_ERR_ARG, "bad shape");
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  const RouteChoice ch = choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus);
+  kernel_name_of(ch, num_sources, num_queries, fused != 0, buf, (size_t)buf_len);
+  return ATTNRES_OK;
+}
+
+int attnres_set_kernel_policy(int policy) {
+  if (policy != ATTNRES_POLICY_AUTO && policy != ATTNRES_POLICY_WORKGROUP && policy != ATTNRES_POLICY_STREAM)
+    return fail(ATTNRES_ERR_ARG, "unknown kernel policy %d", policy);
+  return g_policy.exchange(policy);
+}
 
 int attnres_init(void) {
   DeviceState* st = nullptr;

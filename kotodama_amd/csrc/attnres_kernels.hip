@@ -36,6 +36,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "attnres_params.h"
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -68,14 +70,92 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          false);
 }
 
+// A wave-uniform address held in SGPRs (the value is the same in every lane).
+__device__ __forceinline__ const char* uniform_ptr(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
+}
+
 template <typename T>
 __device__ __forceinline__ T ldg(const void* p) {
   return *reinterpret_cast<const T*>(p);
+}
+
+// Source rows are read exactly once, so they are loaded with the
+// non-temporal hint; on MI355X this raised the routing kernels from ~5.0 to
+// ~5.7 TB/s at S=8.  Non-temporal stores measured slower for the output
+// rows and are off by default.  Build switches:
+#ifndef ATTNRES_NT_LOADS
+#define ATTNRES_NT_LOADS 1
+#endif
+#ifndef ATTNRES_NT_STORES
+#define ATTNRES_NT_STORES 0
+#endif
+
+// Load through an explicitly global pointer: a generic (flat) load would also
+// count against the LDS wait counter and serialise with LDS reads.
+template <typename T>
+__device__ __forceinline__ T ldg_global(const char* p) {
+  const __attribute__((address_space(1))) T* g = (const __attribute__((address_space(1))) T*)(p);
+#if ATTNRES_NT_LOADS
+  return __builtin_nontemporal_load(g);
+#else
+  return *g;
+#endif
 }
 template <typename T>
 __device__ __forceinline__ void stg(void* p, T v) {
   *reinterpret_cast<T*>(p) = v;
 }
+
+template <typename T>
+__device__ __forceinline__ void stg_global(char* p, T v) {
+  __attribute__((address_space(1))) T* g = (__attribute__((address_space(1))) T*)(p);
+#if ATTNRES_NT_STORES
+  __builtin_nontemporal_store(v, g);
+#else
+  *g = v;
+#endif
+}
+
+// In-place accumulator updates on one 32-bit source word.  The tied "+v"
+// operands keep every fp32 accumulator in one register across the softmax
+// branches (written as plain fmaf, the compiler renames the accumulator row
+// per branch and copies at the joins, doubling its register footprint), and
+// the bf16 -> fp32 unpack happens inside, so it cannot be hoisted above the
+// branch into a second copy of the row.
+//   rescale_add: acc = acc * c + x        add_scaled: acc = acc + p * x
+__device__ __forceinline__ void acc_rescale_add_bf16(float& lo, float& hi, uint32_t w, float c) {
+  float t;
+  asm("v_lshlrev_b32 %2, 16, %3\n\t"
+      "v_fma_f32 %0, %0, %4, %2\n\t"
+      "v_and_b32 %2, 0xffff0000, %3\n\t"
+      "v_fma_f32 %1, %1, %4, %2"
+      : "+v"(lo), "+v"(hi), "=&v"(t)
+      : "v"(w), "v"(c));
+}
+__device__ __forceinline__ void acc_add_scaled_bf16(float& lo, float& hi, uint32_t w, float p) {
+  float t;
+  asm("v_lshlrev_b32 %2, 16, %3\n\t"
+      "v_fmac_f32 %0, %4, %2\n\t"
+      "v_and_b32 %2, 0xffff0000, %3\n\t"
+      "v_fmac_f32 %1, %4, %2"
+      : "+v"(lo), "+v"(hi), "=&v"(t)
+      : "v"(w), "v"(p));
+}
+// The scale c / p comes straight from v_exp_f32, a transcendental op whose
+// result a VALU may only read after one wait state.  The compiler inserts
+// that wait for its own code but not inside inline asm, so every asm block
+// above starts with an instruction that does not read c / p.  The fp32
+// forms below have no unpack to put first and stay plain C.
+__device__ __forceinline__ void acc_rescale_add_f32(float& acc, uint32_t w, float c) {
+  acc = __builtin_fmaf(acc, c, as_f32(w));
+}
+__device__ __forceinline__ void acc_add_scaled_f32(float& acc, uint32_t w, float p) {
+  acc = __builtin_fmaf(as_f32(w), p, acc);
+}
+__device__ __forceinline__ void acc_zero(float& acc) { asm("v_mov_b32 %0, 0" : "+v"(acc)); }
 
 // One DPP step: v + v[permuted lane], restricted to the rows in ROW_MASK.
 template <int CTRL, int ROW_MASK>
@@ -246,7 +326,7 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
           if (s == S - 1 && P.mode == ATTNRES_MODE_SET) {
             x[s][k] = u32x4{0, 0, 0, 0};
           } else {
-            x[s][k] = ok[k] ? ldg<u32x4>(row + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
+            x[s][k] = ok[k] ? ldg_global<u32x4>(row + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
           }
         }
       }
@@ -387,16 +467,17 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
           }
           if (P.out_bf16) {
             if constexpr (VEC == 8) {
-              stg<u32x4>(orow + (int64_t)chunk[k] * 16,
-                         u32x4{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3]), pack_bf16(acc[4], acc[5]),
-                               pack_bf16(acc[6], acc[7])});
+              stg_global<u32x4>(orow + (int64_t)chunk[k] * 16,
+                                u32x4{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3]), pack_bf16(acc[4], acc[5]),
+                                      pack_bf16(acc[6], acc[7])});
             } else {
-              stg<u32x2>(orow + (int64_t)chunk[k] * 8, u32x2{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3])});
+              stg_global<u32x2>(orow + (int64_t)chunk[k] * 8,
+                                u32x2{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3])});
             }
           } else {
 #pragma unroll
             for (int h = 0; h < VEC / 4; ++h) {
-              stg<u32x4>(orow + ((int64_t)chunk[k] * VEC + 4 * h) * 4,
+              stg_global<u32x4>(orow + ((int64_t)chunk[k] * VEC + 4 * h) * 4,
                          u32x4{as_u32(acc[4 * h]), as_u32(acc[4 * h + 1]),
                                as_u32(acc[4 * h + 2]),
                                as_u32(acc[4 * h + 3])});
@@ -536,6 +617,291 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
   }
 }
 
+
+// ------------------------------------------------------ stream body --
+//
+// Prefill kernel: one wave64 owns one token row at a time, and the S source
+// rows stream through a two-deep register pipeline (slots A and B): the load
+// of the next (token, source) item is issued before the current one is
+// processed, across token boundaries, so every wave keeps a row of HBM reads
+// in flight.  Lane l holds the 16-byte chunks l, l+64, ... (NCH chunks of a
+// row of NCH KiB), so each wave-wide load covers 1 KiB contiguous.
+//
+// Per source: sum(x^2) and x.qw over the lane's chunks, one DPP wave
+// reduction each (no LDS, no barrier), then an online depth softmax with
+// wave-uniform state (m, l):
+//   first source      m = logit, l = 1,               acc = x
+//   new maximum       c = exp(m - logit), l = l*c+1,  acc = acc*c + x
+//   otherwise         p = exp(logit - m), l += p,     acc = acc + p*x
+// so the rescale and the accumulate are one FMA per element.  The output row
+// is acc / l; lse = m + log(l).  Lane s keeps logit_s and inv_rms_s for the
+// optional weight / aux outputs.  qw sits in LDS, loaded once per workgroup.
+//
+// FUSED: the last slot is the partial block, updated in-kernel from `delta`
+// (MODE_ACCUM: partial + delta, MODE_SET: delta) and written back; the delta
+// row is prefetched with the partial row.
+
+#define ATTNRES_STREAM_WAVES 4
+
+template <int NCH, bool BF16, bool QDOT2, bool FUSED>
+__device__ __forceinline__ void stream_body(const attnres_route_params& P) {
+  const int S = P.num_sources;
+  using C = Chunk<BF16>;
+  constexpr int VEC = C::VEC;
+  constexpr int QF = QDOT2 ? 1 : NCH * 64 * VEC;
+  constexpr int QB = QDOT2 ? NCH * 64 : 1;
+  __shared__ u32x4 qw_b[QB];
+  __shared__ float qw_f[QF];
+  // Source base addresses, indexed by the runtime source number.  Reading
+  // them from the kernel arguments with a runtime index compiles to a vector
+  // load whose wait would also drain the row prefetch; LDS reads are counted
+  // separately (lgkmcnt).
+  __shared__ uint64_t src_base[ATTNRES_KMAX_SOURCES + 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
+
+  // ---- folded query into LDS, once per workgroup ----
+  for (int i = tid; i < NCH * 64; i += blockDim.x) {
+    float t[VEC];
+    load_qw<VEC>(P, 0, i, t);
+    if constexpr (QDOT2) {
+      u32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = pack_bf16(t[2 * e], t[2 * e + 1]);
+      qw_b[i] = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) qw_f[i * VEC + e] = t[e];
+    }
+  }
+  if (tid < S) src_base[tid] = reinterpret_cast<uint64_t>(P.src[tid]);
+  if (tid == 0) src_base[ATTNRES_KMAX_SOURCES] = reinterpret_cast<uint64_t>(P.delta);
+  __syncthreads();
+
+  const int64_t nw = (int64_t)gridDim.x * ATTNRES_STREAM_WAVES;
+  int64_t tok = (int64_t)blockIdx.x * ATTNRES_STREAM_WAVES + wave;
+  if (tok >= P.n_tokens) return;  // no barrier follows
+
+  const int64_t row_bytes = P.src_ld * C::BYTES;
+  const int64_t delta_row_bytes = P.delta_ld * C::BYTES;
+  const int mode = FUSED ? P.mode : ATTNRES_MODE_PLAIN;
+
+  u32x4 bufA[NCH], bufB[NCH];
+  u32x4 dA[FUSED ? NCH : 1], dB[FUSED ? NCH : 1];
+
+  auto load_item = [&](u32x4(&buf)[NCH], u32x4(&dbuf)[FUSED ? NCH : 1], int64_t t, int s) {
+    const bool from_delta = FUSED && s == S - 1 && mode == ATTNRES_MODE_SET;
+    const uint64_t base = src_base[from_delta ? ATTNRES_KMAX_SOURCES : s];
+    const char* row = uniform_ptr(base + (uint64_t)(t * (from_delta ? delta_row_bytes : row_bytes)));
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) buf[c] = ldg_global<u32x4>(row + (uint32_t)(c * 1024 + lane * 16));
+    if constexpr (FUSED) {
+      if (s == S - 1 && mode == ATTNRES_MODE_ACCUM) {
+        const char* drow = uniform_ptr(src_base[ATTNRES_KMAX_SOURCES] + (uint64_t)(t * delta_row_bytes));
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) dbuf[c] = ldg_global<u32x4>(drow + (uint32_t)(c * 1024 + lane * 16));
+      }
+    }
+    // keep the prefetch ahead of the work on the current row
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  float acc[NCH][VEC];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[c][e] = 0.f;
+  }
+  float m = -__builtin_inff(), l = 0.f;
+  float my_logit = 0.f, my_inv = 0.f;  // lane s: logit and inv_rms of source s
+
+  auto process = [&](u32x4(&x)[NCH], u32x4(&dbuf)[FUSED ? NCH : 1], int64_t t, int s, auto slot) {
+    // A distinct marker per pipeline slot keeps the compiler from merging the
+    // two unrolled halves into one body (which would copy the row buffers
+    // through phis and wait for the prefetch before using the current row).
+    if constexpr (decltype(slot)::value == 0) {
+      asm volatile("; attnres stream slot A");
+    } else {
+      asm volatile("; attnres stream slot B");
+    }
+    if constexpr (FUSED) {
+      if (s == S - 1 && mode != ATTNRES_MODE_PLAIN) {
+        if (mode == ATTNRES_MODE_ACCUM) {
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              if constexpr (BF16) {
+                x[c][w] = pack_bf16(bf_lo(x[c][w]) + bf_lo(dbuf[c][w]), bf_hi(x[c][w]) + bf_hi(dbuf[c][w]));
+              } else {
+                x[c][w] = as_u32(as_f32(x[c][w]) + as_f32(dbuf[c][w]));
+              }
+            }
+          }
+        }
+        char* prow = const_cast<char*>(uniform_ptr(src_base[S - 1] + (uint64_t)(t * row_bytes)));
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) stg_global<u32x4>(prow + (uint32_t)(c * 1024 + lane * 16), x[c]);
+      }
+    }
+
+    // ---- sum(x^2) and x.qw over this lane's chunks (two chains each) ----
+    float ss0 = 0.f, ss1 = 0.f, dt0 = 0.f, dt1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if constexpr (QDOT2) {
+        const u32x4 q = qw_b[c * 64 + lane];
+        ss0 = dot2_bf16(x[c][0], x[c][0], ss0);
+        dt0 = dot2_bf16(x[c][0], q[0], dt0);
+        ss1 = dot2_bf16(x[c][1], x[c][1], ss1);
+        dt1 = dot2_bf16(x[c][1], q[1], dt1);
+        ss0 = dot2_bf16(x[c][2], x[c][2], ss0);
+        dt0 = dot2_bf16(x[c][2], q[2], dt0);
+        ss1 = dot2_bf16(x[c][3], x[c][3], ss1);
+        dt1 = dot2_bf16(x[c][3], q[3], dt1);
+      } else {
+        const float* q = &qw_f[(c * 64 + lane) * VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float v = C::elem(x[c], e);
+          if (e & 1) {
+            ss1 = __builtin_fmaf(v, v, ss1);
+            dt1 = __builtin_fmaf(v, q[e], dt1);
+          } else {
+            ss0 = __builtin_fmaf(v, v, ss0);
+            dt0 = __builtin_fmaf(v, q[e], dt0);
+          }
+        }
+      }
+    }
+    float ss = wave_sum_to_lane63(ss0 + ss1);
+    float dt = wave_sum_to_lane63(dt0 + dt1);
+    ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ss), 63));
+    dt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dt), 63));
+    const float inv = __builtin_amdgcn_rsqf(ss * P.inv_d + P.eps);
+    const float logit = dt * inv;
+    if (lane == s) {
+      my_logit = logit;
+      my_inv = inv;
+    }
+
+    // ---- online softmax over depth, rescale folded into the FMA ----
+    // State at a token's first source: m = -inf, l = 0, acc = 0, so the
+    // first source takes the "new maximum" path with c = exp(-inf) = 0.
+    if (logit > m) {
+      const float cf = __expf(m - logit);
+      l = __builtin_fmaf(l, cf, 1.f);
+      m = logit;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          if constexpr (BF16) acc_rescale_add_bf16(acc[c][2 * w], acc[c][2 * w + 1], x[c][w], cf);
+          else acc_rescale_add_f32(acc[c][w], x[c][w], cf);
+        }
+      }
+    } else {
+      const float pr = __expf(logit - m);
+      l += pr;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          if constexpr (BF16) acc_add_scaled_bf16(acc[c][2 * w], acc[c][2 * w + 1], x[c][w], pr);
+          else acc_add_scaled_f32(acc[c][w], x[c][w], pr);
+        }
+      }
+    }
+
+    if (s == S - 1) {
+      // ---- finalize the token row ----
+      // Store addresses: a wave-uniform row base (SGPRs) plus a 32-bit lane offset.
+      const float rl = 1.0f / l;
+      const int oes = P.out_bf16 ? 2 : 4;
+      char* orow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.out) + (uint64_t)(t * P.out_ld * oes)));
+      // Byte offset of this lane's first output element, made opaque so the
+      // per-chunk offsets are recomputed here (mostly as immediate offsets)
+      // rather than hoisted out of the loop and kept live in registers.
+      uint32_t lane_ob = (uint32_t)lane * (uint32_t)(VEC * oes);
+      asm volatile("" : "+v"(lane_ob));
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        float o[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = acc[c][e] * rl;
+        if (P.out_bf16) {
+          char* dst = orow + lane_ob + (uint32_t)(c * 64 * VEC * 2);
+          if constexpr (VEC == 8) {
+            stg_global<u32x4>(dst, u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]),
+                                         pack_bf16(o[6], o[7])});
+          } else {
+            stg_global<u32x2>(dst, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
+          }
+        } else {
+          char* dst = orow + lane_ob + (uint32_t)(c * 64 * VEC * 4);
+#pragma unroll
+          for (int h = 0; h < VEC / 4; ++h) {
+            stg_global<u32x4>(dst + 16 * h, u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]), as_u32(o[4 * h + 2]),
+                                                  as_u32(o[4 * h + 3])});
+          }
+        }
+      }
+      if (P.weights || P.logits || P.inv_rms || P.lse) {
+        if (lane < S) {
+          if (P.weights) P.weights[(int64_t)lane * P.n_tokens + t] = __expf(my_logit - m) * rl;
+          if (P.logits) P.logits[t * S + lane] = my_logit;
+          if (P.inv_rms) P.inv_rms[t * S + lane] = my_inv;
+        }
+        if (lane == 0 && P.lse) P.lse[t] = m + __logf(l);
+      }
+      m = -__builtin_inff();
+      l = 0.f;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc_zero(acc[c][e]);
+      }
+    }
+  };
+
+  // ---- two-slot pipeline over this wave's (token, source) items ----
+  // The prefetch is issued unconditionally (past the last item it re-reads
+  // the current, valid row) so the wait before each use is exactly "all but
+  // the prefetch", with no branch around the loads.
+  using SlotA = std::integral_constant<int, 0>;
+  using SlotB = std::integral_constant<int, 1>;
+  int s = 0;
+  load_item(bufA, dA, tok, 0);
+  while (true) {
+    int64_t t2 = tok;
+    int s2 = s + 1;
+    if (s2 == S) {
+      s2 = 0;
+      t2 += nw;
+    }
+    bool more = t2 < P.n_tokens;
+    load_item(bufB, dB, more ? t2 : tok, more ? s2 : s);
+    process(bufA, dA, tok, s, SlotA{});
+    if (!more) break;
+    tok = t2;
+    s = s2;
+    t2 = tok;
+    s2 = s + 1;
+    if (s2 == S) {
+      s2 = 0;
+      t2 += nw;
+    }
+    more = t2 < P.n_tokens;
+    load_item(bufA, dA, more ? t2 : tok, more ? s2 : s);
+    process(bufB, dB, tok, s, SlotB{});
+    if (!more) break;
+    tok = t2;
+    s = s2;
+  }
+}
+
 }  // namespace
 
 // ------------------------------------------------------- instantiations --
@@ -612,4 +978,39 @@ ROUTE_S(16)
 
 MERGE_V(1)
 MERGE_V(2)
+#endif
+
+// Streaming kernels: attnres_stream_<in>_<qw>_c<NCH>_<plain|fused>, row = NCH KiB.
+// Occupancy target (waves per SIMD): two row buffers + the fp32 accumulator
+// fit 128 VGPRs up to 6 KiB rows, 168 up to 8 KiB.
+#define STREAM_WAVES_PER_EU(NCH) ((NCH) <= 4 ? 4 : (NCH) <= 6 ? 3 : 2)
+
+#define STREAM_ONE(INNAME, BF, QNAME, QD2, NCH)                                                         \
+  extern "C" __global__ void __launch_bounds__(64 * ATTNRES_STREAM_WAVES)                               \
+      __attribute__((amdgpu_waves_per_eu(STREAM_WAVES_PER_EU(NCH))))                                    \
+      attnres_stream_##INNAME##_##QNAME##_c##NCH##_plain(attnres_route_params P) {              \
+    stream_body<NCH, BF, QD2, false>(P);                                                             \
+  }                                                                                                     \
+  extern "C" __global__ void __launch_bounds__(64 * ATTNRES_STREAM_WAVES)                               \
+      __attribute__((amdgpu_waves_per_eu(STREAM_WAVES_PER_EU(NCH))))                                    \
+      attnres_stream_##INNAME##_##QNAME##_c##NCH##_fused(attnres_route_params P) {              \
+    stream_body<NCH, BF, QD2, true>(P);                                                              \
+  }
+
+#define STREAM_TYPES(NCH)                 \
+  STREAM_ONE(bf, true, d2, true, NCH)     \
+  STREAM_ONE(bf, true, fm, false, NCH)    \
+  STREAM_ONE(f32, false, fm, false, NCH)
+
+#if ATTNRES_PART == 2 || defined(ATTNRES_ALL_PARTS)
+STREAM_TYPES(1)
+STREAM_TYPES(2)
+STREAM_TYPES(3)
+STREAM_TYPES(4)
+#endif
+#if ATTNRES_PART == 1 || defined(ATTNRES_ALL_PARTS)
+STREAM_TYPES(5)
+STREAM_TYPES(6)
+STREAM_TYPES(7)
+STREAM_TYPES(8)
 #endif

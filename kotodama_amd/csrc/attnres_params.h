@@ -54,6 +54,7 @@ typedef struct attnres_route_params {
   int32_t param_bf16;   /* query/gain dtype: 1 bf16, 0 fp32 */
   int32_t out_bf16;     /* out dtype: 1 bf16, 0 fp32 */
   int32_t mode;         /* ATTNRES_MODE_* */
+  int32_t num_sources;  /* S (the streaming kernels read it; the others are specialised on it) */
   float eps;
   float inv_d;
 } attnres_route_params;

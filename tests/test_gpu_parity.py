@@ -41,6 +41,15 @@ class Norm(torch.nn.Module):
         self.eps = eps
 
 
+@pytest.fixture(params=["workgroup", "stream"])
+def policy(request, gpu):
+    """Run the test with each kernel family (stream falls back where the shape does not allow it)."""
+    code = {"workgroup": _capi.POLICY_WORKGROUP, "stream": _capi.POLICY_STREAM}[request.param]
+    prev = _capi.set_kernel_policy(code)
+    yield request.param
+    _capi.set_kernel_policy(prev)
+
+
 def np64(t):
     return t.detach().float().cpu().double().numpy()
 
@@ -117,7 +126,7 @@ def test_cfg1_fp32_weights_and_outputs(gpu):
 
 
 @pytest.mark.parametrize("d", [3072, 4096, 512])
-def test_route_static_every_source_count_bf16(gpu, d):
+def test_route_static_every_source_count_bf16(gpu, policy, d):
     max_s = 9 if d == 4096 else 8
     g = torch.Generator(device=gpu).manual_seed(d)
     scales = torch.exp(torch.empty(max_s, device=gpu).uniform_(math.log(0.1), math.log(10), generator=g))
@@ -138,7 +147,7 @@ def test_route_static_every_source_count_bf16(gpu, d):
         assert torch.equal(h, h_mask)
 
 
-def test_route_static_non_prefix_mask_and_list_shim(gpu):
+def test_route_static_non_prefix_mask_and_list_shim(gpu, policy):
     d = 3072
     g = torch.Generator(device=gpu).manual_seed(7)
     buf = torch.randn((6, 1, 64, d), generator=g, device=gpu).to(torch.bfloat16)
@@ -156,7 +165,7 @@ def test_route_static_non_prefix_mask_and_list_shim(gpu):
 # ------------------------------------------------------- edge cases --
 
 
-def test_zero_sources_is_nan_and_one_source_is_exact_copy(gpu):
+def test_zero_sources_is_nan_and_one_source_is_exact_copy(gpu, policy):
     d = 1024
     buf = torch.randn((4, 3, 5, d), device=gpu).to(torch.bfloat16)
     q = torch.randn(d, device=gpu).to(torch.bfloat16)
@@ -170,7 +179,7 @@ def test_zero_sources_is_nan_and_one_source_is_exact_copy(gpu):
 
 
 @pytest.mark.parametrize("n,d,s", [(1, 4096, 9), (7, 3072, 5), (1000, 520, 3), (33, 8, 2), (5, 64, 16), (300, 8192, 4)])
-def test_ragged_and_extreme_shapes(gpu, n, d, s):
+def test_ragged_and_extreme_shapes(gpu, policy, n, d, s):
     g = torch.Generator(device=gpu).manual_seed(n * 31 + d + s)
     buf = torch.randn((s, n, d), generator=g, device=gpu).to(torch.bfloat16)
     q = (torch.randn(d, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
@@ -182,7 +191,7 @@ def test_ragged_and_extreme_shapes(gpu, n, d, s):
     np.testing.assert_allclose(np64(lg[0]), ref["logits"][0], rtol=1e-4, atol=1e-4)
 
 
-def test_fp32_sources_and_mixed_parameter_dtypes(gpu):
+def test_fp32_sources_and_mixed_parameter_dtypes(gpu, policy):
     d, n = 2048, 64
     g = torch.Generator(device=gpu).manual_seed(11)
     buf = torch.randn((4, n, d), generator=g, device=gpu)
@@ -280,7 +289,7 @@ def test_cfg5_dd_blocks_bos_sink_full_size(gpu):
 # ------------------------------------------------ decode / arena path --
 
 
-def test_cfg4_decode_step_block_arena(gpu):
+def test_cfg4_decode_step_block_arena(gpu, policy):
     w = workloads.get("cfg4")
     sched = w.schedule
     L = sched.num_layers
@@ -309,7 +318,7 @@ def test_cfg4_decode_step_block_arena(gpu):
         check_bf16(outs[j].reshape(w.batch, w.hidden), ref["outs"][j], f"decode point {j}")
 
 
-def test_block_arena_state_and_fp32(gpu):
+def test_block_arena_state_and_fp32(gpu, policy):
     # fp32 arena, small: the partial written back and the commit bookkeeping
     d, n = 256, 10
     sched = AttnResSchedule.build(3, boundaries=[0, 2])
@@ -372,7 +381,7 @@ def test_phase1_batched_queries_and_phase2_merge(gpu):
 # ------------------------------------------------------ HIP graphs --
 
 
-def test_decode_step_graph_replays_match_eager(gpu):
+def test_decode_step_graph_replays_match_eager(gpu, policy):
     w = workloads.get("cfg4")
     sched = w.schedule
     L = sched.num_layers
