@@ -1,0 +1,112 @@
+"""A small model with the reference's AttnRes attribute layout (llama.py:446-551),
+for testing the caller-level drop-ins.  Sublayers are cheap deterministic maps,
+not attention/FFN; only the routing path around them matters here."""
+
+import math
+
+import numpy as np
+import torch
+from torch import nn
+
+from oracle import attnres_oracle as O
+
+
+class TinyNorm(nn.Module):
+    def __init__(self, d, eps):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(d))
+
+    def forward(self, x):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps) * self.weight.float()).to(x.dtype)
+
+
+class TinyAttn(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.proj = nn.Linear(d, d, bias=False)
+
+    def forward(self, x, rope_cos, rope_sin, mask=None, layer_past=None, use_cache=False):
+        y = torch.tanh(self.proj(x)) * 0.5
+        if use_cache:
+            return y, (x[..., :4].clone(), x[..., :4].clone())
+        return y
+
+
+class TinyFFN(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.proj = nn.Linear(d, d, bias=False)
+
+    def forward(self, x):
+        return torch.sin(self.proj(x)) * 0.5
+
+
+class TinyLayer(nn.Module):
+    def __init__(self, d, eps):
+        super().__init__()
+        self.attn_norm = TinyNorm(d, eps)
+        self.attn = TinyAttn(d)
+        self.ffn_norm = TinyNorm(d, eps)
+        self.ffn = TinyFFN(d)
+        self.attn_res_query = nn.Parameter(torch.zeros(d))
+        self.attn_res_norm = TinyNorm(d, eps)
+        self.mlp_res_query = nn.Parameter(torch.zeros(d))
+        self.mlp_res_norm = TinyNorm(d, eps)
+
+
+class Cfg:
+    def __init__(self, num_layers, norm_eps):
+        self.num_layers = num_layers
+        self.norm_eps = norm_eps
+
+
+class TinyModel(nn.Module):
+    def __init__(self, d=512, num_layers=4, boundaries=(0, 2), eps=1e-5, seed=0):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        self.config = Cfg(num_layers, eps)
+        self.layers = nn.ModuleList([TinyLayer(d, eps) for _ in range(num_layers)])
+        self.final_res_query = nn.Parameter(torch.zeros(d))
+        self.final_res_norm = TinyNorm(d, eps)
+        self.norm = TinyNorm(d, eps)
+        self._attn_res_boundary_set = frozenset(boundaries)
+        self.register_buffer("rope_cos", torch.zeros(1))
+        self.register_buffer("rope_sin", torch.zeros(1))
+        with torch.no_grad():
+            for p in self.parameters():
+                if p.dim() == 2:
+                    p.copy_(torch.randn(p.shape, generator=g) / math.sqrt(p.shape[1]))
+            for layer in self.layers:
+                for q in (layer.attn_res_query, layer.mlp_res_query):
+                    q.copy_(torch.randn(d, generator=g) * 0.1)
+                for n in (layer.attn_res_norm, layer.mlp_res_norm):
+                    n.weight.copy_(1 + 0.1 * torch.randn(d, generator=g))
+            self.final_res_query.copy_(torch.randn(d, generator=g) * 0.1)
+
+
+def reference_forward_f64(model, embed):
+    """llama.py:666-716 in float64 on the CPU, routing through the oracle."""
+    m = model.double().cpu() if next(model.parameters()).dtype != torch.float64 else model
+    x = embed.double().cpu()
+    shape = x.shape
+    d = shape[-1]
+
+    def route(srcs, q, norm):
+        qw = (q.detach() * norm.weight.detach()).numpy()
+        r = O.route(np.stack([s.reshape(-1, d).numpy() for s in srcs]), qw, norm.eps)
+        return torch.from_numpy(r["out"][0]).reshape(shape)
+
+    committed, partial = [], x
+    with torch.no_grad():
+        for i, layer in enumerate(m.layers):
+            h = route(committed + [partial], layer.attn_res_query, layer.attn_res_norm)
+            if i in m._attn_res_boundary_set:
+                committed.append(partial.clone())
+                partial = torch.zeros_like(partial)
+            partial = partial + layer.attn(layer.attn_norm(h), None, None)
+            h = route(committed + [partial], layer.mlp_res_query, layer.mlp_res_norm)
+            partial = partial + layer.ffn(layer.ffn_norm(h))
+        h = route(committed + [partial], m.final_res_query, m.final_res_norm)
+        return m.norm(h)
