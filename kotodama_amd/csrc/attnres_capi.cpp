@@ -263,14 +263,17 @@ struct RouteChoice {
 };
 
 RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
-                         int num_queries, int num_cus) {
+                         int num_queries, int num_cus, bool equally_spaced) {
   RouteChoice ch;
   const bool bf = src_dtype == ATTNRES_DTYPE_BF16;
   ch.combo = bf ? (param_dtype == ATTNRES_DTYPE_BF16 ? kBfDot2 : kBfFma) : kF32Fma;
   const int64_t row_bytes = (int64_t)hidden * esize(src_dtype);
   ch.nch = (int)(row_bytes / 1024);
+  // The streaming kernel addresses source s as src[0] + s*stride with 32-bit
+  // row/item counters.
   const bool stream_shape = num_queries == 1 && num_sources >= 1 && row_bytes % 1024 == 0 && ch.nch >= 1 &&
-                            ch.nch <= kStreamMaxChunks;
+                            ch.nch <= kStreamMaxChunks && equally_spaced &&
+                            num_tokens * (int64_t)num_sources < (int64_t)1 << 31;
   const int policy = g_policy.load(std::memory_order_relaxed);
   const int want_stream = policy == ATTNRES_POLICY_STREAM      ? 1
                           : policy == ATTNRES_POLICY_WORKGROUP ? 0
@@ -348,7 +351,16 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
 
-  const RouteChoice ch = choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus);
+  // Equally spaced sources (stacked buffers, arenas) get one base + stride.
+  int64_t src_stride = 0;
+  bool equally_spaced = true;
+  if (num_sources >= 2) {
+    src_stride = (int64_t)((uintptr_t)sources[1] - (uintptr_t)sources[0]);
+    for (int s = 2; s < num_sources && equally_spaced; ++s)
+      equally_spaced = (int64_t)((uintptr_t)sources[s] - (uintptr_t)sources[0]) == src_stride * s;
+  }
+  const RouteChoice ch =
+      choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus, equally_spaced);
   if (!ch.stream && ch.v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
 
   hipFunction_t f = nullptr;
@@ -380,6 +392,7 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   P.delta_ld = delta_ld;
   P.out_ld = out_ld;
   P.out_qstride = out_qstride;
+  P.src_stride = src_stride;
   P.d = hidden;
   P.nchunk = nchunk;
   P.num_queries = num_queries;
@@ -411,7 +424,8 @@ int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, i
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
-  const RouteChoice ch = choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus);
+  const RouteChoice ch =
+      choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus, true);
   kernel_name_of(ch, num_sources, num_queries, fused != 0, buf, (size_t)buf_len);
   return ATTNRES_OK;
 }

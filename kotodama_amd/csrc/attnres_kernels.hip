@@ -70,6 +70,13 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          false);
 }
 
+// A wave-uniform 64-bit integer kept in SGPRs.
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // A wave-uniform address held in SGPRs (the value is the same in every lane).
 __device__ __forceinline__ const char* uniform_ptr(uint64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
@@ -84,13 +91,17 @@ __device__ __forceinline__ T ldg(const void* p) {
 
 // Source rows are read exactly once, so they are loaded with the
 // non-temporal hint; on MI355X this raised the routing kernels from ~5.0 to
-// ~5.7 TB/s at S=8.  Non-temporal stores measured slower for the output
-// rows and are off by default.  Build switches:
+// ~5.7 TB/s at S=8.  Output rows are written with system-scope (sc1)
+// buffer stores, which measured 3.5-5% faster than default or non-temporal
+// stores in this read-heavy mix.  Build switches:
 #ifndef ATTNRES_NT_LOADS
 #define ATTNRES_NT_LOADS 1
 #endif
 #ifndef ATTNRES_NT_STORES
 #define ATTNRES_NT_STORES 0
+#endif
+#ifndef ATTNRES_STORE_CPOL
+#define ATTNRES_STORE_CPOL 16  // buffer-store cache policy: 16 = sc1
 #endif
 
 // Load through an explicitly global pointer: a generic (flat) load would also
@@ -107,6 +118,19 @@ __device__ __forceinline__ T ldg_global(const char* p) {
 template <typename T>
 __device__ __forceinline__ void stg(void* p, T v) {
   *reinterpret_cast<T*>(p) = v;
+}
+
+// Output rows: a buffer resource over one row (base in SGPRs, byte range =
+// the row, so a store outside it is dropped by the hardware) and raw buffer
+// stores carrying the cache policy above.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(char* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void st_row(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, ATTNRES_STORE_CPOL);
+}
+__device__ __forceinline__ void st_row(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, ATTNRES_STORE_CPOL);
 }
 
 template <typename T>
@@ -335,6 +359,7 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
       if (P.mode != ATTNRES_MODE_PLAIN) {
         const char* drow = reinterpret_cast<const char*>(P.delta) + tok * P.delta_ld * C::BYTES;
         char* prow = reinterpret_cast<char*>(const_cast<void*>(P.src[S - 1])) + tok * row_bytes_ld;
+        const __amdgpu_buffer_rsrc_t prsrc = row_rsrc(prow, (uint32_t)(P.d * C::BYTES));
 #pragma unroll
         for (int k = 0; k < V; ++k) {
           if (!ok[k]) continue;
@@ -352,7 +377,7 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
             }
           }
           x[S - 1][k] = nv;
-          stg<u32x4>(prow + (int64_t)chunk[k] * 16, nv);
+          st_row(prsrc, (uint32_t)chunk[k] * 16, nv);
         }
       }
 
@@ -454,6 +479,7 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
         }
         char* orow = reinterpret_cast<char*>(P.out) +
                      ((int64_t)q * P.out_qstride + tok * P.out_ld) * (P.out_bf16 ? 2 : 4);
+        const __amdgpu_buffer_rsrc_t orsrc = row_rsrc(orow, (uint32_t)(P.d * (P.out_bf16 ? 2 : 4)));
 #pragma unroll
         for (int k = 0; k < V; ++k) {
           if (!ok[k]) continue;
@@ -467,17 +493,16 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
           }
           if (P.out_bf16) {
             if constexpr (VEC == 8) {
-              stg_global<u32x4>(orow + (int64_t)chunk[k] * 16,
-                                u32x4{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3]), pack_bf16(acc[4], acc[5]),
-                                      pack_bf16(acc[6], acc[7])});
+              st_row(orsrc, (uint32_t)chunk[k] * 16,
+                     u32x4{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3]), pack_bf16(acc[4], acc[5]),
+                           pack_bf16(acc[6], acc[7])});
             } else {
-              stg_global<u32x2>(orow + (int64_t)chunk[k] * 8,
-                                u32x2{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3])});
+              st_row(orsrc, (uint32_t)chunk[k] * 8, u32x2{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3])});
             }
           } else {
 #pragma unroll
             for (int h = 0; h < VEC / 4; ++h) {
-              stg_global<u32x4>(orow + ((int64_t)chunk[k] * VEC + 4 * h) * 4,
+              st_row(orsrc, ((uint32_t)chunk[k] * VEC + 4 * h) * 4,
                          u32x4{as_u32(acc[4 * h]), as_u32(acc[4 * h + 1]),
                                as_u32(acc[4 * h + 2]),
                                as_u32(acc[4 * h + 3])});
@@ -592,6 +617,7 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
     }
 
     char* orow = reinterpret_cast<char*>(P.out) + tok * P.out_ld * (IBF16 ? 2 : 4);
+    const __amdgpu_buffer_rsrc_t orsrc = row_rsrc(orow, (uint32_t)(P.d * (IBF16 ? 2 : 4)));
 #pragma unroll
     for (int k = 0; k < V; ++k) {
       if (!ok[k]) continue;
@@ -600,15 +626,15 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
       for (int e = 0; e < VEC; ++e) o[e] = __builtin_fmaf(pi, C::elem(p[k], e) - iv[k][e], iv[k][e]);
       if constexpr (IBF16) {
         if constexpr (VEC == 8) {
-          stg<u32x4>(orow + (int64_t)chunk[k] * 16,
-                     u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])});
+          st_row(orsrc, (uint32_t)chunk[k] * 16,
+                 u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])});
         } else {
-          stg<u32x2>(orow + (int64_t)chunk[k] * 8, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
+          st_row(orsrc, (uint32_t)chunk[k] * 8, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
         }
       } else {
 #pragma unroll
         for (int h = 0; h < VEC / 4; ++h) {
-          stg<u32x4>(orow + ((int64_t)chunk[k] * VEC + 4 * h) * 4,
+          st_row(orsrc, ((uint32_t)chunk[k] * VEC + 4 * h) * 4,
                      u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]),
                            as_u32(o[4 * h + 2]), as_u32(o[4 * h + 3])});
         }
@@ -642,6 +668,9 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
 // row is prefetched with the partial row.
 
 #define ATTNRES_STREAM_WAVES 4
+#ifndef ATTNRES_STREAM_SLOTS
+#define ATTNRES_STREAM_SLOTS 2  // row buffers in the per-wave pipeline (2 or 3)
+#endif
 
 template <int NCH, bool BF16, bool QDOT2, bool FUSED>
 __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
@@ -652,11 +681,6 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   constexpr int QB = QDOT2 ? NCH * 64 : 1;
   __shared__ u32x4 qw_b[QB];
   __shared__ float qw_f[QF];
-  // Source base addresses, indexed by the runtime source number.  Reading
-  // them from the kernel arguments with a runtime index compiles to a vector
-  // load whose wait would also drain the row prefetch; LDS reads are counted
-  // separately (lgkmcnt).
-  __shared__ uint64_t src_base[ATTNRES_KMAX_SOURCES + 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -676,30 +700,38 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
       for (int e = 0; e < VEC; ++e) qw_f[i * VEC + e] = t[e];
     }
   }
-  if (tid < S) src_base[tid] = reinterpret_cast<uint64_t>(P.src[tid]);
-  if (tid == 0) src_base[ATTNRES_KMAX_SOURCES] = reinterpret_cast<uint64_t>(P.delta);
   __syncthreads();
 
-  const int64_t nw = (int64_t)gridDim.x * ATTNRES_STREAM_WAVES;
-  int64_t tok = (int64_t)blockIdx.x * ATTNRES_STREAM_WAVES + wave;
-  if (tok >= P.n_tokens) return;  // no barrier follows
+  // Item counters are 32-bit and wave-uniform so all loop control and address
+  // arithmetic stays in SGPRs (gfx9 has no scalar 64-bit signed compare).
+  const uint32_t n_tok = (uint32_t)P.n_tokens;
+  const uint32_t nw = gridDim.x * ATTNRES_STREAM_WAVES;
+  uint32_t tok = blockIdx.x * ATTNRES_STREAM_WAVES + wave;
+  if (tok >= n_tok) return;  // no barrier follows
 
-  const int64_t row_bytes = P.src_ld * C::BYTES;
-  const int64_t delta_row_bytes = P.delta_ld * C::BYTES;
+  const uint64_t row_bytes = (uint64_t)P.src_ld * C::BYTES;
+  const uint64_t delta_row_bytes = (uint64_t)P.delta_ld * C::BYTES;
   const int mode = FUSED ? P.mode : ATTNRES_MODE_PLAIN;
+  const uint64_t src0 = reinterpret_cast<uint64_t>(P.src[0]);
+  const uint64_t src_stride = (uint64_t)P.src_stride;
+  const uint64_t delta0 = reinterpret_cast<uint64_t>(P.delta);
 
   u32x4 bufA[NCH], bufB[NCH];
   u32x4 dA[FUSED ? NCH : 1], dB[FUSED ? NCH : 1];
 
-  auto load_item = [&](u32x4(&buf)[NCH], u32x4(&dbuf)[FUSED ? NCH : 1], int64_t t, int s) {
-    const bool from_delta = FUSED && s == S - 1 && mode == ATTNRES_MODE_SET;
-    const uint64_t base = src_base[from_delta ? ATTNRES_KMAX_SOURCES : s];
-    const char* row = uniform_ptr(base + (uint64_t)(t * (from_delta ? delta_row_bytes : row_bytes)));
+  // Sources are equally spaced (the host checks): source s of row t is at
+  // src0 + s*src_stride + t*row_bytes, pure scalar arithmetic.
+  auto load_item = [&](u32x4(&buf)[NCH], u32x4(&dbuf)[FUSED ? NCH : 1], uint32_t t, uint32_t s) {
+    t = __builtin_amdgcn_readfirstlane(t);
+    s = __builtin_amdgcn_readfirstlane(s);
+    const bool from_delta = FUSED && s == (uint32_t)(S - 1) && mode == ATTNRES_MODE_SET;
+    const uint64_t base = from_delta ? delta0 : src0 + (uint64_t)s * src_stride;
+    const char* row = uniform_ptr(base + (uint64_t)t * (from_delta ? delta_row_bytes : row_bytes));
 #pragma unroll
     for (int c = 0; c < NCH; ++c) buf[c] = ldg_global<u32x4>(row + (uint32_t)(c * 1024 + lane * 16));
     if constexpr (FUSED) {
-      if (s == S - 1 && mode == ATTNRES_MODE_ACCUM) {
-        const char* drow = uniform_ptr(src_base[ATTNRES_KMAX_SOURCES] + (uint64_t)(t * delta_row_bytes));
+      if (s == (uint32_t)(S - 1) && mode == ATTNRES_MODE_ACCUM) {
+        const char* drow = uniform_ptr(delta0 + (uint64_t)t * delta_row_bytes);
 #pragma unroll
         for (int c = 0; c < NCH; ++c) dbuf[c] = ldg_global<u32x4>(drow + (uint32_t)(c * 1024 + lane * 16));
       }
@@ -717,17 +749,19 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   float m = -__builtin_inff(), l = 0.f;
   float my_logit = 0.f, my_inv = 0.f;  // lane s: logit and inv_rms of source s
 
-  auto process = [&](u32x4(&x)[NCH], u32x4(&dbuf)[FUSED ? NCH : 1], int64_t t, int s, auto slot) {
+  auto process = [&](u32x4(&x)[NCH], u32x4(&dbuf)[FUSED ? NCH : 1], uint32_t t, uint32_t s, auto slot) {
     // A distinct marker per pipeline slot keeps the compiler from merging the
     // two unrolled halves into one body (which would copy the row buffers
     // through phis and wait for the prefetch before using the current row).
     if constexpr (decltype(slot)::value == 0) {
       asm volatile("; attnres stream slot A");
-    } else {
+    } else if constexpr (decltype(slot)::value == 1) {
       asm volatile("; attnres stream slot B");
+    } else {
+      asm volatile("; attnres stream slot C");
     }
     if constexpr (FUSED) {
-      if (s == S - 1 && mode != ATTNRES_MODE_PLAIN) {
+      if (s == (uint32_t)(S - 1) && mode != ATTNRES_MODE_PLAIN) {
         if (mode == ATTNRES_MODE_ACCUM) {
 #pragma unroll
           for (int c = 0; c < NCH; ++c) {
@@ -741,9 +775,10 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
             }
           }
         }
-        char* prow = const_cast<char*>(uniform_ptr(src_base[S - 1] + (uint64_t)(t * row_bytes)));
+        char* prow = const_cast<char*>(uniform_ptr(src0 + (uint64_t)(S - 1) * src_stride + (uint64_t)t * row_bytes));
+        const __amdgpu_buffer_rsrc_t prsrc = row_rsrc(prow, (uint32_t)(NCH * 1024));
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) stg_global<u32x4>(prow + (uint32_t)(c * 1024 + lane * 16), x[c]);
+        for (int c = 0; c < NCH; ++c) st_row(prsrc, (uint32_t)(c * 1024 + lane * 16), x[c]);
       }
     }
 
@@ -782,7 +817,7 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
     dt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dt), 63));
     const float inv = __builtin_amdgcn_rsqf(ss * P.inv_d + P.eps);
     const float logit = dt * inv;
-    if (lane == s) {
+    if ((uint32_t)lane == s) {
       my_logit = logit;
       my_inv = inv;
     }
@@ -815,12 +850,13 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
       }
     }
 
-    if (s == S - 1) {
+    if (s == (uint32_t)(S - 1)) {
       // ---- finalize the token row ----
       // Store addresses: a wave-uniform row base (SGPRs) plus a 32-bit lane offset.
       const float rl = 1.0f / l;
       const int oes = P.out_bf16 ? 2 : 4;
-      char* orow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.out) + (uint64_t)(t * P.out_ld * oes)));
+      char* orow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.out) + (uint64_t)t * (uint64_t)(P.out_ld * oes)));
+      const __amdgpu_buffer_rsrc_t orsrc = row_rsrc(orow, (uint32_t)(P.d * oes));
       // Byte offset of this lane's first output element, made opaque so the
       // per-chunk offsets are recomputed here (mostly as immediate offsets)
       // rather than hoisted out of the loop and kept live in registers.
@@ -832,27 +868,27 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o[e] = acc[c][e] * rl;
         if (P.out_bf16) {
-          char* dst = orow + lane_ob + (uint32_t)(c * 64 * VEC * 2);
+          const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * 2);
           if constexpr (VEC == 8) {
-            stg_global<u32x4>(dst, u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]),
-                                         pack_bf16(o[6], o[7])});
+            st_row(orsrc, off, u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]),
+                                     pack_bf16(o[6], o[7])});
           } else {
-            stg_global<u32x2>(dst, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
+            st_row(orsrc, off, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
           }
         } else {
-          char* dst = orow + lane_ob + (uint32_t)(c * 64 * VEC * 4);
+          const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * 4);
 #pragma unroll
           for (int h = 0; h < VEC / 4; ++h) {
-            stg_global<u32x4>(dst + 16 * h, u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]), as_u32(o[4 * h + 2]),
-                                                  as_u32(o[4 * h + 3])});
+            st_row(orsrc, off + 16 * h,
+                   u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]), as_u32(o[4 * h + 2]), as_u32(o[4 * h + 3])});
           }
         }
       }
       if (P.weights || P.logits || P.inv_rms || P.lse) {
         if (lane < S) {
           if (P.weights) P.weights[(int64_t)lane * P.n_tokens + t] = __expf(my_logit - m) * rl;
-          if (P.logits) P.logits[t * S + lane] = my_logit;
-          if (P.inv_rms) P.inv_rms[t * S + lane] = my_inv;
+          if (P.logits) P.logits[(int64_t)t * S + lane] = my_logit;
+          if (P.inv_rms) P.inv_rms[(int64_t)t * S + lane] = my_inv;
         }
         if (lane == 0 && P.lse) P.lse[t] = m + __logf(l);
       }
@@ -872,34 +908,62 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   // the prefetch", with no branch around the loads.
   using SlotA = std::integral_constant<int, 0>;
   using SlotB = std::integral_constant<int, 1>;
-  int s = 0;
-  load_item(bufA, dA, tok, 0);
-  while (true) {
-    int64_t t2 = tok;
-    int s2 = s + 1;
-    if (s2 == S) {
-      s2 = 0;
-      t2 += nw;
-    }
-    bool more = t2 < P.n_tokens;
-    load_item(bufB, dB, more ? t2 : tok, more ? s2 : s);
-    process(bufA, dA, tok, s, SlotA{});
-    if (!more) break;
-    tok = t2;
-    s = s2;
-    t2 = tok;
-    s2 = s + 1;
-    if (s2 == S) {
-      s2 = 0;
-      t2 += nw;
-    }
-    more = t2 < P.n_tokens;
-    load_item(bufA, dA, more ? t2 : tok, more ? s2 : s);
-    process(bufB, dB, tok, s, SlotB{});
-    if (!more) break;
-    tok = t2;
-    s = s2;
+  // Items (row, source) of this wave in order; two per iteration so slot A
+  // and slot B alternate.  A counted loop with one exit keeps the control
+  // flow uniform (two break exits were structurised into divergent flow
+  // variables, pulling the counters into VGPRs).
+  const uint32_t rows_here = (n_tok - tok - 1) / nw + 1;
+  const uint32_t n_items = rows_here * (uint32_t)S;
+  auto advance = [&](uint32_t t, uint32_t ss, uint32_t& t_out, uint32_t& s_out) {
+    const bool wrap = ss + 1 == (uint32_t)S;
+    s_out = wrap ? 0u : ss + 1;
+    t_out = wrap ? t + nw : t;
+  };
+#if ATTNRES_STREAM_SLOTS == 3
+  // three-slot ring: two items in flight while one is processed
+  u32x4 bufC[NCH];
+  u32x4 dC[FUSED ? NCH : 1];
+  using SlotC = std::integral_constant<int, 2>;
+  uint32_t t0 = tok, s0 = 0, t1, s1;
+  advance(t0, s0, t1, s1);
+  load_item(bufA, dA, t0, s0);
+  load_item(bufB, dB, n_items > 1 ? t1 : t0, n_items > 1 ? s1 : s0);
+  for (uint32_t i = 0; i < n_items; i += 3) {
+    uint32_t t2, s2, t3, s3, t4, s4;
+    advance(t1, s1, t2, s2);
+    advance(t2, s2, t3, s3);
+    advance(t3, s3, t4, s4);
+    const bool has1 = i + 1 < n_items, has2 = i + 2 < n_items;
+    const bool has3 = i + 3 < n_items, has4 = i + 4 < n_items;
+    load_item(bufC, dC, has2 ? t2 : t0, has2 ? s2 : s0);
+    process(bufA, dA, t0, s0, SlotA{});
+    load_item(bufA, dA, has3 ? t3 : t0, has3 ? s3 : s0);
+    if (has1) process(bufB, dB, t1, s1, SlotB{});
+    load_item(bufB, dB, has4 ? t4 : t0, has4 ? s4 : s0);
+    if (has2) process(bufC, dC, t2, s2, SlotC{});
+    t0 = __builtin_amdgcn_readfirstlane(t3);
+    s0 = __builtin_amdgcn_readfirstlane(s3);
+    t1 = __builtin_amdgcn_readfirstlane(t4);
+    s1 = __builtin_amdgcn_readfirstlane(s4);
   }
+#else
+  uint32_t s = 0;
+  load_item(bufA, dA, tok, 0);
+  for (uint32_t i = 0; i < n_items; i += 2) {
+    const bool has1 = i + 1 < n_items;
+    const bool has2 = i + 2 < n_items;
+    uint32_t t1, s1, t2, s2;
+    advance(tok, s, t1, s1);
+    advance(t1, s1, t2, s2);
+    // past the last item the prefetch re-reads the current (valid) row
+    load_item(bufB, dB, has1 ? t1 : tok, has1 ? s1 : s);
+    process(bufA, dA, tok, s, SlotA{});
+    load_item(bufA, dA, has2 ? t2 : tok, has2 ? s2 : s);
+    if (has1) process(bufB, dB, t1, s1, SlotB{});
+    tok = __builtin_amdgcn_readfirstlane(t2);
+    s = __builtin_amdgcn_readfirstlane(s2);
+  }
+#endif
 }
 
 }  // namespace

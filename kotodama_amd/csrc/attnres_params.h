@@ -48,6 +48,7 @@ typedef struct attnres_route_params {
   int64_t delta_ld;
   int64_t out_ld;
   int64_t out_qstride;
+  int64_t src_stride;   /* bytes from source s to s+1 when the sources are equally spaced, else 0 */
   int32_t d;
   int32_t nchunk;       /* d / elements-per-16-byte-chunk */
   int32_t num_queries;
