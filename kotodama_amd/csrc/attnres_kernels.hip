@@ -103,6 +103,9 @@ __device__ __forceinline__ T ldg(const void* p) {
 #ifndef ATTNRES_STORE_CPOL
 #define ATTNRES_STORE_CPOL 16  // buffer-store cache policy: 16 = sc1
 #endif
+#ifndef ATTNRES_LOAD_CPOL
+#define ATTNRES_LOAD_CPOL -1  // -1: global loads (nt per ATTNRES_NT_LOADS); >= 0: buffer loads with this policy
+#endif
 
 // Load through an explicitly global pointer: a generic (flat) load would also
 // count against the LDS wait counter and serialise with LDS reads.
@@ -125,6 +128,9 @@ __device__ __forceinline__ void stg(void* p, T v) {
 // stores carrying the cache policy above.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(char* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 ld_row(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, ATTNRES_LOAD_CPOL < 0 ? 0 : ATTNRES_LOAD_CPOL);
 }
 __device__ __forceinline__ void st_row(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, ATTNRES_STORE_CPOL);
@@ -727,8 +733,14 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
     const bool from_delta = FUSED && s == (uint32_t)(S - 1) && mode == ATTNRES_MODE_SET;
     const uint64_t base = from_delta ? delta0 : src0 + (uint64_t)s * src_stride;
     const char* row = uniform_ptr(base + (uint64_t)t * (from_delta ? delta_row_bytes : row_bytes));
+#if ATTNRES_LOAD_CPOL >= 0
+    const __amdgpu_buffer_rsrc_t rr = row_rsrc(const_cast<char*>(row), (uint32_t)(NCH * 1024));
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) buf[c] = ld_row(rr, (uint32_t)(c * 1024 + lane * 16));
+#else
 #pragma unroll
     for (int c = 0; c < NCH; ++c) buf[c] = ldg_global<u32x4>(row + (uint32_t)(c * 1024 + lane * 16));
+#endif
     if constexpr (FUSED) {
       if (s == (uint32_t)(S - 1) && mode == ATTNRES_MODE_ACCUM) {
         const char* drow = uniform_ptr(delta0 + (uint64_t)t * delta_row_bytes);
