@@ -159,6 +159,45 @@ int attnres_block_step(void* arena, int num_slots, int64_t slot_stride, int n_co
                        const void* gain, int param_dtype, float eps, void* out, float* weights, float* lse,
                        void* stream);
 
+/*
+ * Bytes of device workspace attnres_route_bwd needs for num_tokens rows of
+ * `hidden` on the current device (per-workgroup fp32 partials of the query
+ * gradient).  An upper bound for every num_sources and dtype.
+ */
+int attnres_route_bwd_workspace_size(int64_t num_tokens, int hidden, int64_t* bytes);
+
+/*
+ * Backward of attnres_route_fwd for one query: given dL/dout (and optionally
+ * dL/dlse), writes dL/dsource for every active source and, through the fold
+ * qw = query * gain, dL/dquery and dL/dgain.
+ *
+ * sources/src_ld/src_dtype/query/gain/param_dtype/eps: as in the forward
+ * call (num_sources >= 1).  The softmax is recomputed from the sources
+ * (nothing saved from the forward is needed).
+ * grad_out:     (num_tokens, hidden) rows of grad_out_dtype, stride grad_out_ld.
+ * grad_lse:     (num_tokens,) fp32, or NULL for no lse term.
+ * grad_sources: num_sources row blocks in src_dtype, row stride grad_ld;
+ *               every element of the first num_tokens rows is written.
+ * workspace:    device memory of at least attnres_route_bwd_workspace_size()
+ *               bytes, 16-byte aligned; its contents are scratch.
+ * grad_query:   (hidden,) param_dtype, or NULL.  With gain == NULL this is
+ *               dL/dqw.  grad_gain: (hidden,) param_dtype or NULL (must be
+ *               NULL when gain is).  Both are written, not accumulated; the
+ *               sum over tokens is taken in a fixed order (deterministic).
+ *
+ * Replaces the Triton backward of the phase-1 op for Q = 1
+ * (src/model/flash_attn_res/ops/phase_1.py:88-284,
+ * kernels/phase_1.py:104-280, kernels/reduce.py) together with the autograd of
+ * `qw = query * norm.weight` (src/model/llama.py:630).  Unlike the Triton op,
+ * which leaves the gradient rows of inactive slots unwritten, callers of a
+ * padded buffer zero those rows themselves.
+ */
+int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
+                      int src_dtype, const void* query, const void* gain, int param_dtype, float eps,
+                      const void* grad_out, int grad_out_dtype, int64_t grad_out_ld, const float* grad_lse,
+                      void* const* grad_sources, int64_t grad_ld, void* workspace, int64_t workspace_bytes,
+                      void* grad_query, void* grad_gain, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

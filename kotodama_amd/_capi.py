@@ -50,6 +50,8 @@ EXPORTS = (
     "attnres_route_fwd",
     "attnres_merge_fwd",
     "attnres_block_step",
+    "attnres_route_bwd_workspace_size",
+    "attnres_route_bwd",
 )
 
 _c_vp = ctypes.c_void_p
@@ -133,6 +135,33 @@ _SIGNATURES = {
         ],
         _c_int,
     ),
+    "attnres_route_bwd_workspace_size": ([_c_i64, _c_int, ctypes.POINTER(_c_i64)], _c_int),
+    "attnres_route_bwd": (
+        [
+            ctypes.POINTER(_c_vp),  # sources
+            _c_int,  # num_sources
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_i64,  # src_ld
+            _c_int,  # src_dtype
+            _c_vp,  # query
+            _c_vp,  # gain
+            _c_int,  # param_dtype
+            _c_float,  # eps
+            _c_vp,  # grad_out
+            _c_int,  # grad_out_dtype
+            _c_i64,  # grad_out_ld
+            _c_vp,  # grad_lse
+            ctypes.POINTER(_c_vp),  # grad_sources
+            _c_i64,  # grad_ld
+            _c_vp,  # workspace
+            _c_i64,  # workspace_bytes
+            _c_vp,  # grad_query
+            _c_vp,  # grad_gain
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
 }
 
 _lock = threading.Lock()
@@ -192,6 +221,17 @@ def merge_fwd(*args) -> None:
 
 def block_step(*args) -> None:
     check("attnres_block_step", lib().attnres_block_step(*args))
+
+
+def route_bwd_workspace_size(num_tokens: int, hidden: int) -> int:
+    """Bytes of workspace :func:`route_bwd` needs on the current device."""
+    out = _c_i64(0)
+    check("attnres_route_bwd_workspace_size", lib().attnres_route_bwd_workspace_size(num_tokens, hidden, ctypes.byref(out)))
+    return int(out.value)
+
+
+def route_bwd(*args) -> None:
+    check("attnres_route_bwd", lib().attnres_route_bwd(*args))
 
 
 def set_kernel_policy(policy: int) -> int:

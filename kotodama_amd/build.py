@@ -3,7 +3,7 @@
 Steps (all outputs under ``kotodama_amd/lib/``):
 
 1. ``hipcc --genco --offload-arch=gfx950`` compiles ``csrc/attnres_kernels.hip``
-   four times (``-DATTNRES_PART=0..3``, in parallel) into code-object parts.
+   six times (``-DATTNRES_PART=0..5``, in parallel) into code-object parts.
 2. ``gcc`` assembles ``csrc/attnres_blob.S``, which ``.incbin``s the parts.
 3. ``g++`` builds ``csrc/attnres_capi.cpp`` + the blob into the shared library,
    linked against ROCm's ``libamdhip64.so.7``.  Loaded after ``import torch``,
@@ -28,7 +28,7 @@ INCLUDE = PKG.parent / "include"
 LIB_NAME = "libattnres_hip.so"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
-NUM_PARTS = 4
+NUM_PARTS = 6
 
 # Packed-fp32 VALU ops are disabled for every HIP compile (the kernels are
 # written with scalar fp32 arithmetic).

@@ -1,4 +1,4 @@
-/* The four gfx950 code-object parts, linked into libattnres_hip.so as bytes
+/* The six gfx950 code-object parts, linked into libattnres_hip.so as bytes
  * and loaded with hipModuleLoadData.  The build passes -I<dir of the .hsaco>. */
     .section .rodata
     .balign 4096
@@ -17,4 +17,12 @@ attnres_hsaco_part2:
     .global attnres_hsaco_part3
 attnres_hsaco_part3:
     .incbin "attnres_gfx950_part3.hsaco"
+    .balign 4096
+    .global attnres_hsaco_part4
+attnres_hsaco_part4:
+    .incbin "attnres_gfx950_part4.hsaco"
+    .balign 4096
+    .global attnres_hsaco_part5
+attnres_hsaco_part5:
+    .incbin "attnres_gfx950_part5.hsaco"
     .section .note.GNU-stack,"",@progbits

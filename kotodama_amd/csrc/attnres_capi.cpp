@@ -27,10 +27,12 @@ extern "C" const unsigned char attnres_hsaco_part0[];
 extern "C" const unsigned char attnres_hsaco_part1[];
 extern "C" const unsigned char attnres_hsaco_part2[];
 extern "C" const unsigned char attnres_hsaco_part3[];
+extern "C" const unsigned char attnres_hsaco_part4[];
+extern "C" const unsigned char attnres_hsaco_part5[];
 
 namespace {
 
-constexpr int kParts = 4;
+constexpr int kParts = 6;
 constexpr int kMaxDevices = 64;
 constexpr int kMaxThreads = 512;  // __launch_bounds__ of every kernel
 
@@ -58,6 +60,8 @@ constexpr int kMergeFuncs = 4 * 2;
 constexpr int kStreamMaxChunks = 8;  // rows of up to 8 KiB
 constexpr int kStreamWaves = 4;      // waves per workgroup of the streaming kernels
 constexpr int kStreamFuncs = kTypeCombos * kStreamMaxChunks * 2;
+constexpr int kBwdFuncs = 2 * kNumS * 2;  // (bf16 | fp32) x S x V
+constexpr int kBwdMaxPerCu = 4;           // workgroups per CU the backward grid may use (workspace bound)
 
 struct DeviceState {
   std::atomic<bool> loaded{false};
@@ -71,6 +75,10 @@ struct DeviceState {
   hipFunction_t merge[kMergeFuncs] = {};
   int merge_bpc[kMergeFuncs] = {};
   int merge_bpc_block[kMergeFuncs] = {};
+  hipFunction_t bwd[kBwdFuncs] = {};
+  int bwd_bpc[kBwdFuncs] = {};
+  int bwd_bpc_block[kBwdFuncs] = {};
+  hipFunction_t reduce = nullptr;
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -111,7 +119,7 @@ int ensure_loaded(DeviceState** out) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (!st.loaded.load(std::memory_order_relaxed)) {
       const unsigned char* blobs[kParts] = {attnres_hsaco_part0, attnres_hsaco_part1, attnres_hsaco_part2,
-                                            attnres_hsaco_part3};
+                                            attnres_hsaco_part3, attnres_hsaco_part4, attnres_hsaco_part5};
       for (int i = 0; i < kParts; ++i) {
         e = hipModuleLoadData(&st.mods[i], blobs[i]);
         if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
@@ -202,6 +210,41 @@ int get_merge(DeviceState& st, bool pbf, bool ibf, int v, int block, hipFunction
   }
   *f = st.merge[idx];
   *bpc = st.merge_bpc[idx];
+  return ATTNRES_OK;
+}
+
+// Backward kernels: S <= 8 and the column reduce in part 4, S >= 9 in part 5.
+int part_of_bwd(int s) { return s <= 8 ? 4 : 5; }
+constexpr int kReducePart = 4;
+
+int get_bwd(DeviceState& st, bool bf, int s, int v, int block, hipFunction_t* f, int* bpc) {
+  const int idx = ((bf ? 0 : 1) * kNumS + s) * 2 + (v - 1);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (st.bwd[idx] == nullptr) {
+    char name[96];
+    snprintf(name, sizeof(name), "attnres_route_bwd_%s_s%d_v%d", bf ? "bf" : "f32", s, v);
+    int rc = find_function(st, part_of_bwd(s), name, &st.bwd[idx]);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  if (st.bwd_bpc_block[idx] != block) {
+    int nb = 0;
+    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.bwd[idx], block, 0);
+    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    st.bwd_bpc[idx] = nb > 0 ? nb : 1;
+    st.bwd_bpc_block[idx] = block;
+  }
+  *f = st.bwd[idx];
+  *bpc = st.bwd_bpc[idx];
+  return ATTNRES_OK;
+}
+
+int get_reduce(DeviceState& st, hipFunction_t* f) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (st.reduce == nullptr) {
+    int rc = find_function(st, kReducePart, "attnres_reduce_dqw", &st.reduce);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  *f = st.reduce;
   return ATTNRES_OK;
 }
 
@@ -533,6 +576,119 @@ int attnres_block_step(void* arena, int num_slots, int64_t slot_stride, int n_co
   return route_launch(srcs, S, num_tokens, hidden, hidden, dtype, query, gain, 1, param_dtype, eps, out, dtype,
                       hidden, (int64_t)num_tokens * hidden, weights, lse, nullptr, nullptr, mode, delta, hidden,
                       stream);
+}
+
+int attnres_route_bwd_workspace_size(int64_t num_tokens, int hidden, int64_t* bytes) {
+  if (bytes == nullptr) return fail(ATTNRES_ERR_ARG, "bytes is NULL");
+  if (num_tokens < 0 || hidden <= 0) return fail(ATTNRES_ERR_ARG, "bad num_tokens/hidden");
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  int64_t parts = (int64_t)st->num_cus * kBwdMaxPerCu;
+  if (parts > num_tokens) parts = num_tokens;
+  *bytes = parts * (int64_t)hidden * (int64_t)sizeof(float);
+  return ATTNRES_OK;
+}
+
+int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
+                      int src_dtype, const void* query, const void* gain, int param_dtype, float eps,
+                      const void* grad_out, int grad_out_dtype, int64_t grad_out_ld, const float* grad_lse,
+                      void* const* grad_sources, int64_t grad_ld, void* workspace, int64_t workspace_bytes,
+                      void* grad_query, void* grad_gain, void* stream) {
+  if (num_sources < 1 || num_sources > ATTNRES_MAX_SOURCES)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "backward: num_sources=%d outside [1, %d]", num_sources,
+                ATTNRES_MAX_SOURCES);
+  if (sources == nullptr || grad_sources == nullptr) return fail(ATTNRES_ERR_ARG, "sources/grad_sources is NULL");
+  if (num_tokens < 0) return fail(ATTNRES_ERR_ARG, "num_tokens=%lld < 0", (long long)num_tokens);
+  if (hidden <= 0) return fail(ATTNRES_ERR_ARG, "hidden=%d <= 0", hidden);
+  if (!valid_dtype(src_dtype) || !valid_dtype(param_dtype) || !valid_dtype(grad_out_dtype))
+    return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (query == nullptr || grad_out == nullptr) return fail(ATTNRES_ERR_ARG, "query/grad_out is NULL");
+  if (gain == nullptr && grad_gain != nullptr) return fail(ATTNRES_ERR_ARG, "grad_gain given without gain");
+  if (!std::isfinite(eps)) return fail(ATTNRES_ERR_ARG, "eps is not finite");
+  const bool bf = src_dtype == ATTNRES_DTYPE_BF16;
+  const int vec = bf ? 8 : 4;
+  if (hidden % vec != 0)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d is not a multiple of %d (16-byte chunks)", hidden, vec);
+  const int nchunk = hidden / vec;
+  if (round64((nchunk + 1) / 2) > kMaxThreads)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d exceeds the largest supported row (%d elements)", hidden,
+                2 * kMaxThreads * vec);
+  // grad_out chunks are read as 16 bytes (bf16 rows as 8-byte halves when
+  // the sources are fp32): rows must be aligned to that.
+  const int gvec_bytes = vec * esize(grad_out_dtype);
+  const int galign = gvec_bytes >= 16 ? 16 : gvec_bytes;
+  if (src_ld < hidden || grad_ld < hidden || grad_out_ld < hidden)
+    return fail(ATTNRES_ERR_ARG, "a row stride is smaller than hidden=%d", hidden);
+  if ((src_ld * esize(src_dtype)) % 16 != 0 || (grad_ld * esize(src_dtype)) % 16 != 0)
+    return fail(ATTNRES_ERR_ALIGN, "source / gradient row stride not 16-byte aligned");
+  if (((uintptr_t)grad_out % galign) != 0 || ((grad_out_ld * esize(grad_out_dtype)) % galign) != 0)
+    return fail(ATTNRES_ERR_ALIGN, "grad_out rows not %d-byte aligned", galign);
+  for (int s = 0; s < num_sources; ++s) {
+    if (sources[s] == nullptr || grad_sources[s] == nullptr)
+      return fail(ATTNRES_ERR_ARG, "sources[%d] or grad_sources[%d] is NULL", s, s);
+    if (!aligned16(sources[s]) || !aligned16(grad_sources[s]))
+      return fail(ATTNRES_ERR_ALIGN, "sources[%d] or grad_sources[%d] not 16-byte aligned", s, s);
+  }
+  if (num_tokens == 0) return ATTNRES_OK;  // no tokens: the query gradients are not written
+
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  const int v = round64(nchunk) <= kMaxThreads ? 1 : 2;
+  const int block = v == 1 ? round64(nchunk) : round64((nchunk + 1) / 2);
+  hipFunction_t f = nullptr;
+  int bpc = 1;
+  rc = get_bwd(*st, bf, num_sources, v, block, &f, &bpc);
+  if (rc != ATTNRES_OK) return rc;
+  int64_t grid = (int64_t)st->num_cus * (bpc < kBwdMaxPerCu ? bpc : kBwdMaxPerCu);
+  if (grid > num_tokens) grid = num_tokens;
+  const int64_t need = grid * (int64_t)hidden * (int64_t)sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(ATTNRES_ERR_ARG, "workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
+                (long long)need);
+  if (!aligned16(workspace)) return fail(ATTNRES_ERR_ALIGN, "workspace not 16-byte aligned");
+  hipFunction_t fr = nullptr;
+  if (grad_query != nullptr || grad_gain != nullptr) {
+    rc = get_reduce(*st, &fr);
+    if (rc != ATTNRES_OK) return rc;
+  }
+
+  attnres_route_bwd_params P;
+  std::memset(&P, 0, sizeof(P));
+  for (int s = 0; s < num_sources; ++s) {
+    P.src[s] = sources[s];
+    P.dsrc[s] = grad_sources[s];
+  }
+  P.query = query;
+  P.gain = gain;
+  P.grad_out = grad_out;
+  P.grad_lse = grad_lse;
+  P.dqw_part = static_cast<float*>(workspace);
+  P.n_tokens = num_tokens;
+  P.src_ld = src_ld;
+  P.dsrc_ld = grad_ld;
+  P.gout_ld = grad_out_ld;
+  P.d = hidden;
+  P.nchunk = nchunk;
+  P.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
+  P.gout_bf16 = grad_out_dtype == ATTNRES_DTYPE_BF16;
+  P.eps = eps;
+  P.inv_d = 1.0f / (float)hidden;
+  rc = launch(f, (int)grid, block, P, stream);
+  if (rc != ATTNRES_OK || fr == nullptr) return rc;
+
+  attnres_reduce_params R;
+  std::memset(&R, 0, sizeof(R));
+  R.part = static_cast<const float*>(workspace);
+  R.query = query;
+  R.gain = gain;
+  R.dquery = grad_query;
+  R.dgain = grad_gain;
+  R.nparts = (int)grid;
+  R.d = hidden;
+  R.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
+  return launch(fr, (hidden + 255) / 256, 256, R, stream);
 }
 
 }  // extern "C"

@@ -77,6 +77,11 @@ __device__ __forceinline__ int64_t uniform_i64(int64_t v) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// A wave-uniform float kept in an SGPR.
+__device__ __forceinline__ float uniform_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, v)));
+}
+
 // A wave-uniform address held in SGPRs (the value is the same in every lane).
 __device__ __forceinline__ const char* uniform_ptr(uint64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
@@ -978,6 +983,239 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
 #endif
 }
 
+
+// ------------------------------------------------------- backward body --
+//
+// One workgroup per token row (grid-stride), thread i owning chunks
+// i, i+blockDim, ... as in route_body.  The S source chunks and the output
+// gradient G are loaded into registers; per source the thread forms
+// sum(x^2), x.qw and x.G, the 3S partial sums go through one DPP wave
+// reduction + LDS exchange, and every thread then recomputes the softmax and
+// writes its chunks of the S source gradients
+//   dx_s = w_s G + c1_s qw + c2_s x_s.
+// The query gradient sum_s c1_s x_s is accumulated in registers over all rows
+// the workgroup handles and written once as this workgroup's partial.
+template <int S, int V, bool BF16>
+__device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P) {
+  using C = Chunk<BF16>;
+  constexpr int VEC = C::VEC;
+  constexpr int NV = 3 * S;
+  constexpr int RLD = ((NV + 3) / 4) * 4;
+  __shared__ float red[2][ATTNRES_KMAX_WAVES][RLD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = (blockDim.x + 63) >> 6;
+
+  int chunk[V];
+  bool ok[V];
+  float qwf[V][VEC];
+  float dqw[V][VEC];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    chunk[k] = tid + k * (int)blockDim.x;
+    ok[k] = chunk[k] < P.nchunk;
+    const int64_t off = (int64_t)chunk[k] * VEC;
+    if (ok[k]) {
+      load_param<VEC>(P.query, off, P.param_bf16, qwf[k]);
+      if (P.gain != nullptr) {
+        float g[VEC];
+        load_param<VEC>(P.gain, off, P.param_bf16, g);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float prod = qwf[k][e] * g[e];
+          qwf[k][e] = P.param_bf16 ? round_bf16(prod) : prod;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) qwf[k][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dqw[k][e] = 0.f;
+  }
+
+  const int64_t row_bytes_ld = P.src_ld * C::BYTES;
+  int ph = 0;
+  for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
+    u32x4 x[S][V];
+    float gf[V][VEC];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const char* row = reinterpret_cast<const char*>(P.src[s]) + tok * row_bytes_ld;
+#pragma unroll
+      for (int k = 0; k < V; ++k) x[s][k] = ok[k] ? ldg_global<u32x4>(row + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
+    }
+    {
+      const char* grow = reinterpret_cast<const char*>(P.grad_out) + tok * P.gout_ld * (P.gout_bf16 ? 2 : 4);
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        if (!ok[k]) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) gf[k][e] = 0.f;
+          continue;
+        }
+        if (P.gout_bf16) {
+          if constexpr (VEC == 8) {
+            const u32x4 t = ldg_global<u32x4>(grow + (int64_t)chunk[k] * 16);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              gf[k][2 * w] = bf_lo(t[w]);
+              gf[k][2 * w + 1] = bf_hi(t[w]);
+            }
+          } else {
+            const u32x2 t = ldg<u32x2>(grow + (int64_t)chunk[k] * 8);
+            gf[k][0] = bf_lo(t[0]);
+            gf[k][1] = bf_hi(t[0]);
+            gf[k][2] = bf_lo(t[1]);
+            gf[k][3] = bf_hi(t[1]);
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < VEC / 4; ++h) {
+            const u32x4 t = ldg_global<u32x4>(grow + ((int64_t)chunk[k] * VEC + 4 * h) * 4);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) gf[k][4 * h + w] = as_f32(t[w]);
+          }
+        }
+      }
+    }
+
+    // ---- sum(x^2), x.qw, x.G per source ----
+    float part[NV];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      float ss = 0.f, dt = 0.f, ag = 0.f;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float v = C::elem(x[s][k], e);
+          ss = __builtin_fmaf(v, v, ss);
+          dt = __builtin_fmaf(v, qwf[k][e], dt);
+          ag = __builtin_fmaf(v, gf[k][e], ag);
+        }
+      }
+      part[s] = ss;
+      part[S + s] = dt;
+      part[2 * S + s] = ag;
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) part[j] = wave_sum_to_lane63(part[j]);
+    if (lane == 63) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) red[ph][wave][j] = part[j];
+    }
+    __syncthreads();
+    float tot[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) tot[j] = 0.f;
+    for (int w = 0; w < nwaves; ++w) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) tot[j] += red[ph][w][j];
+    }
+    ph ^= 1;
+
+    // ---- softmax recomputed, then the coefficients of dx ----
+    float r[S], l[S], wgt[S];
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      r[s] = __builtin_amdgcn_rsqf(tot[s] * P.inv_d + P.eps);
+      l[s] = tot[S + s] * r[s];
+      m = __builtin_fmaxf(m, l[s]);
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      wgt[s] = __expf(l[s] - m);
+      sum += wgt[s];
+    }
+    const float rsum = 1.0f / sum;
+    float go = 0.f;  // G . out = sum_s w_s (G . x_s)
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      wgt[s] *= rsum;
+      go = __builtin_fmaf(wgt[s], tot[2 * S + s], go);
+    }
+    // The coefficients are the same in every lane: keep them in SGPRs.
+    const float glse = P.grad_lse != nullptr ? P.grad_lse[tok] : 0.f;
+    float c1[S], c2[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const float dl = wgt[s] * (glse + tot[2 * S + s] - go);
+      c1[s] = dl * r[s];
+      c2[s] = uniform_f32(-c1[s] * l[s] * r[s] * P.inv_d);
+      c1[s] = uniform_f32(c1[s]);
+      wgt[s] = uniform_f32(wgt[s]);
+    }
+
+    // ---- write the source gradients, accumulate the query gradient ----
+    // The packed rows are re-expanded here rather than kept as fp32 from the
+    // first pass (that would double the register footprint of the sources).
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) asm volatile("" : "+v"(x[s][k]));
+      char* drow = reinterpret_cast<char*>(P.dsrc[s]) + tok * P.dsrc_ld * C::BYTES;
+      const __amdgpu_buffer_rsrc_t drsrc = row_rsrc(drow, (uint32_t)(P.d * C::BYTES));
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        if (!ok[k]) continue;
+        float dx[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float v = C::elem(x[s][k], e);
+          dx[e] = __builtin_fmaf(c2[s], v, __builtin_fmaf(c1[s], qwf[k][e], wgt[s] * gf[k][e]));
+          dqw[k][e] = __builtin_fmaf(c1[s], v, dqw[k][e]);
+        }
+        if constexpr (BF16) {
+          st_row(drsrc, (uint32_t)chunk[k] * 16,
+                 u32x4{pack_bf16(dx[0], dx[1]), pack_bf16(dx[2], dx[3]), pack_bf16(dx[4], dx[5]),
+                       pack_bf16(dx[6], dx[7])});
+        } else {
+          st_row(drsrc, (uint32_t)chunk[k] * 16, u32x4{as_u32(dx[0]), as_u32(dx[1]), as_u32(dx[2]), as_u32(dx[3])});
+        }
+      }
+    }
+  }
+
+  // ---- this workgroup's query-gradient partial ----
+  float* prow = P.dqw_part + (int64_t)blockIdx.x * P.d;
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    if (!ok[k]) continue;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) prow[(int64_t)chunk[k] * VEC + e] = dqw[k][e];
+  }
+}
+
+// Sum the per-workgroup partials of dqw column by column (fixed order, so the
+// result is deterministic) and apply the fold qw = query * gain backwards.
+__device__ __forceinline__ void reduce_dqw_body(const attnres_reduce_params& P) {
+  const int col = blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= P.d) return;
+  float acc = 0.f;
+  for (int p = 0; p < P.nparts; ++p) acc += P.part[(int64_t)p * P.d + col];
+  float q, g = 1.f;
+  if (P.param_bf16) {
+    q = bf_lo(reinterpret_cast<const uint16_t*>(P.query)[col]);
+    if (P.gain) g = bf_lo(reinterpret_cast<const uint16_t*>(P.gain)[col]);
+  } else {
+    q = reinterpret_cast<const float*>(P.query)[col];
+    if (P.gain) g = reinterpret_cast<const float*>(P.gain)[col];
+  }
+  const float dq = P.gain ? acc * g : acc;
+  if (P.param_bf16) {
+    if (P.dquery) reinterpret_cast<__bf16*>(P.dquery)[col] = (__bf16)dq;
+    if (P.dgain) reinterpret_cast<__bf16*>(P.dgain)[col] = (__bf16)(acc * q);
+  } else {
+    if (P.dquery) reinterpret_cast<float*>(P.dquery)[col] = dq;
+    if (P.dgain) reinterpret_cast<float*>(P.dgain)[col] = acc * q;
+  }
+}
+
 }  // namespace
 
 // ------------------------------------------------------- instantiations --
@@ -1009,8 +1247,8 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   ROUTE_TYPES(S, 1) \
   ROUTE_TYPES(S, 2)
 
-// The build compiles this file once per module part (ATTNRES_PART = 0..3)
-// so the parts build in parallel; the host searches every part for a symbol.
+// The build compiles this file once per module part (ATTNRES_PART = 0..5)
+// so the parts build in parallel; the host maps each symbol to its part.
 #ifndef ATTNRES_PART
 #define ATTNRES_PART 0
 #define ATTNRES_ALL_PARTS 1
@@ -1089,4 +1327,38 @@ STREAM_TYPES(5)
 STREAM_TYPES(6)
 STREAM_TYPES(7)
 STREAM_TYPES(8)
+#endif
+
+// Backward: attnres_route_bwd_<in>_s<S>_v<V>; column reduce: attnres_reduce_dqw.
+#define BWD_ONE(INNAME, BF, S, V)                                                                      \
+  extern "C" __global__ void __launch_bounds__(512) attnres_route_bwd_##INNAME##_s##S##_v##V(         \
+      attnres_route_bwd_params P) {                                                                    \
+    route_bwd_body<S, V, BF>(P);                                                                       \
+  }
+#define BWD_S(S)            \
+  BWD_ONE(bf, true, S, 1)   \
+  BWD_ONE(bf, true, S, 2)   \
+  BWD_ONE(f32, false, S, 1) \
+  BWD_ONE(f32, false, S, 2)
+
+#if ATTNRES_PART == 4 || defined(ATTNRES_ALL_PARTS)
+BWD_S(1)
+BWD_S(2)
+BWD_S(3)
+BWD_S(4)
+BWD_S(5)
+BWD_S(6)
+BWD_S(7)
+BWD_S(8)
+extern "C" __global__ void __launch_bounds__(256) attnres_reduce_dqw(attnres_reduce_params P) { reduce_dqw_body(P); }
+#endif
+#if ATTNRES_PART == 5 || defined(ATTNRES_ALL_PARTS)
+BWD_S(9)
+BWD_S(10)
+BWD_S(11)
+BWD_S(12)
+BWD_S(13)
+BWD_S(14)
+BWD_S(15)
+BWD_S(16)
 #endif

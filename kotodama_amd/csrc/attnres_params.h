@@ -61,6 +61,45 @@ typedef struct attnres_route_params {
 } attnres_route_params;
 
 /*
+ * Backward of one routing point (one query).  Per token, with G = grad_out:
+ *   dx_s = w_s G + c1_s qw + c2_s x_s,  c1_s = dl_s r_s,  c2_s = -dl_s l_s r_s^2 / d,
+ *   dl_s = w_s (G.x_s - G.out);  dqw += sum_s c1_s x_s
+ * Every workgroup writes its dqw partial sum to dqw_part[blockIdx.x * d ...];
+ * a reduce kernel then sums the partials in a fixed order.
+ */
+typedef struct attnres_route_bwd_params {
+  const void* src[ATTNRES_KMAX_SOURCES];
+  void* dsrc[ATTNRES_KMAX_SOURCES];  /* gradient rows of each source, src dtype */
+  const void* query;
+  const void* gain;
+  const void* grad_out;  /* (n_tokens, d) */
+  const float* grad_lse; /* (n_tokens,) or NULL */
+  float* dqw_part;       /* (gridDim.x, d) fp32 */
+  int64_t n_tokens;
+  int64_t src_ld;
+  int64_t dsrc_ld;
+  int64_t gout_ld;
+  int32_t d;
+  int32_t nchunk;
+  int32_t param_bf16;
+  int32_t gout_bf16;
+  float eps;
+  float inv_d;
+} attnres_route_bwd_params;
+
+/* Column reduction of the dqw partials into the parameter gradients. */
+typedef struct attnres_reduce_params {
+  const float* part;  /* (nparts, d) */
+  const void* query;  /* (d,) param dtype */
+  const void* gain;   /* (d,) param dtype, or NULL */
+  void* dquery;       /* (d,) param dtype: dqw * gain (dqw when gain is NULL) */
+  void* dgain;        /* (d,) param dtype: dqw * query, or NULL */
+  int32_t nparts;
+  int32_t d;
+  int32_t param_bf16;
+} attnres_reduce_params;
+
+/*
  * Online-softmax merge of one intra-block partial into a phase-1 result:
  *   inv_rms = rsqrt(mean(p^2)+eps); logit = (p . q) * inv_rms
  *   pi = sigmoid(logit - inter_lse); out = inter + pi * (p - inter)

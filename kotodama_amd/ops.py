@@ -4,7 +4,9 @@ Each op is a thin shim over the C ABI (``_capi``): it validates tensors,
 allocates outputs on torch's caching allocator, and launches on the current
 HIP stream of the inputs' device.  Fake (meta) implementations give shapes
 for ``torch.compile``.  Inputs must be ROCm device tensors: there is no CPU
-path, and the ops are forward-only (they raise if autograd would need them).
+path.  ``route`` and ``route_list`` are differentiable for one query (the
+backward kernels of ``attnres_route_bwd``); ``merge`` and ``block_step`` are
+forward-only and raise if autograd would need them.
 
 Ops
 ---
@@ -19,6 +21,13 @@ Ops
 ``attnres_hip::block_step(arena, n_committed, commit, delta, query, gain, eps, want_weights)``
     One routing point over a block arena with the partial update fused in
     (the body of ``llama.py:697-715`` / ``742-762``); mutates ``arena``.
+``attnres_hip::route_bwd`` / ``attnres_hip::route_list_bwd``
+    Backward of ``route`` / ``route_list`` for one query: gradients of the
+    sources, the query and the gain from dL/dout and dL/dlse
+    (``ops/phase_1.py:88-284``, ``kernels/phase_1.py:104-280``).  The weights
+    and the aux outputs (inv_rms, logits) are non-differentiable outputs, as
+    in the reference, whose backward ignores their gradients
+    (``ops/phase_1.py:235-241``).
 
 Returned tuples always have the same arity; outputs that were not requested
 are empty tensors.
@@ -259,6 +268,226 @@ def _route_list_fake(sources, query, gain, eps, out_dtype, want_weights, want_au
     return _outputs(ref.device, out_dtype, nq, len(sources), tuple(ref.shape[:-1]), ref.shape[-1], want_weights, want_aux)
 
 
+# --------------------------------------------------------------- backward --
+
+
+def _launch_route_bwd(
+    ptrs: list[int],
+    grad_ptrs: list[int],
+    src_dtype: torch.dtype,
+    n: int,
+    d: int,
+    device: torch.device,
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    grad_out: Tensor,
+    grad_lse: Optional[Tensor],
+) -> tuple[Tensor, Optional[Tensor]]:
+    """Launch attnres_route_bwd; returns (grad_query, grad_gain) in the parameter dtype.
+
+    ``query``/``gain`` are the op's inputs; when their dtypes differ the fold
+    is taken here (as in the forward) and the product rule applied in torch.
+    """
+    q = query.reshape(-1)
+    mixed = gain is not None and gain.dtype != q.dtype
+    kq, kg, pcode = _fold_query(q, gain)
+    dq = torch.empty(d, device=device, dtype=kq.dtype)
+    dg = torch.empty(d, device=device, dtype=kg.dtype) if kg is not None else None
+    grad_out = grad_out.reshape(n, d).contiguous()
+    if grad_lse is not None:
+        grad_lse = grad_lse.reshape(n).to(torch.float32).contiguous()
+    with _DeviceStream(device) as stream:
+        ws = torch.empty(max(1, _capi.route_bwd_workspace_size(n, d) // 4), device=device, dtype=torch.float32)
+        _capi.route_bwd(
+            _capi.pointer_array(ptrs),
+            len(ptrs),
+            n,
+            d,
+            d,
+            dtype_code(src_dtype),
+            kq.data_ptr(),
+            kg.data_ptr() if kg is not None else None,
+            pcode,
+            float(eps),
+            grad_out.data_ptr(),
+            dtype_code(grad_out.dtype),
+            d,
+            grad_lse.data_ptr() if grad_lse is not None else None,
+            _capi.pointer_array(grad_ptrs),
+            d,
+            ws.data_ptr(),
+            ws.numel() * 4,
+            dq.data_ptr(),
+            dg.data_ptr() if dg is not None else None,
+            stream,
+        )
+    if mixed:
+        # dq is dL/dqw for qw = query * gain taken in the promoted dtype
+        return (dq * gain).to(query.dtype).reshape(query.shape), (dq * q).to(gain.dtype)
+    return dq.reshape(query.shape), dg
+
+
+def _bwd_args(query: Tensor, grad_out: Optional[Tensor], grad_lse: Optional[Tensor], n_out_shape, device, dt):
+    if query.dim() == 2 and query.shape[0] != 1:
+        raise NotImplementedError(
+            "attnres_hip: backward is implemented for one query; the batched phase-1 call with "
+            f"{query.shape[0]} queries is forward-only"
+        )
+    if grad_out is None:
+        grad_out = torch.zeros(n_out_shape, device=device, dtype=dt)
+    return grad_out, grad_lse
+
+
+@torch.library.custom_op("attnres_hip::route_bwd", mutates_args=())
+def route_bwd(
+    buf: Tensor,
+    num_sources: int,
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    grad_out: Tensor,
+    grad_lse: Optional[Tensor],
+) -> tuple[Tensor, Tensor, Tensor]:
+    """(grad_buf, grad_query, grad_gain) of ``route`` with one query.
+
+    ``grad_buf`` is zero in slots at or beyond ``num_sources``; ``grad_gain``
+    is an empty tensor when ``gain`` is None.  With ``num_sources == 0`` the
+    forward output is NaN and so are the gradients.
+    """
+    device = _require_device(buf, query, gain, grad_out, grad_lse)
+    buf = buf.contiguous()
+    d = buf.shape[-1]
+    n = buf[0].numel() // d if buf.shape[0] else 0
+    grad_buf = torch.empty_like(buf)
+    grad_buf[num_sources:].zero_()
+    gq_dtype = query.dtype
+    gg = torch.empty((0,), device=device, dtype=gain.dtype if gain is not None else query.dtype)
+    if num_sources == 0 or n == 0:
+        fill = float("nan") if num_sources == 0 else 0.0
+        grad_buf.fill_(fill)
+        gq = torch.full_like(query, fill, dtype=gq_dtype)
+        if gain is not None:
+            gg = torch.full_like(gain, fill)
+        return grad_buf, gq, gg
+    slot = n * d
+    es = buf.element_size()
+    ptrs = [buf.data_ptr() + i * slot * es for i in range(num_sources)]
+    gptrs = [grad_buf.data_ptr() + i * slot * es for i in range(num_sources)]
+    gq, g2 = _launch_route_bwd(ptrs, gptrs, buf.dtype, n, d, device, query, gain, eps, grad_out, grad_lse)
+    return grad_buf, gq, g2 if g2 is not None else gg
+
+
+@route_bwd.register_fake
+def _route_bwd_fake(buf, num_sources, query, gain, eps, grad_out, grad_lse):
+    gg = torch.empty_like(gain) if gain is not None else query.new_empty((0,))
+    return torch.empty_like(buf), torch.empty_like(query), gg
+
+
+@torch.library.custom_op("attnres_hip::route_list_bwd", mutates_args=())
+def route_list_bwd(
+    sources: list[Tensor],
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    grad_out: Tensor,
+    grad_lse: Optional[Tensor],
+) -> tuple[list[Tensor], Tensor, Tensor]:
+    """(grad_sources, grad_query, grad_gain) of ``route_list`` with one query."""
+    device = _require_device(*sources, query, gain, grad_out, grad_lse)
+    ref = sources[0]
+    d = ref.shape[-1]
+    n = ref.numel() // d
+    srcs = [t if t.is_contiguous() else t.contiguous() for t in sources]
+    grads = [torch.empty(t.shape, device=device, dtype=t.dtype) for t in srcs]
+    gg = torch.empty((0,), device=device, dtype=gain.dtype if gain is not None else query.dtype)
+    if n == 0:
+        gq = torch.zeros_like(query)
+        if gain is not None:
+            gg = torch.zeros_like(gain)
+        return grads, gq, gg
+    gq, g2 = _launch_route_bwd(
+        [t.data_ptr() for t in srcs], [g.data_ptr() for g in grads], ref.dtype, n, d, device, query, gain, eps,
+        grad_out, grad_lse,
+    )
+    return grads, gq, g2 if g2 is not None else gg
+
+
+@route_list_bwd.register_fake
+def _route_list_bwd_fake(sources, query, gain, eps, grad_out, grad_lse):
+    gg = torch.empty_like(gain) if gain is not None else query.new_empty((0,))
+    return [torch.empty_like(t) for t in sources], torch.empty_like(query), gg
+
+
+def _route_setup_context(ctx, inputs, output):
+    buf, num_sources, query, gain, eps, out_dtype, _, _ = inputs
+    out, weights, lse, inv_rms, logits = output
+    ctx.mark_non_differentiable(weights, inv_rms, logits)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(buf, query, gain)
+    ctx.num_sources = num_sources
+    ctx.eps = eps
+    ctx.out_shape = tuple(out.shape)
+    ctx.out_dtype = out_dtype
+
+
+def _route_backward(ctx, g_out, g_w, g_lse, g_inv, g_logits):
+    buf, query, gain = ctx.saved_tensors
+    if g_out is None and g_lse is None:
+        return None, None, None, None, None, None, None, None
+    g_out, g_lse = _bwd_args(query, g_out, g_lse, ctx.out_shape, buf.device, ctx.out_dtype)
+    grad_buf, gq, gg = route_bwd(buf, ctx.num_sources, query, gain, ctx.eps, g_out, g_lse)
+    need = ctx.needs_input_grad
+    return (
+        grad_buf if need[0] else None,
+        None,
+        gq if need[2] else None,
+        gg if (gain is not None and need[3]) else None,
+        None,
+        None,
+        None,
+        None,
+    )
+
+
+route.register_autograd(_route_backward, setup_context=_route_setup_context)
+
+
+def _route_list_setup_context(ctx, inputs, output):
+    sources, query, gain, eps, out_dtype, _, _ = inputs
+    out, weights, lse, inv_rms, logits = output
+    ctx.mark_non_differentiable(weights, inv_rms, logits)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(*sources, query, gain)
+    ctx.num_sources = len(sources)
+    ctx.eps = eps
+    ctx.out_shape = tuple(out.shape)
+    ctx.out_dtype = out_dtype
+
+
+def _route_list_backward(ctx, g_out, g_w, g_lse, g_inv, g_logits):
+    saved = ctx.saved_tensors
+    sources = list(saved[: ctx.num_sources])
+    query, gain = saved[ctx.num_sources], saved[ctx.num_sources + 1]
+    if g_out is None and g_lse is None:
+        return None, None, None, None, None, None, None
+    g_out, g_lse = _bwd_args(query, g_out, g_lse, ctx.out_shape, query.device, ctx.out_dtype)
+    grads, gq, gg = route_list_bwd(sources, query, gain, ctx.eps, g_out, g_lse)
+    need = ctx.needs_input_grad
+    return (
+        list(grads) if need[0] else None,
+        gq if need[1] else None,
+        gg if (gain is not None and need[2]) else None,
+        None,
+        None,
+        None,
+        None,
+    )
+
+
+route_list.register_autograd(_route_list_backward, setup_context=_route_list_setup_context)
+
+
 # ------------------------------------------------------------------ merge --
 
 
@@ -384,4 +613,26 @@ def check_forward_only(*tensors: Optional[Tensor]) -> None:
     _no_grad_needed(*tensors)
 
 
-__all__ = ["route", "route_list", "merge", "block_step", "dtype_code", "check_forward_only"]
+def check_differentiable_queries(query: Tensor, *tensors: Optional[Tensor]) -> None:
+    """Raise before the forward if autograd would need a multi-query backward."""
+    if query.dim() == 2 and query.shape[0] > 1:
+        try:
+            _no_grad_needed(query, *tensors)
+        except NotImplementedError:
+            raise NotImplementedError(
+                f"attnres_hip: backward is implemented for one query; a phase-1 call with {query.shape[0]} "
+                "queries is forward-only (run it under torch.no_grad() or detach the inputs)"
+            ) from None
+
+
+__all__ = [
+    "route",
+    "route_list",
+    "route_bwd",
+    "route_list_bwd",
+    "merge",
+    "block_step",
+    "dtype_code",
+    "check_forward_only",
+    "check_differentiable_queries",
+]

@@ -11,7 +11,9 @@
 Result dtype follows the reference's einsum branch (llama.py:640-644): the
 promotion of the sources' dtype with ``query * norm.weight``'s.  The kernels
 accumulate in fp32 and round the output once.  There is no CPU path: CPU
-tensors raise, and the functions are forward-only.
+tensors raise.  :func:`route_static` and :func:`block_attn_res_from_list` are
+differentiable (gradients of the sources, the query and the norm gain come
+from the backward kernels); :func:`route_weights` is forward-only.
 """
 
 from __future__ import annotations
@@ -44,7 +46,6 @@ def route_static(
     of active slots is routed by passing their pointers.
     """
     gain = norm.weight
-    ops.check_forward_only(buf, query, gain)
     out_dtype = _out_dtype(buf.dtype, query, gain)
     if num_active:
         n = int(num_active)
@@ -66,7 +67,6 @@ def block_attn_res_from_list(sources: Sequence[Tensor], query: Tensor, norm) -> 
     itself gives the same result without building the padded buffer.
     """
     gain = norm.weight
-    ops.check_forward_only(*sources, query, gain)
     out_dtype = _out_dtype(sources[0].dtype, query, gain)
     res = ops.route_list(list(sources), query, gain, float(norm.eps), out_dtype, False, False)
     return res[0][0]

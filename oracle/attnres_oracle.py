@@ -13,6 +13,8 @@ Everything here is float64 numpy restated from the reference's own Python
                          lse / aux outputs                       kernels/phase_1.py:43-101
 * :func:`route_masked`   the einsum branch over a padded buffer
                          with a boolean slot mask                llama.py:640-644
+* :func:`route_backward` gradients of out (and lse) w.r.t. the
+                         sources and the folded query           kernels/phase_1.py:104-280
 * :func:`merge`          phase-2 online-softmax merge           kernels/phase_2.py:40-57
 * :func:`schedule`       boundary set, masks, active counts      llama.py:545-571
 * :func:`block_forward`  caller order: route -> commit -> add    llama.py:697-715 (742-762)
@@ -24,7 +26,9 @@ x_s = c_s*u with u in {+-1}^D, qw = beta*u gives logit_s = c_s*beta*D /
 sqrt(c_s^2+eps)), invariants (scale invariance of logits, permutation
 equivariance, weights sum to 1, masked slots exactly 0, gain folding,
 phase-2 merge == routing over one more source), a pure-Python brute force on
-tiny shapes, and the schedule tables derived by hand from llama.py:545-571.
+tiny shapes, the schedule tables derived by hand from llama.py:545-571, and
+for the backward central finite differences plus float64 torch autograd
+through the einsum branch's op sequence.
 """
 
 from __future__ import annotations
@@ -292,3 +296,41 @@ def route_bruteforce(sources, qw, eps: float) -> dict:
         for k in range(D):
             out[t][k] = math.fsum(weights[s][t] * float(sources[s][t][k]) for s in range(S))
     return {"out": out, "weights": weights}
+
+
+# -------------------------------------------------------------- backward --
+
+
+def route_backward(sources, qw, eps: float, grad_out, grad_lse=None) -> dict:
+    """Gradients of the routing output w.r.t. the sources and the folded query.
+
+    For one query: with r_s = rsqrt(mean(x_s^2)+eps), l_s = (x_s.qw) r_s,
+    w = softmax(l), out = sum_s w_s x_s, lse = logsumexp(l), G = dL/dout and
+    g_lse = dL/dlse (zero when absent),
+      a_s  = G . x_s,  o = G . out,  dl_s = w_s (g_lse + a_s - o)
+      dx_s = w_s G + dl_s r_s qw - dl_s l_s r_s^2 / D * x_s
+      dqw  = sum over tokens and s of dl_s r_s x_s
+    (the chain rule through llama.py:640-644; the Triton backward computes the
+    same terms, kernels/phase_1.py:104-280).  Returns dx (S, N, D), dqw (D,).
+    """
+    x = np.asarray(sources, dtype=np.float64)
+    q = np.asarray(qw, dtype=np.float64).reshape(-1)
+    g = np.asarray(grad_out, dtype=np.float64)
+    S, N, D = x.shape
+    r = 1.0 / np.sqrt(np.mean(x * x, axis=-1) + eps)  # (S, N)
+    l = np.einsum("snd,d->sn", x, q) * r
+    m = l.max(axis=0, keepdims=True)
+    e = np.exp(l - m)
+    w = e / e.sum(axis=0, keepdims=True)  # (S, N)
+    out = np.einsum("sn,snd->nd", w, x)
+    a = np.einsum("nd,snd->sn", g, x)
+    o = np.einsum("nd,nd->n", g, out)
+    gl = np.zeros(N) if grad_lse is None else np.asarray(grad_lse, dtype=np.float64).reshape(N)
+    dl = w * (gl[None, :] + a - o[None, :])
+    dx = (
+        w[:, :, None] * g[None]
+        + (dl * r)[:, :, None] * q[None, None, :]
+        - (dl * l * r * r / D)[:, :, None] * x
+    )
+    dqw = np.einsum("sn,snd->d", dl * r, x)
+    return {"dx": dx, "dqw": dqw}

@@ -1,0 +1,291 @@
+"""Backward of the routing ops on the GPU against the float64 oracle.
+
+The gradients come from ``torch.autograd`` through the drop-ins
+(``route_static``, ``block_attn_res_from_list``, the phase-1 mirror), which
+call ``attnres_route_bwd`` through the C ABI.  The oracle is
+``route_backward`` (pinned on the CPU by finite differences and by float64
+autograd through the einsum branch's op sequence), evaluated on the identical
+input values.
+
+Tolerances:
+* fp32 gradients: |g - ref| <= 1e-4 |ref| + 1e-5 max|ref|  (fp32 dot products of
+  length D and a sum over tokens for the query/gain gradients);
+* bf16 gradients: |g - ref| <= 1 bf16 ulp of |ref| + 1e-3 max|ref|, and at least
+  95% of the elements equal to the correctly rounded oracle (one rounding of
+  an fp32-accumulated value).
+At the full BASELINE shape the oracle runs on sampled rows; on every row the
+identity x_s . dx_s = w_s (G . x_s) + dl_s l_s eps r_s^2 (logits are
+scale-invariant up to eps; dl_s = w_s (g_lse + G.x_s - G.out)) is checked
+against an fp32 torch restatement, which also gives the query and gain
+gradients summed over all rows.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import kotodama_amd
+from kotodama_amd import _capi, ops, workloads
+from kotodama_amd.flash_attn_res import phase_1_batched_attention_triton_op
+from oracle import attnres_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+class Norm(torch.nn.Module):
+    def __init__(self, weight, eps):
+        super().__init__()
+        self.weight = torch.nn.Parameter(weight)
+        self.eps = eps
+
+
+def np64(t):
+    return t.detach().float().cpu().double().numpy()
+
+
+def bf16_ulp(x):
+    a = np.abs(x)
+    e = np.floor(np.log2(np.maximum(a, 2.0**-126)))
+    return 2.0 ** (e - 7)
+
+
+def check_grad(g, ref, dtype, label, exact_frac=0.95):
+    got = np64(g)
+    err = np.abs(got - ref)
+    scale = np.abs(ref).max() if ref.size else 0.0
+    if dtype == torch.float32:
+        tol = 1e-4 * np.abs(ref) + 1e-5 * scale
+        assert (err <= tol).all(), f"{label}: worst err {err.max():.3e} (max|ref| {scale:.3e})"
+    else:
+        tol = bf16_ulp(ref) + 1e-3 * scale
+        assert (err <= tol).all(), f"{label}: worst err {err.max():.3e} (max|ref| {scale:.3e})"
+        same = np.mean(got == O.bf16_round(ref))
+        assert same >= exact_frac, f"{label}: only {same:.4f} equal the correctly rounded oracle"
+
+
+def make_case(gpu, S, extra, B, T, D, dtype, seed, param_dtype=None):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    scales = torch.exp(torch.empty(S + extra).uniform_(np.log(0.5), np.log(4.0), generator=g))
+    buf = torch.randn(S + extra, B, T, D, generator=g) * scales[:, None, None, None]
+    buf[S:] = 0
+    pd = param_dtype or dtype
+    query = (torch.randn(D, generator=g) * 0.05).to(pd)
+    gain = (1 + 0.1 * torch.randn(D, generator=g)).to(pd)
+    # bf16-exact, so the gradient that reaches a bf16 output is G itself
+    G = torch.randn(B, T, D, generator=g).to(torch.bfloat16).float()
+    return buf.to(dtype).to(gpu), query.to(gpu), gain.to(gpu), G.to(gpu)
+
+
+def oracle_grads(buf, S, query, gain, G, eps, param, grad_lse=None):
+    D = buf.shape[-1]
+    x = np64(buf[:S]).reshape(S, -1, D)
+    pd = "bf16" if param == torch.bfloat16 else "f32"
+    qw = O.fold_query(np64(query), np64(gain), pd)
+    b = O.route_backward(x, qw, eps, np64(G).reshape(-1, D), None if grad_lse is None else np64(grad_lse).reshape(-1))
+    return b["dx"], b["dqw"] * np64(gain), b["dqw"] * np64(query)
+
+
+CASES = [
+    # (dtype, S, D, B, T)
+    (torch.float32, 1, 256, 2, 48),
+    (torch.float32, 3, 2048, 1, 64),
+    (torch.float32, 9, 1024, 2, 40),
+    (torch.float32, 16, 512, 1, 33),
+    (torch.bfloat16, 1, 512, 2, 48),
+    (torch.bfloat16, 4, 3072, 1, 64),
+    (torch.bfloat16, 8, 4096, 2, 32),
+    (torch.bfloat16, 9, 8192, 1, 24),
+    (torch.bfloat16, 13, 1024, 2, 20),
+    (torch.bfloat16, 16, 4096, 1, 17),
+]
+
+
+@pytest.mark.parametrize("dtype,S,D,B,T", CASES, ids=[f"{str(c[0])[6:]}-S{c[1]}-D{c[2]}" for c in CASES])
+def test_route_static_backward_matches_oracle(gpu, dtype, S, D, B, T):
+    print(f"route_static backward {dtype} S={S} D={D} B={B} T={T}", flush=True)
+    eps = 1e-5
+    buf, query, gain, G = make_case(gpu, S, 2, B, T, D, dtype, seed=100 + S + D)
+    buf.requires_grad_(True)
+    query.requires_grad_(True)
+    norm = Norm(gain.clone(), eps)
+    mask = torch.zeros(S + 2, dtype=torch.bool, device=gpu)
+    mask[:S] = True
+    out = kotodama_amd.route_static(buf, query, norm, mask, S)
+    (out.float() * G).sum().backward()
+    dx, dq, dg = oracle_grads(buf, S, query, norm.weight, G, eps, dtype)
+    check_grad(buf.grad[:S].reshape(S, -1, D), dx, dtype, "dsources")
+    assert torch.all(buf.grad[S:] == 0), "inactive slots must get zero gradient"
+    check_grad(query.grad, dq, dtype, "dquery")
+    check_grad(norm.weight.grad, dg, dtype, "dgain")
+
+
+def test_list_backward_and_separate_tensors(gpu):
+    # block_attn_res_from_list: each source its own allocation (no stacked buffer)
+    eps = 1e-5
+    S, B, T, D = 5, 2, 30, 2048
+    buf, query, gain, G = make_case(gpu, S, 0, B, T, D, torch.bfloat16, seed=7)
+    srcs = [buf[i].clone().requires_grad_(True) for i in range(S)]
+    norm = Norm(gain.clone(), eps)
+    out = kotodama_amd.block_attn_res_from_list(srcs, query, norm)
+    (out.float() * G).sum().backward()
+    dx, _, dg = oracle_grads(buf, S, query, norm.weight, G, eps, torch.bfloat16)
+    for s in range(S):
+        check_grad(srcs[s].grad.reshape(-1, D), dx[s], torch.bfloat16, f"dsource[{s}]")
+    check_grad(norm.weight.grad, dg, torch.bfloat16, "dgain")
+    assert query.grad is None  # query did not require grad
+
+
+def test_non_prefix_mask_backward(gpu):
+    # any active set: the drop-in routes slots {0, 2, 3} of a 5-slot buffer
+    eps = 1e-5
+    B, T, D = 1, 40, 1024
+    buf, query, gain, G = make_case(gpu, 5, 0, B, T, D, torch.float32, seed=9)
+    idx = [0, 2, 3]
+    buf.requires_grad_(True)
+    norm = Norm(gain.clone(), eps)
+    mask = torch.zeros(5, dtype=torch.bool, device=gpu)
+    mask[idx] = True
+    out = kotodama_amd.route_static(buf, query, norm, mask, 0)
+    (out * G).sum().backward()
+    sub = buf.detach()[idx]
+    dx, _, dg = oracle_grads(sub, 3, query, norm.weight, G, eps, torch.float32)
+    check_grad(buf.grad[idx].reshape(3, -1, D), dx, torch.float32, "dsources")
+    assert torch.all(buf.grad[[1, 4]] == 0)
+    check_grad(norm.weight.grad, dg, torch.float32, "dgain")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_phase_1_backward_with_lse_term(gpu, dtype):
+    # the phase-1 op with Q = 1: the loss uses both the output and the lse
+    eps = 1e-6
+    S, B, T, D = 6, 2, 24, 1024
+    buf, query, gain, G = make_case(gpu, S, 1, B, T, D, dtype, seed=31)
+    qw = (query * gain).detach().requires_grad_(True)
+    buf.requires_grad_(True)
+    gl = torch.randn(1, B, T, device=gpu)
+    out, lse = phase_1_batched_attention_triton_op(buf, qw.unsqueeze(0), eps, num_active=S)
+    (out.float() * G).sum().add_((lse * gl).sum()).backward()
+    x = np64(buf[:S]).reshape(S, -1, D)
+    b = O.route_backward(x, np64(qw), eps, np64(G).reshape(-1, D), np64(gl).reshape(-1))
+    check_grad(buf.grad[:S].reshape(S, -1, D), b["dx"], dtype, "dsources")
+    assert torch.all(buf.grad[S:] == 0)
+    check_grad(qw.grad, b["dqw"], dtype, "dqw")
+
+
+def test_multi_query_grad_raises(gpu):
+    buf = torch.randn(3, 1, 8, 256, device=gpu, requires_grad=True)
+    q = torch.randn(2, 256, device=gpu)
+    with pytest.raises(NotImplementedError, match="one query"):
+        phase_1_batched_attention_triton_op(buf, q, 1e-5)
+    with torch.no_grad():
+        phase_1_batched_attention_triton_op(buf, q, 1e-5)
+
+
+def test_mixed_param_dtypes_backward(gpu):
+    # fp32 query with a bf16 gain: the fold is taken in the promoted dtype
+    eps = 1e-5
+    S, B, T, D = 4, 1, 32, 512
+    buf, query, gain, G = make_case(gpu, S, 0, B, T, D, torch.bfloat16, seed=41, param_dtype=torch.float32)
+    query = query.float().requires_grad_(True)
+    norm = Norm(gain.to(torch.bfloat16), eps)
+    buf.requires_grad_(True)
+    out = kotodama_amd.route_static(buf, query, norm, torch.ones(S, dtype=torch.bool, device=gpu), S)
+    assert out.dtype == torch.float32
+    (out * G).sum().backward()
+    x = np64(buf).reshape(S, -1, D)
+    qw = np64(query) * np64(norm.weight)  # fp32 product of exact values
+    qw = np.asarray(qw, dtype=np.float32).astype(np.float64)
+    b = O.route_backward(x, qw, eps, np64(G).reshape(-1, D))
+    check_grad(buf.grad.reshape(S, -1, D), b["dx"], torch.bfloat16, "dsources")
+    check_grad(query.grad, b["dqw"] * np64(norm.weight), torch.float32, "dquery")
+
+
+def test_query_gradient_is_deterministic(gpu):
+    S, B, T, D = 8, 4, 512, 4096
+    buf, query, gain, G = make_case(gpu, S, 0, B, T, D, torch.bfloat16, seed=5)
+    res = []
+    for _ in range(2):
+        q = query.clone().requires_grad_(True)
+        out = kotodama_amd.route_static(buf, q, Norm(gain.clone(), 1e-5), torch.ones(S, dtype=torch.bool, device=gpu), S)
+        (out.float() * G).sum().backward()
+        res.append(q.grad.clone())
+    assert torch.equal(res[0], res[1])
+
+
+def test_capi_backward_argument_errors(gpu):
+    lib = _capi.lib()
+    x = torch.zeros(4, 256, device=gpu)
+    q = torch.zeros(256, device=gpu)
+    arr = _capi.pointer_array([x.data_ptr()])
+    garr = _capi.pointer_array([x.data_ptr()])
+    ws = torch.empty(16, device=gpu)
+    # workspace too small
+    rc = lib.attnres_route_bwd(arr, 1, 4, 256, 256, _capi.DTYPE_F32, q.data_ptr(), None, _capi.DTYPE_F32, 1e-5,
+                               x.data_ptr(), _capi.DTYPE_F32, 256, None, garr, 256, ws.data_ptr(), 64, None, None,
+                               None)
+    assert rc == _capi.ERR_ARG and b"workspace" in lib.attnres_last_error()
+    # S = 0 has nothing to differentiate
+    rc = lib.attnres_route_bwd(arr, 0, 4, 256, 256, _capi.DTYPE_F32, q.data_ptr(), None, _capi.DTYPE_F32, 1e-5,
+                               x.data_ptr(), _capi.DTYPE_F32, 256, None, garr, 256, ws.data_ptr(), 64, None, None,
+                               None)
+    assert rc == _capi.ERR_UNSUPPORTED
+    # grad_gain without gain
+    rc = lib.attnres_route_bwd(arr, 1, 4, 256, 256, _capi.DTYPE_F32, q.data_ptr(), None, _capi.DTYPE_F32, 1e-5,
+                               x.data_ptr(), _capi.DTYPE_F32, 256, None, garr, 256, ws.data_ptr(), 64, None,
+                               q.data_ptr(), None)
+    assert rc == _capi.ERR_ARG
+
+
+def test_full_size_3b_backward_properties(gpu):
+    # the 3B prefill shape (B=8, T=4096, D=3072) at S=8, bf16
+    w = workloads.get("cfg2")
+    pool = workloads.make_pool(w, gpu, 3)
+    S = 8
+    q, gn = workloads.make_params(w, gpu, 3, 1)
+    eps = w.eps
+    buf = pool[:S].detach().clone().requires_grad_(True)
+    del pool
+    query = q[0].clone().requires_grad_(True)
+    norm = Norm(gn[0].clone(), eps)
+    n, D = buf[0].numel() // buf.shape[-1], buf.shape[-1]
+    gen = torch.Generator(device=gpu).manual_seed(11)
+    G = torch.randn(buf.shape[1:], device=gpu, generator=gen).to(torch.bfloat16).float()
+    gl = torch.randn(buf.shape[1:-1], device=gpu, generator=gen)
+    print(f"full-size backward S={S} N={n} D={D}", flush=True)
+    res = ops.route(buf, S, query, norm.weight, eps, torch.bfloat16, True, False)
+    (res[0][0].float() * G).sum().add_((res[2][0] * gl).sum()).backward()
+    torch.cuda.synchronize()
+
+    # fp32 torch restatement of the backward on every row
+    with torch.no_grad():
+        x = buf.detach().reshape(S, n, D).float()
+        Gf = G.reshape(n, D)
+        qw = (query.detach() * norm.weight.detach()).float()  # bf16 product, as the model folds it
+        r = torch.rsqrt(x.pow(2).mean(-1) + eps)
+        l = torch.einsum("snd,d->sn", x, qw) * r
+        w_ = torch.softmax(l, dim=0)
+        a = torch.einsum("snd,nd->sn", x, Gf)
+        o = (w_ * a).sum(0)
+        dl = w_ * (gl.reshape(1, n) + a - o)
+        dqw = torch.einsum("sn,snd->d", dl * r, x)
+        # every row: x_s . dx_s = w_s a_s + dl_s l_s eps r_s^2 (logits are scale-invariant up to eps)
+        dx = buf.grad.reshape(S, n, D).float()
+        lhs = (x * dx).sum(-1)
+        rhs = w_ * a + dl * l * eps * r * r
+        scale = (x.abs() * dx.abs()).sum(-1) + 1e-30
+        rel = ((lhs - rhs).abs() / scale).max().item()
+        del dx
+    assert rel < 1e-2, f"scale identity violated: rel {rel:.3e}"
+    # the query and gain gradients (sums over all 32768 rows)
+    for got, ref, label in ((query.grad, dqw * norm.weight.detach().float(), "dquery"),
+                            (norm.weight.grad, dqw * query.detach().float(), "dgain")):
+        g64, r64 = np64(got), ref.double().cpu().numpy()
+        tol = bf16_ulp(r64) + 1e-3 * np.abs(r64).max()
+        assert (np.abs(g64 - r64) <= tol).all(), f"{label}: worst err {np.abs(g64 - r64).max():.3e}"
+    # sampled rows against the float64 oracle
+    rows = torch.tensor(sorted({0, n - 1, *np.random.default_rng(3).choice(n, 96, replace=False).tolist()}),
+                        device=gpu)
+    xs = np64(x[:, rows])
+    ref = O.route_backward(xs, O.fold_query(np64(query), np64(norm.weight), "bf16"), eps, np64(Gf[rows]),
+                           np64(gl.reshape(n)[rows]))
+    check_grad(buf.grad.reshape(S, n, D)[:, rows], ref["dx"], torch.bfloat16, "dsources (sampled rows)")

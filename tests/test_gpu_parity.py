@@ -226,12 +226,18 @@ def test_host_checked_errors_raise(gpu):
         ops.route(buf.half(), 2, q.half(), None, 1e-5, torch.float16, False, False)
 
 
-def test_forward_only_on_gpu(gpu):
+def test_forward_only_paths_on_gpu(gpu):
+    # route_static is differentiable; the weights helper and the arena engine are not
     buf = torch.randn((2, 1, 4, 64), device=gpu)
     q = torch.zeros(64, device=gpu, requires_grad=True)
-    with pytest.raises(NotImplementedError):
-        kotodama_amd.route_static(buf, q, Norm(torch.ones(64, device=gpu), 1e-5),
-                                  torch.ones(2, dtype=torch.bool, device=gpu), 2)
+    norm = Norm(torch.ones(64, device=gpu), 1e-5)
+    out = kotodama_amd.route_static(buf, q, norm, torch.ones(2, dtype=torch.bool, device=gpu), 2)
+    assert out.requires_grad
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        kotodama_amd.route_weights(buf, 2, q, norm)
+    arena = torch.zeros((3, 1, 4, 64), device=gpu)
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        ops.check_forward_only(arena, q)
 
 
 # ------------------------------------------------ full-size configs --

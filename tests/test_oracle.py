@@ -192,3 +192,79 @@ def test_block_forward_caller_order():
     assert np.array_equal(r["outs"][0], embed)
     fin = O.route(np.stack([r["committed"][0], r["committed"][1], r["partial"]]), qws[6], 1e-5)
     np.testing.assert_allclose(r["outs"][6], fin["out"][0], rtol=1e-13)
+
+
+# ------------------------------------------------------------- backward --
+
+
+def test_backward_matches_finite_differences():
+    # central differences of L = sum(G * out) in float64 on a tiny case
+    rng = np.random.default_rng(60)
+    S, N, D, eps = 3, 2, 6, 1e-3
+    x = rng.standard_normal((S, N, D)) * np.array([0.5, 1.0, 2.0])[:, None, None]
+    q = rng.standard_normal(D) * 0.7
+    G = rng.standard_normal((N, D))
+    b = O.route_backward(x, q, eps, G)
+
+    def loss(xx, qq):
+        return float(np.sum(G * O.route(xx, qq, eps)["out"][0]))
+
+    h = 1e-6
+    num_dx = np.zeros_like(x)
+    for idx in np.ndindex(*x.shape):
+        xp = x.copy(); xp[idx] += h
+        xm = x.copy(); xm[idx] -= h
+        num_dx[idx] = (loss(xp, q) - loss(xm, q)) / (2 * h)
+    num_dq = np.zeros_like(q)
+    for k in range(D):
+        qp = q.copy(); qp[k] += h
+        qm = q.copy(); qm[k] -= h
+        num_dq[k] = (loss(x, qp) - loss(x, qm)) / (2 * h)
+    np.testing.assert_allclose(b["dx"], num_dx, rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(b["dqw"], num_dq, rtol=1e-6, atol=1e-8)
+
+
+def test_backward_matches_torch_autograd_of_reference_op_sequence():
+    # an independent implementation: autograd through llama.py:640-644's ops in float64
+    g = torch.Generator().manual_seed(61)
+    S, B, T, D = 4, 2, 5, 32
+    buf = (torch.randn(6, B, T, D, generator=g, dtype=torch.float64))
+    buf[S:] = 0
+    buf.requires_grad_(True)
+    query = (torch.randn(D, generator=g, dtype=torch.float64) * 0.3).requires_grad_(True)
+    gain = (1 + 0.1 * torch.randn(D, generator=g, dtype=torch.float64)).requires_grad_(True)
+    mask = torch.tensor([True] * S + [False] * 2)
+    G = torch.randn(B, T, D, generator=g, dtype=torch.float64)
+    out = TP.route_static_cpu(buf, query * gain, 1e-5, mask)
+    (out * G).sum().backward()
+    qw = (query * gain).detach().numpy()
+    b = O.route_backward(buf.detach()[:S].reshape(S, B * T, D).numpy(), qw, 1e-5, G.reshape(B * T, D).numpy())
+    np.testing.assert_allclose(buf.grad[:S].reshape(S, B * T, D).numpy(), b["dx"], rtol=1e-10, atol=1e-12)
+    assert torch.all(buf.grad[S:] == 0)
+    np.testing.assert_allclose(query.grad.numpy(), b["dqw"] * gain.detach().numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(gain.grad.numpy(), b["dqw"] * query.detach().numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_backward_lse_term_matches_finite_differences():
+    # L = sum(G * out) + sum(g_lse * lse): the lse gradient enters the logits only
+    rng = np.random.default_rng(62)
+    S, N, D, eps = 4, 3, 5, 1e-3
+    x = rng.standard_normal((S, N, D))
+    q = rng.standard_normal(D)
+    G = rng.standard_normal((N, D))
+    gl = rng.standard_normal(N)
+    b = O.route_backward(x, q, eps, G, grad_lse=gl)
+
+    def loss(xx, qq):
+        r = O.route(xx, qq, eps)
+        return float(np.sum(G * r["out"][0]) + np.sum(gl * r["lse"][0]))
+
+    h = 1e-6
+    num_dx = np.zeros_like(x)
+    for idx in np.ndindex(*x.shape):
+        xp = x.copy(); xp[idx] += h
+        xm = x.copy(); xm[idx] -= h
+        num_dx[idx] = (loss(xp, q) - loss(xm, q)) / (2 * h)
+    num_dq = np.array([(loss(x, q + h * e) - loss(x, q - h * e)) / (2 * h) for e in np.eye(D)])
+    np.testing.assert_allclose(b["dx"], num_dx, rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(b["dqw"], num_dq, rtol=1e-6, atol=1e-8)
