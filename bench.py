@@ -17,8 +17,11 @@ Also on the JSON line:
   extrapolated to the full step.
 
 ``--workload cfg3|cfg4|cfg5`` measures the other shapes (cfg4 = 8B decode step,
-65 fused block steps captured in one HIP graph).  ``--gpus`` above 1 exits:
-this build measures one GPU.
+65 fused block steps captured in one HIP graph).  ``--pass bwd`` times the
+backward of the same routing calls instead (attnres_route_bwd on preallocated
+gradient buffers: (2S+1) * B*T*D * 2 algorithmic bytes per call — sources and
+dL/dout read, source gradients written).  ``--gpus`` above 1 exits: this
+build measures one GPU.
 """
 
 from __future__ import annotations
@@ -51,6 +54,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOAD_TEXT))
+    ap.add_argument("--pass", dest="pass_", default="fwd", choices=("fwd", "bwd"),
+                    help="time the routing forward (default) or its backward")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="tokens per CPU-baseline sample call")
     return ap.parse_args()
@@ -160,6 +165,66 @@ def bench_sweep(w, steps: int, warmup: int, dev):
     return elapsed, dominant, dom_ms, w.call_bytes(dominant)
 
 
+def bwd_call_bytes(w, s: int) -> int:
+    """Algorithmic bytes of one backward call: S source rows + dL/dout read, S gradient rows written."""
+    return (2 * s + 1) * w.tokens * w.hidden * w.elem_bytes
+
+
+def bench_backward(w, steps: int, warmup: int, dev):
+    """The backward of every routing call of the schedule, through the C ABI on preallocated buffers."""
+    import torch
+
+    from kotodama_amd import _capi, ops, workloads
+
+    pool = workloads.make_pool(w, dev, seed=2)
+    q, gn = workloads.make_params(w, dev, seed=2, count=len(w.calls))
+    gen = torch.Generator(device=dev).manual_seed(5)
+    gout = torch.randn(pool.shape[1:], device=dev, generator=gen).to(w.dtype)
+    grad = torch.empty_like(pool)
+    n, d = w.tokens, w.hidden
+    ws = torch.empty(_capi.route_bwd_workspace_size(n, d) // 4, device=dev, dtype=torch.float32)
+    dq = torch.empty(d, device=dev, dtype=q.dtype)
+    dg = torch.empty(d, device=dev, dtype=gn.dtype)
+    slot = n * d * pool.element_size()
+    src_ptrs = [pool.data_ptr() + i * slot for i in range(pool.shape[0])]
+    grad_ptrs = [grad.data_ptr() + i * slot for i in range(pool.shape[0])]
+    code = ops.dtype_code(w.dtype)
+    pcode = ops.dtype_code(q.dtype)
+    dominant = max(w.calls)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    args = []
+    for j, s in enumerate(w.calls):
+        args.append((s, (
+            _capi.pointer_array(src_ptrs[:s]), s, n, d, d, code, q[j].data_ptr(), gn[j].data_ptr(), pcode, w.eps,
+            gout.data_ptr(), code, d, None, _capi.pointer_array(grad_ptrs[:s]), d, ws.data_ptr(), ws.numel() * 4,
+            dq.data_ptr(), dg.data_ptr(), stream)))
+
+    def step(events=None):
+        for s, a in args:
+            if events is not None and s == dominant:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                _capi.route_bwd(*a)
+                e1.record()
+                events.append((e0, e1))
+            else:
+                _capi.route_bwd(*a)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    events: list = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(events)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    dom_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in events)
+    step_bytes = sum(bwd_call_bytes(w, s) for s in w.calls)
+    return elapsed, dominant, dom_ms, bwd_call_bytes(w, dominant), step_bytes
+
+
 def bench_decode(w, steps: int, warmup: int, dev):
     """cfg4: one decode step = 65 fused block steps, captured in a HIP graph."""
     import torch
@@ -243,6 +308,38 @@ def main() -> int:
         return 0
     w = workloads.get(args.workload)
     roofline = None
+    if args.pass_ == "bwd":
+        if args.workload == "cfg4":
+            print("bench.py: --pass bwd covers the prefill workloads (cfg2, cfg3, cfg5)", file=sys.stderr)
+            return 2
+        elapsed, dominant, dom_ms, dom_bytes, step_bytes = bench_backward(w, args.steps, args.warmup, dev)
+        ms_per_step = elapsed * 1e3 / args.steps
+        gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+        achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+        t = 'bf' if w.dtype == torch.bfloat16 else 'f32'
+        name = f"attnres_route_bwd_{t}_g{t}_s{dominant}_v1 (+ attnres_reduce_dqw_stage, attnres_reduce_dqw)"
+        print(json.dumps({
+            "metric": "AttnRes routing backward achieved HBM GB/s",
+            "value": round(gbs, 2),
+            "unit": "GB/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms_per_step, 4),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "bf16" if w.dtype == torch.bfloat16 else "fp32",
+            "data": "synthetic (seeded sources and dL/dout, resident in HBM)",
+            "config": {"workload": "backward of: " + WORKLOAD_TEXT[args.workload], "routing_calls": len(w.calls),
+                       "algorithmic_bytes_per_step": step_bytes},
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(w.tokens / (ms_per_step * 1e-3), 1),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+                         "algorithmic_bytes": dom_bytes, "avg_ms": round(dom_ms, 4)},
+        }), flush=True)
+        return 0
     if args.workload == "cfg4":
         elapsed, step_bytes, graph_ms = bench_decode(w, args.steps, args.warmup, dev)
         ms_per_step = elapsed * 1e3 / args.steps

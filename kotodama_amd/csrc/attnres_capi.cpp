@@ -60,13 +60,15 @@ constexpr int kMergeFuncs = 4 * 2;
 constexpr int kStreamMaxChunks = 8;  // rows of up to 8 KiB
 constexpr int kStreamWaves = 4;      // waves per workgroup of the streaming kernels
 constexpr int kStreamFuncs = kTypeCombos * kStreamMaxChunks * 2;
-constexpr int kBwdFuncs = 2 * kNumS * 2;  // (bf16 | fp32) x S x V
+constexpr int kBwdFuncs = 4 * kNumS * 2;  // (source, grad_out) dtype pairs x S x V
 constexpr int kBwdMaxPerCu = 4;           // workgroups per CU the backward grid may use (workspace bound)
+constexpr size_t kBwdStaticLds = 2 * ATTNRES_KMAX_WAVES * 48 * sizeof(float);  // reduction buffer, S = 16
 
 struct DeviceState {
   std::atomic<bool> loaded{false};
   hipModule_t mods[kParts] = {};
   int num_cus = 0;
+  int max_lds = 0;  // bytes of LDS one workgroup may use
   hipFunction_t route[kRouteFuncs] = {};
   int route_bpc[kRouteFuncs] = {};  // resident workgroups per CU, for the launch block size used
   int route_bpc_block[kRouteFuncs] = {};
@@ -79,6 +81,7 @@ struct DeviceState {
   int bwd_bpc[kBwdFuncs] = {};
   int bwd_bpc_block[kBwdFuncs] = {};
   hipFunction_t reduce = nullptr;
+  hipFunction_t reduce_stage = nullptr;
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -126,6 +129,8 @@ int ensure_loaded(DeviceState** out) {
       }
       e = hipDeviceGetAttribute(&st.num_cus, hipDeviceAttributeMultiprocessorCount, dev);
       if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
+      e = hipDeviceGetAttribute(&st.max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+      if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MaxSharedMemoryPerBlock)");
       st.loaded.store(true, std::memory_order_release);
     }
   }
@@ -217,18 +222,18 @@ int get_merge(DeviceState& st, bool pbf, bool ibf, int v, int block, hipFunction
 int part_of_bwd(int s) { return s <= 8 ? 4 : 5; }
 constexpr int kReducePart = 4;
 
-int get_bwd(DeviceState& st, bool bf, int s, int v, int block, hipFunction_t* f, int* bpc) {
-  const int idx = ((bf ? 0 : 1) * kNumS + s) * 2 + (v - 1);
+int get_bwd(DeviceState& st, bool bf, bool gbf, int s, int v, int block, size_t lds, hipFunction_t* f, int* bpc) {
+  const int idx = (((bf ? 0 : 2) + (gbf ? 0 : 1)) * kNumS + s) * 2 + (v - 1);
   std::lock_guard<std::mutex> lk(g_mu);
   if (st.bwd[idx] == nullptr) {
     char name[96];
-    snprintf(name, sizeof(name), "attnres_route_bwd_%s_s%d_v%d", bf ? "bf" : "f32", s, v);
+    snprintf(name, sizeof(name), "attnres_route_bwd_%s_g%s_s%d_v%d", bf ? "bf" : "f32", gbf ? "bf" : "f32", s, v);
     int rc = find_function(st, part_of_bwd(s), name, &st.bwd[idx]);
     if (rc != ATTNRES_OK) return rc;
   }
   if (st.bwd_bpc_block[idx] != block) {
     int nb = 0;
-    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.bwd[idx], block, 0);
+    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.bwd[idx], block, lds);
     if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
     st.bwd_bpc[idx] = nb > 0 ? nb : 1;
     st.bwd_bpc_block[idx] = block;
@@ -238,13 +243,16 @@ int get_bwd(DeviceState& st, bool bf, int s, int v, int block, hipFunction_t* f,
   return ATTNRES_OK;
 }
 
-int get_reduce(DeviceState& st, hipFunction_t* f) {
+int get_reduce(DeviceState& st, hipFunction_t* stage, hipFunction_t* fin) {
   std::lock_guard<std::mutex> lk(g_mu);
   if (st.reduce == nullptr) {
-    int rc = find_function(st, kReducePart, "attnres_reduce_dqw", &st.reduce);
+    int rc = find_function(st, kReducePart, "attnres_reduce_dqw_stage", &st.reduce_stage);
+    if (rc != ATTNRES_OK) return rc;
+    rc = find_function(st, kReducePart, "attnres_reduce_dqw", &st.reduce);
     if (rc != ATTNRES_OK) return rc;
   }
-  *f = st.reduce;
+  *stage = st.reduce_stage;
+  *fin = st.reduce;
   return ATTNRES_OK;
 }
 
@@ -284,11 +292,11 @@ bool valid_dtype(int d) { return d == ATTNRES_DTYPE_F32 || d == ATTNRES_DTYPE_BF
 int esize(int d) { return d == ATTNRES_DTYPE_BF16 ? 2 : 4; }
 
 template <typename Params>
-int launch(hipFunction_t f, int grid, int block, Params& P, void* stream) {
+int launch(hipFunction_t f, int grid, int block, Params& P, void* stream, int grid_y = 1, size_t lds = 0) {
   size_t sz = sizeof(Params);
   void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &P, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz, HIP_LAUNCH_PARAM_END};
-  hipError_t e = hipModuleLaunchKernel(f, (unsigned)grid, 1, 1, (unsigned)block, 1, 1, 0, (hipStream_t)stream,
-                                       nullptr, cfg);
+  hipError_t e = hipModuleLaunchKernel(f, (unsigned)grid, (unsigned)grid_y, 1, (unsigned)block, 1, 1, (unsigned)lds,
+                                       (hipStream_t)stream, nullptr, cfg);
   if (e != hipSuccess) return hip_fail(e, "hipModuleLaunchKernel");
   return ATTNRES_OK;
 }
@@ -639,7 +647,13 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   const int block = v == 1 ? round64(nchunk) : round64((nchunk + 1) / 2);
   hipFunction_t f = nullptr;
   int bpc = 1;
-  rc = get_bwd(*st, bf, num_sources, v, block, &f, &bpc);
+  // dynamic LDS (S >= 5): each thread's qw chunks and, with one chunk per
+  // thread, its query-gradient sums (fp32)
+  const size_t lds = num_sources >= 5 ? (size_t)(v == 1 ? 2 : 1) * nchunk * vec * sizeof(float) : 0;
+  if (lds + kBwdStaticLds > (size_t)st->max_lds)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d needs %zu bytes of LDS per workgroup (device limit %d)", hidden,
+                lds + kBwdStaticLds, st->max_lds);
+  rc = get_bwd(*st, bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, v, block, lds, &f, &bpc);
   if (rc != ATTNRES_OK) return rc;
   int64_t grid = (int64_t)st->num_cus * (bpc < kBwdMaxPerCu ? bpc : kBwdMaxPerCu);
   if (grid > num_tokens) grid = num_tokens;
@@ -648,9 +662,9 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
     return fail(ATTNRES_ERR_ARG, "workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
                 (long long)need);
   if (!aligned16(workspace)) return fail(ATTNRES_ERR_ALIGN, "workspace not 16-byte aligned");
-  hipFunction_t fr = nullptr;
+  hipFunction_t fr = nullptr, fs = nullptr;
   if (grad_query != nullptr || grad_gain != nullptr) {
-    rc = get_reduce(*st, &fr);
+    rc = get_reduce(*st, &fs, &fr);
     if (rc != ATTNRES_OK) return rc;
   }
 
@@ -675,19 +689,27 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   P.gout_bf16 = grad_out_dtype == ATTNRES_DTYPE_BF16;
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
-  rc = launch(f, (int)grid, block, P, stream);
+  rc = launch(f, (int)grid, block, P, stream, 1, lds);
   if (rc != ATTNRES_OK || fr == nullptr) return rc;
 
+  // Query/gain gradients: the grid's partial rows are summed in 64-row blocks
+  // (stage 1, in place), then the block sums (final stage); fixed order.
   attnres_reduce_params R;
   std::memset(&R, 0, sizeof(R));
-  R.part = static_cast<const float*>(workspace);
+  R.part = static_cast<float*>(workspace);
   R.query = query;
   R.gain = gain;
   R.dquery = grad_query;
   R.dgain = grad_gain;
   R.nparts = (int)grid;
+  R.part_step = 1;
   R.d = hidden;
   R.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
+  if (grid > 64) {
+    rc = launch(fs, (hidden + 63) / 64, 256, R, stream, (int)((grid + 63) / 64));
+    if (rc != ATTNRES_OK) return rc;
+    R.part_step = 64;
+  }
   return launch(fr, (hidden + 255) / 256, 256, R, stream);
 }
 

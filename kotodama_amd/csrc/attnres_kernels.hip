@@ -985,20 +985,62 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
 
 
 // ------------------------------------------------------- backward body --
+
+// Source counts up to which the next row is loaded before the current row's
+// gradients are stored (the prefetch holds a second copy of the row).
+#ifndef ATTNRES_BWD_PREFETCH_MAX_S
+#define ATTNRES_BWD_PREFETCH_MAX_S 4
+#endif
 //
 // One workgroup per token row (grid-stride), thread i owning chunks
 // i, i+blockDim, ... as in route_body.  The S source chunks and the output
-// gradient G are loaded into registers; per source the thread forms
+// gradient G are held in registers (packed); per source the thread forms
 // sum(x^2), x.qw and x.G, the 3S partial sums go through one DPP wave
 // reduction + LDS exchange, and every thread then recomputes the softmax and
 // writes its chunks of the S source gradients
-//   dx_s = w_s G + c1_s qw + c2_s x_s.
-// The query gradient sum_s c1_s x_s is accumulated in registers over all rows
-// the workgroup handles and written once as this workgroup's partial.
-template <int S, int V, bool BF16>
+//   dx_s = w_s G + c1_s qw + c2_s x_s,
+//   c1_s = dl_s r_s,  c2_s = -dl_s l_s r_s^2 / D,  dl_s = w_s (g_lse + G.x_s - G.out).
+// The next row's sources and G are loaded before the current row's gradients
+// are stored, so a workgroup's loads overlap its own stores.  The query
+// gradient sum_s c1_s x_s is accumulated in registers over all rows the
+// workgroup handles and written once as this workgroup's partial.
+
+// G (dL/dout) for one VEC-element chunk, packed as loaded: GBF = bf16 G.
+template <int VEC, bool GBF>
+struct GradChunk {
+  static constexpr int WORDS = VEC * (GBF ? 2 : 4) / 4;
+  uint32_t w[WORDS];
+  __device__ __forceinline__ void load(const char* row, int chunk) {
+    const char* p = row + (int64_t)chunk * (WORDS * 4);
+    if constexpr (WORDS == 2) {
+      const u32x2 t = ldg_global<u32x2>(p);
+      w[0] = t[0];
+      w[1] = t[1];
+    } else {
+#pragma unroll
+      for (int h = 0; h < WORDS / 4; ++h) {
+        const u32x4 t = ldg_global<u32x4>(p + h * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[4 * h + i] = t[i];
+      }
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < WORDS; ++i) w[i] = 0u;
+  }
+  __device__ __forceinline__ float elem(int e) const {
+    if constexpr (GBF) return (e & 1) ? bf_hi(w[e >> 1]) : bf_lo(w[e >> 1]);
+    else return as_f32(w[e]);
+  }
+};
+
+template <int S, int V, bool BF16, bool GBF>
 __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P) {
+  constexpr bool PF = S <= ATTNRES_BWD_PREFETCH_MAX_S;
   using C = Chunk<BF16>;
   constexpr int VEC = C::VEC;
+  using GC = GradChunk<VEC, GBF>;
   constexpr int NV = 3 * S;
   constexpr int RLD = ((NV + 3) / 4) * 4;
   __shared__ float red[2][ATTNRES_KMAX_WAVES][RLD];
@@ -1008,98 +1050,109 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
   const int wave = tid >> 6;
   const int nwaves = (blockDim.x + 63) >> 6;
 
+  // Where registers are tight (S >= 5) each thread's chunks of qw and, for
+  // V == 1, of its running query-gradient sum live in (dynamic) LDS instead,
+  // nchunk * VEC floats each; the LDS is thread-private, so no barrier.
+  constexpr bool QW_LDS = S >= 5;
+  constexpr bool DQW_LDS = QW_LDS && V == 1;
+  extern __shared__ float4 bwd_lds[];
+  float4* s_qw = bwd_lds;
+  float4* s_dqw = bwd_lds + P.nchunk * (VEC / 4);
+  float qw_reg[QW_LDS ? 1 : V][VEC];
+  float dqw_reg[DQW_LDS ? 1 : V][VEC];
+#pragma unroll
+  for (int k = 0; k < (DQW_LDS ? 1 : V); ++k) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dqw_reg[k][e] = 0.f;
+  }
+
   int chunk[V];
   bool ok[V];
-  float qwf[V][VEC];
-  float dqw[V][VEC];
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     chunk[k] = tid + k * (int)blockDim.x;
     ok[k] = chunk[k] < P.nchunk;
+    if (!ok[k]) continue;
     const int64_t off = (int64_t)chunk[k] * VEC;
-    if (ok[k]) {
-      load_param<VEC>(P.query, off, P.param_bf16, qwf[k]);
-      if (P.gain != nullptr) {
-        float g[VEC];
-        load_param<VEC>(P.gain, off, P.param_bf16, g);
+    float q[VEC];
+    load_param<VEC>(P.query, off, P.param_bf16, q);
+    if (P.gain != nullptr) {
+      float g[VEC];
+      load_param<VEC>(P.gain, off, P.param_bf16, g);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float prod = qwf[k][e] * g[e];
-          qwf[k][e] = P.param_bf16 ? round_bf16(prod) : prod;
-        }
+      for (int e = 0; e < VEC; ++e) {
+        const float prod = q[e] * g[e];
+        q[e] = P.param_bf16 ? round_bf16(prod) : prod;
+      }
+    }
+    if constexpr (QW_LDS) {
+#pragma unroll
+      for (int h = 0; h < VEC / 4; ++h) {
+        s_qw[chunk[k] * (VEC / 4) + h] = make_float4(q[4 * h], q[4 * h + 1], q[4 * h + 2], q[4 * h + 3]);
+        if constexpr (DQW_LDS) s_dqw[chunk[k] * (VEC / 4) + h] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) qwf[k][e] = 0.f;
+      for (int e = 0; e < VEC; ++e) qw_reg[QW_LDS ? 0 : k][e] = q[e];
     }
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) dqw[k][e] = 0.f;
   }
+  auto qw_chunk = [&](int k, float (&q)[VEC]) {
+    if constexpr (QW_LDS) {
+#pragma unroll
+      for (int h = 0; h < VEC / 4; ++h) {
+        const float4 t = s_qw[chunk[k] * (VEC / 4) + h];
+        q[4 * h] = t.x;
+        q[4 * h + 1] = t.y;
+        q[4 * h + 2] = t.z;
+        q[4 * h + 3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) q[e] = ok[k] ? qw_reg[QW_LDS ? 0 : k][e] : 0.f;
+    }
+  };
 
   const int64_t row_bytes_ld = P.src_ld * C::BYTES;
-  int ph = 0;
-  for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
-    u32x4 x[S][V];
-    float gf[V][VEC];
+  const int64_t grow_bytes_ld = P.gout_ld * (GBF ? 2 : 4);
+  u32x4 x[S][V];
+  GC g[V];
+  auto load_row = [&](int64_t t) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const char* row = reinterpret_cast<const char*>(P.src[s]) + tok * row_bytes_ld;
+      const char* row = reinterpret_cast<const char*>(P.src[s]) + t * row_bytes_ld;
 #pragma unroll
       for (int k = 0; k < V; ++k) x[s][k] = ok[k] ? ldg_global<u32x4>(row + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
     }
-    {
-      const char* grow = reinterpret_cast<const char*>(P.grad_out) + tok * P.gout_ld * (P.gout_bf16 ? 2 : 4);
+    const char* grow = reinterpret_cast<const char*>(P.grad_out) + t * grow_bytes_ld;
 #pragma unroll
-      for (int k = 0; k < V; ++k) {
-        if (!ok[k]) {
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) gf[k][e] = 0.f;
-          continue;
-        }
-        if (P.gout_bf16) {
-          if constexpr (VEC == 8) {
-            const u32x4 t = ldg_global<u32x4>(grow + (int64_t)chunk[k] * 16);
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              gf[k][2 * w] = bf_lo(t[w]);
-              gf[k][2 * w + 1] = bf_hi(t[w]);
-            }
-          } else {
-            const u32x2 t = ldg<u32x2>(grow + (int64_t)chunk[k] * 8);
-            gf[k][0] = bf_lo(t[0]);
-            gf[k][1] = bf_hi(t[0]);
-            gf[k][2] = bf_lo(t[1]);
-            gf[k][3] = bf_hi(t[1]);
-          }
-        } else {
-#pragma unroll
-          for (int h = 0; h < VEC / 4; ++h) {
-            const u32x4 t = ldg_global<u32x4>(grow + ((int64_t)chunk[k] * VEC + 4 * h) * 4);
-#pragma unroll
-            for (int w = 0; w < 4; ++w) gf[k][4 * h + w] = as_f32(t[w]);
-          }
-        }
-      }
+    for (int k = 0; k < V; ++k) {
+      if (ok[k]) g[k].load(grow, chunk[k]);
+      else g[k].zero();
     }
+  };
 
+  int ph = 0;
+  int64_t tok = blockIdx.x;
+  if (tok < P.n_tokens) load_row(tok);
+  for (; tok < P.n_tokens; tok += gridDim.x) {
     // ---- sum(x^2), x.qw, x.G per source ----
     float part[NV];
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-      float ss = 0.f, dt = 0.f, ag = 0.f;
+    for (int j = 0; j < NV; ++j) part[j] = 0.f;
 #pragma unroll
-      for (int k = 0; k < V; ++k) {
+    for (int k = 0; k < V; ++k) {
+      float q[VEC];
+      qw_chunk(k, q);
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
           const float v = C::elem(x[s][k], e);
-          ss = __builtin_fmaf(v, v, ss);
-          dt = __builtin_fmaf(v, qwf[k][e], dt);
-          ag = __builtin_fmaf(v, gf[k][e], ag);
+          part[s] = __builtin_fmaf(v, v, part[s]);
+          part[S + s] = __builtin_fmaf(v, q[e], part[S + s]);
+          part[2 * S + s] = __builtin_fmaf(v, g[k].elem(e), part[2 * S + s]);
         }
       }
-      part[s] = ss;
-      part[S + s] = dt;
-      part[2 * S + s] = ag;
     }
 #pragma unroll
     for (int j = 0; j < NV; ++j) part[j] = wave_sum_to_lane63(part[j]);
@@ -1139,8 +1192,8 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
       wgt[s] *= rsum;
       go = __builtin_fmaf(wgt[s], tot[2 * S + s], go);
     }
-    // The coefficients are the same in every lane: keep them in SGPRs.
     const float glse = P.grad_lse != nullptr ? P.grad_lse[tok] : 0.f;
+    // The coefficients are the same in every lane: keep them in SGPRs.
     float c1[S], c2[S];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -1151,24 +1204,43 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
       wgt[s] = uniform_f32(wgt[s]);
     }
 
+    // ---- keep this row, start loading the next one ----
+    u32x4 xc[S][V];
+    GC gc[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) xc[s][k] = x[s][k];
+      gc[k] = g[k];
+    }
+    const int64_t next = tok + gridDim.x;
+    if (PF && next < P.n_tokens) load_row(next);
+
     // ---- write the source gradients, accumulate the query gradient ----
     // The packed rows are re-expanded here rather than kept as fp32 from the
     // first pass (that would double the register footprint of the sources).
 #pragma unroll
     for (int s = 0; s < S; ++s) {
 #pragma unroll
-      for (int k = 0; k < V; ++k) asm volatile("" : "+v"(x[s][k]));
-      char* drow = reinterpret_cast<char*>(P.dsrc[s]) + tok * P.dsrc_ld * C::BYTES;
-      const __amdgpu_buffer_rsrc_t drsrc = row_rsrc(drow, (uint32_t)(P.d * C::BYTES));
+      for (int k = 0; k < V; ++k) asm volatile("" : "+v"(xc[s][k]));
+    }
 #pragma unroll
-      for (int k = 0; k < V; ++k) {
-        if (!ok[k]) continue;
+    for (int k = 0; k < V; ++k) {
+      if (!ok[k]) continue;
+      float q[VEC], acc[VEC];
+      qw_chunk(k, q);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        char* drow = reinterpret_cast<char*>(P.dsrc[s]) + tok * P.dsrc_ld * C::BYTES;
+        const __amdgpu_buffer_rsrc_t drsrc = row_rsrc(drow, (uint32_t)(P.d * C::BYTES));
         float dx[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          const float v = C::elem(x[s][k], e);
-          dx[e] = __builtin_fmaf(c2[s], v, __builtin_fmaf(c1[s], qwf[k][e], wgt[s] * gf[k][e]));
-          dqw[k][e] = __builtin_fmaf(c1[s], v, dqw[k][e]);
+          const float v = C::elem(xc[s][k], e);
+          dx[e] = __builtin_fmaf(c2[s], v, __builtin_fmaf(c1[s], q[e], wgt[s] * gc[k].elem(e)));
+          acc[e] = __builtin_fmaf(c1[s], v, acc[e]);
         }
         if constexpr (BF16) {
           st_row(drsrc, (uint32_t)chunk[k] * 16,
@@ -1178,26 +1250,72 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
           st_row(drsrc, (uint32_t)chunk[k] * 16, u32x4{as_u32(dx[0]), as_u32(dx[1]), as_u32(dx[2]), as_u32(dx[3])});
         }
       }
+      if constexpr (DQW_LDS) {
+#pragma unroll
+        for (int h = 0; h < VEC / 4; ++h) {
+          float4 t = s_dqw[chunk[k] * (VEC / 4) + h];
+          t.x += acc[4 * h];
+          t.y += acc[4 * h + 1];
+          t.z += acc[4 * h + 2];
+          t.w += acc[4 * h + 3];
+          s_dqw[chunk[k] * (VEC / 4) + h] = t;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) dqw_reg[DQW_LDS ? 0 : k][e] += acc[e];
+      }
     }
+    if (!PF && next < P.n_tokens) load_row(next);
   }
 
   // ---- this workgroup's query-gradient partial ----
-  float* prow = P.dqw_part + (int64_t)blockIdx.x * P.d;
+  float4* prow = reinterpret_cast<float4*>(P.dqw_part + (int64_t)blockIdx.x * P.d);
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     if (!ok[k]) continue;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) prow[(int64_t)chunk[k] * VEC + e] = dqw[k][e];
+    for (int h = 0; h < VEC / 4; ++h) {
+      if constexpr (DQW_LDS) {
+        prow[chunk[k] * (VEC / 4) + h] = s_dqw[chunk[k] * (VEC / 4) + h];
+      } else {
+        const float* a = dqw_reg[DQW_LDS ? 0 : k];
+        prow[chunk[k] * (VEC / 4) + h] = make_float4(a[4 * h], a[4 * h + 1], a[4 * h + 2], a[4 * h + 3]);
+      }
+    }
   }
 }
 
-// Sum the per-workgroup partials of dqw column by column (fixed order, so the
-// result is deterministic) and apply the fold qw = query * gain backwards.
+
+// Stage 1 of the query-gradient reduction: workgroup (x, y) sums partial
+// rows [64y, 64y+64) of columns [64x, 64x+64) in a fixed order (four waves of
+// 16 rows, then the four wave sums in order) and stores the sum in row 64y,
+// which no other workgroup reads or writes.
+__device__ __forceinline__ void reduce_dqw_stage_body(const attnres_reduce_params& P) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63;
+  const int slice = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
+  const int row0 = blockIdx.y * 64;
+  float acc = 0.f;
+  if (col < P.d) {
+    const int r0 = row0 + slice * 16;
+    const int r1 = r0 + 16 < P.nparts ? r0 + 16 : P.nparts;
+#pragma unroll 16
+    for (int r = r0; r < r1; ++r) acc += P.part[(int64_t)r * P.d + col];
+  }
+  red[slice][lane] = acc;
+  __syncthreads();
+  if (slice == 0 && col < P.d) P.part[(int64_t)row0 * P.d + col] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+}
+
+// Final stage: sum the partial rows 0, part_step, 2*part_step, ... column by
+// column (fixed order, so the result is deterministic) and apply the fold
+// qw = query * gain backwards.
 __device__ __forceinline__ void reduce_dqw_body(const attnres_reduce_params& P) {
   const int col = blockIdx.x * blockDim.x + threadIdx.x;
   if (col >= P.d) return;
   float acc = 0.f;
-  for (int p = 0; p < P.nparts; ++p) acc += P.part[(int64_t)p * P.d + col];
+  for (int p = 0; p < P.nparts; p += P.part_step) acc += P.part[(int64_t)p * P.d + col];
   float q, g = 1.f;
   if (P.param_bf16) {
     q = bf_lo(reinterpret_cast<const uint16_t*>(P.query)[col]);
@@ -1329,17 +1447,28 @@ STREAM_TYPES(7)
 STREAM_TYPES(8)
 #endif
 
-// Backward: attnres_route_bwd_<in>_s<S>_v<V>; column reduce: attnres_reduce_dqw.
-#define BWD_ONE(INNAME, BF, S, V)                                                                      \
-  extern "C" __global__ void __launch_bounds__(512) attnres_route_bwd_##INNAME##_s##S##_v##V(         \
-      attnres_route_bwd_params P) {                                                                    \
-    route_bwd_body<S, V, BF>(P);                                                                       \
+// Backward: attnres_route_bwd_<in>_g<grad_out>_s<S>_v<V>; column reduce:
+// attnres_reduce_dqw_stage + attnres_reduce_dqw.
+// Waves per SIMD the backward kernels are compiled for: 4 (<= 128 VGPRs) keeps
+// two workgroups of up to 8 waves (rows up to 4096 bf16 / 2048 fp32 elements)
+// resident per CU for S <= 9; S = 9 bf16 spills a few dwords under that cap.
+#ifndef ATTNRES_BWD_CAP_MAX_S
+#define ATTNRES_BWD_CAP_MAX_S 9
+#endif
+#define BWD_WAVES_PER_EU(S, V) ((V) == 1 && (S) <= ATTNRES_BWD_CAP_MAX_S ? 4 : 1)
+#define BWD_ONE(INNAME, BF, GNAME, GBF, S, V)                                                          \
+  extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(BWD_WAVES_PER_EU(S, V)))) \
+  attnres_route_bwd_##INNAME##_g##GNAME##_s##S##_v##V(attnres_route_bwd_params P) {                    \
+    route_bwd_body<S, V, BF, GBF>(P);                                                                  \
   }
-#define BWD_S(S)            \
-  BWD_ONE(bf, true, S, 1)   \
-  BWD_ONE(bf, true, S, 2)   \
-  BWD_ONE(f32, false, S, 1) \
-  BWD_ONE(f32, false, S, 2)
+#define BWD_TYPES(S, V)                 \
+  BWD_ONE(bf, true, bf, true, S, V)     \
+  BWD_ONE(bf, true, f32, false, S, V)   \
+  BWD_ONE(f32, false, f32, false, S, V) \
+  BWD_ONE(f32, false, bf, true, S, V)
+#define BWD_S(S)    \
+  BWD_TYPES(S, 1) \
+  BWD_TYPES(S, 2)
 
 #if ATTNRES_PART == 4 || defined(ATTNRES_ALL_PARTS)
 BWD_S(1)
@@ -1350,6 +1479,9 @@ BWD_S(5)
 BWD_S(6)
 BWD_S(7)
 BWD_S(8)
+extern "C" __global__ void __launch_bounds__(256) attnres_reduce_dqw_stage(attnres_reduce_params P) {
+  reduce_dqw_stage_body(P);
+}
 extern "C" __global__ void __launch_bounds__(256) attnres_reduce_dqw(attnres_reduce_params P) { reduce_dqw_body(P); }
 #endif
 #if ATTNRES_PART == 5 || defined(ATTNRES_ALL_PARTS)

@@ -89,12 +89,13 @@ typedef struct attnres_route_bwd_params {
 
 /* Column reduction of the dqw partials into the parameter gradients. */
 typedef struct attnres_reduce_params {
-  const float* part;  /* (nparts, d) */
+  float* part;        /* (nparts, d); stage 1 overwrites rows 0, 64, 128, ... */
   const void* query;  /* (d,) param dtype */
   const void* gain;   /* (d,) param dtype, or NULL */
   void* dquery;       /* (d,) param dtype: dqw * gain (dqw when gain is NULL) */
   void* dgain;        /* (d,) param dtype: dqw * query, or NULL */
-  int32_t nparts;
+  int32_t nparts;     /* rows of `part` written by the backward kernel */
+  int32_t part_step;  /* final stage sums rows 0, part_step, 2*part_step, ... */
   int32_t d;
   int32_t param_bf16;
 } attnres_reduce_params;
