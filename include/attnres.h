@@ -160,9 +160,10 @@ int attnres_block_step(void* arena, int num_slots, int64_t slot_stride, int n_co
                        void* stream);
 
 /*
- * Bytes of device workspace attnres_route_bwd needs for num_tokens rows of
- * `hidden` on the current device (per-workgroup fp32 partials of the query
- * gradient).  An upper bound for every num_sources and dtype.
+ * Bytes of device workspace attnres_route_bwd and attnres_merge_bwd need for
+ * num_tokens rows of `hidden` on the current device (per-workgroup fp32
+ * partials of the query gradient).  An upper bound for every num_sources and
+ * dtype.
  */
 int attnres_route_bwd_workspace_size(int64_t num_tokens, int hidden, int64_t* bytes);
 
@@ -197,6 +198,23 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
                       const void* grad_out, int grad_out_dtype, int64_t grad_out_ld, const float* grad_lse,
                       void* const* grad_sources, int64_t grad_ld, void* workspace, int64_t workspace_bytes,
                       void* grad_query, void* grad_gain, void* stream);
+
+/*
+ * Backward of attnres_merge_fwd: given dL/dout (num_tokens, hidden) in
+ * inter_dtype, writes dL/dpartial (partial_dtype), dL/dinter (inter_dtype),
+ * dL/dinter_lse ((num_tokens,) fp32, or NULL to skip) and, when grad_query is
+ * not NULL, dL/dquery ((hidden,) param_dtype, summed over tokens in a fixed
+ * order).  The forward's logit and inv_rms are recomputed.  Arguments as in
+ * attnres_merge_fwd; rows contiguous; workspace as for attnres_route_bwd.
+ *
+ * Replaces the Triton phase-2 backward
+ * (src/model/flash_attn_res/ops/phase_2.py:74-255,
+ * kernels/phase_2.py:60-230), whose query gradient is an fp32 atomic sum.
+ */
+int attnres_merge_bwd(const void* partial, int64_t num_tokens, int hidden, int partial_dtype, const void* query,
+                      int param_dtype, const void* inter, int inter_dtype, const float* inter_lse, float eps,
+                      const void* grad_out, void* grad_partial, void* grad_inter, float* grad_inter_lse,
+                      void* workspace, int64_t workspace_bytes, void* grad_query, void* stream);
 
 #ifdef __cplusplus
 }

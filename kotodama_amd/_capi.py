@@ -52,6 +52,7 @@ EXPORTS = (
     "attnres_block_step",
     "attnres_route_bwd_workspace_size",
     "attnres_route_bwd",
+    "attnres_merge_bwd",
 )
 
 _c_vp = ctypes.c_void_p
@@ -162,6 +163,29 @@ _SIGNATURES = {
         ],
         _c_int,
     ),
+    "attnres_merge_bwd": (
+        [
+            _c_vp,  # partial
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_int,  # partial_dtype
+            _c_vp,  # query
+            _c_int,  # param_dtype
+            _c_vp,  # inter
+            _c_int,  # inter_dtype
+            _c_vp,  # inter_lse
+            _c_float,  # eps
+            _c_vp,  # grad_out
+            _c_vp,  # grad_partial
+            _c_vp,  # grad_inter
+            _c_vp,  # grad_inter_lse
+            _c_vp,  # workspace
+            _c_i64,  # workspace_bytes
+            _c_vp,  # grad_query
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
 }
 
 _lock = threading.Lock()
@@ -232,6 +256,10 @@ def route_bwd_workspace_size(num_tokens: int, hidden: int) -> int:
 
 def route_bwd(*args) -> None:
     check("attnres_route_bwd", lib().attnres_route_bwd(*args))
+
+
+def merge_bwd(*args) -> None:
+    check("attnres_merge_bwd", lib().attnres_merge_bwd(*args))
 
 
 def set_kernel_policy(policy: int) -> int:

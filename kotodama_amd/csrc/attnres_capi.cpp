@@ -82,6 +82,9 @@ struct DeviceState {
   int bwd_bpc_block[kBwdFuncs] = {};
   hipFunction_t reduce = nullptr;
   hipFunction_t reduce_stage = nullptr;
+  hipFunction_t merge_bwd[kMergeFuncs] = {};
+  int merge_bwd_bpc[kMergeFuncs] = {};
+  int merge_bwd_bpc_block[kMergeFuncs] = {};
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -240,6 +243,27 @@ int get_bwd(DeviceState& st, bool bf, bool gbf, int s, int v, int block, size_t 
   }
   *f = st.bwd[idx];
   *bpc = st.bwd_bpc[idx];
+  return ATTNRES_OK;
+}
+
+int get_merge_bwd(DeviceState& st, bool pbf, bool ibf, int v, int block, hipFunction_t* f, int* bpc) {
+  const int idx = ((pbf ? 0 : 2) + (ibf ? 0 : 1)) * 2 + (v - 1);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!st.merge_bwd[idx]) {
+    char name[96];
+    snprintf(name, sizeof(name), "attnres_merge_bwd_%s_%s_v%d", pbf ? "bf" : "f32", ibf ? "bf" : "f32", v);
+    int rc = find_function(st, kReducePart, name, &st.merge_bwd[idx]);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  if (st.merge_bwd_bpc_block[idx] != block) {
+    int nb = 0;
+    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.merge_bwd[idx], block, 0);
+    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    st.merge_bwd_bpc[idx] = nb > 0 ? nb : 1;
+    st.merge_bwd_bpc_block[idx] = block;
+  }
+  *f = st.merge_bwd[idx];
+  *bpc = st.merge_bwd_bpc[idx];
   return ATTNRES_OK;
 }
 
@@ -454,6 +478,30 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
   return launch(f, grid_for(work_units, st->num_cus, bpc), block, P, stream);
+}
+
+// Query/gain gradients from `nparts` per-workgroup partial rows in
+// `workspace`: summed in 64-row blocks (stage 1, in place), then the block
+// sums (final stage); a fixed order, so the result is deterministic.
+int reduce_launch(hipFunction_t fs, hipFunction_t fr, void* workspace, int nparts, int hidden, const void* query,
+                  const void* gain, int param_dtype, void* grad_query, void* grad_gain, void* stream) {
+  attnres_reduce_params R;
+  std::memset(&R, 0, sizeof(R));
+  R.part = static_cast<float*>(workspace);
+  R.query = query;
+  R.gain = gain;
+  R.dquery = grad_query;
+  R.dgain = grad_gain;
+  R.nparts = nparts;
+  R.part_step = 1;
+  R.d = hidden;
+  R.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
+  if (nparts > 64) {
+    int rc = launch(fs, (hidden + 63) / 64, 256, R, stream, (nparts + 63) / 64);
+    if (rc != ATTNRES_OK) return rc;
+    R.part_step = 64;
+  }
+  return launch(fr, (hidden + 255) / 256, 256, R, stream);
 }
 
 }  // namespace
@@ -692,25 +740,79 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   rc = launch(f, (int)grid, block, P, stream, 1, lds);
   if (rc != ATTNRES_OK || fr == nullptr) return rc;
 
-  // Query/gain gradients: the grid's partial rows are summed in 64-row blocks
-  // (stage 1, in place), then the block sums (final stage); fixed order.
-  attnres_reduce_params R;
-  std::memset(&R, 0, sizeof(R));
-  R.part = static_cast<float*>(workspace);
-  R.query = query;
-  R.gain = gain;
-  R.dquery = grad_query;
-  R.dgain = grad_gain;
-  R.nparts = (int)grid;
-  R.part_step = 1;
-  R.d = hidden;
-  R.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
-  if (grid > 64) {
-    rc = launch(fs, (hidden + 63) / 64, 256, R, stream, (int)((grid + 63) / 64));
+  return reduce_launch(fs, fr, workspace, (int)grid, hidden, query, gain, param_dtype, grad_query, grad_gain, stream);
+}
+
+int attnres_merge_bwd(const void* partial, int64_t num_tokens, int hidden, int partial_dtype, const void* query,
+                      int param_dtype, const void* inter, int inter_dtype, const float* inter_lse, float eps,
+                      const void* grad_out, void* grad_partial, void* grad_inter, float* grad_inter_lse,
+                      void* workspace, int64_t workspace_bytes, void* grad_query, void* stream) {
+  if (partial == nullptr || query == nullptr || inter == nullptr || inter_lse == nullptr || grad_out == nullptr ||
+      grad_partial == nullptr || grad_inter == nullptr)
+    return fail(ATTNRES_ERR_ARG, "merge backward: partial, query, inter, inter_lse, grad_out, grad_partial and "
+                                 "grad_inter are required");
+  if (num_tokens < 0) return fail(ATTNRES_ERR_ARG, "num_tokens=%lld < 0", (long long)num_tokens);
+  if (hidden <= 0) return fail(ATTNRES_ERR_ARG, "hidden=%d <= 0", hidden);
+  if (!valid_dtype(partial_dtype) || !valid_dtype(param_dtype) || !valid_dtype(inter_dtype))
+    return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (!std::isfinite(eps)) return fail(ATTNRES_ERR_ARG, "eps is not finite");
+  const bool pbf = partial_dtype == ATTNRES_DTYPE_BF16;
+  const bool ibf = inter_dtype == ATTNRES_DTYPE_BF16;
+  const int vec = pbf ? 8 : 4;
+  if (hidden % vec != 0)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d is not a multiple of %d (16-byte chunks)", hidden, vec);
+  const int nchunk = hidden / vec;
+  if (round64((nchunk + 1) / 2) > kMaxThreads)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d exceeds the largest supported row", hidden);
+  const int ialign = (vec * esize(inter_dtype)) >= 16 ? 16 : vec * esize(inter_dtype);
+  if (!aligned16(partial) || !aligned16(grad_partial) || ((uintptr_t)inter % ialign) != 0 ||
+      ((uintptr_t)grad_out % ialign) != 0 || ((uintptr_t)grad_inter % ialign) != 0 ||
+      ((int64_t)hidden * esize(inter_dtype)) % ialign != 0)
+    return fail(ATTNRES_ERR_ALIGN, "merge backward rows not aligned");
+  if (num_tokens == 0) return ATTNRES_OK;  // no tokens: grad_query is not written
+
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  const int v = round64(nchunk) <= kMaxThreads ? 1 : 2;
+  const int block = v == 1 ? round64(nchunk) : round64((nchunk + 1) / 2);
+  hipFunction_t f = nullptr;
+  int bpc = 1;
+  rc = get_merge_bwd(*st, pbf, ibf, v, block, &f, &bpc);
+  if (rc != ATTNRES_OK) return rc;
+  int64_t grid = (int64_t)st->num_cus * (bpc < kBwdMaxPerCu ? bpc : kBwdMaxPerCu);
+  if (grid > num_tokens) grid = num_tokens;
+  const int64_t need = grid * (int64_t)hidden * (int64_t)sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(ATTNRES_ERR_ARG, "workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
+                (long long)need);
+  if (!aligned16(workspace)) return fail(ATTNRES_ERR_ALIGN, "workspace not 16-byte aligned");
+  hipFunction_t fr = nullptr, fs = nullptr;
+  if (grad_query != nullptr) {
+    rc = get_reduce(*st, &fs, &fr);
     if (rc != ATTNRES_OK) return rc;
-    R.part_step = 64;
   }
-  return launch(fr, (hidden + 255) / 256, 256, R, stream);
+
+  attnres_merge_bwd_params P;
+  std::memset(&P, 0, sizeof(P));
+  P.partial = partial;
+  P.query = query;
+  P.inter = inter;
+  P.inter_lse = inter_lse;
+  P.grad_out = grad_out;
+  P.grad_partial = grad_partial;
+  P.grad_inter = grad_inter;
+  P.grad_lse = grad_inter_lse;
+  P.dq_part = static_cast<float*>(workspace);
+  P.n_tokens = num_tokens;
+  P.d = hidden;
+  P.nchunk = nchunk;
+  P.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
+  P.eps = eps;
+  P.inv_d = 1.0f / (float)hidden;
+  rc = launch(f, (int)grid, block, P, stream);
+  if (rc != ATTNRES_OK || fr == nullptr) return rc;
+  return reduce_launch(fs, fr, workspace, (int)grid, hidden, query, nullptr, param_dtype, grad_query, nullptr, stream);
 }
 
 }  // extern "C"

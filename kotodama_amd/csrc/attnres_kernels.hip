@@ -1286,6 +1286,176 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
 }
 
 
+// ------------------------------------------------ merge backward body --
+
+// VEC consecutive elements of a bf16 or fp32 row as fp32 (chunk = VEC elements).
+template <bool BF, int VEC>
+__device__ __forceinline__ void load_f32_chunk(const char* row, int chunk, float (&v)[VEC]) {
+  if constexpr (BF) {
+    if constexpr (VEC == 8) {
+      const u32x4 t = ldg_global<u32x4>(row + (int64_t)chunk * 16);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        v[2 * w] = bf_lo(t[w]);
+        v[2 * w + 1] = bf_hi(t[w]);
+      }
+    } else {
+      const u32x2 t = ldg_global<u32x2>(row + (int64_t)chunk * 8);
+      v[0] = bf_lo(t[0]);
+      v[1] = bf_hi(t[0]);
+      v[2] = bf_lo(t[1]);
+      v[3] = bf_hi(t[1]);
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < VEC / 4; ++h) {
+      const u32x4 t = ldg_global<u32x4>(row + ((int64_t)chunk * VEC + 4 * h) * 4);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v[4 * h + w] = as_f32(t[w]);
+    }
+  }
+}
+
+// Store VEC fp32 values as one chunk of a bf16 or fp32 row.
+template <bool BF, int VEC>
+__device__ __forceinline__ void store_f32_chunk(__amdgpu_buffer_rsrc_t r, int chunk, const float (&o)[VEC]) {
+  if constexpr (BF) {
+    if constexpr (VEC == 8) {
+      st_row(r, (uint32_t)chunk * 16,
+             u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])});
+    } else {
+      st_row(r, (uint32_t)chunk * 8, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < VEC / 4; ++h)
+      st_row(r, (uint32_t)(chunk * VEC + 4 * h) * 4,
+             u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]), as_u32(o[4 * h + 2]), as_u32(o[4 * h + 3])});
+  }
+}
+
+// Backward of the phase-2 merge out = inter + pi (p - inter),
+// pi = sigmoid(logit - lse), logit = (p.q) r, r = rsqrt(mean(p^2) + eps).
+// With G = dL/dout, a = G.(p - inter) and gl = pi (1 - pi) a = dL/dlogit:
+//   dinter = (1 - pi) G,   dlse = -gl,
+//   dp = pi G + gl r q - gl logit r^2 / D p,   dq = sum over rows of gl r p.
+// One workgroup per row as merge_body; the query gradient is accumulated in
+// registers and written as this workgroup's partial (reduced by
+// attnres_reduce_dqw_stage / attnres_reduce_dqw).
+template <int V, bool PBF16, bool IBF16>
+__device__ __forceinline__ void merge_bwd_body(const attnres_merge_bwd_params& P) {
+  using C = Chunk<PBF16>;
+  constexpr int VEC = C::VEC;
+  __shared__ float red[2][ATTNRES_KMAX_WAVES][4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = (blockDim.x + 63) >> 6;
+  constexpr int IB = IBF16 ? 2 : 4;
+
+  int chunk[V];
+  bool ok[V];
+  float qw[V][VEC];
+  float dqa[V][VEC];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    chunk[k] = tid + k * (int)blockDim.x;
+    ok[k] = chunk[k] < P.nchunk;
+    if (ok[k]) {
+      load_param<VEC>(P.query, (int64_t)chunk[k] * VEC, P.param_bf16, qw[k]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) qw[k][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dqa[k][e] = 0.f;
+  }
+
+  int ph = 0;
+  for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
+    const char* prow = reinterpret_cast<const char*>(P.partial) + tok * (int64_t)P.d * C::BYTES;
+    const char* irow = reinterpret_cast<const char*>(P.inter) + tok * (int64_t)P.d * IB;
+    const char* grow = reinterpret_cast<const char*>(P.grad_out) + tok * (int64_t)P.d * IB;
+    u32x4 p[V];
+    float iv[V][VEC], gv[V][VEC];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      if (ok[k]) {
+        p[k] = ldg_global<u32x4>(prow + (int64_t)chunk[k] * 16);
+        load_f32_chunk<IBF16, VEC>(irow, chunk[k], iv[k]);
+        load_f32_chunk<IBF16, VEC>(grow, chunk[k], gv[k]);
+      } else {
+        p[k] = u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) iv[k][e] = gv[k][e] = 0.f;
+      }
+    }
+
+    float ss = 0.f, dt = 0.f, ga = 0.f;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float v = C::elem(p[k], e);
+        ss = __builtin_fmaf(v, v, ss);
+        dt = __builtin_fmaf(v, qw[k][e], dt);
+        ga = __builtin_fmaf(gv[k][e], v - iv[k][e], ga);
+      }
+    }
+    ss = wave_sum_to_lane63(ss);
+    dt = wave_sum_to_lane63(dt);
+    ga = wave_sum_to_lane63(ga);
+    if (lane == 63) {
+      red[ph][wave][0] = ss;
+      red[ph][wave][1] = dt;
+      red[ph][wave][2] = ga;
+    }
+    __syncthreads();
+    float tss = 0.f, tdt = 0.f, tga = 0.f;
+    for (int w = 0; w < nwaves; ++w) {
+      tss += red[ph][w][0];
+      tdt += red[ph][w][1];
+      tga += red[ph][w][2];
+    }
+    ph ^= 1;
+    const float r = __builtin_amdgcn_rsqf(tss * P.inv_d + P.eps);
+    const float logit = tdt * r;
+    const float pi = 1.0f / (1.0f + __expf(-(logit - P.inter_lse[tok])));
+    const float gl = pi * (1.0f - pi) * tga;
+    if (tid == 0 && P.grad_lse) P.grad_lse[tok] = -gl;
+    const float cq = uniform_f32(gl * r);
+    const float cp = uniform_f32(-gl * logit * r * r * P.inv_d);
+    const float pu = uniform_f32(pi);
+
+    char* gprow = reinterpret_cast<char*>(P.grad_partial) + tok * (int64_t)P.d * C::BYTES;
+    char* girow = reinterpret_cast<char*>(P.grad_inter) + tok * (int64_t)P.d * IB;
+    const __amdgpu_buffer_rsrc_t prs = row_rsrc(gprow, (uint32_t)(P.d * C::BYTES));
+    const __amdgpu_buffer_rsrc_t irs = row_rsrc(girow, (uint32_t)(P.d * IB));
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      if (!ok[k]) continue;
+      float dp[VEC], di[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float v = C::elem(p[k], e);
+        dp[e] = __builtin_fmaf(cp, v, __builtin_fmaf(cq, qw[k][e], pu * gv[k][e]));
+        di[e] = gv[k][e] - pu * gv[k][e];
+        dqa[k][e] = __builtin_fmaf(cq, v, dqa[k][e]);
+      }
+      store_f32_chunk<PBF16, VEC>(prs, chunk[k], dp);
+      store_f32_chunk<IBF16, VEC>(irs, chunk[k], di);
+    }
+  }
+
+  float* qrow = P.dq_part + (int64_t)blockIdx.x * P.d;
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    if (!ok[k]) continue;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) qrow[(int64_t)chunk[k] * VEC + e] = dqa[k][e];
+  }
+}
+
 // Stage 1 of the query-gradient reduction: workgroup (x, y) sums partial
 // rows [64y, 64y+64) of columns [64x, 64x+64) in a fixed order (four waves of
 // 16 rows, then the four wave sums in order) and stores the sum in row 64y,
@@ -1479,6 +1649,19 @@ BWD_S(5)
 BWD_S(6)
 BWD_S(7)
 BWD_S(8)
+// Merge backward: attnres_merge_bwd_<partial>_<inter>_v<V>.
+#define MERGE_BWD_ONE(PN, PB, IN, IB, V)                                                             \
+  extern "C" __global__ void __launch_bounds__(512) attnres_merge_bwd_##PN##_##IN##_v##V(             \
+      attnres_merge_bwd_params P) {                                                                  \
+    merge_bwd_body<V, PB, IB>(P);                                                                    \
+  }
+#define MERGE_BWD_V(V)                   \
+  MERGE_BWD_ONE(bf, true, bf, true, V)   \
+  MERGE_BWD_ONE(bf, true, f32, false, V) \
+  MERGE_BWD_ONE(f32, false, bf, true, V) \
+  MERGE_BWD_ONE(f32, false, f32, false, V)
+MERGE_BWD_V(1)
+MERGE_BWD_V(2)
 extern "C" __global__ void __launch_bounds__(256) attnres_reduce_dqw_stage(attnres_reduce_params P) {
   reduce_dqw_stage_body(P);
 }

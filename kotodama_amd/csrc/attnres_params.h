@@ -125,4 +125,23 @@ typedef struct attnres_merge_params {
   float inv_d;
 } attnres_merge_params;
 
+/* Phase-2 merge backward. */
+typedef struct attnres_merge_bwd_params {
+  const void* partial;    /* (n_tokens, d), partial dtype */
+  const void* query;      /* (d,) pre-folded, param dtype */
+  const void* inter;      /* (n_tokens, d), inter dtype */
+  const float* inter_lse; /* (n_tokens,) */
+  const void* grad_out;   /* (n_tokens, d), inter dtype */
+  void* grad_partial;     /* (n_tokens, d), partial dtype */
+  void* grad_inter;       /* (n_tokens, d), inter dtype */
+  float* grad_lse;        /* (n_tokens,) or NULL */
+  float* dq_part;         /* (gridDim.x, d) fp32 */
+  int64_t n_tokens;
+  int32_t d;
+  int32_t nchunk;
+  int32_t param_bf16;
+  float eps;
+  float inv_d;
+} attnres_merge_bwd_params;
+
 #endif /* KOTODAMA_AMD_ATTNRES_PARAMS_H */

@@ -11,9 +11,9 @@ Contract kept from the reference:
 * ``num_active=None`` means every slot is active (ops/phase_1.py:75-76);
   otherwise the first ``num_active`` slots are (a prefix, as the Triton
   kernel's ``source < num_active`` mask at kernels/phase_1.py:31-33);
-* differentiable for one query (the training path, llama.py:635-638), with
+* differentiable (ops/phase_1.py:160-290) in the blocks and the queries, with
   the aux outputs non-differentiable as in the reference's backward
-  (ops/phase_1.py:235-241); a multi-query call needing grad raises.
+  (ops/phase_1.py:235-241).
 """
 
 from __future__ import annotations
@@ -38,7 +38,6 @@ def phase_1_batched_attention_forward_with_aux(
     Slots at or beyond ``num_active`` carry 0 in the two aux outputs (the
     reference leaves them unwritten).
     """
-    ops.check_differentiable_queries(pseudo_queries, block_representations)
     s_total = block_representations.shape[0]
     out, _, lse, inv_rms, logits = ops.route(
         block_representations, int(num_active), pseudo_queries, None, float(eps), torch.bfloat16, True, True
@@ -57,7 +56,6 @@ def phase_1_batched_attention(
     num_active: Optional[int] = None,
 ) -> tuple[Tensor, Tensor]:
     """(out (Q, B, T, D) bf16, lse (Q, B, T) fp32) — ops/phase_1.py:69-85."""
-    ops.check_differentiable_queries(pseudo_queries, block_representations)
     if num_active is None:
         num_active = block_representations.shape[0]
     out, _, lse, _, _ = ops.route(

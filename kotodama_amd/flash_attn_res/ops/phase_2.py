@@ -9,6 +9,9 @@ routing over committed blocks + partial is
     out   = inter + pi * (p - inter)
 
 (kernels/phase_2.py:40-57).  Output dtype = ``inter``'s (ops/phase_2.py:41-45).
+Differentiable in all four tensor inputs (the phase-2 backward,
+ops/phase_2.py:211-261); the logit and inverse-RMS outputs are not, as in the
+reference.
 """
 
 from __future__ import annotations
@@ -26,7 +29,6 @@ def phase_2_online_softmax_merge_forward_with_aux(
     eps: float,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """(merged (B,T,D), intrablock_logit (B,T), intrablock_inverse_rms_norm (B,T))."""
-    ops.check_forward_only(intrablock_partial_sum, pseudo_query, interblock_normalized_output)
     return ops.merge(intrablock_partial_sum, pseudo_query, interblock_normalized_output, interblock_lse, float(eps))
 
 

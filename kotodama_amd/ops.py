@@ -4,9 +4,8 @@ Each op is a thin shim over the C ABI (``_capi``): it validates tensors,
 allocates outputs on torch's caching allocator, and launches on the current
 HIP stream of the inputs' device.  Fake (meta) implementations give shapes
 for ``torch.compile``.  Inputs must be ROCm device tensors: there is no CPU
-path.  ``route`` and ``route_list`` are differentiable for one query (the
-backward kernels of ``attnres_route_bwd``); ``merge`` and ``block_step`` are
-forward-only and raise if autograd would need them.
+path.  ``route``, ``route_list`` and ``merge`` are differentiable (the backward kernels of ``attnres_route_bwd`` /
+``attnres_merge_bwd``); ``block_step`` is forward-only.
 
 Ops
 ---
@@ -21,13 +20,15 @@ Ops
 ``attnres_hip::block_step(arena, n_committed, commit, delta, query, gain, eps, want_weights)``
     One routing point over a block arena with the partial update fused in
     (the body of ``llama.py:697-715`` / ``742-762``); mutates ``arena``.
-``attnres_hip::route_bwd`` / ``attnres_hip::route_list_bwd``
-    Backward of ``route`` / ``route_list`` for one query: gradients of the
-    sources, the query and the gain from dL/dout and dL/dlse
+``attnres_hip::route_bwd`` / ``attnres_hip::route_list_bwd`` / ``attnres_hip::merge_bwd``
+    Backward of ``route`` / ``route_list``: gradients of the sources, the
+    query (one row per query) and the gain from dL/dout and dL/dlse
     (``ops/phase_1.py:88-284``, ``kernels/phase_1.py:104-280``).  The weights
     and the aux outputs (inv_rms, logits) are non-differentiable outputs, as
     in the reference, whose backward ignores their gradients
-    (``ops/phase_1.py:235-241``).
+    (``ops/phase_1.py:235-241``).  ``merge_bwd`` is the phase-2 backward
+    (``ops/phase_2.py:74-255``); its logit / inv_rms outputs are likewise
+    non-differentiable.
 
 Returned tuples always have the same arity; outputs that were not requested
 are empty tensors.
@@ -328,15 +329,57 @@ def _launch_route_bwd(
     return dq.reshape(query.shape), dg
 
 
-def _bwd_args(query: Tensor, grad_out: Optional[Tensor], grad_lse: Optional[Tensor], n_out_shape, device, dt):
-    if query.dim() == 2 and query.shape[0] != 1:
-        raise NotImplementedError(
-            "attnres_hip: backward is implemented for one query; the batched phase-1 call with "
-            f"{query.shape[0]} queries is forward-only"
-        )
+def _bwd_args(grad_out: Optional[Tensor], n_out_shape, device, dt) -> Tensor:
     if grad_out is None:
         grad_out = torch.zeros(n_out_shape, device=device, dtype=dt)
-    return grad_out, grad_lse
+    return grad_out
+
+
+def _route_bwd_any(
+    srcs: list[Tensor],
+    grads: list[Tensor],
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    grad_out: Tensor,
+    grad_lse: Optional[Tensor],
+) -> tuple[Tensor, Optional[Tensor]]:
+    """Backward over contiguous sources into the preallocated ``grads``.
+
+    One query: one attnres_route_bwd call.  Q > 1 queries (the batched
+    phase-1 call): one call per query on fp32 copies of the sources, the
+    source gradients summed in fp32 and rounded once, the query gradients
+    stacked and the gain gradients summed (ops/phase_1.py:160-170 accumulates
+    the same sum over queries).
+    """
+    device = srcs[0].device
+    d = srcs[0].shape[-1]
+    n = srcs[0].numel() // d
+    if query.dim() == 1 or query.shape[0] == 1:
+        return _launch_route_bwd(
+            [t.data_ptr() for t in srcs], [g.data_ptr() for g in grads], srcs[0].dtype, n, d, device, query, gain,
+            eps, grad_out, grad_lse,
+        )
+    nq = query.shape[0]
+    s32 = [t.float().contiguous() for t in srcs]
+    acc = [torch.zeros(t.shape, device=device, dtype=torch.float32) for t in srcs]
+    tmp = [torch.empty(t.shape, device=device, dtype=torch.float32) for t in srcs]
+    go = grad_out.reshape(nq, n, d)
+    gl = grad_lse.reshape(nq, n) if grad_lse is not None else None
+    dqs, dg = [], None
+    for j in range(nq):
+        dq_j, dg_j = _launch_route_bwd(
+            [t.data_ptr() for t in s32], [t.data_ptr() for t in tmp], torch.float32, n, d, device, query[j], gain,
+            eps, go[j], gl[j] if gl is not None else None,
+        )
+        for a, t in zip(acc, tmp):
+            a.add_(t)
+        dqs.append(dq_j)
+        if dg_j is not None:
+            dg = dg_j.float() if dg is None else dg + dg_j.float()
+    for g, a in zip(grads, acc):
+        g.copy_(a)
+    return torch.stack(dqs, 0), (dg.to(gain.dtype) if dg is not None else None)
 
 
 @torch.library.custom_op("attnres_hip::route_bwd", mutates_args=())
@@ -349,7 +392,7 @@ def route_bwd(
     grad_out: Tensor,
     grad_lse: Optional[Tensor],
 ) -> tuple[Tensor, Tensor, Tensor]:
-    """(grad_buf, grad_query, grad_gain) of ``route`` with one query.
+    """(grad_buf, grad_query, grad_gain) of ``route``.
 
     ``grad_buf`` is zero in slots at or beyond ``num_sources``; ``grad_gain``
     is an empty tensor when ``gain`` is None.  With ``num_sources == 0`` the
@@ -370,12 +413,9 @@ def route_bwd(
         if gain is not None:
             gg = torch.full_like(gain, fill)
         return grad_buf, gq, gg
-    slot = n * d
-    es = buf.element_size()
-    ptrs = [buf.data_ptr() + i * slot * es for i in range(num_sources)]
-    gptrs = [grad_buf.data_ptr() + i * slot * es for i in range(num_sources)]
-    gq, g2 = _launch_route_bwd(ptrs, gptrs, buf.dtype, n, d, device, query, gain, eps, grad_out, grad_lse)
-    return grad_buf, gq, g2 if g2 is not None else gg
+    gq, g2 = _route_bwd_any(list(buf[:num_sources]), list(grad_buf[:num_sources]), query, gain, eps, grad_out,
+                            grad_lse)
+    return grad_buf, gq.reshape(query.shape), g2 if g2 is not None else gg
 
 
 @route_bwd.register_fake
@@ -393,7 +433,7 @@ def route_list_bwd(
     grad_out: Tensor,
     grad_lse: Optional[Tensor],
 ) -> tuple[list[Tensor], Tensor, Tensor]:
-    """(grad_sources, grad_query, grad_gain) of ``route_list`` with one query."""
+    """(grad_sources, grad_query, grad_gain) of ``route_list``."""
     device = _require_device(*sources, query, gain, grad_out, grad_lse)
     ref = sources[0]
     d = ref.shape[-1]
@@ -406,11 +446,8 @@ def route_list_bwd(
         if gain is not None:
             gg = torch.zeros_like(gain)
         return grads, gq, gg
-    gq, g2 = _launch_route_bwd(
-        [t.data_ptr() for t in srcs], [g.data_ptr() for g in grads], ref.dtype, n, d, device, query, gain, eps,
-        grad_out, grad_lse,
-    )
-    return grads, gq, g2 if g2 is not None else gg
+    gq, g2 = _route_bwd_any(srcs, grads, query, gain, eps, grad_out, grad_lse)
+    return grads, gq.reshape(query.shape), g2 if g2 is not None else gg
 
 
 @route_list_bwd.register_fake
@@ -435,7 +472,7 @@ def _route_backward(ctx, g_out, g_w, g_lse, g_inv, g_logits):
     buf, query, gain = ctx.saved_tensors
     if g_out is None and g_lse is None:
         return None, None, None, None, None, None, None, None
-    g_out, g_lse = _bwd_args(query, g_out, g_lse, ctx.out_shape, buf.device, ctx.out_dtype)
+    g_out = _bwd_args(g_out, ctx.out_shape, buf.device, ctx.out_dtype)
     grad_buf, gq, gg = route_bwd(buf, ctx.num_sources, query, gain, ctx.eps, g_out, g_lse)
     need = ctx.needs_input_grad
     return (
@@ -471,7 +508,7 @@ def _route_list_backward(ctx, g_out, g_w, g_lse, g_inv, g_logits):
     query, gain = saved[ctx.num_sources], saved[ctx.num_sources + 1]
     if g_out is None and g_lse is None:
         return None, None, None, None, None, None, None
-    g_out, g_lse = _bwd_args(query, g_out, g_lse, ctx.out_shape, query.device, ctx.out_dtype)
+    g_out = _bwd_args(g_out, ctx.out_shape, query.device, ctx.out_dtype)
     grads, gq, gg = route_list_bwd(sources, query, gain, ctx.eps, g_out, g_lse)
     need = ctx.needs_input_grad
     return (
@@ -537,6 +574,87 @@ def _merge_fake(partial, query, inter, inter_lse, eps):
         partial.new_empty(shp, dtype=torch.float32),
         partial.new_empty(shp, dtype=torch.float32),
     )
+
+
+@torch.library.custom_op("attnres_hip::merge_bwd", mutates_args=())
+def merge_bwd(
+    partial: Tensor, query: Tensor, inter: Tensor, inter_lse: Tensor, eps: float, grad_out: Tensor
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(grad_partial, grad_query, grad_inter, grad_inter_lse) of ``merge``."""
+    device = _require_device(partial, query, inter, inter_lse, grad_out)
+    d = partial.shape[-1]
+    partial = partial.contiguous()
+    inter = inter.contiguous()
+    inter_lse = inter_lse.contiguous()
+    query = query.contiguous()
+    grad_out = grad_out.to(inter.dtype).contiguous()
+    n = partial.numel() // d
+    gp = torch.empty_like(partial)
+    gi = torch.empty_like(inter)
+    gl = torch.empty(partial.shape[:-1], device=device, dtype=torch.float32)
+    gq = torch.zeros_like(query) if n == 0 else torch.empty_like(query)
+    if n == 0:
+        return gp, gq, gi, gl
+    with _DeviceStream(device) as stream:
+        ws = torch.empty(max(1, _capi.route_bwd_workspace_size(n, d) // 4), device=device, dtype=torch.float32)
+        _capi.merge_bwd(
+            partial.data_ptr(),
+            n,
+            d,
+            dtype_code(partial.dtype),
+            query.data_ptr(),
+            dtype_code(query.dtype),
+            inter.data_ptr(),
+            dtype_code(inter.dtype),
+            inter_lse.data_ptr(),
+            float(eps),
+            grad_out.data_ptr(),
+            gp.data_ptr(),
+            gi.data_ptr(),
+            gl.data_ptr(),
+            ws.data_ptr(),
+            ws.numel() * 4,
+            gq.data_ptr(),
+            stream,
+        )
+    return gp, gq, gi, gl
+
+
+@merge_bwd.register_fake
+def _merge_bwd_fake(partial, query, inter, inter_lse, eps, grad_out):
+    return (
+        torch.empty_like(partial),
+        torch.empty_like(query),
+        torch.empty_like(inter),
+        partial.new_empty(partial.shape[:-1], dtype=torch.float32),
+    )
+
+
+def _merge_setup_context(ctx, inputs, output):
+    partial, query, inter, inter_lse, eps = inputs
+    _, logit, inv_rms = output
+    ctx.mark_non_differentiable(logit, inv_rms)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(partial, query, inter, inter_lse)
+    ctx.eps = eps
+
+
+def _merge_backward(ctx, g_out, g_logit, g_inv):
+    if g_out is None:
+        return None, None, None, None, None
+    partial, query, inter, inter_lse = ctx.saved_tensors
+    gp, gq, gi, gl = merge_bwd(partial, query, inter, inter_lse, ctx.eps, g_out)
+    need = ctx.needs_input_grad
+    return (
+        gp if need[0] else None,
+        gq if need[1] else None,
+        gi if need[2] else None,
+        gl if need[3] else None,
+        None,
+    )
+
+
+merge.register_autograd(_merge_backward, setup_context=_merge_setup_context)
 
 
 # ------------------------------------------------------------- block step --
@@ -613,26 +731,14 @@ def check_forward_only(*tensors: Optional[Tensor]) -> None:
     _no_grad_needed(*tensors)
 
 
-def check_differentiable_queries(query: Tensor, *tensors: Optional[Tensor]) -> None:
-    """Raise before the forward if autograd would need a multi-query backward."""
-    if query.dim() == 2 and query.shape[0] > 1:
-        try:
-            _no_grad_needed(query, *tensors)
-        except NotImplementedError:
-            raise NotImplementedError(
-                f"attnres_hip: backward is implemented for one query; a phase-1 call with {query.shape[0]} "
-                "queries is forward-only (run it under torch.no_grad() or detach the inputs)"
-            ) from None
-
-
 __all__ = [
     "route",
     "route_list",
     "route_bwd",
     "route_list_bwd",
     "merge",
+    "merge_bwd",
     "block_step",
     "dtype_code",
     "check_forward_only",
-    "check_differentiable_queries",
 ]

@@ -16,6 +16,7 @@ Everything here is float64 numpy restated from the reference's own Python
 * :func:`route_backward` gradients of out (and lse) w.r.t. the
                          sources and the folded query           kernels/phase_1.py:104-280
 * :func:`merge`          phase-2 online-softmax merge           kernels/phase_2.py:40-57
+* :func:`merge_backward` gradients of the merge                 kernels/phase_2.py:60-230
 * :func:`schedule`       boundary set, masks, active counts      llama.py:545-571
 * :func:`block_forward`  caller order: route -> commit -> add    llama.py:697-715 (742-762)
 * :func:`bf16_round`     round-to-nearest-even to bfloat16       (torch's bf16 cast)
@@ -171,6 +172,34 @@ def merge(partial, q, inter, inter_lse, eps: float) -> dict:
     pi = 1.0 / (1.0 + np.exp(-(logit - lse)))
     out = it + pi[..., None] * (p - it)
     return {"out": out, "logit": logit, "inv_rms": inv}
+
+
+def merge_backward(partial, q, inter, inter_lse, eps: float, grad_out) -> dict:
+    """Gradients of the phase-2 merge (kernels/phase_2.py:60-230).
+
+    With pi = sigmoid(logit - lse), a = G.(p - inter) and gl = pi (1 - pi) a
+    (= dL/dlogit):  dinter = (1 - pi) G;  dlse = -gl;
+    dp = pi G + gl (r q - logit r^2 p / D);  dq = sum over rows of gl r p.
+    Returns dpartial, dinter (N, D), dlse (N,), dq (D,).
+    """
+    p = np.asarray(partial, dtype=np.float64)
+    qv = np.asarray(q, dtype=np.float64)
+    it = np.asarray(inter, dtype=np.float64)
+    lse = np.asarray(inter_lse, dtype=np.float64)
+    g = np.asarray(grad_out, dtype=np.float64)
+    D = p.shape[-1]
+    r = 1.0 / np.sqrt(np.mean(p * p, axis=-1) + eps)
+    logit = (p @ qv) * r
+    pi = 1.0 / (1.0 + np.exp(-(logit - lse)))
+    a = np.sum(g * (p - it), axis=-1)
+    gl = pi * (1.0 - pi) * a
+    dp = pi[..., None] * g + gl[..., None] * (r[..., None] * qv - (logit * r * r / D)[..., None] * p)
+    return {
+        "dpartial": dp,
+        "dinter": (1.0 - pi)[..., None] * g,
+        "dlse": -gl,
+        "dq": np.einsum("n,nd->d", (gl * r).reshape(-1), p.reshape(-1, D)),
+    }
 
 
 # -------------------------------------------------------------- schedule --

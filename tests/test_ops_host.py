@@ -25,10 +25,8 @@ def test_cpu_tensors_raise_no_fallback():
 
 
 def test_forward_only_guards():
-    # the multi-query phase-1 call and the weights/engine paths have no backward
+    # the weights helper and the arena engine have no backward
     buf = torch.randn(3, 1, 4, 64, requires_grad=True)
-    with pytest.raises(NotImplementedError, match="one query"):
-        phase_1_batched_attention_triton_op(buf, torch.zeros(2, 64), 1e-5)
     q = torch.zeros(64, requires_grad=True)
     with pytest.raises(NotImplementedError, match="forward-only"):
         kotodama_amd.route_weights(buf, 3, q, Norm(64))
@@ -57,6 +55,10 @@ def test_fake_kernels_give_reference_shapes():
         assert gb.shape == buf.shape and gq.shape == (128,) and gg.numel() == 0
         gl, gq2, gg2 = torch.ops.attnres_hip.route_list_bwd([buf[0], buf[1]], q[0], q[1], 1e-5, out[0], lse[0])
         assert len(gl) == 2 and gl[0].shape == buf[0].shape and gg2.shape == (128,)
+        gb3, gq3, _ = torch.ops.attnres_hip.route_bwd(buf, 5, q, None, 1e-5, out, lse)
+        assert gq3.shape == (3, 128)
+        gp, gq4, gi, glse = torch.ops.attnres_hip.merge_bwd(buf[0], q[0], out[0], lse[0], 1e-5, out[0])
+        assert gp.shape == buf[0].shape and gi.shape == out[0].shape and glse.shape == lse[0].shape
         arena = torch.empty(9, 4, 1, 128, dtype=torch.bfloat16, device="cuda")
         o, w2, l2 = torch.ops.attnres_hip.block_step(arena, 3, True, arena[0], q[0], None, 1e-5, True)
         assert o.shape == (4, 1, 128) and w2.shape == (5, 4, 1)

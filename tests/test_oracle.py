@@ -268,3 +268,53 @@ def test_backward_lse_term_matches_finite_differences():
     num_dq = np.array([(loss(x, q + h * e) - loss(x, q - h * e)) / (2 * h) for e in np.eye(D)])
     np.testing.assert_allclose(b["dx"], num_dx, rtol=1e-6, atol=1e-8)
     np.testing.assert_allclose(b["dqw"], num_dq, rtol=1e-6, atol=1e-8)
+
+
+def test_merge_backward_matches_finite_differences():
+    rng = np.random.default_rng(63)
+    N, D, eps = 3, 6, 1e-3
+    p = rng.standard_normal((N, D)) * 1.5
+    q = rng.standard_normal(D)
+    it = rng.standard_normal((N, D))
+    lse = rng.standard_normal(N)
+    G = rng.standard_normal((N, D))
+    b = O.merge_backward(p, q, it, lse, eps, G)
+
+    def loss(pp=p, qq=q, ii=it, ll=lse):
+        return float(np.sum(G * O.merge(pp, qq, ii, ll, eps)["out"]))
+
+    h = 1e-6
+
+    def num(x, f):
+        out = np.zeros_like(x)
+        for idx in np.ndindex(*x.shape):
+            xp = x.copy(); xp[idx] += h
+            xm = x.copy(); xm[idx] -= h
+            out[idx] = (f(xp) - f(xm)) / (2 * h)
+        return out
+
+    np.testing.assert_allclose(b["dpartial"], num(p, lambda x: loss(pp=x)), rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(b["dq"], num(q, lambda x: loss(qq=x)), rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(b["dinter"], num(it, lambda x: loss(ii=x)), rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(b["dlse"], num(lse, lambda x: loss(ll=x)), rtol=1e-6, atol=1e-8)
+
+
+def test_merge_backward_equals_routing_backward_over_one_more_source():
+    # merge(p, phase1(C)) == route(C + [p]), so the gradients w.r.t. p and the
+    # query agree with the routing backward's (the sources C enter through inter/lse)
+    rng = np.random.default_rng(64)
+    S, N, D, eps = 3, 4, 16, 1e-5
+    x = rng.standard_normal((S + 1, N, D))
+    q = rng.standard_normal(D) * 0.3
+    G = rng.standard_normal((N, D))
+    ph1 = O.route(x[:S], q, eps)
+    m = O.merge(x[S], q, ph1["out"][0], ph1["lse"][0], eps)
+    full = O.route(x, q, eps)
+    np.testing.assert_allclose(m["out"], full["out"][0], rtol=1e-12, atol=1e-12)
+    mb = O.merge_backward(x[S], q, ph1["out"][0], ph1["lse"][0], eps, G)
+    rb = O.route_backward(x, q, eps, G)
+    np.testing.assert_allclose(mb["dpartial"], rb["dx"][S], rtol=1e-10, atol=1e-12)
+    # chain the merge's inter/lse gradients through phase 1 for the committed sources
+    p1b = O.route_backward(x[:S], q, eps, mb["dinter"], grad_lse=mb["dlse"])
+    np.testing.assert_allclose(p1b["dx"], rb["dx"][:S], rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(p1b["dqw"] + mb["dq"], rb["dqw"], rtol=1e-10, atol=1e-12)
