@@ -10,9 +10,12 @@ Hand-written HIP kernels behind a C ABI (``include/attnres.h``,
   ``phase_2_online_softmax_merge_triton_op``
 * :func:`kotodama_amd.engine.forward_attn_res` / ``forward_attn_res_cached`` —
   the prefill / KV-cache caller loops over a preallocated block arena
+* :mod:`kotodama_amd.checkpoint` — routing weights from trained checkpoints
+  (safe loading only)
 """
 
 from . import ops  # noqa: F401  (registers the attnres_hip ops)
+from .checkpoint import RoutingWeights, load_checkpoint_registry, load_routing_weights
 from .engine import AttnResRouter, BlockArena, forward_attn_res, forward_attn_res_cached
 from .routing import block_attn_res_from_list, route_static, route_weights
 from .schedule import AttnResSchedule
@@ -21,9 +24,12 @@ __all__ = [
     "AttnResRouter",
     "AttnResSchedule",
     "BlockArena",
+    "RoutingWeights",
     "block_attn_res_from_list",
     "forward_attn_res",
     "forward_attn_res_cached",
+    "load_checkpoint_registry",
+    "load_routing_weights",
     "route_static",
     "route_weights",
 ]

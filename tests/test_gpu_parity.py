@@ -411,3 +411,47 @@ def test_decode_step_graph_replays_match_eager(gpu, policy):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(captured, eager), f"replay {rep} differs from eager"
+
+
+# ------------------------------------------------ loaded checkpoint weights --
+
+
+@pytest.mark.parametrize("tokens", [(64, 1), (2, 256)], ids=["decode", "prefill"])
+def test_routing_with_loaded_checkpoint_weights(gpu, tmp_path, tokens):
+    # trained routing weights are peaky (large query norms): save a checkpoint in the
+    # reference's layout, load it through the safe loader, route with it on the GPU
+    from kotodama_amd.checkpoint import load_routing_weights
+
+    L, D, eps = 8, 2048, 1e-5
+    g = torch.Generator().manual_seed(12)
+    sd = {}
+    for i in range(L):
+        for kind in ("attn", "mlp"):
+            sd[f"_orig_mod.layers.{i}.{kind}_res_query"] = (torch.randn(D, generator=g) * 0.3).to(torch.bfloat16)
+            sd[f"_orig_mod.layers.{i}.{kind}_res_norm.weight"] = (1 + 0.2 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    sd["_orig_mod.final_res_query"] = (torch.randn(D, generator=g) * 0.3).to(torch.bfloat16)
+    sd["_orig_mod.final_res_norm.weight"] = torch.ones(D).to(torch.bfloat16)
+    path = tmp_path / "step_00001000.pt"
+    torch.save({"step": 1000, "model": sd}, path)
+    w = load_routing_weights(path, device=gpu)
+    sched = w.schedule(n_blocks=3)
+    router = w.router(sched, eps)
+    B, T = tokens
+    embed = torch.randn((B, T, D), generator=g).to(torch.bfloat16).to(gpu)
+    deltas = [torch.randn((B, T, D), generator=g).to(torch.bfloat16).to(gpu) for _ in range(2 * L)]
+    outs = []
+
+    def sublayer(j, h):
+        outs.append(h.clone())
+        return deltas[j]
+
+    with torch.no_grad():
+        outs.append(router.forward(embed, sublayer))
+    qws = [O.fold_query(np64(w.queries[j]), np64(w.gains[j]), "bf16") for j in range(sched.num_points)]
+    ref = O.block_forward(np64(embed).reshape(-1, D), [np64(x).reshape(-1, D) for x in deltas], qws, eps, L,
+                          sched.boundary_set, dtype="bf16", want_weights=True)
+    # the weights really are peaky: most rows put > 90% on one source somewhere in the forward
+    peak = max(float(np.mean(np.max(wj, axis=0) > 0.9)) for wj in ref["weights"][1:])
+    assert peak > 0.5
+    for j in range(sched.num_points):
+        check_bf16(outs[j].reshape(-1, D), ref["outs"][j], f"point {j}")
