@@ -85,7 +85,7 @@ def kernel_name(s: int, tokens: int, hidden: int, dtype) -> str:
     buf = ctypes.create_string_buffer(128)
     code = ops.dtype_code(dtype)
     _capi.check("attnres_route_kernel_name",
-                _capi.lib().attnres_route_kernel_name(s, tokens, hidden, code, code, 1, 0, buf, len(buf)))
+                _capi.lib().attnres_route_kernel_name(s, tokens, hidden, code, code, code, 1, 0, buf, len(buf)))
     return buf.value.decode()
 
 

@@ -68,11 +68,12 @@ int attnres_set_kernel_policy(int policy);
  * Symbol name of the kernel attnres_route_fwd (fused == 0) or
  * attnres_block_step (fused == 1) launches for these arguments under the
  * current policy, assuming equally spaced sources (a stacked buffer or an
- * arena), for matching profiler output; written NUL-terminated into buf.  Loads the code object on the current device.  No counterpart in the
+ * arena), for matching profiler output; written NUL-terminated into buf.
+ * Loads the code object on the current device.  No counterpart in the
  * reference.
  */
 int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
-                              int num_queries, int fused, char* buf, int buf_len);
+                              int out_dtype, int num_queries, int fused, char* buf, int buf_len);
 
 /*
  * Load the gfx950 code object on the current HIP device.  Optional: the

@@ -59,7 +59,7 @@ constexpr int kRouteFuncs = kTypeCombos * kNumS * 2 * 2;
 constexpr int kMergeFuncs = 4 * 2;
 constexpr int kStreamMaxChunks = 8;  // rows of up to 8 KiB
 constexpr int kStreamWaves = 4;      // waves per workgroup of the streaming kernels
-constexpr int kStreamFuncs = kTypeCombos * kStreamMaxChunks * 2;
+constexpr int kStreamFuncs = kTypeCombos * 2 * kStreamMaxChunks * 2;  // combo x out dtype x KiB x fused
 constexpr int kBwdFuncs = 4 * kNumS * 2;  // (source, grad_out) dtype pairs x S x V
 constexpr int kBwdMaxPerCu = 4;           // workgroups per CU the backward grid may use (workspace bound)
 constexpr size_t kBwdStaticLds = 2 * ATTNRES_KMAX_WAVES * 48 * sizeof(float);  // reduction buffer, S = 16
@@ -157,13 +157,14 @@ int find_function(DeviceState& st, int part, const char* name, hipFunction_t* f)
 
 int part_of_stream(int nch) { return nch <= 4 ? 2 : 1; }
 
-int get_stream(DeviceState& st, int combo, int nch, bool fused, hipFunction_t* f, int* bpc) {
-  const int idx = (combo * kStreamMaxChunks + (nch - 1)) * 2 + (fused ? 1 : 0);
+int get_stream(DeviceState& st, int combo, bool out_bf, int nch, bool fused, hipFunction_t* f, int* bpc) {
+  const int idx = ((combo * 2 + (out_bf ? 0 : 1)) * kStreamMaxChunks + (nch - 1)) * 2 + (fused ? 1 : 0);
   std::lock_guard<std::mutex> lk(g_mu);
   if (!st.stream[idx]) {
     static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
     char name[96];
-    snprintf(name, sizeof(name), "attnres_stream_%s_c%d_%s", combo_names[combo], nch, fused ? "fused" : "plain");
+    snprintf(name, sizeof(name), "attnres_stream_%s_o%s_c%d_%s", combo_names[combo], out_bf ? "bf" : "f32", nch,
+             fused ? "fused" : "plain");
     int rc = find_function(st, part_of_stream(nch), name, &st.stream[idx]);
     if (rc != ATTNRES_OK) return rc;
     int nb = 0;
@@ -362,10 +363,12 @@ RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int sr
   return ch;
 }
 
-void kernel_name_of(const RouteChoice& ch, int num_sources, int num_queries, bool fused, char* buf, size_t n) {
+void kernel_name_of(const RouteChoice& ch, int num_sources, int num_queries, bool fused, bool out_bf, char* buf,
+                    size_t n) {
   static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
   if (ch.stream) {
-    snprintf(buf, n, "attnres_stream_%s_c%d_%s", combo_names[ch.combo], ch.nch, fused ? "fused" : "plain");
+    snprintf(buf, n, "attnres_stream_%s_o%s_c%d_%s", combo_names[ch.combo], out_bf ? "bf" : "f32", ch.nch,
+             fused ? "fused" : "plain");
   } else {
     snprintf(buf, n, "attnres_route_%s_s%d_v%d_%s", combo_names[ch.combo], num_sources, ch.v,
              num_queries > 1 ? "qn" : "q1");
@@ -443,7 +446,7 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   int block = ch.block;
   int64_t work_units = num_tokens;  // rows per workgroup-slot of the grid
   if (ch.stream) {
-    rc = get_stream(*st, ch.combo, ch.nch, mode != ATTNRES_MODE_PLAIN, &f, &bpc);
+    rc = get_stream(*st, ch.combo, out_dtype == ATTNRES_DTYPE_BF16, ch.nch, mode != ATTNRES_MODE_PLAIN, &f, &bpc);
     if (rc != ATTNRES_OK) return rc;
     work_units = (num_tokens + kStreamWaves - 1) / kStreamWaves;
   } else {
@@ -515,9 +518,10 @@ int attnres_max_sources(void) { return ATTNRES_MAX_SOURCES; }
 const char* attnres_last_error(void) { return g_err.c_str(); }
 
 int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
-                              int num_queries, int fused, char* buf, int buf_len) {
+                              int out_dtype, int num_queries, int fused, char* buf, int buf_len) {
   if (buf == nullptr || buf_len < 1) return fail(ATTNRES_ERR_ARG, "no output buffer");
-  if (!valid_dtype(src_dtype) || !valid_dtype(param_dtype)) return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (!valid_dtype(src_dtype) || !valid_dtype(param_dtype) || !valid_dtype(out_dtype))
+    return fail(ATTNRES_ERR_ARG, "unknown dtype code");
   if (num_sources < 0 || num_sources > ATTNRES_MAX_SOURCES || hidden <= 0 || num_queries < 1)
     return fail(ATTNRES_ERR_ARG, "bad shape");
   DeviceState* st = nullptr;
@@ -525,7 +529,7 @@ int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, i
   if (rc != ATTNRES_OK) return rc;
   const RouteChoice ch =
       choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus, true);
-  kernel_name_of(ch, num_sources, num_queries, fused != 0, buf, (size_t)buf_len);
+  kernel_name_of(ch, num_sources, num_queries, fused != 0, out_dtype == ATTNRES_DTYPE_BF16, buf, (size_t)buf_len);
   return ATTNRES_OK;
 }
 

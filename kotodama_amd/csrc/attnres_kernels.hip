@@ -683,7 +683,7 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
 #define ATTNRES_STREAM_SLOTS 2  // row buffers in the per-wave pipeline (2 or 3)
 #endif
 
-template <int NCH, bool BF16, bool QDOT2, bool FUSED>
+template <int NCH, bool BF16, bool QDOT2, bool FUSED, bool OUTBF>
 __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   const int S = P.num_sources;
   using C = Chunk<BF16>;
@@ -778,7 +778,8 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
       asm volatile("; attnres stream slot C");
     }
     if constexpr (FUSED) {
-      if (s == (uint32_t)(S - 1) && mode != ATTNRES_MODE_PLAIN) {
+      const bool wb = s == (uint32_t)(S - 1) && mode != ATTNRES_MODE_PLAIN;
+      if (wb) {
         if (mode == ATTNRES_MODE_ACCUM) {
 #pragma unroll
           for (int c = 0; c < NCH; ++c) {
@@ -792,6 +793,8 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
             }
           }
         }
+        // the updated partial row is written back (in a branch: an unconditional
+        // write-back through an empty resource made these kernels spill)
         char* prow = const_cast<char*>(uniform_ptr(src0 + (uint64_t)(S - 1) * src_stride + (uint64_t)t * row_bytes));
         const __amdgpu_buffer_rsrc_t prsrc = row_rsrc(prow, (uint32_t)(NCH * 1024));
 #pragma unroll
@@ -871,7 +874,7 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
       // ---- finalize the token row ----
       // Store addresses: a wave-uniform row base (SGPRs) plus a 32-bit lane offset.
       const float rl = 1.0f / l;
-      const int oes = P.out_bf16 ? 2 : 4;
+      constexpr int oes = OUTBF ? 2 : 4;
       char* orow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.out) + (uint64_t)t * (uint64_t)(P.out_ld * oes)));
       const __amdgpu_buffer_rsrc_t orsrc = row_rsrc(orow, (uint32_t)(P.d * oes));
       // Byte offset of this lane's first output element, made opaque so the
@@ -879,25 +882,27 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
       // rather than hoisted out of the loop and kept live in registers.
       uint32_t lane_ob = (uint32_t)lane * (uint32_t)(VEC * oes);
       asm volatile("" : "+v"(lane_ob));
+      {
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        float o[VEC];
+        for (int c = 0; c < NCH; ++c) {
+          float o[VEC];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) o[e] = acc[c][e] * rl;
-        if (P.out_bf16) {
-          const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * 2);
-          if constexpr (VEC == 8) {
-            st_row(orsrc, off, u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]),
-                                     pack_bf16(o[6], o[7])});
+          for (int e = 0; e < VEC; ++e) o[e] = acc[c][e] * rl;
+          if constexpr (OUTBF) {
+            const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * 2);
+            if constexpr (VEC == 8) {
+              st_row(orsrc, off, u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]),
+                                       pack_bf16(o[6], o[7])});
+            } else {
+              st_row(orsrc, off, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
+            }
           } else {
-            st_row(orsrc, off, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
-          }
-        } else {
-          const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * 4);
+            const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * 4);
 #pragma unroll
-          for (int h = 0; h < VEC / 4; ++h) {
-            st_row(orsrc, off + 16 * h,
-                   u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]), as_u32(o[4 * h + 2]), as_u32(o[4 * h + 3])});
+            for (int h = 0; h < VEC / 4; ++h) {
+              st_row(orsrc, off + 16 * h,
+                     u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]), as_u32(o[4 * h + 2]), as_u32(o[4 * h + 3])});
+            }
           }
         }
       }
@@ -1586,18 +1591,23 @@ MERGE_V(2)
 // Occupancy target (waves per SIMD): two row buffers + the fp32 accumulator
 // fit 128 VGPRs up to 6 KiB rows, 168 up to 8 KiB.
 #define STREAM_WAVES_PER_EU(NCH) ((NCH) <= 4 ? 4 : (NCH) <= 6 ? 3 : 2)
+// The fused kernels also hold the delta row of both pipeline slots.
+#define STREAM_FUSED_WAVES_PER_EU(NCH) ((NCH) <= 3 ? 4 : (NCH) <= 4 ? 3 : 2)
 
-#define STREAM_ONE(INNAME, BF, QNAME, QD2, NCH)                                                         \
+#define STREAM_ONE_OUT(INNAME, BF, QNAME, QD2, ONAME, OBF, NCH)                                        \
   extern "C" __global__ void __launch_bounds__(64 * ATTNRES_STREAM_WAVES)                               \
       __attribute__((amdgpu_waves_per_eu(STREAM_WAVES_PER_EU(NCH))))                                    \
-      attnres_stream_##INNAME##_##QNAME##_c##NCH##_plain(attnres_route_params P) {              \
-    stream_body<NCH, BF, QD2, false>(P);                                                             \
+      attnres_stream_##INNAME##_##QNAME##_o##ONAME##_c##NCH##_plain(attnres_route_params P) {           \
+    stream_body<NCH, BF, QD2, false, OBF>(P);                                                           \
   }                                                                                                     \
   extern "C" __global__ void __launch_bounds__(64 * ATTNRES_STREAM_WAVES)                               \
-      __attribute__((amdgpu_waves_per_eu(STREAM_WAVES_PER_EU(NCH))))                                    \
-      attnres_stream_##INNAME##_##QNAME##_c##NCH##_fused(attnres_route_params P) {              \
-    stream_body<NCH, BF, QD2, true>(P);                                                              \
+      __attribute__((amdgpu_waves_per_eu(STREAM_FUSED_WAVES_PER_EU(NCH))))                              \
+      attnres_stream_##INNAME##_##QNAME##_o##ONAME##_c##NCH##_fused(attnres_route_params P) {           \
+    stream_body<NCH, BF, QD2, true, OBF>(P);                                                            \
   }
+#define STREAM_ONE(INNAME, BF, QNAME, QD2, NCH)             \
+  STREAM_ONE_OUT(INNAME, BF, QNAME, QD2, bf, true, NCH)     \
+  STREAM_ONE_OUT(INNAME, BF, QNAME, QD2, f32, false, NCH)
 
 #define STREAM_TYPES(NCH)                 \
   STREAM_ONE(bf, true, d2, true, NCH)     \
