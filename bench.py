@@ -318,6 +318,7 @@ def main() -> int:
         achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
         t = 'bf' if w.dtype == torch.bfloat16 else 'f32'
         name = f"attnres_route_bwd_{t}_g{t}_s{dominant}_v1 (+ attnres_reduce_dqw_stage, attnres_reduce_dqw)"
+        traffic, traffic_src = load_traffic(f"bwd_{args.workload}_s{dominant}")
         print(json.dumps({
             "metric": "AttnRes routing backward achieved HBM GB/s",
             "value": round(gbs, 2),
@@ -336,8 +337,9 @@ def main() -> int:
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "tokens_per_s": round(w.tokens / (ms_per_step * 1e-3), 1),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
-                         "algorithmic_bytes": dom_bytes, "avg_ms": round(dom_ms, 4)},
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": name,
+                         "algorithmic_bytes": dom_bytes, "avg_ms": round(dom_ms, 4),
+                         **({"traffic_source": traffic_src} if traffic_src else {})},
         }), flush=True)
         return 0
     if args.workload == "cfg4":
