@@ -339,7 +339,7 @@ struct RouteChoice {
 };
 
 RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
-                         int num_queries, int num_cus, bool equally_spaced) {
+                         int num_queries, int num_cus, bool stream_ok) {
   RouteChoice ch;
   const bool bf = src_dtype == ATTNRES_DTYPE_BF16;
   ch.combo = bf ? (param_dtype == ATTNRES_DTYPE_BF16 ? kBfDot2 : kBfFma) : kF32Fma;
@@ -348,7 +348,7 @@ RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int sr
   // The streaming kernel addresses source s as src[0] + s*stride with 32-bit
   // row/item counters.
   const bool stream_shape = num_queries == 1 && num_sources >= 1 && row_bytes % 1024 == 0 && ch.nch >= 1 &&
-                            ch.nch <= kStreamMaxChunks && equally_spaced &&
+                            ch.nch <= kStreamMaxChunks && stream_ok &&
                             num_tokens * (int64_t)num_sources < (int64_t)1 << 31;
   const int policy = g_policy.load(std::memory_order_relaxed);
   const int want_stream = policy == ATTNRES_POLICY_STREAM      ? 1
@@ -437,8 +437,11 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
     for (int s = 2; s < num_sources && equally_spaced; ++s)
       equally_spaced = (int64_t)((uintptr_t)sources[s] - (uintptr_t)sources[0]) == src_stride * s;
   }
+  // The streaming kernel shares one delta buffer between its two pipeline
+  // slots, which needs S >= 2 when accumulating into the partial.
+  const bool stream_ok = equally_spaced && !(mode == ATTNRES_MODE_ACCUM && num_sources < 2);
   const RouteChoice ch =
-      choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus, equally_spaced);
+      choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus, stream_ok);
   if (!ch.stream && ch.v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
 
   hipFunction_t f = nullptr;

@@ -679,9 +679,6 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
 // row is prefetched with the partial row.
 
 #define ATTNRES_STREAM_WAVES 4
-#ifndef ATTNRES_STREAM_SLOTS
-#define ATTNRES_STREAM_SLOTS 2  // row buffers in the per-wave pipeline (2 or 3)
-#endif
 
 template <int NCH, bool BF16, bool QDOT2, bool FUSED, bool OUTBF>
 __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
@@ -728,7 +725,12 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   const uint64_t delta0 = reinterpret_cast<uint64_t>(P.delta);
 
   u32x4 bufA[NCH], bufB[NCH];
-  u32x4 dA[FUSED ? NCH : 1], dB[FUSED ? NCH : 1];
+  // Fused accumulate mode: the delta row of the token's partial source.  One
+  // buffer serves both pipeline slots: with S >= 2 (the host sends S == 1
+  // accumulate calls to the workgroup kernel) the two items in flight are
+  // never both a token's last source, and the delta is consumed by the item
+  // that loaded it before the next partial item is loaded.
+  u32x4 dX[FUSED ? NCH : 1];
 
   // Sources are equally spaced (the host checks): source s of row t is at
   // src0 + s*src_stride + t*row_bytes, pure scalar arithmetic.
@@ -772,10 +774,8 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
     // through phis and wait for the prefetch before using the current row).
     if constexpr (decltype(slot)::value == 0) {
       asm volatile("; attnres stream slot A");
-    } else if constexpr (decltype(slot)::value == 1) {
-      asm volatile("; attnres stream slot B");
     } else {
-      asm volatile("; attnres stream slot C");
+      asm volatile("; attnres stream slot B");
     }
     if constexpr (FUSED) {
       const bool wb = s == (uint32_t)(S - 1) && mode != ATTNRES_MODE_PLAIN;
@@ -941,36 +941,8 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
     s_out = wrap ? 0u : ss + 1;
     t_out = wrap ? t + nw : t;
   };
-#if ATTNRES_STREAM_SLOTS == 3
-  // three-slot ring: two items in flight while one is processed
-  u32x4 bufC[NCH];
-  u32x4 dC[FUSED ? NCH : 1];
-  using SlotC = std::integral_constant<int, 2>;
-  uint32_t t0 = tok, s0 = 0, t1, s1;
-  advance(t0, s0, t1, s1);
-  load_item(bufA, dA, t0, s0);
-  load_item(bufB, dB, n_items > 1 ? t1 : t0, n_items > 1 ? s1 : s0);
-  for (uint32_t i = 0; i < n_items; i += 3) {
-    uint32_t t2, s2, t3, s3, t4, s4;
-    advance(t1, s1, t2, s2);
-    advance(t2, s2, t3, s3);
-    advance(t3, s3, t4, s4);
-    const bool has1 = i + 1 < n_items, has2 = i + 2 < n_items;
-    const bool has3 = i + 3 < n_items, has4 = i + 4 < n_items;
-    load_item(bufC, dC, has2 ? t2 : t0, has2 ? s2 : s0);
-    process(bufA, dA, t0, s0, SlotA{});
-    load_item(bufA, dA, has3 ? t3 : t0, has3 ? s3 : s0);
-    if (has1) process(bufB, dB, t1, s1, SlotB{});
-    load_item(bufB, dB, has4 ? t4 : t0, has4 ? s4 : s0);
-    if (has2) process(bufC, dC, t2, s2, SlotC{});
-    t0 = __builtin_amdgcn_readfirstlane(t3);
-    s0 = __builtin_amdgcn_readfirstlane(s3);
-    t1 = __builtin_amdgcn_readfirstlane(t4);
-    s1 = __builtin_amdgcn_readfirstlane(s4);
-  }
-#else
   uint32_t s = 0;
-  load_item(bufA, dA, tok, 0);
+  load_item(bufA, dX, tok, 0);
   for (uint32_t i = 0; i < n_items; i += 2) {
     const bool has1 = i + 1 < n_items;
     const bool has2 = i + 2 < n_items;
@@ -978,14 +950,13 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
     advance(tok, s, t1, s1);
     advance(t1, s1, t2, s2);
     // past the last item the prefetch re-reads the current (valid) row
-    load_item(bufB, dB, has1 ? t1 : tok, has1 ? s1 : s);
-    process(bufA, dA, tok, s, SlotA{});
-    load_item(bufA, dA, has2 ? t2 : tok, has2 ? s2 : s);
-    if (has1) process(bufB, dB, t1, s1, SlotB{});
+    load_item(bufB, dX, has1 ? t1 : tok, has1 ? s1 : s);
+    process(bufA, dX, tok, s, SlotA{});
+    load_item(bufA, dX, has2 ? t2 : tok, has2 ? s2 : s);
+    if (has1) process(bufB, dX, t1, s1, SlotB{});
     tok = __builtin_amdgcn_readfirstlane(t2);
     s = __builtin_amdgcn_readfirstlane(s2);
   }
-#endif
 }
 
 

@@ -351,6 +351,34 @@ def test_block_arena_state_and_fp32(gpu, policy):
         check_f32(outs[j], ref["outs"][j], f"arena point {j}")
 
 
+@pytest.mark.parametrize("d", [512, 3072, 4096])
+def test_block_arena_accumulate_without_first_boundary(gpu, policy, d):
+    # boundaries not including layer 0: the first pre-MLP point accumulates into
+    # the partial with S = 1 (routed to the workgroup kernel even under the
+    # streaming policy), later points accumulate with S >= 2 (streaming kernel,
+    # one delta buffer shared by the two pipeline slots), bf16, rows of whole KiB
+    n = 40
+    sched = AttnResSchedule.build(5, boundaries=[1, 3])
+    g = torch.Generator(device=gpu).manual_seed(13)
+    embed = torch.randn((n, d), generator=g, device=gpu).to(torch.bfloat16)
+    deltas = torch.randn((10, n, d), generator=g, device=gpu).to(torch.bfloat16)
+    q = (torch.randn((11, d), generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+    gn = (1 + 0.1 * torch.randn((11, d), generator=g, device=gpu)).to(torch.bfloat16)
+    router = AttnResRouter(sched, list(q), list(gn), 1e-5)
+    outs = []
+
+    def sublayer(j, h):
+        outs.append(h.clone())
+        return deltas[j]
+
+    outs.append(router.forward(embed, sublayer))
+    assert sched.active_counts[1] == 1 and not sched.commit_before[1]
+    qws = [fold(q[j], gn[j], torch.bfloat16) for j in range(11)]
+    ref = O.block_forward(np64(embed), [np64(deltas[j]) for j in range(10)], qws, 1e-5, 5, {1, 3}, dtype="bf16")
+    for j in range(11):
+        check_bf16(outs[j], ref["outs"][j], f"arena point {j}")
+
+
 # ------------------------------------------------- phase 1 / phase 2 --
 
 
