@@ -481,6 +481,7 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   P.out_bf16 = out_dtype == ATTNRES_DTYPE_BF16;
   P.mode = mode;
   P.num_sources = num_sources;
+  P.block = block;
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
   return launch(f, grid_for(work_units, st->num_cus, bpc), block, P, stream);
@@ -608,6 +609,7 @@ int attnres_merge_fwd(const void* partial, int64_t num_tokens, int hidden, int p
   P.nchunk = nchunk;
   P.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
   P.inter_bf16 = ibf;
+  P.block = block;
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
   return launch(f, grid_for(num_tokens, st->num_cus, bpc), block, P, stream);

@@ -265,6 +265,38 @@ __device__ __forceinline__ void load_qw(const attnres_route_params& P, int q, in
   }
 }
 
+// A parameter chunk (VEC elements, bf16 or fp32 by a runtime flag) loaded
+// packed; converted with param_elem after every load of the prologue has been
+// issued, so the loads share one wait.
+template <int VEC>
+struct ParamRaw {
+  u32x4 w[VEC == 8 ? 2 : 1];
+};
+template <int VEC>
+__device__ __forceinline__ void load_param_raw(const void* base, int chunk, bool bf16, ParamRaw<VEC>& r) {
+  const char* b = reinterpret_cast<const char*>(base);
+  if (bf16) {
+    if constexpr (VEC == 8) {
+      r.w[0] = ldg_global<u32x4>(b + (int64_t)chunk * 16);
+      r.w[1] = u32x4{0, 0, 0, 0};
+    } else {
+      const u32x2 t = ldg_global<u32x2>(b + (int64_t)chunk * 8);
+      r.w[0] = u32x4{t[0], t[1], 0, 0};
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < VEC / 4; ++h) r.w[h] = ldg_global<u32x4>(b + ((int64_t)chunk * VEC + 4 * h) * 4);
+  }
+}
+template <int VEC>
+__device__ __forceinline__ float param_elem(const ParamRaw<VEC>& r, int e, bool bf16) {
+  if (bf16) {
+    const uint32_t w = r.w[0][e >> 1];
+    return (e & 1) ? bf_hi(w) : bf_lo(w);
+  }
+  return as_f32(r.w[e >> 2][e & 3]);
+}
+
 // ------------------------------------------------------------ route body --
 
 // S     : number of active sources (0 writes NaN, as softmax over no sources)
@@ -283,21 +315,31 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int nwaves = (blockDim.x + 63) >> 6;
+  const int block = P.block;
+  const int nwaves = (block + 63) >> 6;
   const int nq = MULTIQ ? P.num_queries : 1;
 
   int chunk[V];
   bool ok[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) {
-    chunk[k] = tid + k * (int)blockDim.x;
+    chunk[k] = tid + k * block;
     ok[k] = chunk[k] < P.nchunk;
   }
 
   // Pseudo-query chunks, kept in registers across the token loop (Q == 1).
   float qwf[V][VEC];
   uint32_t qwb[V][VEC / 2];
-  auto fetch_qw = [&](int q) {
+  auto set_qw = [&](int k, const float (&t)[VEC]) {
+    if constexpr (QDOT2) {
+#pragma unroll
+      for (int e = 0; e < VEC / 2; ++e) qwb[k][e] = pack_bf16(t[2 * e], t[2 * e + 1]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) qwf[k][e] = t[e];
+    }
+  };
+  auto fetch_qw = [&](int q) {  // multi-query: query q of the batch
 #pragma unroll
     for (int k = 0; k < V; ++k) {
       float t[VEC];
@@ -307,18 +349,66 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) t[e] = 0.f;
       }
-      if constexpr (QDOT2) {
-#pragma unroll
-        for (int e = 0; e < VEC / 2; ++e) qwb[k][e] = pack_bf16(t[2 * e], t[2 * e + 1]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) qwf[k][e] = t[e];
-      }
+      set_qw(k, t);
     }
   };
-  if constexpr (!MULTIQ) fetch_qw(0);
-
   const int64_t row_bytes_ld = P.src_ld * C::BYTES;
+  // One token row of sources (and, fused, of the delta) in registers.  The
+  // first row is requested before the parameters, so a workgroup that owns a
+  // single row (decode) waits for memory once, not once per dependent load.
+  constexpr int SX = S > 0 ? S : 1;
+  u32x4 x[SX][V];
+  u32x4 dvr[V];
+  auto load_row = [&](int64_t t) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const char* row = reinterpret_cast<const char*>(P.src[s]) + t * row_bytes_ld;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        if (s == S - 1 && P.mode == ATTNRES_MODE_SET) {
+          x[s][k] = u32x4{0, 0, 0, 0};
+        } else {
+          x[s][k] = ok[k] ? ldg_global<u32x4>(row + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
+        }
+      }
+    }
+    if (S > 0 && P.mode != ATTNRES_MODE_PLAIN) {
+      const char* drow = reinterpret_cast<const char*>(P.delta) + t * P.delta_ld * C::BYTES;
+#pragma unroll
+      for (int k = 0; k < V; ++k) dvr[k] = ok[k] ? ldg_global<u32x4>(drow + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
+    }
+  };
+  if (S > 0 && (int64_t)blockIdx.x < P.n_tokens) load_row(blockIdx.x);
+  if constexpr (!MULTIQ) {
+    // query and gain issued back to back, folded after both arrive
+    ParamRaw<VEC> rq[V], rg[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      if (!ok[k]) continue;
+      load_param_raw<VEC>(P.query, chunk[k], P.param_bf16, rq[k]);
+      if (P.gain != nullptr) load_param_raw<VEC>(P.gain, chunk[k], P.param_bf16, rg[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      float t[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        if (!ok[k]) {
+          t[e] = 0.f;
+          continue;
+        }
+        const float qv = param_elem<VEC>(rq[k], e, P.param_bf16);
+        if (P.gain != nullptr) {
+          const float prod = qv * param_elem<VEC>(rg[k], e, P.param_bf16);
+          t[e] = P.param_bf16 ? round_bf16(prod) : prod;
+        } else {
+          t[e] = qv;
+        }
+      }
+      set_qw(k, t);
+    }
+  }
+
   int ph = 0;
 
   for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
@@ -351,30 +441,12 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
       }
       continue;
     } else {
-      // ---- stream the S source chunks of this token into registers ----
-      u32x4 x[S][V];
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        const char* row = reinterpret_cast<const char*>(P.src[s]) + tok * row_bytes_ld;
-#pragma unroll
-        for (int k = 0; k < V; ++k) {
-          if (s == S - 1 && P.mode == ATTNRES_MODE_SET) {
-            x[s][k] = u32x4{0, 0, 0, 0};
-          } else {
-            x[s][k] = ok[k] ? ldg_global<u32x4>(row + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
-          }
-        }
-      }
-
       // ---- fused partial update: partial (+)= delta, written back ----
       if (P.mode != ATTNRES_MODE_PLAIN) {
-        const char* drow = reinterpret_cast<const char*>(P.delta) + tok * P.delta_ld * C::BYTES;
-        char* prow = reinterpret_cast<char*>(const_cast<void*>(P.src[S - 1])) + tok * row_bytes_ld;
-        const __amdgpu_buffer_rsrc_t prsrc = row_rsrc(prow, (uint32_t)(P.d * C::BYTES));
 #pragma unroll
         for (int k = 0; k < V; ++k) {
           if (!ok[k]) continue;
-          const u32x4 dv = ldg<u32x4>(drow + (int64_t)chunk[k] * 16);
+          const u32x4 dv = dvr[k];
           u32x4 nv = dv;
           if (P.mode == ATTNRES_MODE_ACCUM) {
             if constexpr (BF16) {
@@ -388,7 +460,6 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
             }
           }
           x[S - 1][k] = nv;
-          st_row(prsrc, (uint32_t)chunk[k] * 16, nv);
         }
       }
 
@@ -521,11 +592,53 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
           }
         }
       }
+      // The updated partial row is written back after the output row: a store
+      // issued before the dot products would be waited for with the loads.
+      if (P.mode != ATTNRES_MODE_PLAIN) {
+        char* prow = reinterpret_cast<char*>(const_cast<void*>(P.src[S - 1])) + tok * row_bytes_ld;
+        const __amdgpu_buffer_rsrc_t prsrc = row_rsrc(prow, (uint32_t)(P.d * C::BYTES));
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+          if (ok[k]) st_row(prsrc, (uint32_t)chunk[k] * 16, x[S - 1][k]);
+        }
+      }
+      if (tok + gridDim.x < P.n_tokens) load_row(tok + gridDim.x);
     }
   }
 }
 
 // ------------------------------------------------------------ merge body --
+
+// One VEC-element chunk of a bf16 (GBF) or fp32 row, packed as loaded.
+template <int VEC, bool GBF>
+struct PackedChunk {
+  static constexpr int WORDS = VEC * (GBF ? 2 : 4) / 4;
+  uint32_t w[WORDS];
+  __device__ __forceinline__ void load(const char* row, int chunk) {
+    const char* p = row + (int64_t)chunk * (WORDS * 4);
+    if constexpr (WORDS == 2) {
+      const u32x2 t = ldg_global<u32x2>(p);
+      w[0] = t[0];
+      w[1] = t[1];
+    } else {
+#pragma unroll
+      for (int h = 0; h < WORDS / 4; ++h) {
+        const u32x4 t = ldg_global<u32x4>(p + h * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[4 * h + i] = t[i];
+      }
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < WORDS; ++i) w[i] = 0u;
+  }
+  __device__ __forceinline__ float elem(int e) const {
+    if constexpr (GBF) return (e & 1) ? bf_hi(w[e >> 1]) : bf_lo(w[e >> 1]);
+    else return as_f32(w[e]);
+  }
+};
+
 
 // Phase-2 merge of the intra-block partial into the phase-1 inter-block
 // result (kernels/phase_2.py:40-57 semantics): one token row per workgroup.
@@ -533,19 +646,43 @@ template <int V, bool PBF16, bool IBF16>
 __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
   using C = Chunk<PBF16>;
   constexpr int VEC = C::VEC;
+  using IC = PackedChunk<VEC, IBF16>;
   __shared__ float red[2][ATTNRES_KMAX_WAVES][4];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int nwaves = (blockDim.x + 63) >> 6;
+  const int block = P.block;
+  const int nwaves = (block + 63) >> 6;
 
   int chunk[V];
   bool ok[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    chunk[k] = tid + k * block;
+    ok[k] = chunk[k] < P.nchunk;
+  }
+  // The row (partial and inter, packed) is requested before the query, so a
+  // workgroup that owns one row waits for memory once.
+  u32x4 p[V];
+  IC ic[V];
+  auto load_row = [&](int64_t t) {
+    const char* prow = reinterpret_cast<const char*>(P.partial) + t * P.partial_ld * C::BYTES;
+    const char* irow = reinterpret_cast<const char*>(P.inter) + t * P.inter_ld * (IBF16 ? 2 : 4);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      if (ok[k]) {
+        p[k] = ldg_global<u32x4>(prow + (int64_t)chunk[k] * 16);
+        ic[k].load(irow, chunk[k]);
+      } else {
+        p[k] = u32x4{0, 0, 0, 0};
+        ic[k].zero();
+      }
+    }
+  };
+  if ((int64_t)blockIdx.x < P.n_tokens) load_row(blockIdx.x);
   float qw[V][VEC];
 #pragma unroll
   for (int k = 0; k < V; ++k) {
-    chunk[k] = tid + k * (int)blockDim.x;
-    ok[k] = chunk[k] < P.nchunk;
     if (ok[k]) {
       load_param<VEC>(P.query, (int64_t)chunk[k] * VEC, P.param_bf16, qw[k]);
     } else {
@@ -556,46 +693,6 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
 
   int ph = 0;
   for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
-    const char* prow = reinterpret_cast<const char*>(P.partial) + tok * P.partial_ld * C::BYTES;
-    const char* irow = reinterpret_cast<const char*>(P.inter) + tok * P.inter_ld * (IBF16 ? 2 : 4);
-    u32x4 p[V];
-    float iv[V][VEC];
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-      p[k] = ok[k] ? ldg<u32x4>(prow + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
-      if (ok[k]) {
-        if constexpr (IBF16) {
-#pragma unroll
-          for (int h = 0; h < VEC / 8 + (VEC < 8); ++h) {
-            if constexpr (VEC == 8) {
-              const u32x4 t = ldg<u32x4>(irow + (int64_t)chunk[k] * 16);
-#pragma unroll
-              for (int w = 0; w < 4; ++w) {
-                iv[k][2 * w] = bf_lo(t[w]);
-                iv[k][2 * w + 1] = bf_hi(t[w]);
-              }
-            } else {
-              const u32x2 t = ldg<u32x2>(irow + (int64_t)chunk[k] * 8);
-              iv[k][0] = bf_lo(t[0]);
-              iv[k][1] = bf_hi(t[0]);
-              iv[k][2] = bf_lo(t[1]);
-              iv[k][3] = bf_hi(t[1]);
-            }
-          }
-        } else {
-#pragma unroll
-          for (int h = 0; h < VEC / 4; ++h) {
-            const u32x4 t = ldg<u32x4>(irow + ((int64_t)chunk[k] * VEC + 4 * h) * 4);
-#pragma unroll
-            for (int w = 0; w < 4; ++w) iv[k][4 * h + w] = as_f32(t[w]);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) iv[k][e] = 0.f;
-      }
-    }
-
     float ss = 0.f, dt = 0.f;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
@@ -634,7 +731,10 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
       if (!ok[k]) continue;
       float o[VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) o[e] = __builtin_fmaf(pi, C::elem(p[k], e) - iv[k][e], iv[k][e]);
+      for (int e = 0; e < VEC; ++e) {
+        const float iv = ic[k].elem(e);
+        o[e] = __builtin_fmaf(pi, C::elem(p[k], e) - iv, iv);
+      }
       if constexpr (IBF16) {
         if constexpr (VEC == 8) {
           st_row(orsrc, (uint32_t)chunk[k] * 16,
@@ -651,6 +751,7 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
         }
       }
     }
+    if (tok + gridDim.x < P.n_tokens) load_row(tok + gridDim.x);
   }
 }
 
@@ -981,42 +1082,13 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
 // gradient sum_s c1_s x_s is accumulated in registers over all rows the
 // workgroup handles and written once as this workgroup's partial.
 
-// G (dL/dout) for one VEC-element chunk, packed as loaded: GBF = bf16 G.
-template <int VEC, bool GBF>
-struct GradChunk {
-  static constexpr int WORDS = VEC * (GBF ? 2 : 4) / 4;
-  uint32_t w[WORDS];
-  __device__ __forceinline__ void load(const char* row, int chunk) {
-    const char* p = row + (int64_t)chunk * (WORDS * 4);
-    if constexpr (WORDS == 2) {
-      const u32x2 t = ldg_global<u32x2>(p);
-      w[0] = t[0];
-      w[1] = t[1];
-    } else {
-#pragma unroll
-      for (int h = 0; h < WORDS / 4; ++h) {
-        const u32x4 t = ldg_global<u32x4>(p + h * 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[4 * h + i] = t[i];
-      }
-    }
-  }
-  __device__ __forceinline__ void zero() {
-#pragma unroll
-    for (int i = 0; i < WORDS; ++i) w[i] = 0u;
-  }
-  __device__ __forceinline__ float elem(int e) const {
-    if constexpr (GBF) return (e & 1) ? bf_hi(w[e >> 1]) : bf_lo(w[e >> 1]);
-    else return as_f32(w[e]);
-  }
-};
 
 template <int S, int V, bool BF16, bool GBF>
 __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P) {
   constexpr bool PF = S <= ATTNRES_BWD_PREFETCH_MAX_S;
   using C = Chunk<BF16>;
   constexpr int VEC = C::VEC;
-  using GC = GradChunk<VEC, GBF>;
+  using GC = PackedChunk<VEC, GBF>;
   constexpr int NV = 3 * S;
   constexpr int RLD = ((NV + 3) / 4) * 4;
   __shared__ float red[2][ATTNRES_KMAX_WAVES][RLD];

@@ -56,6 +56,8 @@ typedef struct attnres_route_params {
   int32_t out_bf16;     /* out dtype: 1 bf16, 0 fp32 */
   int32_t mode;         /* ATTNRES_MODE_* */
   int32_t num_sources;  /* S (the streaming kernels read it; the others are specialised on it) */
+  int32_t block;        /* threads per workgroup (read as a kernel argument, not from the
+                           dispatch packet, so it costs no vector load) */
   float eps;
   float inv_d;
 } attnres_route_params;
@@ -121,6 +123,7 @@ typedef struct attnres_merge_params {
   int32_t nchunk;
   int32_t param_bf16;
   int32_t inter_bf16;
+  int32_t block;          /* threads per workgroup */
   float eps;
   float inv_d;
 } attnres_merge_params;
