@@ -94,3 +94,63 @@ def test_merge_argument_errors():
     a = list(args)
     a[2] = 60
     assert lib.attnres_merge_fwd(*a) == _capi.ERR_UNSUPPORTED
+
+
+def bwd(sources=None, S=None, N=16, D=64, ld=None, sdt=_capi.DTYPE_BF16, query=FAKE, gain=None,
+        pdt=_capi.DTYPE_BF16, eps=1e-5, gout=FAKE, gdt=_capi.DTYPE_BF16, gld=None, grads=None, grad_ld=None,
+        ws=FAKE, ws_bytes=1 << 30, dq=FAKE, dg=None):
+    sources = [FAKE + 4096 * i for i in range(3)] if sources is None else sources
+    grads = [FAKE + (1 << 20) + 4096 * i for i in range(len(sources))] if grads is None else grads
+    S = len(sources) if S is None else S
+    return _capi.lib().attnres_route_bwd(
+        _capi.pointer_array(sources), S, N, D, ld if ld is not None else D, sdt, query, gain, pdt, eps, gout, gdt,
+        gld if gld is not None else D, None, _capi.pointer_array(grads), grad_ld if grad_ld is not None else D, ws,
+        ws_bytes, dq, dg, None)
+
+
+def test_route_bwd_argument_errors():
+    assert bwd(N=0) == _capi.OK  # no tokens: returns before any HIP call
+    assert bwd(S=0) == _capi.ERR_UNSUPPORTED  # nothing to differentiate
+    assert bwd(sources=[FAKE] * 17, grads=[FAKE] * 17) == _capi.ERR_UNSUPPORTED
+    assert bwd(query=None) == _capi.ERR_ARG
+    assert bwd(gout=None) == _capi.ERR_ARG
+    assert bwd(dg=FAKE) == _capi.ERR_ARG  # grad_gain without gain
+    assert bwd(gdt=5) == _capi.ERR_ARG
+    assert bwd(D=12) == _capi.ERR_UNSUPPORTED
+    assert bwd(D=8192 + 8) == _capi.ERR_UNSUPPORTED
+    assert bwd(grad_ld=32) == _capi.ERR_ARG
+    assert bwd(gout=FAKE + 4) == _capi.ERR_ALIGN
+    assert bwd(grads=[FAKE, FAKE + 8, FAKE]) == _capi.ERR_ALIGN
+    assert bwd(eps=float("inf")) == _capi.ERR_ARG
+    assert bwd(grads=[FAKE, 0, FAKE]) == _capi.ERR_ARG
+    assert "grad_sources[1]" in _capi.lib().attnres_last_error().decode()
+
+
+def test_merge_bwd_argument_errors():
+    lib = _capi.lib()
+    args = [FAKE, 16, 64, _capi.DTYPE_BF16, FAKE, _capi.DTYPE_BF16, FAKE, _capi.DTYPE_BF16, FAKE, 1e-5, FAKE,
+            FAKE + 8192, FAKE + 16384, None, FAKE, 1 << 30, FAKE, None]
+    a = list(args)
+    a[1] = 0
+    assert lib.attnres_merge_bwd(*a) == _capi.OK
+    for i in (0, 4, 6, 8, 10, 11, 12):  # required pointers
+        a = list(args)
+        a[i] = None
+        assert lib.attnres_merge_bwd(*a) == _capi.ERR_ARG, i
+    a = list(args)
+    a[2] = 60
+    assert lib.attnres_merge_bwd(*a) == _capi.ERR_UNSUPPORTED
+    a = list(args)
+    a[11] = FAKE + 8
+    assert lib.attnres_merge_bwd(*a) == _capi.ERR_ALIGN
+    a = list(args)
+    a[9] = float("nan")
+    assert lib.attnres_merge_bwd(*a) == _capi.ERR_ARG
+
+
+def test_kernel_name_argument_errors():
+    lib = _capi.lib()
+    buf = ctypes.create_string_buffer(8)
+    assert lib.attnres_route_kernel_name(3, 16, 64, 1, 1, 1, 1, 0, None, 0) == _capi.ERR_ARG
+    assert lib.attnres_route_kernel_name(3, 16, 64, 1, 1, 9, 1, 0, buf, 8) == _capi.ERR_ARG  # out dtype
+    assert lib.attnres_route_kernel_name(17, 16, 64, 1, 1, 1, 1, 0, buf, 8) == _capi.ERR_ARG
