@@ -45,3 +45,67 @@ def test_serve_fast_path_matches_stack_free_forward_bf16(gpu):
     # the fast path rounds each phase-1 result to bf16 before merging (as the reference's)
     rel = (fast.float() - slow.float()).norm() / slow.float().norm()
     assert rel < 1e-2, f"relative difference {rel:.3e}"
+
+
+def _training_forward(model, embed, route_fn):
+    """The training loop of llama.py:666-716 (pad + stack before every routing call,
+    out-of-place partial updates), with the routing function swapped in."""
+    from kotodama_amd import AttnResSchedule
+
+    sched = AttnResSchedule.build(model.config.num_layers, boundaries=sorted(model._attn_res_boundary_set))
+    masks = sched.masks(embed.device)
+    counts = sched.active_counts
+    committed, partial = [], embed
+    zero = torch.zeros_like(embed)
+
+    def pad_and_stack():
+        sources = committed + [partial]
+        sources += [zero] * (sched.max_sources - len(sources))
+        return torch.stack(sources, dim=0)
+
+    for i, layer in enumerate(model.layers):
+        h = route_fn(pad_and_stack(), layer.attn_res_query, layer.attn_res_norm, masks[2 * i], counts[2 * i])
+        if i in model._attn_res_boundary_set:
+            committed.append(partial.clone())
+            partial = zero.clone()
+        partial = partial + layer.attn(layer.attn_norm(h), None, None)
+        h = route_fn(pad_and_stack(), layer.mlp_res_query, layer.mlp_res_norm, masks[2 * i + 1], counts[2 * i + 1])
+        partial = partial + layer.ffn(layer.ffn_norm(h))
+    x = route_fn(pad_and_stack(), model.final_res_query, model.final_res_norm, masks[-1], counts[-1])
+    return model.norm(x)
+
+
+def test_training_step_gradients_match_float64_reference(gpu):
+    # the reference's training forward with _route_static swapped for the HIP op:
+    # loss and every parameter gradient (routing queries and gains, sublayer
+    # weights upstream of the routing calls) against the same loop in float64
+    # on the CPU with the einsum branch's op sequence
+    from kotodama_amd import route_static
+    from oracle.torch_cpu_path import route_static_cpu
+
+    model = TinyModel(d=512, num_layers=4, boundaries=(0, 2), seed=21)
+    ref_model = copy.deepcopy(model).double()
+    g = torch.Generator().manual_seed(22)
+    embed = torch.randn((2, 16, 512), generator=g)
+    G = torch.randn((2, 16, 512), generator=g)
+
+    out_ref = _training_forward(ref_model, embed.double(),
+                                lambda buf, q, norm, mask, n: route_static_cpu(buf, q * norm.weight, norm.eps, mask))
+    loss_ref = (out_ref * G.double()).sum()
+    loss_ref.backward()
+
+    m = model.to(gpu)
+    out = _training_forward(m, embed.to(gpu), route_static)
+    loss = (out * G.to(gpu)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    assert abs(loss.item() - loss_ref.item()) <= 1e-4 * abs(loss_ref.item()) + 1e-3
+    checked = 0
+    for (name, p), (_, pr) in zip(m.named_parameters(), ref_model.named_parameters()):
+        if pr.grad is None:
+            continue
+        got, want = p.grad.double().cpu(), pr.grad
+        tol = 2e-4 * want.abs().max().item() + 1e-7
+        assert (got - want).abs().max().item() <= tol, f"{name}: max err {(got - want).abs().max().item():.3e}"
+        checked += 1
+    assert checked == len(list(m.parameters()))  # every parameter is upstream of the loss
