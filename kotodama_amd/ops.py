@@ -391,19 +391,23 @@ def route_bwd(
     eps: float,
     grad_out: Tensor,
     grad_lse: Optional[Tensor],
+    zero_inactive: bool = True,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """(grad_buf, grad_query, grad_gain) of ``route``.
 
-    ``grad_buf`` is zero in slots at or beyond ``num_sources``; ``grad_gain``
-    is an empty tensor when ``gain`` is None.  With ``num_sources == 0`` the
-    forward output is NaN and so are the gradients.
+    ``grad_buf`` is zero in slots at or beyond ``num_sources`` (left
+    unwritten when ``zero_inactive`` is False: for a caller whose gradient
+    of those slots is discarded); ``grad_gain`` is an empty tensor when
+    ``gain`` is None.  With ``num_sources == 0`` the forward output is NaN and
+    so are the gradients.
     """
     device = _require_device(buf, query, gain, grad_out, grad_lse)
     buf = buf.contiguous()
     d = buf.shape[-1]
     n = buf[0].numel() // d if buf.shape[0] else 0
     grad_buf = torch.empty_like(buf)
-    grad_buf[num_sources:].zero_()
+    if zero_inactive:
+        grad_buf[num_sources:].zero_()
     gq_dtype = query.dtype
     gg = torch.empty((0,), device=device, dtype=gain.dtype if gain is not None else query.dtype)
     if num_sources == 0 or n == 0:
@@ -419,7 +423,7 @@ def route_bwd(
 
 
 @route_bwd.register_fake
-def _route_bwd_fake(buf, num_sources, query, gain, eps, grad_out, grad_lse):
+def _route_bwd_fake(buf, num_sources, query, gain, eps, grad_out, grad_lse, zero_inactive=True):
     gg = torch.empty_like(gain) if gain is not None else query.new_empty((0,))
     return torch.empty_like(buf), torch.empty_like(query), gg
 
@@ -456,12 +460,30 @@ def _route_list_bwd_fake(sources, query, gain, eps, grad_out, grad_lse):
     return [torch.empty_like(t) for t in sources], torch.empty_like(query), gg
 
 
+def _inactive_grads_discarded(buf: Tensor, num_sources: int) -> bool:
+    """True when ``buf`` is a ``torch.stack`` whose inputs from ``num_sources`` on
+    do not require grad (the reference's zero padding, llama.py:690-695):
+    their gradient rows are then dropped by the stack's backward, so the
+    routing backward need not write them (zeroing them costs one row write
+    per padding slot per call).  Any other producer keeps the zero fill."""
+    fn = buf.grad_fn
+    if fn is None or fn.name() != "StackBackward0":
+        return False
+    if getattr(buf, "retains_grad", False) or getattr(buf, "_backward_hooks", None):
+        return False  # the buffer's own gradient is observed
+    nxt = fn.next_functions
+    if len(nxt) != buf.shape[0]:
+        return False
+    return all(f is None for f, _ in nxt[num_sources:])
+
+
 def _route_setup_context(ctx, inputs, output):
     buf, num_sources, query, gain, eps, out_dtype, _, _ = inputs
     out, weights, lse, inv_rms, logits = output
     ctx.mark_non_differentiable(weights, inv_rms, logits)
     ctx.set_materialize_grads(False)
     ctx.save_for_backward(buf, query, gain)
+    ctx.zero_inactive = not _inactive_grads_discarded(buf, num_sources)
     ctx.num_sources = num_sources
     ctx.eps = eps
     ctx.out_shape = tuple(out.shape)
@@ -473,7 +495,7 @@ def _route_backward(ctx, g_out, g_w, g_lse, g_inv, g_logits):
     if g_out is None and g_lse is None:
         return None, None, None, None, None, None, None, None
     g_out = _bwd_args(g_out, ctx.out_shape, buf.device, ctx.out_dtype)
-    grad_buf, gq, gg = route_bwd(buf, ctx.num_sources, query, gain, ctx.eps, g_out, g_lse)
+    grad_buf, gq, gg = route_bwd(buf, ctx.num_sources, query, gain, ctx.eps, g_out, g_lse, ctx.zero_inactive)
     need = ctx.needs_input_grad
     return (
         grad_buf if need[0] else None,

@@ -119,6 +119,32 @@ def test_route_static_backward_matches_oracle(gpu, dtype, S, D, B, T):
     check_grad(norm.weight.grad, dg, dtype, "dgain")
 
 
+def test_padded_stack_backward_like_the_training_loop(gpu):
+    # llama.py:690-699: committed blocks + partial + zero padding stacked, then
+    # routed; the padding does not require grad, so its gradient rows are not
+    # written, and the real sources still get the oracle's gradients
+    eps = 1e-5
+    S, B, T, D = 3, 2, 24, 3072
+    buf, query, gain, G = make_case(gpu, S, 0, B, T, D, torch.bfloat16, seed=91)
+    srcs = [buf[i].clone().requires_grad_(True) for i in range(S)]
+    zero = torch.zeros_like(srcs[0])
+    stacked = torch.stack(srcs + [zero] * 5)
+    norm = Norm(gain.clone(), eps)
+    mask = torch.zeros(8, dtype=torch.bool, device=gpu)
+    mask[:S] = True
+    out = kotodama_amd.route_static(stacked, query, norm, mask, S)
+    (out.float() * G).sum().backward()
+    dx, _, dg = oracle_grads(buf, S, query, norm.weight, G, eps, torch.bfloat16)
+    for s in range(S):
+        check_grad(srcs[s].grad.reshape(-1, D), dx[s], torch.bfloat16, f"dsource[{s}]")
+    check_grad(norm.weight.grad, dg, torch.bfloat16, "dgain")
+    # an observed buffer gradient keeps exact zeros in the padding slots
+    stacked2 = torch.stack([s.detach().clone().requires_grad_(True) for s in srcs] + [zero] * 5)
+    stacked2.retain_grad()
+    kotodama_amd.route_static(stacked2, query, norm, mask, S).float().mul(G).sum().backward()
+    assert torch.all(stacked2.grad[S:] == 0)
+
+
 def test_list_backward_and_separate_tensors(gpu):
     # block_attn_res_from_list: each source its own allocation (no stacked buffer)
     eps = 1e-5
