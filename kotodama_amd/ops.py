@@ -74,8 +74,9 @@ def _require_device(*tensors: Optional[Tensor]) -> torch.device:
 def _no_grad_needed(*tensors: Optional[Tensor]) -> None:
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
         raise NotImplementedError(
-            "attnres_hip ops are forward-only: backward through AttnRes routing is not implemented "
-            "(run under torch.no_grad()/inference_mode, or detach the inputs)"
+            "this attnres_hip path (the block-arena engine / the routing-weights helper) is forward-only: "
+            "run it under torch.no_grad()/inference_mode or detach the inputs; for training route through "
+            "route_static / block_attn_res_from_list, which are differentiable"
         )
 
 
