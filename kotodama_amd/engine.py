@@ -15,6 +15,9 @@ call per routing point adds the previous sublayer's output to the partial
 and routes — a commit is only an index bump.  Per routing point this moves
 (S+3) rows instead of the reference's stack (max_S writes + S reads), route
 and separate add.
+
+Under autograd (training) the same loop runs with differentiable list-based
+routing calls instead (no arena mutation, still no stacked copy).
 """
 
 from __future__ import annotations
@@ -119,11 +122,16 @@ class AttnResRouter:
         return h
 
 
-def _model_router(model) -> AttnResRouter:
+def _model_schedule(model) -> AttnResSchedule:
     sched = getattr(model, "_kotodama_amd_schedule", None)
     if sched is None:
         sched = AttnResSchedule.build(model.config.num_layers, boundaries=sorted(model._attn_res_boundary_set))
         model._kotodama_amd_schedule = sched
+    return sched
+
+
+def _model_router(model) -> AttnResRouter:
+    sched = _model_schedule(model)
     queries, gains = [], []
     for layer in model.layers:
         queries += [layer.attn_res_query, layer.mlp_res_query]
@@ -133,17 +141,52 @@ def _model_router(model) -> AttnResRouter:
     return AttnResRouter(sched, queries, gains, model.final_res_norm.eps)
 
 
+def _grad_needed(model, embed: Tensor) -> bool:
+    return torch.is_grad_enabled() and (embed.requires_grad or any(p.requires_grad for p in model.parameters()))
+
+
+def _route_points_autograd(model, embed: Tensor, sublayer: Callable[[int, Tensor], Tensor]) -> Tensor:
+    """The caller loop of llama.py:697-715 under autograd, without the stacks.
+
+    Every routing point passes the committed blocks and the partial as a list
+    of tensors (``attnres_hip::route_list``: one pointer per source, no
+    padded ``(max_S, B, T, D)`` copy, differentiable through the backward
+    kernels).  A commit appends the partial itself (nothing mutates it later)
+    and the new partial starts as the next sublayer output, which is what
+    ``zero.clone() + attn_out`` gives.
+    """
+    committed: list[Tensor] = []
+    partial: Optional[Tensor] = embed
+
+    def route(query: Tensor, norm) -> Tensor:
+        gain = norm.weight
+        out_dtype = torch.promote_types(embed.dtype, torch.promote_types(query.dtype, gain.dtype))
+        return ops.route_list(committed + [partial], query, gain, float(norm.eps), out_dtype, False, False)[0][0]
+
+    boundaries = model._attn_res_boundary_set
+    for i, layer in enumerate(model.layers):
+        h = route(layer.attn_res_query, layer.attn_res_norm)
+        if i in boundaries:
+            committed.append(partial)
+            partial = None
+        d = sublayer(2 * i, h)
+        partial = d.to(torch.promote_types(embed.dtype, d.dtype)) if partial is None else partial + d
+        h = route(layer.mlp_res_query, layer.mlp_res_norm)
+        partial = partial + sublayer(2 * i + 1, h)
+    return route(model.final_res_query, model.final_res_norm)
+
+
 def forward_attn_res(model, embed: Tensor, mask: Optional[Tensor] = None) -> Tensor:
-    """Drop-in for ``LuxiaBaseModel._forward_attn_res`` (llama.py:666-716), forward only.
+    """Drop-in for ``LuxiaBaseModel._forward_attn_res`` (llama.py:666-716).
 
     ``model`` has the reference's attributes (``layers[i].attn``, ``attn_norm``,
     ``ffn``, ``ffn_norm``, the AttnRes queries and norms, ``final_res_*``,
     ``norm``, ``rope_cos/sin``, ``_attn_res_boundary_set``).  All AttnRes
     norms are built with the same ``config.norm_eps`` (llama.py:462,464,543),
-    so one eps serves every routing point.
+    so one eps serves every routing point.  Without autograd the routing
+    points run as fused block steps over one arena; when gradients are needed
+    (training) they run as differentiable list-based routing calls.
     """
-    ops.check_forward_only(embed)
-    router = _model_router(model)
     rope_cos, rope_sin = model.rope_cos, model.rope_sin
     layers = model.layers
 
@@ -153,15 +196,15 @@ def forward_attn_res(model, embed: Tensor, mask: Optional[Tensor] = None) -> Ten
             return layer.attn(layer.attn_norm(h), rope_cos, rope_sin, mask)
         return layer.ffn(layer.ffn_norm(h))
 
-    return model.norm(router.forward(embed, sublayer))
+    if _grad_needed(model, embed):
+        return model.norm(_route_points_autograd(model, embed, sublayer))
+    return model.norm(_model_router(model).forward(embed, sublayer))
 
 
 def forward_attn_res_cached(model, embed: Tensor, mask: Optional[Tensor] = None, past_kv=None):
     """Drop-in for ``_forward_attn_res_cached`` (llama.py:718-763): the KV-cache
     engine's forward (prefill, and T=1 decode steps), returning
-    ``(hidden, new_kv_list)``."""
-    ops.check_forward_only(embed)
-    router = _model_router(model)
+    ``(hidden, new_kv_list)``; differentiable like :func:`forward_attn_res`."""
     rope_cos, rope_sin = model.rope_cos, model.rope_sin
     layers = model.layers
     new_kv: list = []
@@ -176,5 +219,8 @@ def forward_attn_res_cached(model, embed: Tensor, mask: Optional[Tensor] = None,
             return out
         return layer.ffn(layer.ffn_norm(h))
 
-    x = router.forward(embed, sublayer)
+    if _grad_needed(model, embed):
+        x = _route_points_autograd(model, embed, sublayer)
+    else:
+        x = _model_router(model).forward(embed, sublayer)
     return model.norm(x), new_kv

@@ -109,3 +109,31 @@ def test_training_step_gradients_match_float64_reference(gpu):
         assert (got - want).abs().max().item() <= tol, f"{name}: max err {(got - want).abs().max().item():.3e}"
         checked += 1
     assert checked == len(list(m.parameters()))  # every parameter is upstream of the loss
+
+
+def test_stack_free_forward_trains_like_the_reference_loop(gpu):
+    # forward_attn_res under autograd (list-based routing, no stacks) against the
+    # reference's pad-and-stack loop in float64: loss and every parameter gradient
+    from oracle.torch_cpu_path import route_static_cpu
+
+    model = TinyModel(d=512, num_layers=4, boundaries=(1, 3), seed=23)
+    ref_model = copy.deepcopy(model).double()
+    g = torch.Generator().manual_seed(24)
+    embed = torch.randn((2, 16, 512), generator=g)
+    G = torch.randn((2, 16, 512), generator=g)
+    out_ref = _training_forward(ref_model, embed.double(),
+                                lambda buf, q, norm, mask, n: route_static_cpu(buf, q * norm.weight, norm.eps, mask))
+    (out_ref * G.double()).sum().backward()
+    m = model.to(gpu)
+    out = forward_attn_res(m, embed.to(gpu))
+    (out * G.to(gpu)).sum().backward()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.detach().double().cpu(), out_ref.detach(), rtol=2e-4, atol=2e-4)
+    for (name, p), (_, pr) in zip(m.named_parameters(), ref_model.named_parameters()):
+        got, want = p.grad.double().cpu(), pr.grad
+        tol = 2e-4 * want.abs().max().item() + 1e-7
+        assert (got - want).abs().max().item() <= tol, f"{name}: max err {(got - want).abs().max().item():.3e}"
+    # without autograd the same call takes the fused arena path and agrees
+    with torch.no_grad():
+        out2 = forward_attn_res(m, embed.to(gpu))
+    torch.testing.assert_close(out2, out.detach(), rtol=1e-5, atol=1e-5)
