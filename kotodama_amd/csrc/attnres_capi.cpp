@@ -59,7 +59,8 @@ constexpr int kRouteFuncs = kTypeCombos * kNumS * 2 * 2;
 constexpr int kMergeFuncs = 4 * 2;
 constexpr int kStreamMaxChunks = 8;  // rows of up to 8 KiB
 constexpr int kStreamWaves = 4;      // waves per workgroup of the streaming kernels
-constexpr int kStreamFuncs = kTypeCombos * 2 * kStreamMaxChunks * 2;  // combo x out dtype x KiB x fused
+// combo x out dtype x KiB x variant (plain / pointer table / fused)
+constexpr int kStreamFuncs = kTypeCombos * 2 * kStreamMaxChunks * 3;
 constexpr int kBwdFuncs = 4 * kNumS * 2;  // (source, grad_out) dtype pairs x S x V
 constexpr int kBwdMaxPerCu = 4;           // workgroups per CU the backward grid may use (workspace bound)
 constexpr size_t kBwdStaticLds = 2 * ATTNRES_KMAX_WAVES * 48 * sizeof(float);  // reduction buffer, S = 16
@@ -157,14 +158,17 @@ int find_function(DeviceState& st, int part, const char* name, hipFunction_t* f)
 
 int part_of_stream(int nch) { return nch <= 4 ? 2 : 1; }
 
-int get_stream(DeviceState& st, int combo, bool out_bf, int nch, bool fused, hipFunction_t* f, int* bpc) {
-  const int idx = ((combo * 2 + (out_bf ? 0 : 1)) * kStreamMaxChunks + (nch - 1)) * 2 + (fused ? 1 : 0);
+enum StreamVariant { kStreamPlain = 0, kStreamTable = 1, kStreamFused = 2 };
+const char* const kStreamVariantNames[3] = {"plain", "table", "fused"};
+
+int get_stream(DeviceState& st, int combo, bool out_bf, int nch, int variant, hipFunction_t* f, int* bpc) {
+  const int idx = ((combo * 2 + (out_bf ? 0 : 1)) * kStreamMaxChunks + (nch - 1)) * 3 + variant;
   std::lock_guard<std::mutex> lk(g_mu);
   if (!st.stream[idx]) {
     static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
     char name[96];
     snprintf(name, sizeof(name), "attnres_stream_%s_o%s_c%d_%s", combo_names[combo], out_bf ? "bf" : "f32", nch,
-             fused ? "fused" : "plain");
+             kStreamVariantNames[variant]);
     int rc = find_function(st, part_of_stream(nch), name, &st.stream[idx]);
     if (rc != ATTNRES_OK) return rc;
     int nb = 0;
@@ -345,8 +349,7 @@ RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int sr
   ch.combo = bf ? (param_dtype == ATTNRES_DTYPE_BF16 ? kBfDot2 : kBfFma) : kF32Fma;
   const int64_t row_bytes = (int64_t)hidden * esize(src_dtype);
   ch.nch = (int)(row_bytes / 1024);
-  // The streaming kernel addresses source s as src[0] + s*stride with 32-bit
-  // row/item counters.
+  // The streaming kernel uses 32-bit row/item counters.
   const bool stream_shape = num_queries == 1 && num_sources >= 1 && row_bytes % 1024 == 0 && ch.nch >= 1 &&
                             ch.nch <= kStreamMaxChunks && stream_ok &&
                             num_tokens * (int64_t)num_sources < (int64_t)1 << 31;
@@ -437,9 +440,11 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
     for (int s = 2; s < num_sources && equally_spaced; ++s)
       equally_spaced = (int64_t)((uintptr_t)sources[s] - (uintptr_t)sources[0]) == src_stride * s;
   }
-  // The streaming kernel shares one delta buffer between its two pipeline
-  // slots, which needs S >= 2 when accumulating into the partial.
-  const bool stream_ok = equally_spaced && !(mode == ATTNRES_MODE_ACCUM && num_sources < 2);
+  // The streaming kernel addresses equally spaced sources as base + s*stride
+  // and any others through the kernel-argument pointer table (stride 0); it
+  // shares one delta buffer between its two pipeline slots, which needs
+  // S >= 2 when accumulating into the partial.
+  const bool stream_ok = !(mode == ATTNRES_MODE_ACCUM && num_sources < 2);
   const RouteChoice ch =
       choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus, stream_ok);
   if (!ch.stream && ch.v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
@@ -449,7 +454,10 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   int block = ch.block;
   int64_t work_units = num_tokens;  // rows per workgroup-slot of the grid
   if (ch.stream) {
-    rc = get_stream(*st, ch.combo, out_dtype == ATTNRES_DTYPE_BF16, ch.nch, mode != ATTNRES_MODE_PLAIN, &f, &bpc);
+    const int variant = mode != ATTNRES_MODE_PLAIN ? kStreamFused
+                        : (equally_spaced || num_sources < 2) ? kStreamPlain
+                                                              : kStreamTable;
+    rc = get_stream(*st, ch.combo, out_dtype == ATTNRES_DTYPE_BF16, ch.nch, variant, &f, &bpc);
     if (rc != ATTNRES_OK) return rc;
     work_units = (num_tokens + kStreamWaves - 1) / kStreamWaves;
   } else {

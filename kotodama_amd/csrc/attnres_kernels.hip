@@ -781,7 +781,10 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
 
 #define ATTNRES_STREAM_WAVES 4
 
-template <int NCH, bool BF16, bool QDOT2, bool FUSED, bool OUTBF>
+// TBL: sources addressed through the kernel-argument pointer table (any
+// pointers) instead of base + s * stride (equally spaced: stacked buffers,
+// arenas).
+template <int NCH, bool BF16, bool QDOT2, bool FUSED, bool OUTBF, bool TBL>
 __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   const int S = P.num_sources;
   using C = Chunk<BF16>;
@@ -823,6 +826,13 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   const int mode = FUSED ? P.mode : ATTNRES_MODE_PLAIN;
   const uint64_t src0 = reinterpret_cast<uint64_t>(P.src[0]);
   const uint64_t src_stride = (uint64_t)P.src_stride;
+  // Sources that are not equally spaced are addressed through the pointer
+  // table of the kernel arguments, read with a scalar load at the
+  // wave-uniform source index (indexing the by-value parameter struct would
+  // copy it to scratch).
+  typedef const __attribute__((address_space(4))) uint64_t kptr_u64;
+  kptr_u64* src_tbl = (kptr_u64*)((const __attribute__((address_space(4))) char*)__builtin_amdgcn_kernarg_segment_ptr() +
+                                   offsetof(attnres_route_params, src));
   const uint64_t delta0 = reinterpret_cast<uint64_t>(P.delta);
 
   u32x4 bufA[NCH], bufB[NCH];
@@ -839,7 +849,14 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
     t = __builtin_amdgcn_readfirstlane(t);
     s = __builtin_amdgcn_readfirstlane(s);
     const bool from_delta = FUSED && s == (uint32_t)(S - 1) && mode == ATTNRES_MODE_SET;
-    const uint64_t base = from_delta ? delta0 : src0 + (uint64_t)s * src_stride;
+    uint64_t base;
+    if (from_delta) {
+      base = delta0;
+    } else if constexpr (TBL) {
+      base = src_tbl[s];
+    } else {
+      base = src0 + (uint64_t)s * src_stride;
+    }
     const char* row = uniform_ptr(base + (uint64_t)t * (from_delta ? delta_row_bytes : row_bytes));
 #if ATTNRES_LOAD_CPOL >= 0
     const __amdgpu_buffer_rsrc_t rr = row_rsrc(const_cast<char*>(row), (uint32_t)(NCH * 1024));
@@ -896,7 +913,8 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
         }
         // the updated partial row is written back (in a branch: an unconditional
         // write-back through an empty resource made these kernels spill)
-        char* prow = const_cast<char*>(uniform_ptr(src0 + (uint64_t)(S - 1) * src_stride + (uint64_t)t * row_bytes));
+        const uint64_t pbase = TBL ? src_tbl[S - 1] : src0 + (uint64_t)(S - 1) * src_stride;
+        char* prow = const_cast<char*>(uniform_ptr(pbase + (uint64_t)t * row_bytes));
         const __amdgpu_buffer_rsrc_t prsrc = row_rsrc(prow, (uint32_t)(NCH * 1024));
 #pragma unroll
         for (int c = 0; c < NCH; ++c) st_row(prsrc, (uint32_t)(c * 1024 + lane * 16), x[c]);
@@ -1641,12 +1659,17 @@ MERGE_V(2)
   extern "C" __global__ void __launch_bounds__(64 * ATTNRES_STREAM_WAVES)                               \
       __attribute__((amdgpu_waves_per_eu(STREAM_WAVES_PER_EU(NCH))))                                    \
       attnres_stream_##INNAME##_##QNAME##_o##ONAME##_c##NCH##_plain(attnres_route_params P) {           \
-    stream_body<NCH, BF, QD2, false, OBF>(P);                                                           \
+    stream_body<NCH, BF, QD2, false, OBF, false>(P);                                                    \
+  }                                                                                                     \
+  extern "C" __global__ void __launch_bounds__(64 * ATTNRES_STREAM_WAVES)                               \
+      __attribute__((amdgpu_waves_per_eu(STREAM_WAVES_PER_EU(NCH))))                                    \
+      attnres_stream_##INNAME##_##QNAME##_o##ONAME##_c##NCH##_table(attnres_route_params P) {           \
+    stream_body<NCH, BF, QD2, false, OBF, true>(P);                                                     \
   }                                                                                                     \
   extern "C" __global__ void __launch_bounds__(64 * ATTNRES_STREAM_WAVES)                               \
       __attribute__((amdgpu_waves_per_eu(STREAM_FUSED_WAVES_PER_EU(NCH))))                              \
       attnres_stream_##INNAME##_##QNAME##_o##ONAME##_c##NCH##_fused(attnres_route_params P) {           \
-    stream_body<NCH, BF, QD2, true, OBF>(P);                                                            \
+    stream_body<NCH, BF, QD2, true, OBF, false>(P);                                                     \
   }
 #define STREAM_ONE(INNAME, BF, QNAME, QD2, NCH)             \
   STREAM_ONE_OUT(INNAME, BF, QNAME, QD2, bf, true, NCH)     \

@@ -162,6 +162,24 @@ def test_route_static_non_prefix_mask_and_list_shim(gpu, policy):
     assert torch.equal(h, h2)
 
 
+def test_list_of_separate_allocations(gpu, policy):
+    # nine sources in separate allocations, passed in an order that is not
+    # equally spaced: the streaming family addresses them through its pointer table
+    d, n = 4096, 96
+    g = torch.Generator(device=gpu).manual_seed(17)
+    srcs = [(torch.randn((2, n // 2, d), generator=g, device=gpu) * (0.5 + 0.3 * i)).to(torch.bfloat16)
+            for i in range(9)]
+    order = [3, 0, 8, 1, 7, 2, 6, 4, 5]
+    lst = [srcs[i] for i in order]
+    query = (torch.randn(d, generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+    norm = Norm((1 + 0.1 * torch.randn(d, generator=g, device=gpu)).to(torch.bfloat16), 1e-5)
+    with torch.no_grad():
+        h = kotodama_amd.block_attn_res_from_list(lst, query, norm)
+    ref = O.route(np.stack([np64(t).reshape(-1, d) for t in lst]), fold(query, norm.weight, torch.bfloat16),
+                  1e-5)["out"][0]
+    check_bf16(h.reshape(-1, d), ref, "separate allocations")
+
+
 # ------------------------------------------------------- edge cases --
 
 
