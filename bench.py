@@ -17,7 +17,9 @@ Also on the JSON line:
   extrapolated to the full step.
 
 ``--workload cfg3|cfg4|cfg5`` measures the other shapes (cfg4 = 8B decode step,
-65 fused block steps captured in one HIP graph).  ``--pass bwd`` times the
+65 fused block steps captured in one HIP graph); ``cfg2serve`` the serving
+engine's two-phase routing at the 3B shape (batched phase 1 per block + phase-2
+merges: (S + Q) rows per phase-1 call, 3 rows per merge).  ``--pass bwd`` times the
 backward of the same routing calls instead (attnres_route_bwd on preallocated
 gradient buffers: (2S+1) * B*T*D * 2 algorithmic bytes per call — sources and
 dL/dout read, source gradients written).  ``--gpus`` above 1 exits: this
@@ -45,6 +47,8 @@ WORKLOAD_TEXT = {
     "cfg4": "8B decode step: T=1, B=256, D=4096, 65 fused block steps (S=1..9) in one HIP graph, bf16",
     "cfg5": "3B data-driven blocks {0,3,7,12,18,23}: D=3072, B=2, T=4096, 57 calls S=1..7 (sum S=267), BOS x20, bf16",
     "copy": "calibration: torch device copy of 1 GiB (bf16), the plain copy kernel that scales rocprof byte counters",
+    "cfg2serve": "3B serving two-phase routing (serve.py:113-164): 7 blocks of 8 sublayers, one batched phase-1 call "
+    "(Q=8, S=1..7) + 7 phase-2 merges per block, final phase 1 (S=8); D=3072, B=8, T=4096, bf16",
 }
 
 
@@ -163,6 +167,77 @@ def bench_sweep(w, steps: int, warmup: int, dev):
         elapsed = time.perf_counter() - t0
     dom_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in events)
     return elapsed, dominant, dom_ms, w.call_bytes(dominant)
+
+
+def bench_serve(steps: int, warmup: int, dev):
+    """cfg2serve: the routing calls of serve.py:113-164 at the 3B prefill shape.
+
+    Per block of sublayers: one batched phase-1 call over the committed blocks
+    for all its pseudo-queries, then a phase-2 merge for every sublayer after
+    the first; a final phase-1 call over all blocks.  The running partials fed
+    to the merges are synthetic rows generated up front (the sublayers
+    themselves are not part of the routing path), so the timed region holds
+    only the routing kernels.  Returns (elapsed, step_bytes, merge_ms,
+    merge_bytes, p1_ms, p1_bytes) with the per-launch averages of the merges
+    and of the deepest phase-1 call.
+    """
+    import torch
+
+    from kotodama_amd import ops, workloads
+
+    w = workloads.get("cfg2")
+    sched = w.schedule
+    n, d = w.tokens, w.hidden
+    row = n * d * w.elem_bytes
+    pool = workloads.make_pool(w, dev, seed=2)  # blocks: embed + committed summaries
+    blocks_all = [pool[i] for i in range(pool.shape[0])]
+    q, gn = workloads.make_params(w, dev, seed=2, count=sched.num_points)
+    pq = (q * gn).contiguous()  # folded in the parameter dtype, stacked [attn_0, mlp_0, ..., final]
+    bounds = [2 * b for b in sorted(sched.boundary_set)]
+    n_sub = 2 * sched.num_layers
+    ranges = [(st, bounds[i + 1] if i + 1 < len(bounds) else n_sub) for i, st in enumerate(bounds)]
+    partials = workloads.make_deltas(w, dev, 7, max(e - st for st, e in ranges))
+    step_bytes = 0
+    for k, (st, e) in enumerate(ranges):
+        step_bytes += (k + 1 + (e - st)) * row + (e - st - 1) * 3 * row
+    step_bytes += (len(ranges) + 2) * row  # final phase 1 over every block + the partial's block
+    deepest = len(ranges)  # S of the last block's phase-1 call
+
+    def step(ev_merge=None, ev_p1=None):
+        for k, (st, e) in enumerate(ranges):
+            blocks = blocks_all[: k + 1]
+            if ev_p1 is not None and k + 1 == deepest:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+            out, _, lse, _, _ = ops.route_list(blocks, pq[st:e], None, w.eps, torch.bfloat16, True, False)
+            if ev_p1 is not None and k + 1 == deepest:
+                e1.record()
+                ev_p1.append((e0, e1))
+            for qo in range(1, e - st):
+                if ev_merge is not None:
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                ops.merge(partials[qo - 1], pq[st + qo], out[qo], lse[qo], w.eps)
+                if ev_merge is not None:
+                    e1.record()
+                    ev_merge.append((e0, e1))
+        ops.route_list(blocks_all[: len(ranges) + 1], pq[-1:], None, w.eps, torch.bfloat16, True, False)
+
+    with torch.inference_mode():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        evm: list = []
+        evp: list = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(evm, evp)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    merge_ms = statistics.mean(a.elapsed_time(b) for a, b in evm)
+    p1_ms = statistics.mean(a.elapsed_time(b) for a, b in evp)
+    p1_q = ranges[-1][1] - ranges[-1][0]
+    return elapsed, step_bytes, merge_ms, 3 * row, p1_ms, (deepest + p1_q) * row
 
 
 def bwd_call_bytes(w, s: int) -> int:
@@ -305,6 +380,37 @@ def main() -> int:
         ms = elapsed * 1e3 / args.steps
         print(json.dumps({"workload": WORKLOAD_TEXT["copy"], "bytes_read": nbytes // 2, "bytes_written": nbytes // 2,
                           "ms_per_copy": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return 0
+    if args.workload == "cfg2serve":
+        elapsed, step_bytes, merge_ms, merge_bytes, p1_ms, p1_bytes = bench_serve(args.steps, args.warmup, dev)
+        ms_per_step = elapsed * 1e3 / args.steps
+        gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+        w2 = workloads.get("cfg2")
+        ach = merge_bytes / (merge_ms * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": "AttnRes serving two-phase routing achieved HBM GB/s",
+            "value": round(gbs, 2),
+            "unit": "GB/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms_per_step, 4),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "bf16",
+            "data": "synthetic (seeded blocks and partials, resident in HBM)",
+            "config": {"workload": WORKLOAD_TEXT["cfg2serve"], "algorithmic_bytes_per_step": step_bytes},
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(w2.tokens / (ms_per_step * 1e-3), 1),
+            "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "attnres_merge_bf_bf_v2 (phase-2 merge, 3 rows per token)",
+                         "algorithmic_bytes": merge_bytes, "avg_ms": round(merge_ms, 4)},
+            "phase1_deepest": {"kernel": "attnres_route_bf_d2_s7_v2_qn (Q=8)", "algorithmic_bytes": p1_bytes,
+                               "avg_ms": round(p1_ms, 4),
+                               "GB/s": round(p1_bytes / (p1_ms * 1e-3) / 1e9, 2)},
+        }), flush=True)
         return 0
     w = workloads.get(args.workload)
     roofline = None

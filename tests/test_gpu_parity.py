@@ -180,6 +180,23 @@ def test_list_of_separate_allocations(gpu, policy):
     check_bf16(h.reshape(-1, d), ref, "separate allocations")
 
 
+def test_batched_queries_wide_rows_fp32_queries(gpu):
+    # 8 fp32 queries at D=8192 (two chunks per thread): every query's output,
+    # lse, weights, logits and the shared inverse RMS must match
+    d, n, S, Q = 8192, 40, 5, 8
+    g = torch.Generator(device=gpu).manual_seed(19)
+    buf = torch.randn((S, 1, n, d), generator=g, device=gpu).to(torch.bfloat16)
+    qs = torch.randn((Q, d), generator=g, device=gpu) * 0.03
+    out, w, lse, inv, lg = ops.route(buf, S, qs, None, 1e-5, torch.bfloat16, True, True)
+    ref = O.route(np64(buf).reshape(S, n, d), np64(qs), 1e-5)
+    for q in range(Q):
+        check_bf16(out[q].reshape(n, d), ref["out"][q], f"query {q}")
+        check_weights(w[q].reshape(S, n), ref["weights"][q], f"weights {q}")
+        np.testing.assert_allclose(np64(lse[q]).reshape(n), ref["lse"][q], rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(np64(lg[q]).reshape(n, S), ref["logits"][q], rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(np64(inv).reshape(n, S), ref["inv_rms"], rtol=1e-5)
+
+
 # ------------------------------------------------------- edge cases --
 
 
