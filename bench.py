@@ -80,7 +80,7 @@ def load_traffic(kernel_tag: str):
         return None, None
 
 
-def kernel_name(s: int, tokens: int, hidden: int, dtype) -> str:
+def kernel_name(s: int, tokens: int, hidden: int, dtype, queries: int = 1) -> str:
     """The kernel symbol the library launches for one routing call of this shape."""
     import ctypes
 
@@ -89,7 +89,8 @@ def kernel_name(s: int, tokens: int, hidden: int, dtype) -> str:
     buf = ctypes.create_string_buffer(128)
     code = ops.dtype_code(dtype)
     _capi.check("attnres_route_kernel_name",
-                _capi.lib().attnres_route_kernel_name(s, tokens, hidden, code, code, code, 1, 0, buf, len(buf)))
+                _capi.lib().attnres_route_kernel_name(s, tokens, hidden, code, code, code, queries, 0, buf,
+                                                      len(buf)))
     return buf.value.decode()
 
 
@@ -407,7 +408,8 @@ def main() -> int:
                          "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                          "kernel": "attnres_merge_bf_bf_v2 (phase-2 merge, 3 rows per token)",
                          "algorithmic_bytes": merge_bytes, "avg_ms": round(merge_ms, 4)},
-            "phase1_deepest": {"kernel": "attnres_route_bf_d2_s7_v2_qn (Q=8)", "algorithmic_bytes": p1_bytes,
+            "phase1_deepest": {"kernel": kernel_name(7, w2.tokens, w2.hidden, w2.dtype, 8) + " (Q=8)",
+                               "algorithmic_bytes": p1_bytes,
                                "avg_ms": round(p1_ms, 4),
                                "GB/s": round(p1_bytes / (p1_ms * 1e-3) / 1e9, 2)},
         }), flush=True)

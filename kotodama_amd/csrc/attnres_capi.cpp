@@ -64,6 +64,7 @@ constexpr int kStreamFuncs = kTypeCombos * 2 * kStreamMaxChunks * 3;
 constexpr int kBwdFuncs = 4 * kNumS * 2;  // (source, grad_out) dtype pairs x S x V
 constexpr int kBwdMaxPerCu = 4;           // workgroups per CU the backward grid may use (workspace bound)
 constexpr size_t kBwdStaticLds = 2 * ATTNRES_KMAX_WAVES * 48 * sizeof(float);  // reduction buffer, S = 16
+constexpr size_t kQgStaticLds = 2 * ATTNRES_KMAX_WAVES * 72 * sizeof(float);   // batched-query reduction buffer
 
 struct DeviceState {
   std::atomic<bool> loaded{false};
@@ -73,6 +74,10 @@ struct DeviceState {
   hipFunction_t route[kRouteFuncs] = {};
   int route_bpc[kRouteFuncs] = {};  // resident workgroups per CU, for the launch block size used
   int route_bpc_block[kRouteFuncs] = {};
+  hipFunction_t route_qg[kNumS * 2] = {};  // batched-query kernels: S x V
+  int route_qg_bpc[kNumS * 2] = {};
+  int route_qg_block[kNumS * 2] = {};
+  size_t route_qg_lds[kNumS * 2] = {};
   hipFunction_t stream[kStreamFuncs] = {};
   int stream_bpc[kStreamFuncs] = {};
   hipFunction_t merge[kMergeFuncs] = {};
@@ -95,14 +100,16 @@ std::atomic<int> g_policy{ATTNRES_POLICY_AUTO};
 // Tuning knobs read once: ATTNRES_V forces chunks per thread (1 or 2) of the
 // row-per-workgroup kernels, ATTNRES_STREAM / ATTNRES_STREAM_MIN_TOKENS choose
 // when the row-per-wave streaming kernels run, ATTNRES_GRID_MULT scales the
-// resident-workgroup grid.
+// resident-workgroup grid, ATTNRES_QG=0 turns off the batched-query kernel.
 struct Tuning {
   int force_v = 0;
+  int qg = 1;
   int stream = -1;  // -1: by size, 0: never, 1: whenever the shape allows
   int64_t stream_min_tokens = 2048;
   double grid_mult = 1.0;
   Tuning() {
     if (const char* v = std::getenv("ATTNRES_V")) force_v = std::atoi(v);
+    if (const char* v = std::getenv("ATTNRES_QG")) qg = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_STREAM")) stream = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_STREAM_MIN_TOKENS")) stream_min_tokens = std::atoll(v);
     if (const char* g = std::getenv("ATTNRES_GRID_MULT")) {
@@ -202,6 +209,30 @@ int get_route(DeviceState& st, int combo, int s, int v, bool multiq, int block, 
   }
   *f = st.route[idx];
   *bpc = st.route_bpc[idx];
+  return ATTNRES_OK;
+}
+
+// Batched-query kernel (bf16 sources and parameters, Q >= 2) with `lds` bytes
+// of dynamic LDS for the staged queries.
+int get_route_qg(DeviceState& st, int s, int v, int block, size_t lds, hipFunction_t* f, int* bpc) {
+  const int idx = s * 2 + (v - 1);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!st.route_qg[idx]) {
+    char name[96];
+    snprintf(name, sizeof(name), "attnres_route_bf_d2_s%d_v%d_qg", s, v);
+    int rc = find_function(st, part_of_route(s), name, &st.route_qg[idx]);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  if (st.route_qg_block[idx] != block || st.route_qg_lds[idx] != lds) {
+    int nb = 0;
+    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.route_qg[idx], block, lds);
+    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    st.route_qg_bpc[idx] = nb > 0 ? nb : 1;
+    st.route_qg_block[idx] = block;
+    st.route_qg_lds[idx] = lds;
+  }
+  *f = st.route_qg[idx];
+  *bpc = st.route_qg_bpc[idx];
   return ATTNRES_OK;
 }
 
@@ -340,7 +371,18 @@ struct RouteChoice {
   int nch = 0;    // streaming: KiB per row
   int v = 0;      // workgroup: chunks per thread (0: no shape fits)
   int block = 0;  // threads per workgroup
+  size_t qg_lds = 0;  // > 0: the batched-query kernel, with this much dynamic LDS
 };
+
+// The batched-query kernel takes Q >= 2 queries over bf16 sources with bf16
+// parameters and a bf16 output, with the Q folded queries staged in LDS.
+void choose_qg(RouteChoice& ch, int num_sources, int num_queries, int hidden, int out_dtype, int mode, int max_lds) {
+  if (ch.stream || ch.v == 0 || ch.combo != kBfDot2 || num_queries < 2 || num_sources < 1 ||
+      out_dtype != ATTNRES_DTYPE_BF16 || mode != ATTNRES_MODE_PLAIN || tuning().qg == 0)
+    return;
+  const size_t lds = (size_t)num_queries * (size_t)(hidden / 8) * 16;
+  if (lds + kQgStaticLds <= (size_t)max_lds) ch.qg_lds = lds;
+}
 
 RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
                          int num_queries, int num_cus, bool stream_ok) {
@@ -374,7 +416,7 @@ void kernel_name_of(const RouteChoice& ch, int num_sources, int num_queries, boo
              fused ? "fused" : "plain");
   } else {
     snprintf(buf, n, "attnres_route_%s_s%d_v%d_%s", combo_names[ch.combo], num_sources, ch.v,
-             num_queries > 1 ? "qn" : "q1");
+             ch.qg_lds > 0 ? "qg" : num_queries > 1 ? "qn" : "q1");
   }
 }
 
@@ -445,9 +487,10 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   // shares one delta buffer between its two pipeline slots, which needs
   // S >= 2 when accumulating into the partial.
   const bool stream_ok = !(mode == ATTNRES_MODE_ACCUM && num_sources < 2);
-  const RouteChoice ch =
+  RouteChoice ch =
       choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus, stream_ok);
   if (!ch.stream && ch.v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
+  choose_qg(ch, num_sources, num_queries, hidden, out_dtype, mode, st->max_lds);
 
   hipFunction_t f = nullptr;
   int bpc = 1;
@@ -460,6 +503,9 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
     rc = get_stream(*st, ch.combo, out_dtype == ATTNRES_DTYPE_BF16, ch.nch, variant, &f, &bpc);
     if (rc != ATTNRES_OK) return rc;
     work_units = (num_tokens + kStreamWaves - 1) / kStreamWaves;
+  } else if (ch.qg_lds > 0) {
+    rc = get_route_qg(*st, num_sources, ch.v, block, ch.qg_lds, &f, &bpc);
+    if (rc != ATTNRES_OK) return rc;
   } else {
     rc = get_route(*st, ch.combo, num_sources, ch.v, num_queries > 1, block, &f, &bpc);
     if (rc != ATTNRES_OK) return rc;
@@ -492,7 +538,7 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   P.block = block;
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
-  return launch(f, grid_for(work_units, st->num_cus, bpc), block, P, stream);
+  return launch(f, grid_for(work_units, st->num_cus, bpc), block, P, stream, 1, ch.qg_lds);
 }
 
 // Query/gain gradients from `nparts` per-workgroup partial rows in
@@ -539,8 +585,10 @@ int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, i
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
-  const RouteChoice ch =
+  RouteChoice ch =
       choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus, true);
+  choose_qg(ch, num_sources, num_queries, hidden, out_dtype, fused ? ATTNRES_MODE_SET : ATTNRES_MODE_PLAIN,
+            st->max_lds);
   kernel_name_of(ch, num_sources, num_queries, fused != 0, out_dtype == ATTNRES_DTYPE_BF16, buf, (size_t)buf_len);
   return ATTNRES_OK;
 }

@@ -607,6 +607,204 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
   }
 }
 
+// ------------------------------------------------- batched-query body --
+//
+// Phase-1 batching for bf16 sources and bf16 parameters (the serving
+// engine's case): Q >= 2 pseudo-queries over one set of sources.  One
+// workgroup per token row, the S source chunks loaded once per row.  The Q
+// folded queries are staged in LDS once per workgroup (packed bf16).  Per
+// group of QG queries: sum(x^2) (first group only) and every x.qw with
+// v_dot2_f32_bf16, one DPP reduction round and one LDS exchange for the whole
+// group, the QG depth softmaxes (weights are wave-uniform), then the mixing
+// pass unpacks each source word once and accumulates all QG output rows from
+// it.  Compared with one query at a time this halves the VALU work of both
+// the dot and the mixing phases, which bound this kernel.
+
+// Queries per group: the partial sums of a group (S * (QG + 1)) and the
+// unpacked sources share the register file; beyond S = 5 a group of 8 drops
+// the kernel to two waves per SIMD, which measured slower than groups of 4.
+#define QG_OF(S) ((S) <= 5 ? 8 : (S) <= 12 ? 4 : 2)
+
+template <int S, int V>
+__device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
+  constexpr int VEC = 8;
+  constexpr int QG = QG_OF(S);
+  constexpr int NV = S * (QG + 1);
+  constexpr int RLD = ((NV + 3) / 4) * 4;
+  __shared__ float red[2][ATTNRES_KMAX_WAVES][RLD];
+  extern __shared__ u32x4 qg_lds[];  // [query][chunk] packed folded queries
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int block = P.block;
+  const int nwaves = (block + 63) >> 6;
+  const int nq = P.num_queries;
+  const int nchunk = P.nchunk;
+
+  int chunk[V];
+  bool ok[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    chunk[k] = tid + k * block;
+    ok[k] = chunk[k] < nchunk;
+  }
+
+  // ---- the batch's folded queries into LDS, once per workgroup ----
+  for (int i = tid; i < nq * nchunk; i += block) {
+    const int q = i / nchunk, c = i - q * nchunk;
+    float t[VEC];
+    load_qw<VEC>(P, q, c, t);
+    qg_lds[i] = u32x4{pack_bf16(t[0], t[1]), pack_bf16(t[2], t[3]), pack_bf16(t[4], t[5]), pack_bf16(t[6], t[7])};
+  }
+
+  const int64_t row_bytes_ld = P.src_ld * 2;
+  u32x4 x[S][V];
+  auto load_row = [&](int64_t t) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const char* row = reinterpret_cast<const char*>(P.src[s]) + t * row_bytes_ld;
+#pragma unroll
+      for (int k = 0; k < V; ++k) x[s][k] = ok[k] ? ldg_global<u32x4>(row + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
+    }
+  };
+  if ((int64_t)blockIdx.x < P.n_tokens) load_row(blockIdx.x);
+  __syncthreads();
+
+  int ph = 0;
+  for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
+    float inv[S];
+    for (int q0 = 0; q0 < nq; q0 += QG) {
+      const int ng = nq - q0 < QG ? nq - q0 : QG;
+
+      // ---- sum(x^2) and the group's x.qw, packed dot products ----
+      float part[NV];
+#pragma unroll
+      for (int j = 0; j < NV; ++j) part[j] = 0.f;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        if (!ok[k]) continue;
+        u32x4 qv[QG];
+#pragma unroll
+        for (int g = 0; g < QG; ++g) qv[g] = g < ng ? qg_lds[(q0 + g) * nchunk + chunk[k]] : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            if (q0 == 0) part[s] = dot2_bf16(x[s][k][w], x[s][k][w], part[s]);
+#pragma unroll
+            for (int g = 0; g < QG; ++g) part[S + g * S + s] = dot2_bf16(x[s][k][w], qv[g][w], part[S + g * S + s]);
+          }
+        }
+      }
+
+      // ---- one reduction round and one LDS exchange for the group ----
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        if (j >= S || q0 == 0) part[j] = wave_sum_to_lane63(part[j]);
+      }
+      if (lane == 63) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          if (j >= S || q0 == 0) red[ph][wave][j] = part[j];
+        }
+      }
+      __syncthreads();
+      float tot[NV];
+#pragma unroll
+      for (int j = 0; j < NV; ++j) tot[j] = 0.f;
+      for (int w = 0; w < nwaves; ++w) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          if (j >= S || q0 == 0) tot[j] += red[ph][w][j];
+        }
+      }
+      ph ^= 1;
+      if (q0 == 0) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) inv[s] = __builtin_amdgcn_rsqf(tot[s] * P.inv_d + P.eps);
+        if (tid == 0 && P.inv_rms) {
+#pragma unroll
+          for (int s = 0; s < S; ++s) P.inv_rms[tok * S + s] = inv[s];
+        }
+      }
+
+      // ---- the group's depth softmaxes (wave-uniform weights) ----
+      float wgt[QG][S];
+#pragma unroll
+      for (int g = 0; g < QG; ++g) {
+        float logit[S];
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          logit[s] = tot[S + g * S + s] * inv[s];
+          m = __builtin_fmaxf(m, logit[s]);
+        }
+        float sum = 0.f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          wgt[g][s] = __expf(logit[s] - m);
+          sum += wgt[g][s];
+        }
+        const float rsum = 1.0f / sum;
+#pragma unroll
+        for (int s = 0; s < S; ++s) wgt[g][s] = uniform_f32(wgt[g][s] * rsum);
+        if (g < ng && tid == 0) {
+          const int q = q0 + g;
+          if (P.weights) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) P.weights[((int64_t)q * S + s) * P.n_tokens + tok] = wgt[g][s];
+          }
+          if (P.lse) P.lse[(int64_t)q * P.n_tokens + tok] = m + __logf(sum);
+          if (P.logits) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) P.logits[((int64_t)q * P.n_tokens + tok) * S + s] = logit[s];
+          }
+        }
+      }
+
+      // ---- mixing: each source word unpacked once for all the group's rows ----
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) asm volatile("" : "+v"(x[s][k]));
+      }
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        if (!ok[k]) continue;
+        uint32_t ow[QG][4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          float xl[S], xh[S];
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            xl[s] = bf_lo(x[s][k][w]);
+            xh[s] = bf_hi(x[s][k][w]);
+          }
+#pragma unroll
+          for (int g = 0; g < QG; ++g) {
+            float lo = wgt[g][0] * xl[0], hi = wgt[g][0] * xh[0];
+#pragma unroll
+            for (int s = 1; s < S; ++s) {
+              lo = __builtin_fmaf(wgt[g][s], xl[s], lo);
+              hi = __builtin_fmaf(wgt[g][s], xh[s], hi);
+            }
+            ow[g][w] = pack_bf16(lo, hi);
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < QG; ++g) {
+          if (g >= ng) continue;
+          char* orow = reinterpret_cast<char*>(P.out) + ((int64_t)(q0 + g) * P.out_qstride + tok * P.out_ld) * 2;
+          st_row(row_rsrc(orow, (uint32_t)(P.d * 2)), (uint32_t)chunk[k] * 16,
+                 u32x4{ow[g][0], ow[g][1], ow[g][2], ow[g][3]});
+        }
+      }
+    }
+    if (tok + gridDim.x < P.n_tokens) load_row(tok + gridDim.x);
+  }
+}
+
 // ------------------------------------------------------------ merge body --
 
 // One VEC-element chunk of a bf16 (GBF) or fp32 row, packed as loaded.
@@ -1592,11 +1790,35 @@ __device__ __forceinline__ void reduce_dqw_body(const attnres_reduce_params& P) 
     route_body<S, V, BF, QD2, true>(P);                                                               \
   }
 
+// bf16 sources and parameters, Q >= 2, bf16 output: the batched-query body
+#define ROUTE_QG(S, V)                                                                                \
+  extern "C" __global__ void ROUTE_LB(V) attnres_route_bf_d2_s##S##_v##V##_qg(attnres_route_params P) { \
+    route_qg_body<S, V>(P);                                                                           \
+  }
 #define ROUTE_TYPES(S, V)                 \
   ROUTE_ONE(bf, true, d2, true, S, V)     \
   ROUTE_ONE(bf, true, fm, false, S, V)    \
-  ROUTE_ONE(f32, false, fm, false, S, V)
+  ROUTE_ONE(f32, false, fm, false, S, V)  \
+  ROUTE_QG_IF(S, V)
 
+#define ROUTE_QG_IF(S, V) ROUTE_QG_##S(V)
+#define ROUTE_QG_0(V)
+#define ROUTE_QG_1(V) ROUTE_QG(1, V)
+#define ROUTE_QG_2(V) ROUTE_QG(2, V)
+#define ROUTE_QG_3(V) ROUTE_QG(3, V)
+#define ROUTE_QG_4(V) ROUTE_QG(4, V)
+#define ROUTE_QG_5(V) ROUTE_QG(5, V)
+#define ROUTE_QG_6(V) ROUTE_QG(6, V)
+#define ROUTE_QG_7(V) ROUTE_QG(7, V)
+#define ROUTE_QG_8(V) ROUTE_QG(8, V)
+#define ROUTE_QG_9(V) ROUTE_QG(9, V)
+#define ROUTE_QG_10(V) ROUTE_QG(10, V)
+#define ROUTE_QG_11(V) ROUTE_QG(11, V)
+#define ROUTE_QG_12(V) ROUTE_QG(12, V)
+#define ROUTE_QG_13(V) ROUTE_QG(13, V)
+#define ROUTE_QG_14(V) ROUTE_QG(14, V)
+#define ROUTE_QG_15(V) ROUTE_QG(15, V)
+#define ROUTE_QG_16(V) ROUTE_QG(16, V)
 #define ROUTE_S(S) \
   ROUTE_TYPES(S, 1) \
   ROUTE_TYPES(S, 2)

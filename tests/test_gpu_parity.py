@@ -197,6 +197,63 @@ def test_batched_queries_wide_rows_fp32_queries(gpu):
     np.testing.assert_allclose(np64(inv).reshape(n, S), ref["inv_rms"], rtol=1e-5)
 
 
+def route_kernel(s, n, d, q):
+    import ctypes
+
+    buf = ctypes.create_string_buffer(128)
+    _capi.check("attnres_route_kernel_name", _capi.lib().attnres_route_kernel_name(s, n, d, 1, 1, 1, q, 0, buf, 128))
+    return buf.value.decode()
+
+
+@pytest.mark.parametrize("d,n,queries", [(1024, 24, (2, 9)), (8192, 12, (3, 8)), (3072, 600, (5,))])
+def test_batched_query_kernel_every_source_count(gpu, d, n, queries):
+    # bf16 folded queries (the serving engine's phase 1): the batched-query
+    # kernel, groups of 8/4/2 queries with a ragged last group, one chunk per
+    # thread (d=1024), two (d=8192; d=3072 with enough rows); every output
+    # against the oracle, and each query's row equal to a single-query call
+    g = torch.Generator(device=gpu).manual_seed(d + n)
+    for S in range(1, 17):
+        if d == 3072 and S not in (1, 6, 7, 13):
+            continue
+        scales = torch.exp(torch.empty(S, device=gpu).uniform_(math.log(0.2), math.log(5), generator=g))
+        buf = (torch.randn((S, n, d), generator=g, device=gpu) * scales.view(-1, 1, 1)).to(torch.bfloat16)
+        for Q in queries:
+            pq = (torch.randn((Q, d), generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+            name = route_kernel(S, n, d, Q)
+            assert name.endswith("_qg"), name
+            out, w, lse, inv, lg = ops.route(buf, S, pq, None, 1e-5, torch.bfloat16, True, True)
+            ref = O.route(np64(buf), np64(pq), 1e-5)
+            for q in range(Q):
+                label = f"S={S} Q={Q} q={q} {name}"
+                check_bf16(out[q], ref["out"][q], label)
+                check_weights(w[q], ref["weights"][q], label)
+                np.testing.assert_allclose(np64(lse[q]), ref["lse"][q], rtol=1e-5, atol=1e-5)
+                np.testing.assert_allclose(np64(lg[q]).reshape(n, S), ref["logits"][q], rtol=1e-4, atol=1e-4)
+            np.testing.assert_allclose(np64(inv).reshape(n, S), ref["inv_rms"], rtol=1e-5)
+            if n < 2 * 256:  # the single-query call runs the workgroup kernel with the same summation order
+                for q in (0, Q - 1):
+                    o1, w1, l1, _, _ = ops.route(buf, S, pq[q], None, 1e-5, torch.bfloat16, True, False)
+                    assert torch.equal(o1[0], out[q]) and torch.equal(w1[0], w[q]) and torch.equal(l1[0], lse[q])
+
+
+def test_batched_query_kernel_falls_back_past_lds(gpu):
+    # 11 queries of 8192 elements (176 KiB of staged queries) exceed one
+    # workgroup's LDS: the per-query kernel runs, with the same results
+    d, n, S, Q = 8192, 10, 4, 11
+    assert route_kernel(S, n, d, Q).endswith("_qn")
+    g = torch.Generator(device=gpu).manual_seed(23)
+    buf = torch.randn((S, n, d), generator=g, device=gpu).to(torch.bfloat16)
+    pq = (torch.randn((Q, d), generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+    out, w, lse, _, _ = ops.route(buf, S, pq, None, 1e-5, torch.bfloat16, True, False)
+    ref = O.route(np64(buf), np64(pq), 1e-5)
+    for q in range(Q):
+        check_bf16(out[q], ref["out"][q], f"fallback q={q}")
+        check_weights(w[q], ref["weights"][q], f"fallback q={q}")
+    o8, w8, _, _, _ = ops.route(buf, S, pq[:8], None, 1e-5, torch.bfloat16, True, False)
+    assert route_kernel(S, n, d, 8).endswith("_qg")
+    assert torch.equal(o8, out[:8]) and torch.equal(w8, w[:8])
+
+
 # ------------------------------------------------------- edge cases --
 
 
