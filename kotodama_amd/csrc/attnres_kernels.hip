@@ -613,25 +613,72 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
 // engine's case): Q >= 2 pseudo-queries over one set of sources.  One
 // workgroup per token row, the S source chunks loaded once per row.  The Q
 // folded queries are staged in LDS once per workgroup (packed bf16).  Per
-// group of QG queries: sum(x^2) (first group only) and every x.qw with
-// v_dot2_f32_bf16, one DPP reduction round and one LDS exchange for the whole
-// group, the QG depth softmaxes (weights are wave-uniform), then the mixing
-// pass unpacks each source word once and accumulates all QG output rows from
-// it.  Compared with one query at a time this halves the VALU work of both
-// the dot and the mixing phases, which bound this kernel.
+// group of QG queries:
+//  * sum(x^2) (once per row) and every x.qw with v_dot2_f32_bf16;
+//  * the NV partial sums are reduced over the wave by a transposing tree:
+//    v_permlane32_swap and v_permlane16_swap exchange half of the values
+//    between lane halves (one instruction moves two registers' halves), so
+//    each register carries four different values, one per 16-lane row, and
+//    four DPP steps finish the row sums: ~2.5 instructions per value instead
+//    of 6 for a full DPP reduction of each;
+//  * one LDS exchange and one barrier; lane g*P + s then sums value (g, s)
+//    over the waves and runs the QG depth softmaxes in parallel, P-lane
+//    segments reduced with DPP (max, sum);
+//  * the weights move to scalar registers (v_readlane) and the mixing pass
+//    unpacks each source word once for all QG output rows.
 
 // Queries per group: the partial sums of a group (S * (QG + 1)) and the
 // unpacked sources share the register file; beyond S = 5 a group of 8 drops
 // the kernel to two waves per SIMD, which measured slower than groups of 4.
 #define QG_OF(S) ((S) <= 5 ? 8 : (S) <= 12 ? 4 : 2)
 
+// Exchange lanes 32..63 of a with lanes 0..31 of b (v_permlane32_swap), and
+// the odd 16-lane rows of a with the even rows of b (v_permlane16_swap).  The
+// leading s_nop covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void swap_halves32(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap_rows16(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max(float v) {
+  const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false);
+  return __builtin_fmaxf(v, __builtin_bit_cast(float, t));
+}
+
+// Max / sum over aligned segments of SEG (8 or 16) lanes, result in every
+// lane of the segment: quad_perm[1,0,3,2], quad_perm[2,3,0,1],
+// row_half_mirror (8 lanes), row_mirror (16 lanes).
+template <int SEG>
+__device__ __forceinline__ float seg_max(float v) {
+  v = dpp_max<0xB1, 0xF>(v);
+  v = dpp_max<0x4E, 0xF>(v);
+  v = dpp_max<0x141, 0xF>(v);
+  if constexpr (SEG == 16) v = dpp_max<0x140, 0xF>(v);
+  return v;
+}
+template <int SEG>
+__device__ __forceinline__ float seg_sum(float v) {
+  v = dpp_add<0xB1, 0xF>(v);
+  v = dpp_add<0x4E, 0xF>(v);
+  v = dpp_add<0x141, 0xF>(v);
+  if constexpr (SEG == 16) v = dpp_add<0x140, 0xF>(v);
+  return v;
+}
+
 template <int S, int V>
 __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
   constexpr int VEC = 8;
   constexpr int QG = QG_OF(S);
-  constexpr int NV = S * (QG + 1);
-  constexpr int RLD = ((NV + 3) / 4) * 4;
-  __shared__ float red[2][ATTNRES_KMAX_WAVES][RLD];
+  constexpr int SEG = S <= 8 ? 8 : 16;      // lanes per query in the softmax
+  constexpr int NV = S * (QG + 1);          // sum(x^2) per source, then x.qw per (query, source)
+  constexpr int H2 = (NV + 3) / 4;          // registers after the two swap rounds
+  constexpr int H1 = 2 * H2;                // registers after the first
+  constexpr int NP = 4 * H2;                // NV padded to a multiple of 4
+  static_assert(QG * SEG <= 64 && NP <= 64, "one lane per (query, source) and per reduced value");
+  __shared__ float red[2][ATTNRES_KMAX_WAVES][64];
   extern __shared__ u32x4 qg_lds[];  // [query][chunk] packed folded queries
 
   const int tid = threadIdx.x;
@@ -642,12 +689,11 @@ __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
   const int nq = P.num_queries;
   const int nchunk = P.nchunk;
 
-  int chunk[V];
-  bool ok[V];
+  int chunk[V], qchunk[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     chunk[k] = tid + k * block;
-    ok[k] = chunk[k] < nchunk;
+    qchunk[k] = chunk[k] < nchunk ? chunk[k] : nchunk - 1;  // rows past the end hold zeros
   }
 
   // ---- the batch's folded queries into LDS, once per workgroup ----
@@ -658,109 +704,120 @@ __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
     qg_lds[i] = u32x4{pack_bf16(t[0], t[1]), pack_bf16(t[2], t[3]), pack_bf16(t[4], t[5]), pack_bf16(t[6], t[7])};
   }
 
+  // Source rows through buffer resources: a chunk past the row end reads 0.
   const int64_t row_bytes_ld = P.src_ld * 2;
   u32x4 x[S][V];
   auto load_row = [&](int64_t t) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const char* row = reinterpret_cast<const char*>(P.src[s]) + t * row_bytes_ld;
+      char* row = reinterpret_cast<char*>(const_cast<void*>(P.src[s])) + t * row_bytes_ld;
+      const __amdgpu_buffer_rsrc_t rs = row_rsrc(row, (uint32_t)(P.d * 2));
 #pragma unroll
-      for (int k = 0; k < V; ++k) x[s][k] = ok[k] ? ldg_global<u32x4>(row + (int64_t)chunk[k] * 16) : u32x4{0, 0, 0, 0};
+      for (int k = 0; k < V; ++k) x[s][k] = ld_row(rs, (uint32_t)chunk[k] * 16);
     }
   };
   if ((int64_t)blockIdx.x < P.n_tokens) load_row(blockIdx.x);
+
+  // The softmax lane of this thread: query g of the group, source s.
+  const int sg = lane / SEG, ss = lane % SEG;
+  const bool slot = ss < S && sg < QG;
+  // Where the reduced value of register j lands: row rho of the wave holds
+  // value j + (rho & 1) * H2 + (rho >> 1) * H1 after the two swap rounds.
+  const int rho = lane >> 4;
+  const int vbase = (rho & 1) * H2 + (rho >> 1) * H1;
   __syncthreads();
 
   int ph = 0;
   for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
-    float inv[S];
+    // sum(x^2) partials, once per row; every group reduces them again (the
+    // same values), which costs less than selecting them out of later groups
+    float ssp[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      ssp[s] = 0.f;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) ssp[s] = dot2_bf16(x[s][k][w], x[s][k][w], ssp[s]);
+      }
+    }
     for (int q0 = 0; q0 < nq; q0 += QG) {
       const int ng = nq - q0 < QG ? nq - q0 : QG;
 
-      // ---- sum(x^2) and the group's x.qw, packed dot products ----
-      float part[NV];
+      // ---- the group's x.qw, packed dot products ----
+      float part[NP];
 #pragma unroll
-      for (int j = 0; j < NV; ++j) part[j] = 0.f;
+      for (int j = 0; j < NP; ++j) part[j] = j < S ? ssp[j] : 0.f;
 #pragma unroll
       for (int k = 0; k < V; ++k) {
-        if (!ok[k]) continue;
         u32x4 qv[QG];
 #pragma unroll
-        for (int g = 0; g < QG; ++g) qv[g] = g < ng ? qg_lds[(q0 + g) * nchunk + chunk[k]] : u32x4{0, 0, 0, 0};
+        for (int g = 0; g < QG; ++g) {
+          const int q = q0 + g < nq ? q0 + g : nq - 1;  // a repeated query past the batch: weights unused
+          qv[g] = qg_lds[q * nchunk + qchunk[k]];
+        }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
-            if (q0 == 0) part[s] = dot2_bf16(x[s][k][w], x[s][k][w], part[s]);
 #pragma unroll
             for (int g = 0; g < QG; ++g) part[S + g * S + s] = dot2_bf16(x[s][k][w], qv[g][w], part[S + g * S + s]);
           }
         }
       }
 
-      // ---- one reduction round and one LDS exchange for the group ----
+      // ---- transposing wave reduction: swap rounds, then row sums ----
+      float r1[H1];
 #pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        if (j >= S || q0 == 0) part[j] = wave_sum_to_lane63(part[j]);
+      for (int j = 0; j < H1; ++j) {
+        float a = part[j], b = part[j + H1];
+        swap_halves32(a, b);
+        r1[j] = a + b;
       }
-      if (lane == 63) {
+      float r2[H2];
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-          if (j >= S || q0 == 0) red[ph][wave][j] = part[j];
-        }
+      for (int j = 0; j < H2; ++j) {
+        float a = r1[j], b = r1[j + H2];
+        swap_rows16(a, b);
+        r2[j] = a + b;
+      }
+#pragma unroll
+      for (int j = 0; j < H2; ++j) r2[j] = seg_sum<16>(r2[j]);
+      if ((lane & 15) == 0) {
+#pragma unroll
+        for (int j = 0; j < H2; ++j) red[ph][wave][vbase + j] = r2[j];
       }
       __syncthreads();
-      float tot[NV];
-#pragma unroll
-      for (int j = 0; j < NV; ++j) tot[j] = 0.f;
-      for (int w = 0; w < nwaves; ++w) {
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-          if (j >= S || q0 == 0) tot[j] += red[ph][w][j];
+
+      // ---- totals over the waves and the softmaxes, one lane per (query, source) ----
+      const int vi = S + sg * S + ss;
+      float dot = 0.f, sq = 0.f;
+      if (slot) {
+        for (int w = 0; w < nwaves; ++w) {
+          dot += red[ph][w][vi];
+          sq += red[ph][w][ss];
         }
       }
       ph ^= 1;
-      if (q0 == 0) {
-#pragma unroll
-        for (int s = 0; s < S; ++s) inv[s] = __builtin_amdgcn_rsqf(tot[s] * P.inv_d + P.eps);
-        if (tid == 0 && P.inv_rms) {
-#pragma unroll
-          for (int s = 0; s < S; ++s) P.inv_rms[tok * S + s] = inv[s];
-        }
+      const float inv = __builtin_amdgcn_rsqf(sq * P.inv_d + P.eps);
+      const float logit = slot ? dot * inv : -__builtin_inff();
+      const float m = seg_max<SEG>(logit);
+      const float e = slot ? __expf(logit - m) : 0.f;
+      const float sum = seg_sum<SEG>(e);
+      const float wl = e * (1.0f / sum);
+      if (wave == 0 && slot && sg < ng) {
+        const int q = q0 + sg;
+        if (P.weights) P.weights[((int64_t)q * S + ss) * P.n_tokens + tok] = wl;
+        if (P.logits) P.logits[((int64_t)q * P.n_tokens + tok) * S + ss] = logit;
+        if (P.lse && ss == 0) P.lse[(int64_t)q * P.n_tokens + tok] = m + __logf(sum);
+        if (P.inv_rms && q0 == 0 && sg == 0) P.inv_rms[tok * S + ss] = inv;
       }
-
-      // ---- the group's depth softmaxes (wave-uniform weights) ----
       float wgt[QG][S];
 #pragma unroll
       for (int g = 0; g < QG; ++g) {
-        float logit[S];
-        float m = -__builtin_inff();
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-          logit[s] = tot[S + g * S + s] * inv[s];
-          m = __builtin_fmaxf(m, logit[s]);
-        }
-        float sum = 0.f;
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          wgt[g][s] = __expf(logit[s] - m);
-          sum += wgt[g][s];
-        }
-        const float rsum = 1.0f / sum;
-#pragma unroll
-        for (int s = 0; s < S; ++s) wgt[g][s] = uniform_f32(wgt[g][s] * rsum);
-        if (g < ng && tid == 0) {
-          const int q = q0 + g;
-          if (P.weights) {
-#pragma unroll
-            for (int s = 0; s < S; ++s) P.weights[((int64_t)q * S + s) * P.n_tokens + tok] = wgt[g][s];
-          }
-          if (P.lse) P.lse[(int64_t)q * P.n_tokens + tok] = m + __logf(sum);
-          if (P.logits) {
-#pragma unroll
-            for (int s = 0; s < S; ++s) P.logits[((int64_t)q * P.n_tokens + tok) * S + s] = logit[s];
-          }
-        }
+        for (int s = 0; s < S; ++s)
+          wgt[g][s] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), g * SEG + s));
       }
 
       // ---- mixing: each source word unpacked once for all the group's rows ----
@@ -771,7 +828,6 @@ __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
       }
 #pragma unroll
       for (int k = 0; k < V; ++k) {
-        if (!ok[k]) continue;
         uint32_t ow[QG][4];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -792,6 +848,7 @@ __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
             ow[g][w] = pack_bf16(lo, hi);
           }
         }
+        // chunks past the row end fall outside the buffer range: the store is dropped
 #pragma unroll
         for (int g = 0; g < QG; ++g) {
           if (g >= ng) continue;
