@@ -86,6 +86,7 @@ def build(verbose: bool = False, out_dir: Path | None = None, defines: tuple = (
                 "-std=c++17",
                 "-Wall",
                 "-D__HIP_PLATFORM_AMD__",
+                *extra,
                 f"-I{INCLUDE}",
                 f"-I{CSRC}",
                 f"-I{ROCM / 'include'}",

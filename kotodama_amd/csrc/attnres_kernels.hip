@@ -668,6 +668,36 @@ __device__ __forceinline__ float seg_sum(float v) {
   return v;
 }
 
+// Sum over the 64 lanes of each of NP = 4*H2 values part[0..NP), written to
+// red_row[v] for every v < NP by the first lane of each 16-lane row.  Two
+// swap rounds leave register j of row rho holding value
+// j + (rho & 1) * H2 + (rho >> 1) * 2 * H2 (summed over 4 lanes); four DPP
+// steps finish the 16-lane row sums.
+template <int H2>
+__device__ __forceinline__ void wave_reduce_to_lds(float (&part)[4 * H2], float* red_row, int lane) {
+  constexpr int H1 = 2 * H2;
+  float r1[H1];
+#pragma unroll
+  for (int j = 0; j < H1; ++j) {
+    float a = part[j], b = part[j + H1];
+    swap_halves32(a, b);
+    r1[j] = a + b;
+  }
+  float r2[H2];
+#pragma unroll
+  for (int j = 0; j < H2; ++j) {
+    float a = r1[j], b = r1[j + H2];
+    swap_rows16(a, b);
+    r2[j] = seg_sum<16>(a + b);
+  }
+  const int rho = lane >> 4;
+  if ((lane & 15) == 0) {
+    float* dst = red_row + (rho & 1) * H2 + (rho >> 1) * H1;
+#pragma unroll
+    for (int j = 0; j < H2; ++j) dst[j] = r2[j];
+  }
+}
+
 template <int S, int V>
 __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
   constexpr int VEC = 8;
@@ -675,7 +705,6 @@ __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
   constexpr int SEG = S <= 8 ? 8 : 16;      // lanes per query in the softmax
   constexpr int NV = S * (QG + 1);          // sum(x^2) per source, then x.qw per (query, source)
   constexpr int H2 = (NV + 3) / 4;          // registers after the two swap rounds
-  constexpr int H1 = 2 * H2;                // registers after the first
   constexpr int NP = 4 * H2;                // NV padded to a multiple of 4
   static_assert(QG * SEG <= 64 && NP <= 64, "one lane per (query, source) and per reduced value");
   __shared__ float red[2][ATTNRES_KMAX_WAVES][64];
@@ -721,10 +750,6 @@ __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
   // The softmax lane of this thread: query g of the group, source s.
   const int sg = lane / SEG, ss = lane % SEG;
   const bool slot = ss < S && sg < QG;
-  // Where the reduced value of register j lands: row rho of the wave holds
-  // value j + (rho & 1) * H2 + (rho >> 1) * H1 after the two swap rounds.
-  const int rho = lane >> 4;
-  const int vbase = (rho & 1) * H2 + (rho >> 1) * H1;
   __syncthreads();
 
   int ph = 0;
@@ -766,27 +791,8 @@ __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
         }
       }
 
-      // ---- transposing wave reduction: swap rounds, then row sums ----
-      float r1[H1];
-#pragma unroll
-      for (int j = 0; j < H1; ++j) {
-        float a = part[j], b = part[j + H1];
-        swap_halves32(a, b);
-        r1[j] = a + b;
-      }
-      float r2[H2];
-#pragma unroll
-      for (int j = 0; j < H2; ++j) {
-        float a = r1[j], b = r1[j + H2];
-        swap_rows16(a, b);
-        r2[j] = a + b;
-      }
-#pragma unroll
-      for (int j = 0; j < H2; ++j) r2[j] = seg_sum<16>(r2[j]);
-      if ((lane & 15) == 0) {
-#pragma unroll
-        for (int j = 0; j < H2; ++j) red[ph][wave][vbase + j] = r2[j];
-      }
+      // ---- transposing wave reduction, one LDS exchange ----
+      wave_reduce_to_lds<H2>(part, red[ph][wave], lane);
       __syncthreads();
 
       // ---- totals over the waves and the softmaxes, one lane per (query, source) ----
@@ -1362,9 +1368,11 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
   using C = Chunk<BF16>;
   constexpr int VEC = C::VEC;
   using GC = PackedChunk<VEC, GBF>;
-  constexpr int NV = 3 * S;
-  constexpr int RLD = ((NV + 3) / 4) * 4;
-  __shared__ float red[2][ATTNRES_KMAX_WAVES][RLD];
+  constexpr int NV = 3 * S;             // sum(x^2), x.qw, x.G per source
+  constexpr int H2 = (NV + 3) / 4;
+  constexpr int NP = 4 * H2;
+  constexpr int SEG = S <= 8 ? 8 : 16;  // lanes of the softmax
+  __shared__ float red[2][ATTNRES_KMAX_WAVES][NP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1457,9 +1465,9 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
   if (tok < P.n_tokens) load_row(tok);
   for (; tok < P.n_tokens; tok += gridDim.x) {
     // ---- sum(x^2), x.qw, x.G per source ----
-    float part[NV];
+    float part[NP];
 #pragma unroll
-    for (int j = 0; j < NV; ++j) part[j] = 0.f;
+    for (int j = 0; j < NP; ++j) part[j] = 0.f;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
       float q[VEC];
@@ -1475,54 +1483,38 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
         }
       }
     }
-#pragma unroll
-    for (int j = 0; j < NV; ++j) part[j] = wave_sum_to_lane63(part[j]);
-    if (lane == 63) {
-#pragma unroll
-      for (int j = 0; j < NV; ++j) red[ph][wave][j] = part[j];
-    }
+    // ---- transposing wave reduction, one LDS exchange ----
+    wave_reduce_to_lds<H2>(part, red[ph][wave], lane);
     __syncthreads();
-    float tot[NV];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) tot[j] = 0.f;
-    for (int w = 0; w < nwaves; ++w) {
-#pragma unroll
-      for (int j = 0; j < NV; ++j) tot[j] += red[ph][w][j];
+
+    // ---- softmax recomputed and the coefficients of dx, lane s per source ----
+    const int ls = lane % SEG;
+    const bool slot = ls < S;
+    float t_ss = 0.f, t_dot = 0.f, t_gx = 0.f;
+    if (slot) {
+      for (int w = 0; w < nwaves; ++w) {
+        t_ss += red[ph][w][ls];
+        t_dot += red[ph][w][S + ls];
+        t_gx += red[ph][w][2 * S + ls];
+      }
     }
     ph ^= 1;
-
-    // ---- softmax recomputed, then the coefficients of dx ----
-    float r[S], l[S], wgt[S];
-    float m = -__builtin_inff();
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      r[s] = __builtin_amdgcn_rsqf(tot[s] * P.inv_d + P.eps);
-      l[s] = tot[S + s] * r[s];
-      m = __builtin_fmaxf(m, l[s]);
-    }
-    float sum = 0.f;
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      wgt[s] = __expf(l[s] - m);
-      sum += wgt[s];
-    }
-    const float rsum = 1.0f / sum;
-    float go = 0.f;  // G . out = sum_s w_s (G . x_s)
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      wgt[s] *= rsum;
-      go = __builtin_fmaf(wgt[s], tot[2 * S + s], go);
-    }
+    const float rl = __builtin_amdgcn_rsqf(t_ss * P.inv_d + P.eps);
+    const float ll = slot ? t_dot * rl : -__builtin_inff();
+    const float m = seg_max<SEG>(ll);
+    const float el = slot ? __expf(ll - m) : 0.f;
+    const float wl = el * (1.0f / seg_sum<SEG>(el));
+    const float go = seg_sum<SEG>(wl * t_gx);  // G . out = sum_s w_s (G . x_s)
     const float glse = P.grad_lse != nullptr ? P.grad_lse[tok] : 0.f;
-    // The coefficients are the same in every lane: keep them in SGPRs.
-    float c1[S], c2[S];
+    const float c1l = wl * (glse + t_gx - go) * rl;
+    const float c2l = -c1l * ll * rl * P.inv_d;
+    // The coefficients are the same in every lane: scalar registers.
+    float c1[S], c2[S], wgt[S];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const float dl = wgt[s] * (glse + tot[2 * S + s] - go);
-      c1[s] = dl * r[s];
-      c2[s] = uniform_f32(-c1[s] * l[s] * r[s] * P.inv_d);
-      c1[s] = uniform_f32(c1[s]);
-      wgt[s] = uniform_f32(wgt[s]);
+      wgt[s] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), s));
+      c1[s] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c1l), s));
+      c2[s] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c2l), s));
     }
 
     // ---- keep this row, start loading the next one ----
