@@ -1,0 +1,144 @@
+"""Row strides through the C ABI (GPU).
+
+A caller binding ``attnres_route_fwd`` / ``attnres_route_bwd`` directly may
+pass rows of wider buffers: ``src_ld``, ``out_ld`` and ``out_qstride`` (forward),
+``grad_out_ld`` and ``grad_ld`` (backward) in elements.  Each case routes rows
+that sit inside a canary-filled buffer and checks the results against the
+float64 oracle and that no byte outside the rows was written.  The cases cover
+every kernel family the host can pick: the row-per-workgroup kernel (few rows),
+the streaming kernel (both its base+stride and pointer-table addressing), the
+batched-query kernel (bf16 queries) and the per-query kernel (fp32 queries),
+bf16 and fp32.  Tolerances as in test_gpu_parity / test_gpu_backward.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from kotodama_amd import _capi
+from oracle import attnres_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+CANARY = 7.0  # exact in bf16; no routed value here equals it
+
+
+def np64(t):
+    return t.detach().float().cpu().double().numpy()
+
+
+def bf16_ulp(x):
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0**-126)))
+    return 2.0 ** (e - 7)
+
+
+def check_out(out, ref, dtype, label):
+    got = np64(out)
+    err = np.abs(got - ref)
+    if dtype == torch.float32:
+        tol = 1e-5 * np.abs(ref) + 1e-6 * np.abs(ref).max()
+    else:
+        tol = np.maximum(2e-2, bf16_ulp(ref))
+    assert (err <= tol).all(), f"{label}: worst err {err.max():.3e}"
+
+
+def code(dtype):
+    return _capi.DTYPE_BF16 if dtype == torch.bfloat16 else _capi.DTYPE_F32
+
+
+def kernel_name(s, n, d, src, par, out, q):
+    buf = ctypes.create_string_buffer(128)
+    _capi.check("attnres_route_kernel_name",
+                _capi.lib().attnres_route_kernel_name(s, n, d, code(src), code(par), code(out), q, 0, buf, 128))
+    return buf.value.decode()
+
+
+# (label, S, n, d, source dtype, query dtype, Q, separate allocations, expected kernel suffix)
+FWD_CASES = [
+    ("workgroup-bf16", 5, 96, 3072, torch.bfloat16, torch.bfloat16, 1, False, "_q1"),
+    ("workgroup-f32", 3, 40, 1024, torch.float32, torch.float32, 1, False, "_q1"),
+    ("stream-plain", 4, 4096, 2048, torch.bfloat16, torch.bfloat16, 1, False, "_plain"),
+    ("stream-table", 4, 4096, 2048, torch.bfloat16, torch.bfloat16, 1, True, "_plain"),
+    ("batched-bf16", 6, 64, 1024, torch.bfloat16, torch.bfloat16, 5, False, "_qg"),
+    ("per-query-f32q", 3, 64, 1024, torch.bfloat16, torch.float32, 3, False, "_qn"),
+]
+
+
+@pytest.mark.parametrize("label,S,n,d,sdt,qdt,Q,separate,suffix", FWD_CASES, ids=[c[0] for c in FWD_CASES])
+def test_route_fwd_row_strides(gpu, label, S, n, d, sdt, qdt, Q, separate, suffix):
+    # the kernel-name query reports the plain variant for the pointer table's shape too:
+    # the table is chosen at launch from the source addresses
+    assert kernel_name(S, n, d, sdt, qdt, sdt, Q).endswith(suffix)
+    g = torch.Generator(device=gpu).manual_seed(n + d + Q)
+    src_ld, out_ld = d + 64, d + 32
+    es = 2 if sdt == torch.bfloat16 else 4
+    if separate:  # one allocation per source, in an order that is not equally spaced
+        bufs = [torch.full((n, src_ld), CANARY, device=gpu, dtype=sdt) for _ in range(S + 2)]
+        rows = [bufs[i] for i in (2, 0, 4, 1)][:S]
+    else:
+        big = torch.full((S, n, src_ld), CANARY, device=gpu, dtype=sdt)
+        rows = [big[s] for s in range(S)]
+    for s, r in enumerate(rows):
+        r[:, :d] = (torch.randn((n, d), generator=g, device=gpu) * (0.5 + s)).to(sdt)
+    qs = (torch.randn((Q, d), generator=g, device=gpu) * 0.05).to(qdt)
+    qstride = n * out_ld + 64
+    obuf = torch.full(((Q - 1) * qstride + n * out_ld,), CANARY, device=gpu, dtype=sdt)
+    weights = torch.full((Q, S, n), CANARY, device=gpu)
+    lse = torch.full((Q, n), CANARY, device=gpu)
+    srcs_before = [r.clone() for r in rows]
+    _capi.route_fwd(
+        _capi.pointer_array([r.data_ptr() for r in rows]), S, n, d, src_ld, code(sdt), qs.data_ptr(), None, Q,
+        code(qdt), 1e-5, obuf.data_ptr(), code(sdt), out_ld, qstride, weights.data_ptr(), lse.data_ptr(), None,
+        None, torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize()
+    ref = O.route(np.stack([np64(r[:, :d]) for r in rows]), np64(qs), 1e-5)
+    for q in range(Q):
+        view = obuf[q * qstride: q * qstride + n * out_ld].view(n, out_ld)
+        check_out(view[:, :d], ref["out"][q], sdt, f"{label} q={q}")
+        assert torch.all(view[:, d:] == CANARY), f"{label}: output row padding written"
+        if q + 1 < Q:
+            assert torch.all(obuf[q * qstride + n * out_ld: (q + 1) * qstride] == CANARY), f"{label}: gap written"
+        assert np.abs(np64(weights[q]) - ref["weights"][q]).max() <= 1e-5
+        np.testing.assert_allclose(np64(lse[q]), ref["lse"][q], rtol=1e-5, atol=1e-5)
+    for a, b in zip(rows, srcs_before):
+        assert torch.equal(a, b), f"{label}: a source was modified"
+
+
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+@pytest.mark.parametrize("S", [3, 6])
+def test_route_bwd_row_strides(gpu, sdt, S):
+    n, d = 300, 2048
+    src_ld, gout_ld, grad_ld = d + 64, d + 128, d + 32
+    g = torch.Generator(device=gpu).manual_seed(S * 7 + (sdt == torch.float32))
+    big = torch.full((S, n, src_ld), CANARY, device=gpu, dtype=sdt)
+    for s in range(S):
+        big[s, :, :d] = (torch.randn((n, d), generator=g, device=gpu) * (0.5 + s)).to(sdt)
+    qdt = sdt
+    q = (torch.randn(d, generator=g, device=gpu) * 0.05).to(qdt)
+    gbuf = torch.full((n, gout_ld), CANARY, device=gpu, dtype=sdt)
+    gbuf[:, :d] = torch.randn((n, d), generator=g, device=gpu).to(sdt)
+    glse = torch.randn(n, generator=g, device=gpu) * 0.1
+    dbig = torch.full((S, n, grad_ld), CANARY, device=gpu, dtype=sdt)
+    ws = torch.empty(_capi.route_bwd_workspace_size(n, d) // 4, device=gpu)
+    dq = torch.empty(d, device=gpu, dtype=qdt)
+    _capi.route_bwd(
+        _capi.pointer_array([big[s].data_ptr() for s in range(S)]), S, n, d, src_ld, code(sdt), q.data_ptr(), None,
+        code(qdt), 1e-5, gbuf.data_ptr(), code(sdt), gout_ld, glse.data_ptr(),
+        _capi.pointer_array([dbig[s].data_ptr() for s in range(S)]), grad_ld, ws.data_ptr(), ws.numel() * 4,
+        dq.data_ptr(), None, torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize()
+    ref = O.route_backward(np64(big[:, :, :d]), np64(q), 1e-5, np64(gbuf[:, :d]), np64(glse))
+    got = np64(dbig[:, :, :d])
+    scale = np.abs(ref["dx"]).max()
+    if sdt == torch.float32:
+        tol = 1e-4 * np.abs(ref["dx"]) + 1e-5 * scale
+    else:
+        tol = bf16_ulp(ref["dx"]) + 1e-3 * scale
+    assert (np.abs(got - ref["dx"]) <= tol).all(), f"dx worst err {np.abs(got - ref['dx']).max():.3e}"
+    assert torch.all(dbig[:, :, d:] == CANARY), "gradient row padding written"
+    dqr = ref["dqw"]
+    tq = 1e-4 * np.abs(dqr) + 1e-5 * np.abs(dqr).max() if qdt == torch.float32 else \
+        bf16_ulp(dqr) + 1e-3 * np.abs(dqr).max()
+    assert (np.abs(np64(dq) - dqr) <= tq).all(), "query gradient"
