@@ -150,15 +150,15 @@ def bench_sweep(w, steps: int, warmup: int, dev):
                 e0 = torch.cuda.Event(enable_timing=True)
                 e1 = torch.cuda.Event(enable_timing=True)
                 e0.record()
-                ops.route(pool, s, q[j], gn[j], w.eps, w.dtype, False, False)
+                ops.route_call(pool, s, q[j], gn[j], w.eps, w.dtype)
                 e1.record()
                 events.append((e0, e1))
             else:
-                ops.route(pool, s, q[j], gn[j], w.eps, w.dtype, False, False)
+                ops.route_call(pool, s, q[j], gn[j], w.eps, w.dtype)
 
     with torch.inference_mode():
-        for _ in range(warmup):
-            step()
+        for _ in range(warmup):  # the same calls as the timed steps, event records included
+            step([])
         torch.cuda.synchronize()
         events: list = []
         t0 = time.perf_counter()
@@ -210,7 +210,7 @@ def bench_serve(steps: int, warmup: int, dev):
             if ev_p1 is not None and k + 1 == deepest:
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
-            out, _, lse, _, _ = ops.route_list(blocks, pq[st:e], None, w.eps, torch.bfloat16, True, False)
+            out, _, lse, _, _ = ops.route_list_call(blocks, pq[st:e], None, w.eps, torch.bfloat16, True)
             if ev_p1 is not None and k + 1 == deepest:
                 e1.record()
                 ev_p1.append((e0, e1))
@@ -218,15 +218,15 @@ def bench_serve(steps: int, warmup: int, dev):
                 if ev_merge is not None:
                     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                     e0.record()
-                ops.merge(partials[qo - 1], pq[st + qo], out[qo], lse[qo], w.eps)
+                ops.merge_call(partials[qo - 1], pq[st + qo], out[qo], lse[qo], w.eps)
                 if ev_merge is not None:
                     e1.record()
                     ev_merge.append((e0, e1))
-        ops.route_list(blocks_all[: len(ranges) + 1], pq[-1:], None, w.eps, torch.bfloat16, True, False)
+        ops.route_list_call(blocks_all[: len(ranges) + 1], pq[-1:], None, w.eps, torch.bfloat16, True)
 
     with torch.inference_mode():
-        for _ in range(warmup):
-            step()
+        for _ in range(warmup):  # the same calls as the timed steps, event records included
+            step([], [])
         torch.cuda.synchronize()
         evm: list = []
         evp: list = []
@@ -287,8 +287,8 @@ def bench_backward(w, steps: int, warmup: int, dev):
             else:
                 _capi.route_bwd(*a)
 
-    for _ in range(warmup):
-        step()
+    for _ in range(warmup):  # the same calls as the timed steps, event records included
+        step([])
     torch.cuda.synchronize()
     events: list = []
     t0 = time.perf_counter()
@@ -324,8 +324,12 @@ def bench_decode(w, steps: int, warmup: int, dev):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             router.forward(embed, lambda j, h: deltas[j], arena=arena)
-        for _ in range(warmup):
+        for _ in range(warmup):  # as the timed steps, event records included
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
             graph.replay()
+            e1.record()
         torch.cuda.synchronize()
         events = []
         t0 = time.perf_counter()

@@ -161,7 +161,7 @@ def _route_points_autograd(model, embed: Tensor, sublayer: Callable[[int, Tensor
     def route(query: Tensor, norm) -> Tensor:
         gain = norm.weight
         out_dtype = torch.promote_types(embed.dtype, torch.promote_types(query.dtype, gain.dtype))
-        return ops.route_list(committed + [partial], query, gain, float(norm.eps), out_dtype, False, False)[0][0]
+        return ops.route_list_call(committed + [partial], query, gain, float(norm.eps), out_dtype)[0][0]
 
     boundaries = model._attn_res_boundary_set
     for i, layer in enumerate(model.layers):

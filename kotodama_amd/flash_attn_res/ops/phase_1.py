@@ -39,7 +39,7 @@ def phase_1_batched_attention_forward_with_aux(
     reference leaves them unwritten).
     """
     s_total = block_representations.shape[0]
-    out, _, lse, inv_rms, logits = ops.route(
+    out, _, lse, inv_rms, logits = ops.route_call(
         block_representations, int(num_active), pseudo_queries, None, float(eps), torch.bfloat16, True, True
     )
     if num_active < s_total:
@@ -58,8 +58,8 @@ def phase_1_batched_attention(
     """(out (Q, B, T, D) bf16, lse (Q, B, T) fp32) — ops/phase_1.py:69-85."""
     if num_active is None:
         num_active = block_representations.shape[0]
-    out, _, lse, _, _ = ops.route(
-        block_representations, int(num_active), pseudo_queries, None, float(eps), torch.bfloat16, True, False
+    out, _, lse, _, _ = ops.route_call(
+        block_representations, int(num_active), pseudo_queries, None, float(eps), torch.bfloat16, True
     )
     return out, lse
 

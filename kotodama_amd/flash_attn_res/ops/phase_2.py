@@ -40,9 +40,7 @@ def phase_2_online_softmax_merge(
     eps: float,
 ) -> Tensor:
     """Merged routing output (B, T, D) — ops/phase_2.py:8-24."""
-    return phase_2_online_softmax_merge_forward_with_aux(
-        intrablock_partial_sum, pseudo_query, interblock_normalized_output, interblock_lse, eps
-    )[0]
+    return ops.merge_call(intrablock_partial_sum, pseudo_query, interblock_normalized_output, interblock_lse, float(eps))
 
 
 # The reference's name for the same entry point (ops/phase_2.py:8).

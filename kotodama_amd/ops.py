@@ -95,7 +95,7 @@ class _DeviceStream:
         if cur != idx:
             self.prev = cur
             torch.cuda.set_device(idx)
-        return torch.cuda.current_stream(idx).cuda_stream
+        return torch._C._cuda_getCurrentRawStream(idx)
 
     def __exit__(self, *exc) -> None:
         if self.prev is not None:
@@ -127,10 +127,15 @@ def _outputs(
     d: int,
     want_weights: bool,
     want_aux: bool,
-) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    placeholders: bool = True,
+) -> tuple:
     f32 = torch.float32
-    # every returned tensor is its own allocation: custom ops may not return aliases
+    # every returned tensor is its own allocation: custom ops may not return
+    # aliases.  Without placeholders (the dispatcher-free eager path) outputs
+    # that were not requested are None.
     def alloc(shape, wanted):
+        if not wanted and not placeholders:
+            return None
         return torch.empty(shape if wanted else (0,), device=device, dtype=f32)
 
     out = torch.empty((nq, *batch, d), device=device, dtype=out_dtype)
@@ -154,7 +159,8 @@ def _launch_route(
     out_dtype: torch.dtype,
     want_weights: bool,
     want_aux: bool,
-) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    placeholders: bool = True,
+) -> tuple:
     if query.dim() == 1:
         query = query.unsqueeze(0)
     if query.dim() != 2 or query.shape[1] != d:
@@ -167,11 +173,11 @@ def _launch_route(
     n = 1
     for b in batch:
         n *= b
-    outs = _outputs(device, out_dtype, nq, s, batch, d, want_weights, want_aux)
+    outs = _outputs(device, out_dtype, nq, s, batch, d, want_weights, want_aux, placeholders)
     out, weights, lse, inv_rms, logits = outs
 
-    def p(t: Tensor) -> Optional[int]:
-        return t.data_ptr() if t.numel() else None
+    def p(t: Optional[Tensor]) -> Optional[int]:
+        return t.data_ptr() if t is not None and t.numel() else None
 
     with _DeviceStream(device) as stream:
         _capi.route_fwd(
@@ -202,17 +208,7 @@ def _launch_route(
 # ------------------------------------------------------------------ route --
 
 
-@torch.library.custom_op("attnres_hip::route", mutates_args=())
-def route(
-    buf: Tensor,
-    num_sources: int,
-    query: Tensor,
-    gain: Optional[Tensor],
-    eps: float,
-    out_dtype: torch.dtype,
-    want_weights: bool,
-    want_aux: bool,
-) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+def _route_impl(buf, num_sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=True):
     device = _require_device(buf, query, gain)
     if buf.dim() < 2:
         raise ValueError("attnres_hip::route: buf must be (max_S, *batch, D)")
@@ -226,7 +222,22 @@ def route(
     es = buf.element_size()
     base = buf.data_ptr()
     ptrs = [base + i * slot * es for i in range(num_sources)]
-    return _launch_route(ptrs, d, buf.dtype, batch, d, device, query, gain, eps, out_dtype, want_weights, want_aux)
+    return _launch_route(ptrs, d, buf.dtype, batch, d, device, query, gain, eps, out_dtype, want_weights, want_aux,
+                         placeholders)
+
+
+@torch.library.custom_op("attnres_hip::route", mutates_args=())
+def route(
+    buf: Tensor,
+    num_sources: int,
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    out_dtype: torch.dtype,
+    want_weights: bool,
+    want_aux: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    return _route_impl(buf, num_sources, query, gain, eps, out_dtype, want_weights, want_aux)
 
 
 @route.register_fake
@@ -235,16 +246,7 @@ def _route_fake(buf, num_sources, query, gain, eps, out_dtype, want_weights, wan
     return _outputs(buf.device, out_dtype, nq, num_sources, tuple(buf.shape[1:-1]), buf.shape[-1], want_weights, want_aux)
 
 
-@torch.library.custom_op("attnres_hip::route_list", mutates_args=())
-def route_list(
-    sources: list[Tensor],
-    query: Tensor,
-    gain: Optional[Tensor],
-    eps: float,
-    out_dtype: torch.dtype,
-    want_weights: bool,
-    want_aux: bool,
-) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+def _route_list_impl(sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=True):
     if len(sources) == 0:
         raise ValueError("attnres_hip::route_list: empty source list (use route with num_sources=0)")
     device = _require_device(*sources, query, gain)
@@ -259,8 +261,21 @@ def route_list(
     srcs = [t if t.is_contiguous() else t.contiguous() for t in sources]
     return _launch_route(
         [t.data_ptr() for t in srcs], d, ref.dtype, tuple(ref.shape[:-1]), d, device, query, gain, eps, out_dtype,
-        want_weights, want_aux,
+        want_weights, want_aux, placeholders,
     )
+
+
+@torch.library.custom_op("attnres_hip::route_list", mutates_args=())
+def route_list(
+    sources: list[Tensor],
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    out_dtype: torch.dtype,
+    want_weights: bool,
+    want_aux: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    return _route_list_impl(sources, query, gain, eps, out_dtype, want_weights, want_aux)
 
 
 @route_list.register_fake
@@ -553,6 +568,11 @@ route_list.register_autograd(_route_list_backward, setup_context=_route_list_set
 
 @torch.library.custom_op("attnres_hip::merge", mutates_args=())
 def merge(partial: Tensor, query: Tensor, inter: Tensor, inter_lse: Tensor, eps: float) -> tuple[Tensor, Tensor, Tensor]:
+    return _merge_impl(partial, query, inter, inter_lse, eps)
+
+
+def _merge_impl(partial, query, inter, inter_lse, eps, aux=True):
+    """Merged rows plus, with ``aux``, the fp32 logit and inverse RMS of the partial (kept for the backward)."""
     device = _require_device(partial, query, inter, inter_lse)
     d = partial.shape[-1]
     if inter.shape != partial.shape:
@@ -567,8 +587,8 @@ def merge(partial: Tensor, query: Tensor, inter: Tensor, inter_lse: Tensor, eps:
     query = query.contiguous()
     n = partial.numel() // d
     out = torch.empty_like(inter)
-    logit = torch.empty(partial.shape[:-1], device=device, dtype=torch.float32)
-    inv_rms = torch.empty(partial.shape[:-1], device=device, dtype=torch.float32)
+    logit = torch.empty(partial.shape[:-1], device=device, dtype=torch.float32) if aux else None
+    inv_rms = torch.empty(partial.shape[:-1], device=device, dtype=torch.float32) if aux else None
     with _DeviceStream(device) as stream:
         _capi.merge_fwd(
             partial.data_ptr(),
@@ -582,8 +602,8 @@ def merge(partial: Tensor, query: Tensor, inter: Tensor, inter_lse: Tensor, eps:
             inter_lse.data_ptr(),
             float(eps),
             out.data_ptr(),
-            logit.data_ptr() if logit.numel() else None,
-            inv_rms.data_ptr() if inv_rms.numel() else None,
+            logit.data_ptr() if logit is not None and logit.numel() else None,
+            inv_rms.data_ptr() if inv_rms is not None and inv_rms.numel() else None,
             stream,
         )
     return out, logit, inv_rms
@@ -597,6 +617,57 @@ def _merge_fake(partial, query, inter, inter_lse, eps):
         partial.new_empty(shp, dtype=torch.float32),
         partial.new_empty(shp, dtype=torch.float32),
     )
+
+
+# ------------------------------------------------------------ eager calls --
+#
+# Called through the dispatcher, each op costs ~24 us of host time per call
+# (measured on an MI355X host: the dispatcher, four placeholder outputs, the ctypes call),
+# several times the kernel of a small routing call.  The drop-ins go through
+# the helpers below, which launch the same implementation directly when there
+# is nothing to record: eager mode, no autograd graph to build, no tracing,
+# no dispatch or function mode, plain tensors.  Otherwise they call the op.
+# Outputs that were not requested are None on the direct path.
+
+_PLAIN_TYPES = (torch.Tensor, torch.nn.Parameter)
+
+
+def _eager_direct(*tensors: Optional[Tensor]) -> bool:
+    if (
+        torch.compiler.is_compiling()
+        or torch._C._len_torch_dispatch_stack()
+        or torch._C._is_torch_function_mode_enabled()
+        or torch._C._are_functorch_transforms_active()
+    ):
+        return False
+    grad = torch.is_grad_enabled()
+    for t in tensors:
+        if t is None:
+            continue
+        if type(t) not in _PLAIN_TYPES or (grad and t.requires_grad):
+            return False
+    return True
+
+
+def route_call(buf, num_sources, query, gain, eps, out_dtype, want_weights=False, want_aux=False) -> tuple:
+    """:func:`route`, launched directly when nothing needs the dispatcher."""
+    if _eager_direct(buf, query, gain):
+        return _route_impl(buf, num_sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=False)
+    return route(buf, num_sources, query, gain, eps, out_dtype, want_weights, want_aux)
+
+
+def route_list_call(sources, query, gain, eps, out_dtype, want_weights=False, want_aux=False) -> tuple:
+    """:func:`route_list`, launched directly when nothing needs the dispatcher."""
+    if _eager_direct(query, gain, *sources):
+        return _route_list_impl(sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=False)
+    return route_list(list(sources), query, gain, eps, out_dtype, want_weights, want_aux)
+
+
+def merge_call(partial, query, inter, inter_lse, eps) -> Tensor:
+    """The merged rows of :func:`merge`, launched directly when nothing needs the dispatcher."""
+    if _eager_direct(partial, query, inter, inter_lse):
+        return _merge_impl(partial, query, inter, inter_lse, eps, aux=False)[0]
+    return merge(partial, query, inter, inter_lse, eps)[0]
 
 
 @torch.library.custom_op("attnres_hip::merge_bwd", mutates_args=())
@@ -764,4 +835,7 @@ __all__ = [
     "block_step",
     "dtype_code",
     "check_forward_only",
+    "route_call",
+    "route_list_call",
+    "merge_call",
 ]

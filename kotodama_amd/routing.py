@@ -49,13 +49,13 @@ def route_static(
     out_dtype = _out_dtype(buf.dtype, query, gain)
     if num_active:
         n = int(num_active)
-        res = ops.route(buf, n, query, gain, float(norm.eps), out_dtype, False, False)
+        res = ops.route_call(buf, n, query, gain, float(norm.eps), out_dtype)
         return res[0][0]
     idx = [i for i, a in enumerate(active_mask.reshape(-1).tolist()) if a]
     if idx == list(range(len(idx))):
-        res = ops.route(buf, len(idx), query, gain, float(norm.eps), out_dtype, False, False)
+        res = ops.route_call(buf, len(idx), query, gain, float(norm.eps), out_dtype)
     else:
-        res = ops.route_list([buf[i] for i in idx], query, gain, float(norm.eps), out_dtype, False, False)
+        res = ops.route_list_call([buf[i] for i in idx], query, gain, float(norm.eps), out_dtype)
     return res[0][0]
 
 
@@ -68,7 +68,7 @@ def block_attn_res_from_list(sources: Sequence[Tensor], query: Tensor, norm) -> 
     """
     gain = norm.weight
     out_dtype = _out_dtype(sources[0].dtype, query, gain)
-    res = ops.route_list(list(sources), query, gain, float(norm.eps), out_dtype, False, False)
+    res = ops.route_list_call(list(sources), query, gain, float(norm.eps), out_dtype)
     return res[0][0]
 
 
@@ -79,5 +79,5 @@ def route_weights(buf: Tensor, num_active: int, query: Tensor, norm) -> tuple[Te
     gain = norm.weight
     ops.check_forward_only(buf, query, gain)
     out_dtype = _out_dtype(buf.dtype, query, gain)
-    out, w, lse, _, _ = ops.route(buf, int(num_active), query, gain, float(norm.eps), out_dtype, True, False)
+    out, w, lse, _, _ = ops.route_call(buf, int(num_active), query, gain, float(norm.eps), out_dtype, True)
     return out[0], w[0], lse[0]

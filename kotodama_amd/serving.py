@@ -64,7 +64,7 @@ class FastAttnResContext:
 
 def _phase_1(blocks: list[Tensor], queries: Tensor, eps: float) -> tuple[Tensor, Tensor]:
     """(out (Q, B, T, D) bf16, lse (Q, B, T)) over a list of committed blocks."""
-    out, _, lse, _, _ = ops.route_list(blocks, queries, None, eps, torch.bfloat16, True, False)
+    out, _, lse, _, _ = ops.route_list_call(blocks, queries, None, eps, torch.bfloat16, True)
     return out, lse
 
 
@@ -86,7 +86,7 @@ def fast_forward_attn_res(ctx: FastAttnResContext, embed: Tensor) -> Tensor:
             if qo == 0:
                 curr = ctx.sublayers[j](p1_out[0])
             else:
-                merged, _, _ = ops.merge(curr, pq[j], p1_out[qo], p1_lse[qo], eps)
+                merged = ops.merge_call(curr, pq[j], p1_out[qo], p1_lse[qo], eps)
                 curr = curr + ctx.sublayers[j](merged)
         blocks.append(curr)
     final_out, _ = _phase_1(blocks, pq[-1:], eps)

@@ -137,3 +137,44 @@ def test_stack_free_forward_trains_like_the_reference_loop(gpu):
     with torch.no_grad():
         out2 = forward_attn_res(m, embed.to(gpu))
     torch.testing.assert_close(out2, out.detach(), rtol=1e-5, atol=1e-5)
+
+
+def test_eager_calls_skip_the_dispatcher_only_when_nothing_is_recorded(gpu, monkeypatch):
+    # the drop-ins launch the op's implementation directly in eager no-grad
+    # use (same values as the op), and go through the op when autograd or a
+    # dispatch mode must see the call
+    from kotodama_amd import ops, routing
+
+    d = 1024
+    g = torch.Generator(device=gpu).manual_seed(31)
+    buf = torch.randn((4, 2, 16, d), generator=g, device=gpu).to(torch.bfloat16)
+    query = (torch.randn(d, generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+    norm = torch.nn.Module()
+    norm.weight = torch.nn.Parameter((1 + 0.1 * torch.randn(d, generator=g, device=gpu)).to(torch.bfloat16))
+    norm.eps = 1e-5
+    mask = torch.ones(4, dtype=torch.bool, device=gpu)
+    via_op = ops.route(buf, 3, query, norm.weight, 1e-5, torch.bfloat16, False, False)[0][0]
+    partial = torch.randn((2, 16, d), generator=g, device=gpu).to(torch.bfloat16)
+    lse = torch.randn((2, 16), generator=g, device=gpu)
+    merged_op = ops.merge(partial, query, buf[0], lse, 1e-5)[0]
+
+    calls = []
+    real_route, real_merge = ops.route, ops.merge
+    monkeypatch.setattr(ops, "route", lambda *a: calls.append("route") or real_route(*a))
+    monkeypatch.setattr(ops, "merge", lambda *a: calls.append("merge") or real_merge(*a))
+    with torch.no_grad():
+        h = routing.route_static(buf, query, norm, mask, 3)
+        m = ops.merge_call(partial, query, buf[0], lse, 1e-5)
+    assert calls == [] and torch.equal(h, via_op) and torch.equal(m, merged_op)
+    # a parameter that requires grad under autograd: the op (and its backward) runs
+    h2 = routing.route_static(buf, query, norm, mask, 3)
+    assert calls == ["route"] and h2.requires_grad and torch.equal(h2.detach(), via_op)
+    calls.clear()
+
+    class PassThrough(torch.utils._python_dispatch.TorchDispatchMode):
+        def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+            return func(*args, **(kwargs or {}))
+
+    with torch.no_grad(), PassThrough():
+        h3 = routing.route_static(buf, query, norm, mask, 3)
+    assert calls == ["route"] and torch.equal(h3, via_op)
