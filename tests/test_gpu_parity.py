@@ -205,12 +205,14 @@ def route_kernel(s, n, d, q):
     return buf.value.decode()
 
 
-@pytest.mark.parametrize("d,n,queries", [(1024, 24, (2, 9)), (8192, 12, (3, 8)), (3072, 600, (5,)), (520, 7, (4,))])
+@pytest.mark.parametrize("d,n,queries", [(1024, 24, (2, 9)), (8192, 12, (3, 8)), (3072, 600, (5,)), (520, 7, (4,)),
+                                         (8184, 5, (3,))])
 def test_batched_query_kernel_every_source_count(gpu, d, n, queries):
     # bf16 folded queries (the serving engine's phase 1): the batched-query
     # kernel, groups of 8/4/2 queries with a ragged last group, one chunk per
     # thread (d=1024; d=520 leaves 63 idle lanes past the row end), two
-    # (d=8192; d=3072 with enough rows); every output against the oracle
+    # (d=8192; d=3072 with enough rows; d=8184: the last thread's second
+    # chunk is past the row end); every output against the oracle
     g = torch.Generator(device=gpu).manual_seed(d + n)
     for S in range(1, 17):
         if d == 3072 and S not in (1, 6, 7, 13):
