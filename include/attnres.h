@@ -201,6 +201,46 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
                       void* grad_query, void* grad_gain, void* stream);
 
 /*
+ * Bytes of device workspace attnres_route_bwd_queries needs on the current
+ * device: the fp32 coefficients (num_tokens, num_queries, num_sources) plus
+ * per-workgroup partials of the num_queries query gradients.
+ */
+int attnres_route_bwd_queries_workspace_size(int64_t num_tokens, int hidden, int num_sources, int num_queries,
+                                             int64_t* bytes);
+
+/*
+ * Backward of attnres_route_fwd for num_queries >= 1 queries over the same
+ * sources (the batched phase-1 call), in one pass over the sources:
+ *   dL/dsource_s = sum over queries of the single-query terms,
+ * plus dL/dquery for every query and dL/dgain summed over the queries.
+ *
+ * query:        (num_queries, hidden) param_dtype; gain (hidden,) or NULL.
+ * grad_out:     num_queries blocks of (num_tokens, hidden) rows, row stride
+ *               grad_out_ld, query stride grad_out_qstride (elements).
+ * grad_lse:     (num_queries, num_tokens) fp32, or NULL.
+ * grad_query:   (num_queries, hidden) param_dtype, or NULL; grad_gain as in
+ *               attnres_route_bwd.  Sums over tokens in a fixed order.
+ * workspace:    attnres_route_bwd_queries_workspace_size() bytes.
+ * Other arguments as in attnres_route_bwd.  Returns ATTNRES_ERR_UNSUPPORTED
+ * for shapes without a batched kernel (num_sources * 8 * V > 72 for bf16
+ * sources, num_sources * 4 * V > 72 for fp32, V = 2 for rows above 512
+ * chunks of 16 bytes); attnres_route_bwd once per query covers those.
+ *
+ * Replaces the Triton backward of the phase-1 op for Q > 1
+ * (src/model/flash_attn_res/ops/phase_1.py:88-284,
+ * kernels/phase_1.py:104-280 with NUM_QUERIES_PER_BLOCK > 1, which also sums
+ * the source gradients over the queries in one program), with the query
+ * gradients formed in a second pass over the sources instead of per-row
+ * partials (kernels/reduce.py).
+ */
+int attnres_route_bwd_queries(const void* const* sources, int num_sources, int64_t num_tokens, int hidden,
+                              int64_t src_ld, int src_dtype, const void* query, const void* gain, int num_queries,
+                              int param_dtype, float eps, const void* grad_out, int grad_out_dtype,
+                              int64_t grad_out_ld, int64_t grad_out_qstride, const float* grad_lse,
+                              void* const* grad_sources, int64_t grad_ld, void* workspace, int64_t workspace_bytes,
+                              void* grad_query, void* grad_gain, void* stream);
+
+/*
  * Backward of attnres_merge_fwd: given dL/dout (num_tokens, hidden) in
  * inter_dtype, writes dL/dpartial (partial_dtype), dL/dinter (inter_dtype),
  * dL/dinter_lse ((num_tokens,) fp32, or NULL to skip) and, when grad_query is

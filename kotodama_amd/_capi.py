@@ -52,6 +52,8 @@ EXPORTS = (
     "attnres_block_step",
     "attnres_route_bwd_workspace_size",
     "attnres_route_bwd",
+    "attnres_route_bwd_queries_workspace_size",
+    "attnres_route_bwd_queries",
     "attnres_merge_bwd",
 )
 
@@ -163,6 +165,35 @@ _SIGNATURES = {
         ],
         _c_int,
     ),
+    "attnres_route_bwd_queries_workspace_size": ([_c_i64, _c_int, _c_int, _c_int, ctypes.POINTER(_c_i64)], _c_int),
+    "attnres_route_bwd_queries": (
+        [
+            ctypes.POINTER(_c_vp),  # sources
+            _c_int,  # num_sources
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_i64,  # src_ld
+            _c_int,  # src_dtype
+            _c_vp,  # query
+            _c_vp,  # gain
+            _c_int,  # num_queries
+            _c_int,  # param_dtype
+            _c_float,  # eps
+            _c_vp,  # grad_out
+            _c_int,  # grad_out_dtype
+            _c_i64,  # grad_out_ld
+            _c_i64,  # grad_out_qstride
+            _c_vp,  # grad_lse
+            ctypes.POINTER(_c_vp),  # grad_sources
+            _c_i64,  # grad_ld
+            _c_vp,  # workspace
+            _c_i64,  # workspace_bytes
+            _c_vp,  # grad_query
+            _c_vp,  # grad_gain
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
     "attnres_merge_bwd": (
         [
             _c_vp,  # partial
@@ -256,6 +287,23 @@ def route_bwd_workspace_size(num_tokens: int, hidden: int) -> int:
 
 def route_bwd(*args) -> None:
     check("attnres_route_bwd", lib().attnres_route_bwd(*args))
+
+
+def route_bwd_queries_workspace_size(num_tokens: int, hidden: int, num_sources: int, num_queries: int) -> int:
+    """Bytes of workspace :func:`route_bwd_queries` needs on the current device."""
+    out = _c_i64(0)
+    check("attnres_route_bwd_queries_workspace_size",
+          lib().attnres_route_bwd_queries_workspace_size(num_tokens, hidden, num_sources, num_queries,
+                                                         ctypes.byref(out)))
+    return out.value
+
+
+def route_bwd_queries(*args) -> int:
+    """attnres_route_bwd_queries; returns its code (ERR_UNSUPPORTED: no batched kernel for the shape)."""
+    code = lib().attnres_route_bwd_queries(*args)
+    if code not in (OK, ERR_UNSUPPORTED):
+        check("attnres_route_bwd_queries", code)
+    return code
 
 
 def merge_bwd(*args) -> None:

@@ -1,4 +1,4 @@
-/* The six gfx950 code-object parts, linked into libattnres_hip.so as bytes
+/* The seven gfx950 code-object parts, linked into libattnres_hip.so as bytes
  * and loaded with hipModuleLoadData.  The build passes -I<dir of the .hsaco>. */
     .section .rodata
     .balign 4096
@@ -25,4 +25,8 @@ attnres_hsaco_part4:
     .global attnres_hsaco_part5
 attnres_hsaco_part5:
     .incbin "attnres_gfx950_part5.hsaco"
+    .balign 4096
+    .global attnres_hsaco_part6
+attnres_hsaco_part6:
+    .incbin "attnres_gfx950_part6.hsaco"
     .section .note.GNU-stack,"",@progbits

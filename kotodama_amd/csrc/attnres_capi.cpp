@@ -29,10 +29,11 @@ extern "C" const unsigned char attnres_hsaco_part2[];
 extern "C" const unsigned char attnres_hsaco_part3[];
 extern "C" const unsigned char attnres_hsaco_part4[];
 extern "C" const unsigned char attnres_hsaco_part5[];
+extern "C" const unsigned char attnres_hsaco_part6[];
 
 namespace {
 
-constexpr int kParts = 6;
+constexpr int kParts = 7;
 constexpr int kMaxDevices = 64;
 constexpr int kMaxThreads = 512;  // __launch_bounds__ of every kernel
 
@@ -91,6 +92,12 @@ struct DeviceState {
   hipFunction_t merge_bwd[kMergeFuncs] = {};
   int merge_bwd_bpc[kMergeFuncs] = {};
   int merge_bwd_bpc_block[kMergeFuncs] = {};
+  hipFunction_t bwd_mq[kBwdFuncs] = {};  // batched-query backward: (source, grad_out) dtypes x S x V
+  int bwd_mq_bpc[kBwdFuncs] = {};
+  int bwd_mq_bpc_block[kBwdFuncs] = {};
+  hipFunction_t bwd_dqw[4] = {};  // source dtype x V
+  int bwd_dqw_bpc[4] = {};
+  int bwd_dqw_bpc_block[4] = {};
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -133,7 +140,8 @@ int ensure_loaded(DeviceState** out) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (!st.loaded.load(std::memory_order_relaxed)) {
       const unsigned char* blobs[kParts] = {attnres_hsaco_part0, attnres_hsaco_part1, attnres_hsaco_part2,
-                                            attnres_hsaco_part3, attnres_hsaco_part4, attnres_hsaco_part5};
+                                            attnres_hsaco_part3, attnres_hsaco_part4, attnres_hsaco_part5,
+                                            attnres_hsaco_part6};
       for (int i = 0; i < kParts; ++i) {
         e = hipModuleLoadData(&st.mods[i], blobs[i]);
         if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
@@ -279,6 +287,57 @@ int get_bwd(DeviceState& st, bool bf, bool gbf, int s, int v, int block, size_t 
   }
   *f = st.bwd[idx];
   *bpc = st.bwd_bpc[idx];
+  return ATTNRES_OK;
+}
+
+// Batched-query backward kernels (code-object part 6).  Source-gradient
+// accumulators are S * VEC * V fp32 registers per thread; the kernels exist
+// where that stays within 72.
+constexpr int kBwdMqPart = 6;
+bool bwd_mq_available(bool bf, int s, int v) {
+  const int vec = bf ? 8 : 4;
+  return s >= 1 && s <= ATTNRES_KMAX_SOURCES && (v == 1 || v == 2) && s * vec * v <= 72;
+}
+
+int get_bwd_mq(DeviceState& st, bool bf, bool gbf, int s, int v, int block, hipFunction_t* f, int* bpc) {
+  const int idx = (((bf ? 0 : 2) + (gbf ? 0 : 1)) * kNumS + s) * 2 + (v - 1);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (st.bwd_mq[idx] == nullptr) {
+    char name[96];
+    snprintf(name, sizeof(name), "attnres_route_bwd_mq_%s_g%s_s%d_v%d", bf ? "bf" : "f32", gbf ? "bf" : "f32", s, v);
+    int rc = find_function(st, kBwdMqPart, name, &st.bwd_mq[idx]);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  if (st.bwd_mq_bpc_block[idx] != block) {
+    int nb = 0;
+    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.bwd_mq[idx], block, 0);
+    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    st.bwd_mq_bpc[idx] = nb > 0 ? nb : 1;
+    st.bwd_mq_bpc_block[idx] = block;
+  }
+  *f = st.bwd_mq[idx];
+  *bpc = st.bwd_mq_bpc[idx];
+  return ATTNRES_OK;
+}
+
+int get_bwd_dqw(DeviceState& st, bool bf, int v, int block, hipFunction_t* f, int* bpc) {
+  const int idx = (bf ? 0 : 2) + (v - 1);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (st.bwd_dqw[idx] == nullptr) {
+    char name[96];
+    snprintf(name, sizeof(name), "attnres_route_bwd_dqw_%s_v%d", bf ? "bf" : "f32", v);
+    int rc = find_function(st, kBwdMqPart, name, &st.bwd_dqw[idx]);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  if (st.bwd_dqw_bpc_block[idx] != block) {
+    int nb = 0;
+    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.bwd_dqw[idx], block, 0);
+    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    st.bwd_dqw_bpc[idx] = nb > 0 ? nb : 1;
+    st.bwd_dqw_bpc_block[idx] = block;
+  }
+  *f = st.bwd_dqw[idx];
+  *bpc = st.bwd_dqw_bpc[idx];
   return ATTNRES_OK;
 }
 
@@ -545,7 +604,8 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
 // `workspace`: summed in 64-row blocks (stage 1, in place), then the block
 // sums (final stage); a fixed order, so the result is deterministic.
 int reduce_launch(hipFunction_t fs, hipFunction_t fr, void* workspace, int nparts, int hidden, const void* query,
-                  const void* gain, int param_dtype, void* grad_query, void* grad_gain, void* stream) {
+                  const void* gain, int param_dtype, void* grad_query, void* grad_gain, void* stream,
+                  int num_queries = 1) {
   attnres_reduce_params R;
   std::memset(&R, 0, sizeof(R));
   R.part = static_cast<float*>(workspace);
@@ -557,8 +617,10 @@ int reduce_launch(hipFunction_t fs, hipFunction_t fr, void* workspace, int npart
   R.part_step = 1;
   R.d = hidden;
   R.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
+  R.num_queries = num_queries;
   if (nparts > 64) {
-    int rc = launch(fs, (hidden + 63) / 64, 256, R, stream, (nparts + 63) / 64);
+    const int64_t width = (int64_t)hidden * num_queries;
+    int rc = launch(fs, (int)((width + 63) / 64), 256, R, stream, (nparts + 63) / 64);
     if (rc != ATTNRES_OK) return rc;
     R.part_step = 64;
   }
@@ -810,6 +872,158 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   if (rc != ATTNRES_OK || fr == nullptr) return rc;
 
   return reduce_launch(fs, fr, workspace, (int)grid, hidden, query, gain, param_dtype, grad_query, grad_gain, stream);
+}
+
+// Workspace of the batched-query backward: c1 coefficients (num_tokens, Q, S)
+// fp32, then the per-workgroup query-gradient partials (grid, Q, hidden).
+constexpr int kBwdDqwPerCu = 2;
+int64_t bwd_mq_c1_bytes(int64_t num_tokens, int num_sources, int num_queries) {
+  const int64_t b = num_tokens * (int64_t)num_queries * num_sources * (int64_t)sizeof(float);
+  return (b + 255) / 256 * 256;
+}
+
+int attnres_route_bwd_queries_workspace_size(int64_t num_tokens, int hidden, int num_sources, int num_queries,
+                                             int64_t* bytes) {
+  if (bytes == nullptr) return fail(ATTNRES_ERR_ARG, "bytes is NULL");
+  if (num_tokens < 0 || hidden <= 0 || num_sources < 1 || num_sources > ATTNRES_MAX_SOURCES || num_queries < 1)
+    return fail(ATTNRES_ERR_ARG, "bad num_tokens/hidden/num_sources/num_queries");
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  int64_t parts = (int64_t)st->num_cus * kBwdDqwPerCu;
+  if (parts > num_tokens) parts = num_tokens;
+  *bytes = bwd_mq_c1_bytes(num_tokens, num_sources, num_queries) +
+           parts * (int64_t)num_queries * hidden * (int64_t)sizeof(float);
+  return ATTNRES_OK;
+}
+
+int attnres_route_bwd_queries(const void* const* sources, int num_sources, int64_t num_tokens, int hidden,
+                              int64_t src_ld, int src_dtype, const void* query, const void* gain, int num_queries,
+                              int param_dtype, float eps, const void* grad_out, int grad_out_dtype,
+                              int64_t grad_out_ld, int64_t grad_out_qstride, const float* grad_lse,
+                              void* const* grad_sources, int64_t grad_ld, void* workspace, int64_t workspace_bytes,
+                              void* grad_query, void* grad_gain, void* stream) {
+  if (num_sources < 1 || num_sources > ATTNRES_MAX_SOURCES)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "backward: num_sources=%d outside [1, %d]", num_sources,
+                ATTNRES_MAX_SOURCES);
+  if (num_queries < 1) return fail(ATTNRES_ERR_ARG, "num_queries=%d < 1", num_queries);
+  if (sources == nullptr || grad_sources == nullptr) return fail(ATTNRES_ERR_ARG, "sources/grad_sources is NULL");
+  if (num_tokens < 0) return fail(ATTNRES_ERR_ARG, "num_tokens=%lld < 0", (long long)num_tokens);
+  if (hidden <= 0) return fail(ATTNRES_ERR_ARG, "hidden=%d <= 0", hidden);
+  if (!valid_dtype(src_dtype) || !valid_dtype(param_dtype) || !valid_dtype(grad_out_dtype))
+    return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (query == nullptr || grad_out == nullptr) return fail(ATTNRES_ERR_ARG, "query/grad_out is NULL");
+  if (gain == nullptr && grad_gain != nullptr) return fail(ATTNRES_ERR_ARG, "grad_gain given without gain");
+  if (!std::isfinite(eps)) return fail(ATTNRES_ERR_ARG, "eps is not finite");
+  const bool bf = src_dtype == ATTNRES_DTYPE_BF16;
+  const int vec = bf ? 8 : 4;
+  if (hidden % vec != 0)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d is not a multiple of %d (16-byte chunks)", hidden, vec);
+  const int nchunk = hidden / vec;
+  if (round64((nchunk + 1) / 2) > kMaxThreads)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d exceeds the largest supported row (%d elements)", hidden,
+                2 * kMaxThreads * vec);
+  const int v = round64(nchunk) <= kMaxThreads ? 1 : 2;
+  if (!bwd_mq_available(bf, num_sources, v))
+    return fail(ATTNRES_ERR_UNSUPPORTED,
+                "batched backward of S=%d sources with %d chunks per thread is not built; call attnres_route_bwd "
+                "once per query",
+                num_sources, v);
+  const int gvec_bytes = vec * esize(grad_out_dtype);
+  const int galign = gvec_bytes >= 16 ? 16 : gvec_bytes;
+  if (src_ld < hidden || grad_ld < hidden || grad_out_ld < hidden)
+    return fail(ATTNRES_ERR_ARG, "a row stride is smaller than hidden=%d", hidden);
+  if (num_queries > 1 && grad_out_qstride < num_tokens * grad_out_ld)
+    return fail(ATTNRES_ERR_ARG, "grad_out_qstride=%lld overlaps query rows", (long long)grad_out_qstride);
+  if ((src_ld * esize(src_dtype)) % 16 != 0 || (grad_ld * esize(src_dtype)) % 16 != 0)
+    return fail(ATTNRES_ERR_ALIGN, "source / gradient row stride not 16-byte aligned");
+  if (((uintptr_t)grad_out % galign) != 0 || ((grad_out_ld * esize(grad_out_dtype)) % galign) != 0 ||
+      ((grad_out_qstride * esize(grad_out_dtype)) % galign) != 0)
+    return fail(ATTNRES_ERR_ALIGN, "grad_out rows not %d-byte aligned", galign);
+  for (int s = 0; s < num_sources; ++s) {
+    if (sources[s] == nullptr || grad_sources[s] == nullptr)
+      return fail(ATTNRES_ERR_ARG, "sources[%d] or grad_sources[%d] is NULL", s, s);
+    if (!aligned16(sources[s]) || !aligned16(grad_sources[s]))
+      return fail(ATTNRES_ERR_ALIGN, "sources[%d] or grad_sources[%d] not 16-byte aligned", s, s);
+  }
+  if (num_tokens == 0) return ATTNRES_OK;  // no tokens: the query gradients are not written
+
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  const int block = v == 1 ? round64(nchunk) : round64((nchunk + 1) / 2);
+  hipFunction_t f = nullptr, fq = nullptr;
+  int bpc = 1, bpcq = 1;
+  rc = get_bwd_mq(*st, bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, v, block, &f, &bpc);
+  if (rc != ATTNRES_OK) return rc;
+  const bool want_q = grad_query != nullptr || grad_gain != nullptr;
+  hipFunction_t fr = nullptr, fs = nullptr;
+  int64_t grid_q = 0;
+  if (want_q) {
+    rc = get_bwd_dqw(*st, bf, v, block, &fq, &bpcq);
+    if (rc != ATTNRES_OK) return rc;
+    rc = get_reduce(*st, &fs, &fr);
+    if (rc != ATTNRES_OK) return rc;
+    grid_q = (int64_t)st->num_cus * (bpcq < kBwdDqwPerCu ? bpcq : kBwdDqwPerCu);
+    if (grid_q > num_tokens) grid_q = num_tokens;
+  }
+  const int64_t c1_bytes = bwd_mq_c1_bytes(num_tokens, num_sources, num_queries);
+  const int64_t need = c1_bytes + grid_q * (int64_t)num_queries * hidden * (int64_t)sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(ATTNRES_ERR_ARG, "workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
+                (long long)need);
+  if (!aligned16(workspace)) return fail(ATTNRES_ERR_ALIGN, "workspace not 16-byte aligned");
+  float* c1 = static_cast<float*>(workspace);
+  float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + c1_bytes);
+
+  attnres_route_bwd_mq_params P;
+  std::memset(&P, 0, sizeof(P));
+  for (int s = 0; s < num_sources; ++s) {
+    P.src[s] = sources[s];
+    P.dsrc[s] = grad_sources[s];
+  }
+  P.query = query;
+  P.gain = gain;
+  P.grad_out = grad_out;
+  P.grad_lse = grad_lse;
+  P.c1 = c1;
+  P.n_tokens = num_tokens;
+  P.src_ld = src_ld;
+  P.dsrc_ld = grad_ld;
+  P.gout_ld = grad_out_ld;
+  P.gout_qstride = grad_out_qstride;
+  P.d = hidden;
+  P.nchunk = nchunk;
+  P.num_queries = num_queries;
+  P.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
+  P.block = block;
+  P.eps = eps;
+  P.inv_d = 1.0f / (float)hidden;
+  // two resident workgroups per CU, as the single-query backward
+  int64_t grid = (int64_t)st->num_cus * (bpc < 2 ? bpc : 2);
+  if (grid > num_tokens) grid = num_tokens;
+  rc = launch(f, (int)grid, block, P, stream);
+  if (rc != ATTNRES_OK || !want_q) return rc;
+
+  attnres_route_bwd_dqw_params Q;
+  std::memset(&Q, 0, sizeof(Q));
+  for (int s = 0; s < num_sources; ++s) Q.src[s] = sources[s];
+  Q.c1 = c1;
+  Q.part = part;
+  Q.n_tokens = num_tokens;
+  Q.src_ld = src_ld;
+  Q.d = hidden;
+  Q.nchunk = nchunk;
+  Q.num_sources = num_sources;
+  Q.num_queries = num_queries;
+  Q.block = block;
+  for (int q0 = 0; q0 < num_queries; q0 += 8) {  // eight queries per pass over the sources
+    Q.q0 = q0;
+    rc = launch(fq, (int)grid_q, block, Q, stream);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  return reduce_launch(fs, fr, part, (int)grid_q, hidden, query, gain, param_dtype, grad_query, grad_gain, stream,
+                       num_queries);
 }
 
 int attnres_merge_bwd(const void* partial, int64_t num_tokens, int hidden, int partial_dtype, const void* query,

@@ -1599,6 +1599,318 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
 }
 
 
+// ------------------------------------------- batched-query backward body --
+//
+// Backward of Q >= 2 queries over one set of sources (the batched phase-1
+// call, ops/phase_1.py:88-284 with NUM_QUERIES_PER_BLOCK > 1), one pass over
+// the sources.  One workgroup per token row (grid-stride), chunks as in
+// route_bwd_body; the S source chunks stay in registers for all queries.  Per
+// query q: x.qw_q and x.G_q per source (sum(x^2) once per row), the
+// transposing wave reduction and one LDS exchange, the softmax and the
+// coefficients lane-parallel (lane s per source), then
+//   acc_s  += w_qs G_q + c1_qs qw_q      (fp32 registers)
+//   c2sum_s += c2_qs                      (lane s)
+// and once per row dx_s = acc_s + c2sum_s x_s.  c1_qs goes to `c1`
+// (n_tokens, Q, S): the query gradients sum_rows sum_s c1_qs x_s are formed by
+// route_bwd_dqw_body in a second pass over the sources.
+
+template <int VEC>
+__device__ __forceinline__ void load_qw_ptr(const void* query, const void* gain, bool bf16, int q, int d, int chunk,
+                                            float (&qw)[VEC]) {
+  const int64_t off = (int64_t)chunk * VEC;
+  load_param<VEC>(query, (int64_t)q * d + off, bf16, qw);
+  if (gain != nullptr) {
+    float g[VEC];
+    load_param<VEC>(gain, off, bf16, g);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float prod = qw[e] * g[e];
+      qw[e] = bf16 ? round_bf16(prod) : prod;
+    }
+  }
+}
+
+template <int S, int V, bool BF16, bool GBF>
+__device__ __forceinline__ void route_bwd_mq_body(const attnres_route_bwd_mq_params& P) {
+  using C = Chunk<BF16>;
+  constexpr int VEC = C::VEC;
+  using GC = PackedChunk<VEC, GBF>;
+  constexpr int NV = 3 * S;  // sum(x^2), x.qw_q, x.G_q per source
+  constexpr int H2 = (NV + 3) / 4;
+  constexpr int NP = 4 * H2;
+  constexpr int SEG = S <= 8 ? 8 : 16;
+  __shared__ float red[2][ATTNRES_KMAX_WAVES][NP];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int block = P.block;
+  const int nwaves = (block + 63) >> 6;
+  const int nq = P.num_queries;
+
+  int chunk[V];
+  bool ok[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    chunk[k] = tid + k * block;
+    ok[k] = chunk[k] < P.nchunk;
+  }
+
+  // Source rows through buffer resources: a chunk past the row end reads 0
+  // and its gradient store is dropped.
+  const int64_t row_bytes_ld = P.src_ld * C::BYTES;
+  const uint32_t row_bytes = (uint32_t)(P.d * C::BYTES);
+  u32x4 x[S][V];
+  auto load_row = [&](int64_t t) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      char* row = reinterpret_cast<char*>(const_cast<void*>(P.src[s])) + t * row_bytes_ld;
+      const __amdgpu_buffer_rsrc_t rs = row_rsrc(row, row_bytes);
+#pragma unroll
+      for (int k = 0; k < V; ++k) x[s][k] = ld_row(rs, (uint32_t)chunk[k] * 16);
+    }
+  };
+
+  const int ls = lane % SEG;  // the source of this lane in the softmax
+  const bool slot = ls < S;
+  const int64_t grow_bytes_ld = P.gout_ld * (GBF ? 2 : 4);
+  const int64_t gq_bytes = P.gout_qstride * (GBF ? 2 : 4);
+  float gain_reg[V][VEC];  // the norm gain of the fold, once per thread
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    if (P.gain != nullptr && ok[k]) {
+      load_param<VEC>(P.gain, (int64_t)chunk[k] * VEC, P.param_bf16, gain_reg[k]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) gain_reg[k][e] = 1.f;
+    }
+  }
+
+  int ph = 0;
+  if ((int64_t)blockIdx.x < P.n_tokens) load_row(blockIdx.x);
+  for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
+    float ssp[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      ssp[s] = 0.f;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float v = C::elem(x[s][k], e);
+          ssp[s] = __builtin_fmaf(v, v, ssp[s]);
+        }
+      }
+    }
+    float acc[S][V][VEC];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[s][k][e] = 0.f;
+      }
+    }
+    float c2sum = 0.f;
+
+    // The next query's output-gradient and query chunks are requested before
+    // the current query is processed (one query ahead), so the per-query
+    // loads overlap the previous query's reduction and accumulation.
+    GC gn[V];
+    ParamRaw<VEC> qn[V];
+    auto fetch_query = [&](int q) {
+      const char* grow = reinterpret_cast<const char*>(P.grad_out) + q * gq_bytes + tok * grow_bytes_ld;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        if (ok[k]) {
+          gn[k].load(grow, chunk[k]);
+          load_param_raw<VEC>(reinterpret_cast<const char*>(P.query) + (int64_t)q * P.d * (P.param_bf16 ? 2 : 4),
+                              chunk[k], P.param_bf16, qn[k]);
+        } else {
+          gn[k].zero();
+          qn[k].w[0] = u32x4{0, 0, 0, 0};
+          if constexpr (VEC == 8) qn[k].w[1] = u32x4{0, 0, 0, 0};
+        }
+      }
+    };
+    fetch_query(0);
+    for (int q = 0; q < nq; ++q) {
+      // ---- this query's folded query and output-gradient chunks ----
+      float qw[V][VEC];
+      GC g[V];
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        g[k] = gn[k];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float qv = param_elem<VEC>(qn[k], e, P.param_bf16);
+          if (P.gain != nullptr) {
+            const float prod = qv * gain_reg[k][e];
+            qw[k][e] = P.param_bf16 ? round_bf16(prod) : prod;
+          } else {
+            qw[k][e] = qv;
+          }
+        }
+      }
+      if (q + 1 < nq) fetch_query(q + 1);
+
+      // ---- sum(x^2), x.qw_q, x.G_q; transposing reduction; one exchange ----
+      float part[NP];
+#pragma unroll
+      for (int j = 0; j < NP; ++j) part[j] = j < S ? ssp[j] : 0.f;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const float v = C::elem(x[s][k], e);
+            part[S + s] = __builtin_fmaf(v, qw[k][e], part[S + s]);
+            part[2 * S + s] = __builtin_fmaf(v, g[k].elem(e), part[2 * S + s]);
+          }
+        }
+      }
+      wave_reduce_to_lds<H2>(part, red[ph][wave], lane);
+      __syncthreads();
+
+      // ---- softmax and coefficients, lane s per source ----
+      float t_ss = 0.f, t_dot = 0.f, t_gx = 0.f;
+      if (slot) {
+        for (int w = 0; w < nwaves; ++w) {
+          t_ss += red[ph][w][ls];
+          t_dot += red[ph][w][S + ls];
+          t_gx += red[ph][w][2 * S + ls];
+        }
+      }
+      ph ^= 1;
+      const float rl = __builtin_amdgcn_rsqf(t_ss * P.inv_d + P.eps);
+      const float ll = slot ? t_dot * rl : -__builtin_inff();
+      const float m = seg_max<SEG>(ll);
+      const float el = slot ? __expf(ll - m) : 0.f;
+      const float wl = el * (1.0f / seg_sum<SEG>(el));
+      const float go = seg_sum<SEG>(wl * t_gx);  // G_q . out_q
+      const float glse = P.grad_lse != nullptr ? P.grad_lse[(int64_t)q * P.n_tokens + tok] : 0.f;
+      const float c1l = slot ? wl * (glse + t_gx - go) * rl : 0.f;
+      c2sum += slot ? -c1l * ll * rl * P.inv_d : 0.f;
+      if (wave == 0 && lane < S) P.c1[(tok * nq + q) * S + lane] = c1l;
+      float wgt[S], c1[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        wgt[s] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), s));
+        c1[s] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c1l), s));
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e)
+            acc[s][k][e] = __builtin_fmaf(wgt[s], g[k].elem(e), __builtin_fmaf(c1[s], qw[k][e], acc[s][k][e]));
+        }
+      }
+    }
+
+    // ---- dx_s = acc_s + c2sum_s x_s, stored once ----
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const float c2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c2sum), s));
+      char* drow = reinterpret_cast<char*>(P.dsrc[s]) + tok * P.dsrc_ld * C::BYTES;
+      const __amdgpu_buffer_rsrc_t drs = row_rsrc(drow, row_bytes);
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        float dx[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) dx[e] = __builtin_fmaf(c2, C::elem(x[s][k], e), acc[s][k][e]);
+        if constexpr (BF16) {
+          st_row(drs, (uint32_t)chunk[k] * 16,
+                 u32x4{pack_bf16(dx[0], dx[1]), pack_bf16(dx[2], dx[3]), pack_bf16(dx[4], dx[5]),
+                       pack_bf16(dx[6], dx[7])});
+        } else {
+          st_row(drs, (uint32_t)chunk[k] * 16, u32x4{as_u32(dx[0]), as_u32(dx[1]), as_u32(dx[2]), as_u32(dx[3])});
+        }
+      }
+    }
+    if (tok + gridDim.x < P.n_tokens) load_row(tok + gridDim.x);
+  }
+}
+
+// Query-gradient partials of the batched backward: each workgroup sums
+// c1_qs x_s over its rows (grid-stride) and sources for up to 8 queries
+// q0 .. q0+7 and writes them as its row of `part` (gridDim.x, Q, d).  Source
+// chunks are requested four at a time.
+template <int V, bool BF16>
+__device__ __forceinline__ void route_bwd_dqw_body(const attnres_route_bwd_dqw_params& P) {
+  using C = Chunk<BF16>;
+  constexpr int VEC = C::VEC;
+  constexpr int QG = 8;
+  const int tid = threadIdx.x;
+  const int block = P.block;
+  const int S = P.num_sources;
+  const int nq = P.num_queries;
+  const int q0 = P.q0;
+  const int ng = nq - q0 < QG ? nq - q0 : QG;
+
+  int chunk[V];
+  bool ok[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    chunk[k] = tid + k * block;
+    ok[k] = chunk[k] < P.nchunk;
+  }
+  float acc[QG][V][VEC];
+#pragma unroll
+  for (int g = 0; g < QG; ++g) {
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[g][k][e] = 0.f;
+    }
+  }
+  const int64_t row_bytes_ld = P.src_ld * C::BYTES;
+  const uint32_t row_bytes = (uint32_t)(P.d * C::BYTES);
+  constexpr int SG = 4;  // sources requested together
+  for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
+    const float* crow = P.c1 + (tok * nq + q0) * S;
+    for (int s0 = 0; s0 < S; s0 += SG) {
+      u32x4 x[SG][V];
+#pragma unroll
+      for (int i = 0; i < SG; ++i) {
+        const int s = s0 + i < S ? s0 + i : S - 1;  // past S: a repeated row, weight 0 below
+        char* row = reinterpret_cast<char*>(const_cast<void*>(P.src[s])) + tok * row_bytes_ld;
+        const __amdgpu_buffer_rsrc_t rs = row_rsrc(row, row_bytes);
+#pragma unroll
+        for (int k = 0; k < V; ++k) x[i][k] = ld_row(rs, (uint32_t)chunk[k] * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < SG; ++i) {
+#pragma unroll
+        for (int g = 0; g < QG; ++g) {
+          const float c = (g < ng && s0 + i < S) ? crow[g * S + s0 + i] : 0.f;
+#pragma unroll
+          for (int k = 0; k < V; ++k) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc[g][k][e] = __builtin_fmaf(c, C::elem(x[i][k], e), acc[g][k][e]);
+          }
+        }
+      }
+    }
+  }
+  float* prow = P.part + (int64_t)blockIdx.x * nq * P.d;
+#pragma unroll
+  for (int g = 0; g < QG; ++g) {
+    if (g >= ng) break;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      if (!ok[k]) continue;
+      float4* dst = reinterpret_cast<float4*>(prow + (int64_t)(q0 + g) * P.d + (int64_t)chunk[k] * VEC);
+#pragma unroll
+      for (int h = 0; h < VEC / 4; ++h)
+        dst[h] = make_float4(acc[g][k][4 * h], acc[g][k][4 * h + 1], acc[g][k][4 * h + 2], acc[g][k][4 * h + 3]);
+    }
+  }
+}
+
+
 // ------------------------------------------------ merge backward body --
 
 // VEC consecutive elements of a bf16 or fp32 row as fp32 (chunk = VEC elements).
@@ -1777,18 +2089,20 @@ __device__ __forceinline__ void reduce_dqw_stage_body(const attnres_reduce_param
   __shared__ float red[4][64];
   const int lane = threadIdx.x & 63;
   const int slice = threadIdx.x >> 6;
+  const int width = P.d * (P.num_queries > 1 ? P.num_queries : 1);
   const int col = blockIdx.x * 64 + lane;
   const int row0 = blockIdx.y * 64;
   float acc = 0.f;
-  if (col < P.d) {
+  if (col < width) {
     const int r0 = row0 + slice * 16;
     const int r1 = r0 + 16 < P.nparts ? r0 + 16 : P.nparts;
 #pragma unroll 16
-    for (int r = r0; r < r1; ++r) acc += P.part[(int64_t)r * P.d + col];
+    for (int r = r0; r < r1; ++r) acc += P.part[(int64_t)r * width + col];
   }
   red[slice][lane] = acc;
   __syncthreads();
-  if (slice == 0 && col < P.d) P.part[(int64_t)row0 * P.d + col] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  if (slice == 0 && col < width)
+    P.part[(int64_t)row0 * width + col] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
 }
 
 // Final stage: sum the partial rows 0, part_step, 2*part_step, ... column by
@@ -1797,23 +2111,28 @@ __device__ __forceinline__ void reduce_dqw_stage_body(const attnres_reduce_param
 __device__ __forceinline__ void reduce_dqw_body(const attnres_reduce_params& P) {
   const int col = blockIdx.x * blockDim.x + threadIdx.x;
   if (col >= P.d) return;
-  float acc = 0.f;
-  for (int p = 0; p < P.nparts; p += P.part_step) acc += P.part[(int64_t)p * P.d + col];
-  float q, g = 1.f;
-  if (P.param_bf16) {
-    q = bf_lo(reinterpret_cast<const uint16_t*>(P.query)[col]);
-    if (P.gain) g = bf_lo(reinterpret_cast<const uint16_t*>(P.gain)[col]);
-  } else {
-    q = reinterpret_cast<const float*>(P.query)[col];
-    if (P.gain) g = reinterpret_cast<const float*>(P.gain)[col];
+  const int nq = P.num_queries > 1 ? P.num_queries : 1;
+  const int64_t width = (int64_t)P.d * nq;
+  float g = 1.f;
+  if (P.gain) g = P.param_bf16 ? bf_lo(reinterpret_cast<const uint16_t*>(P.gain)[col])
+                               : reinterpret_cast<const float*>(P.gain)[col];
+  float dg = 0.f;
+  for (int qi = 0; qi < nq; ++qi) {
+    const int64_t c = (int64_t)qi * P.d + col;
+    float acc = 0.f;
+    for (int p = 0; p < P.nparts; p += P.part_step) acc += P.part[(int64_t)p * width + c];
+    const float q = P.param_bf16 ? bf_lo(reinterpret_cast<const uint16_t*>(P.query)[c])
+                                 : reinterpret_cast<const float*>(P.query)[c];
+    const float dq = P.gain ? acc * g : acc;
+    dg = __builtin_fmaf(acc, q, dg);
+    if (P.dquery) {
+      if (P.param_bf16) reinterpret_cast<__bf16*>(P.dquery)[c] = (__bf16)dq;
+      else reinterpret_cast<float*>(P.dquery)[c] = dq;
+    }
   }
-  const float dq = P.gain ? acc * g : acc;
-  if (P.param_bf16) {
-    if (P.dquery) reinterpret_cast<__bf16*>(P.dquery)[col] = (__bf16)dq;
-    if (P.dgain) reinterpret_cast<__bf16*>(P.dgain)[col] = (__bf16)(acc * q);
-  } else {
-    if (P.dquery) reinterpret_cast<float*>(P.dquery)[col] = dq;
-    if (P.dgain) reinterpret_cast<float*>(P.dgain)[col] = acc * q;
+  if (P.dgain) {
+    if (P.param_bf16) reinterpret_cast<__bf16*>(P.dgain)[col] = (__bf16)dg;
+    else reinterpret_cast<float*>(P.dgain)[col] = dg;
   }
 }
 
@@ -2023,4 +2342,34 @@ BWD_S(13)
 BWD_S(14)
 BWD_S(15)
 BWD_S(16)
+#endif
+
+// Batched-query backward: attnres_route_bwd_mq_<in>_g<grad_out>_s<S>_v<V>,
+// instantiated where the per-thread source-gradient accumulators (S * VEC * V
+// floats) stay within 72 registers; attnres_route_bwd_dqw_<in>_v<V>.
+#define BWD_MQ_ONE(INNAME, BF, GNAME, GBF, S, V)                                                  \
+  extern "C" __global__ void __launch_bounds__(512)                                               \
+  attnres_route_bwd_mq_##INNAME##_g##GNAME##_s##S##_v##V(attnres_route_bwd_mq_params P) {       \
+    route_bwd_mq_body<S, V, BF, GBF>(P);                                                          \
+  }
+#define BWD_MQ(INNAME, BF, S, V) \
+  BWD_MQ_ONE(INNAME, BF, bf, true, S, V) \
+  BWD_MQ_ONE(INNAME, BF, f32, false, S, V)
+#define BWD_DQW(INNAME, BF, V)                                                                   \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+  attnres_route_bwd_dqw_##INNAME##_v##V(attnres_route_bwd_dqw_params P) {                        \
+    route_bwd_dqw_body<V, BF>(P);                                                                \
+  }
+#if ATTNRES_PART == 6 || defined(ATTNRES_ALL_PARTS)
+BWD_MQ(bf, true, 1, 1) BWD_MQ(bf, true, 2, 1) BWD_MQ(bf, true, 3, 1) BWD_MQ(bf, true, 4, 1) BWD_MQ(bf, true, 5, 1)
+BWD_MQ(bf, true, 6, 1) BWD_MQ(bf, true, 7, 1) BWD_MQ(bf, true, 8, 1) BWD_MQ(bf, true, 9, 1)
+BWD_MQ(bf, true, 1, 2) BWD_MQ(bf, true, 2, 2) BWD_MQ(bf, true, 3, 2) BWD_MQ(bf, true, 4, 2)
+BWD_MQ(f32, false, 1, 1) BWD_MQ(f32, false, 2, 1) BWD_MQ(f32, false, 3, 1) BWD_MQ(f32, false, 4, 1)
+BWD_MQ(f32, false, 5, 1) BWD_MQ(f32, false, 6, 1) BWD_MQ(f32, false, 7, 1) BWD_MQ(f32, false, 8, 1)
+BWD_MQ(f32, false, 9, 1) BWD_MQ(f32, false, 10, 1) BWD_MQ(f32, false, 11, 1) BWD_MQ(f32, false, 12, 1)
+BWD_MQ(f32, false, 13, 1) BWD_MQ(f32, false, 14, 1) BWD_MQ(f32, false, 15, 1) BWD_MQ(f32, false, 16, 1)
+BWD_MQ(f32, false, 1, 2) BWD_MQ(f32, false, 2, 2) BWD_MQ(f32, false, 3, 2) BWD_MQ(f32, false, 4, 2)
+BWD_MQ(f32, false, 5, 2) BWD_MQ(f32, false, 6, 2) BWD_MQ(f32, false, 7, 2) BWD_MQ(f32, false, 8, 2)
+BWD_MQ(f32, false, 9, 2)
+BWD_DQW(bf, true, 1) BWD_DQW(bf, true, 2) BWD_DQW(f32, false, 1) BWD_DQW(f32, false, 2)
 #endif

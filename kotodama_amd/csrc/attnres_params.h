@@ -89,17 +89,65 @@ typedef struct attnres_route_bwd_params {
   float inv_d;
 } attnres_route_bwd_params;
 
+/*
+ * Backward of Q >= 2 queries over one set of sources (the batched phase-1
+ * call), source gradients in one pass:
+ *   dx_s = sum_q (w_qs G_q + c1_qs qw_q) + (sum_q c2_qs) x_s
+ * with c1_qs stored to `c1` (n_tokens, Q, S) for the query gradients.
+ */
+typedef struct attnres_route_bwd_mq_params {
+  const void* src[ATTNRES_KMAX_SOURCES];
+  void* dsrc[ATTNRES_KMAX_SOURCES];
+  const void* query;     /* (Q, d) param dtype */
+  const void* gain;      /* (d,) param dtype, or NULL */
+  const void* grad_out;  /* (Q, n_tokens) rows of gout_ld, query stride gout_qstride */
+  const float* grad_lse; /* (Q, n_tokens) or NULL */
+  float* c1;             /* (n_tokens, Q, S) fp32 */
+  int64_t n_tokens;
+  int64_t src_ld;
+  int64_t dsrc_ld;
+  int64_t gout_ld;
+  int64_t gout_qstride;
+  int32_t d;
+  int32_t nchunk;
+  int32_t num_queries;
+  int32_t param_bf16;
+  int32_t block;
+  float eps;
+  float inv_d;
+} attnres_route_bwd_mq_params;
+
+/*
+ * Query-gradient partials of the batched backward: per workgroup
+ *   part[wg][q][:] = sum over its rows, sources of c1_qs x_s
+ * for queries q0 .. q0+7 (one more pass over the sources).
+ */
+typedef struct attnres_route_bwd_dqw_params {
+  const void* src[ATTNRES_KMAX_SOURCES];
+  const float* c1;  /* (n_tokens, Q, S) */
+  float* part;      /* (gridDim.x, Q, d) */
+  int64_t n_tokens;
+  int64_t src_ld;
+  int32_t d;
+  int32_t nchunk;
+  int32_t num_sources;
+  int32_t num_queries;
+  int32_t q0;
+  int32_t block;
+} attnres_route_bwd_dqw_params;
+
 /* Column reduction of the dqw partials into the parameter gradients. */
 typedef struct attnres_reduce_params {
-  float* part;        /* (nparts, d); stage 1 overwrites rows 0, 64, 128, ... */
-  const void* query;  /* (d,) param dtype */
+  float* part;        /* (nparts, num_queries * d); stage 1 overwrites rows 0, 64, 128, ... */
+  const void* query;  /* (num_queries, d) param dtype */
   const void* gain;   /* (d,) param dtype, or NULL */
-  void* dquery;       /* (d,) param dtype: dqw * gain (dqw when gain is NULL) */
-  void* dgain;        /* (d,) param dtype: dqw * query, or NULL */
+  void* dquery;       /* (num_queries, d) param dtype: dqw * gain (dqw when gain is NULL) */
+  void* dgain;        /* (d,) param dtype: sum over queries of dqw * query, or NULL */
   int32_t nparts;     /* rows of `part` written by the backward kernel */
   int32_t part_step;  /* final stage sums rows 0, part_step, 2*part_step, ... */
   int32_t d;
   int32_t param_bf16;
+  int32_t num_queries; /* 0 or 1: one query */
 } attnres_reduce_params;
 
 /*

@@ -345,6 +345,47 @@ def _launch_route_bwd(
     return dq.reshape(query.shape), dg
 
 
+def _launch_route_bwd_queries(
+    ptrs: list[int],
+    grad_ptrs: list[int],
+    src_dtype: torch.dtype,
+    n: int,
+    d: int,
+    device: torch.device,
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    grad_out: Tensor,
+    grad_lse: Optional[Tensor],
+) -> Optional[tuple[Tensor, Optional[Tensor]]]:
+    """Launch attnres_route_bwd_queries for Q >= 2 queries; (grad_query (Q, D), grad_gain), or None
+    when the library has no batched kernel for the shape (nothing was written)."""
+    nq = query.shape[0]
+    mixed = gain is not None and gain.dtype != query.dtype
+    kq, kg, pcode = _fold_query(query, gain)
+    dq = torch.empty((nq, d), device=device, dtype=kq.dtype)
+    dg = torch.empty(d, device=device, dtype=kg.dtype) if kg is not None else None
+    grad_out = grad_out.reshape(nq, n, d).contiguous()
+    if grad_lse is not None:
+        grad_lse = grad_lse.reshape(nq, n).to(torch.float32).contiguous()
+    with _DeviceStream(device) as stream:
+        nbytes = _capi.route_bwd_queries_workspace_size(n, d, len(ptrs), nq)
+        ws = torch.empty(max(1, (nbytes + 3) // 4), device=device, dtype=torch.float32)
+        code = _capi.route_bwd_queries(
+            _capi.pointer_array(ptrs), len(ptrs), n, d, d, dtype_code(src_dtype), kq.data_ptr(),
+            kg.data_ptr() if kg is not None else None, nq, pcode, float(eps), grad_out.data_ptr(),
+            dtype_code(grad_out.dtype), d, n * d, grad_lse.data_ptr() if grad_lse is not None else None,
+            _capi.pointer_array(grad_ptrs), d, ws.data_ptr(), ws.numel() * 4, dq.data_ptr(),
+            dg.data_ptr() if dg is not None else None, stream,
+        )
+    if code != _capi.OK:
+        return None
+    if mixed:
+        # dq is dL/dqw for qw = query * gain taken in the promoted dtype
+        return (dq * gain).to(query.dtype), (dq * query).sum(0).to(gain.dtype)
+    return dq, dg
+
+
 def _bwd_args(grad_out: Optional[Tensor], n_out_shape, device, dt) -> Tensor:
     if grad_out is None:
         grad_out = torch.zeros(n_out_shape, device=device, dtype=dt)
@@ -363,10 +404,12 @@ def _route_bwd_any(
     """Backward over contiguous sources into the preallocated ``grads``.
 
     One query: one attnres_route_bwd call.  Q > 1 queries (the batched
-    phase-1 call): one call per query on fp32 copies of the sources, the
-    source gradients summed in fp32 and rounded once, the query gradients
-    stacked and the gain gradients summed (ops/phase_1.py:160-170 accumulates
-    the same sum over queries).
+    phase-1 call): attnres_route_bwd_queries, one pass over the sources for
+    all queries (ops/phase_1.py:160-170 accumulates the same sum over
+    queries); for shapes it does not cover, one attnres_route_bwd call per
+    query on fp32 copies of the sources, the source gradients summed in fp32
+    and rounded once, the query gradients stacked and the gain gradients
+    summed.
     """
     device = srcs[0].device
     d = srcs[0].shape[-1]
@@ -377,6 +420,12 @@ def _route_bwd_any(
             eps, grad_out, grad_lse,
         )
     nq = query.shape[0]
+    res = _launch_route_bwd_queries(
+        [t.data_ptr() for t in srcs], [g.data_ptr() for g in grads], srcs[0].dtype, n, d, device, query, gain, eps,
+        grad_out, grad_lse,
+    )
+    if res is not None:
+        return res
     s32 = [t.float().contiguous() for t in srcs]
     acc = [torch.zeros(t.shape, device=device, dtype=torch.float32) for t in srcs]
     tmp = [torch.empty(t.shape, device=device, dtype=torch.float32) for t in srcs]

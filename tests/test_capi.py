@@ -126,6 +126,31 @@ def test_route_bwd_argument_errors():
     assert "grad_sources[1]" in _capi.lib().attnres_last_error().decode()
 
 
+def bwdq(sources=None, S=None, N=16, D=64, Q=3, sdt=_capi.DTYPE_BF16, gain=None, gld=None, gqs=None, ws=FAKE,
+         dq=FAKE, dg=None):
+    sources = [FAKE + 4096 * i for i in range(3)] if sources is None else sources
+    grads = [FAKE + (1 << 20) + 4096 * i for i in range(len(sources))]
+    S = len(sources) if S is None else S
+    gld = D if gld is None else gld
+    return _capi.lib().attnres_route_bwd_queries(
+        _capi.pointer_array(sources), S, N, D, D, sdt, FAKE, gain, Q, _capi.DTYPE_BF16, 1e-5, FAKE,
+        _capi.DTYPE_BF16, gld, N * gld if gqs is None else gqs, None, _capi.pointer_array(grads), D, ws, 1 << 30,
+        dq, dg, None)
+
+
+def test_route_bwd_queries_argument_errors():
+    assert bwdq(N=0) == _capi.OK  # no tokens: returns before any HIP call
+    assert bwdq(S=0) == _capi.ERR_UNSUPPORTED
+    assert bwdq(Q=0) == _capi.ERR_ARG
+    assert bwdq(dg=FAKE) == _capi.ERR_ARG  # grad_gain without gain
+    assert bwdq(gqs=8) == _capi.ERR_ARG  # query blocks of grad_out overlap
+    # bf16 sources, one chunk per thread: batched kernels up to S = 9
+    srcs = [FAKE + 4096 * i for i in range(10)]
+    assert bwdq(sources=srcs) == _capi.ERR_UNSUPPORTED
+    assert "attnres_route_bwd once per query" in _capi.lib().attnres_last_error().decode()
+    assert bwdq(D=12) == _capi.ERR_UNSUPPORTED
+
+
 def test_merge_bwd_argument_errors():
     lib = _capi.lib()
     args = [FAKE, 16, 64, _capi.DTYPE_BF16, FAKE, _capi.DTYPE_BF16, FAKE, _capi.DTYPE_BF16, FAKE, 1e-5, FAKE,

@@ -220,6 +220,56 @@ def test_multi_query_phase_1_backward(gpu):
     assert torch.all(buf.grad[S:] == 0)
 
 
+MQ_CASES = [
+    # (dtype, S, D, B, T, Q, with gain, batched kernel expected)
+    (torch.bfloat16, 1, 1024, 2, 20, 2, False, True),
+    (torch.bfloat16, 7, 3072, 1, 40, 9, True, True),
+    (torch.bfloat16, 9, 2048, 2, 12, 4, False, True),
+    (torch.bfloat16, 3, 8192, 1, 16, 3, True, True),
+    (torch.bfloat16, 12, 1024, 1, 24, 3, False, False),
+    (torch.float32, 16, 1024, 1, 20, 2, True, True),
+    (torch.float32, 5, 4096, 1, 16, 9, False, True),
+]
+
+
+@pytest.mark.parametrize("dtype,S,D,B,T,Q,with_gain,batched", MQ_CASES,
+                         ids=[f"{str(c[0])[6:]}-S{c[1]}-D{c[2]}-Q{c[5]}" for c in MQ_CASES])
+def test_batched_query_backward_matches_oracle(gpu, monkeypatch, dtype, S, D, B, T, Q, with_gain, batched):
+    # Q queries over one stack with an lse term: the source gradients summed
+    # over the queries, every query's gradient and the gain gradient summed
+    # over the queries; one pass of attnres_route_bwd_queries where a batched
+    # kernel exists (nine queries: two passes of the query-gradient kernel),
+    # one attnres_route_bwd per query otherwise
+    print(f"batched-query backward {dtype} S={S} D={D} Q={Q} gain={with_gain}", flush=True)
+    eps = 1e-5
+    buf, _, _, _ = make_case(gpu, S, 0, B, T, D, dtype, seed=60 + S + Q)
+    g = torch.Generator(device="cpu").manual_seed(61 + D)
+    qs = (torch.randn(Q, D, generator=g) * 0.05).to(dtype).to(gpu).requires_grad_(True)
+    gain = (1 + 0.1 * torch.randn(D, generator=g)).to(dtype).to(gpu).requires_grad_(True) if with_gain else None
+    G = torch.randn(Q, B, T, D, generator=g).to(torch.bfloat16).float().to(gpu)
+    GL = torch.randn(Q, B, T, generator=g).to(gpu)
+    buf.requires_grad_(True)
+    per_query = []
+    real = ops._launch_route_bwd
+    monkeypatch.setattr(ops, "_launch_route_bwd", lambda *a: per_query.append(1) or real(*a))
+    out, _, lse, _, _ = ops.route(buf, S, qs, gain, eps, dtype, True, False)
+    (out.float() * G).sum().add_((lse * GL).sum()).backward()
+    assert (len(per_query) == 0) == batched, f"per-query launches: {len(per_query)}"
+    pd = "bf16" if dtype == torch.bfloat16 else "f32"
+    x = np64(buf).reshape(S, -1, D)
+    dx = np.zeros_like(x)
+    dgain = np.zeros(D)
+    for j in range(Q):
+        qw = O.fold_query(np64(qs[j]), np64(gain) if with_gain else None, pd)
+        b = O.route_backward(x, qw, eps, np64(G[j]).reshape(-1, D), np64(GL[j]).reshape(-1))
+        dx += b["dx"]
+        check_grad(qs.grad[j], b["dqw"] * (np64(gain) if with_gain else 1.0), dtype, f"dquery[{j}]")
+        dgain += b["dqw"] * np64(qs[j])
+    check_grad(buf.grad.reshape(S, -1, D), dx, dtype, "dsources (sum over queries)")
+    if with_gain:
+        check_grad(gain.grad, dgain, dtype, "dgain (sum over queries)")
+
+
 MERGE_CASES = [
     (torch.bfloat16, torch.bfloat16, 3072),
     (torch.bfloat16, torch.bfloat16, 8192),
