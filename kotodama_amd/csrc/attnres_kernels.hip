@@ -297,6 +297,74 @@ __device__ __forceinline__ float param_elem(const ParamRaw<VEC>& r, int e, bool 
   return as_f32(r.w[e >> 2][e & 3]);
 }
 
+// ------------------------------------------------ wave reductions --
+
+// Exchange lanes 32..63 of a with lanes 0..31 of b (v_permlane32_swap), and
+// the odd 16-lane rows of a with the even rows of b (v_permlane16_swap).  The
+// leading s_nop covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void swap_halves32(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap_rows16(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max(float v) {
+  const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false);
+  return __builtin_fmaxf(v, __builtin_bit_cast(float, t));
+}
+
+// Max / sum over aligned segments of SEG (8 or 16) lanes, result in every
+// lane of the segment: quad_perm[1,0,3,2], quad_perm[2,3,0,1],
+// row_half_mirror (8 lanes), row_mirror (16 lanes).
+template <int SEG>
+__device__ __forceinline__ float seg_max(float v) {
+  v = dpp_max<0xB1, 0xF>(v);
+  v = dpp_max<0x4E, 0xF>(v);
+  v = dpp_max<0x141, 0xF>(v);
+  if constexpr (SEG == 16) v = dpp_max<0x140, 0xF>(v);
+  return v;
+}
+template <int SEG>
+__device__ __forceinline__ float seg_sum(float v) {
+  v = dpp_add<0xB1, 0xF>(v);
+  v = dpp_add<0x4E, 0xF>(v);
+  v = dpp_add<0x141, 0xF>(v);
+  if constexpr (SEG == 16) v = dpp_add<0x140, 0xF>(v);
+  return v;
+}
+
+// Sum over the 64 lanes of each of NP = 4*H2 values part[0..NP), written to
+// red_row[v] for every v < NP by the first lane of each 16-lane row.  Two
+// swap rounds leave register j of row rho holding value
+// j + (rho & 1) * H2 + (rho >> 1) * 2 * H2 (summed over 4 lanes); four DPP
+// steps finish the 16-lane row sums.
+template <int H2>
+__device__ __forceinline__ void wave_reduce_to_lds(float (&part)[4 * H2], float* red_row, int lane) {
+  constexpr int H1 = 2 * H2;
+  float r1[H1];
+#pragma unroll
+  for (int j = 0; j < H1; ++j) {
+    float a = part[j], b = part[j + H1];
+    swap_halves32(a, b);
+    r1[j] = a + b;
+  }
+  float r2[H2];
+#pragma unroll
+  for (int j = 0; j < H2; ++j) {
+    float a = r1[j], b = r1[j + H2];
+    swap_rows16(a, b);
+    r2[j] = seg_sum<16>(a + b);
+  }
+  const int rho = lane >> 4;
+  if ((lane & 15) == 0) {
+    float* dst = red_row + (rho & 1) * H2 + (rho >> 1) * H1;
+#pragma unroll
+    for (int j = 0; j < H2; ++j) dst[j] = r2[j];
+  }
+}
+
 // ------------------------------------------------------------ route body --
 
 // S     : number of active sources (0 writes NaN, as softmax over no sources)
@@ -309,8 +377,9 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
   using C = Chunk<BF16>;
   constexpr int VEC = C::VEC;
   constexpr int NV = 2 * S;                  // sum(x^2) and x.qw per source
-  constexpr int RLD = ((NV + 3) / 4) * 4;    // row pitch of the LDS exchange
-  __shared__ float red[2][ATTNRES_KMAX_WAVES][RLD > 0 ? RLD : 4];
+  constexpr int NP = ((NV + 3) / 4) * 4 > 0 ? ((NV + 3) / 4) * 4 : 4;  // padded for the reduction
+  constexpr int SEG = S <= 8 ? 8 : 16;       // lanes of the depth softmax
+  __shared__ float red[2][ATTNRES_KMAX_WAVES][NP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -318,6 +387,8 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
   const int block = P.block;
   const int nwaves = (block + 63) >> 6;
   const int nq = MULTIQ ? P.num_queries : 1;
+  const int ls = lane % SEG;  // the source of this lane in the softmax
+  const bool slot = ls < S;
 
   int chunk[V];
   bool ok[V];
@@ -463,12 +534,13 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
         }
       }
 
-      float ss_tot[S];
       for (int q = 0; q < nq; ++q) {
         if constexpr (MULTIQ) fetch_qw(q);
 
         // ---- per-thread partial sums ----
-        float part[NV];
+        float part[NP];
+#pragma unroll
+        for (int j = NV; j < NP; ++j) part[j] = 0.f;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           float ss = 0.f, dt = 0.f;
@@ -498,57 +570,35 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
           part[S + s] = dt;
         }
 
-        // ---- wave reduce, then one LDS exchange across the waves ----
-#pragma unroll
-        for (int j = 0; j < NV; ++j) part[j] = wave_sum_to_lane63(part[j]);
-        if (lane == 63) {
-#pragma unroll
-          for (int j = 0; j < NV; ++j) red[ph][wave][j] = part[j];
-        }
+        // ---- transposing wave reduction, one LDS exchange across the waves ----
+        wave_reduce_to_lds<NP / 4>(part, red[ph][wave], lane);
         __syncthreads();
-        float tot[NV];
-#pragma unroll
-        for (int j = 0; j < NV; ++j) tot[j] = 0.f;
-        for (int w = 0; w < nwaves; ++w) {
-#pragma unroll
-          for (int j = 0; j < NV; ++j) tot[j] += red[ph][w][j];
+
+        // ---- softmax over depth, lane s per source (segments of SEG lanes) ----
+        float t_ss = 0.f, t_dot = 0.f;
+        if (slot) {
+          for (int w = 0; w < nwaves; ++w) {
+            t_ss += red[ph][w][ls];
+            t_dot += red[ph][w][S + ls];
+          }
         }
         ph ^= 1;
-
-        // ---- softmax over depth ----
-        float logit[S], wgt[S];
-        float m = -__builtin_inff();
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          if (q == 0) ss_tot[s] = __builtin_amdgcn_rsqf(tot[s] * P.inv_d + P.eps);
-          logit[s] = tot[S + s] * ss_tot[s];
-          m = __builtin_fmaxf(m, logit[s]);
+        const float inv = __builtin_amdgcn_rsqf(t_ss * P.inv_d + P.eps);
+        const float logit = slot ? t_dot * inv : -__builtin_inff();
+        const float m = seg_max<SEG>(logit);
+        const float el = slot ? __expf(logit - m) : 0.f;
+        const float sum = seg_sum<SEG>(el);
+        const float wl = el * (1.0f / sum);
+        if (wave == 0 && lane < S) {
+          if (P.weights) P.weights[((int64_t)q * S + lane) * P.n_tokens + tok] = wl;
+          if (P.logits) P.logits[((int64_t)q * P.n_tokens + tok) * S + lane] = logit;
+          if (q == 0 && P.inv_rms) P.inv_rms[tok * S + lane] = inv;
+          if (lane == 0 && P.lse) P.lse[(int64_t)q * P.n_tokens + tok] = m + __logf(sum);
         }
-        float sum = 0.f;
+        float wgt[S];
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-          wgt[s] = __expf(logit[s] - m);
-          sum += wgt[s];
-        }
-        const float rsum = 1.0f / sum;
-#pragma unroll
-        for (int s = 0; s < S; ++s) wgt[s] *= rsum;
-
-        if (tid == 0) {
-          if (P.weights) {
-#pragma unroll
-            for (int s = 0; s < S; ++s) P.weights[((int64_t)q * S + s) * P.n_tokens + tok] = wgt[s];
-          }
-          if (P.lse) P.lse[(int64_t)q * P.n_tokens + tok] = m + __logf(sum);
-          if (P.logits) {
-#pragma unroll
-            for (int s = 0; s < S; ++s) P.logits[((int64_t)q * P.n_tokens + tok) * S + s] = logit[s];
-          }
-          if (q == 0 && P.inv_rms) {
-#pragma unroll
-            for (int s = 0; s < S; ++s) P.inv_rms[tok * S + s] = ss_tot[s];
-          }
-        }
+        for (int s = 0; s < S; ++s)
+          wgt[s] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), s));
 
         // ---- weighted sum of the raw sources, one output row ----
         // The empty asm makes the rows opaque here, so the compiler re-unpacks
@@ -631,72 +681,6 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
 // unpacked sources share the register file; beyond S = 5 a group of 8 drops
 // the kernel to two waves per SIMD, which measured slower than groups of 4.
 #define QG_OF(S) ((S) <= 5 ? 8 : (S) <= 12 ? 4 : 2)
-
-// Exchange lanes 32..63 of a with lanes 0..31 of b (v_permlane32_swap), and
-// the odd 16-lane rows of a with the even rows of b (v_permlane16_swap).  The
-// leading s_nop covers the VALU-write -> permlane-read hazard.
-__device__ __forceinline__ void swap_halves32(float& a, float& b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ void swap_rows16(float& a, float& b) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_max(float v) {
-  const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false);
-  return __builtin_fmaxf(v, __builtin_bit_cast(float, t));
-}
-
-// Max / sum over aligned segments of SEG (8 or 16) lanes, result in every
-// lane of the segment: quad_perm[1,0,3,2], quad_perm[2,3,0,1],
-// row_half_mirror (8 lanes), row_mirror (16 lanes).
-template <int SEG>
-__device__ __forceinline__ float seg_max(float v) {
-  v = dpp_max<0xB1, 0xF>(v);
-  v = dpp_max<0x4E, 0xF>(v);
-  v = dpp_max<0x141, 0xF>(v);
-  if constexpr (SEG == 16) v = dpp_max<0x140, 0xF>(v);
-  return v;
-}
-template <int SEG>
-__device__ __forceinline__ float seg_sum(float v) {
-  v = dpp_add<0xB1, 0xF>(v);
-  v = dpp_add<0x4E, 0xF>(v);
-  v = dpp_add<0x141, 0xF>(v);
-  if constexpr (SEG == 16) v = dpp_add<0x140, 0xF>(v);
-  return v;
-}
-
-// Sum over the 64 lanes of each of NP = 4*H2 values part[0..NP), written to
-// red_row[v] for every v < NP by the first lane of each 16-lane row.  Two
-// swap rounds leave register j of row rho holding value
-// j + (rho & 1) * H2 + (rho >> 1) * 2 * H2 (summed over 4 lanes); four DPP
-// steps finish the 16-lane row sums.
-template <int H2>
-__device__ __forceinline__ void wave_reduce_to_lds(float (&part)[4 * H2], float* red_row, int lane) {
-  constexpr int H1 = 2 * H2;
-  float r1[H1];
-#pragma unroll
-  for (int j = 0; j < H1; ++j) {
-    float a = part[j], b = part[j + H1];
-    swap_halves32(a, b);
-    r1[j] = a + b;
-  }
-  float r2[H2];
-#pragma unroll
-  for (int j = 0; j < H2; ++j) {
-    float a = r1[j], b = r1[j + H2];
-    swap_rows16(a, b);
-    r2[j] = seg_sum<16>(a + b);
-  }
-  const int rho = lane >> 4;
-  if ((lane & 15) == 0) {
-    float* dst = red_row + (rho & 1) * H2 + (rho >> 1) * H1;
-#pragma unroll
-    for (int j = 0; j < H2; ++j) dst[j] = r2[j];
-  }
-}
 
 template <int S, int V>
 __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
