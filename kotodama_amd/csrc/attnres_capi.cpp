@@ -107,14 +107,20 @@ std::atomic<int> g_policy{ATTNRES_POLICY_AUTO};
 // Tuning knobs read once: ATTNRES_V forces chunks per thread (1 or 2) of the
 // row-per-workgroup kernels, ATTNRES_STREAM / ATTNRES_STREAM_MIN_TOKENS choose
 // when the row-per-wave streaming kernels run, ATTNRES_GRID_MULT scales the
-// resident-workgroup grid, ATTNRES_QG=0 turns off the batched-query kernel.
+// resident-workgroup grid, ATTNRES_STREAM_PER_CU sets the streaming kernels'
+// workgroups per CU (0: the occupancy limit), ATTNRES_BWD_PER_CU the
+// backward's, ATTNRES_QG=0 turns off the batched-query kernel.
 struct Tuning {
   int force_v = 0;
   int qg = 1;
   int stream = -1;  // -1: by size, 0: never, 1: whenever the shape allows
   int64_t stream_min_tokens = 2048;
   double grid_mult = 1.0;
+  double stream_per_cu = 1.0;  // workgroups per CU of the streaming kernels
+  int bwd_per_cu = 0;          // > 0: resident workgroups per CU of the routing backward
   Tuning() {
+    if (const char* v = std::getenv("ATTNRES_BWD_PER_CU")) bwd_per_cu = std::atoi(v);
+    if (const char* v = std::getenv("ATTNRES_STREAM_PER_CU")) stream_per_cu = std::atof(v);
     if (const char* v = std::getenv("ATTNRES_V")) force_v = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_QG")) qg = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_STREAM")) stream = std::atoi(v);
@@ -597,7 +603,17 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   P.block = block;
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
-  return launch(f, grid_for(work_units, st->num_cus, bpc), block, P, stream, 1, ch.qg_lds);
+  // The streaming kernels run one 4-wave workgroup per CU: at the occupancy
+  // limit (up to four per CU) four times the requests are in flight and the
+  // same traffic measured 4-6% slower.
+  int grid = grid_for(work_units, st->num_cus, bpc);
+  if (ch.stream && tuning().stream_per_cu > 0.0) {
+    int64_t g = (int64_t)(st->num_cus * (tuning().stream_per_cu < bpc ? tuning().stream_per_cu : (double)bpc));
+    if (g < 1) g = 1;
+    if (g > work_units) g = work_units;
+    grid = (int)g;
+  }
+  return launch(f, grid, block, P, stream, 1, ch.qg_lds);
 }
 
 // Query/gain gradients from `nparts` per-workgroup partial rows in
@@ -833,7 +849,7 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   // Resident workgroups per CU: more than two (where registers allow three or
   // four) measured 4-12% slower for S >= 2 at the 3B shapes; S = 1 gains
   // from a third.
-  const int per_cu = num_sources == 1 ? 3 : 2;
+  const int per_cu = tuning().bwd_per_cu > 0 ? tuning().bwd_per_cu : num_sources == 1 ? 3 : 2;
   int64_t grid = (int64_t)st->num_cus * (bpc < per_cu ? bpc : per_cu);
   if (grid > num_tokens) grid = num_tokens;
   const int64_t need = grid * (int64_t)hidden * (int64_t)sizeof(float);
