@@ -834,7 +834,8 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
-  const int v = round64(nchunk) <= kMaxThreads ? 1 : 2;
+  // one chunk per thread where the row fits in one workgroup (ATTNRES_V=2 forces two)
+  const int v = round64(nchunk) <= kMaxThreads && tuning().force_v != 2 ? 1 : 2;
   const int block = v == 1 ? round64(nchunk) : round64((nchunk + 1) / 2);
   hipFunction_t f = nullptr;
   int bpc = 1;
