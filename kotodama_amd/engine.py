@@ -69,7 +69,7 @@ class BlockArena:
         Returns the routed ``(*batch, D)`` row block, or ``(out, weights,
         lse)`` when ``want_weights``.
         """
-        out, w, lse = ops.block_step(self.buf, self.n_committed, commit, delta, query, gain, eps, want_weights)
+        out, w, lse = ops.block_step_call(self.buf, self.n_committed, commit, delta, query, gain, eps, want_weights)
         if commit:
             self.n_committed += 1
         return (out, w, lse) if want_weights else out

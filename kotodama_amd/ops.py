@@ -803,17 +803,7 @@ merge.register_autograd(_merge_backward, setup_context=_merge_setup_context)
 # ------------------------------------------------------------- block step --
 
 
-@torch.library.custom_op("attnres_hip::block_step", mutates_args=("arena",))
-def block_step(
-    arena: Tensor,
-    n_committed: int,
-    commit: bool,
-    delta: Optional[Tensor],
-    query: Tensor,
-    gain: Optional[Tensor],
-    eps: float,
-    want_weights: bool,
-) -> tuple[Tensor, Tensor, Tensor]:
+def _block_step_impl(arena, n_committed, commit, delta, query, gain, eps, want_weights, placeholders=True):
     device = _require_device(arena, delta, query, gain)
     if not arena.is_contiguous():
         raise ValueError("attnres_hip::block_step: the arena must be contiguous")
@@ -833,9 +823,11 @@ def block_step(
     if want_weights:
         weights = torch.empty((s, *batch), device=device, dtype=f32)
         lse = torch.empty(batch, device=device, dtype=f32)
-    else:
+    elif placeholders:
         weights = torch.empty((0,), device=device, dtype=f32)
         lse = torch.empty((0,), device=device, dtype=f32)
+    else:
+        weights = lse = None
     with _DeviceStream(device) as stream:
         _capi.block_step(
             arena.data_ptr(),
@@ -852,11 +844,32 @@ def block_step(
             pcode,
             float(eps),
             out.data_ptr() if out.numel() else None,
-            weights.data_ptr() if weights.numel() else None,
-            lse.data_ptr() if lse.numel() else None,
+            weights.data_ptr() if weights is not None and weights.numel() else None,
+            lse.data_ptr() if lse is not None and lse.numel() else None,
             stream,
         )
     return out, weights, lse
+
+
+@torch.library.custom_op("attnres_hip::block_step", mutates_args=("arena",))
+def block_step(
+    arena: Tensor,
+    n_committed: int,
+    commit: bool,
+    delta: Optional[Tensor],
+    query: Tensor,
+    gain: Optional[Tensor],
+    eps: float,
+    want_weights: bool,
+) -> tuple[Tensor, Tensor, Tensor]:
+    return _block_step_impl(arena, n_committed, commit, delta, query, gain, eps, want_weights)
+
+
+def block_step_call(arena, n_committed, commit, delta, query, gain, eps, want_weights=False) -> tuple:
+    """:func:`block_step`, launched directly when nothing needs the dispatcher."""
+    if _eager_direct(arena, delta, query, gain):
+        return _block_step_impl(arena, n_committed, commit, delta, query, gain, eps, want_weights, placeholders=False)
+    return block_step(arena, n_committed, commit, delta, query, gain, eps, want_weights)
 
 
 @block_step.register_fake
@@ -887,4 +900,5 @@ __all__ = [
     "route_call",
     "route_list_call",
     "merge_call",
+    "block_step_call",
 ]
