@@ -426,6 +426,11 @@ def _route_bwd_any(
     )
     if res is not None:
         return res
+    if d > 4096:  # fp32 copies of these rows exceed the fp32 row limit
+        raise RuntimeError(
+            f"attnres_hip: the backward of {nq} queries over {len(srcs)} sources of {d} elements is not supported "
+            "(no batched kernel for this shape, and fp32 rows are limited to 4096 elements)"
+        )
     s32 = [t.float().contiguous() for t in srcs]
     acc = [torch.zeros(t.shape, device=device, dtype=torch.float32) for t in srcs]
     tmp = [torch.empty(t.shape, device=device, dtype=torch.float32) for t in srcs]

@@ -270,6 +270,18 @@ def test_batched_query_backward_matches_oracle(gpu, monkeypatch, dtype, S, D, B,
         check_grad(gain.grad, dgain, dtype, "dgain (sum over queries)")
 
 
+def test_batched_query_backward_unsupported_shape_raises(gpu):
+    # bf16 rows above 4096 elements (two chunks per thread) with 5 sources and
+    # several queries: no batched kernel, and the per-query composition's fp32
+    # copies would exceed the fp32 row limit: a clear error
+    S, D, Q = 5, 8192, 2
+    buf = torch.randn(S, 1, 4, D, device=gpu).to(torch.bfloat16).requires_grad_(True)
+    qs = (torch.randn(Q, D, device=gpu) * 0.05).to(torch.bfloat16)
+    out, _, _, _, _ = ops.route(buf, S, qs, None, 1e-5, torch.bfloat16, False, False)
+    with pytest.raises(RuntimeError, match="not supported"):
+        out.float().sum().backward()
+
+
 MERGE_CASES = [
     (torch.bfloat16, torch.bfloat16, 3072),
     (torch.bfloat16, torch.bfloat16, 8192),
