@@ -210,7 +210,7 @@ def bench_serve(steps: int, warmup: int, dev):
             if ev_p1 is not None and k + 1 == deepest:
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
-            out, _, lse, _, _ = ops.route_list_call(blocks, pq[st:e], None, w.eps, torch.bfloat16, True)
+            out, _, lse, _, _ = ops.route_list_call(blocks, pq[st:e], None, w.eps, torch.bfloat16, want_lse=True)
             if ev_p1 is not None and k + 1 == deepest:
                 e1.record()
                 ev_p1.append((e0, e1))
@@ -222,7 +222,7 @@ def bench_serve(steps: int, warmup: int, dev):
                 if ev_merge is not None:
                     e1.record()
                     ev_merge.append((e0, e1))
-        ops.route_list_call(blocks_all[: len(ranges) + 1], pq[-1:], None, w.eps, torch.bfloat16, True)
+        ops.route_list_call(blocks_all[: len(ranges) + 1], pq[-1:], None, w.eps, torch.bfloat16, want_lse=True)
 
     with torch.inference_mode():
         for _ in range(warmup):  # the same calls as the timed steps, event records included

@@ -40,7 +40,8 @@ def phase_1_batched_attention_forward_with_aux(
     """
     s_total = block_representations.shape[0]
     out, _, lse, inv_rms, logits = ops.route_call(
-        block_representations, int(num_active), pseudo_queries, None, float(eps), torch.bfloat16, True, True
+        block_representations, int(num_active), pseudo_queries, None, float(eps), torch.bfloat16, want_aux=True,
+        want_lse=True,
     )
     if num_active < s_total:
         pad = (0, s_total - int(num_active))
@@ -59,7 +60,7 @@ def phase_1_batched_attention(
     if num_active is None:
         num_active = block_representations.shape[0]
     out, _, lse, _, _ = ops.route_call(
-        block_representations, int(num_active), pseudo_queries, None, float(eps), torch.bfloat16, True
+        block_representations, int(num_active), pseudo_queries, None, float(eps), torch.bfloat16, want_lse=True
     )
     return out, lse
 

@@ -128,6 +128,7 @@ def _outputs(
     want_weights: bool,
     want_aux: bool,
     placeholders: bool = True,
+    want_lse: Optional[bool] = None,
 ) -> tuple:
     f32 = torch.float32
     # every returned tensor is its own allocation: custom ops may not return
@@ -140,7 +141,7 @@ def _outputs(
 
     out = torch.empty((nq, *batch, d), device=device, dtype=out_dtype)
     weights = alloc((nq, s, *batch), want_weights)
-    lse = alloc((nq, *batch), want_weights)
+    lse = alloc((nq, *batch), want_weights if want_lse is None else want_lse)
     inv_rms = alloc((*batch, s), want_aux)
     logits = alloc((nq, *batch, s), want_aux)
     return out, weights, lse, inv_rms, logits
@@ -160,6 +161,7 @@ def _launch_route(
     want_weights: bool,
     want_aux: bool,
     placeholders: bool = True,
+    want_lse: Optional[bool] = None,
 ) -> tuple:
     if query.dim() == 1:
         query = query.unsqueeze(0)
@@ -173,7 +175,7 @@ def _launch_route(
     n = 1
     for b in batch:
         n *= b
-    outs = _outputs(device, out_dtype, nq, s, batch, d, want_weights, want_aux, placeholders)
+    outs = _outputs(device, out_dtype, nq, s, batch, d, want_weights, want_aux, placeholders, want_lse)
     out, weights, lse, inv_rms, logits = outs
 
     def p(t: Optional[Tensor]) -> Optional[int]:
@@ -208,7 +210,8 @@ def _launch_route(
 # ------------------------------------------------------------------ route --
 
 
-def _route_impl(buf, num_sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=True):
+def _route_impl(buf, num_sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=True,
+                want_lse=None):
     device = _require_device(buf, query, gain)
     if buf.dim() < 2:
         raise ValueError("attnres_hip::route: buf must be (max_S, *batch, D)")
@@ -223,7 +226,7 @@ def _route_impl(buf, num_sources, query, gain, eps, out_dtype, want_weights, wan
     base = buf.data_ptr()
     ptrs = [base + i * slot * es for i in range(num_sources)]
     return _launch_route(ptrs, d, buf.dtype, batch, d, device, query, gain, eps, out_dtype, want_weights, want_aux,
-                         placeholders)
+                         placeholders, want_lse)
 
 
 @torch.library.custom_op("attnres_hip::route", mutates_args=())
@@ -246,7 +249,8 @@ def _route_fake(buf, num_sources, query, gain, eps, out_dtype, want_weights, wan
     return _outputs(buf.device, out_dtype, nq, num_sources, tuple(buf.shape[1:-1]), buf.shape[-1], want_weights, want_aux)
 
 
-def _route_list_impl(sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=True):
+def _route_list_impl(sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=True,
+                     want_lse=None):
     if len(sources) == 0:
         raise ValueError("attnres_hip::route_list: empty source list (use route with num_sources=0)")
     device = _require_device(*sources, query, gain)
@@ -261,7 +265,7 @@ def _route_list_impl(sources, query, gain, eps, out_dtype, want_weights, want_au
     srcs = [t if t.is_contiguous() else t.contiguous() for t in sources]
     return _launch_route(
         [t.data_ptr() for t in srcs], d, ref.dtype, tuple(ref.shape[:-1]), d, device, query, gain, eps, out_dtype,
-        want_weights, want_aux, placeholders,
+        want_weights, want_aux, placeholders, want_lse,
     )
 
 
@@ -703,18 +707,26 @@ def _eager_direct(*tensors: Optional[Tensor]) -> bool:
     return True
 
 
-def route_call(buf, num_sources, query, gain, eps, out_dtype, want_weights=False, want_aux=False) -> tuple:
-    """:func:`route`, launched directly when nothing needs the dispatcher."""
+def route_call(buf, num_sources, query, gain, eps, out_dtype, want_weights=False, want_aux=False,
+               want_lse=None) -> tuple:
+    """:func:`route`, launched directly when nothing needs the dispatcher.
+
+    ``want_lse`` asks for the lse without the weights (the op ties them).
+    """
     if _eager_direct(buf, query, gain):
-        return _route_impl(buf, num_sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=False)
-    return route(buf, num_sources, query, gain, eps, out_dtype, want_weights, want_aux)
+        return _route_impl(buf, num_sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=False,
+                           want_lse=want_lse)
+    return route(buf, num_sources, query, gain, eps, out_dtype, want_weights or bool(want_lse), want_aux)
 
 
-def route_list_call(sources, query, gain, eps, out_dtype, want_weights=False, want_aux=False) -> tuple:
-    """:func:`route_list`, launched directly when nothing needs the dispatcher."""
+def route_list_call(sources, query, gain, eps, out_dtype, want_weights=False, want_aux=False,
+                    want_lse=None) -> tuple:
+    """:func:`route_list`, launched directly when nothing needs the dispatcher (``want_lse`` as in
+    :func:`route_call`)."""
     if _eager_direct(query, gain, *sources):
-        return _route_list_impl(sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=False)
-    return route_list(list(sources), query, gain, eps, out_dtype, want_weights, want_aux)
+        return _route_list_impl(sources, query, gain, eps, out_dtype, want_weights, want_aux, placeholders=False,
+                                want_lse=want_lse)
+    return route_list(list(sources), query, gain, eps, out_dtype, want_weights or bool(want_lse), want_aux)
 
 
 def merge_call(partial, query, inter, inter_lse, eps) -> Tensor:

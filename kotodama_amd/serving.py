@@ -64,7 +64,7 @@ class FastAttnResContext:
 
 def _phase_1(blocks: list[Tensor], queries: Tensor, eps: float) -> tuple[Tensor, Tensor]:
     """(out (Q, B, T, D) bf16, lse (Q, B, T)) over a list of committed blocks."""
-    out, _, lse, _, _ = ops.route_list_call(blocks, queries, None, eps, torch.bfloat16, True)
+    out, _, lse, _, _ = ops.route_list_call(blocks, queries, None, eps, torch.bfloat16, want_lse=True)
     return out, lse
 
 
