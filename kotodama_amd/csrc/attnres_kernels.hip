@@ -301,7 +301,9 @@ __device__ __forceinline__ float param_elem(const ParamRaw<VEC>& r, int e, bool 
 
 // Exchange lanes 32..63 of a with lanes 0..31 of b (v_permlane32_swap), and
 // the odd 16-lane rows of a with the even rows of b (v_permlane16_swap).  The
-// leading s_nop covers the VALU-write -> permlane-read hazard.
+// leading s_nop covers the VALU-write -> permlane-read hazard.  Inline asm:
+// this compiler's __builtin_amdgcn_permlane{16,32}_swap return the first
+// register for both results.
 __device__ __forceinline__ void swap_halves32(float& a, float& b) {
   asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
@@ -671,8 +673,8 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
 //    each register carries four different values, one per 16-lane row, and
 //    four DPP steps finish the row sums: ~2.5 instructions per value instead
 //    of 6 for a full DPP reduction of each;
-//  * one LDS exchange and one barrier; lane g*P + s then sums value (g, s)
-//    over the waves and runs the QG depth softmaxes in parallel, P-lane
+//  * one LDS exchange and one barrier; lane g*SEG + s then sums value (g, s)
+//    over the waves and runs the QG depth softmaxes in parallel, SEG-lane
 //    segments reduced with DPP (max, sum);
 //  * the weights move to scalar registers (v_readlane) and the mixing pass
 //    unpacks each source word once for all QG output rows.
