@@ -70,6 +70,19 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          false);
 }
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_4x4x4_16b_bf16: sixteen independent 4x4x4 products per wave,
+// block b on lanes 4b..4b+3.  Lane 4b+i supplies row i of A and lane 4b+j
+// column j of B (four bf16 along k each, packed two per word); lane 4b+j
+// receives column j of D, element i holding D[i][j] = C[i][j] + sum_k
+// A[i][k] B[k][j] in fp32.
+__device__ __forceinline__ f32x4 mfma_4x4x4(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0,
+                                                0, 0);
+}
+
 // A wave-uniform 64-bit integer kept in SGPRs.
 __device__ __forceinline__ int64_t uniform_i64(int64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
@@ -676,13 +689,24 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
 //  * one LDS exchange and one barrier; lane g*SEG + s then sums value (g, s)
 //    over the waves and runs the QG depth softmaxes in parallel, SEG-lane
 //    segments reduced with DPP (max, sum);
-//  * the weights move to scalar registers (v_readlane) and the mixing pass
-//    unpacks each source word once for all QG output rows.
+//  * mixing on the matrix cores (groups of a multiple of 4 queries): per
+//    element of a lane, out[q] = sum_s w[q][s] x_s is column j of a 4x4x4
+//    block product whose k runs over four sources: B is the lane's own
+//    sources at that element (two v_perm_b32 per source pair and element
+//    pair), A the weights of four queries, moved from the softmax lanes
+//    with ds_bpermute and split into a bf16 hi and lo part (w = hi + lo to
+//    2^-18 relative; each product and the sum are fp32), two MFMAs per
+//    four sources.  Groups of 2 queries (S >= 13) mix on the VALU: the
+//    weights move to scalar registers (v_readlane) and each source word is
+//    unpacked once for all the group's output rows.
 
-// Queries per group: the partial sums of a group (S * (QG + 1)) and the
-// unpacked sources share the register file; beyond S = 5 a group of 8 drops
-// the kernel to two waves per SIMD, which measured slower than groups of 4.
-#define QG_OF(S) ((S) <= 5 ? 8 : (S) <= 12 ? 4 : 2)
+// Queries per group: one lane per (query, source) in the softmax and at most
+// 64 partial sums per group (S * (QG + 1)); groups of 8 up to S = 7 (at
+// S = 6-7 they cost occupancy, 2 waves per SIMD instead of 3-4, and still
+// measured 2-3% faster than groups of 4 with the mixing on the matrix cores).
+#ifndef QG_OF
+#define QG_OF(S) ((S) <= 7 ? 8 : (S) <= 12 ? 4 : 2)
+#endif
 
 template <int S, int V>
 __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
@@ -804,49 +828,129 @@ __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
         if (P.lse && ss == 0) P.lse[(int64_t)q * P.n_tokens + tok] = m + __logf(sum);
         if (P.inv_rms && q0 == 0 && sg == 0) P.inv_rms[tok * S + ss] = inv;
       }
-      float wgt[QG][S];
+      if constexpr (QG % 4 == 0) {
+        // ---- mixing on the matrix cores ----
+        constexpr int NG4 = QG / 4, KS = (S + 3) / 4;
+        // A operands: lane 4b+i takes the weights of query q0 + 4*g4 + i over
+        // sources 4*ks .. 4*ks+3 (zero past S) from the softmax lanes
+        const int ai = lane & 3;
+        u32x2 ahi[NG4][KS], alo[NG4][KS];
 #pragma unroll
-      for (int g = 0; g < QG; ++g) {
+        for (int g4 = 0; g4 < NG4; ++g4) {
 #pragma unroll
-        for (int s = 0; s < S; ++s)
-          wgt[g][s] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), g * SEG + s));
-      }
-
-      // ---- mixing: each source word unpacked once for all the group's rows ----
+          for (int ks = 0; ks < KS; ++ks) {
+            float wv[4];
 #pragma unroll
-      for (int s = 0; s < S; ++s) {
-#pragma unroll
-        for (int k = 0; k < V; ++k) asm volatile("" : "+v"(x[s][k]));
-      }
-#pragma unroll
-      for (int k = 0; k < V; ++k) {
-        uint32_t ow[QG][4];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          float xl[S], xh[S];
-#pragma unroll
-          for (int s = 0; s < S; ++s) {
-            xl[s] = bf_lo(x[s][k][w]);
-            xh[s] = bf_hi(x[s][k][w]);
-          }
-#pragma unroll
-          for (int g = 0; g < QG; ++g) {
-            float lo = wgt[g][0] * xl[0], hi = wgt[g][0] * xh[0];
-#pragma unroll
-            for (int s = 1; s < S; ++s) {
-              lo = __builtin_fmaf(wgt[g][s], xl[s], lo);
-              hi = __builtin_fmaf(wgt[g][s], xh[s], hi);
+            for (int kk = 0; kk < 4; ++kk) {
+              const int sidx = 4 * ks + kk;
+              wv[kk] = sidx < S ? __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                                ((4 * g4 + ai) * SEG + sidx) * 4,
+                                                                __builtin_bit_cast(int, wl)))
+                                : 0.f;
             }
-            ow[g][w] = pack_bf16(lo, hi);
+            const uint32_t h01 = pack_bf16(wv[0], wv[1]), h23 = pack_bf16(wv[2], wv[3]);
+            ahi[g4][ks] = u32x2{h01, h23};
+            alo[g4][ks] = u32x2{pack_bf16(wv[0] - bf_lo(h01), wv[1] - bf_hi(h01)),
+                                pack_bf16(wv[2] - bf_lo(h23), wv[3] - bf_hi(h23))};
           }
         }
-        // chunks past the row end fall outside the buffer range: the store is dropped
+#pragma unroll
+        for (int sidx = 0; sidx < S; ++sidx) {
+#pragma unroll
+          for (int k = 0; k < V; ++k) asm volatile("" : "+v"(x[sidx][k]));
+        }
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+          // acc[h][g4][i]: out[q0 + 4*g4 + i] at element h of this lane's chunk
+          f32x4 acc[8][NG4];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            // B operands of elements 2w (low halves) and 2w+1 (high halves)
+            u32x2 blo[KS], bhi[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+              for (int p = 0; p < 2; ++p) {
+                const int s0 = 4 * ks + 2 * p, s1 = s0 + 1;
+                const uint32_t a = s0 < S ? x[s0][k][w] : 0u;
+                const uint32_t b = s1 < S ? x[s1][k][w] : 0u;
+                blo[ks][p] = __builtin_amdgcn_perm(b, a, 0x05040100u);
+                bhi[ks][p] = __builtin_amdgcn_perm(b, a, 0x07060302u);
+              }
+            }
+#pragma unroll
+            for (int g4 = 0; g4 < NG4; ++g4) {
+              f32x4 cl = {0.f, 0.f, 0.f, 0.f}, ch = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int ks = 0; ks < KS; ++ks) {
+                cl = mfma_4x4x4(ahi[g4][ks], blo[ks], cl);
+                ch = mfma_4x4x4(ahi[g4][ks], bhi[ks], ch);
+                cl = mfma_4x4x4(alo[g4][ks], blo[ks], cl);
+                ch = mfma_4x4x4(alo[g4][ks], bhi[ks], ch);
+              }
+              acc[2 * w][g4] = cl;
+              acc[2 * w + 1][g4] = ch;
+            }
+          }
+          // chunks past the row end fall outside the buffer range: the store is dropped
+#pragma unroll
+          for (int g4 = 0; g4 < NG4; ++g4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int g = 4 * g4 + i;
+              if (g >= ng) continue;
+              char* orow = reinterpret_cast<char*>(P.out) + ((int64_t)(q0 + g) * P.out_qstride + tok * P.out_ld) * 2;
+              st_row(row_rsrc(orow, (uint32_t)(P.d * 2)), (uint32_t)chunk[k] * 16,
+                     u32x4{pack_bf16(acc[0][g4][i], acc[1][g4][i]), pack_bf16(acc[2][g4][i], acc[3][g4][i]),
+                           pack_bf16(acc[4][g4][i], acc[5][g4][i]), pack_bf16(acc[6][g4][i], acc[7][g4][i])});
+            }
+          }
+        }
+      } else {
+        float wgt[QG][S];
 #pragma unroll
         for (int g = 0; g < QG; ++g) {
-          if (g >= ng) continue;
-          char* orow = reinterpret_cast<char*>(P.out) + ((int64_t)(q0 + g) * P.out_qstride + tok * P.out_ld) * 2;
-          st_row(row_rsrc(orow, (uint32_t)(P.d * 2)), (uint32_t)chunk[k] * 16,
-                 u32x4{ow[g][0], ow[g][1], ow[g][2], ow[g][3]});
+#pragma unroll
+          for (int s = 0; s < S; ++s)
+            wgt[g][s] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), g * SEG + s));
+        }
+
+        // ---- mixing: each source word unpacked once for all the group's rows ----
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+#pragma unroll
+          for (int k = 0; k < V; ++k) asm volatile("" : "+v"(x[s][k]));
+        }
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+          uint32_t ow[QG][4];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            float xl[S], xh[S];
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+              xl[s] = bf_lo(x[s][k][w]);
+              xh[s] = bf_hi(x[s][k][w]);
+            }
+#pragma unroll
+            for (int g = 0; g < QG; ++g) {
+              float lo = wgt[g][0] * xl[0], hi = wgt[g][0] * xh[0];
+#pragma unroll
+              for (int s = 1; s < S; ++s) {
+                lo = __builtin_fmaf(wgt[g][s], xl[s], lo);
+                hi = __builtin_fmaf(wgt[g][s], xh[s], hi);
+              }
+              ow[g][w] = pack_bf16(lo, hi);
+            }
+          }
+          // chunks past the row end fall outside the buffer range: the store is dropped
+#pragma unroll
+          for (int g = 0; g < QG; ++g) {
+            if (g >= ng) continue;
+            char* orow = reinterpret_cast<char*>(P.out) + ((int64_t)(q0 + g) * P.out_qstride + tok * P.out_ld) * 2;
+            st_row(row_rsrc(orow, (uint32_t)(P.d * 2)), (uint32_t)chunk[k] * 16,
+                   u32x4{ow[g][0], ow[g][1], ow[g][2], ow[g][3]});
+          }
         }
       }
     }
