@@ -221,10 +221,13 @@ int attnres_route_bwd_queries_workspace_size(int64_t num_tokens, int hidden, int
  * grad_query:   (num_queries, hidden) param_dtype, or NULL; grad_gain as in
  *               attnres_route_bwd.  Sums over tokens in a fixed order.
  * workspace:    attnres_route_bwd_queries_workspace_size() bytes.
- * Other arguments as in attnres_route_bwd.  Returns ATTNRES_ERR_UNSUPPORTED
- * for shapes without a batched kernel (num_sources * 8 * V > 72 for bf16
- * sources, num_sources * 4 * V > 72 for fp32, V = 2 for rows above 512
- * chunks of 16 bytes); attnres_route_bwd once per query covers those.
+ * Other arguments as in attnres_route_bwd.  bf16 sources, output gradients
+ * and parameters with num_sources <= 8, num_queries <= 8 and hidden <= 4096
+ * run on the matrix cores; other shapes on the VALU kernel, which exists
+ * where num_sources * 8 * V <= 72 for bf16 sources and num_sources * 4 * V
+ * <= 72 for fp32 (V = 2 for rows above 512 chunks of 16 bytes).  Returns
+ * ATTNRES_ERR_UNSUPPORTED for shapes neither covers; attnres_route_bwd once
+ * per query covers those.
  *
  * Replaces the Triton backward of the phase-1 op for Q > 1
  * (src/model/flash_attn_res/ops/phase_1.py:88-284,
@@ -239,6 +242,15 @@ int attnres_route_bwd_queries(const void* const* sources, int num_sources, int64
                               int64_t grad_out_ld, int64_t grad_out_qstride, const float* grad_lse,
                               void* const* grad_sources, int64_t grad_ld, void* workspace, int64_t workspace_bytes,
                               void* grad_query, void* grad_gain, void* stream);
+
+/*
+ * Symbol name of the first kernel attnres_route_bwd_queries launches for
+ * these arguments, for matching profiler output and for tests; an empty
+ * string where it would return ATTNRES_ERR_UNSUPPORTED.  Loads the code
+ * object on the current device.  No counterpart in the reference.
+ */
+int attnres_route_bwd_queries_kernel_name(int num_sources, int hidden, int src_dtype, int param_dtype,
+                                          int grad_out_dtype, int num_queries, char* buf, int buf_len);
 
 /*
  * Backward of attnres_merge_fwd: given dL/dout (num_tokens, hidden) in

@@ -1,4 +1,4 @@
-/* The seven gfx950 code-object parts, linked into libattnres_hip.so as bytes
+/* The eight gfx950 code-object parts, linked into libattnres_hip.so as bytes
  * and loaded with hipModuleLoadData.  The build passes -I<dir of the .hsaco>. */
     .section .rodata
     .balign 4096
@@ -29,4 +29,8 @@ attnres_hsaco_part5:
     .global attnres_hsaco_part6
 attnres_hsaco_part6:
     .incbin "attnres_gfx950_part6.hsaco"
+    .balign 4096
+    .global attnres_hsaco_part7
+attnres_hsaco_part7:
+    .incbin "attnres_gfx950_part7.hsaco"
     .section .note.GNU-stack,"",@progbits

@@ -30,10 +30,11 @@ extern "C" const unsigned char attnres_hsaco_part3[];
 extern "C" const unsigned char attnres_hsaco_part4[];
 extern "C" const unsigned char attnres_hsaco_part5[];
 extern "C" const unsigned char attnres_hsaco_part6[];
+extern "C" const unsigned char attnres_hsaco_part7[];
 
 namespace {
 
-constexpr int kParts = 7;
+constexpr int kParts = 8;
 constexpr int kMaxDevices = 64;
 constexpr int kMaxThreads = 512;  // __launch_bounds__ of every kernel
 
@@ -66,6 +67,7 @@ constexpr int kBwdFuncs = 4 * kNumS * 2;  // (source, grad_out) dtype pairs x S 
 constexpr int kBwdMaxPerCu = 4;           // workgroups per CU the backward grid may use (workspace bound)
 constexpr size_t kBwdStaticLds = 2 * ATTNRES_KMAX_WAVES * 48 * sizeof(float);  // reduction buffer, S = 16
 constexpr size_t kQgStaticLds = 2 * ATTNRES_KMAX_WAVES * 64 * sizeof(float);   // batched-query reduction buffer
+constexpr size_t kMqgStaticLds = 2 * ATTNRES_KMAX_WAVES * 72 * sizeof(float);  // its backward's (S <= 8)
 
 struct DeviceState {
   std::atomic<bool> loaded{false};
@@ -98,6 +100,10 @@ struct DeviceState {
   hipFunction_t bwd_dqw[4] = {};  // source dtype x V
   int bwd_dqw_bpc[4] = {};
   int bwd_dqw_bpc_block[4] = {};
+  hipFunction_t bwd_mqg[2 * 9] = {};  // batched-query backward on the matrix cores: query groups x S
+  int bwd_mqg_bpc[2 * 9] = {};
+  int bwd_mqg_block[2 * 9] = {};
+  size_t bwd_mqg_lds[2 * 9] = {};
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -118,7 +124,9 @@ struct Tuning {
   double grid_mult = 1.0;
   double stream_per_cu = 1.0;  // workgroups per CU of the streaming kernels
   int bwd_per_cu = 0;          // > 0: resident workgroups per CU of the routing backward
+  int mqg = 1;                 // 0: the batched-query backward never uses the matrix-core kernel
   Tuning() {
+    if (const char* v = std::getenv("ATTNRES_MQG")) mqg = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_BWD_PER_CU")) bwd_per_cu = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_STREAM_PER_CU")) stream_per_cu = std::atof(v);
     if (const char* v = std::getenv("ATTNRES_V")) force_v = std::atoi(v);
@@ -147,7 +155,7 @@ int ensure_loaded(DeviceState** out) {
     if (!st.loaded.load(std::memory_order_relaxed)) {
       const unsigned char* blobs[kParts] = {attnres_hsaco_part0, attnres_hsaco_part1, attnres_hsaco_part2,
                                             attnres_hsaco_part3, attnres_hsaco_part4, attnres_hsaco_part5,
-                                            attnres_hsaco_part6};
+                                            attnres_hsaco_part6, attnres_hsaco_part7};
       for (int i = 0; i < kParts; ++i) {
         e = hipModuleLoadData(&st.mods[i], blobs[i]);
         if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
@@ -344,6 +352,39 @@ int get_bwd_dqw(DeviceState& st, bool bf, int v, int block, hipFunction_t* f, in
   }
   *f = st.bwd_dqw[idx];
   *bpc = st.bwd_dqw_bpc[idx];
+  return ATTNRES_OK;
+}
+
+// Batched-query backward on the matrix cores (code-object part 7): bf16
+// sources, output gradients and parameters, 1 <= S <= 8, Q <= 8, two chunks
+// per thread in workgroups of at most 256 threads, the Q folded queries in
+// `lds` bytes of dynamic LDS.
+constexpr int kBwdMqgPart = 7;
+constexpr int kBwdMqgMaxThreads = 256;
+bool bwd_mqg_shape(bool bf, bool gbf, bool pbf, int s, int nq, int nchunk) {
+  return tuning().mqg != 0 && bf && gbf && pbf && s >= 1 && s <= 8 && nq >= 1 && nq <= 8 &&
+         ((nchunk + 1) / 2 + 63) / 64 * 64 <= kBwdMqgMaxThreads;
+}
+
+int get_bwd_mqg(DeviceState& st, int s, int nq4, int block, size_t lds, hipFunction_t* f, int* bpc) {
+  const int idx = (nq4 - 1) * 9 + s;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (st.bwd_mqg[idx] == nullptr) {
+    char name[96];
+    snprintf(name, sizeof(name), "attnres_route_bwd_mqg_s%d_q%d", s, nq4);
+    int rc = find_function(st, kBwdMqgPart, name, &st.bwd_mqg[idx]);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  if (st.bwd_mqg_block[idx] != block || st.bwd_mqg_lds[idx] != lds) {
+    int nb = 0;
+    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.bwd_mqg[idx], block, lds);
+    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    st.bwd_mqg_bpc[idx] = nb > 0 ? nb : 1;
+    st.bwd_mqg_block[idx] = block;
+    st.bwd_mqg_lds[idx] = lds;
+  }
+  *f = st.bwd_mqg[idx];
+  *bpc = st.bwd_mqg_bpc[idx];
   return ATTNRES_OK;
 }
 
@@ -671,6 +712,35 @@ int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, i
   return ATTNRES_OK;
 }
 
+int attnres_route_bwd_queries_kernel_name(int num_sources, int hidden, int src_dtype, int param_dtype,
+                                          int grad_out_dtype, int num_queries, char* buf, int buf_len) {
+  if (buf == nullptr || buf_len < 1) return fail(ATTNRES_ERR_ARG, "no output buffer");
+  if (!valid_dtype(src_dtype) || !valid_dtype(param_dtype) || !valid_dtype(grad_out_dtype))
+    return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (num_sources < 1 || num_sources > ATTNRES_MAX_SOURCES || hidden <= 0 || num_queries < 1)
+    return fail(ATTNRES_ERR_ARG, "bad shape");
+  const bool bf = src_dtype == ATTNRES_DTYPE_BF16;
+  const int vec = bf ? 8 : 4;
+  if (hidden % vec != 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d is not a multiple of %d", hidden, vec);
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  const int nchunk = hidden / vec;
+  const int v = round64(nchunk) <= kMaxThreads ? 1 : 2;
+  const bool gbf = grad_out_dtype == ATTNRES_DTYPE_BF16;
+  const size_t lds = (size_t)((num_queries + 3) / 4 * 4) * (size_t)nchunk * 16;
+  if (bwd_mqg_shape(bf, gbf, param_dtype == ATTNRES_DTYPE_BF16, num_sources, num_queries, nchunk) &&
+      lds + kMqgStaticLds <= (size_t)st->max_lds) {
+    snprintf(buf, (size_t)buf_len, "attnres_route_bwd_mqg_s%d_q%d", num_sources, (num_queries + 3) / 4);
+  } else if (bwd_mq_available(bf, num_sources, v)) {
+    snprintf(buf, (size_t)buf_len, "attnres_route_bwd_mq_%s_g%s_s%d_v%d", bf ? "bf" : "f32", gbf ? "bf" : "f32",
+             num_sources, v);
+  } else {
+    buf[0] = '\0';  // no batched kernel: attnres_route_bwd_queries returns ATTNRES_ERR_UNSUPPORTED
+  }
+  return ATTNRES_OK;
+}
+
 int attnres_set_kernel_policy(int policy) {
   if (policy != ATTNRES_POLICY_AUTO && policy != ATTNRES_POLICY_WORKGROUP && policy != ATTNRES_POLICY_STREAM)
     return fail(ATTNRES_ERR_ARG, "unknown kernel policy %d", policy);
@@ -941,7 +1011,10 @@ int attnres_route_bwd_queries(const void* const* sources, int num_sources, int64
     return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d exceeds the largest supported row (%d elements)", hidden,
                 2 * kMaxThreads * vec);
   const int v = round64(nchunk) <= kMaxThreads ? 1 : 2;
-  if (!bwd_mq_available(bf, num_sources, v))
+  const size_t mqg_lds = (size_t)((num_queries + 3) / 4 * 4) * (size_t)nchunk * 16;  // query slots of 4
+  const bool mqg_shape = bwd_mqg_shape(bf, grad_out_dtype == ATTNRES_DTYPE_BF16,
+                                       param_dtype == ATTNRES_DTYPE_BF16, num_sources, num_queries, nchunk);
+  if (!mqg_shape && !bwd_mq_available(bf, num_sources, v))
     return fail(ATTNRES_ERR_UNSUPPORTED,
                 "batched backward of S=%d sources with %d chunks per thread is not built; call attnres_route_bwd "
                 "once per query",
@@ -968,10 +1041,22 @@ int attnres_route_bwd_queries(const void* const* sources, int num_sources, int64
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
+  // the matrix-core kernel where its staged queries fit in LDS
+  const bool mqg = mqg_shape && mqg_lds + kMqgStaticLds <= (size_t)st->max_lds;
+  if (!mqg && !bwd_mq_available(bf, num_sources, v))
+    return fail(ATTNRES_ERR_UNSUPPORTED,
+                "batched backward of S=%d sources: %zu bytes of staged queries exceed the LDS and the VALU kernel "
+                "is not built for %d chunks per thread; call attnres_route_bwd once per query",
+                num_sources, mqg_lds, v);
   const int block = v == 1 ? round64(nchunk) : round64((nchunk + 1) / 2);
+  const int mqg_block = round64((nchunk + 1) / 2);
   hipFunction_t f = nullptr, fq = nullptr;
   int bpc = 1, bpcq = 1;
-  rc = get_bwd_mq(*st, bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, v, block, &f, &bpc);
+  if (mqg) {
+    rc = get_bwd_mqg(*st, num_sources, (num_queries + 3) / 4, mqg_block, mqg_lds, &f, &bpc);
+  } else {
+    rc = get_bwd_mq(*st, bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, v, block, &f, &bpc);
+  }
   if (rc != ATTNRES_OK) return rc;
   const bool want_q = grad_query != nullptr || grad_gain != nullptr;
   hipFunction_t fr = nullptr, fs = nullptr;
@@ -1013,13 +1098,15 @@ int attnres_route_bwd_queries(const void* const* sources, int num_sources, int64
   P.nchunk = nchunk;
   P.num_queries = num_queries;
   P.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
-  P.block = block;
+  P.block = mqg ? mqg_block : block;
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
-  // two resident workgroups per CU, as the single-query backward
-  int64_t grid = (int64_t)st->num_cus * (bpc < 2 ? bpc : 2);
+  // two resident workgroups per CU, as the single-query backward; the
+  // matrix-core kernel at its occupancy limit
+  const int per_cu = mqg ? bpc : (bpc < 2 ? bpc : 2);
+  int64_t grid = (int64_t)st->num_cus * per_cu;
   if (grid > num_tokens) grid = num_tokens;
-  rc = launch(f, (int)grid, block, P, stream);
+  rc = mqg ? launch(f, (int)grid, mqg_block, P, stream, 1, mqg_lds) : launch(f, (int)grid, block, P, stream);
   if (rc != ATTNRES_OK || !want_q) return rc;
 
   attnres_route_bwd_dqw_params Q;

@@ -1924,6 +1924,274 @@ __device__ __forceinline__ void route_bwd_mq_body(const attnres_route_bwd_mq_par
   }
 }
 
+// ------------------------------- batched-query backward on the matrix cores --
+//
+// The source gradients of the batched-query routing for bf16 sources, bf16
+// output gradients and bf16 parameters with Q <= 4*NQ4 queries (the serving
+// engine's phase 1 under autograd).  One workgroup per row (grid-stride),
+// thread i owning chunks i, i+block, ...; per row the S source chunks and
+// the output-gradient chunks of every query are loaded once (the next row's
+// after the current row's stores), the folded queries sit in dynamic LDS.
+// Per group of four queries:
+//  * sum(x^2), x.qw_q and x.G_q per (query, source) with v_dot2_f32_bf16,
+//    reduced by the transposing tree, one LDS exchange;
+//  * lane 8g + s runs the softmax of query g over the sources and forms
+//      w_qs, c1_qs = w_qs (g_lse + G_q.x_s - G_q.out_q) r_s,
+//      c2_qs = -c1_qs l_qs r_s / D
+//    (G_q.out_q = sum_s w_qs G_q.x_s, from the reduced values);
+//  * w and c1 move into MFMA A operands (ds_bpermute): lane 4b+i carries
+//    source 4ks+i of a group of four sources, the four queries along k, as
+//    bf16 hi + lo parts.
+// Then per chunk and element the matrix cores form
+//   dx_s = sum_q (w_qs G_q + c1_qs qw_q)
+// for four sources at a time (v_mfma_f32_4x4x4_16b_bf16 with B = the
+// lane's own G_q / qw_q at that element, four queries along k), the VALU
+// adds (sum_q c2_qs) x_s and each gradient row is written once.  c1 goes to
+// the workspace for the query-gradient pass (route_bwd_dqw_body).
+template <int S, int V, int NQ4>
+__device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_params& P) {
+  constexpr int VEC = 8;
+  constexpr int SEG = 8;                 // lanes per query in the softmax (S <= 8)
+  constexpr int KS = (S + 3) / 4;        // groups of four sources
+  constexpr int NQ = 4 * NQ4;            // query slots
+  // per group two reductions: sum(x^2) and x.qw of 4 queries (5S values),
+  // then x.G of 4 queries (4S values), so fewer partial sums are live at once
+  constexpr int HA = (5 * S + 3) / 4, HB = S;
+  constexpr int NPA = 4 * HA, NPB = 4 * HB;
+  static_assert(S >= 1 && S <= SEG, "one softmax lane per (query, source)");
+  __shared__ float red[2][ATTNRES_KMAX_WAVES][NPA + NPB];
+  extern __shared__ u32x4 qg_lds[];  // [chunk][query slot] packed folded queries, zero past the batch
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int block = P.block;
+  const int nwaves = (block + 63) >> 6;
+  const int nq = P.num_queries;
+  const int nchunk = P.nchunk;
+
+  int chunk[V];
+  const u32x4* qrow[V];  // this thread's chunks of the staged queries: qrow[k][q], q < NQ
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    chunk[k] = tid + k * block;
+    qrow[k] = qg_lds + (chunk[k] < nchunk ? chunk[k] : nchunk - 1) * NQ;  // rows past the end hold zeros
+  }
+
+  // ---- the folded queries into LDS, once per workgroup; chunk-major, so a
+  // thread's queries sit at constant offsets from one address ----
+  for (int i = tid; i < NQ * nchunk; i += block) {
+    const int c = i / NQ, q = i % NQ;
+    float t[VEC];
+    if (q < nq) {
+      load_qw_ptr<VEC>(P.query, P.gain, true, q, P.d, c, t);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) t[e] = 0.f;
+    }
+    qg_lds[i] = u32x4{pack_bf16(t[0], t[1]), pack_bf16(t[2], t[3]), pack_bf16(t[4], t[5]), pack_bf16(t[6], t[7])};
+  }
+
+  // Rows through buffer resources: a chunk past the row end reads 0 and its
+  // gradient store is dropped; query slots past the batch hold zeros.
+  const int64_t row_bytes_ld = P.src_ld * 2;
+  const uint32_t row_bytes = (uint32_t)(P.d * 2);
+  u32x4 x[S][V], gq[NQ][V];
+  auto load_row = [&](int64_t t) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      char* row = reinterpret_cast<char*>(const_cast<void*>(P.src[s])) + t * row_bytes_ld;
+      const __amdgpu_buffer_rsrc_t rs = row_rsrc(row, row_bytes);
+#pragma unroll
+      for (int k = 0; k < V; ++k) x[s][k] = ld_row(rs, (uint32_t)chunk[k] * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      char* grow = reinterpret_cast<char*>(const_cast<void*>(P.grad_out)) + (q * P.gout_qstride + t * P.gout_ld) * 2;
+      const __amdgpu_buffer_rsrc_t rg = row_rsrc(grow, q < nq ? row_bytes : 0u);
+#pragma unroll
+      for (int k = 0; k < V; ++k) gq[q][k] = ld_row(rg, (uint32_t)chunk[k] * 16);
+    }
+  };
+  if ((int64_t)blockIdx.x < P.n_tokens) load_row(blockIdx.x);
+
+  const int sg = lane / SEG, ss = lane % SEG;  // softmax lane: query sg of the group, source ss
+  const int ai = lane & 3;                     // A-operand row: source 4*ks + ai
+  __syncthreads();
+
+  int ph = 0;
+  for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
+    float ssp[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      ssp[s] = 0.f;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) ssp[s] = dot2_bf16(x[s][k][w], x[s][k][w], ssp[s]);
+      }
+    }
+    u32x2 awh[NQ4][KS], awl[NQ4][KS], ach[NQ4][KS], acl[NQ4][KS];
+    float c2acc = 0.f;
+#pragma unroll
+    for (int g4 = 0; g4 < NQ4; ++g4) {
+      const int q0 = 4 * g4;
+      // ---- x.qw and x.G of four queries, packed dot products, two reductions ----
+      {
+        float part[NPA];
+#pragma unroll
+        for (int j = 0; j < NPA; ++j) part[j] = j < S ? ssp[j] : 0.f;
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+          u32x4 qv[4];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) qv[g] = qrow[k][q0 + g];
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+#pragma unroll
+              for (int g = 0; g < 4; ++g) part[S + g * S + s] = dot2_bf16(x[s][k][w], qv[g][w], part[S + g * S + s]);
+            }
+          }
+        }
+        wave_reduce_to_lds<HA>(part, red[ph][wave], lane);
+      }
+      {
+        float part[NPB];
+#pragma unroll
+        for (int j = 0; j < NPB; ++j) part[j] = 0.f;
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+#pragma unroll
+              for (int g = 0; g < 4; ++g) part[g * S + s] = dot2_bf16(x[s][k][w], gq[q0 + g][k][w], part[g * S + s]);
+            }
+          }
+        }
+        wave_reduce_to_lds<HB>(part, red[ph][wave] + NPA, lane);
+      }
+      __syncthreads();
+
+      // ---- softmax and coefficients, lane 8g + s ----
+      const int q = q0 + sg;
+      const bool slot = sg < 4 && ss < S && q < nq;
+      float t_ss = 0.f, t_dot = 0.f, t_gx = 0.f;
+      if (slot) {
+        for (int w = 0; w < nwaves; ++w) {
+          t_ss += red[ph][w][ss];
+          t_dot += red[ph][w][S + sg * S + ss];
+          t_gx += red[ph][w][NPA + sg * S + ss];
+        }
+      }
+      ph ^= 1;
+      const float rl = __builtin_amdgcn_rsqf(t_ss * P.inv_d + P.eps);
+      const float ll = slot ? t_dot * rl : -__builtin_inff();
+      const float m = seg_max<SEG>(ll);
+      const float el = slot ? __expf(ll - m) : 0.f;
+      const float sum = seg_sum<SEG>(el);
+      const float wl = slot ? el * (1.0f / sum) : 0.f;
+      const float go = seg_sum<SEG>(wl * t_gx);  // G_q . out_q
+      const float glse = slot && P.grad_lse != nullptr ? P.grad_lse[(int64_t)q * P.n_tokens + tok] : 0.f;
+      const float c1l = slot ? wl * (glse + t_gx - go) * rl : 0.f;
+      c2acc += slot ? -c1l * ll * rl * P.inv_d : 0.f;
+      if (wave == 0 && slot) P.c1[(tok * nq + q) * S + ss] = c1l;
+
+      // ---- A operands: source 4*ks + ai, queries q0 .. q0+3 along k ----
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int src_s = 4 * ks + ai;
+        float wv[4], cv[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int from = (g * SEG + src_s) * 4;
+          wv[g] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(from, __builtin_bit_cast(int, wl)));
+          cv[g] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(from, __builtin_bit_cast(int, c1l)));
+          if (src_s >= S) wv[g] = cv[g] = 0.f;
+        }
+        const uint32_t w01 = pack_bf16(wv[0], wv[1]), w23 = pack_bf16(wv[2], wv[3]);
+        const uint32_t c01 = pack_bf16(cv[0], cv[1]), c23 = pack_bf16(cv[2], cv[3]);
+        awh[g4][ks] = u32x2{w01, w23};
+        awl[g4][ks] = u32x2{pack_bf16(wv[0] - bf_lo(w01), wv[1] - bf_hi(w01)),
+                            pack_bf16(wv[2] - bf_lo(w23), wv[3] - bf_hi(w23))};
+        ach[g4][ks] = u32x2{c01, c23};
+        acl[g4][ks] = u32x2{pack_bf16(cv[0] - bf_lo(c01), cv[1] - bf_hi(c01)),
+                            pack_bf16(cv[2] - bf_lo(c23), cv[3] - bf_hi(c23))};
+      }
+    }
+
+    // sum over the queries of c2_qs, per source (lanes 8g + s)
+    float c2s[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        t += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c2acc), g * SEG + s));
+      c2s[s] = t;
+    }
+
+    // ---- dx_s = sum_q (w_qs G_q + c1_qs qw_q) + c2_s x_s, per chunk and group of four sources ----
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        f32x4 acc[8];  // acc[h][i]: dx of source 4*ks + i at element h of this lane's chunk
+#pragma unroll
+        for (int h = 0; h < 8; ++h) acc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g4 = 0; g4 < NQ4; ++g4) {
+          u32x4 qv[4];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) qv[g] = qrow[k][4 * g4 + g];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            // B operands of elements 2w (low halves) and 2w+1 (high halves), four queries along k
+            const u32x2 bgl = {__builtin_amdgcn_perm(gq[4 * g4 + 1][k][w], gq[4 * g4][k][w], 0x05040100u),
+                               __builtin_amdgcn_perm(gq[4 * g4 + 3][k][w], gq[4 * g4 + 2][k][w], 0x05040100u)};
+            const u32x2 bgh = {__builtin_amdgcn_perm(gq[4 * g4 + 1][k][w], gq[4 * g4][k][w], 0x07060302u),
+                               __builtin_amdgcn_perm(gq[4 * g4 + 3][k][w], gq[4 * g4 + 2][k][w], 0x07060302u)};
+            const u32x2 bql = {__builtin_amdgcn_perm(qv[1][w], qv[0][w], 0x05040100u),
+                               __builtin_amdgcn_perm(qv[3][w], qv[2][w], 0x05040100u)};
+            const u32x2 bqh = {__builtin_amdgcn_perm(qv[1][w], qv[0][w], 0x07060302u),
+                               __builtin_amdgcn_perm(qv[3][w], qv[2][w], 0x07060302u)};
+            f32x4 lo = acc[2 * w], hi = acc[2 * w + 1];
+            lo = mfma_4x4x4(awh[g4][ks], bgl, lo);
+            hi = mfma_4x4x4(awh[g4][ks], bgh, hi);
+            lo = mfma_4x4x4(awl[g4][ks], bgl, lo);
+            hi = mfma_4x4x4(awl[g4][ks], bgh, hi);
+            lo = mfma_4x4x4(ach[g4][ks], bql, lo);
+            hi = mfma_4x4x4(ach[g4][ks], bqh, hi);
+            lo = mfma_4x4x4(acl[g4][ks], bql, lo);
+            hi = mfma_4x4x4(acl[g4][ks], bqh, hi);
+            acc[2 * w] = lo;
+            acc[2 * w + 1] = hi;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int s = 4 * ks + i;
+          if (s >= S) break;
+          float dx[8];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            dx[2 * w] = __builtin_fmaf(c2s[s], bf_lo(x[s][k][w]), acc[2 * w][i]);
+            dx[2 * w + 1] = __builtin_fmaf(c2s[s], bf_hi(x[s][k][w]), acc[2 * w + 1][i]);
+          }
+          char* drow = reinterpret_cast<char*>(P.dsrc[s]) + tok * P.dsrc_ld * 2;
+          st_row(row_rsrc(drow, row_bytes), (uint32_t)chunk[k] * 16,
+                 u32x4{pack_bf16(dx[0], dx[1]), pack_bf16(dx[2], dx[3]), pack_bf16(dx[4], dx[5]),
+                       pack_bf16(dx[6], dx[7])});
+        }
+      }
+    }
+    if (tok + gridDim.x < P.n_tokens) load_row(tok + gridDim.x);
+  }
+}
+
 // Query-gradient partials of the batched backward: each workgroup sums
 // c1_qs x_s over its rows (grid-stride) and sources for up to 8 queries
 // q0 .. q0+7 and writes them as its row of `part` (gridDim.x, Q, d).  Source
@@ -2281,7 +2549,7 @@ __device__ __forceinline__ void reduce_dqw_body(const attnres_reduce_params& P) 
   ROUTE_TYPES(S, 1) \
   ROUTE_TYPES(S, 2)
 
-// The build compiles this file once per module part (ATTNRES_PART = 0..5)
+// The build compiles this file once per module part (ATTNRES_PART = 0..7)
 // so the parts build in parallel; the host maps each symbol to its part.
 #ifndef ATTNRES_PART
 #define ATTNRES_PART 0
@@ -2462,4 +2730,13 @@ BWD_MQ(f32, false, 1, 2) BWD_MQ(f32, false, 2, 2) BWD_MQ(f32, false, 3, 2) BWD_M
 BWD_MQ(f32, false, 5, 2) BWD_MQ(f32, false, 6, 2) BWD_MQ(f32, false, 7, 2) BWD_MQ(f32, false, 8, 2)
 BWD_MQ(f32, false, 9, 2)
 BWD_DQW(bf, true, 1) BWD_DQW(bf, true, 2) BWD_DQW(f32, false, 1) BWD_DQW(f32, false, 2)
+#endif
+
+// Batched-query backward on the matrix cores (bf16 sources, output gradients
+// and parameters): attnres_route_bwd_mqg_s<S>_q<NQ4>, up to 4*NQ4 queries, two
+// chunks per thread, at most 256 threads (rows of up to 4096 bf16 elements).
+#define BWD_MQG(S, NQ4)                                                                           extern "C" __global__ void __launch_bounds__(512) attnres_route_bwd_mqg_s##S##_q##NQ4(              attnres_route_bwd_mq_params P) {                                                              route_bwd_mqg_body<S, 2, NQ4>(P);                                                             }
+#if ATTNRES_PART == 7 || defined(ATTNRES_ALL_PARTS)
+BWD_MQG(1, 1) BWD_MQG(2, 1) BWD_MQG(3, 1) BWD_MQG(4, 1) BWD_MQG(5, 1) BWD_MQG(6, 1) BWD_MQG(7, 1) BWD_MQG(8, 1)
+BWD_MQG(1, 2) BWD_MQG(2, 2) BWD_MQG(3, 2) BWD_MQG(4, 2) BWD_MQG(5, 2) BWD_MQG(6, 2) BWD_MQG(7, 2) BWD_MQG(8, 2)
 #endif

@@ -221,26 +221,49 @@ def test_multi_query_phase_1_backward(gpu):
 
 
 MQ_CASES = [
-    # (dtype, S, D, B, T, Q, with gain, batched kernel expected)
-    (torch.bfloat16, 1, 1024, 2, 20, 2, False, True),
-    (torch.bfloat16, 7, 3072, 1, 40, 9, True, True),
-    (torch.bfloat16, 9, 2048, 2, 12, 4, False, True),
-    (torch.bfloat16, 3, 8192, 1, 16, 3, True, True),
-    (torch.bfloat16, 12, 1024, 1, 24, 3, False, False),
-    (torch.float32, 16, 1024, 1, 20, 2, True, True),
-    (torch.float32, 5, 4096, 1, 16, 9, False, True),
+    # (dtype, S, D, B, T, Q, with gain, batched kernel: "mqg" matrix cores, "mq" VALU, None per query)
+    (torch.bfloat16, 1, 1024, 2, 20, 2, False, "mqg"),
+    (torch.bfloat16, 7, 3072, 1, 40, 8, True, "mqg"),
+    (torch.bfloat16, 8, 1024, 2, 16, 5, False, "mqg"),  # a ragged second group of queries
+    (torch.bfloat16, 4, 4096, 1, 12, 4, True, "mqg"),  # 256-thread rows
+    (torch.bfloat16, 5, 520, 1, 9, 3, False, "mqg"),  # one thread holds the row's last chunk
+    (torch.bfloat16, 3, 2056, 1, 10, 6, True, "mqg"),  # 257 chunks: threads past the end
+    (torch.bfloat16, 7, 3072, 1, 40, 9, True, "mq"),  # nine queries
+    (torch.bfloat16, 9, 2048, 2, 12, 4, False, "mq"),
+    (torch.bfloat16, 3, 8192, 1, 16, 3, True, "mq"),
+    (torch.bfloat16, 12, 1024, 1, 24, 3, False, None),
+    (torch.float32, 16, 1024, 1, 20, 2, True, "mq"),
+    (torch.float32, 5, 4096, 1, 16, 9, False, "mq"),
 ]
 
 
-@pytest.mark.parametrize("dtype,S,D,B,T,Q,with_gain,batched", MQ_CASES,
+def bwd_queries_kernel(S, D, dtype, Q):
+    import ctypes
+
+    code = ops.dtype_code(dtype)
+    buf = ctypes.create_string_buffer(128)
+    _capi.check("attnres_route_bwd_queries_kernel_name",
+                _capi.lib().attnres_route_bwd_queries_kernel_name(S, D, code, code, code, Q, buf, 128))
+    return buf.value.decode()
+
+
+@pytest.mark.parametrize("dtype,S,D,B,T,Q,with_gain,kernel", MQ_CASES,
                          ids=[f"{str(c[0])[6:]}-S{c[1]}-D{c[2]}-Q{c[5]}" for c in MQ_CASES])
-def test_batched_query_backward_matches_oracle(gpu, monkeypatch, dtype, S, D, B, T, Q, with_gain, batched):
+def test_batched_query_backward_matches_oracle(gpu, monkeypatch, dtype, S, D, B, T, Q, with_gain, kernel):
     # Q queries over one stack with an lse term: the source gradients summed
     # over the queries, every query's gradient and the gain gradient summed
     # over the queries; one pass of attnres_route_bwd_queries where a batched
-    # kernel exists (nine queries: two passes of the query-gradient kernel),
-    # one attnres_route_bwd per query otherwise
-    print(f"batched-query backward {dtype} S={S} D={D} Q={Q} gain={with_gain}", flush=True)
+    # kernel exists (on the matrix cores for bf16 with S <= 8, Q <= 8 and
+    # D <= 4096; nine queries: two passes of the query-gradient kernel), one
+    # attnres_route_bwd per query otherwise
+    name = bwd_queries_kernel(S, D, dtype, Q)
+    print(f"batched-query backward {dtype} S={S} D={D} Q={Q} gain={with_gain} kernel={name or 'per query'}",
+          flush=True)
+    if kernel is None:
+        assert name == ""
+    else:
+        assert name.startswith(f"attnres_route_bwd_{kernel}_"), name
+    batched = kernel is not None
     eps = 1e-5
     buf, _, _, _ = make_case(gpu, S, 0, B, T, D, dtype, seed=60 + S + Q)
     g = torch.Generator(device="cpu").manual_seed(61 + D)
