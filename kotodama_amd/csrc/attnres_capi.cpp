@@ -308,6 +308,7 @@ int get_bwd(DeviceState& st, bool bf, bool gbf, int s, int v, int block, size_t 
 // accumulators are S * VEC * V fp32 registers per thread; the kernels exist
 // where that stays within 72.
 constexpr int kBwdMqPart = 6;
+constexpr int kBwdMqgPart = 7;  // the matrix-core batched backward and query-gradient pass
 bool bwd_mq_available(bool bf, int s, int v) {
   const int vec = bf ? 8 : 4;
   return s >= 1 && s <= ATTNRES_KMAX_SOURCES && (v == 1 || v == 2) && s * vec * v <= 72;
@@ -334,13 +335,19 @@ int get_bwd_mq(DeviceState& st, bool bf, bool gbf, int s, int v, int block, hipF
   return ATTNRES_OK;
 }
 
+// bf16 sources: the matrix-core variant (part 7) unless ATTNRES_MQG=0.
 int get_bwd_dqw(DeviceState& st, bool bf, int v, int block, hipFunction_t* f, int* bpc) {
   const int idx = (bf ? 0 : 2) + (v - 1);
   std::lock_guard<std::mutex> lk(g_mu);
   if (st.bwd_dqw[idx] == nullptr) {
     char name[96];
-    snprintf(name, sizeof(name), "attnres_route_bwd_dqw_%s_v%d", bf ? "bf" : "f32", v);
-    int rc = find_function(st, kBwdMqPart, name, &st.bwd_dqw[idx]);
+    const bool mfma = bf && tuning().mqg != 0;
+    if (mfma) {
+      snprintf(name, sizeof(name), "attnres_route_bwd_dqwm_bf_v%d", v);
+    } else {
+      snprintf(name, sizeof(name), "attnres_route_bwd_dqw_%s_v%d", bf ? "bf" : "f32", v);
+    }
+    int rc = find_function(st, mfma ? kBwdMqgPart : kBwdMqPart, name, &st.bwd_dqw[idx]);
     if (rc != ATTNRES_OK) return rc;
   }
   if (st.bwd_dqw_bpc_block[idx] != block) {
@@ -359,7 +366,6 @@ int get_bwd_dqw(DeviceState& st, bool bf, int v, int block, hipFunction_t* f, in
 // sources, output gradients and parameters, 1 <= S <= 8, Q <= 8, two chunks
 // per thread in workgroups of at most 256 threads, the Q folded queries in
 // `lds` bytes of dynamic LDS.
-constexpr int kBwdMqgPart = 7;
 constexpr int kBwdMqgMaxThreads = 256;
 bool bwd_mqg_shape(bool bf, bool gbf, bool pbf, int s, int nq, int nchunk) {
   return tuning().mqg != 0 && bf && gbf && pbf && s >= 1 && s <= 8 && nq >= 1 && nq <= 8 &&

@@ -2269,6 +2269,101 @@ __device__ __forceinline__ void route_bwd_dqw_body(const attnres_route_bwd_dqw_p
 }
 
 
+// Query-gradient partials on the matrix cores (bf16 sources): as
+// route_bwd_dqw_body, with sum_s c1_qs x_s formed per element as column j
+// of a 4x4x4 block product: A = c1 of four queries (lane 4b+i: query
+// q0 + 4*g4 + i) over four sources (k), as bf16 hi + lo parts; B = the
+// lane's own four sources at that element.  Per row and group of four
+// sources: the source chunks and the lane's c1 values are requested
+// together, then 2 * 2 MFMAs per element (two query groups, hi and lo).
+template <int V>
+__device__ __forceinline__ void route_bwd_dqwm_body(const attnres_route_bwd_dqw_params& P) {
+  constexpr int NQ4 = 2;  // eight queries per pass
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int block = P.block;
+  const int S = P.num_sources;
+  const int nq = P.num_queries;
+  const int q0 = P.q0;
+  const int ng = nq - q0 < 4 * NQ4 ? nq - q0 : 4 * NQ4;
+  const int ai = lane & 3;
+
+  int chunk[V];
+  bool ok[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    chunk[k] = tid + k * block;
+    ok[k] = chunk[k] < P.nchunk;
+  }
+  f32x4 acc[V][8][NQ4];  // element h of chunk k, queries q0 + 4*g4 + i in acc[k][h][g4][i]
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+#pragma unroll
+      for (int g4 = 0; g4 < NQ4; ++g4) acc[k][h][g4] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  const int64_t row_bytes_ld = P.src_ld * 2;
+  const uint32_t row_bytes = (uint32_t)(P.d * 2);
+  for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
+    const float* crow = P.c1 + (tok * nq + q0) * S;
+    for (int s0 = 0; s0 < S; s0 += 4) {
+      u32x4 x[4][V];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int s = s0 + i < S ? s0 + i : S - 1;  // past S: a repeated row, coefficient 0 below
+        char* row = reinterpret_cast<char*>(const_cast<void*>(P.src[s])) + tok * row_bytes_ld;
+        const __amdgpu_buffer_rsrc_t rs = row_rsrc(row, row_bytes);
+#pragma unroll
+        for (int k = 0; k < V; ++k) x[i][k] = ld_row(rs, (uint32_t)chunk[k] * 16);
+      }
+      u32x2 ah[NQ4], al[NQ4];
+#pragma unroll
+      for (int g4 = 0; g4 < NQ4; ++g4) {
+        const int g = 4 * g4 + ai;
+        float c[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) c[kk] = (g < ng && s0 + kk < S) ? crow[g * S + s0 + kk] : 0.f;
+        const uint32_t h01 = pack_bf16(c[0], c[1]), h23 = pack_bf16(c[2], c[3]);
+        ah[g4] = u32x2{h01, h23};
+        al[g4] = u32x2{pack_bf16(c[0] - bf_lo(h01), c[1] - bf_hi(h01)), pack_bf16(c[2] - bf_lo(h23), c[3] - bf_hi(h23))};
+      }
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const u32x2 blo = {__builtin_amdgcn_perm(x[1][k][w], x[0][k][w], 0x05040100u),
+                             __builtin_amdgcn_perm(x[3][k][w], x[2][k][w], 0x05040100u)};
+          const u32x2 bhi = {__builtin_amdgcn_perm(x[1][k][w], x[0][k][w], 0x07060302u),
+                             __builtin_amdgcn_perm(x[3][k][w], x[2][k][w], 0x07060302u)};
+#pragma unroll
+          for (int g4 = 0; g4 < NQ4; ++g4) {
+            acc[k][2 * w][g4] = mfma_4x4x4(al[g4], blo, mfma_4x4x4(ah[g4], blo, acc[k][2 * w][g4]));
+            acc[k][2 * w + 1][g4] = mfma_4x4x4(al[g4], bhi, mfma_4x4x4(ah[g4], bhi, acc[k][2 * w + 1][g4]));
+          }
+        }
+      }
+    }
+  }
+  float* prow = P.part + (int64_t)blockIdx.x * nq * P.d;
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    if (!ok[k]) continue;
+#pragma unroll
+    for (int g4 = 0; g4 < NQ4; ++g4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int g = 4 * g4 + i;
+        if (g >= ng) continue;
+        float4* dst = reinterpret_cast<float4*>(prow + (int64_t)(q0 + g) * P.d + (int64_t)chunk[k] * 8);
+        dst[0] = make_float4(acc[k][0][g4][i], acc[k][1][g4][i], acc[k][2][g4][i], acc[k][3][g4][i]);
+        dst[1] = make_float4(acc[k][4][g4][i], acc[k][5][g4][i], acc[k][6][g4][i], acc[k][7][g4][i]);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------ merge backward body --
 
 // VEC consecutive elements of a bf16 or fp32 row as fp32 (chunk = VEC elements).
@@ -2736,7 +2831,13 @@ BWD_DQW(bf, true, 1) BWD_DQW(bf, true, 2) BWD_DQW(f32, false, 1) BWD_DQW(f32, fa
 // and parameters): attnres_route_bwd_mqg_s<S>_q<NQ4>, up to 4*NQ4 queries, two
 // chunks per thread, at most 256 threads (rows of up to 4096 bf16 elements).
 #define BWD_MQG(S, NQ4)                                                                           extern "C" __global__ void __launch_bounds__(512) attnres_route_bwd_mqg_s##S##_q##NQ4(              attnres_route_bwd_mq_params P) {                                                              route_bwd_mqg_body<S, 2, NQ4>(P);                                                             }
+#define BWD_DQWM(V)                                                                             \
+  extern "C" __global__ void __launch_bounds__(512) attnres_route_bwd_dqwm_bf_v##V(             \
+      attnres_route_bwd_dqw_params P) {                                                         \
+    route_bwd_dqwm_body<V>(P);                                                                  \
+  }
 #if ATTNRES_PART == 7 || defined(ATTNRES_ALL_PARTS)
+BWD_DQWM(1) BWD_DQWM(2)
 BWD_MQG(1, 1) BWD_MQG(2, 1) BWD_MQG(3, 1) BWD_MQG(4, 1) BWD_MQG(5, 1) BWD_MQG(6, 1) BWD_MQG(7, 1) BWD_MQG(8, 1)
 BWD_MQG(1, 2) BWD_MQG(2, 2) BWD_MQG(3, 2) BWD_MQG(4, 2) BWD_MQG(5, 2) BWD_MQG(6, 2) BWD_MQG(7, 2) BWD_MQG(8, 2)
 #endif
