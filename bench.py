@@ -22,8 +22,9 @@ engine's two-phase routing at the 3B shape (batched phase 1 per block + phase-2
 merges: (S + Q) rows per phase-1 call, 3 rows per merge).  ``--pass bwd`` times the
 backward of the same routing calls instead (attnres_route_bwd on preallocated
 gradient buffers: (2S+1) * B*T*D * 2 algorithmic bytes per call — sources and
-dL/dout read, source gradients written).  ``--gpus`` above 1 exits: this
-build measures one GPU.
+dL/dout read, source gradients written; for cfg2serve the batched-query
+backward of each phase-1 call, (3S+Q) rows, and the merge backward, 5 rows).
+``--gpus`` above 1 exits: this build measures one GPU.
 """
 
 from __future__ import annotations
@@ -241,6 +242,18 @@ def bench_serve(steps: int, warmup: int, dev):
     return elapsed, step_bytes, merge_ms, 3 * row, p1_ms, (deepest + p1_q) * row
 
 
+def bwdq_kernel_name(s: int, hidden: int, queries: int) -> str:
+    """Symbol of the first kernel of the bf16 batched-query backward for this shape."""
+    import ctypes
+
+    from kotodama_amd import _capi
+
+    buf = ctypes.create_string_buffer(128)
+    _capi.check("attnres_route_bwd_queries_kernel_name", _capi.lib().attnres_route_bwd_queries_kernel_name(
+        s, hidden, _capi.DTYPE_BF16, _capi.DTYPE_BF16, _capi.DTYPE_BF16, queries, buf, 128))
+    return buf.value.decode()
+
+
 def bwd_call_bytes(w, s: int) -> int:
     """Algorithmic bytes of one backward call: S source rows + dL/dout read, S gradient rows written."""
     return (2 * s + 1) * w.tokens * w.hidden * w.elem_bytes
@@ -299,6 +312,102 @@ def bench_backward(w, steps: int, warmup: int, dev):
     dom_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in events)
     step_bytes = sum(bwd_call_bytes(w, s) for s in w.calls)
     return elapsed, dominant, dom_ms, bwd_call_bytes(w, dominant), step_bytes
+
+
+def bench_serve_backward(steps: int, warmup: int, dev):
+    """Backward of cfg2serve's routing calls, through the C ABI on preallocated buffers.
+
+    Per block of sublayers: the batched-query backward of its phase-1 call
+    (attnres_route_bwd_queries, Q=8 over S=1..7 blocks) and the backward of
+    its 7 merges (attnres_merge_bwd); the final phase-1 call's backward
+    (attnres_route_bwd, S=8).  Algorithmic bytes: batched backward (3S + Q)
+    rows (S read for the source gradients and again for the query gradients,
+    Q output gradients read, S gradients written), merge backward 5 rows
+    (partial, inter, dL/dout read; dL/dpartial, dL/dinter written), final
+    2S + 1 rows.  Returns (elapsed, step_bytes, deepest_ms, deepest_bytes).
+    """
+    import torch
+
+    from kotodama_amd import _capi, ops, workloads
+
+    w = workloads.get("cfg2")
+    sched = w.schedule
+    n, d = w.tokens, w.hidden
+    row = n * d * w.elem_bytes
+    pool = workloads.make_pool(w, dev, seed=2)
+    q, gn = workloads.make_params(w, dev, seed=2, count=sched.num_points)
+    pq = (q * gn).contiguous()
+    bounds = [2 * b for b in sorted(sched.boundary_set)]
+    n_sub = 2 * sched.num_layers
+    ranges = [(st, bounds[i + 1] if i + 1 < len(bounds) else n_sub) for i, st in enumerate(bounds)]
+    qmax = max(e - st for st, e in ranges)
+    gen = torch.Generator(device=dev).manual_seed(6)
+    gout = torch.randn((qmax, n, d), device=dev, generator=gen).to(w.dtype)
+    glse = torch.randn((qmax, n), device=dev, generator=gen)
+    partials = workloads.make_deltas(w, dev, 7, 1)
+    grad = torch.empty_like(pool)
+    slot = n * d * pool.element_size()
+    src_ptrs = [pool.data_ptr() + i * slot for i in range(pool.shape[0])]
+    grad_ptrs = [grad.data_ptr() + i * slot for i in range(pool.shape[0])]
+    nbw = max(_capi.route_bwd_queries_workspace_size(n, d, k + 1, e - st) for k, (st, e) in enumerate(ranges))
+    nbw = max(nbw, _capi.route_bwd_workspace_size(n, d))
+    ws = torch.empty(nbw // 4 + 1, device=dev, dtype=torch.float32)
+    dq = torch.empty((qmax, d), device=dev, dtype=pq.dtype)
+    gp, gi = torch.empty((n, d), device=dev, dtype=w.dtype), torch.empty((n, d), device=dev, dtype=w.dtype)
+    gl = torch.empty(n, device=dev, dtype=torch.float32)
+    code = ops.dtype_code(w.dtype)
+    pcode = ops.dtype_code(pq.dtype)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    deepest = len(ranges)
+    calls, step_bytes = [], 0
+    for k, (st, e) in enumerate(ranges):
+        s, nq = k + 1, e - st
+        calls.append(("q", s == deepest, (
+            _capi.pointer_array(src_ptrs[:s]), s, n, d, d, code, pq[st].data_ptr(), None, nq, pcode, w.eps,
+            gout.data_ptr(), code, d, n * d, glse.data_ptr(), _capi.pointer_array(grad_ptrs[:s]), d, ws.data_ptr(),
+            ws.numel() * 4, dq.data_ptr(), None, stream)))
+        step_bytes += (3 * s + nq) * row
+        for qo in range(1, nq):
+            calls.append(("m", False, (
+                partials[0].data_ptr(), n, d, code, pq[st + qo].data_ptr(), pcode, gout[qo].data_ptr(), code,
+                glse[qo].data_ptr(), w.eps, gout[0].data_ptr(), gp.data_ptr(), gi.data_ptr(), gl.data_ptr(),
+                ws.data_ptr(), ws.numel() * 4, dq.data_ptr(), stream)))
+            step_bytes += 5 * row
+    s = len(ranges) + 1
+    calls.append(("r", False, (
+        _capi.pointer_array(src_ptrs[:s]), s, n, d, d, code, pq[-1].data_ptr(), None, pcode, w.eps,
+        gout[0].data_ptr(), code, d, glse[0].data_ptr(), _capi.pointer_array(grad_ptrs[:s]), d, ws.data_ptr(),
+        ws.numel() * 4, dq.data_ptr(), None, stream)))
+    step_bytes += (2 * s + 1) * row
+
+    def step(events=None):
+        for kind, timed, a in calls:
+            if events is not None and timed:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+            if kind == "q":
+                if _capi.route_bwd_queries(*a) != _capi.OK:
+                    raise RuntimeError("batched-query backward unsupported for the serving shape")
+            elif kind == "m":
+                _capi.merge_bwd(*a)
+            else:
+                _capi.route_bwd(*a)
+            if events is not None and timed:
+                e1.record()
+                events.append((e0, e1))
+
+    with torch.inference_mode():
+        for _ in range(warmup):  # the same calls as the timed steps, event records included
+            step([])
+        torch.cuda.synchronize()
+        events: list = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(events)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    deepest_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in events)
+    return elapsed, step_bytes, deepest_ms, (3 * deepest + (ranges[-1][1] - ranges[-1][0])) * row
 
 
 def bench_decode(w, steps: int, warmup: int, dev):
@@ -385,6 +494,34 @@ def main() -> int:
         ms = elapsed * 1e3 / args.steps
         print(json.dumps({"workload": WORKLOAD_TEXT["copy"], "bytes_read": nbytes // 2, "bytes_written": nbytes // 2,
                           "ms_per_copy": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return 0
+    if args.workload == "cfg2serve" and args.pass_ == "bwd":
+        elapsed, step_bytes, deep_ms, deep_bytes = bench_serve_backward(args.steps, args.warmup, dev)
+        ms_per_step = elapsed * 1e3 / args.steps
+        gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+        w2 = workloads.get("cfg2")
+        ach = deep_bytes / (deep_ms * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": "AttnRes serving two-phase routing backward achieved HBM GB/s",
+            "value": round(gbs, 2),
+            "unit": "GB/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms_per_step, 4),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "bf16",
+            "data": "synthetic (seeded blocks, partials and output gradients, resident in HBM)",
+            "config": {"workload": "backward of: " + WORKLOAD_TEXT["cfg2serve"], "algorithmic_bytes_per_step": step_bytes},
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(w2.tokens / (ms_per_step * 1e-3), 1),
+            "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": bwdq_kernel_name(7, w2.hidden, 8) + " (+ query-gradient pass, reduction; S=7, Q=8)",
+                         "algorithmic_bytes": deep_bytes, "avg_ms": round(deep_ms, 4)},
+        }), flush=True)
         return 0
     if args.workload == "cfg2serve":
         elapsed, step_bytes, merge_ms, merge_bytes, p1_ms, p1_bytes = bench_serve(args.steps, args.warmup, dev)
