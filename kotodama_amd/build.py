@@ -3,7 +3,7 @@
 Steps (all outputs under ``kotodama_amd/lib/``):
 
 1. ``hipcc --genco --offload-arch=gfx950`` compiles ``csrc/attnres_kernels.hip``
-   six times (``-DATTNRES_PART=0..5``, in parallel) into code-object parts.
+   once per code-object part (``-DATTNRES_PART=0..7``, in parallel).
 2. ``gcc`` assembles ``csrc/attnres_blob.S``, which ``.incbin``s the parts.
 3. ``g++`` builds ``csrc/attnres_capi.cpp`` + the blob into the shared library,
    linked against ROCm's ``libamdhip64.so.7``.  Loaded after ``import torch``,
