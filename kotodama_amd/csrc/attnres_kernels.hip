@@ -2830,7 +2830,15 @@ BWD_DQW(bf, true, 1) BWD_DQW(bf, true, 2) BWD_DQW(f32, false, 1) BWD_DQW(f32, fa
 // Batched-query backward on the matrix cores (bf16 sources, output gradients
 // and parameters): attnres_route_bwd_mqg_s<S>_q<NQ4>, up to 4*NQ4 queries, two
 // chunks per thread, at most 256 threads (rows of up to 4096 bf16 elements).
-#define BWD_MQG(S, NQ4)                                                                           extern "C" __global__ void __launch_bounds__(512) attnres_route_bwd_mqg_s##S##_q##NQ4(              attnres_route_bwd_mq_params P) {                                                              route_bwd_mqg_body<S, 2, NQ4>(P);                                                             }
+#ifndef MQG_WAVES_PER_EU
+#define MQG_WAVES_PER_EU(S, NQ4) 2
+#endif
+#define BWD_MQG(S, NQ4)                                                                         \
+  extern "C" __global__ void __launch_bounds__(256)                                             \
+      __attribute__((amdgpu_waves_per_eu(MQG_WAVES_PER_EU(S, NQ4))))                            \
+      attnres_route_bwd_mqg_s##S##_q##NQ4(attnres_route_bwd_mq_params P) {                      \
+    route_bwd_mqg_body<S, 2, NQ4>(P);                                                           \
+  }
 #define BWD_DQWM(V)                                                                             \
   extern "C" __global__ void __launch_bounds__(512) attnres_route_bwd_dqwm_bf_v##V(             \
       attnres_route_bwd_dqw_params P) {                                                         \
