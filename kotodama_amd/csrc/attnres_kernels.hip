@@ -1933,8 +1933,8 @@ __device__ __forceinline__ void route_bwd_mq_body(const attnres_route_bwd_mq_par
 // the output-gradient chunks of every query are loaded once (the next row's
 // after the current row's stores), the folded queries sit in dynamic LDS.
 // Per group of four queries:
-//  * sum(x^2), x.qw_q and x.G_q per (query, source) with v_dot2_f32_bf16,
-//    reduced by the transposing tree, one LDS exchange;
+//  * x.qw_q and x.G_q per (query, source) with v_dot2_f32_bf16 (sum(x^2) in
+//    the first group), reduced by the transposing tree, one LDS exchange;
 //  * lane 8g + s runs the softmax of query g over the sources and forms
 //      w_qs, c1_qs = w_qs (g_lse + G_q.x_s - G_q.out_q) r_s,
 //      c2_qs = -c1_qs l_qs r_s / D
@@ -2015,32 +2015,38 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
   };
   if ((int64_t)blockIdx.x < P.n_tokens) load_row(blockIdx.x);
 
-  const int sg = lane / SEG, ss = lane % SEG;  // softmax lane: query sg of the group, source ss
-  const int ai = lane & 3;                     // A-operand row: source 4*ks + ai
   __syncthreads();
 
   int ph = 0;
   for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
-    float ssp[S];
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      ssp[s] = 0.f;
-#pragma unroll
-      for (int k = 0; k < V; ++k) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) ssp[s] = dot2_bf16(x[s][k][w], x[s][k][w], ssp[s]);
-      }
-    }
+    // Lane-derived indices and addresses are recomputed per row from an
+    // opaque copy of the lane id: hoisted out of the row loop they stayed
+    // live across it and spilled.
+    int lr = lane;
+    asm volatile("" : "+v"(lr));
+    const int sg = lr / SEG, ss = lr % SEG;  // softmax lane: query sg of the group, source ss
+    const int ai = lr & 3;                   // A-operand row: source 4*ks + ai
     u32x2 awh[NQ4][KS], awl[NQ4][KS], ach[NQ4][KS], acl[NQ4][KS];
     float c2acc = 0.f;
+    float rl = 0.f;  // 1/rms of source ss, from the first group's reduction
 #pragma unroll
     for (int g4 = 0; g4 < NQ4; ++g4) {
       const int q0 = 4 * g4;
-      // ---- x.qw and x.G of four queries, packed dot products, two reductions ----
+      // ---- sum(x^2) (first group), x.qw and x.G of four queries, packed dot products, two reductions ----
       {
         float part[NPA];
 #pragma unroll
-        for (int j = 0; j < NPA; ++j) part[j] = j < S ? ssp[j] : 0.f;
+        for (int j = 0; j < NPA; ++j) part[j] = 0.f;
+        if (g4 == 0) {
+#pragma unroll
+          for (int k = 0; k < V; ++k) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+#pragma unroll
+              for (int w = 0; w < 4; ++w) part[s] = dot2_bf16(x[s][k][w], x[s][k][w], part[s]);
+            }
+          }
+        }
 #pragma unroll
         for (int k = 0; k < V; ++k) {
           u32x4 qv[4];
@@ -2055,7 +2061,7 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
             }
           }
         }
-        wave_reduce_to_lds<HA>(part, red[ph][wave], lane);
+        wave_reduce_to_lds<HA>(part, red[ph][wave], lr);
       }
       {
         float part[NPB];
@@ -2072,7 +2078,7 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
             }
           }
         }
-        wave_reduce_to_lds<HB>(part, red[ph][wave] + NPA, lane);
+        wave_reduce_to_lds<HB>(part, red[ph][wave] + NPA, lr);
       }
       __syncthreads();
 
@@ -2082,13 +2088,13 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
       float t_ss = 0.f, t_dot = 0.f, t_gx = 0.f;
       if (slot) {
         for (int w = 0; w < nwaves; ++w) {
-          t_ss += red[ph][w][ss];
+          if (g4 == 0) t_ss += red[ph][w][ss];
           t_dot += red[ph][w][S + sg * S + ss];
           t_gx += red[ph][w][NPA + sg * S + ss];
         }
       }
       ph ^= 1;
-      const float rl = __builtin_amdgcn_rsqf(t_ss * P.inv_d + P.eps);
+      if (g4 == 0) rl = __builtin_amdgcn_rsqf(t_ss * P.inv_d + P.eps);
       const float ll = slot ? t_dot * rl : -__builtin_inff();
       const float m = seg_max<SEG>(ll);
       const float el = slot ? __expf(ll - m) : 0.f;
