@@ -242,6 +242,19 @@ def bench_serve(steps: int, warmup: int, dev):
     return elapsed, step_bytes, merge_ms, 3 * row, p1_ms, (deepest + p1_q) * row
 
 
+def bwd_kernel_name(s: int, tokens: int, hidden: int, dtype) -> str:
+    """Symbol of the single-query backward kernel for this shape (dL/dout in the source dtype)."""
+    import ctypes
+
+    from kotodama_amd import _capi, ops
+
+    code = ops.dtype_code(dtype)
+    buf = ctypes.create_string_buffer(128)
+    _capi.check("attnres_route_bwd_kernel_name",
+                _capi.lib().attnres_route_bwd_kernel_name(s, tokens, hidden, code, code, buf, 128))
+    return buf.value.decode()
+
+
 def bwdq_kernel_name(s: int, hidden: int, queries: int) -> str:
     """Symbol of the first kernel of the bf16 batched-query backward for this shape."""
     import ctypes
@@ -565,8 +578,7 @@ def main() -> int:
         ms_per_step = elapsed * 1e3 / args.steps
         gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
         achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-        t = 'bf' if w.dtype == torch.bfloat16 else 'f32'
-        name = f"attnres_route_bwd_{t}_g{t}_s{dominant}_v1 (+ attnres_reduce_dqw_stage, attnres_reduce_dqw)"
+        name = bwd_kernel_name(dominant, w.tokens, w.hidden, w.dtype) + " (+ attnres_reduce_dqw_stage, attnres_reduce_dqw)"
         traffic, traffic_src = load_traffic(f"bwd_{args.workload}_s{dominant}")
         print(json.dumps({
             "metric": "AttnRes routing backward achieved HBM GB/s",

@@ -201,6 +201,14 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
                       void* grad_query, void* grad_gain, void* stream);
 
 /*
+ * Symbol name of the kernel attnres_route_bwd launches for these arguments,
+ * for matching profiler output; written NUL-terminated into buf.  Loads the
+ * code object on the current device.  No counterpart in the reference.
+ */
+int attnres_route_bwd_kernel_name(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int grad_out_dtype,
+                                  char* buf, int buf_len);
+
+/*
  * Bytes of device workspace attnres_route_bwd_queries needs on the current
  * device: the fp32 coefficients (num_tokens, num_queries, num_sources) plus
  * per-workgroup partials of the num_queries query gradients.

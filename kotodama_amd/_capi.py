@@ -52,6 +52,7 @@ EXPORTS = (
     "attnres_block_step",
     "attnres_route_bwd_workspace_size",
     "attnres_route_bwd",
+    "attnres_route_bwd_kernel_name",
     "attnres_route_bwd_queries_workspace_size",
     "attnres_route_bwd_queries",
     "attnres_route_bwd_queries_kernel_name",
@@ -167,6 +168,10 @@ _SIGNATURES = {
         _c_int,
     ),
     "attnres_route_bwd_queries_workspace_size": ([_c_i64, _c_int, _c_int, _c_int, ctypes.POINTER(_c_i64)], _c_int),
+    "attnres_route_bwd_kernel_name": (
+        [_c_int, _c_i64, _c_int, _c_int, _c_int, ctypes.c_char_p, _c_int],
+        _c_int,
+    ),
     "attnres_route_bwd_queries_kernel_name": (
         [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.c_char_p, _c_int],
         _c_int,

@@ -457,6 +457,20 @@ int grid_for(int64_t n_tokens, int num_cus, int bpc) {
   return (int)grid;
 }
 
+// Chunks per thread of the single-query backward: one where the row fits in
+// one workgroup, except S >= 5 over many rows of at most 384 chunks: there
+// two (half the waves per row) measured 2-4% faster per call at the 3B
+// prefill shape (32768 rows), while at 8192 rows and for 512-chunk rows two
+// measured 1-2% slower.  ATTNRES_V=1 / 2 force one or two.
+int bwd_chunks_per_thread(int nchunk, int num_sources, int64_t num_tokens, int num_cus) {
+  const bool fits1 = round64(nchunk) <= kMaxThreads;
+  int v = fits1 ? 1 : 2;
+  if (v == 1 && num_sources >= 5 && nchunk <= 384 && num_tokens >= 64LL * num_cus) v = 2;
+  if (tuning().force_v == 2) v = 2;
+  if (tuning().force_v == 1 && fits1) v = 1;
+  return v;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 bool valid_dtype(int d) { return d == ATTNRES_DTYPE_F32 || d == ATTNRES_DTYPE_BF16; }
@@ -718,6 +732,24 @@ int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, i
   return ATTNRES_OK;
 }
 
+int attnres_route_bwd_kernel_name(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int grad_out_dtype,
+                                  char* buf, int buf_len) {
+  if (buf == nullptr || buf_len < 1) return fail(ATTNRES_ERR_ARG, "no output buffer");
+  if (!valid_dtype(src_dtype) || !valid_dtype(grad_out_dtype)) return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (num_sources < 1 || num_sources > ATTNRES_MAX_SOURCES || hidden <= 0 || num_tokens < 0)
+    return fail(ATTNRES_ERR_ARG, "bad shape");
+  const bool bf = src_dtype == ATTNRES_DTYPE_BF16;
+  const int vec = bf ? 8 : 4;
+  if (hidden % vec != 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d is not a multiple of %d", hidden, vec);
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  const int v = bwd_chunks_per_thread(hidden / vec, num_sources, num_tokens, st->num_cus);
+  snprintf(buf, (size_t)buf_len, "attnres_route_bwd_%s_g%s_s%d_v%d", bf ? "bf" : "f32",
+           grad_out_dtype == ATTNRES_DTYPE_BF16 ? "bf" : "f32", num_sources, v);
+  return ATTNRES_OK;
+}
+
 int attnres_route_bwd_queries_kernel_name(int num_sources, int hidden, int src_dtype, int param_dtype,
                                           int grad_out_dtype, int num_queries, char* buf, int buf_len) {
   if (buf == nullptr || buf_len < 1) return fail(ATTNRES_ERR_ARG, "no output buffer");
@@ -910,8 +942,7 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
-  // one chunk per thread where the row fits in one workgroup (ATTNRES_V=2 forces two)
-  const int v = round64(nchunk) <= kMaxThreads && tuning().force_v != 2 ? 1 : 2;
+  const int v = bwd_chunks_per_thread(nchunk, num_sources, num_tokens, st->num_cus);
   const int block = v == 1 ? round64(nchunk) : round64((nchunk + 1) / 2);
   hipFunction_t f = nullptr;
   int bpc = 1;
