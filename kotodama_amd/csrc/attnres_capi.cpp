@@ -458,14 +458,15 @@ int grid_for(int64_t n_tokens, int num_cus, int bpc) {
 }
 
 // Chunks per thread of the single-query backward: one where the row fits in
-// one workgroup, except S >= 5 over many rows of at most 384 chunks: there
-// two (half the waves per row) measured 2-4% faster per call at the 3B
+// one workgroup, except 5 <= S <= 8 over many rows of at most 384 chunks:
+// there two (half the waves per row) measured 2-4% faster per call at the 3B
 // prefill shape (32768 rows), while at 8192 rows and for 512-chunk rows two
-// measured 1-2% slower.  ATTNRES_V=1 / 2 force one or two.
+// measured 1-2% slower (and the two-chunk instances spill from S = 12).
+// ATTNRES_V=1 / 2 force one or two.
 int bwd_chunks_per_thread(int nchunk, int num_sources, int64_t num_tokens, int num_cus) {
   const bool fits1 = round64(nchunk) <= kMaxThreads;
   int v = fits1 ? 1 : 2;
-  if (v == 1 && num_sources >= 5 && nchunk <= 384 && num_tokens >= 64LL * num_cus) v = 2;
+  if (v == 1 && num_sources >= 5 && num_sources <= 8 && nchunk <= 384 && num_tokens >= 64LL * num_cus) v = 2;
   if (tuning().force_v == 2) v = 2;
   if (tuning().force_v == 1 && fits1) v = 1;
   return v;
