@@ -293,6 +293,38 @@ def test_batched_query_backward_matches_oracle(gpu, monkeypatch, dtype, S, D, B,
         check_grad(gain.grad, dgain, dtype, "dgain (sum over queries)")
 
 
+@pytest.mark.parametrize("S,Q", [(3, 8), (7, 6)])
+def test_batched_query_backward_many_rows_per_workgroup(gpu, S, Q):
+    # 12288 rows of 512 elements on the matrix-core kernels: more rows than
+    # the resident grid, so every workgroup walks several rows (next-row
+    # loads, coefficients and reductions per row, query-gradient accumulators
+    # across rows)
+    eps, D, N = 1e-5, 512, 12288
+    name = bwd_queries_kernel(S, D, torch.bfloat16, Q)
+    assert name.startswith("attnres_route_bwd_mqg_"), name
+    print(f"batched-query backward over {N} rows S={S} Q={Q} {name}", flush=True)
+    buf, _, _, _ = make_case(gpu, S, 0, 1, N, D, torch.bfloat16, seed=200 + S)
+    g = torch.Generator(device="cpu").manual_seed(201 + S)
+    qs = (torch.randn(Q, D, generator=g) * 0.05).to(torch.bfloat16).to(gpu).requires_grad_(True)
+    gain = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(gpu).requires_grad_(True)
+    G = torch.randn(Q, 1, N, D, generator=g).to(torch.bfloat16).float().to(gpu)
+    GL = torch.randn(Q, 1, N, generator=g).to(gpu)
+    buf.requires_grad_(True)
+    out, _, lse, _, _ = ops.route(buf, S, qs, gain, eps, torch.bfloat16, True, False)
+    (out.float() * G).sum().add_((lse * GL).sum()).backward()
+    x = np64(buf).reshape(S, -1, D)
+    dx = np.zeros_like(x)
+    dgain = np.zeros(D)
+    for j in range(Q):
+        qw = O.fold_query(np64(qs[j]), np64(gain), "bf16")
+        b = O.route_backward(x, qw, eps, np64(G[j]).reshape(-1, D), np64(GL[j]).reshape(-1))
+        dx += b["dx"]
+        check_grad(qs.grad[j], b["dqw"] * np64(gain), torch.bfloat16, f"dquery[{j}]")
+        dgain += b["dqw"] * np64(qs[j])
+    check_grad(buf.grad.reshape(S, -1, D), dx, torch.bfloat16, "dsources (sum over queries)")
+    check_grad(gain.grad, dgain, torch.bfloat16, "dgain (sum over queries)")
+
+
 def test_batched_query_backward_unsupported_shape_raises(gpu):
     # bf16 rows above 4096 elements (two chunks per thread) with 5 sources and
     # several queries: no batched kernel, and the per-query composition's fp32

@@ -234,6 +234,29 @@ def test_batched_query_kernel_every_source_count(gpu, d, n, queries):
             np.testing.assert_allclose(np64(inv).reshape(n, S), ref["inv_rms"], rtol=1e-5)
 
 
+@pytest.mark.parametrize("S,Q", [(3, 8), (7, 5)])
+def test_batched_query_kernel_many_rows_per_workgroup(gpu, S, Q):
+    # 12288 rows of 512 elements: more rows than the resident grid holds
+    # workgroups, so every workgroup walks several rows (next-row loads,
+    # double-buffered reduction rows); rows sampled from start, middle and end
+    d, n = 512, 12288
+    g = torch.Generator(device=gpu).manual_seed(101 + S)
+    scales = torch.exp(torch.empty(S, device=gpu).uniform_(math.log(0.3), math.log(4), generator=g))
+    buf = (torch.randn((S, n, d), generator=g, device=gpu) * scales.view(-1, 1, 1)).to(torch.bfloat16)
+    pq = (torch.randn((Q, d), generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+    name = route_kernel(S, n, d, Q)
+    assert name.endswith("_qg"), name
+    print(f"batched-query kernel over {n} rows S={S} Q={Q} {name}", flush=True)
+    out, w, lse, _, _ = ops.route(buf, S, pq, None, 1e-5, torch.bfloat16, True, False)
+    rows = np.concatenate([np.arange(0, 256), np.arange(n // 2 - 128, n // 2 + 128), np.arange(n - 256, n)])
+    ref = O.route(np64(buf)[:, rows], np64(pq), 1e-5)
+    for q in range(Q):
+        label = f"S={S} Q={Q} q={q} rows sampled"
+        check_bf16(out[q][rows], ref["out"][q], label)
+        check_weights(w[q][:, rows], ref["weights"][q], label)
+        np.testing.assert_allclose(np64(lse[q])[rows], ref["lse"][q], rtol=1e-5, atol=1e-5)
+
+
 def test_batched_query_kernel_falls_back_past_lds(gpu):
     # 11 queries of 8192 elements (176 KiB of staged queries) exceed one
     # workgroup's LDS: the per-query kernel runs, with the same results
