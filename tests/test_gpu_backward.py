@@ -293,6 +293,27 @@ def test_batched_query_backward_matches_oracle(gpu, monkeypatch, dtype, S, D, B,
         check_grad(gain.grad, dgain, dtype, "dgain (sum over queries)")
 
 
+def test_batched_query_backward_without_lse_gradient(gpu):
+    # the loss uses the routed rows only: no dL/dlse reaches the batched
+    # backward (grad_lse NULL through the C ABI), on the matrix-core kernel
+    eps, S, Q, D, N = 1e-5, 4, 5, 1024, 48
+    assert bwd_queries_kernel(S, D, torch.bfloat16, Q).startswith("attnres_route_bwd_mqg_")
+    buf, _, _, _ = make_case(gpu, S, 0, 1, N, D, torch.bfloat16, seed=300)
+    g = torch.Generator(device="cpu").manual_seed(301)
+    qs = (torch.randn(Q, D, generator=g) * 0.05).to(torch.bfloat16).to(gpu).requires_grad_(True)
+    G = torch.randn(Q, 1, N, D, generator=g).to(torch.bfloat16).float().to(gpu)
+    buf.requires_grad_(True)
+    out, _, _, _, _ = ops.route(buf, S, qs, None, eps, torch.bfloat16, False, False)
+    (out.float() * G).sum().backward()
+    x = np64(buf).reshape(S, -1, D)
+    dx = np.zeros_like(x)
+    for j in range(Q):
+        b = O.route_backward(x, np64(qs[j]), eps, np64(G[j]).reshape(-1, D), np.zeros(N))
+        dx += b["dx"]
+        check_grad(qs.grad[j], b["dqw"], torch.bfloat16, f"dquery[{j}]")
+    check_grad(buf.grad.reshape(S, -1, D), dx, torch.bfloat16, "dsources (sum over queries)")
+
+
 @pytest.mark.parametrize("S,Q", [(3, 8), (7, 6)])
 def test_batched_query_backward_many_rows_per_workgroup(gpu, S, Q):
     # 12288 rows of 512 elements on the matrix-core kernels: more rows than
