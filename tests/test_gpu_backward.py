@@ -293,6 +293,26 @@ def test_batched_query_backward_matches_oracle(gpu, monkeypatch, dtype, S, D, B,
         check_grad(gain.grad, dgain, dtype, "dgain (sum over queries)")
 
 
+def test_backward_chunks_per_thread_policy(gpu):
+    # two chunks per thread for 5 <= S <= 8 over many rows of at most 384
+    # chunks (3B prefill shape), one elsewhere (fewer rows, wider rows, S <= 4
+    # or S >= 9, whose two-chunk instances spill from S = 12)
+    import ctypes
+
+    def name(s, n, d):
+        buf = ctypes.create_string_buffer(128)
+        code = _capi.DTYPE_BF16
+        _capi.check("attnres_route_bwd_kernel_name", _capi.lib().attnres_route_bwd_kernel_name(s, n, d, code, code, buf, 128))
+        return buf.value.decode()
+
+    assert name(7, 32768, 3072).endswith("_s7_v2")
+    assert name(4, 32768, 3072).endswith("_s4_v1")
+    assert name(9, 32768, 3072).endswith("_s9_v1")
+    assert name(7, 8192, 3072).endswith("_s7_v1")
+    assert name(7, 32768, 4096).endswith("_s7_v1")
+    assert name(3, 64, 8192).endswith("_s3_v2")  # rows above 512 chunks: always two
+
+
 def test_batched_query_backward_without_lse_gradient(gpu):
     # the loss uses the routed rows only: no dL/dlse reaches the batched
     # backward (grad_lse NULL through the C ABI), on the matrix-core kernel
