@@ -66,7 +66,7 @@ constexpr int kStreamFuncs = kTypeCombos * 2 * kStreamMaxChunks * 3;
 constexpr int kBwdFuncs = 4 * kNumS * 2;  // (source, grad_out) dtype pairs x S x V
 constexpr int kBwdMaxPerCu = 4;           // workgroups per CU the backward grid may use (workspace bound)
 constexpr size_t kBwdStaticLds = 2 * ATTNRES_KMAX_WAVES * 48 * sizeof(float);  // reduction buffer, S = 16
-constexpr size_t kQgStaticLds = 2 * ATTNRES_KMAX_WAVES * 64 * sizeof(float);   // batched-query reduction buffer
+constexpr size_t kQgStaticLds = 2 * ATTNRES_KMAX_WAVES * 72 * sizeof(float);   // batched-query reduction buffer
 constexpr size_t kMqgStaticLds = 2 * ATTNRES_KMAX_WAVES * 72 * sizeof(float);  // its backward's (S <= 8)
 
 struct DeviceState {

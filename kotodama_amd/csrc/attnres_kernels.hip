@@ -700,13 +700,14 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
 //    weights move to scalar registers (v_readlane) and each source word is
 //    unpacked once for all the group's output rows.
 
-// Queries per group: one lane per (query, source) in the softmax and at most
-// 64 partial sums per group (S * (QG + 1)); groups of 8 up to S = 7 (at
-// S = 6-7 they cost occupancy, 2 waves per SIMD instead of 3-4, and still
-// measured 2-3% faster than groups of 4 with the mixing on the matrix cores).
+// Queries per group: one lane per (query, source) in the softmax (QG * SEG
+// <= 64 lanes); groups of 8 up to S = 8 (at S = 6-8 they cost occupancy,
+// 2 waves per SIMD instead of 3-4, and still measured 2-3% faster than
+// groups of 4 with the mixing on the matrix cores).
 #ifndef QG_OF
-#define QG_OF(S) ((S) <= 7 ? 8 : (S) <= 12 ? 4 : 2)
+#define QG_OF(S) ((S) <= 8 ? 8 : (S) <= 12 ? 4 : 2)
 #endif
+#define ATTNRES_QG_MAX_NP 72  // partial sums of a group: 4 * ceil(S * (QG + 1) / 4), S = 8 with QG = 8
 
 template <int S, int V>
 __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
@@ -716,8 +717,8 @@ __device__ __forceinline__ void route_qg_body(const attnres_route_params& P) {
   constexpr int NV = S * (QG + 1);          // sum(x^2) per source, then x.qw per (query, source)
   constexpr int H2 = (NV + 3) / 4;          // registers after the two swap rounds
   constexpr int NP = 4 * H2;                // NV padded to a multiple of 4
-  static_assert(QG * SEG <= 64 && NP <= 64, "one lane per (query, source) and per reduced value");
-  __shared__ float red[2][ATTNRES_KMAX_WAVES][64];
+  static_assert(QG * SEG <= 64 && NP <= ATTNRES_QG_MAX_NP, "one lane per (query, source); reduction rows fit");
+  __shared__ float red[2][ATTNRES_KMAX_WAVES][ATTNRES_QG_MAX_NP];
   extern __shared__ u32x4 qg_lds[];  // [query][chunk] packed folded queries
 
   const int tid = threadIdx.x;
