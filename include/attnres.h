@@ -200,6 +200,33 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
                       void* const* grad_sources, int64_t grad_ld, void* workspace, int64_t workspace_bytes,
                       void* grad_query, void* grad_gain, void* stream);
 
+/* Size of the device scratch array attnres_route_bwd_noalloc uses (32 MiB:
+ * 256 CUs x 4 workgroups x 8192 fp32 columns, the largest workspace
+ * attnres_route_bwd_workspace_size() reports on an MI355X). */
+#define ATTNRES_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/*
+ * attnres_route_bwd without the workspace argument: the query-gradient
+ * partials go to a fixed device array of ATTNRES_NOALLOC_SCRATCH_BYTES that
+ * the library holds on every device it runs on until the process ends.  The
+ * call allocates nothing (no hipMalloc, no allocating library routine); the
+ * array's device address is resolved at set-up (attnres_init(), or the first
+ * call on a device).  Shapes whose workspace would exceed the array return
+ * ATTNRES_ERR_UNSUPPORTED.  Every call on a device shares that device's
+ * array: calls that overlap on one device (concurrent streams or threads)
+ * race and must be ordered by the caller.  Results are bit-identical to
+ * attnres_route_bwd with a workspace.
+ *
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).
+ */
+int attnres_route_bwd_noalloc(const void* const* sources, int num_sources, int64_t num_tokens, int hidden,
+                              int64_t src_ld, int src_dtype, const void* query, const void* gain, int param_dtype,
+                              float eps, const void* grad_out, int grad_out_dtype, int64_t grad_out_ld,
+                              const float* grad_lse, void* const* grad_sources, int64_t grad_ld, void* grad_query,
+                              void* grad_gain, void* stream);
+
 /*
  * Symbol name of the kernel attnres_route_bwd launches for these arguments,
  * for matching profiler output; written NUL-terminated into buf.  Loads the

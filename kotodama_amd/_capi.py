@@ -52,6 +52,7 @@ EXPORTS = (
     "attnres_block_step",
     "attnres_route_bwd_workspace_size",
     "attnres_route_bwd",
+    "attnres_route_bwd_noalloc",
     "attnres_route_bwd_kernel_name",
     "attnres_route_bwd_queries_workspace_size",
     "attnres_route_bwd_queries",
@@ -161,6 +162,30 @@ _SIGNATURES = {
             _c_i64,  # grad_ld
             _c_vp,  # workspace
             _c_i64,  # workspace_bytes
+            _c_vp,  # grad_query
+            _c_vp,  # grad_gain
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
+    "attnres_route_bwd_noalloc": (
+        [
+            ctypes.POINTER(_c_vp),  # sources
+            _c_int,  # num_sources
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_i64,  # src_ld
+            _c_int,  # src_dtype
+            _c_vp,  # query
+            _c_vp,  # gain
+            _c_int,  # param_dtype
+            _c_float,  # eps
+            _c_vp,  # grad_out
+            _c_int,  # grad_out_dtype
+            _c_i64,  # grad_out_ld
+            _c_vp,  # grad_lse
+            ctypes.POINTER(_c_vp),  # grad_sources
+            _c_i64,  # grad_ld
             _c_vp,  # grad_query
             _c_vp,  # grad_gain
             _c_vp,  # stream
@@ -297,6 +322,14 @@ def route_bwd_workspace_size(num_tokens: int, hidden: int) -> int:
 
 def route_bwd(*args) -> None:
     check("attnres_route_bwd", lib().attnres_route_bwd(*args))
+
+
+def route_bwd_noalloc(*args) -> None:
+    """attnres_route_bwd without a workspace (the library's fixed scratch array)."""
+    check("attnres_route_bwd_noalloc", lib().attnres_route_bwd_noalloc(*args))
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20  # ATTNRES_NOALLOC_SCRATCH_BYTES
 
 
 def route_bwd_queries_workspace_size(num_tokens: int, hidden: int, num_sources: int, num_queries: int) -> int:

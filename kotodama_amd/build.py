@@ -5,8 +5,10 @@ Steps (all outputs under ``kotodama_amd/lib/``):
 1. ``hipcc --genco --offload-arch=gfx950`` compiles ``csrc/attnres_kernels.hip``
    once per code-object part (``-DATTNRES_PART=0..7``, in parallel).
 2. ``gcc`` assembles ``csrc/attnres_blob.S``, which ``.incbin``s the parts.
-3. ``g++`` builds ``csrc/attnres_capi.cpp`` + the blob into the shared library,
-   linked against ROCm's ``libamdhip64.so.7``.  Loaded after ``import torch``,
+3. ``hipcc -c -fPIC`` compiles ``csrc/attnres_noalloc.hip`` (the no-alloc
+   entry point; its device array needs HIP device code of its own).
+4. ``g++`` links ``csrc/attnres_capi.cpp``, the blob and that object into the
+   shared library, linked against ROCm's ``libamdhip64.so.7``.  Loaded after ``import torch``,
    the dynamic linker binds that soname to the HIP runtime torch already
    loaded, so streams and device memory are shared with torch.
 
@@ -76,6 +78,12 @@ def build(verbose: bool = False, out_dir: Path | None = None, defines: tuple = (
                 raise RuntimeError(f"hipcc failed ({p.returncode}): {' '.join(cmd)}\n{so}\n{se}")
         blob_o = tmpd / "attnres_blob.o"
         _run(["gcc", "-c", f"-I{tmpd}", str(CSRC / "attnres_blob.S"), "-o", str(blob_o)])
+        noalloc_o = tmpd / "attnres_noalloc.o"
+        noalloc_cmd = [hipcc, *[f for f in HIP_FLAGS if f != "--genco"], *extra, "-c", "-fPIC", f"-I{INCLUDE}",
+                       str(CSRC / "attnres_noalloc.hip"), "-o", str(noalloc_o)]
+        if verbose:
+            print(" ".join(noalloc_cmd), flush=True)
+        _run(noalloc_cmd)
         so_tmp = tmpd / LIB_NAME
         _run(
             [
@@ -92,6 +100,7 @@ def build(verbose: bool = False, out_dir: Path | None = None, defines: tuple = (
                 f"-I{ROCM / 'include'}",
                 str(CSRC / "attnres_capi.cpp"),
                 str(blob_o),
+                str(noalloc_o),
                 f"-L{ROCM / 'lib'}",
                 "-lamdhip64",
                 f"-Wl,-rpath,{ROCM / 'lib'}",

@@ -707,7 +707,16 @@ int reduce_launch(hipFunction_t fs, hipFunction_t fr, void* workspace, int npart
 
 }  // namespace
 
+// Device address of the no-alloc entry point's scratch array on the current
+// device, resolved once per device (attnres_noalloc.hip).
+extern "C" int attnres_internal_scratch_setup(void);
+
 extern "C" {
+
+// Sets attnres_last_error() for attnres_noalloc.hip; returns `code`.
+__attribute__((visibility("hidden"))) int attnres_internal_fail(int code, const char* msg) {
+  return fail(code, "%s", msg);
+}
 
 int attnres_version(void) { return 10000; }
 
@@ -788,7 +797,9 @@ int attnres_set_kernel_policy(int policy) {
 
 int attnres_init(void) {
   DeviceState* st = nullptr;
-  return ensure_loaded(&st);
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  return attnres_internal_scratch_setup();
 }
 
 int attnres_route_fwd(const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
