@@ -19,6 +19,8 @@ Everything here is float64 numpy restated from the reference's own Python
 * :func:`merge_backward` gradients of the merge                 kernels/phase_2.py:60-230
 * :func:`schedule`       boundary set, masks, active counts      llama.py:545-571
 * :func:`block_forward`  caller order: route -> commit -> add    llama.py:697-715 (742-762)
+* :func:`two_phase_forward` serving schedule: phase 1 per block,
+                         phase-2 merge per later sublayer        serve.py:113-164
 * :func:`bf16_round`     round-to-nearest-even to bfloat16       (torch's bf16 cast)
 
 Parity pinning (every function has checks that do not retype its formula;
@@ -27,9 +29,11 @@ x_s = c_s*u with u in {+-1}^D, qw = beta*u gives logit_s = c_s*beta*D /
 sqrt(c_s^2+eps)), invariants (scale invariance of logits, permutation
 equivariance, weights sum to 1, masked slots exactly 0, gain folding,
 phase-2 merge == routing over one more source), a pure-Python brute force on
-tiny shapes, the schedule tables derived by hand from llama.py:545-571, and
-for the backward central finite differences plus float64 torch autograd
-through the einsum branch's op sequence.
+tiny shapes, the schedule tables derived by hand from llama.py:545-571, the
+two-phase schedule equal to the one-pass caller loop in float64 (the merge
+identity at every merged sublayer; the leading-layer skip as a shifted
+one-pass loop), and for the backward central finite differences plus float64
+torch autograd through the einsum branch's op sequence.
 """
 
 from __future__ import annotations
@@ -297,6 +301,65 @@ def block_forward(
     if want_weights:
         res["weights"] = wts
     return res
+
+
+def two_phase_forward(
+    embed,
+    deltas: Sequence,
+    qws: Sequence,
+    eps: float,
+    num_layers: int,
+    boundary_set,
+    dtype: str = "f64",
+) -> dict:
+    """The serving engine's two-phase forward (serve.py:113-164) with the sublayer outputs given.
+
+    Sublayer j returns ``deltas[j]`` (its routed input h_j is recorded, not
+    consumed), as in :func:`block_forward`.  Block ranges of sublayers start at
+    ``2*b`` for the sorted boundaries b and end at the next start or at 2L
+    (serve.py:117-126; sublayers before the first boundary never run).  Per
+    range: one phase-1 routing of the range's folded queries over the committed
+    blocks (serve.py:128-136); the range's first sublayer takes the phase-1
+    output directly, every later one the phase-2 merge of the running block
+    into it (serve.py:138-156); the block's sum joins the blocks
+    (serve.py:158).  Final: phase 1 over every block with the last query
+    (serve.py:160-166).
+
+    With ``dtype == 'bf16'`` the values are rounded where the reference's
+    kernels and tensors round them: the phase-1 output to bf16
+    (kernels/phase_1.py:94, always bf16), its lse to fp32, the merge output
+    to the inter dtype bf16 (kernels/phase_2.py:54-57), and the running block
+    ``curr + delta`` to the model dtype.  With 'f64' nothing is rounded.
+    ``qws`` holds the 2L+1 folded queries ``[attn_0, mlp_0, ..., final]``.
+    Returns ``h`` ({sublayer j: its routed input (N, D)}), ``pi`` ({j: the
+    merge's weight of the running block, merged sublayers only}), ``inter``
+    ({j: the phase-1 output row it merged into}), ``final`` and ``blocks``.
+    """
+    rnd = (lambda a: round_to(a, dtype)) if dtype != "f64" else (lambda a: np.asarray(a, dtype=np.float64))
+    rnd_lse = (lambda a: round_to(a, "f32")) if dtype != "f64" else (lambda a: np.asarray(a, dtype=np.float64))
+    blocks = [rnd(embed)]
+    n_sub = 2 * num_layers
+    starts = [2 * b for b in sorted(boundary_set)]
+    ranges = [(st, starts[i + 1] if i + 1 < len(starts) else n_sub) for i, st in enumerate(starts)]
+    h, pis, inters = {}, {}, {}
+    for st, end in ranges:
+        p1 = route(np.stack(blocks), np.stack([qws[j] for j in range(st, end)]), eps)
+        p1_out, p1_lse = rnd(p1["out"]), rnd_lse(p1["lse"])
+        curr = None
+        for qo in range(end - st):
+            j = st + qo
+            if qo == 0:
+                h[j] = p1_out[0]
+                curr = rnd(deltas[j])
+            else:
+                mg = merge(curr, qws[j], p1_out[qo], p1_lse[qo], eps)
+                h[j] = rnd(mg["out"])
+                pis[j] = 1.0 / (1.0 + np.exp(-(mg["logit"] - p1_lse[qo])))
+                inters[j] = p1_out[qo]
+                curr = rnd(curr + np.asarray(deltas[j], dtype=np.float64))
+        blocks.append(curr)
+    final = rnd(route(np.stack(blocks), qws[n_sub], eps)["out"][0])
+    return {"h": h, "pi": pis, "inter": inters, "final": final, "blocks": blocks}
 
 
 # ------------------------------------------------------- brute force --

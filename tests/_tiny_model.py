@@ -23,14 +23,26 @@ class TinyNorm(nn.Module):
 
 
 class TinyAttn(nn.Module):
+    """A causal stand-in for attention with a KV cache: position t adds the mean of the
+    keys of every position up to t (the cached ones first) to a projection of x_t, so a
+    decode step depends on ``layer_past`` and decoding with the cache equals recomputing
+    the whole sequence (the contract of the reference's attention, llama.py:384-401)."""
+
     def __init__(self, d):
         super().__init__()
         self.proj = nn.Linear(d, d, bias=False)
+        self.kproj = nn.Linear(d, d, bias=False)
 
     def forward(self, x, rope_cos, rope_sin, mask=None, layer_past=None, use_cache=False):
-        y = torch.tanh(self.proj(x)) * 0.5
+        k = torch.tanh(self.kproj(x)) * 0.5
+        k_all = torch.cat([layer_past[0], k], dim=-2) if layer_past is not None else k
+        t = x.shape[-2]
+        t0 = k_all.shape[-2] - t
+        pos = torch.arange(t0 + 1, t0 + t + 1, device=x.device).to(x.dtype).unsqueeze(-1)
+        ctx = torch.cumsum(k_all, dim=-2)[..., t0:, :] / pos
+        y = torch.tanh(self.proj(x) + ctx) * 0.5
         if use_cache:
-            return y, (x[..., :4].clone(), x[..., :4].clone())
+            return y, (k_all, k_all)
         return y
 
 
@@ -110,3 +122,33 @@ def reference_forward_f64(model, embed):
             partial = partial + layer.ffn(layer.ffn_norm(h))
         h = route(committed + [partial], m.final_res_query, m.final_res_norm)
         return m.norm(h)
+
+
+def reference_cached_forward_f64(model, embed, past_kv=None):
+    """llama.py:718-763 in float64 on the CPU, routing through the oracle: the KV-cache
+    engine's forward (a prefill, or a decode step with ``past_kv`` from the previous
+    call); returns (hidden, new_kv_list).  ``model`` is a float64 CPU copy."""
+    x = embed.double().cpu()
+    shape = x.shape
+    d = shape[-1]
+
+    def route(srcs, q, norm):
+        qw = (q.detach() * norm.weight.detach()).numpy()
+        r = O.route(np.stack([s.reshape(-1, d).numpy() for s in srcs]), qw, norm.eps)
+        return torch.from_numpy(r["out"][0]).reshape(shape)
+
+    committed, partial, new_kv = [], x, []
+    with torch.no_grad():
+        for i, layer in enumerate(model.layers):
+            h = route(committed + [partial], layer.attn_res_query, layer.attn_res_norm)
+            if i in model._attn_res_boundary_set:
+                committed.append(partial.clone())
+                partial = torch.zeros_like(partial)
+            layer_past = past_kv[i] if past_kv is not None else None
+            attn_out, kv = layer.attn(layer.attn_norm(h), None, None, None, layer_past, use_cache=True)
+            new_kv.append(kv)
+            partial = partial + attn_out
+            h = route(committed + [partial], layer.mlp_res_query, layer.mlp_res_norm)
+            partial = partial + layer.ffn(layer.ffn_norm(h))
+        h = route(committed + [partial], model.final_res_query, model.final_res_norm)
+        return model.norm(h), new_kv

@@ -194,6 +194,65 @@ def test_block_forward_caller_order():
     np.testing.assert_allclose(r["outs"][6], fin["out"][0], rtol=1e-13)
 
 
+@pytest.mark.parametrize("boundaries", [{0, 2}, {0, 1, 3}, {0}, {0, 1, 2, 3}])
+def test_two_phase_forward_equals_one_pass_caller_loop_in_float64(boundaries):
+    # serve.py's two-phase schedule (phase 1 over the committed blocks for a whole
+    # block of queries, then one merge per sublayer) computes the same function as
+    # the training loop's one routing call per point when nothing is rounded: the
+    # merge identity, applied at every sublayer after a block's first
+    L, N, D = 4, 5, 24
+    embed = rnd(60, N, D)
+    deltas = [rnd(61 + j, N, D) for j in range(2 * L)]
+    qws = [rnd(80 + j, D, scale=0.3) for j in range(2 * L + 1)]
+    one = O.block_forward(embed, deltas, qws, 1e-5, L, boundaries)
+    two = O.two_phase_forward(embed, deltas, qws, 1e-5, L, boundaries)
+    assert sorted(two["h"]) == list(range(2 * L))
+    for j in range(2 * L):
+        np.testing.assert_allclose(two["h"][j], one["outs"][j], rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(two["final"], one["outs"][2 * L], rtol=1e-11, atol=1e-12)
+    # the merged sublayers are exactly those after each block's first
+    firsts = {2 * b for b in boundaries}
+    assert set(two["pi"]) == set(range(2 * L)) - firsts
+
+
+def test_two_phase_forward_skips_sublayers_before_the_first_boundary():
+    # boundaries {1, 3}: serve.py's ranges start at sublayer 2, so layer 0 never
+    # runs; the result is the one-pass loop over layers 1..3 with the embedding
+    # as the first committed block and the boundaries shifted to {0, 2}
+    L, N, D = 4, 3, 16
+    embed = rnd(90, N, D)
+    deltas = [rnd(91 + j, N, D) for j in range(2 * L)]
+    qws = [rnd(110 + j, D, scale=0.3) for j in range(2 * L + 1)]
+    two = O.two_phase_forward(embed, deltas, qws, 1e-5, L, {1, 3})
+    one = O.block_forward(embed, deltas[2:], qws[2:], 1e-5, L - 1, {0, 2})
+    assert sorted(two["h"]) == list(range(2, 2 * L))
+    for j in range(2, 2 * L):
+        np.testing.assert_allclose(two["h"][j], one["outs"][j - 2], rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(two["final"], one["outs"][-1], rtol=1e-11, atol=1e-12)
+
+
+def test_two_phase_forward_bf16_rounds_at_the_kernel_outputs():
+    # bf16 mode: every recorded value lies on the bf16 grid (phase-1 and merge outputs,
+    # the running blocks), the lse stays fp32, and the result is the float64 one up to
+    # the few bf16 roundings per point (<= 4 ulps of the largest value here)
+    L, N, D = 3, 6, 32
+    embed = O.bf16_round(rnd(120, N, D)).astype(np.float64)
+    deltas = [O.bf16_round(rnd(121 + j, N, D)).astype(np.float64) for j in range(2 * L)]
+    qws = [O.bf16_round(rnd(140 + j, D, scale=0.3)).astype(np.float64) for j in range(2 * L + 1)]
+    b = O.two_phase_forward(embed, deltas, qws, 1e-5, L, {0, 2}, dtype="bf16")
+    f = O.two_phase_forward(embed, deltas, qws, 1e-5, L, {0, 2}, dtype="f64")
+    for v in list(b["h"].values()) + b["blocks"] + [b["final"]]:
+        assert np.array_equal(v, O.bf16_round(v))
+    scale = max(np.abs(v).max() for v in f["h"].values())
+    for j, v in b["h"].items():
+        assert np.abs(v - f["h"][j]).max() <= 4 * 2.0 ** (math.floor(math.log2(scale)) - 7)
+    # a merged point differs from merging the unrounded phase-1 output: the rounding
+    # point is observable (a restatement that skipped it would not round here)
+    # (sublayer 5 merges into phase 1 over the embedding and block 0)
+    assert 5 in b["pi"]
+    assert not np.array_equal(b["inter"][5], O.route(np.stack(b["blocks"][:2]), qws[5], 1e-5)["out"][0])
+
+
 # ------------------------------------------------------------- backward --
 
 
