@@ -95,6 +95,10 @@ CASES = [
     (torch.bfloat16, 4, 3072, 1, 64),
     (torch.bfloat16, 8, 4096, 2, 32),
     (torch.bfloat16, 9, 8192, 1, 24),
+    # 1023 chunks: two chunks per thread on 512 threads, the last thread's second chunk
+    # past the row end (odd chunk count, ragged tail)
+    (torch.bfloat16, 3, 8184, 1, 40),
+    (torch.bfloat16, 8, 8184, 2, 12),
     (torch.bfloat16, 13, 1024, 2, 20),
     (torch.bfloat16, 16, 4096, 1, 17),
 ]
@@ -486,11 +490,18 @@ def test_capi_backward_argument_errors(gpu):
     assert rc == _capi.ERR_ARG
 
 
-def test_full_size_3b_backward_properties(gpu):
-    # the 3B prefill shape (B=8, T=4096, D=3072) at S=8, bf16
+@pytest.mark.parametrize("S", [5, 8])
+def test_full_size_3b_backward_properties(gpu, S):
+    # the 3B prefill shape (B=8, T=4096, D=3072), bf16, at two source counts that run
+    # the two-chunks-per-thread kernel (checked through the kernel-name query)
+    import ctypes
+
     w = workloads.get("cfg2")
+    kn = ctypes.create_string_buffer(128)
+    _capi.check("attnres_route_bwd_kernel_name", _capi.lib().attnres_route_bwd_kernel_name(
+        S, w.tokens, w.hidden, _capi.DTYPE_BF16, _capi.DTYPE_BF16, kn, 128))
+    assert kn.value.decode().endswith(f"_s{S}_v2")
     pool = workloads.make_pool(w, gpu, 3)
-    S = 8
     q, gn = workloads.make_params(w, gpu, 3, 1)
     eps = w.eps
     buf = pool[:S].detach().clone().requires_grad_(True)
@@ -532,8 +543,10 @@ def test_full_size_3b_backward_properties(gpu):
         g64, r64 = np64(got), ref.double().cpu().numpy()
         tol = bf16_ulp(r64) + 1e-3 * np.abs(r64).max()
         assert (np.abs(g64 - r64) <= tol).all(), f"{label}: worst err {np.abs(g64 - r64).max():.3e}"
-    # sampled rows against the float64 oracle
-    rows = torch.tensor(sorted({0, n - 1, *np.random.default_rng(3).choice(n, 96, replace=False).tolist()}),
+    # sampled rows against the float64 oracle, elementwise: the first, middle and last
+    # rows (the grid-stride loop's first and last iterations) plus 96 at random
+    fixed = {0, 1, n // 2 - 1, n // 2, n - 2, n - 1}
+    rows = torch.tensor(sorted(fixed | set(np.random.default_rng(S).choice(n, 96, replace=False).tolist())),
                         device=gpu)
     xs = np64(x[:, rows])
     ref = O.route_backward(xs, O.fold_query(np64(query), np64(norm.weight), "bf16"), eps, np64(Gf[rows]),
