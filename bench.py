@@ -11,10 +11,14 @@ Also on the JSON line:
   S=8 launch inside the timed region, against MI355X's 8 TB/s HBM peak;
   ``traffic`` is the measured HBM bytes per launch from rocprofv3 FETCH_SIZE
   + WRITE_SIZE counters when a committed summary holds them.
+* ``cfg3`` — the 8B prefill shape (S=9, D=4096, B=4, T=4096, 8 calls),
+  measured in the same run with the same steps: step time, GB/s and its own
+  ``roofline`` block for the S=9 kernel.
 * ``cpu_baseline`` — the reference's CPU routing path (oracle/torch_cpu_path:
   the einsum-branch op sequence over the padded buffer, fp32) timed on this
   host on a bounded sample (one call per distinct S at 2048 tokens),
-  extrapolated to the full step.
+  extrapolated to the full step; with the threads used, the host's logical
+  CPUs, the CPUs this process may use and the CPU model.
 
 ``--workload cfg3|cfg4|cfg5`` measures the other shapes (cfg4 = 8B decode step,
 65 fused block steps captured in one HIP graph); ``cfg2serve`` the serving
@@ -90,9 +94,24 @@ def kernel_name(s: int, tokens: int, hidden: int, dtype, queries: int = 1) -> st
     buf = ctypes.create_string_buffer(128)
     code = ops.dtype_code(dtype)
     _capi.check("attnres_route_kernel_name",
-                _capi.lib().attnres_route_kernel_name(s, tokens, hidden, code, code, code, queries, 0, buf,
+                _capi.lib().attnres_route_kernel_name(s, tokens, hidden, code, code, code, queries, 0, 1, buf,
                                                       len(buf)))
     return buf.value.decode()
+
+
+def host_cpu_info() -> dict:
+    """The host the CPU baseline ran on: logical CPUs, those this process may use, and the model."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"host_logical_cpus": os.cpu_count(), "usable_cpus": usable, "cpu_model": model}
 
 
 def cpu_baseline(w, tokens: int) -> dict:
@@ -102,6 +121,7 @@ def cpu_baseline(w, tokens: int) -> dict:
     from oracle import torch_cpu_path as TP
 
     threads = torch.get_num_threads()
+    host = host_cpu_info()
     max_s = max(w.calls)
     g = torch.Generator().manual_seed(0)
     buf = torch.randn((max_s, 1, tokens, w.hidden), generator=g).to(torch.bfloat16).float()
@@ -124,6 +144,7 @@ def cpu_baseline(w, tokens: int) -> dict:
         "value": round(gbs, 3),
         "unit": "GB/s",
         "cores": threads,
+        **host,
         "kind": "port",
         "sample": (
             f"reference CPU op sequence (llama.py:640-644, fp32, padded max_S={max_s} buffer) timed once per "
@@ -488,6 +509,28 @@ def bench_copy(steps: int, warmup: int, dev):
     return time.perf_counter() - t0, 2 * n * 2
 
 
+def secondary_cfg3(steps: int, warmup: int, dev) -> dict:
+    """The 8B prefill shape (cfg3: S=9, D=4096, B=4, T=4096, 8 calls) measured in the same run as cfg2."""
+    from kotodama_amd import workloads
+
+    w = workloads.get("cfg3")
+    elapsed, dominant, dom_ms, dom_bytes = bench_sweep(w, steps, warmup, dev)
+    ms = elapsed * 1e3 / steps
+    gbs = w.step_bytes() / (ms * 1e-3) / 1e9
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    traffic, traffic_src = load_traffic(f"cfg3_s{dominant}")
+    roof = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": kernel_name(dominant, w.tokens, w.hidden, w.dtype), "algorithmic_bytes": dom_bytes,
+            "avg_ms": round(dom_ms, 4)}
+    if traffic_src:
+        roof["traffic_source"] = traffic_src
+    return {"workload": WORKLOAD_TEXT["cfg3"], "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+            "value": round(gbs, 2), "unit": "GB/s", "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(w.tokens / (ms * 1e-3), 1), "algorithmic_bytes_per_step": w.step_bytes(),
+            "roofline": roof}
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -666,6 +709,8 @@ def main() -> int:
         "tokens_per_s": round(tokens / (ms_per_step * 1e-3), 1),
         "roofline": roofline,
     }
+    if args.workload == "cfg2":
+        line["cfg3"] = secondary_cfg3(args.steps, args.warmup, dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, min(args.cpu_tokens, w.tokens)) if args.workload != "cfg4" else \
             cpu_baseline(w, w.tokens)

@@ -65,15 +65,19 @@ const char* attnres_last_error(void);
 int attnres_set_kernel_policy(int policy);
 
 /*
- * Symbol name of the kernel attnres_route_fwd (fused == 0) or
- * attnres_block_step (fused == 1) launches for these arguments under the
- * current policy, assuming equally spaced sources (a stacked buffer or an
- * arena), for matching profiler output; written NUL-terminated into buf.
- * Loads the code object on the current device.  No counterpart in the
- * reference.
+ * Symbol name of the kernel a routing call launches for these arguments under
+ * the current policy, for matching profiler output; written NUL-terminated
+ * into buf.  fused: 0 = attnres_route_fwd (or attnres_block_step with no
+ * delta and no commit), 1 = attnres_block_step accumulating a delta into the
+ * partial, 2 = attnres_block_step with a commit.  equally_spaced: nonzero when
+ * the source pointers are equally spaced (a stacked buffer, an arena), zero
+ * for arbitrary pointers (a list of separate tensors).  The same function
+ * chooses the kernel here and at launch.  Loads the code object on the
+ * current device.  No counterpart in the reference.
  */
 int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
-                              int out_dtype, int num_queries, int fused, char* buf, int buf_len);
+                              int out_dtype, int num_queries, int fused, int equally_spaced, char* buf,
+                              int buf_len);
 
 /*
  * Load the gfx950 code object on the current HIP device.  Optional: the

@@ -72,7 +72,7 @@ _SIGNATURES = {
     "attnres_init": ([], _c_int),
     "attnres_set_kernel_policy": ([_c_int], _c_int),
     "attnres_route_kernel_name": (
-        [_c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.c_char_p, _c_int],
+        [_c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.c_char_p, _c_int],
         _c_int,
     ),
     "attnres_route_fwd": (

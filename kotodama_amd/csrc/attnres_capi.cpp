@@ -110,12 +110,16 @@ DeviceState g_dev[kMaxDevices];
 std::mutex g_mu;
 std::atomic<int> g_policy{ATTNRES_POLICY_AUTO};
 
-// Tuning knobs read once: ATTNRES_V forces chunks per thread (1 or 2) of the
-// row-per-workgroup kernels, ATTNRES_STREAM / ATTNRES_STREAM_MIN_TOKENS choose
-// when the row-per-wave streaming kernels run, ATTNRES_GRID_MULT scales the
-// resident-workgroup grid, ATTNRES_STREAM_PER_CU sets the streaming kernels'
-// workgroups per CU (0: the occupancy limit), ATTNRES_BWD_PER_CU the
-// backward's, ATTNRES_QG=0 turns off the batched-query kernel.
+// Measurement knobs, read once and only when ATTNRES_TUNING=1 is set (so a
+// stray variable cannot change kernel selection in a user's process; the
+// defaults are the measured choices): ATTNRES_V forces chunks per thread (1 or
+// 2) of the row-per-workgroup kernels, ATTNRES_STREAM /
+// ATTNRES_STREAM_MIN_TOKENS choose when the row-per-wave streaming kernels
+// run, ATTNRES_GRID_MULT scales the resident-workgroup grid,
+// ATTNRES_STREAM_PER_CU sets the streaming kernels' workgroups per CU (0: the
+// occupancy limit), ATTNRES_BWD_PER_CU the backward's (at most
+// kBwdMaxPerCu, the bound its workspace size assumes), ATTNRES_QG=0 turns off
+// the batched-query kernel, ATTNRES_MQG=0 the matrix-core batched backward.
 struct Tuning {
   int force_v = 0;
   int qg = 1;
@@ -126,8 +130,13 @@ struct Tuning {
   int bwd_per_cu = 0;          // > 0: resident workgroups per CU of the routing backward
   int mqg = 1;                 // 0: the batched-query backward never uses the matrix-core kernel
   Tuning() {
+    const char* on = std::getenv("ATTNRES_TUNING");
+    if (on == nullptr || std::strcmp(on, "1") != 0) return;
     if (const char* v = std::getenv("ATTNRES_MQG")) mqg = std::atoi(v);
-    if (const char* v = std::getenv("ATTNRES_BWD_PER_CU")) bwd_per_cu = std::atoi(v);
+    if (const char* v = std::getenv("ATTNRES_BWD_PER_CU")) {
+      bwd_per_cu = std::atoi(v);
+      if (bwd_per_cu > kBwdMaxPerCu) bwd_per_cu = kBwdMaxPerCu;
+    }
     if (const char* v = std::getenv("ATTNRES_STREAM_PER_CU")) stream_per_cu = std::atof(v);
     if (const char* v = std::getenv("ATTNRES_V")) force_v = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_QG")) qg = std::atoi(v);
@@ -156,14 +165,27 @@ int ensure_loaded(DeviceState** out) {
       const unsigned char* blobs[kParts] = {attnres_hsaco_part0, attnres_hsaco_part1, attnres_hsaco_part2,
                                             attnres_hsaco_part3, attnres_hsaco_part4, attnres_hsaco_part5,
                                             attnres_hsaco_part6, attnres_hsaco_part7};
+      // On a failure nothing stays half-loaded: the next call starts over.
+      auto unload = [&st](int n) {
+        for (int j = 0; j < n; ++j) {
+          (void)hipModuleUnload(st.mods[j]);
+          st.mods[j] = nullptr;
+        }
+      };
       for (int i = 0; i < kParts; ++i) {
         e = hipModuleLoadData(&st.mods[i], blobs[i]);
-        if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
+        if (e != hipSuccess) {
+          st.mods[i] = nullptr;
+          unload(i);
+          return hip_fail(e, "hipModuleLoadData");
+        }
       }
       e = hipDeviceGetAttribute(&st.num_cus, hipDeviceAttributeMultiprocessorCount, dev);
-      if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
-      e = hipDeviceGetAttribute(&st.max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
-      if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MaxSharedMemoryPerBlock)");
+      if (e == hipSuccess) e = hipDeviceGetAttribute(&st.max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+      if (e != hipSuccess) {
+        unload(kParts);
+        return hip_fail(e, "hipDeviceGetAttribute");
+      }
       st.loaded.store(true, std::memory_order_release);
     }
   }
@@ -429,6 +451,13 @@ int get_reduce(DeviceState& st, hipFunction_t* stage, hipFunction_t* fin) {
 }
 
 inline int round64(int64_t t) { return (int)(((t + 63) / 64) * 64); }
+inline int round16(int64_t t) { return (int)(((t + 15) / 16) * 16); }
+
+// Dynamic LDS of the batched-query matrix-core backward: the folded queries in
+// query slots of four, chunks in blocks of 16 ([chunk/16][slot][chunk%16]).
+inline size_t mqg_lds_bytes(int num_queries, int nchunk) {
+  return (size_t)((num_queries + 3) / 4 * 4) * (size_t)round16(nchunk) * 16;
+}
 
 // Chunks per thread V and the workgroup size for a row of `nchunk` 16-byte
 // chunks.  Returns 0 when no variant fits in kMaxThreads.
@@ -496,6 +525,7 @@ struct RouteChoice {
   bool stream = false;
   int combo = 0;
   int nch = 0;    // streaming: KiB per row
+  int variant = kStreamPlain;  // streaming: plain / pointer table / fused
   int v = 0;      // workgroup: chunks per thread (0: no shape fits)
   int block = 0;  // threads per workgroup
   size_t qg_lds = 0;  // > 0: the batched-query kernel, with this much dynamic LDS
@@ -535,12 +565,33 @@ RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int sr
   return ch;
 }
 
-void kernel_name_of(const RouteChoice& ch, int num_sources, int num_queries, bool fused, bool out_bf, char* buf,
-                    size_t n) {
+// The whole kernel choice of one routing call (family, streaming variant,
+// chunks per thread, batched-query kernel), shared by the launch and the
+// kernel-name query.  The streaming kernel addresses equally spaced sources
+// as base + s*stride and any others through the kernel-argument pointer table;
+// it shares one delta buffer between its two pipeline slots, which needs
+// S >= 2 when accumulating into the partial (S = 1 accumulate calls run the
+// workgroup kernel).
+RouteChoice plan_route(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
+                       int out_dtype, int num_queries, int mode, bool equally_spaced, const DeviceState& st) {
+  const bool stream_ok = !(mode == ATTNRES_MODE_ACCUM && num_sources < 2);
+  RouteChoice ch =
+      choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st.num_cus, stream_ok);
+  if (ch.stream) {
+    ch.variant = mode != ATTNRES_MODE_PLAIN ? kStreamFused
+                 : (equally_spaced || num_sources < 2) ? kStreamPlain
+                                                       : kStreamTable;
+  } else if (ch.v != 0) {
+    choose_qg(ch, num_sources, num_queries, hidden, out_dtype, mode, st.max_lds);
+  }
+  return ch;
+}
+
+void kernel_name_of(const RouteChoice& ch, int num_sources, int num_queries, bool out_bf, char* buf, size_t n) {
   static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
   if (ch.stream) {
     snprintf(buf, n, "attnres_stream_%s_o%s_c%d_%s", combo_names[ch.combo], out_bf ? "bf" : "f32", ch.nch,
-             fused ? "fused" : "plain");
+             kStreamVariantNames[ch.variant]);
   } else {
     snprintf(buf, n, "attnres_route_%s_s%d_v%d_%s", combo_names[ch.combo], num_sources, ch.v,
              ch.qg_lds > 0 ? "qg" : num_queries > 1 ? "qn" : "q1");
@@ -609,25 +660,16 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
     for (int s = 2; s < num_sources && equally_spaced; ++s)
       equally_spaced = (int64_t)((uintptr_t)sources[s] - (uintptr_t)sources[0]) == src_stride * s;
   }
-  // The streaming kernel addresses equally spaced sources as base + s*stride
-  // and any others through the kernel-argument pointer table (stride 0); it
-  // shares one delta buffer between its two pipeline slots, which needs
-  // S >= 2 when accumulating into the partial.
-  const bool stream_ok = !(mode == ATTNRES_MODE_ACCUM && num_sources < 2);
-  RouteChoice ch =
-      choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus, stream_ok);
+  const RouteChoice ch = plan_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, out_dtype, num_queries,
+                                    mode, equally_spaced, *st);
   if (!ch.stream && ch.v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
-  choose_qg(ch, num_sources, num_queries, hidden, out_dtype, mode, st->max_lds);
 
   hipFunction_t f = nullptr;
   int bpc = 1;
   int block = ch.block;
   int64_t work_units = num_tokens;  // rows per workgroup-slot of the grid
   if (ch.stream) {
-    const int variant = mode != ATTNRES_MODE_PLAIN ? kStreamFused
-                        : (equally_spaced || num_sources < 2) ? kStreamPlain
-                                                              : kStreamTable;
-    rc = get_stream(*st, ch.combo, out_dtype == ATTNRES_DTYPE_BF16, ch.nch, variant, &f, &bpc);
+    rc = get_stream(*st, ch.combo, out_dtype == ATTNRES_DTYPE_BF16, ch.nch, ch.variant, &f, &bpc);
     if (rc != ATTNRES_OK) return rc;
     work_units = (num_tokens + kStreamWaves - 1) / kStreamWaves;
   } else if (ch.qg_lds > 0) {
@@ -725,20 +767,22 @@ int attnres_max_sources(void) { return ATTNRES_MAX_SOURCES; }
 const char* attnres_last_error(void) { return g_err.c_str(); }
 
 int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
-                              int out_dtype, int num_queries, int fused, char* buf, int buf_len) {
+                              int out_dtype, int num_queries, int fused, int equally_spaced, char* buf,
+                              int buf_len) {
   if (buf == nullptr || buf_len < 1) return fail(ATTNRES_ERR_ARG, "no output buffer");
   if (!valid_dtype(src_dtype) || !valid_dtype(param_dtype) || !valid_dtype(out_dtype))
     return fail(ATTNRES_ERR_ARG, "unknown dtype code");
   if (num_sources < 0 || num_sources > ATTNRES_MAX_SOURCES || hidden <= 0 || num_queries < 1)
     return fail(ATTNRES_ERR_ARG, "bad shape");
+  if (fused < 0 || fused > 2) return fail(ATTNRES_ERR_ARG, "fused=%d is not 0, 1 or 2", fused);
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
-  RouteChoice ch =
-      choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st->num_cus, true);
-  choose_qg(ch, num_sources, num_queries, hidden, out_dtype, fused ? ATTNRES_MODE_SET : ATTNRES_MODE_PLAIN,
-            st->max_lds);
-  kernel_name_of(ch, num_sources, num_queries, fused != 0, out_dtype == ATTNRES_DTYPE_BF16, buf, (size_t)buf_len);
+  const int mode = fused == 0 ? ATTNRES_MODE_PLAIN : fused == 1 ? ATTNRES_MODE_ACCUM : ATTNRES_MODE_SET;
+  const RouteChoice ch = plan_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, out_dtype, num_queries,
+                                    mode, equally_spaced != 0, *st);
+  if (!ch.stream && ch.v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
+  kernel_name_of(ch, num_sources, num_queries, out_dtype == ATTNRES_DTYPE_BF16, buf, (size_t)buf_len);
   return ATTNRES_OK;
 }
 
@@ -776,7 +820,7 @@ int attnres_route_bwd_queries_kernel_name(int num_sources, int hidden, int src_d
   const int nchunk = hidden / vec;
   const int v = round64(nchunk) <= kMaxThreads ? 1 : 2;
   const bool gbf = grad_out_dtype == ATTNRES_DTYPE_BF16;
-  const size_t lds = (size_t)((num_queries + 3) / 4 * 4) * (size_t)nchunk * 16;
+  const size_t lds = mqg_lds_bytes(num_queries, nchunk);
   if (bwd_mqg_shape(bf, gbf, param_dtype == ATTNRES_DTYPE_BF16, num_sources, num_queries, nchunk) &&
       lds + kMqgStaticLds <= (size_t)st->max_lds) {
     snprintf(buf, (size_t)buf_len, "attnres_route_bwd_mqg_s%d_q%d", num_sources, (num_queries + 3) / 4);
@@ -959,8 +1003,8 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   hipFunction_t f = nullptr;
   int bpc = 1;
   // dynamic LDS (S >= 5): each thread's qw chunks and, with one chunk per
-  // thread, its query-gradient sums (fp32)
-  const size_t lds = num_sources >= 5 ? (size_t)(v == 1 ? 2 : 1) * nchunk * vec * sizeof(float) : 0;
+  // thread, its query-gradient sums (fp32), in blocks of 16 chunks
+  const size_t lds = num_sources >= 5 ? (size_t)(v == 1 ? 2 : 1) * round16(nchunk) * vec * sizeof(float) : 0;
   if (lds + kBwdStaticLds > (size_t)st->max_lds)
     return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d needs %zu bytes of LDS per workgroup (device limit %d)", hidden,
                 lds + kBwdStaticLds, st->max_lds);
@@ -1060,7 +1104,7 @@ int attnres_route_bwd_queries(const void* const* sources, int num_sources, int64
     return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d exceeds the largest supported row (%d elements)", hidden,
                 2 * kMaxThreads * vec);
   const int v = round64(nchunk) <= kMaxThreads ? 1 : 2;
-  const size_t mqg_lds = (size_t)((num_queries + 3) / 4 * 4) * (size_t)nchunk * 16;  // query slots of 4
+  const size_t mqg_lds = mqg_lds_bytes(num_queries, nchunk);
   const bool mqg_shape = bwd_mqg_shape(bf, grad_out_dtype == ATTNRES_DTYPE_BF16,
                                        param_dtype == ATTNRES_DTYPE_BF16, num_sources, num_queries, nchunk);
   if (!mqg_shape && !bwd_mq_available(bf, num_sources, v))

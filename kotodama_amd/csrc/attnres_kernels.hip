@@ -1473,11 +1473,17 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
   // Where registers are tight (S >= 5) each thread's chunks of qw and, for
   // V == 1, of its running query-gradient sum live in (dynamic) LDS instead,
   // nchunk * VEC floats each; the LDS is thread-private, so no barrier.
+  // Layout [chunk / 16][h][chunk % 16] (float4 h of a chunk's VEC floats):
+  // sixteen consecutive lanes touch 256 contiguous bytes per access, so the
+  // 128-bit LDS accesses are free of bank conflicts, and h is an immediate
+  // offset.  Each array holds round16(nchunk) * VEC / 4 float4s.
   constexpr bool QW_LDS = S >= 5;
   constexpr bool DQW_LDS = QW_LDS && V == 1;
+  constexpr int NPL = VEC / 4;
   extern __shared__ float4 bwd_lds[];
   float4* s_qw = bwd_lds;
-  float4* s_dqw = bwd_lds + P.nchunk * (VEC / 4);
+  float4* s_dqw = bwd_lds + ((P.nchunk + 15) & ~15) * NPL;
+  auto lds_at = [](int c, int h) { return (c & ~15) * NPL + h * 16 + (c & 15); };
   float qw_reg[QW_LDS ? 1 : V][VEC];
   float dqw_reg[DQW_LDS ? 1 : V][VEC];
 #pragma unroll
@@ -1508,8 +1514,8 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
     if constexpr (QW_LDS) {
 #pragma unroll
       for (int h = 0; h < VEC / 4; ++h) {
-        s_qw[chunk[k] * (VEC / 4) + h] = make_float4(q[4 * h], q[4 * h + 1], q[4 * h + 2], q[4 * h + 3]);
-        if constexpr (DQW_LDS) s_dqw[chunk[k] * (VEC / 4) + h] = make_float4(0.f, 0.f, 0.f, 0.f);
+        s_qw[lds_at(chunk[k], h)] = make_float4(q[4 * h], q[4 * h + 1], q[4 * h + 2], q[4 * h + 3]);
+        if constexpr (DQW_LDS) s_dqw[lds_at(chunk[k], h)] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     } else {
 #pragma unroll
@@ -1520,7 +1526,7 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
     if constexpr (QW_LDS) {
 #pragma unroll
       for (int h = 0; h < VEC / 4; ++h) {
-        const float4 t = s_qw[chunk[k] * (VEC / 4) + h];
+        const float4 t = s_qw[lds_at(chunk[k], h)];
         q[4 * h] = t.x;
         q[4 * h + 1] = t.y;
         q[4 * h + 2] = t.z;
@@ -1657,12 +1663,12 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
       if constexpr (DQW_LDS) {
 #pragma unroll
         for (int h = 0; h < VEC / 4; ++h) {
-          float4 t = s_dqw[chunk[k] * (VEC / 4) + h];
+          float4 t = s_dqw[lds_at(chunk[k], h)];
           t.x += acc[4 * h];
           t.y += acc[4 * h + 1];
           t.z += acc[4 * h + 2];
           t.w += acc[4 * h + 3];
-          s_dqw[chunk[k] * (VEC / 4) + h] = t;
+          s_dqw[lds_at(chunk[k], h)] = t;
         }
       } else {
 #pragma unroll
@@ -1680,7 +1686,7 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
 #pragma unroll
     for (int h = 0; h < VEC / 4; ++h) {
       if constexpr (DQW_LDS) {
-        prow[chunk[k] * (VEC / 4) + h] = s_dqw[chunk[k] * (VEC / 4) + h];
+        prow[chunk[k] * (VEC / 4) + h] = s_dqw[lds_at(chunk[k], h)];
       } else {
         const float* a = dqw_reg[DQW_LDS ? 0 : k];
         prow[chunk[k] * (VEC / 4) + h] = make_float4(a[4 * h], a[4 * h + 1], a[4 * h + 2], a[4 * h + 3]);
@@ -1961,7 +1967,10 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
   constexpr int NPA = 4 * HA, NPB = 4 * HB;
   static_assert(S >= 1 && S <= SEG, "one softmax lane per (query, source)");
   __shared__ float red[2][ATTNRES_KMAX_WAVES][NPA + NPB];
-  extern __shared__ u32x4 qg_lds[];  // [chunk][query slot] packed folded queries, zero past the batch
+  // packed folded queries, zero past the batch, laid out [chunk / 16][query slot][chunk % 16]:
+  // sixteen consecutive lanes read 256 contiguous bytes (no LDS bank conflicts)
+  // and a thread's queries sit at immediate offsets of 256 bytes from one address
+  extern __shared__ u32x4 qg_lds[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1971,18 +1980,19 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
   const int nq = P.num_queries;
   const int nchunk = P.nchunk;
 
+  auto qslot = [](int c) { return (c & ~15) * NQ + (c & 15); };  // query q at + 16 * q
   int chunk[V];
-  const u32x4* qrow[V];  // this thread's chunks of the staged queries: qrow[k][q], q < NQ
+  const u32x4* qrow[V];  // this thread's chunks of the staged queries: qrow[k][16 * q], q < NQ
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     chunk[k] = tid + k * block;
-    qrow[k] = qg_lds + (chunk[k] < nchunk ? chunk[k] : nchunk - 1) * NQ;  // rows past the end hold zeros
+    qrow[k] = qg_lds + qslot(chunk[k] < nchunk ? chunk[k] : nchunk - 1);  // chunks past the end read zeros
   }
 
-  // ---- the folded queries into LDS, once per workgroup; chunk-major, so a
-  // thread's queries sit at constant offsets from one address ----
+  // ---- the folded queries into LDS, once per workgroup (consecutive threads
+  // read consecutive chunks of one query) ----
   for (int i = tid; i < NQ * nchunk; i += block) {
-    const int c = i / NQ, q = i % NQ;
+    const int q = i / nchunk, c = i % nchunk;
     float t[VEC];
     if (q < nq) {
       load_qw_ptr<VEC>(P.query, P.gain, true, q, P.d, c, t);
@@ -1990,7 +2000,8 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
 #pragma unroll
       for (int e = 0; e < VEC; ++e) t[e] = 0.f;
     }
-    qg_lds[i] = u32x4{pack_bf16(t[0], t[1]), pack_bf16(t[2], t[3]), pack_bf16(t[4], t[5]), pack_bf16(t[6], t[7])};
+    qg_lds[qslot(c) + 16 * q] =
+        u32x4{pack_bf16(t[0], t[1]), pack_bf16(t[2], t[3]), pack_bf16(t[4], t[5]), pack_bf16(t[6], t[7])};
   }
 
   // Rows through buffer resources: a chunk past the row end reads 0 and its
@@ -2052,7 +2063,7 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
         for (int k = 0; k < V; ++k) {
           u32x4 qv[4];
 #pragma unroll
-          for (int g = 0; g < 4; ++g) qv[g] = qrow[k][q0 + g];
+          for (int g = 0; g < 4; ++g) qv[g] = qrow[k][16 * (q0 + g)];
 #pragma unroll
           for (int s = 0; s < S; ++s) {
 #pragma unroll
@@ -2153,7 +2164,7 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
         for (int g4 = 0; g4 < NQ4; ++g4) {
           u32x4 qv[4];
 #pragma unroll
-          for (int g = 0; g < 4; ++g) qv[g] = qrow[k][4 * g4 + g];
+          for (int g = 0; g < 4; ++g) qv[g] = qrow[k][16 * (4 * g4 + g)];
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             // B operands of elements 2w (low halves) and 2w+1 (high halves), four queries along k

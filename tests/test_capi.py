@@ -176,6 +176,6 @@ def test_merge_bwd_argument_errors():
 def test_kernel_name_argument_errors():
     lib = _capi.lib()
     buf = ctypes.create_string_buffer(8)
-    assert lib.attnres_route_kernel_name(3, 16, 64, 1, 1, 1, 1, 0, None, 0) == _capi.ERR_ARG
-    assert lib.attnres_route_kernel_name(3, 16, 64, 1, 1, 9, 1, 0, buf, 8) == _capi.ERR_ARG  # out dtype
-    assert lib.attnres_route_kernel_name(17, 16, 64, 1, 1, 1, 1, 0, buf, 8) == _capi.ERR_ARG
+    assert lib.attnres_route_kernel_name(3, 16, 64, 1, 1, 1, 1, 0, 1, None, 0) == _capi.ERR_ARG
+    assert lib.attnres_route_kernel_name(3, 16, 64, 1, 1, 9, 1, 0, 1, buf, 8) == _capi.ERR_ARG  # out dtype
+    assert lib.attnres_route_kernel_name(17, 16, 64, 1, 1, 1, 1, 0, 1, buf, 8) == _capi.ERR_ARG

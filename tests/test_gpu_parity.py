@@ -201,8 +201,31 @@ def route_kernel(s, n, d, q):
     import ctypes
 
     buf = ctypes.create_string_buffer(128)
-    _capi.check("attnres_route_kernel_name", _capi.lib().attnres_route_kernel_name(s, n, d, 1, 1, 1, q, 0, buf, 128))
+    _capi.check("attnres_route_kernel_name", _capi.lib().attnres_route_kernel_name(s, n, d, 1, 1, 1, q, 0, 1, buf, 128))
     return buf.value.decode()
+
+
+def test_kernel_name_query_follows_the_launch_choice(gpu):
+    # the name query and the launch share one choice: streaming variants by mode and
+    # source spacing, and the workgroup kernel for a one-source accumulate
+    import ctypes
+
+    def name(s, n, d, fused, spaced):
+        buf = ctypes.create_string_buffer(128)
+        _capi.check("attnres_route_kernel_name",
+                    _capi.lib().attnres_route_kernel_name(s, n, d, 1, 1, 1, 1, fused, spaced, buf, 128))
+        return buf.value.decode()
+
+    assert name(4, 32768, 3072, 0, 1) == "attnres_stream_bf_d2_obf_c6_plain"
+    assert name(4, 32768, 3072, 0, 0) == "attnres_stream_bf_d2_obf_c6_table"
+    assert name(4, 32768, 3072, 1, 1) == "attnres_stream_bf_d2_obf_c6_fused"
+    assert name(2, 32768, 3072, 2, 1) == "attnres_stream_bf_d2_obf_c6_fused"
+    one = name(1, 32768, 3072, 1, 1)  # S = 1 accumulate: the workgroup kernel
+    assert one.startswith("attnres_route_bf_d2_s1_v") and one.endswith("_q1"), one
+    assert name(1, 32768, 3072, 0, 1) == "attnres_stream_bf_d2_obf_c6_plain"
+    assert name(9, 256, 4096, 1, 1) == "attnres_route_bf_d2_s9_v1_q1"  # decode rows
+    buf = ctypes.create_string_buffer(128)
+    assert _capi.lib().attnres_route_kernel_name(2, 64, 512, 1, 1, 1, 1, 3, 1, buf, 128) == _capi.ERR_ARG
 
 
 @pytest.mark.parametrize("d,n,queries", [(1024, 24, (2, 9)), (8192, 12, (3, 8)), (3072, 600, (5,)), (520, 7, (4,)),

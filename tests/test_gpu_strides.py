@@ -48,10 +48,11 @@ def code(dtype):
     return _capi.DTYPE_BF16 if dtype == torch.bfloat16 else _capi.DTYPE_F32
 
 
-def kernel_name(s, n, d, src, par, out, q):
+def kernel_name(s, n, d, src, par, out, q, equally_spaced=True):
     buf = ctypes.create_string_buffer(128)
     _capi.check("attnres_route_kernel_name",
-                _capi.lib().attnres_route_kernel_name(s, n, d, code(src), code(par), code(out), q, 0, buf, 128))
+                _capi.lib().attnres_route_kernel_name(s, n, d, code(src), code(par), code(out), q, 0,
+                                                      int(equally_spaced), buf, 128))
     return buf.value.decode()
 
 
@@ -60,7 +61,7 @@ FWD_CASES = [
     ("workgroup-bf16", 5, 96, 3072, torch.bfloat16, torch.bfloat16, 1, False, "_q1"),
     ("workgroup-f32", 3, 40, 1024, torch.float32, torch.float32, 1, False, "_q1"),
     ("stream-plain", 4, 4096, 2048, torch.bfloat16, torch.bfloat16, 1, False, "_plain"),
-    ("stream-table", 4, 4096, 2048, torch.bfloat16, torch.bfloat16, 1, True, "_plain"),
+    ("stream-table", 4, 4096, 2048, torch.bfloat16, torch.bfloat16, 1, True, "_table"),
     ("batched-bf16", 6, 64, 1024, torch.bfloat16, torch.bfloat16, 5, False, "_qg"),
     ("per-query-f32q", 3, 64, 1024, torch.bfloat16, torch.float32, 3, False, "_qn"),
 ]
@@ -68,9 +69,8 @@ FWD_CASES = [
 
 @pytest.mark.parametrize("label,S,n,d,sdt,qdt,Q,separate,suffix", FWD_CASES, ids=[c[0] for c in FWD_CASES])
 def test_route_fwd_row_strides(gpu, label, S, n, d, sdt, qdt, Q, separate, suffix):
-    # the kernel-name query reports the plain variant for the pointer table's shape too:
-    # the table is chosen at launch from the source addresses
-    assert kernel_name(S, n, d, sdt, qdt, sdt, Q).endswith(suffix)
+    # the kernel-name query takes the spacing of the source pointers, as the launch does
+    assert kernel_name(S, n, d, sdt, qdt, sdt, Q, equally_spaced=not separate).endswith(suffix)
     g = torch.Generator(device=gpu).manual_seed(n + d + Q)
     src_ld, out_ld = d + 64, d + 32
     es = 2 if sdt == torch.bfloat16 else 4
