@@ -84,6 +84,13 @@ class TinyModel(nn.Module):
         self.final_res_norm = TinyNorm(d, eps)
         self.norm = TinyNorm(d, eps)
         self._attn_res_boundary_set = frozenset(boundaries)
+        # the schedule the reference precomputes at init (llama.py:545-571)
+        from kotodama_amd import AttnResSchedule
+
+        sched = AttnResSchedule.build(num_layers, boundaries=sorted(boundaries))
+        self._attn_res_max_sources = sched.max_sources
+        self._attn_res_active_counts = list(sched.active_counts)
+        self.register_buffer("_attn_res_masks", sched.masks(), persistent=False)
         self.register_buffer("rope_cos", torch.zeros(1))
         self.register_buffer("rope_sin", torch.zeros(1))
         with torch.no_grad():
@@ -152,3 +159,30 @@ def reference_cached_forward_f64(model, embed, past_kv=None):
             partial = partial + layer.ffn(layer.ffn_norm(h))
         h = route(committed + [partial], model.final_res_query, model.final_res_norm)
         return model.norm(h), new_kv
+
+
+def training_forward(model, embed, route_fn):
+    """The training loop of llama.py:666-716 (pad + stack before every routing call,
+    out-of-place partial updates, the schedule's masks and counts precomputed at init),
+    with the routing function swapped in: ``route_fn(buf, query, norm, mask, num_active)``."""
+    masks = model._attn_res_masks
+    counts = model._attn_res_active_counts
+    max_s = model._attn_res_max_sources
+    committed, partial = [], embed
+    zero = torch.zeros_like(embed)
+
+    def pad_and_stack():
+        sources = committed + [partial]
+        sources += [zero] * (max_s - len(sources))
+        return torch.stack(sources, dim=0)
+
+    for i, layer in enumerate(model.layers):
+        h = route_fn(pad_and_stack(), layer.attn_res_query, layer.attn_res_norm, masks[2 * i], counts[2 * i])
+        if i in model._attn_res_boundary_set:
+            committed.append(partial.clone())
+            partial = zero.clone()
+        partial = partial + layer.attn(layer.attn_norm(h), None, None)
+        h = route_fn(pad_and_stack(), layer.mlp_res_query, layer.mlp_res_norm, masks[2 * i + 1], counts[2 * i + 1])
+        partial = partial + layer.ffn(layer.ffn_norm(h))
+    x = route_fn(pad_and_stack(), model.final_res_query, model.final_res_norm, masks[-1], counts[-1])
+    return model.norm(x)

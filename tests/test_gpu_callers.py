@@ -12,7 +12,7 @@ import torch
 from kotodama_amd import forward_attn_res, forward_attn_res_cached
 from oracle import attnres_oracle as O
 
-from ._tiny_model import TinyModel, reference_forward_f64
+from ._tiny_model import TinyModel, reference_forward_f64, training_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -133,34 +133,6 @@ def test_serve_fast_path_matches_two_phase_oracle(gpu, L, boundaries):
     assert exact >= 0.98 * total
 
 
-def _training_forward(model, embed, route_fn):
-    """The training loop of llama.py:666-716 (pad + stack before every routing call,
-    out-of-place partial updates), with the routing function swapped in."""
-    from kotodama_amd import AttnResSchedule
-
-    sched = AttnResSchedule.build(model.config.num_layers, boundaries=sorted(model._attn_res_boundary_set))
-    masks = sched.masks(embed.device)
-    counts = sched.active_counts
-    committed, partial = [], embed
-    zero = torch.zeros_like(embed)
-
-    def pad_and_stack():
-        sources = committed + [partial]
-        sources += [zero] * (sched.max_sources - len(sources))
-        return torch.stack(sources, dim=0)
-
-    for i, layer in enumerate(model.layers):
-        h = route_fn(pad_and_stack(), layer.attn_res_query, layer.attn_res_norm, masks[2 * i], counts[2 * i])
-        if i in model._attn_res_boundary_set:
-            committed.append(partial.clone())
-            partial = zero.clone()
-        partial = partial + layer.attn(layer.attn_norm(h), None, None)
-        h = route_fn(pad_and_stack(), layer.mlp_res_query, layer.mlp_res_norm, masks[2 * i + 1], counts[2 * i + 1])
-        partial = partial + layer.ffn(layer.ffn_norm(h))
-    x = route_fn(pad_and_stack(), model.final_res_query, model.final_res_norm, masks[-1], counts[-1])
-    return model.norm(x)
-
-
 def test_training_step_gradients_match_float64_reference(gpu):
     # the reference's training forward with _route_static swapped for the HIP op:
     # loss and every parameter gradient (routing queries and gains, sublayer
@@ -175,13 +147,13 @@ def test_training_step_gradients_match_float64_reference(gpu):
     embed = torch.randn((2, 16, 512), generator=g)
     G = torch.randn((2, 16, 512), generator=g)
 
-    out_ref = _training_forward(ref_model, embed.double(),
+    out_ref = training_forward(ref_model, embed.double(),
                                 lambda buf, q, norm, mask, n: route_static_cpu(buf, q * norm.weight, norm.eps, mask))
     loss_ref = (out_ref * G.double()).sum()
     loss_ref.backward()
 
     m = model.to(gpu)
-    out = _training_forward(m, embed.to(gpu), route_static)
+    out = training_forward(m, embed.to(gpu), route_static)
     loss = (out * G.to(gpu)).sum()
     loss.backward()
     torch.cuda.synchronize()
@@ -207,7 +179,7 @@ def test_stack_free_forward_trains_like_the_reference_loop(gpu):
     g = torch.Generator().manual_seed(24)
     embed = torch.randn((2, 16, 512), generator=g)
     G = torch.randn((2, 16, 512), generator=g)
-    out_ref = _training_forward(ref_model, embed.double(),
+    out_ref = training_forward(ref_model, embed.double(),
                                 lambda buf, q, norm, mask, n: route_static_cpu(buf, q * norm.weight, norm.eps, mask))
     (out_ref * G.double()).sum().backward()
     m = model.to(gpu)
