@@ -1238,6 +1238,56 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   float m = -__builtin_inff(), l = 0.f;
   float my_logit = 0.f, my_inv = 0.f;  // lane s: logit and inv_rms of source s
 
+  // ---- output rows ----
+  // Store addresses: a wave-uniform row base (SGPRs) plus a 32-bit lane offset.
+  constexpr int OES = OUTBF ? 2 : 4;                       // output element bytes
+  constexpr int OPC = OUTBF ? 1 : VEC / 4;                 // pieces per lane and chunk
+  constexpr int OPB = (OUTBF && VEC == 4) ? 8 : 16;        // bytes per piece
+  auto out_rsrc = [&](uint32_t tt) {
+    char* orow = const_cast<char*>(
+        uniform_ptr(reinterpret_cast<uint64_t>(P.out) + (uint64_t)tt * (uint64_t)(P.out_ld * OES)));
+    return row_rsrc(orow, (uint32_t)(P.d * OES));
+  };
+  // Byte offset of this lane's first output element, made opaque so the
+  // per-chunk offsets are recomputed where used (mostly as immediate offsets)
+  // rather than hoisted out of the loop and kept live in registers.
+  auto lane_out_offset = [&]() {
+    uint32_t lane_ob = (uint32_t)lane * (uint32_t)(VEC * OES);
+    asm volatile("" : "+v"(lane_ob));
+    return lane_ob;
+  };
+  // Finished rows can be staged in dynamic LDS and stored in batches of
+  // P.out_batch rows per wave: the output stores then reach memory in bursts
+  // between long stretches of pure reads, which this HBM serves far better
+  // than one row interleaved after every S source rows (a store-only
+  // variant of the access pattern: 78.5% -> 90.9% of peak at S = 8, batches
+  // of 8).  The staged layout is [row][chunk][piece][lane] (consecutive lanes
+  // 8 or 16 bytes apart: no bank conflicts); a wave reads back only what its
+  // own lanes wrote, so no barrier is needed.
+  const uint32_t batch = (uint32_t)P.out_batch;
+  extern __shared__ u32x4 stream_stage[];
+  constexpr uint32_t STAGE_ROW = NCH * OPC * 64 * OPB;     // bytes of one staged row
+  auto stage_row = [&](uint32_t b) {
+    return reinterpret_cast<char*>(stream_stage) + ((uint32_t)wave * batch + b) * STAGE_ROW;
+  };
+  uint32_t nheld = 0, t_first = 0;
+  auto flush_staged = [&]() {
+    for (uint32_t b = 0; b < nheld; ++b) {
+      const __amdgpu_buffer_rsrc_t orsrc = out_rsrc(t_first + b * nw);
+      const uint32_t lane_ob = lane_out_offset();
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+        for (int h = 0; h < OPC; ++h) {
+          const char* sp = stage_row(b) + ((c * OPC + h) * 64 + lane) * OPB;
+          const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * OES + 16 * h);
+          if constexpr (OPB == 16) st_row(orsrc, off, *reinterpret_cast<const u32x4*>(sp));
+          else st_row(orsrc, off, *reinterpret_cast<const u32x2*>(sp));
+        }
+      }
+    }
+  };
+
   auto process = [&](u32x4(&x)[NCH], u32x4(&dbuf)[FUSED ? NCH : 1], uint32_t t, uint32_t s, auto slot) {
     // A distinct marker per pipeline slot keeps the compiler from merging the
     // two unrolled halves into one body (which would copy the row buffers
@@ -1343,37 +1393,53 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
 
     if (s == (uint32_t)(S - 1)) {
       // ---- finalize the token row ----
-      // Store addresses: a wave-uniform row base (SGPRs) plus a 32-bit lane offset.
       const float rl = 1.0f / l;
-      constexpr int oes = OUTBF ? 2 : 4;
-      char* orow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.out) + (uint64_t)t * (uint64_t)(P.out_ld * oes)));
-      const __amdgpu_buffer_rsrc_t orsrc = row_rsrc(orow, (uint32_t)(P.d * oes));
-      // Byte offset of this lane's first output element, made opaque so the
-      // per-chunk offsets are recomputed here (mostly as immediate offsets)
-      // rather than hoisted out of the loop and kept live in registers.
-      uint32_t lane_ob = (uint32_t)lane * (uint32_t)(VEC * oes);
-      asm volatile("" : "+v"(lane_ob));
-      {
+      // The lane's part of the output row: OPC pieces of OPB bytes per chunk.
+      u32x4 pk[NCH][OPC];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        float o[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = acc[c][e] * rl;
+        if constexpr (OUTBF) {
+          if constexpr (VEC == 8) {
+            pk[c][0] = u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])};
+          } else {
+            pk[c][0] = u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), 0u, 0u};
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < OPC; ++h)
+            pk[c][h] = u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]), as_u32(o[4 * h + 2]), as_u32(o[4 * h + 3])};
+        }
+      }
+      if (batch > 1) {
+        // stage the row; the wave's batch is stored when full (or at the end)
+        if (nheld == 0) t_first = t;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
-          float o[VEC];
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) o[e] = acc[c][e] * rl;
-          if constexpr (OUTBF) {
-            const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * 2);
-            if constexpr (VEC == 8) {
-              st_row(orsrc, off, u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]),
-                                       pack_bf16(o[6], o[7])});
-            } else {
-              st_row(orsrc, off, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
-            }
-          } else {
-            const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * 4);
+          for (int h = 0; h < OPC; ++h) {
+            char* sp = stage_row(nheld) + ((c * OPC + h) * 64 + lane) * OPB;
+            if constexpr (OPB == 16) *reinterpret_cast<u32x4*>(sp) = pk[c][h];
+            else *reinterpret_cast<u32x2*>(sp) = u32x2{pk[c][h][0], pk[c][h][1]};
+          }
+        }
+        nheld = __builtin_amdgcn_readfirstlane(nheld + 1);
+        if (nheld == batch) {
+          flush_staged();
+          nheld = 0;
+        }
+      } else {
+        const __amdgpu_buffer_rsrc_t orsrc = out_rsrc(t);
+        const uint32_t lane_ob = lane_out_offset();
 #pragma unroll
-            for (int h = 0; h < VEC / 4; ++h) {
-              st_row(orsrc, off + 16 * h,
-                     u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]), as_u32(o[4 * h + 2]), as_u32(o[4 * h + 3])});
-            }
+        for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+          for (int h = 0; h < OPC; ++h) {
+            const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * OES + 16 * h);
+            if constexpr (OPB == 16) st_row(orsrc, off, pk[c][h]);
+            else st_row(orsrc, off, u32x2{pk[c][h][0], pk[c][h][1]});
           }
         }
       }
@@ -1428,6 +1494,7 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
     tok = __builtin_amdgcn_readfirstlane(t2);
     s = __builtin_amdgcn_readfirstlane(s2);
   }
+  if (nheld > 0) flush_staged();
 }
 
 

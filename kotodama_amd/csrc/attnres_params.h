@@ -58,6 +58,8 @@ typedef struct attnres_route_params {
   int32_t num_sources;  /* S (the streaming kernels read it; the others are specialised on it) */
   int32_t block;        /* threads per workgroup (read as a kernel argument, not from the
                            dispatch packet, so it costs no vector load) */
+  int32_t out_batch;    /* streaming kernels: finished output rows each wave stages in
+                           (dynamic) LDS and stores together; 1 = store each row at once */
   float eps;
   float inv_d;
 } attnres_route_params;
