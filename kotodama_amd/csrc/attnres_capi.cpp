@@ -135,12 +135,17 @@ struct Tuning {
   int mqg = 1;                 // 0: the batched-query backward never uses the matrix-core kernel
   int out_batch = 0;           // > 0: at most this many staged output rows per streaming wave (1: none)
   int out_batch_min_s = 4;     // sources from which the streaming kernels stage output rows
+  int stream_waves = 0;        // > 0: waves per workgroup of the streaming kernels (1..4); 0: by S
   Tuning() {
     const char* on = std::getenv("ATTNRES_TUNING");
     if (on == nullptr || std::strcmp(on, "1") != 0) return;
     if (const char* v = std::getenv("ATTNRES_MQG")) mqg = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_OUT_BATCH")) out_batch = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_OUT_BATCH_MIN_S")) out_batch_min_s = std::atoi(v);
+    if (const char* v = std::getenv("ATTNRES_STREAM_WAVES")) {
+      const int w = std::atoi(v);
+      if (w >= 1 && w <= kStreamWaves) stream_waves = w;
+    }
     if (const char* v = std::getenv("ATTNRES_BWD_PER_CU")) {
       bwd_per_cu = std::atoi(v);
       if (bwd_per_cu > kBwdMaxPerCu) bwd_per_cu = kBwdMaxPerCu;
@@ -253,10 +258,10 @@ int get_stream(DeviceState& st, int combo, bool out_bf, int nch, int variant, hi
 // 8); at S = 2 the batches measured slower, so they start at S = 4.  As many
 // rows as the LDS left over by the kernel's own arrays holds, at most 8.
 constexpr int kOutBatchMax = 8;
-int stream_out_batch(int num_sources, int64_t out_row_bytes, int static_lds, int max_lds) {
+int stream_out_batch(int num_sources, int64_t out_row_bytes, int static_lds, int max_lds, int waves) {
   const int min_s = tuning().out_batch_min_s;
   if (num_sources < min_s || out_row_bytes <= 0) return 1;
-  int64_t cap = ((int64_t)max_lds - static_lds) / ((int64_t)kStreamWaves * out_row_bytes);
+  int64_t cap = ((int64_t)max_lds - static_lds) / ((int64_t)waves * out_row_bytes);
   const int limit = tuning().out_batch > 0 ? tuning().out_batch : kOutBatchMax;
   if (cap > limit) cap = limit;
   return cap >= 2 ? (int)cap : 1;
@@ -571,8 +576,26 @@ void choose_qg(RouteChoice& ch, int num_sources, int num_queries, int hidden, in
   if (lds + kQgStaticLds <= (size_t)max_lds) ch.qg_lds = lds;
 }
 
+// Waves per workgroup of the streaming kernels (one workgroup per CU).  From
+// S = 6 over enough rows three waves run faster than four (3B shape, 32768
+// rows: S = 8 81.6% -> 85.3% of peak, S = 7 81.4% -> 84.6%; 8B shape, 16384
+// rows, S = 9: 77.7% -> 80.9%): the HBM serves this read stream best with
+// about one row in flight per wave of 768, and four waves' two-slot pipelines
+// keep ~1.4 rows each in flight.  At S <= 5 four waves are faster (S = 3:
+// 84.3% against 75.6%), and so they are over 8192 rows (config 5: 2.57 against
+// 2.61 ms per sweep), where a wave's share is short.  The fused (arena)
+// variants, whose partial write-back adds a second write stream, gain from
+// three only at 32768 rows (arena sweep at the 3B shape 15.45 -> 15.12 ms;
+// 16384 rows of the 8B schedule 11.34 -> 11.60 ms, slower).
+constexpr int kStreamFewWavesMinS = 6;
+int stream_waves_for(int num_sources, int64_t num_tokens, bool fused) {
+  if (tuning().stream_waves > 0) return tuning().stream_waves;
+  const int64_t min_rows = fused ? 32768 : 16384;
+  return num_sources >= kStreamFewWavesMinS && num_tokens >= min_rows ? 3 : kStreamWaves;
+}
+
 RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
-                         int num_queries, int num_cus, bool stream_ok) {
+                         int num_queries, int num_cus, bool stream_ok, bool fused) {
   RouteChoice ch;
   const bool bf = src_dtype == ATTNRES_DTYPE_BF16;
   ch.combo = bf ? (param_dtype == ATTNRES_DTYPE_BF16 ? kBfDot2 : kBfFma) : kF32Fma;
@@ -588,7 +611,7 @@ RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int sr
                                                                : tuning().stream;
   ch.stream = stream_shape && (want_stream == 1 || (want_stream < 0 && num_tokens >= tuning().stream_min_tokens));
   if (ch.stream) {
-    ch.block = 64 * kStreamWaves;
+    ch.block = 64 * stream_waves_for(num_sources, num_tokens, fused);
   } else {
     ch.v = pick_v(num_tokens, hidden / (bf ? 8 : 4), num_cus, &ch.block);
   }
@@ -605,8 +628,8 @@ RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int sr
 RouteChoice plan_route(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
                        int out_dtype, int num_queries, int mode, bool equally_spaced, const DeviceState& st) {
   const bool stream_ok = !(mode == ATTNRES_MODE_ACCUM && num_sources < 2);
-  RouteChoice ch =
-      choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st.num_cus, stream_ok);
+  RouteChoice ch = choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st.num_cus,
+                                stream_ok, mode != ATTNRES_MODE_PLAIN);
   if (ch.stream) {
     ch.variant = mode != ATTNRES_MODE_PLAIN ? kStreamFused
                  : (equally_spaced || num_sources < 2) ? kStreamPlain
@@ -704,10 +727,13 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
     int slds = 0;
     rc = get_stream(*st, ch.combo, out_dtype == ATTNRES_DTYPE_BF16, ch.nch, ch.variant, &f, &bpc, &slds);
     if (rc != ATTNRES_OK) return rc;
-    work_units = (num_tokens + kStreamWaves - 1) / kStreamWaves;
+    const int waves = block / 64;
+    work_units = (num_tokens + waves - 1) / waves;
     const int64_t out_row_bytes = (int64_t)hidden * esize(out_dtype);
-    out_batch = stream_out_batch(num_sources, out_row_bytes, slds, st->max_lds);
-    if (out_batch > 1) stream_lds = (size_t)kStreamWaves * out_batch * out_row_bytes;
+    // the fused variants write their partial rows back as they go: batching
+    // the output rows alone measured 1-2% slower there
+    out_batch = ch.variant == kStreamFused ? 1 : stream_out_batch(num_sources, out_row_bytes, slds, st->max_lds, waves);
+    if (out_batch > 1) stream_lds = (size_t)waves * out_batch * out_row_bytes;
   } else if (ch.qg_lds > 0) {
     rc = get_route_qg(*st, num_sources, ch.v, block, ch.qg_lds, &f, &bpc);
     if (rc != ATTNRES_OK) return rc;

@@ -406,6 +406,50 @@ def _full_config_check(gpu, name, seed, calls, rows=384):
     torch.cuda.empty_cache()
 
 
+# (workload, source counts): the streaming kernel's launch shapes at full size -
+# three waves per workgroup with 8 staged output rows (3B, S >= 6), four waves
+# with 6 staged rows (S = 4, 5), no staging (S <= 3), three waves with 6 staged
+# 8 KiB rows (8B, S = 9); the last batch of most waves is partial
+STREAM_FULL = [("cfg2", (2, 4, 5, 6, 8)), ("cfg3", (9,))]
+
+
+@pytest.mark.parametrize("name,calls", STREAM_FULL, ids=[c[0] for c in STREAM_FULL])
+def test_streaming_kernel_matches_workgroup_kernel_every_row(gpu, name, calls):
+    # every element of every row: the row-per-wave streaming kernel (online
+    # softmax, staged and batched output stores) against the row-per-workgroup
+    # kernel (two-pass softmax, direct stores), two independent fp32
+    # computations of the same rows.  Each is its bf16 rounding (half an ulp)
+    # of a fp32 sum whose own error is below S * 2^-24 * max_s |x_s|, so they
+    # agree to one ulp plus 2^-16 * max_s |x_s| (the second term matters only
+    # where the sum cancels far below its sources), and >= 99% of elements are
+    # equal; the oracle checks both on sampled rows elsewhere
+    w = workloads.get(name)
+    pool = workloads.make_pool(w, gpu, 7)
+    q, gn = workloads.make_params(w, gpu, 7, len(calls))
+    for j, s in enumerate(calls):
+        print(f"stream vs workgroup {name} S={s} rows={w.tokens}", flush=True)
+        outs = []
+        for pol in (_capi.POLICY_STREAM, _capi.POLICY_WORKGROUP):
+            prev = _capi.set_kernel_policy(pol)
+            try:
+                with torch.no_grad():
+                    outs.append(ops.route_call(pool, s, q[j], gn[j], w.eps, w.dtype)[0][0].float())
+            finally:
+                _capi.set_kernel_policy(prev)
+        torch.cuda.synchronize()
+        a, b = outs
+        xmax = pool[:s].abs().amax(0).float().reshape(b.shape)
+        tol = torch.exp2(torch.floor(torch.log2(torch.clamp(b.abs(), min=2.0**-126))) - 7) + 2.0**-16 * xmax
+        excess = ((a - b).abs() / tol).max().item()
+        same = (a == b).float().mean().item()
+        print(f"  max |diff| / tol {excess:.3f}, {same:.5f} of elements equal", flush=True)
+        assert excess <= 1.0, f"{name} S={s}: streaming and workgroup kernels differ by {excess:.2f}x the bar"
+        assert same >= 0.99, f"{name} S={s}: only {same:.4f} of elements equal"
+        del outs, a, b, tol, xmax
+    del pool
+    torch.cuda.empty_cache()
+
+
 def test_cfg3_8b_deepest_routing_full_size(gpu):
     _full_config_check(gpu, "cfg3", 3, (9, 9))
 
