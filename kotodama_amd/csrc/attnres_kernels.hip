@@ -1169,8 +1169,10 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   // Item counters are 32-bit and wave-uniform so all loop control and address
   // arithmetic stays in SGPRs (gfx9 has no scalar 64-bit signed compare).
   const uint32_t n_tok = (uint32_t)P.n_tokens;
-  const uint32_t nw = gridDim.x * ATTNRES_STREAM_WAVES;
-  uint32_t tok = blockIdx.x * ATTNRES_STREAM_WAVES + wave;
+  // waves per workgroup: up to ATTNRES_STREAM_WAVES, chosen at launch (P.block)
+  const uint32_t wpb = __builtin_amdgcn_readfirstlane((uint32_t)P.block >> 6);
+  const uint32_t nw = gridDim.x * wpb;
+  uint32_t tok = blockIdx.x * wpb + wave;
   if (tok >= n_tok) return;  // no barrier follows
 
   const uint64_t row_bytes = (uint64_t)P.src_ld * C::BYTES;
@@ -1263,7 +1265,9 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   // variant of the access pattern: 78.5% -> 90.9% of peak at S = 8, batches
   // of 8).  The staged layout is [row][chunk][piece][lane] (consecutive lanes
   // 8 or 16 bytes apart: no bank conflicts); a wave reads back only what its
-  // own lanes wrote, so no barrier is needed.
+  // own lanes wrote, so no barrier is needed.  The fused variants store each
+  // row at once (their partial write-back is a second write stream; staging
+  // measured slower there) and carry no staging code.
   const uint32_t batch = (uint32_t)P.out_batch;
   extern __shared__ u32x4 stream_stage[];
   constexpr uint32_t STAGE_ROW = NCH * OPC * 64 * OPB;     // bytes of one staged row
@@ -1413,7 +1417,7 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
             pk[c][h] = u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]), as_u32(o[4 * h + 2]), as_u32(o[4 * h + 3])};
         }
       }
-      if (batch > 1) {
+      if (!FUSED && batch > 1) {
         // stage the row; the wave's batch is stored when full (or at the end)
         if (nheld == 0) t_first = t;
 #pragma unroll
@@ -1494,7 +1498,9 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
     tok = __builtin_amdgcn_readfirstlane(t2);
     s = __builtin_amdgcn_readfirstlane(s2);
   }
-  if (nheld > 0) flush_staged();
+  if constexpr (!FUSED) {
+    if (nheld > 0) flush_staged();
+  }
 }
 
 
