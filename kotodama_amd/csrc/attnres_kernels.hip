@@ -9,29 +9,37 @@
 //   w        = softmax over s of logit                 (llama.py:642-643)
 //   out      = sum_s w_s * x_s   (raw, un-normalised)  (llama.py:644)
 //
-// The work is a GEMV per token at ~2 flop/byte, so it is bound by HBM and
-// uses no MFMA.  Layout of the computation:
+// With one query the work is a GEMV per token at ~2 flop/byte, bound by HBM.
+// The kernel families (each row-block of a source is a separate pointer; no
+// stacked copy is needed):
 //
-//   * One workgroup owns one token row at a time (grid-stride loop over
-//     tokens).  Thread i owns the 16-byte chunks i, i+blockDim, ... of the
-//     row (V chunks), so every wave-wide load is 1 KiB contiguous.
-//   * All S source chunks of the token are loaded into registers up front
-//     (S*V 128-bit loads in flight per thread), so each source byte leaves
-//     HBM exactly once and the softmax can be exact (two-pass over
-//     registers, no online rescaling).
-//   * Per thread: partial sum(x^2) and x.qw per source (bf16 pairs through
-//     v_dot2c_f32_bf16, fp32 accumulation).  Per wave: DPP row reductions
-//     and row broadcasts leave the wave total in lane 63, which writes the
-//     2S totals to LDS.  One barrier per token; every thread then sums the
-//     per-wave totals (broadcast LDS reads), forms the S logits and the
-//     softmax, and writes its chunks of the weighted sum.
-//   * The LDS exchange buffer is double-buffered by round parity, so one
-//     barrier per round is enough.
+//   * attnres_stream_*  one wave per token row (prefill; the hot path).  A
+//     lane holds 16-byte chunks l, l+64, ..., so each wave-wide load is 1 KiB
+//     contiguous.  The wave's (token, source) items flow through a two-slot
+//     register pipeline (the next row is requested before the current one is
+//     processed); per source: sum(x^2) and x.qw, one DPP wave reduction each,
+//     then an online softmax with the rescale folded into the accumulating
+//     FMA.  Finished output rows are staged in LDS and stored in batches per
+//     wave; one workgroup of three or four waves per CU.
+//   * attnres_route_*   one workgroup per token row (decode, few rows, Q > 1
+//     queries, the fused arena modes).  Thread i owns chunks i, i+blockDim,
+//     ...; all S source chunks are loaded at once, partial sums are reduced
+//     per wave by a transposing permlane/DPP tree and across waves through
+//     one double-buffered LDS exchange, and the softmax is exact (two-pass
+//     over registers).  The _qg instances batch Q queries (staged in LDS) and
+//     mix sources on the matrix cores (v_mfma_f32_4x4x4_16b_bf16, weights as
+//     bf16 hi + lo), since Q queries turn the mix into a small product.
+//   * attnres_merge_*   the phase-2 merge of a running block into a phase-1
+//     result, one workgroup per row.
+//   * attnres_route_bwd_* / _mq_ / _mqg_ / _dqw* / merge_bwd / reduce_dqw*:
+//     the backward of routing and merge (source, query and gain gradients;
+//     the query gradient summed over rows in a fixed order), the batched-
+//     query forms again on the matrix cores.
 //
-// The S sources are separate pointers (no stacked copy is needed), the
-// number of sources S is a template parameter (register arrays stay in
-// VGPRs), and the last slot can be formed in-kernel from a sublayer delta
-// (fused partial accumulate / block commit for the decode and arena paths).
+// S is a template parameter of the row-per-workgroup kernels (register arrays
+// stay in VGPRs) and a runtime argument of the streaming ones; the last slot
+// can be formed in-kernel from a sublayer delta (fused partial accumulate /
+// block commit for the decode and arena paths).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>

@@ -61,12 +61,21 @@ def bf16_ulp(x):
 
 
 def check_bf16(out, ref, label, exact_frac=0.98):
+    """bf16 bar: |err| <= max(2e-2, 1 ulp of |ref|) and >= exact_frac equal to the correctly rounded
+    oracle.  Prints the statistics that show how much of the bar is used: the share of elements equal
+    to the correctly rounded oracle, the worst error in ulps, and the worst error in ulps where the ulp
+    term sets the bar (|ref| >= 4, one ulp >= 2^-5 > 2e-2) — correct rounding needs at most 0.5 there."""
     out = np64(out)
     err = np.abs(out - ref)
-    tol = np.maximum(2e-2, bf16_ulp(ref))
+    ulp = bf16_ulp(ref)
+    tol = np.maximum(2e-2, ulp)
     bad = err > tol
     assert not bad.any(), f"{label}: {bad.sum()} elements over tolerance, worst err {err.max():.3e}"
     same = np.mean(out == O.bf16_round(ref))
+    big = np.abs(ref) >= 4.0
+    worst_big = float((err[big] / ulp[big]).max()) if big.any() else 0.0
+    print(f"[bf16] {label}: {same:.5f} equal to the rounded oracle; worst {float((err / ulp).max()):.2f} ulp; "
+          f"where |ref| >= 4 ({int(big.sum())} elements) worst {worst_big:.2f} ulp", flush=True)
     assert same >= exact_frac, f"{label}: only {same:.4f} of elements equal the correctly rounded oracle"
 
 
