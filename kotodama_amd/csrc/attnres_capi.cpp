@@ -69,6 +69,14 @@ constexpr size_t kBwdStaticLds = 2 * ATTNRES_KMAX_WAVES * 48 * sizeof(float);  /
 constexpr size_t kQgStaticLds = 2 * ATTNRES_KMAX_WAVES * 72 * sizeof(float);   // batched-query reduction buffer
 constexpr size_t kMqgStaticLds = 2 * ATTNRES_KMAX_WAVES * 72 * sizeof(float);  // its backward's (S <= 8)
 
+// Query-gradient reduction kernels: one launch (`cols`), or two (`stage`
+// then `fin`) where the one-launch form's 32-bit offsets would not fit.
+struct ReduceFns {
+  hipFunction_t stage = nullptr;
+  hipFunction_t fin = nullptr;
+  hipFunction_t cols = nullptr;
+};
+
 struct DeviceState {
   std::atomic<bool> loaded{false};
   hipModule_t mods[kParts] = {};
@@ -90,8 +98,7 @@ struct DeviceState {
   hipFunction_t bwd[kBwdFuncs] = {};
   int bwd_bpc[kBwdFuncs] = {};
   int bwd_bpc_block[kBwdFuncs] = {};
-  hipFunction_t reduce = nullptr;
-  hipFunction_t reduce_stage = nullptr;
+  ReduceFns reduce;
   hipFunction_t merge_bwd[kMergeFuncs] = {};
   int merge_bwd_bpc[kMergeFuncs] = {};
   int merge_bwd_bpc_block[kMergeFuncs] = {};
@@ -118,12 +125,13 @@ std::atomic<int> g_policy{ATTNRES_POLICY_AUTO};
 // ATTNRES_STREAM_MIN_TOKENS choose when the row-per-wave streaming kernels
 // run, ATTNRES_GRID_MULT scales the resident-workgroup grid,
 // ATTNRES_STREAM_PER_CU sets the streaming kernels' workgroups per CU (0: the
-// occupancy limit), ATTNRES_BWD_PER_CU the backward's (at most
+// occupancy limit), ATTNRES_BWD_PER_CU caps the backward kernels' (at most
 // kBwdMaxPerCu, the bound its workspace size assumes), ATTNRES_QG=0 turns off
 // the batched-query kernel, ATTNRES_MQG=0 the matrix-core batched backward,
 // ATTNRES_OUT_BATCH caps the streaming kernels' staged output rows per wave
 // (1: store each row at once), ATTNRES_OUT_BATCH_MIN_S sets the source count
-// from which they stage.
+// from which they stage, ATTNRES_REDUCE_TWO_STAGE=1 reduces the query
+// gradients in two launches always.
 struct Tuning {
   int force_v = 0;
   int qg = 1;
@@ -136,12 +144,14 @@ struct Tuning {
   int out_batch = 0;           // > 0: at most this many staged output rows per streaming wave (1: none)
   int out_batch_min_s = 4;     // sources from which the streaming kernels stage output rows
   int stream_waves = 0;        // > 0: waves per workgroup of the streaming kernels (1..4); 0: by S
+  int reduce_two_stage = 0;    // 1: the query-gradient reduction in two launches
   Tuning() {
     const char* on = std::getenv("ATTNRES_TUNING");
     if (on == nullptr || std::strcmp(on, "1") != 0) return;
     if (const char* v = std::getenv("ATTNRES_MQG")) mqg = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_OUT_BATCH")) out_batch = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_OUT_BATCH_MIN_S")) out_batch_min_s = std::atoi(v);
+    if (const char* v = std::getenv("ATTNRES_REDUCE_TWO_STAGE")) reduce_two_stage = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_STREAM_WAVES")) {
       const int w = std::atoi(v);
       if (w >= 1 && w <= kStreamWaves) stream_waves = w;
@@ -472,16 +482,17 @@ int get_merge_bwd(DeviceState& st, bool pbf, bool ibf, int v, int block, hipFunc
   return ATTNRES_OK;
 }
 
-int get_reduce(DeviceState& st, hipFunction_t* stage, hipFunction_t* fin) {
+int get_reduce(DeviceState& st, const ReduceFns** out) {
   std::lock_guard<std::mutex> lk(g_mu);
-  if (st.reduce == nullptr) {
-    int rc = find_function(st, kReducePart, "attnres_reduce_dqw_stage", &st.reduce_stage);
+  if (st.reduce.fin == nullptr) {
+    int rc = find_function(st, kReducePart, "attnres_reduce_dqw_stage", &st.reduce.stage);
     if (rc != ATTNRES_OK) return rc;
-    rc = find_function(st, kReducePart, "attnres_reduce_dqw", &st.reduce);
+    rc = find_function(st, kReducePart, "attnres_reduce_dqw_cols", &st.reduce.cols);
+    if (rc != ATTNRES_OK) return rc;
+    rc = find_function(st, kReducePart, "attnres_reduce_dqw", &st.reduce.fin);
     if (rc != ATTNRES_OK) return rc;
   }
-  *stage = st.reduce_stage;
-  *fin = st.reduce;
+  *out = &st.reduce;
   return ATTNRES_OK;
 }
 
@@ -786,7 +797,7 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
 // Query/gain gradients from `nparts` per-workgroup partial rows in
 // `workspace`: summed in 64-row blocks (stage 1, in place), then the block
 // sums (final stage); a fixed order, so the result is deterministic.
-int reduce_launch(hipFunction_t fs, hipFunction_t fr, void* workspace, int nparts, int hidden, const void* query,
+int reduce_launch(const ReduceFns& fn, void* workspace, int nparts, int hidden, const void* query,
                   const void* gain, int param_dtype, void* grad_query, void* grad_gain, void* stream,
                   int num_queries = 1) {
   attnres_reduce_params R;
@@ -801,13 +812,18 @@ int reduce_launch(hipFunction_t fs, hipFunction_t fr, void* workspace, int npart
   R.d = hidden;
   R.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
   R.num_queries = num_queries;
+  const int64_t width = (int64_t)hidden * num_queries;
+  // one launch (32 columns per 1024-thread workgroup) for up to four queries
+  // where its byte offsets, up to 1024 rows past the last partial row, fit in
+  // 32 bits; else two
+  if (!tuning().reduce_two_stage && num_queries <= 4 && (int64_t)(nparts + 1024) * width * 4 < (int64_t)1 << 32)
+    return launch(fn.cols, (hidden + 31) / 32, 1024, R, stream);
   if (nparts > 64) {
-    const int64_t width = (int64_t)hidden * num_queries;
-    int rc = launch(fs, (int)((width + 63) / 64), 256, R, stream, (nparts + 63) / 64);
+    int rc = launch(fn.stage, (int)((width + 63) / 64), 256, R, stream, (nparts + 63) / 64);
     if (rc != ATTNRES_OK) return rc;
     R.part_step = 64;
   }
-  return launch(fr, (hidden + 255) / 256, 256, R, stream);
+  return launch(fn.fin, (hidden + 255) / 256, 256, R, stream);
 }
 
 }  // namespace
@@ -1084,9 +1100,9 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
     return fail(ATTNRES_ERR_ARG, "workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
                 (long long)need);
   if (!aligned16(workspace)) return fail(ATTNRES_ERR_ALIGN, "workspace not 16-byte aligned");
-  hipFunction_t fr = nullptr, fs = nullptr;
+  const ReduceFns* red = nullptr;
   if (grad_query != nullptr || grad_gain != nullptr) {
-    rc = get_reduce(*st, &fs, &fr);
+    rc = get_reduce(*st, &red);
     if (rc != ATTNRES_OK) return rc;
   }
 
@@ -1112,9 +1128,9 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
   rc = launch(f, (int)grid, block, P, stream, 1, lds);
-  if (rc != ATTNRES_OK || fr == nullptr) return rc;
+  if (rc != ATTNRES_OK || red == nullptr) return rc;
 
-  return reduce_launch(fs, fr, workspace, (int)grid, hidden, query, gain, param_dtype, grad_query, grad_gain, stream);
+  return reduce_launch(*red, workspace, (int)grid, hidden, query, gain, param_dtype, grad_query, grad_gain, stream);
 }
 
 // Workspace of the batched-query backward: c1 coefficients (num_tokens, Q, S)
@@ -1215,12 +1231,12 @@ int attnres_route_bwd_queries(const void* const* sources, int num_sources, int64
   }
   if (rc != ATTNRES_OK) return rc;
   const bool want_q = grad_query != nullptr || grad_gain != nullptr;
-  hipFunction_t fr = nullptr, fs = nullptr;
+  const ReduceFns* red = nullptr;
   int64_t grid_q = 0;
   if (want_q) {
     rc = get_bwd_dqw(*st, bf, v, block, &fq, &bpcq);
     if (rc != ATTNRES_OK) return rc;
-    rc = get_reduce(*st, &fs, &fr);
+    rc = get_reduce(*st, &red);
     if (rc != ATTNRES_OK) return rc;
     grid_q = (int64_t)st->num_cus * (bpcq < kBwdDqwPerCu ? bpcq : kBwdDqwPerCu);
     if (grid_q > num_tokens) grid_q = num_tokens;
@@ -1259,7 +1275,8 @@ int attnres_route_bwd_queries(const void* const* sources, int num_sources, int64
   P.inv_d = 1.0f / (float)hidden;
   // two resident workgroups per CU, as the single-query backward; the
   // matrix-core kernel at its occupancy limit
-  const int per_cu = mqg ? bpc : (bpc < 2 ? bpc : 2);
+  int per_cu = mqg ? bpc : (bpc < 2 ? bpc : 2);
+  if (tuning().bwd_per_cu > 0 && tuning().bwd_per_cu < per_cu) per_cu = tuning().bwd_per_cu;
   int64_t grid = (int64_t)st->num_cus * per_cu;
   if (grid > num_tokens) grid = num_tokens;
   rc = mqg ? launch(f, (int)grid, mqg_block, P, stream, 1, mqg_lds) : launch(f, (int)grid, block, P, stream);
@@ -1282,7 +1299,7 @@ int attnres_route_bwd_queries(const void* const* sources, int num_sources, int64
     rc = launch(fq, (int)grid_q, block, Q, stream);
     if (rc != ATTNRES_OK) return rc;
   }
-  return reduce_launch(fs, fr, part, (int)grid_q, hidden, query, gain, param_dtype, grad_query, grad_gain, stream,
+  return reduce_launch(*red, part, (int)grid_q, hidden, query, gain, param_dtype, grad_query, grad_gain, stream,
                        num_queries);
 }
 
@@ -1334,9 +1351,9 @@ int attnres_merge_bwd(const void* partial, int64_t num_tokens, int hidden, int p
     return fail(ATTNRES_ERR_ARG, "workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
                 (long long)need);
   if (!aligned16(workspace)) return fail(ATTNRES_ERR_ALIGN, "workspace not 16-byte aligned");
-  hipFunction_t fr = nullptr, fs = nullptr;
+  const ReduceFns* red = nullptr;
   if (grad_query != nullptr) {
-    rc = get_reduce(*st, &fs, &fr);
+    rc = get_reduce(*st, &red);
     if (rc != ATTNRES_OK) return rc;
   }
 
@@ -1358,8 +1375,8 @@ int attnres_merge_bwd(const void* partial, int64_t num_tokens, int hidden, int p
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
   rc = launch(f, (int)grid, block, P, stream);
-  if (rc != ATTNRES_OK || fr == nullptr) return rc;
-  return reduce_launch(fs, fr, workspace, (int)grid, hidden, query, nullptr, param_dtype, grad_query, nullptr, stream);
+  if (rc != ATTNRES_OK || red == nullptr) return rc;
+  return reduce_launch(*red, workspace, (int)grid, hidden, query, nullptr, param_dtype, grad_query, nullptr, stream);
 }
 
 }  // extern "C"

@@ -2232,32 +2232,34 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
         t += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c2acc), g * SEG + s));
       c2s[s] = t;
     }
-
-    // ---- dx_s = sum_q (w_qs G_q + c1_qs qw_q) + c2_s x_s, per chunk and group of four sources ----
+    // ---- dx_s = sum_q (w_qs G_q + c1_qs qw_q) + c2_s x_s, per chunk, group of
+    // four sources and element pair: the two accumulators of a pair are rounded
+    // and packed as soon as its queries are summed, so a source group holds 16
+    // packed words, not 32 fp32 sums ----
 #pragma unroll
     for (int k = 0; k < V; ++k) {
+      const uint32_t* qword = reinterpret_cast<const uint32_t*>(qrow[k]);  // query q, word w at [64 q + w]
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        f32x4 acc[8];  // acc[h][i]: dx of source 4*ks + i at element h of this lane's chunk
+        uint32_t packed[4][4];  // packed[i][w]: elements 2w, 2w+1 of source 4*ks + i
 #pragma unroll
-        for (int h = 0; h < 8; ++h) acc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int w = 0; w < 4; ++w) {
+          f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int g4 = 0; g4 < NQ4; ++g4) {
-          u32x4 qv[4];
+          for (int g4 = 0; g4 < NQ4; ++g4) {
+            const int q0 = 4 * g4;
+            uint32_t qv[4];
 #pragma unroll
-          for (int g = 0; g < 4; ++g) qv[g] = qrow[k][16 * (4 * g4 + g)];
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
+            for (int g = 0; g < 4; ++g) qv[g] = qword[64 * (q0 + g) + w];
             // B operands of elements 2w (low halves) and 2w+1 (high halves), four queries along k
-            const u32x2 bgl = {__builtin_amdgcn_perm(gq[4 * g4 + 1][k][w], gq[4 * g4][k][w], 0x05040100u),
-                               __builtin_amdgcn_perm(gq[4 * g4 + 3][k][w], gq[4 * g4 + 2][k][w], 0x05040100u)};
-            const u32x2 bgh = {__builtin_amdgcn_perm(gq[4 * g4 + 1][k][w], gq[4 * g4][k][w], 0x07060302u),
-                               __builtin_amdgcn_perm(gq[4 * g4 + 3][k][w], gq[4 * g4 + 2][k][w], 0x07060302u)};
-            const u32x2 bql = {__builtin_amdgcn_perm(qv[1][w], qv[0][w], 0x05040100u),
-                               __builtin_amdgcn_perm(qv[3][w], qv[2][w], 0x05040100u)};
-            const u32x2 bqh = {__builtin_amdgcn_perm(qv[1][w], qv[0][w], 0x07060302u),
-                               __builtin_amdgcn_perm(qv[3][w], qv[2][w], 0x07060302u)};
-            f32x4 lo = acc[2 * w], hi = acc[2 * w + 1];
+            const u32x2 bgl = {__builtin_amdgcn_perm(gq[q0 + 1][k][w], gq[q0][k][w], 0x05040100u),
+                               __builtin_amdgcn_perm(gq[q0 + 3][k][w], gq[q0 + 2][k][w], 0x05040100u)};
+            const u32x2 bgh = {__builtin_amdgcn_perm(gq[q0 + 1][k][w], gq[q0][k][w], 0x07060302u),
+                               __builtin_amdgcn_perm(gq[q0 + 3][k][w], gq[q0 + 2][k][w], 0x07060302u)};
+            const u32x2 bql = {__builtin_amdgcn_perm(qv[1], qv[0], 0x05040100u),
+                               __builtin_amdgcn_perm(qv[3], qv[2], 0x05040100u)};
+            const u32x2 bqh = {__builtin_amdgcn_perm(qv[1], qv[0], 0x07060302u),
+                               __builtin_amdgcn_perm(qv[3], qv[2], 0x07060302u)};
             lo = mfma_4x4x4(awh[g4][ks], bgl, lo);
             hi = mfma_4x4x4(awh[g4][ks], bgh, hi);
             lo = mfma_4x4x4(awl[g4][ks], bgl, lo);
@@ -2266,24 +2268,22 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
             hi = mfma_4x4x4(ach[g4][ks], bqh, hi);
             lo = mfma_4x4x4(acl[g4][ks], bql, lo);
             hi = mfma_4x4x4(acl[g4][ks], bqh, hi);
-            acc[2 * w] = lo;
-            acc[2 * w + 1] = hi;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int s = 4 * ks + i;
+            if (s >= S) break;
+            packed[i][w] = pack_bf16(__builtin_fmaf(c2s[s], bf_lo(x[s][k][w]), lo[i]),
+                                     __builtin_fmaf(c2s[s], bf_hi(x[s][k][w]), hi[i]));
           }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int s = 4 * ks + i;
           if (s >= S) break;
-          float dx[8];
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            dx[2 * w] = __builtin_fmaf(c2s[s], bf_lo(x[s][k][w]), acc[2 * w][i]);
-            dx[2 * w + 1] = __builtin_fmaf(c2s[s], bf_hi(x[s][k][w]), acc[2 * w + 1][i]);
-          }
           char* drow = reinterpret_cast<char*>(P.dsrc[s]) + tok * P.dsrc_ld * 2;
           st_row(row_rsrc(drow, row_bytes), (uint32_t)chunk[k] * 16,
-                 u32x4{pack_bf16(dx[0], dx[1]), pack_bf16(dx[2], dx[3]), pack_bf16(dx[4], dx[5]),
-                       pack_bf16(dx[6], dx[7])});
+                 u32x4{packed[i][0], packed[i][1], packed[i][2], packed[i][3]});
         }
       }
     }
@@ -2369,12 +2369,16 @@ __device__ __forceinline__ void route_bwd_dqw_body(const attnres_route_bwd_dqw_p
 
 
 // Query-gradient partials on the matrix cores (bf16 sources): as
-// route_bwd_dqw_body, with sum_s c1_qs x_s formed per element as column j
-// of a 4x4x4 block product: A = c1 of four queries (lane 4b+i: query
-// q0 + 4*g4 + i) over four sources (k), as bf16 hi + lo parts; B = the
-// lane's own four sources at that element.  Per row and group of four
-// sources: the source chunks and the lane's c1 values are requested
-// together, then 2 * 2 MFMAs per element (two query groups, hi and lo).
+// route_bwd_dqw_body, with sum c1_qs x_s formed per element as column j of a
+// 4x4x4 block product: A = c1 of four queries (lane 4b+i: query
+// q0 + 4*g4 + i) over four (row, source) pairs (k), as bf16 hi + lo parts;
+// B = the lane's own chunks of those four pairs at that element.  The
+// workgroup's pairs (its rows grid-stride, each row's S sources in order) are
+// taken four at a time whatever S is, so every k slot carries a real row (at
+// S = 1 four rows, at S = 5 a row and a quarter); the next four pairs' chunks
+// and c1 values are requested before the current four's 2 * 2 MFMAs per
+// element (two query groups, hi and lo).  Slots past the last pair read
+// through a zero-byte buffer resource: zeros, no memory traffic.
 template <int V>
 __device__ __forceinline__ void route_bwd_dqwm_body(const attnres_route_bwd_dqw_params& P) {
   constexpr int NQ4 = 2;  // eight queries per pass
@@ -2405,44 +2409,73 @@ __device__ __forceinline__ void route_bwd_dqwm_body(const attnres_route_bwd_dqw_
   }
   const int64_t row_bytes_ld = P.src_ld * 2;
   const uint32_t row_bytes = (uint32_t)(P.d * 2);
-  for (int64_t tok = blockIdx.x; tok < P.n_tokens; tok += gridDim.x) {
-    const float* crow = P.c1 + (tok * nq + q0) * S;
-    for (int s0 = 0; s0 < S; s0 += 4) {
-      u32x4 x[4][V];
+  const uint32_t rows =
+      (int64_t)blockIdx.x < P.n_tokens ? (uint32_t)((P.n_tokens - 1 - blockIdx.x) / gridDim.x + 1) : 0u;
+  const uint32_t npairs = rows * (uint32_t)S;
+  const uint32_t items = (npairs + 3) / 4;
+
+  // the next pair to request: row blockIdx.x + pj * gridDim.x, source ps
+  uint32_t pj = 0, ps = 0, pnext = 0;
+  auto load_item = [&](u32x4 (&x)[4][V], float (&c)[NQ4][4]) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int s = s0 + i < S ? s0 + i : S - 1;  // past S: a repeated row, coefficient 0 below
-        char* row = reinterpret_cast<char*>(const_cast<void*>(P.src[s])) + tok * row_bytes_ld;
-        const __amdgpu_buffer_rsrc_t rs = row_rsrc(row, row_bytes);
+    for (int i = 0; i < 4; ++i) {
+      const bool valid = pnext < npairs;
+      const int64_t tok = (int64_t)blockIdx.x + (int64_t)pj * gridDim.x;
+      char* row = reinterpret_cast<char*>(const_cast<void*>(P.src[ps])) + tok * row_bytes_ld;
+      const __amdgpu_buffer_rsrc_t rs = row_rsrc(row, valid ? row_bytes : 0u);
 #pragma unroll
-        for (int k = 0; k < V; ++k) x[i][k] = ld_row(rs, (uint32_t)chunk[k] * 16);
-      }
-      u32x2 ah[NQ4], al[NQ4];
+      for (int k = 0; k < V; ++k) x[i][k] = ld_row(rs, (uint32_t)chunk[k] * 16);
+      const float* crow = P.c1 + (tok * nq + q0) * S + ps;  // c1 of query q0 + g at crow[g * S]
 #pragma unroll
       for (int g4 = 0; g4 < NQ4; ++g4) {
         const int g = 4 * g4 + ai;
-        float c[4];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) c[kk] = (g < ng && s0 + kk < S) ? crow[g * S + s0 + kk] : 0.f;
-        const uint32_t h01 = pack_bf16(c[0], c[1]), h23 = pack_bf16(c[2], c[3]);
-        ah[g4] = u32x2{h01, h23};
-        al[g4] = u32x2{pack_bf16(c[0] - bf_lo(h01), c[1] - bf_hi(h01)), pack_bf16(c[2] - bf_lo(h23), c[3] - bf_hi(h23))};
+        c[g4][i] = (valid && g < ng) ? crow[g * S] : 0.f;
       }
+      ++pnext;
+      if (++ps == (uint32_t)S) {
+        ps = 0;
+        ++pj;
+      }
+    }
+  };
+
+  u32x4 xa[4][V], xb[4][V];
+  float ca[NQ4][4], cb[NQ4][4];
+  if (items > 0) load_item(xa, ca);
+  for (uint32_t it = 0; it < items; ++it) {
+    if (it + 1 < items) load_item(xb, cb);
+    u32x2 ah[NQ4], al[NQ4];
 #pragma unroll
-      for (int k = 0; k < V; ++k) {
+    for (int g4 = 0; g4 < NQ4; ++g4) {
+      const float* c = ca[g4];
+      const uint32_t h01 = pack_bf16(c[0], c[1]), h23 = pack_bf16(c[2], c[3]);
+      ah[g4] = u32x2{h01, h23};
+      al[g4] = u32x2{pack_bf16(c[0] - bf_lo(h01), c[1] - bf_hi(h01)), pack_bf16(c[2] - bf_lo(h23), c[3] - bf_hi(h23))};
+    }
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const u32x2 blo = {__builtin_amdgcn_perm(x[1][k][w], x[0][k][w], 0x05040100u),
-                             __builtin_amdgcn_perm(x[3][k][w], x[2][k][w], 0x05040100u)};
-          const u32x2 bhi = {__builtin_amdgcn_perm(x[1][k][w], x[0][k][w], 0x07060302u),
-                             __builtin_amdgcn_perm(x[3][k][w], x[2][k][w], 0x07060302u)};
+    for (int k = 0; k < V; ++k) {
 #pragma unroll
-          for (int g4 = 0; g4 < NQ4; ++g4) {
-            acc[k][2 * w][g4] = mfma_4x4x4(al[g4], blo, mfma_4x4x4(ah[g4], blo, acc[k][2 * w][g4]));
-            acc[k][2 * w + 1][g4] = mfma_4x4x4(al[g4], bhi, mfma_4x4x4(ah[g4], bhi, acc[k][2 * w + 1][g4]));
-          }
+      for (int w = 0; w < 4; ++w) {
+        const u32x2 blo = {__builtin_amdgcn_perm(xa[1][k][w], xa[0][k][w], 0x05040100u),
+                           __builtin_amdgcn_perm(xa[3][k][w], xa[2][k][w], 0x05040100u)};
+        const u32x2 bhi = {__builtin_amdgcn_perm(xa[1][k][w], xa[0][k][w], 0x07060302u),
+                           __builtin_amdgcn_perm(xa[3][k][w], xa[2][k][w], 0x07060302u)};
+#pragma unroll
+        for (int g4 = 0; g4 < NQ4; ++g4) {
+          acc[k][2 * w][g4] = mfma_4x4x4(al[g4], blo, mfma_4x4x4(ah[g4], blo, acc[k][2 * w][g4]));
+          acc[k][2 * w + 1][g4] = mfma_4x4x4(al[g4], bhi, mfma_4x4x4(ah[g4], bhi, acc[k][2 * w + 1][g4]));
         }
       }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) xa[i][k] = xb[i][k];
+    }
+#pragma unroll
+    for (int g4 = 0; g4 < NQ4; ++g4) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) ca[g4][kk] = cb[g4][kk];
     }
   }
   float* prow = P.part + (int64_t)blockIdx.x * nq * P.d;
@@ -2657,6 +2690,94 @@ __device__ __forceinline__ void reduce_dqw_stage_body(const attnres_reduce_param
     P.part[(int64_t)row0 * width + col] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
 }
 
+// The whole query-gradient reduction in one launch: workgroup x (1024
+// threads) owns columns [32x, 32x + 32) of every query, so each wave reads
+// whole 128-byte lines of two partial rows.  Thread (r, c) = (tid / 32,
+// tid % 32) sums partial rows r, r + 32, r + 64, ... of column c in that
+// order (32 rows of one query requested at once, through a buffer resource
+// over the nparts rows with 32-bit offsets; rows past the end read zeros);
+// the 32 row lanes are then added in a fixed tree through LDS (lanes
+// 4k..4k+3 in order, then the 8 sums in order) and the fold
+// qw = query * gain is applied backwards: dquery = dqw * gain, dgain = sum
+// over queries (in order) of dqw * query.  Every sum has a fixed order, so
+// the result is deterministic.
+__device__ __forceinline__ void reduce_dqw_cols_body(const attnres_reduce_params& P) {
+  constexpr int CW = 32, RL = 32, QB = 1, RB = 32;
+  __shared__ float red[QB][RL][CW + 1];
+  __shared__ float red2[QB][RL / 4][CW + 1];
+  const int c = threadIdx.x & (CW - 1), r = threadIdx.x / CW;
+  const int col = blockIdx.x * CW + c;
+  const bool in = col < P.d;
+  const int nq = P.num_queries > 1 ? P.num_queries : 1;
+  const int64_t width = (int64_t)P.d * nq;
+  const __amdgpu_buffer_rsrc_t rs = row_rsrc(reinterpret_cast<char*>(P.part), (uint32_t)(P.nparts * width * 4));
+  float g = 1.f;
+  if (P.gain && in) g = P.param_bf16 ? bf_lo(reinterpret_cast<const uint16_t*>(P.gain)[col])
+                                     : reinterpret_cast<const float*>(P.gain)[col];
+  float dg = 0.f;
+  for (int q0 = 0; q0 < nq; q0 += QB) {
+    float acc[QB];
+#pragma unroll
+    for (int b = 0; b < QB; ++b) acc[b] = 0.f;
+    if (in) {
+      // lane offsets carry the row (so rows at or past nparts fail the
+      // resource's range check and read zeros), the scalar offset the query
+      // column block within a row
+      for (int r0 = r; r0 < P.nparts; r0 += RL * RB) {
+        float v[QB][RB];
+#pragma unroll
+        for (int b = 0; b < QB; ++b) {
+          const uint32_t soff = (uint32_t)((int64_t)(q0 + b) * P.d * 4);
+#pragma unroll
+          for (int j = 0; j < RB; ++j) {
+            const uint32_t voff = (uint32_t)(((int64_t)(r0 + RL * j) * width + col) * 4);
+            v[b][j] = q0 + b < nq ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, 0))
+                                  : 0.f;
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < QB; ++b) {
+#pragma unroll
+          for (int j = 0; j < RB; ++j) acc[b] += v[b][j];
+        }
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < QB; ++b) red[b][r][c] = acc[b];
+    __syncthreads();
+    if (r < RL / 4) {
+#pragma unroll
+      for (int b = 0; b < QB; ++b)
+        red2[b][r][c] = ((red[b][4 * r][c] + red[b][4 * r + 1][c]) + red[b][4 * r + 2][c]) + red[b][4 * r + 3][c];
+    }
+    __syncthreads();
+    if (r == 0 && in) {
+#pragma unroll
+      for (int b = 0; b < QB; ++b) {
+        const int qi = q0 + b;
+        if (qi >= nq) break;
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < RL / 4; ++k) t += red2[b][k][c];
+        const int64_t ci = (int64_t)qi * P.d + col;
+        const float q = P.param_bf16 ? bf_lo(reinterpret_cast<const uint16_t*>(P.query)[ci])
+                                     : reinterpret_cast<const float*>(P.query)[ci];
+        const float dq = P.gain ? t * g : t;
+        dg = __builtin_fmaf(t, q, dg);
+        if (P.dquery) {
+          if (P.param_bf16) reinterpret_cast<__bf16*>(P.dquery)[ci] = (__bf16)dq;
+          else reinterpret_cast<float*>(P.dquery)[ci] = dq;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (r == 0 && in && P.dgain) {
+    if (P.param_bf16) reinterpret_cast<__bf16*>(P.dgain)[col] = (__bf16)dg;
+    else reinterpret_cast<float*>(P.dgain)[col] = dg;
+  }
+}
+
 // Final stage: sum the partial rows 0, part_step, 2*part_step, ... column by
 // column (fixed order, so the result is deterministic) and apply the fold
 // qw = query * gain backwards.
@@ -2665,21 +2786,48 @@ __device__ __forceinline__ void reduce_dqw_body(const attnres_reduce_params& P) 
   if (col >= P.d) return;
   const int nq = P.num_queries > 1 ? P.num_queries : 1;
   const int64_t width = (int64_t)P.d * nq;
+  const int nrows = (P.nparts + P.part_step - 1) / P.part_step;  // rows 0, part_step, 2 part_step, ...
   float g = 1.f;
   if (P.gain) g = P.param_bf16 ? bf_lo(reinterpret_cast<const uint16_t*>(P.gain)[col])
                                : reinterpret_cast<const float*>(P.gain)[col];
   float dg = 0.f;
-  for (int qi = 0; qi < nq; ++qi) {
-    const int64_t c = (int64_t)qi * P.d + col;
-    float acc = 0.f;
-    for (int p = 0; p < P.nparts; p += P.part_step) acc += P.part[(int64_t)p * width + c];
-    const float q = P.param_bf16 ? bf_lo(reinterpret_cast<const uint16_t*>(P.query)[c])
-                                 : reinterpret_cast<const float*>(P.query)[c];
-    const float dq = P.gain ? acc * g : acc;
-    dg = __builtin_fmaf(acc, q, dg);
-    if (P.dquery) {
-      if (P.param_bf16) reinterpret_cast<__bf16*>(P.dquery)[c] = (__bf16)dq;
-      else reinterpret_cast<float*>(P.dquery)[c] = dq;
+  // QB queries x RB rows requested at once; each query's rows summed in row order
+  constexpr int QB = 4, RB = 16;
+  for (int q0 = 0; q0 < nq; q0 += QB) {
+    float acc[QB];
+#pragma unroll
+    for (int b = 0; b < QB; ++b) acc[b] = 0.f;
+    for (int r0 = 0; r0 < nrows; r0 += RB) {
+      float v[QB][RB];
+#pragma unroll
+      for (int b = 0; b < QB; ++b) {
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+          const bool in = q0 + b < nq && r0 + j < nrows;
+          v[b][j] = in ? P.part[(int64_t)(r0 + j) * P.part_step * width + (int64_t)(q0 + b) * P.d + col] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < QB; ++b) {
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+          if (r0 + j < nrows) acc[b] += v[b][j];
+        }
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < QB; ++b) {
+      const int qi = q0 + b;
+      if (qi >= nq) break;
+      const int64_t c = (int64_t)qi * P.d + col;
+      const float q = P.param_bf16 ? bf_lo(reinterpret_cast<const uint16_t*>(P.query)[c])
+                                   : reinterpret_cast<const float*>(P.query)[c];
+      const float dq = P.gain ? acc[b] * g : acc[b];
+      dg = __builtin_fmaf(acc[b], q, dg);
+      if (P.dquery) {
+        if (P.param_bf16) reinterpret_cast<__bf16*>(P.dquery)[c] = (__bf16)dq;
+        else reinterpret_cast<float*>(P.dquery)[c] = dq;
+      }
     }
   }
   if (P.dgain) {
@@ -2884,6 +3032,9 @@ extern "C" __global__ void __launch_bounds__(256) attnres_reduce_dqw_stage(attnr
   reduce_dqw_stage_body(P);
 }
 extern "C" __global__ void __launch_bounds__(256) attnres_reduce_dqw(attnres_reduce_params P) { reduce_dqw_body(P); }
+extern "C" __global__ void __launch_bounds__(1024) attnres_reduce_dqw_cols(attnres_reduce_params P) {
+  reduce_dqw_cols_body(P);
+}
 #endif
 #if ATTNRES_PART == 5 || defined(ATTNRES_ALL_PARTS)
 BWD_S(9)

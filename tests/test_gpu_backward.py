@@ -232,6 +232,8 @@ MQ_CASES = [
     (torch.bfloat16, 4, 4096, 1, 12, 4, True, "mqg"),  # 256-thread rows
     (torch.bfloat16, 5, 520, 1, 9, 3, False, "mqg"),  # one thread holds the row's last chunk
     (torch.bfloat16, 3, 2056, 1, 10, 6, True, "mqg"),  # 257 chunks: threads past the end
+    (torch.bfloat16, 8, 4096, 1, 12, 8, True, "mqg"),  # two chunks per thread, eight queries
+    (torch.bfloat16, 6, 3584, 1, 10, 7, False, "mqg"),  # 448 chunks: second chunks past the end
     (torch.bfloat16, 7, 3072, 1, 40, 9, True, "mq"),  # nine queries
     (torch.bfloat16, 9, 2048, 2, 12, 4, False, "mq"),
     (torch.bfloat16, 3, 8192, 1, 16, 3, True, "mq"),
