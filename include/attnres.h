@@ -58,9 +58,10 @@ const char* attnres_last_error(void);
 #define ATTNRES_POLICY_STREAM 2    /* one wave per token row, sources streamed (where the shape allows) */
 
 /*
- * Select the kernel family; returns the previous policy (or ATTNRES_ERR_ARG).
- * Both families compute the same function; AUTO picks by launch size.  A
- * tuning and testing switch with no counterpart in the reference.
+ * Select the kernel family of routing and merge calls; returns the previous
+ * policy (or ATTNRES_ERR_ARG).  Both families compute the same function; AUTO
+ * picks by launch size.  A tuning and testing switch with no counterpart in
+ * the reference.
  */
 int attnres_set_kernel_policy(int policy);
 

@@ -93,6 +93,7 @@ struct DeviceState {
   int stream_bpc[kStreamFuncs] = {};
   int stream_slds[kStreamFuncs] = {};  // static LDS bytes of each streaming kernel
   hipFunction_t merge[kMergeFuncs] = {};
+  hipFunction_t merge_stream[2 * kStreamMaxChunks] = {};  // row-per-wave merge: query path x row KiB
   int merge_bpc[kMergeFuncs] = {};
   int merge_bpc_block[kMergeFuncs] = {};
   hipFunction_t bwd[kBwdFuncs] = {};
@@ -131,7 +132,8 @@ std::atomic<int> g_policy{ATTNRES_POLICY_AUTO};
 // ATTNRES_OUT_BATCH caps the streaming kernels' staged output rows per wave
 // (1: store each row at once), ATTNRES_OUT_BATCH_MIN_S sets the source count
 // from which they stage, ATTNRES_REDUCE_TWO_STAGE=1 reduces the query
-// gradients in two launches always.
+// gradients in two launches always, ATTNRES_MERGE_STREAM=0 keeps the merge on
+// its row-per-workgroup kernel.
 struct Tuning {
   int force_v = 0;
   int qg = 1;
@@ -145,6 +147,7 @@ struct Tuning {
   int out_batch_min_s = 4;     // sources from which the streaming kernels stage output rows
   int stream_waves = 0;        // > 0: waves per workgroup of the streaming kernels (1..4); 0: by S
   int reduce_two_stage = 0;    // 1: the query-gradient reduction in two launches
+  int merge_stream = 1;        // 0: the merge never uses the row-per-wave kernel
   Tuning() {
     const char* on = std::getenv("ATTNRES_TUNING");
     if (on == nullptr || std::strcmp(on, "1") != 0) return;
@@ -152,6 +155,7 @@ struct Tuning {
     if (const char* v = std::getenv("ATTNRES_OUT_BATCH")) out_batch = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_OUT_BATCH_MIN_S")) out_batch_min_s = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_REDUCE_TWO_STAGE")) reduce_two_stage = std::atoi(v);
+    if (const char* v = std::getenv("ATTNRES_MERGE_STREAM")) merge_stream = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_STREAM_WAVES")) {
       const int w = std::atoi(v);
       if (w >= 1 && w <= kStreamWaves) stream_waves = w;
@@ -322,6 +326,21 @@ int get_route_qg(DeviceState& st, int s, int v, int block, size_t lds, hipFuncti
   }
   *f = st.route_qg[idx];
   *bpc = st.route_qg_bpc[idx];
+  return ATTNRES_OK;
+}
+
+// Row-per-wave merge (code-object part 3): bf16 rows of nch KiB, the query on
+// the v_dot2 path (bf16 parameter) or in fp32.
+int get_merge_stream(DeviceState& st, bool d2, int nch, hipFunction_t* f) {
+  const int idx = (d2 ? 0 : kStreamMaxChunks) + (nch - 1);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!st.merge_stream[idx]) {
+    char name[96];
+    snprintf(name, sizeof(name), "attnres_merge_stream_%s_c%d", d2 ? "d2" : "fm", nch);
+    int rc = find_function(st, kMergePart, name, &st.merge_stream[idx]);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  *f = st.merge_stream[idx];
   return ATTNRES_OK;
 }
 
@@ -961,12 +980,30 @@ int attnres_merge_fwd(const void* partial, int64_t num_tokens, int hidden, int p
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
-  int block = 0;
-  const int v = pick_v(num_tokens, nchunk, st->num_cus, &block);
-  if (v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
+  // The row-per-wave kernel for bf16 rows of whole 1 KiB chunks over enough
+  // rows (the routing kernels' policy and threshold), one workgroup of four
+  // waves per CU; else one workgroup per row.
+  const int64_t row_bytes = (int64_t)hidden * 2;
+  const int nch = (int)(row_bytes / 1024);
+  const bool stream_shape = tuning().merge_stream != 0 && pbf && ibf && row_bytes % 1024 == 0 && nch >= 1 &&
+                            nch <= kStreamMaxChunks && num_tokens < (int64_t)1 << 31;
+  const int policy = g_policy.load(std::memory_order_relaxed);
+  const int want_stream = policy == ATTNRES_POLICY_STREAM      ? 1
+                          : policy == ATTNRES_POLICY_WORKGROUP ? 0
+                                                               : tuning().stream;
+  const bool use_stream =
+      stream_shape && (want_stream == 1 || (want_stream < 0 && num_tokens >= tuning().stream_min_tokens));
+  int block = 0, v = 0;
   hipFunction_t f = nullptr;
   int bpc = 1;
-  rc = get_merge(*st, pbf, ibf, v, block, &f, &bpc);
+  if (use_stream) {
+    block = 64 * (tuning().stream_waves > 0 ? tuning().stream_waves : kStreamWaves);
+    rc = get_merge_stream(*st, param_dtype == ATTNRES_DTYPE_BF16, nch, &f);
+  } else {
+    v = pick_v(num_tokens, nchunk, st->num_cus, &block);
+    if (v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
+    rc = get_merge(*st, pbf, ibf, v, block, &f, &bpc);
+  }
   if (rc != ATTNRES_OK) return rc;
 
   attnres_merge_params P;
@@ -989,6 +1026,11 @@ int attnres_merge_fwd(const void* partial, int64_t num_tokens, int hidden, int p
   P.block = block;
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
+  if (use_stream) {
+    // one workgroup per CU, fewer when there are fewer rows than waves
+    const int64_t need = (num_tokens + block / 64 - 1) / (block / 64);
+    return launch(f, (int)(need < st->num_cus ? need : st->num_cus), block, P, stream);
+  }
   return launch(f, grid_for(num_tokens, st->num_cus, bpc), block, P, stream);
 }
 

@@ -1115,6 +1115,126 @@ __device__ __forceinline__ void merge_body(const attnres_merge_params& P) {
   }
 }
 
+// Phase-2 merge, one wave per token row (bf16 partial, inter and output rows
+// of NCH KiB): lane l holds the 16-byte chunks l, l+64, ... of a row.  The
+// wave's rows stream through a two-slot register pipeline one row per slot,
+// as the routing kernel's sources do: slot A takes token t's partial row,
+// slot B its inter row, and each load is requested before the previous row
+// is processed.  From the partial row: sum(p^2) and p.q per lane, one DPP
+// wave reduction each, pi = sigmoid((p.q) r - lse), r = rsqrt(mean(p^2) +
+// eps); the partial row is kept while the inter row arrives, then
+//   out = inter + pi (p - inter)
+// and one store of the row.  The query sits in LDS (bf16 pairs for the
+// v_dot2 path when the parameter is bf16, else fp32), read once per
+// workgroup.  Same arithmetic as merge_body; only the order of the row sums
+// differs.
+template <int NCH, bool QDOT2>
+__device__ __forceinline__ void merge_stream_body(const attnres_merge_params& P) {
+  constexpr int QF = QDOT2 ? 1 : NCH * 64 * 8;
+  constexpr int QB = QDOT2 ? NCH * 64 : 1;
+  __shared__ u32x4 qw_b[QB];
+  __shared__ float qw_f[QF];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  for (int i = tid; i < NCH * 64; i += blockDim.x) {
+    float t[8];
+    load_param<8>(P.query, (int64_t)i * 8, P.param_bf16, t);
+    if constexpr (QDOT2) {
+      qw_b[i] = u32x4{pack_bf16(t[0], t[1]), pack_bf16(t[2], t[3]), pack_bf16(t[4], t[5]), pack_bf16(t[6], t[7])};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qw_f[i * 8 + e] = t[e];
+    }
+  }
+  __syncthreads();
+
+  // 32-bit wave-uniform row counters (the host checks n_tokens < 2^31)
+  const uint32_t n_tok = (uint32_t)P.n_tokens;
+  const uint32_t wpb = __builtin_amdgcn_readfirstlane((uint32_t)P.block >> 6);
+  const uint32_t nw = gridDim.x * wpb;
+  uint32_t tok = blockIdx.x * wpb + wave;
+  if (tok >= n_tok) return;  // no barrier follows
+  const uint32_t rows = (n_tok - tok - 1) / nw + 1;
+  const uint64_t p0 = reinterpret_cast<uint64_t>(P.partial), i0 = reinterpret_cast<uint64_t>(P.inter);
+  const uint64_t o0 = reinterpret_cast<uint64_t>(P.out);
+  const uint64_t p_ld = (uint64_t)P.partial_ld * 2, i_ld = (uint64_t)P.inter_ld * 2, o_ld = (uint64_t)P.out_ld * 2;
+
+  // rows are read once: global loads with the non-temporal hint, as the
+  // routing kernels' source rows
+  auto load_row = [&](u32x4(&buf)[NCH], uint64_t base, uint64_t ld, uint32_t t) {
+    t = __builtin_amdgcn_readfirstlane(t);
+    const char* row = uniform_ptr(base + (uint64_t)t * ld);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) buf[c] = ldg_global<u32x4>(row + (uint32_t)(c * 1024 + lane * 16));
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  u32x4 pa[NCH], ib[NCH], ph[NCH];
+  load_row(pa, p0, p_ld, tok);
+  for (uint32_t i = 0; i < rows; ++i) {
+    const uint32_t tn = i + 1 < rows ? tok + nw : tok;  // past the last row: re-read a valid row
+    load_row(ib, i0, i_ld, tok);
+    const float lse = P.inter_lse[tok];
+    // ---- the partial row: sum(p^2), p.q, pi ----
+    asm volatile("; attnres merge stream partial");
+    float ss0 = 0.f, ss1 = 0.f, dt0 = 0.f, dt1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if constexpr (QDOT2) {
+        const u32x4 q = qw_b[c * 64 + lane];
+        ss0 = dot2_bf16(pa[c][0], pa[c][0], ss0);
+        dt0 = dot2_bf16(pa[c][0], q[0], dt0);
+        ss1 = dot2_bf16(pa[c][1], pa[c][1], ss1);
+        dt1 = dot2_bf16(pa[c][1], q[1], dt1);
+        ss0 = dot2_bf16(pa[c][2], pa[c][2], ss0);
+        dt0 = dot2_bf16(pa[c][2], q[2], dt0);
+        ss1 = dot2_bf16(pa[c][3], pa[c][3], ss1);
+        dt1 = dot2_bf16(pa[c][3], q[3], dt1);
+      } else {
+        const float* q = &qw_f[(c * 64 + lane) * 8];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float a = bf_lo(pa[c][w]), b = bf_hi(pa[c][w]);
+          ss0 = __builtin_fmaf(a, a, ss0);
+          dt0 = __builtin_fmaf(a, q[2 * w], dt0);
+          ss1 = __builtin_fmaf(b, b, ss1);
+          dt1 = __builtin_fmaf(b, q[2 * w + 1], dt1);
+        }
+      }
+    }
+    float ss = wave_sum_to_lane63(ss0 + ss1);
+    float dt = wave_sum_to_lane63(dt0 + dt1);
+    ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ss), 63));
+    dt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dt), 63));
+    const float inv = __builtin_amdgcn_rsqf(ss * P.inv_d + P.eps);
+    const float logit = dt * inv;
+    const float pi = 1.0f / (1.0f + __expf(-(logit - lse)));
+    if (lane == 0) {
+      if (P.logit) P.logit[tok] = logit;
+      if (P.inv_rms) P.inv_rms[tok] = inv;
+    }
+    // keep the partial row; its slot takes the next token's partial row
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) ph[c] = pa[c];
+    load_row(pa, p0, p_ld, tn);
+    // ---- the inter row: out = inter + pi (p - inter) ----
+    asm volatile("; attnres merge stream inter");
+    const __amdgpu_buffer_rsrc_t orr = row_rsrc(const_cast<char*>(uniform_ptr(o0 + (uint64_t)tok * o_ld)), NCH * 1024);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      u32x4 o;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float il = bf_lo(ib[c][w]), ih = bf_hi(ib[c][w]);
+        o[w] = pack_bf16(__builtin_fmaf(pi, bf_lo(ph[c][w]) - il, il), __builtin_fmaf(pi, bf_hi(ph[c][w]) - ih, ih));
+      }
+      st_row(orr, (uint32_t)(c * 1024 + lane * 16), o);
+    }
+    tok = __builtin_amdgcn_readfirstlane(tn);
+  }
+}
+
 
 // ------------------------------------------------------ stream body --
 //
@@ -2936,6 +3056,24 @@ ROUTE_S(16)
 
 MERGE_V(1)
 MERGE_V(2)
+// Row-per-wave merge: attnres_merge_stream_<qw>_c<NCH> (bf16 rows of NCH KiB;
+// qw: d2 = bf16 query on the v_dot2 path, fm = fp32 query), four waves per
+// workgroup.
+#define MERGE_STREAM(NCH)                                                                            \
+  extern "C" __global__ void __launch_bounds__(256) attnres_merge_stream_d2_c##NCH(attnres_merge_params P) { \
+    merge_stream_body<NCH, true>(P);                                                                 \
+  }                                                                                                  \
+  extern "C" __global__ void __launch_bounds__(256) attnres_merge_stream_fm_c##NCH(attnres_merge_params P) { \
+    merge_stream_body<NCH, false>(P);                                                                \
+  }
+MERGE_STREAM(1)
+MERGE_STREAM(2)
+MERGE_STREAM(3)
+MERGE_STREAM(4)
+MERGE_STREAM(5)
+MERGE_STREAM(6)
+MERGE_STREAM(7)
+MERGE_STREAM(8)
 #endif
 
 // Streaming kernels: attnres_stream_<in>_<qw>_c<NCH>_<plain|fused>, row = NCH KiB.

@@ -603,6 +603,63 @@ def test_phase1_batched_queries_and_phase2_merge(gpu):
     assert (err <= np.maximum(4e-2, 3 * bf16_ulp(full))).all()
 
 
+MERGE_CASES = [
+    # (hidden, rows, query dtype): row-per-wave kernel instances c1, c6, c8 and c4;
+    # fewer rows than one grid of waves, a single row, the fp32-query path
+    (512, 37, torch.bfloat16),
+    (3072, 2050, torch.bfloat16),
+    (4096, 300, torch.float32),
+    (2048, 1, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("d,rows,qdt", MERGE_CASES, ids=[f"D{c[0]}-N{c[1]}-{str(c[2])[6:]}" for c in MERGE_CASES])
+def test_merge_both_kernels_match_oracle(gpu, policy, d, rows, qdt):
+    # the phase-2 merge on the row-per-workgroup kernel and on the row-per-wave
+    # kernel (bf16 rows of whole KiB, policy "stream"), output and aux against
+    # the float64 oracle (kernels/phase_2.py:40-57)
+    g = torch.Generator(device=gpu).manual_seed(31 + d + rows)
+    partial = torch.randn((rows, d), generator=g, device=gpu).to(torch.bfloat16)
+    inter = (0.5 * torch.randn((rows, d), generator=g, device=gpu)).to(torch.bfloat16)
+    lse = torch.randn((rows,), generator=g, device=gpu)
+    q = (torch.randn((d,), generator=g, device=gpu) * 0.05).to(qdt)
+    merged, logit, inv = ops.merge(partial, q, inter, lse, 1e-5)
+    ref = O.merge(np64(partial), np64(q), np64(inter), np64(lse), 1e-5)
+    check_bf16(merged, ref["out"], f"merge {policy} D={d} N={rows}")
+    np.testing.assert_allclose(np64(logit), ref["logit"], rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(np64(inv), ref["inv_rms"], rtol=1e-5)
+
+
+def test_streaming_merge_matches_workgroup_merge_every_row(gpu):
+    # every element of every row at the 3B shape (32768 rows of 3072): the
+    # row-per-wave merge against the row-per-workgroup merge; they differ only
+    # in the order of the two row sums, so pi agrees to a few fp32 ulps and
+    # the outputs to one bf16 ulp plus 2^-16 of the larger input
+    n, d = 32768, 3072
+    g = torch.Generator(device=gpu).manual_seed(41)
+    partial = torch.randn((n, d), generator=g, device=gpu).to(torch.bfloat16)
+    inter = (0.5 * torch.randn((n, d), generator=g, device=gpu)).to(torch.bfloat16)
+    lse = torch.randn((n,), generator=g, device=gpu)
+    q = (torch.randn((d,), generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+    outs = []
+    for pol in (_capi.POLICY_STREAM, _capi.POLICY_WORKGROUP):
+        prev = _capi.set_kernel_policy(pol)
+        try:
+            with torch.no_grad():
+                outs.append(ops.merge_call(partial, q, inter, lse, 1e-5).float())
+        finally:
+            _capi.set_kernel_policy(prev)
+    torch.cuda.synchronize()
+    a, b = outs
+    xmax = torch.maximum(partial.abs(), inter.abs()).float()
+    tol = torch.exp2(torch.floor(torch.log2(torch.clamp(b.abs(), min=2.0**-126))) - 7) + 2.0**-16 * xmax
+    excess = ((a - b).abs() / tol).max().item()
+    same = (a == b).float().mean().item()
+    print(f"merge stream vs workgroup: max |diff| / tol {excess:.3f}, {same:.5f} of elements equal", flush=True)
+    assert excess <= 1.0
+    assert same >= 0.99
+
+
 # ------------------------------------------------------ HIP graphs --
 
 
