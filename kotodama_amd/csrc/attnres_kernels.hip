@@ -1156,7 +1156,9 @@ __device__ __forceinline__ void merge_stream_body(const attnres_merge_params& P)
   const uint32_t nw = gridDim.x * wpb;
   uint32_t tok = blockIdx.x * wpb + wave;
   if (tok >= n_tok) return;  // no barrier follows
-  const uint32_t rows = (n_tok - tok - 1) / nw + 1;
+  // wave-uniform (the division is expanded on the VALU): a loop bound in a
+  // VGPR would make the row loop divergent
+  const uint32_t rows = __builtin_amdgcn_readfirstlane((n_tok - tok - 1) / nw + 1);
   const uint64_t p0 = reinterpret_cast<uint64_t>(P.partial), i0 = reinterpret_cast<uint64_t>(P.inter);
   const uint64_t o0 = reinterpret_cast<uint64_t>(P.out);
   const uint64_t p_ld = (uint64_t)P.partial_ld * 2, i_ld = (uint64_t)P.inter_ld * 2, o_ld = (uint64_t)P.out_ld * 2;
@@ -1171,11 +1173,15 @@ __device__ __forceinline__ void merge_stream_body(const attnres_merge_params& P)
     __builtin_amdgcn_sched_barrier(0);
   };
   u32x4 pa[NCH], ib[NCH], ph[NCH];
+  // The lse of a token is requested with its partial row, a row ahead of its
+  // use: a scalar load counts against the same wait counter as the LDS reads
+  // of the query, so one requested just before use would stall every row.
   load_row(pa, p0, p_ld, tok);
+  float lse_next = P.inter_lse[tok];
   for (uint32_t i = 0; i < rows; ++i) {
     const uint32_t tn = i + 1 < rows ? tok + nw : tok;  // past the last row: re-read a valid row
+    const float lse = lse_next;
     load_row(ib, i0, i_ld, tok);
-    const float lse = P.inter_lse[tok];
     // ---- the partial row: sum(p^2), p.q, pi ----
     asm volatile("; attnres merge stream partial");
     float ss0 = 0.f, ss1 = 0.f, dt0 = 0.f, dt1 = 0.f;
@@ -1218,6 +1224,7 @@ __device__ __forceinline__ void merge_stream_body(const attnres_merge_params& P)
 #pragma unroll
     for (int c = 0; c < NCH; ++c) ph[c] = pa[c];
     load_row(pa, p0, p_ld, tn);
+    lse_next = P.inter_lse[tn];
     // ---- the inter row: out = inter + pi (p - inter) ----
     asm volatile("; attnres merge stream inter");
     const __amdgpu_buffer_rsrc_t orr = row_rsrc(const_cast<char*>(uniform_ptr(o0 + (uint64_t)tok * o_ld)), NCH * 1024);
