@@ -276,6 +276,19 @@ def bwd_kernel_name(s: int, tokens: int, hidden: int, dtype) -> str:
     return buf.value.decode()
 
 
+def merge_kernel_name(tokens: int, hidden: int) -> str:
+    """Symbol of the kernel a bf16 merge call launches (C-ABI name query)."""
+    import ctypes
+
+    from kotodama_amd import _capi
+
+    buf = ctypes.create_string_buffer(128)
+    code = _capi.DTYPE_BF16
+    _capi.check("attnres_merge_kernel_name",
+                _capi.lib().attnres_merge_kernel_name(tokens, hidden, code, code, code, buf, 128))
+    return buf.value.decode()
+
+
 def bwdq_kernel_name(s: int, hidden: int, queries: int) -> str:
     """Symbol of the first kernel of the bf16 batched-query backward for this shape."""
     import ctypes
@@ -603,7 +616,7 @@ def main() -> int:
             "tokens_per_s": round(w2.tokens / (ms_per_step * 1e-3), 1),
             "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                         "kernel": "attnres_merge_bf_bf_v2 (phase-2 merge, 3 rows per token)",
+                         "kernel": merge_kernel_name(w2.tokens, w2.hidden) + " (phase-2 merge, 3 rows per token)",
                          "algorithmic_bytes": merge_bytes, "avg_ms": round(merge_ms, 4)},
             "phase1_deepest": {"kernel": kernel_name(7, w2.tokens, w2.hidden, w2.dtype, 8) + " (Q=8)",
                                "algorithmic_bytes": p1_bytes,
@@ -621,7 +634,7 @@ def main() -> int:
         ms_per_step = elapsed * 1e3 / args.steps
         gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
         achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-        name = bwd_kernel_name(dominant, w.tokens, w.hidden, w.dtype) + " (+ attnres_reduce_dqw_stage, attnres_reduce_dqw)"
+        name = bwd_kernel_name(dominant, w.tokens, w.hidden, w.dtype) + " (+ attnres_reduce_dqw_cols)"
         traffic, traffic_src = load_traffic(f"bwd_{args.workload}_s{dominant}")
         print(json.dumps({
             "metric": "AttnRes routing backward achieved HBM GB/s",

@@ -140,6 +140,16 @@ int attnres_merge_fwd(const void* partial, int64_t num_tokens, int hidden, int p
                       void* out, float* logit, float* inv_rms, void* stream);
 
 /*
+ * Symbol name of the kernel attnres_merge_fwd launches for these arguments
+ * (the row-per-wave attnres_merge_stream_* or the row-per-workgroup
+ * attnres_merge_*), for matching profiler output; written NUL-terminated into
+ * buf.  Loads the code object on the current device.  No counterpart in the
+ * reference.
+ */
+int attnres_merge_kernel_name(int64_t num_tokens, int hidden, int partial_dtype, int param_dtype, int inter_dtype,
+                              char* buf, int buf_len);
+
+/*
  * One routing point of the block schedule over a preallocated block arena,
  * with the partial-block update fused in.  The arena holds num_slots slots of
  * (num_tokens, hidden) rows, slot s at arena + s*slot_stride elements; slots

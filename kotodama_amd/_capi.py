@@ -49,6 +49,7 @@ EXPORTS = (
     "attnres_init",
     "attnres_route_fwd",
     "attnres_merge_fwd",
+    "attnres_merge_kernel_name",
     "attnres_block_step",
     "attnres_route_bwd_workspace_size",
     "attnres_route_bwd",
@@ -195,6 +196,10 @@ _SIGNATURES = {
     "attnres_route_bwd_queries_workspace_size": ([_c_i64, _c_int, _c_int, _c_int, ctypes.POINTER(_c_i64)], _c_int),
     "attnres_route_bwd_kernel_name": (
         [_c_int, _c_i64, _c_int, _c_int, _c_int, ctypes.c_char_p, _c_int],
+        _c_int,
+    ),
+    "attnres_merge_kernel_name": (
+        [_c_i64, _c_int, _c_int, _c_int, _c_int, ctypes.c_char_p, _c_int],
         _c_int,
     ),
     "attnres_route_bwd_queries_kernel_name": (

@@ -683,6 +683,36 @@ void kernel_name_of(const RouteChoice& ch, int num_sources, int num_queries, boo
 
 // Shared validation + launch of the route kernel.  `mode`/`delta` are the
 // fused partial-update inputs of attnres_block_step.
+// The kernel choice of one merge call, shared by the launch and the name
+// query: the row-per-wave kernel for bf16 rows of whole 1 KiB chunks (at most
+// kStreamMaxChunks) over enough rows (the routing kernels' policy and
+// threshold), one workgroup of four waves per CU; else one workgroup per row.
+struct MergeChoice {
+  bool stream = false;
+  int nch = 0;    // row KiB (row-per-wave kernel)
+  int v = 0;      // chunks per thread (row-per-workgroup kernel); 0: no launch shape
+  int block = 0;  // threads per workgroup
+};
+MergeChoice plan_merge(int64_t num_tokens, int hidden, int partial_dtype, int inter_dtype, const DeviceState& st) {
+  MergeChoice ch;
+  const bool pbf = partial_dtype == ATTNRES_DTYPE_BF16, ibf = inter_dtype == ATTNRES_DTYPE_BF16;
+  const int64_t row_bytes = (int64_t)hidden * 2;
+  ch.nch = (int)(row_bytes / 1024);
+  const bool stream_shape = tuning().merge_stream != 0 && pbf && ibf && row_bytes % 1024 == 0 && ch.nch >= 1 &&
+                            ch.nch <= kStreamMaxChunks && num_tokens < (int64_t)1 << 31;
+  const int policy = g_policy.load(std::memory_order_relaxed);
+  const int want_stream = policy == ATTNRES_POLICY_STREAM      ? 1
+                          : policy == ATTNRES_POLICY_WORKGROUP ? 0
+                                                               : tuning().stream;
+  ch.stream = stream_shape && (want_stream == 1 || (want_stream < 0 && num_tokens >= tuning().stream_min_tokens));
+  if (ch.stream) {
+    ch.block = 64 * (tuning().stream_waves > 0 ? tuning().stream_waves : kStreamWaves);
+  } else {
+    ch.v = pick_v(num_tokens, hidden / (pbf ? 8 : 4), st.num_cus, &ch.block);
+  }
+  return ch;
+}
+
 int route_launch(const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
                  int src_dtype, const void* query, const void* gain, int num_queries, int param_dtype, float eps,
                  void* out, int out_dtype, int64_t out_ld, int64_t out_qstride, float* weights, float* lse,
@@ -884,6 +914,30 @@ int attnres_route_kernel_name(int num_sources, int64_t num_tokens, int hidden, i
   return ATTNRES_OK;
 }
 
+int attnres_merge_kernel_name(int64_t num_tokens, int hidden, int partial_dtype, int param_dtype, int inter_dtype,
+                              char* buf, int buf_len) {
+  if (buf == nullptr || buf_len < 1) return fail(ATTNRES_ERR_ARG, "no output buffer");
+  if (!valid_dtype(partial_dtype) || !valid_dtype(param_dtype) || !valid_dtype(inter_dtype))
+    return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (num_tokens < 1 || hidden <= 0) return fail(ATTNRES_ERR_ARG, "bad shape");
+  const int vec = partial_dtype == ATTNRES_DTYPE_BF16 ? 8 : 4;
+  if (hidden % vec != 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d is not a multiple of %d", hidden, vec);
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  const MergeChoice ch = plan_merge(num_tokens, hidden, partial_dtype, inter_dtype, *st);
+  if (ch.stream) {
+    snprintf(buf, (size_t)buf_len, "attnres_merge_stream_%s_c%d", param_dtype == ATTNRES_DTYPE_BF16 ? "d2" : "fm",
+             ch.nch);
+  } else if (ch.v != 0) {
+    snprintf(buf, (size_t)buf_len, "attnres_merge_%s_%s_v%d", partial_dtype == ATTNRES_DTYPE_BF16 ? "bf" : "f32",
+             inter_dtype == ATTNRES_DTYPE_BF16 ? "bf" : "f32", ch.v);
+  } else {
+    buf[0] = '\0';
+  }
+  return ATTNRES_OK;
+}
+
 int attnres_route_bwd_kernel_name(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int grad_out_dtype,
                                   char* buf, int buf_len) {
   if (buf == nullptr || buf_len < 1) return fail(ATTNRES_ERR_ARG, "no output buffer");
@@ -980,30 +1034,14 @@ int attnres_merge_fwd(const void* partial, int64_t num_tokens, int hidden, int p
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
-  // The row-per-wave kernel for bf16 rows of whole 1 KiB chunks over enough
-  // rows (the routing kernels' policy and threshold), one workgroup of four
-  // waves per CU; else one workgroup per row.
-  const int64_t row_bytes = (int64_t)hidden * 2;
-  const int nch = (int)(row_bytes / 1024);
-  const bool stream_shape = tuning().merge_stream != 0 && pbf && ibf && row_bytes % 1024 == 0 && nch >= 1 &&
-                            nch <= kStreamMaxChunks && num_tokens < (int64_t)1 << 31;
-  const int policy = g_policy.load(std::memory_order_relaxed);
-  const int want_stream = policy == ATTNRES_POLICY_STREAM      ? 1
-                          : policy == ATTNRES_POLICY_WORKGROUP ? 0
-                                                               : tuning().stream;
-  const bool use_stream =
-      stream_shape && (want_stream == 1 || (want_stream < 0 && num_tokens >= tuning().stream_min_tokens));
-  int block = 0, v = 0;
+  const MergeChoice ch = plan_merge(num_tokens, hidden, partial_dtype, inter_dtype, *st);
+  if (!ch.stream && ch.v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
+  const bool use_stream = ch.stream;
+  const int block = ch.block;
   hipFunction_t f = nullptr;
   int bpc = 1;
-  if (use_stream) {
-    block = 64 * (tuning().stream_waves > 0 ? tuning().stream_waves : kStreamWaves);
-    rc = get_merge_stream(*st, param_dtype == ATTNRES_DTYPE_BF16, nch, &f);
-  } else {
-    v = pick_v(num_tokens, nchunk, st->num_cus, &block);
-    if (v == 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d has no launch shape", hidden);
-    rc = get_merge(*st, pbf, ibf, v, block, &f, &bpc);
-  }
+  rc = use_stream ? get_merge_stream(*st, param_dtype == ATTNRES_DTYPE_BF16, ch.nch, &f)
+                  : get_merge(*st, pbf, ibf, ch.v, block, &f, &bpc);
   if (rc != ATTNRES_OK) return rc;
 
   attnres_merge_params P;

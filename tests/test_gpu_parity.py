@@ -630,6 +630,33 @@ def test_merge_both_kernels_match_oracle(gpu, policy, d, rows, qdt):
     np.testing.assert_allclose(np64(inv), ref["inv_rms"], rtol=1e-5)
 
 
+def merge_kernel(n, d, qdt=torch.bfloat16):
+    import ctypes
+
+    buf = ctypes.create_string_buffer(128)
+    code = _capi.DTYPE_BF16
+    _capi.check("attnres_merge_kernel_name",
+                _capi.lib().attnres_merge_kernel_name(n, d, code, ops.dtype_code(qdt), code, buf, 128))
+    return buf.value.decode()
+
+
+def test_merge_kernel_name_follows_the_launch_choice(gpu):
+    # the name query and the launch share one choice: the row-per-wave kernel
+    # for bf16 rows of whole KiB over >= 2048 rows (or always under the stream
+    # policy), the row-per-workgroup kernel otherwise (or always under the
+    # workgroup policy)
+    assert merge_kernel(32768, 3072) == "attnres_merge_stream_d2_c6"
+    assert merge_kernel(32768, 4096, torch.float32) == "attnres_merge_stream_fm_c8"
+    assert merge_kernel(1000, 3072).startswith("attnres_merge_bf_bf_v")
+    assert merge_kernel(32768, 3080).startswith("attnres_merge_bf_bf_v")  # rows not whole KiB
+    for pol, want in ((_capi.POLICY_STREAM, "attnres_merge_stream_d2_c6"), (_capi.POLICY_WORKGROUP, "attnres_merge_bf_bf_v")):
+        prev = _capi.set_kernel_policy(pol)
+        try:
+            assert merge_kernel(1000 if pol == _capi.POLICY_STREAM else 32768, 3072).startswith(want)
+        finally:
+            _capi.set_kernel_policy(prev)
+
+
 def test_streaming_merge_matches_workgroup_merge_every_row(gpu):
     # every element of every row at the 3B shape (32768 rows of 3072): the
     # row-per-wave merge against the row-per-workgroup merge; they differ only
