@@ -30,7 +30,9 @@
 //     mix sources on the matrix cores (v_mfma_f32_4x4x4_16b_bf16, weights as
 //     bf16 hi + lo), since Q queries turn the mix into a small product.
 //   * attnres_merge_*   the phase-2 merge of a running block into a phase-1
-//     result, one workgroup per row.
+//     result: attnres_merge_stream_* one wave per row (the partial and inter
+//     rows stream one row per pipeline slot), attnres_merge_<p>_<i>_v* one
+//     workgroup per row.
 //   * attnres_route_bwd_* / _mq_ / _mqg_ / _dqw* / merge_bwd / reduce_dqw*:
 //     the backward of routing and merge (source, query and gain gradients;
 //     the query gradient summed over rows in a fixed order), the batched-
@@ -2678,7 +2680,7 @@ __device__ __forceinline__ void store_f32_chunk(__amdgpu_buffer_rsrc_t r, int ch
 //   dp = pi G + gl r q - gl logit r^2 / D p,   dq = sum over rows of gl r p.
 // One workgroup per row as merge_body; the query gradient is accumulated in
 // registers and written as this workgroup's partial (reduced by
-// attnres_reduce_dqw_stage / attnres_reduce_dqw).
+// attnres_reduce_dqw_cols, or attnres_reduce_dqw_stage then attnres_reduce_dqw).
 template <int V, bool PBF16, bool IBF16>
 __device__ __forceinline__ void merge_bwd_body(const attnres_merge_bwd_params& P) {
   using C = Chunk<PBF16>;
@@ -3129,7 +3131,8 @@ STREAM_TYPES(8)
 #endif
 
 // Backward: attnres_route_bwd_<in>_g<grad_out>_s<S>_v<V>; column reduce:
-// attnres_reduce_dqw_stage + attnres_reduce_dqw.
+// attnres_reduce_dqw_cols (one launch, up to four queries) or
+// attnres_reduce_dqw_stage + attnres_reduce_dqw (two).
 // Waves per SIMD the backward kernels are compiled for: 4 (<= 128 VGPRs) keeps
 // two workgroups of up to 8 waves (rows up to 4096 bf16 / 2048 fp32 elements)
 // resident per CU for S <= 9; S = 9 bf16 spills a few dwords under that cap.
