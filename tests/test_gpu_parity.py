@@ -610,6 +610,10 @@ MERGE_CASES = [
     (3072, 2050, torch.bfloat16),
     (4096, 300, torch.float32),
     (2048, 1, torch.bfloat16),
+    (1536, 4099, torch.bfloat16),  # c3, a prime row count: ragged last rows per wave
+    (2560, 997, torch.float32),    # c5, fp32 query
+    (3584, 1031, torch.bfloat16),  # c7
+    (1024, 5, torch.bfloat16),     # c2, fewer rows than one workgroup's waves
 ]
 
 
