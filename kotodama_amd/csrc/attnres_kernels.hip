@@ -2759,12 +2759,19 @@ __device__ __forceinline__ void merge_bwd_body(const attnres_merge_bwd_params& P
     ph ^= 1;
     const float r = __builtin_amdgcn_rsqf(tss * P.inv_d + P.eps);
     const float logit = tdt * r;
-    const float pi = 1.0f / (1.0f + __expf(-(logit - P.inter_lse[tok])));
-    const float gl = pi * (1.0f - pi) * tga;
+    // pi = sigmoid(z) and 1 - pi = sigmoid(-z), each from its own exponential:
+    // as pi -> 1, 1.0 - pi (the reference's form, kernels/phase_2.py:141) or
+    // G - pi G keeps none of the small values of 1 - pi below fp32's spacing
+    // near 1, which dinter = (1 - pi) G and pi (1 - pi) need
+    const float z = logit - P.inter_lse[tok];
+    const float pi = 1.0f / (1.0f + __expf(-z));
+    const float qi = 1.0f / (1.0f + __expf(z));
+    const float gl = pi * qi * tga;
     if (tid == 0 && P.grad_lse) P.grad_lse[tok] = -gl;
     const float cq = uniform_f32(gl * r);
     const float cp = uniform_f32(-gl * logit * r * r * P.inv_d);
     const float pu = uniform_f32(pi);
+    const float qu = uniform_f32(qi);
 
     char* gprow = reinterpret_cast<char*>(P.grad_partial) + tok * (int64_t)P.d * C::BYTES;
     char* girow = reinterpret_cast<char*>(P.grad_inter) + tok * (int64_t)P.d * IB;
@@ -2778,7 +2785,7 @@ __device__ __forceinline__ void merge_bwd_body(const attnres_merge_bwd_params& P
       for (int e = 0; e < VEC; ++e) {
         const float v = C::elem(p[k], e);
         dp[e] = __builtin_fmaf(cp, v, __builtin_fmaf(cq, qw[k][e], pu * gv[k][e]));
-        di[e] = gv[k][e] - pu * gv[k][e];
+        di[e] = qu * gv[k][e];
         dqa[k][e] = __builtin_fmaf(cq, v, dqa[k][e]);
       }
       store_f32_chunk<PBF16, VEC>(prs, chunk[k], dp);

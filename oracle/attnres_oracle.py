@@ -194,13 +194,17 @@ def merge_backward(partial, q, inter, inter_lse, eps: float, grad_out) -> dict:
     D = p.shape[-1]
     r = 1.0 / np.sqrt(np.mean(p * p, axis=-1) + eps)
     logit = (p @ qv) * r
-    pi = 1.0 / (1.0 + np.exp(-(logit - lse)))
+    # pi and 1 - pi each from its own exponential (1 - pi = sigmoid(lse - logit)):
+    # 1.0 - pi cancels to nothing as pi -> 1, where dinter and pi (1 - pi) are small
+    with np.errstate(over="ignore"):
+        pi = 1.0 / (1.0 + np.exp(-(logit - lse)))
+        qi = 1.0 / (1.0 + np.exp(logit - lse))
     a = np.sum(g * (p - it), axis=-1)
-    gl = pi * (1.0 - pi) * a
+    gl = pi * qi * a
     dp = pi[..., None] * g + gl[..., None] * (r[..., None] * qv - (logit * r * r / D)[..., None] * p)
     return {
         "dpartial": dp,
-        "dinter": (1.0 - pi)[..., None] * g,
+        "dinter": qi[..., None] * g,
         "dlse": -gl,
         "dq": np.einsum("n,nd->d", (gl * r).reshape(-1), p.reshape(-1, D)),
     }

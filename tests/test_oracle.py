@@ -358,6 +358,27 @@ def test_merge_backward_matches_finite_differences():
     np.testing.assert_allclose(b["dlse"], num(lse, lambda x: loss(ll=x)), rtol=1e-6, atol=1e-8)
 
 
+def test_merge_backward_keeps_small_one_minus_pi():
+    # a saturated merge (logit - lse = z >> 1): 1 - pi = 1 / (1 + e^z) and
+    # pi (1 - pi) = e^z / (1 + e^z)^2 in closed form, far below float64's
+    # spacing near 1 at z = 60, where 1.0 - pi would be exactly 0
+    rng = np.random.default_rng(64)
+    D, eps = 8, 1e-6
+    p = rng.standard_normal((1, D))
+    q = rng.standard_normal(D)
+    it = rng.standard_normal((1, D))
+    G = rng.standard_normal((1, D))
+    logit = O.merge(p, q, it, np.zeros(1), eps)["logit"]
+    for z in (5.0, 30.0, 60.0):
+        lse = logit - z
+        b = O.merge_backward(p, q, it, lse, eps, G)
+        one_minus_pi = 1.0 / (1.0 + np.exp(z))
+        np.testing.assert_allclose(b["dinter"], one_minus_pi * G, rtol=1e-12)
+        a = np.sum(G * (p - it))
+        np.testing.assert_allclose(b["dlse"], -np.exp(z) / (1.0 + np.exp(z)) ** 2 * a, rtol=1e-12)
+        assert np.all(b["dinter"] != 0.0)
+
+
 def test_merge_backward_equals_routing_backward_over_one_more_source():
     # merge(p, phase1(C)) == route(C + [p]), so the gradients w.r.t. p and the
     # query agree with the routing backward's (the sources C enter through inter/lse)
