@@ -28,6 +28,8 @@ backward of the same routing calls instead (attnres_route_bwd on preallocated
 gradient buffers: (2S+1) * B*T*D * 2 algorithmic bytes per call — sources and
 dL/dout read, source gradients written; for cfg2serve the batched-query
 backward of each phase-1 call, (3S+Q) rows, and the merge backward, 5 rows).
+``--workload mall`` checks what the 256 MB last-level cache serves of a call's
+bytes (the dominant calls back to back vs after other memory traffic).
 ``--gpus`` above 1 exits: this build measures one GPU.
 """
 
@@ -52,6 +54,8 @@ WORKLOAD_TEXT = {
     "cfg4": "8B decode step: T=1, B=256, D=4096, 65 fused block steps (S=1..9) in one HIP graph, bf16",
     "cfg5": "3B data-driven blocks {0,3,7,12,18,23}: D=3072, B=2, T=4096, 57 calls S=1..7 (sum S=267), BOS x20, bf16",
     "copy": "calibration: torch device copy of 1 GiB (bf16), the plain copy kernel that scales rocprof byte counters",
+    "mall": "cache check: the dominant cfg2 (S=8) and cfg3 (S=9) calls back to back vs after a 512 MiB write, "
+    "a 512 MiB read, or a call on a second pool",
     "cfg2serve": "3B serving two-phase routing (serve.py:113-164): 7 blocks of 8 sublayers, one batched phase-1 call "
     "(Q=8, S=1..7) + 7 phase-2 merges per block, final phase 1 (S=8); D=3072, B=8, T=4096, bf16",
 }
@@ -522,6 +526,64 @@ def bench_copy(steps: int, warmup: int, dev):
     return time.perf_counter() - t0, 2 * n * 2
 
 
+def bench_mall(steps: int, warmup: int, dev) -> dict:
+    """Does the 256 MB last-level cache (MALL) serve part of a call's bytes?
+
+    The dominant call of cfg2 (S=8) and of cfg3 (S=9) timed with HIP events,
+    in alternating rounds, four ways: back to back on one pool (consecutive
+    calls of one block read the same sources); with a 512 MiB write between
+    launches; with a 512 MiB read between launches (evicts without leaving
+    dirty lines); and alternating between two pools of the same shape, so
+    every call follows one that touched other memory, as in the model where
+    attention and MLP sublayers run between routing calls.
+    """
+    import torch
+
+    from kotodama_amd import ops, workloads
+
+    flush = torch.ones(256 << 20, dtype=torch.bfloat16, device=dev)  # 512 MiB
+    modes = ("back_to_back", "write_flushed", "read_flushed", "alternating_pools")
+    out = {}
+    for name in ("cfg2", "cfg3"):
+        w = workloads.get(name)
+        pools = [workloads.make_pool(w, dev, seed=2), workloads.make_pool(w, dev, seed=3)]
+        q, gn = workloads.make_params(w, dev, seed=2, count=len(w.calls))
+        s = max(w.calls)
+        j = w.calls.index(s)
+        times = {m: [] for m in modes}
+        with torch.inference_mode():
+            for rnd in range(4):
+                for mode in modes:
+                    ev = []
+                    for i in range(warmup + steps):
+                        if mode == "write_flushed":
+                            flush.fill_(float(1 + (rnd + i) % 7))
+                        elif mode == "read_flushed":
+                            flush.amax()
+                        pool = pools[i % 2] if mode == "alternating_pools" else pools[0]
+                        e0 = torch.cuda.Event(enable_timing=True)
+                        e1 = torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                        ops.route_call(pool, s, q[j], gn[j], w.eps, w.dtype)
+                        e1.record()
+                        if i >= warmup:
+                            ev.append((e0, e1))
+                    torch.cuda.synchronize()
+                    times[mode] += [a.elapsed_time(b) for a, b in ev]
+        nbytes = w.call_bytes(s)
+        rec = {"kernel": kernel_name(s, w.tokens, w.hidden, w.dtype), "algorithmic_bytes": nbytes,
+               "launches_each": steps * 4}
+        base = statistics.median(times["back_to_back"])
+        for mode, ts in times.items():
+            med = statistics.median(ts)
+            rec[mode] = {"median_us": round(med * 1e3, 2), "mean_us": round(statistics.mean(ts) * 1e3, 2),
+                         "GB/s": round(nbytes / (med * 1e-3) / 1e9, 1), "vs_back_to_back": round(med / base, 4)}
+        out[f"{name}_s{s}"] = rec
+        del pools, q, gn
+        torch.cuda.empty_cache()
+    return out
+
+
 def secondary_cfg3(steps: int, warmup: int, dev) -> dict:
     """The 8B prefill shape (cfg3: S=9, D=4096, B=4, T=4096, 8 calls) measured in the same run as cfg2."""
     from kotodama_amd import workloads
@@ -563,6 +625,10 @@ def main() -> int:
         ms = elapsed * 1e3 / args.steps
         print(json.dumps({"workload": WORKLOAD_TEXT["copy"], "bytes_read": nbytes // 2, "bytes_written": nbytes // 2,
                           "ms_per_copy": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return 0
+    if args.workload == "mall":
+        print(json.dumps({"workload": WORKLOAD_TEXT["mall"], "steps": args.steps, "warmup": args.warmup,
+                          **bench_mall(args.steps, args.warmup, dev)}), flush=True)
         return 0
     if args.workload == "cfg2serve" and args.pass_ == "bwd":
         elapsed, step_bytes, deep_ms, deep_bytes = bench_serve_backward(args.steps, args.warmup, dev)
