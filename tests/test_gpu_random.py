@@ -170,3 +170,111 @@ def test_random_batched_queries_forward_backward(gpu, seed):
     check_grad(buf.grad.reshape(S, N, D), dx, torch.bfloat16, f"seed {seed} dsources")
     if with_gain:
         check_grad(gain.grad, dgain, torch.bfloat16, f"seed {seed} dgain")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_block_arena_forward(gpu, seed):
+    # the stack-free caller (fused block steps over one arena): random layer
+    # count and boundary set (with or without layer 0), arena dtype, width,
+    # rows, gains and kernel policy; every routing point, the committed blocks
+    # and the final partial against the oracle's caller loop
+    from kotodama_amd.engine import AttnResRouter
+    from kotodama_amd.schedule import AttnResSchedule
+
+    rng = np.random.default_rng(7000 + seed)
+    dtype = [torch.bfloat16, torch.float32][int(rng.integers(2))]
+    L = int(rng.integers(1, 9))
+    bounds = sorted(int(b) for b in rng.choice(L, size=int(rng.integers(0, L + 1)), replace=False))
+    vec = 8 if dtype == torch.bfloat16 else 4
+    D = vec * int(rng.integers(8, (8192 if dtype == torch.bfloat16 else 4096) // vec + 1))
+    if rng.integers(2):  # half the cases on widths the row-per-wave kernels take
+        D = (512 if dtype == torch.bfloat16 else 256) * int(rng.integers(1, 9))
+    sched = AttnResSchedule.build(L, boundaries=bounds)
+    N = _rows(rng, D * sum(sched.active_counts) // 4)
+    with_gain = bool(rng.integers(2))
+    pol = _policy(rng)
+    print(f"random arena seed={seed}: {dtype} L={L} boundaries={bounds} D={D} N={N} gain={with_gain} policy={pol}",
+          flush=True)
+    g = torch.Generator(device="cpu").manual_seed(8000 + seed)
+    P = sched.num_points
+    embed = torch.randn(N, D, generator=g).to(dtype).to(gpu)
+    deltas = (torch.randn(2 * L, N, D, generator=g) * 0.5).to(dtype).to(gpu)
+    q = (torch.randn(P, D, generator=g) * [0.05, 0.5][int(rng.integers(2))]).to(dtype).to(gpu)
+    gn = [(1 + 0.1 * torch.randn(D, generator=g)).to(dtype).to(gpu) if with_gain else None for _ in range(P)]
+    router = AttnResRouter(sched, list(q), gn, 1e-5)
+    outs = []
+
+    def sublayer(j, h):
+        outs.append(h.clone())
+        return deltas[j]
+
+    def run():
+        arena = router.new_arena((N,), D, dtype, gpu)
+        outs.append(router.forward(embed, sublayer, arena=arena))
+        torch.cuda.synchronize()
+        return arena
+
+    arena = _with_policy(pol, run)
+    pd = "bf16" if dtype == torch.bfloat16 else "f32"
+    qws = [O.fold_query(np64(q[j]), np64(gn[j]) if with_gain else None, pd) for j in range(P)]
+    ref = O.block_forward(np64(embed), [np64(deltas[j]) for j in range(2 * L)], qws, 1e-5, L, set(bounds), dtype=pd)
+    check = check_bf16 if dtype == torch.bfloat16 else check_f32
+    assert len(outs) == P and arena.n_committed == len(bounds)
+    for j in range(P):
+        check(outs[j], ref["outs"][j], f"seed {seed} point {j}")
+    for b in range(len(bounds)):
+        assert np.array_equal(np64(arena.committed[b]), ref["committed"][b]), f"seed {seed} committed {b}"
+    assert np.array_equal(np64(arena.partial), ref["partial"]), f"seed {seed} partial"
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_list_routing_weights_and_backward(gpu, seed):
+    # list routing over separate allocations in a random order (the pointer-
+    # table kernel instance when they are not equally spaced), with the
+    # routing weights and lse requested, and its backward
+    rng = np.random.default_rng(9000 + seed)
+    dtype = [torch.bfloat16, torch.float32][int(rng.integers(2))]
+    vec = 8 if dtype == torch.bfloat16 else 4
+    S = int(rng.integers(1, 13))
+    D = vec * int(rng.integers(8, (8192 if dtype == torch.bfloat16 else 4096) // vec + 1))
+    if rng.integers(2):
+        D = (512 if dtype == torch.bfloat16 else 256) * int(rng.integers(1, 9))
+    N = _rows(rng, 2 * S * D)
+    want_weights = bool(rng.integers(2))
+    pol = _policy(rng)
+    print(f"random list seed={seed}: {dtype} S={S} D={D} N={N} weights={want_weights} policy={pol}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(10000 + seed)
+    srcs = [(torch.randn(N, D, generator=g) * float(np.exp(rng.uniform(np.log(0.25), np.log(4.0)))))
+            .to(dtype).to(gpu).requires_grad_(True) for _ in range(S)]
+    lst = [srcs[i] for i in rng.permutation(S)]
+    query = (torch.randn(D, generator=g) * 0.2).to(dtype).to(gpu).requires_grad_(True)
+    gain = (1 + 0.1 * torch.randn(D, generator=g)).to(dtype).to(gpu).requires_grad_(True)
+    G = torch.randn(N, D, generator=g).to(torch.bfloat16).float().to(gpu)
+    GL = torch.randn(N, generator=g).to(gpu)
+
+    def run():
+        out, weights, lse, _, _ = ops.route_list(lst, query, gain, 1e-5, dtype, want_weights, False)
+        loss = (out.float() * G).sum()
+        if want_weights:
+            loss = loss + (lse.reshape(-1) * GL).sum()
+        loss.backward()
+        torch.cuda.synchronize()
+        return out, weights, lse
+
+    out, weights, lse = _with_policy(pol, run)
+    pd = "bf16" if dtype == torch.bfloat16 else "f32"
+    qw = O.fold_query(np64(query), np64(gain), pd)
+    x = np.stack([np64(t) for t in lst])
+    r = O.route(x, qw, 1e-5)
+    if dtype == torch.bfloat16:
+        check_bf16(out.reshape(N, D), r["out"][0], f"seed {seed} out")
+    else:
+        check_f32(out.reshape(N, D), r["out"][0], f"seed {seed} out")
+    if want_weights:
+        np.testing.assert_allclose(np64(weights).reshape(S, N), r["weights"][0], atol=1e-5)
+        np.testing.assert_allclose(np64(lse).reshape(N), r["lse"][0], atol=2e-5, rtol=1e-6)
+    b = O.route_backward(x, qw, 1e-5, np64(G), np64(GL) if want_weights else None)
+    for k, t in enumerate(lst):
+        check_grad(t.grad, b["dx"][k], dtype, f"seed {seed} dsource {k}")
+    check_grad(query.grad, b["dqw"] * np64(gain), dtype, f"seed {seed} dquery")
+    check_grad(gain.grad, b["dqw"] * np64(query), dtype, f"seed {seed} dgain")
