@@ -1,4 +1,4 @@
-"""Routing weights from trained checkpoints (§ real-weight loading).
+"""Routing weights from trained checkpoints (real-weight loading).
 
 The reference loads whole models from ``.pt`` checkpoints
 (``serve.py:186-232``; ``src/eval/model_loader.py:109-199``): the file is
