@@ -606,22 +606,20 @@ void choose_qg(RouteChoice& ch, int num_sources, int num_queries, int hidden, in
   if (lds + kQgStaticLds <= (size_t)max_lds) ch.qg_lds = lds;
 }
 
-// Waves per workgroup of the streaming kernels (one workgroup per CU).  From
-// S = 6 over enough rows three waves run faster than four (3B shape, 32768
-// rows: S = 8 81.6% -> 85.3% of peak, S = 7 81.4% -> 84.6%; 8B shape, 16384
-// rows, S = 9: 77.7% -> 80.9%): the HBM serves this read stream best with
-// about one row in flight per wave of 768, and four waves' two-slot pipelines
-// keep ~1.4 rows each in flight.  At S <= 5 four waves are faster (S = 3:
-// 84.3% against 75.6%), and so they are over 8192 rows (config 5: 2.57 against
-// 2.61 ms per sweep), where a wave's share is short.  The fused (arena)
-// variants, whose partial write-back adds a second write stream, gain from
-// three only at 32768 rows (arena sweep at the 3B shape 15.45 -> 15.12 ms;
-// 16384 rows of the 8B schedule 11.34 -> 11.60 ms, slower).
-constexpr int kStreamFewWavesMinS = 6;
-int stream_waves_for(int num_sources, int64_t num_tokens, bool fused) {
+// Waves per workgroup of the streaming kernels (one workgroup per CU), one
+// per SIMD.  Each wave requests its next row only once the current one has
+// arrived, so a CU keeps one row per wave in flight, and the HBM serves this
+// stream best with about 24-28 KiB per CU in flight: four waves up to 7 KiB
+// rows (3B shape, S = 8: 86.3% of peak against 79.5% with three; 7 KiB rows
+// at S = 9: 82.0% against 80.4%; 5 KiB 80.2% against 67%), three for
+// 8 KiB rows (8B shape, S = 9: 84.8% against 80.6%).  The fused variants
+// keep four at 8 KiB (8B schedule arena prefill 11.39 against 11.44 ms).
+// (An earlier pipeline that requested the next row before the current one
+// arrived kept up to two rows per wave in flight and ran best with three
+// waves from S = 6.)
+int stream_waves_for(int row_kib, bool fused) {
   if (tuning().stream_waves > 0) return tuning().stream_waves;
-  const int64_t min_rows = fused ? 32768 : 16384;
-  return num_sources >= kStreamFewWavesMinS && num_tokens >= min_rows ? 3 : kStreamWaves;
+  return !fused && row_kib >= 8 ? 3 : kStreamWaves;
 }
 
 RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
@@ -641,7 +639,7 @@ RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int sr
                                                                : tuning().stream;
   ch.stream = stream_shape && (want_stream == 1 || (want_stream < 0 && num_tokens >= tuning().stream_min_tokens));
   if (ch.stream) {
-    ch.block = 64 * stream_waves_for(num_sources, num_tokens, fused);
+    ch.block = 64 * stream_waves_for(ch.nch, fused);
   } else {
     ch.v = pick_v(num_tokens, hidden / (bf ? 8 : 4), num_cus, &ch.block);
   }

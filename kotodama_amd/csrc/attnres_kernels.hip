@@ -135,6 +135,18 @@ __device__ __forceinline__ T ldg(const void* p) {
 #define ATTNRES_LOAD_CPOL -1  // -1: global loads (nt per ATTNRES_NT_LOADS); >= 0: buffer loads with this policy
 #endif
 
+// Zero that the compiler cannot fold, computed from v: adding it to the next
+// load's offset makes that load wait until v has arrived.  The streaming
+// kernels pass the last register of the row just loaded, so a wave requests
+// its next row only once the current one is in (one row per wave in flight
+// while the wave works on it; loads return in order, so the last register
+// arriving means the whole row has).
+__device__ __forceinline__ uint32_t arrival_zero(uint32_t v) {
+  uint32_t z;
+  asm volatile("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(v));
+  return z;
+}
+
 // Load through an explicitly global pointer: a generic (flat) load would also
 // count against the LDS wait counter and serialise with LDS reads.
 template <typename T>
@@ -1336,7 +1348,8 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
 
   // Sources are equally spaced (the host checks): source s of row t is at
   // src0 + s*src_stride + t*row_bytes, pure scalar arithmetic.
-  auto load_item = [&](u32x4(&buf)[NCH], u32x4(&dbuf)[FUSED ? NCH : 1], uint32_t t, uint32_t s) {
+  // z: an arrival_zero() added to the lane offsets (0 for the first item).
+  auto load_item = [&](u32x4(&buf)[NCH], u32x4(&dbuf)[FUSED ? NCH : 1], uint32_t t, uint32_t s, uint32_t z) {
     t = __builtin_amdgcn_readfirstlane(t);
     s = __builtin_amdgcn_readfirstlane(s);
     const bool from_delta = FUSED && s == (uint32_t)(S - 1) && mode == ATTNRES_MODE_SET;
@@ -1352,10 +1365,10 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
 #if ATTNRES_LOAD_CPOL >= 0
     const __amdgpu_buffer_rsrc_t rr = row_rsrc(const_cast<char*>(row), (uint32_t)(NCH * 1024));
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) buf[c] = ld_row(rr, (uint32_t)(c * 1024 + lane * 16));
+    for (int c = 0; c < NCH; ++c) buf[c] = ld_row(rr, (uint32_t)(c * 1024 + lane * 16) + z);
 #else
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) buf[c] = ldg_global<u32x4>(row + (uint32_t)(c * 1024 + lane * 16));
+    for (int c = 0; c < NCH; ++c) buf[c] = ldg_global<u32x4>(row + ((uint32_t)(c * 1024 + lane * 16) + z));
 #endif
     if constexpr (FUSED) {
       if (s == (uint32_t)(S - 1) && mode == ATTNRES_MODE_ACCUM) {
@@ -1603,9 +1616,14 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   };
 
   // ---- two-slot pipeline over this wave's (token, source) items ----
-  // The prefetch is issued unconditionally (past the last item it re-reads
-  // the current, valid row) so the wait before each use is exactly "all but
-  // the prefetch", with no branch around the loads.
+  // The next item is requested as soon as the current one has arrived and
+  // before the wave works on it: one row per wave in flight, its load
+  // overlapping the work.  (Requesting it before the current row has
+  // arrived, with up to two rows per wave in flight, measured 1.5-4 points
+  // of peak slower at S >= 4, and the HBM then served three waves per CU
+  // better than four.)  The prefetch is issued unconditionally (past the
+  // last item it re-reads the current, valid row), with no branch around
+  // the loads.
   using SlotA = std::integral_constant<int, 0>;
   using SlotB = std::integral_constant<int, 1>;
   // Items (row, source) of this wave in order; two per iteration so slot A
@@ -1620,7 +1638,7 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
     t_out = wrap ? t + nw : t;
   };
   uint32_t s = 0;
-  load_item(bufA, dX, tok, 0);
+  load_item(bufA, dX, tok, 0, 0u);
   for (uint32_t i = 0; i < n_items; i += 2) {
     const bool has1 = i + 1 < n_items;
     const bool has2 = i + 2 < n_items;
@@ -1628,9 +1646,9 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
     advance(tok, s, t1, s1);
     advance(t1, s1, t2, s2);
     // past the last item the prefetch re-reads the current (valid) row
-    load_item(bufB, dX, has1 ? t1 : tok, has1 ? s1 : s);
+    load_item(bufB, dX, has1 ? t1 : tok, has1 ? s1 : s, arrival_zero(bufA[NCH - 1][3]));
     process(bufA, dX, tok, s, SlotA{});
-    load_item(bufA, dX, has2 ? t2 : tok, has2 ? s2 : s);
+    load_item(bufA, dX, has2 ? t2 : tok, has2 ? s2 : s, arrival_zero(bufB[NCH - 1][3]));
     if (has1) process(bufB, dX, t1, s1, SlotB{});
     tok = __builtin_amdgcn_readfirstlane(t2);
     s = __builtin_amdgcn_readfirstlane(s2);

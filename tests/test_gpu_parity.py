@@ -416,9 +416,9 @@ def _full_config_check(gpu, name, seed, calls, rows=384):
 
 
 # (workload, source counts): the streaming kernel's launch shapes at full size -
-# three waves per workgroup with 8 staged output rows (3B, S >= 6), four waves
-# with 6 staged rows (S = 4, 5), no staging (S <= 3), three waves with 6 staged
-# 8 KiB rows (8B, S = 9); the last batch of most waves is partial
+# four waves per workgroup with 6 staged output rows (3B, S >= 4), no staging
+# (S <= 3), three waves with 6 staged 8 KiB rows (8B, S = 9); the last batch of
+# most waves is partial
 STREAM_FULL = [("cfg2", (2, 4, 5, 6, 8)), ("cfg3", (9,))]
 
 
