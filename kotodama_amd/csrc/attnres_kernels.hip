@@ -16,11 +16,12 @@
 //   * attnres_stream_*  one wave per token row (prefill; the hot path).  A
 //     lane holds 16-byte chunks l, l+64, ..., so each wave-wide load is 1 KiB
 //     contiguous.  The wave's (token, source) items flow through a two-slot
-//     register pipeline (the next row is requested before the current one is
-//     processed); per source: sum(x^2) and x.qw, one DPP wave reduction each,
-//     then an online softmax with the rescale folded into the accumulating
-//     FMA.  Finished output rows are staged in LDS and stored in batches per
-//     wave; one workgroup of three or four waves per CU.
+//     register pipeline (the next row is requested once the current one has
+//     arrived, before it is processed: one row per wave in flight); per
+//     source: sum(x^2) and x.qw, one DPP wave reduction each, then an online
+//     softmax with the rescale folded into the accumulating FMA.  Finished
+//     output rows are staged in LDS and stored in batches per wave; one
+//     workgroup of four waves per CU (three for 8 KiB rows).
 //   * attnres_route_*   one workgroup per token row (decode, few rows, Q > 1
 //     queries, the fused arena modes).  Thread i owns chunks i, i+blockDim,
 //     ...; all S source chunks are loaded at once, partial sums are reduced
@@ -1261,9 +1262,9 @@ __device__ __forceinline__ void merge_stream_body(const attnres_merge_params& P)
 //
 // Prefill kernel: one wave64 owns one token row at a time, and the S source
 // rows stream through a two-deep register pipeline (slots A and B): the load
-// of the next (token, source) item is issued before the current one is
-// processed, across token boundaries, so every wave keeps a row of HBM reads
-// in flight.  Lane l holds the 16-byte chunks l, l+64, ... (NCH chunks of a
+// of the next (token, source) item is issued as soon as the current one has
+// arrived and before it is processed, across token boundaries, so every wave
+// keeps exactly one row of HBM reads in flight.  Lane l holds the 16-byte chunks l, l+64, ... (NCH chunks of a
 // row of NCH KiB), so each wave-wide load covers 1 KiB contiguous.
 //
 // Per source: sum(x^2) and x.qw over the lane's chunks, one DPP wave
