@@ -270,7 +270,9 @@ int get_stream(DeviceState& st, int combo, bool out_bf, int nch, int variant, hi
 // bursts run the read-heavy stream far faster (the store-only access pattern
 // at the 3B shape: S = 4 83% -> 90%, S = 8 79% -> 91% of peak with batches of
 // 8); at S = 2 the batches measured slower, so they start at S = 4.  As many
-// rows as the LDS left over by the kernel's own arrays holds, at most 8.
+// rows as the LDS left over by the kernel's own arrays holds, at most 8; the
+// plain and table kernels add rows held in registers to each batch (4 up to
+// 6 KiB rows, 2 above).
 constexpr int kOutBatchMax = 8;
 int stream_out_batch(int num_sources, int64_t out_row_bytes, int static_lds, int max_lds, int waves) {
   const int min_s = tuning().out_batch_min_s;

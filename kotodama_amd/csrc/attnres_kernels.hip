@@ -1409,8 +1409,9 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
     asm volatile("" : "+v"(lane_ob));
     return lane_ob;
   };
-  // Finished rows can be staged in dynamic LDS and stored in batches of
-  // P.out_batch rows per wave: the output stores then reach memory in bursts
+  // Finished rows can be staged in dynamic LDS (P.out_batch rows per wave,
+  // plus REG_ROWS held in registers, below) and stored in batches: the
+  // output stores then reach memory in bursts
   // between long stretches of pure reads, which this HBM serves far better
   // than one row interleaved after every S source rows (a store-only
   // variant of the access pattern: 78.5% -> 90.9% of peak at S = 8, batches
@@ -1425,9 +1426,33 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   auto stage_row = [&](uint32_t b) {
     return reinterpret_cast<char*>(stream_stage) + ((uint32_t)wave * batch + b) * STAGE_ROW;
   };
+  // Past the LDS slots a wave holds REG_ROWS more finished rows in registers
+  // (one wave per SIMD leaves the register file for it), so a batch is
+  // P.out_batch + REG_ROWS rows: 8 and 10 row batches measured 1-1.5 points
+  // of peak faster than the 6 the LDS holds at four waves (S = 4..8).
+  constexpr int REG_ROWS = FUSED ? 1 : (NCH <= 6 ? 4 : 2);
+  u32x4 held[REG_ROWS][NCH][OPC];
+  const uint32_t full_batch = (!FUSED && batch > 1) ? batch + REG_ROWS : batch;
   uint32_t nheld = 0, t_first = 0;
   auto flush_staged = [&]() {
-    for (uint32_t b = 0; b < nheld; ++b) {
+#pragma unroll
+    for (int r = 0; r < REG_ROWS; ++r) {
+      if (batch + (uint32_t)r < nheld) {
+        const __amdgpu_buffer_rsrc_t orsrc = out_rsrc(t_first + (batch + r) * nw);
+        const uint32_t lane_ob = lane_out_offset();
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+          for (int h = 0; h < OPC; ++h) {
+            const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * OES + 16 * h);
+            if constexpr (OPB == 16) st_row(orsrc, off, held[r][c][h]);
+            else st_row(orsrc, off, u32x2{held[r][c][h][0], held[r][c][h][1]});
+          }
+        }
+      }
+    }
+    const uint32_t in_lds = nheld < batch ? nheld : batch;
+    for (uint32_t b = 0; b < in_lds; ++b) {
       const __amdgpu_buffer_rsrc_t orsrc = out_rsrc(t_first + b * nw);
       const uint32_t lane_ob = lane_out_offset();
 #pragma unroll
@@ -1571,17 +1596,31 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
       if (!FUSED && batch > 1) {
         // stage the row; the wave's batch is stored when full (or at the end)
         if (nheld == 0) t_first = t;
+        if (nheld < batch) {
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
+          for (int c = 0; c < NCH; ++c) {
 #pragma unroll
-          for (int h = 0; h < OPC; ++h) {
-            char* sp = stage_row(nheld) + ((c * OPC + h) * 64 + lane) * OPB;
-            if constexpr (OPB == 16) *reinterpret_cast<u32x4*>(sp) = pk[c][h];
-            else *reinterpret_cast<u32x2*>(sp) = u32x2{pk[c][h][0], pk[c][h][1]};
+            for (int h = 0; h < OPC; ++h) {
+              char* sp = stage_row(nheld) + ((c * OPC + h) * 64 + lane) * OPB;
+              if constexpr (OPB == 16) *reinterpret_cast<u32x4*>(sp) = pk[c][h];
+              else *reinterpret_cast<u32x2*>(sp) = u32x2{pk[c][h][0], pk[c][h][1]};
+            }
+          }
+        } else {
+          // register slot nheld - batch, selected with compile-time indices
+#pragma unroll
+          for (int r = 0; r < REG_ROWS; ++r) {
+            if (nheld == batch + (uint32_t)r) {
+#pragma unroll
+              for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+                for (int h = 0; h < OPC; ++h) held[r][c][h] = pk[c][h];
+              }
+            }
           }
         }
         nheld = __builtin_amdgcn_readfirstlane(nheld + 1);
-        if (nheld == batch) {
+        if (nheld == full_batch) {
           flush_staged();
           nheld = 0;
         }
@@ -3112,9 +3151,10 @@ MERGE_STREAM(8)
 #endif
 
 // Streaming kernels: attnres_stream_<in>_<qw>_c<NCH>_<plain|fused>, row = NCH KiB.
-// Occupancy target (waves per SIMD): two row buffers + the fp32 accumulator
-// fit 128 VGPRs up to 6 KiB rows, 168 up to 8 KiB.
-#define STREAM_WAVES_PER_EU(NCH) ((NCH) <= 4 ? 4 : (NCH) <= 6 ? 3 : 2)
+// Occupancy target (waves per SIMD): the plain and table kernels run one
+// wave per SIMD (one workgroup per CU), so their register budget also holds
+// the staged output rows past the LDS slots.
+#define STREAM_WAVES_PER_EU(NCH) 1
 // The fused kernels also hold the delta row of both pipeline slots.
 #define STREAM_FUSED_WAVES_PER_EU(NCH) ((NCH) <= 3 ? 4 : (NCH) <= 4 ? 3 : 2)
 
