@@ -144,7 +144,7 @@ struct Tuning {
   int bwd_per_cu = 0;          // > 0: resident workgroups per CU of the routing backward
   int mqg = 1;                 // 0: the batched-query backward never uses the matrix-core kernel
   int out_batch = 0;           // > 0: at most this many staged output rows per streaming wave (1: none)
-  int out_batch_min_s = 4;     // sources from which the streaming kernels stage output rows
+  int out_batch_min_s = 3;     // sources from which the streaming kernels stage output rows
   int stream_waves = 0;        // > 0: waves per workgroup of the streaming kernels (1..4); 0: by S
   int reduce_two_stage = 0;    // 1: the query-gradient reduction in two launches
   int merge_stream = 1;        // 0: the merge never uses the row-per-wave kernel
@@ -266,13 +266,14 @@ int get_stream(DeviceState& st, int combo, bool out_bf, int nch, int variant, hi
 }
 
 // Output rows a streaming-kernel wave stages in LDS and stores together
-// (attnres_route_params.out_batch).  From S = 4 sources per row, stores in
+// (attnres_route_params.out_batch).  With several sources per row, stores in
 // bursts run the read-heavy stream far faster (the store-only access pattern
 // at the 3B shape: S = 4 83% -> 90%, S = 8 79% -> 91% of peak with batches of
-// 8); at S = 2 the batches measured slower, so they start at S = 4.  As many
-// rows as the LDS left over by the kernel's own arrays holds, at most 8; the
-// plain and table kernels add rows held in registers to each batch (4 up to
-// 6 KiB rows, 2 above).
+// 8).  At S = 2 the batches measured slower (84.4% -> 83.3%) and at S = 3
+// faster once they reached 10 rows (83.9% -> 85.4%), so they start at S = 3.
+// As many rows as the LDS left over by the kernel's own arrays holds, at most
+// 8; the plain and table kernels add rows held in registers to each batch (4
+// up to 6 KiB rows, 2 above).
 constexpr int kOutBatchMax = 8;
 int stream_out_batch(int num_sources, int64_t out_row_bytes, int static_lds, int max_lds, int waves) {
   const int min_s = tuning().out_batch_min_s;

@@ -416,10 +416,11 @@ def _full_config_check(gpu, name, seed, calls, rows=384):
 
 
 # (workload, source counts): the streaming kernel's launch shapes at full size -
-# four waves per workgroup with 6 staged output rows (3B, S >= 4), no staging
-# (S <= 3), three waves with 6 staged 8 KiB rows (8B, S = 9); the last batch of
-# most waves is partial
-STREAM_FULL = [("cfg2", (2, 4, 5, 6, 8)), ("cfg3", (9,))]
+# four waves per workgroup with batches of 6 output rows staged in LDS plus 4
+# held in registers (3B, S >= 3), no staging (S = 2), three waves with 6 + 2
+# rows of 8 KiB (8B, S = 9); the last batch of most waves is partial and ends
+# in the LDS or in the register rows
+STREAM_FULL = [("cfg2", (2, 3, 4, 5, 6, 8)), ("cfg3", (9,))]
 
 
 @pytest.mark.parametrize("name,calls", STREAM_FULL, ids=[c[0] for c in STREAM_FULL])
