@@ -460,6 +460,51 @@ def test_streaming_kernel_matches_workgroup_kernel_every_row(gpu, name, calls):
     torch.cuda.empty_cache()
 
 
+def _stream_vs_workgroup(pool, s, q, gn, eps, label):
+    """Every element: streaming kernel against the workgroup kernel, at the bar of the full-size test above."""
+    outs = []
+    for pol in (_capi.POLICY_STREAM, _capi.POLICY_WORKGROUP):
+        prev = _capi.set_kernel_policy(pol)
+        try:
+            with torch.no_grad():
+                outs.append(ops.route_call(pool, s, q, gn, eps, torch.bfloat16)[0][0].float())
+        finally:
+            _capi.set_kernel_policy(prev)
+    torch.cuda.synchronize()
+    a, b = outs
+    xmax = pool[:s].abs().amax(0).float().reshape(b.shape)
+    tol = torch.exp2(torch.floor(torch.log2(torch.clamp(b.abs(), min=2.0**-126))) - 7) + 2.0**-16 * xmax
+    excess = ((a - b).abs() / tol).max().item()
+    same = (a == b).float().mean().item()
+    print(f"  {label}: max |diff| / tol {excess:.3f}, {same:.5f} of elements equal", flush=True)
+    assert excess <= 1.0, f"{label}: streaming and workgroup kernels differ by {excess:.2f}x the bar"
+    assert same >= 0.99, f"{label}: only {same:.4f} of elements equal"
+
+
+# (hidden, S, waves per workgroup, batch rows: LDS + registers) - row counts
+# chosen from the device's CU count so that every wave's last batch is either
+# exactly full or ends in the register-held rows (the full-size shapes end
+# theirs in the LDS rows)
+BATCH_TAILS = [(3072, 3, 4, 6 + 4), (3072, 6, 4, 6 + 4), (4096, 5, 3, 6 + 2)]
+
+
+@pytest.mark.parametrize("d,s,waves,batch", BATCH_TAILS, ids=[f"d{c[0]}_s{c[1]}" for c in BATCH_TAILS])
+def test_streaming_batches_ending_in_register_rows(gpu, d, s, waves, batch):
+    ncu = torch.cuda.get_device_properties(gpu).multi_processor_count
+    nw = ncu * waves
+    g = torch.Generator(device=gpu).manual_seed(d + s)
+    q = (torch.randn(d, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    gn = (1 + 0.1 * torch.randn(d, generator=g, device=gpu)).to(torch.bfloat16)
+    # half the waves get batch - 1 rows, half a full batch; then batch - 3 / batch - 2
+    for n in (nw * (batch - 1) + nw // 2, nw * (batch - 3) + nw // 2):
+        scales = torch.exp(torch.empty(s, device=gpu).uniform_(math.log(0.5), math.log(4.0), generator=g))
+        pool = (torch.randn((s, 1, n, d), generator=g, device=gpu) * scales.view(-1, 1, 1, 1)).to(torch.bfloat16)
+        print(f"stream batch tails d={d} S={s} rows={n} (rows per wave {n // nw}-{n // nw + 1})", flush=True)
+        _stream_vs_workgroup(pool, s, q, gn, 1e-5, f"d={d} S={s} rows={n}")
+        del pool
+    torch.cuda.empty_cache()
+
+
 def test_cfg3_8b_deepest_routing_full_size(gpu):
     _full_config_check(gpu, "cfg3", 3, (9, 9))
 
