@@ -1411,15 +1411,15 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   };
   // Finished rows can be staged in dynamic LDS (P.out_batch rows per wave,
   // plus REG_ROWS held in registers, below) and stored in batches: the
-  // output stores then reach memory in bursts
-  // between long stretches of pure reads, which this HBM serves far better
-  // than one row interleaved after every S source rows (a store-only
-  // variant of the access pattern: 78.5% -> 90.9% of peak at S = 8, batches
-  // of 8).  The staged layout is [row][chunk][piece][lane] (consecutive lanes
-  // 8 or 16 bytes apart: no bank conflicts); a wave reads back only what its
-  // own lanes wrote, so no barrier is needed.  The fused variants store each
-  // row at once (their partial write-back is a second write stream; staging
-  // measured slower there) and carry no staging code.
+  // output stores then reach memory in bursts between long stretches of
+  // pure reads, which this HBM serves far better than one row interleaved
+  // after every S source rows (a store-only variant of the access pattern:
+  // 78.5% -> 90.9% of peak at S = 8, batches of 8).  The staged layout is
+  // [row][chunk][piece][lane] (consecutive lanes 8 or 16 bytes apart: no
+  // bank conflicts); a wave reads back only what its own lanes wrote, so no
+  // barrier is needed.  The fused variants store each row at once (their
+  // partial write-back is a second write stream; staging measured slower
+  // there) and carry no staging code.
   const uint32_t batch = (uint32_t)P.out_batch;
   extern __shared__ u32x4 stream_stage[];
   constexpr uint32_t STAGE_ROW = NCH * OPC * 64 * OPB;     // bytes of one staged row
