@@ -1790,8 +1790,17 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
       for (int e = 0; e < VEC; ++e) qw_reg[QW_LDS ? 0 : k][e] = q[e];
     }
   }
+  // Chunks past the row end get zeros: their LDS slots were never written
+  // (and lie past the array where the block has more threads than 16-chunk
+  // groups), and stale contents there can be Inf or NaN, which 0 * x would
+  // carry into the row's dot products.
   auto qw_chunk = [&](int k, float (&q)[VEC]) {
     if constexpr (QW_LDS) {
+      if (!ok[k]) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) q[e] = 0.f;
+        return;
+      }
 #pragma unroll
       for (int h = 0; h < VEC / 4; ++h) {
         const float4 t = s_qw[lds_at(chunk[k], h)];

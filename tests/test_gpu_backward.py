@@ -49,6 +49,15 @@ def bf16_ulp(x):
     return 2.0 ** (e - 7)
 
 
+# Gradients this close to fp32's underflow threshold (2^-126 ~ 1.2e-38) are
+# products of softmax weights that underflowed: the kernels flush fp32
+# subnormals to zero, as the reference's Triton kernels do (their exp is the
+# flush-to-zero exp2), so such an element can come out 0 where the float64
+# oracle keeps a subnormal or barely normal value.  The exact-rounding count
+# leaves them out; the error bar still covers them.
+UNDERFLOW_RANGE = 1e-30
+
+
 def check_grad(g, ref, dtype, label, exact_frac=0.95):
     got = np64(g)
     err = np.abs(got - ref)
@@ -59,8 +68,10 @@ def check_grad(g, ref, dtype, label, exact_frac=0.95):
     else:
         tol = bf16_ulp(ref) + 1e-3 * scale
         assert (err <= tol).all(), f"{label}: worst err {err.max():.3e} (max|ref| {scale:.3e})"
-        same = np.mean(got == O.bf16_round(ref))
-        assert same >= exact_frac, f"{label}: only {same:.4f} equal the correctly rounded oracle"
+        counted = np.abs(ref) >= UNDERFLOW_RANGE
+        if counted.any():
+            same = np.mean(got[counted] == O.bf16_round(ref[counted]))
+            assert same >= exact_frac, f"{label}: only {same:.4f} equal the correctly rounded oracle"
 
 
 def make_case(gpu, S, extra, B, T, D, dtype, seed, param_dtype=None):
@@ -119,6 +130,38 @@ def test_route_static_backward_matches_oracle(gpu, dtype, S, D, B, T):
     dx, dq, dg = oracle_grads(buf, S, query, norm.weight, G, eps, dtype)
     check_grad(buf.grad[:S].reshape(S, -1, D), dx, dtype, "dsources")
     assert torch.all(buf.grad[S:] == 0), "inactive slots must get zero gradient"
+    check_grad(query.grad, dq, dtype, "dquery")
+    check_grad(norm.weight.grad, dg, dtype, "dgain")
+
+
+# Rows narrower than one block of the routing backward (11 bf16 chunks or 15
+# fp32 chunks in a 64-thread block) with S >= 5, where each thread's query
+# chunks sit in LDS: the threads past the row end must not read the slots no
+# thread wrote (stale Inf or NaN times a zero source chunk is NaN, which the
+# row reduction spreads to the whole row).
+NARROW = [(torch.bfloat16, 5, 88, 1, 2402), (torch.float32, 6, 60, 1, 1117)]
+
+
+@pytest.mark.parametrize("dtype,S,D,B,T", NARROW, ids=[f"{str(c[0])[6:]}-S{c[1]}-D{c[2]}" for c in NARROW])
+def test_narrow_rows_backward_ignores_stale_lds(gpu, dtype, S, D, B, T):
+    # a streaming forward over NaN rows first: the finished rows it stages in
+    # LDS on every CU leave NaN there for the next kernel
+    pool = torch.full((3, 1, 32768, 3072), float("nan"), dtype=torch.bfloat16, device=gpu)
+    with torch.no_grad():
+        ops.route_call(pool, 3, torch.zeros(3072, dtype=torch.bfloat16, device=gpu), None, 1e-5, torch.bfloat16)
+    del pool
+    print(f"narrow-row backward {dtype} S={S} D={D} rows={B * T}", flush=True)
+    eps = 1e-5
+    buf, query, gain, G = make_case(gpu, S, 0, B, T, D, dtype, seed=300 + S + D)
+    buf.requires_grad_(True)
+    query.requires_grad_(True)
+    norm = Norm(gain.clone(), eps)
+    out = kotodama_amd.route_static(buf, query, norm, torch.ones(S, dtype=torch.bool, device=gpu), S)
+    (out.float() * G).sum().backward()
+    torch.cuda.synchronize()
+    assert torch.isfinite(buf.grad).all() and torch.isfinite(query.grad).all()
+    dx, dq, dg = oracle_grads(buf, S, query, norm.weight, G, eps, dtype)
+    check_grad(buf.grad.reshape(S, -1, D), dx, dtype, "dsources")
     check_grad(query.grad, dq, dtype, "dquery")
     check_grad(norm.weight.grad, dg, dtype, "dgain")
 

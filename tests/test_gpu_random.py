@@ -6,10 +6,15 @@ row count, source and parameter dtypes, gain or none, a flat or a peaky
 softmax (query scale), and the kernel policy (row-per-wave or
 row-per-workgroup).  It runs the drop-in forward and backward through
 torch.autograd and checks outputs and gradients against the float64 oracle
-at the bars of the other parity tests (check_bf16 / check_f32 for outputs,
-check_grad for gradients).  Row counts are capped so that the float64 oracle
-handles at most ~2M source elements per case.
+at the bars of the other parity tests (check_bf16 for bf16 outputs,
+check_grad for bf16 gradients; fp32 outputs with logits to 8 fp32 ulps and
+fp32 gradients within 4x of the reference's op sequence differentiated in
+fp32, see check_f32_logits and check_grad_f32).  Row counts are capped so that the float64 oracle
+handles at most ~2M source elements per case.  ATTNRES_RANDOM_SEEDS=<n> runs n
+seeds per family instead of the default 8-12.
 """
+
+import os
 
 import numpy as np
 import pytest
@@ -18,6 +23,7 @@ import torch
 import kotodama_amd
 from kotodama_amd import _capi, ops
 from oracle import attnres_oracle as O
+from oracle import torch_cpu_path as TP
 
 from .test_gpu_backward import Norm, check_grad, np64
 from .test_gpu_parity import check_bf16, check_f32
@@ -25,6 +31,54 @@ from .test_gpu_parity import check_bf16, check_f32
 pytestmark = pytest.mark.gpu
 
 MAX_ELEMS = 2_000_000
+# seeds per family; ATTNRES_RANDOM_SEEDS=<n> runs a longer sweep
+SEEDS = int(os.environ.get("ATTNRES_RANDOM_SEEDS", "0"))
+
+
+def check_f32_logits(out, ref, x, weights, logits, label, ulps=8):
+    """fp32 outputs, per row: |err| <= 1e-5 |ref| + 1e-6 max|ref| (the contract bar)
+    + ulps * 2^-23 * max_s |logit_s| * sum_s w_s |x_s - ref|, the outputs' first-order
+    response to logits that are correct to `ulps` fp32 ulps of the row's largest logit.
+    The last term matters on peaked rows (logits of 30-60 with comparable weights),
+    where any fp32 evaluation moves the output by a few times the contract bar;
+    weights and logits are the float64 oracle's ((S, N) and (N, S))."""
+    got = np64(out)
+    sens = np.einsum("sn,snd->nd", weights, np.abs(x - ref[None]))
+    lmax = np.abs(logits).max(1)
+    tol = 1e-5 * np.abs(ref) + 1e-6 * np.abs(ref).max() + ulps * 2.0**-23 * lmax[:, None] * sens
+    e = float((np.abs(got - ref) / tol).max())
+    assert e <= 1.0, f"{label}: {e:.2f}x the fp32 bar (logits to {ulps} ulps)"
+
+
+def check_grad_f32(got, ref, ref32, label, factor=5.0):
+    """fp32 gradients: the contract bar of check_grad (1e-4 |ref| + 1e-5 max|ref|), or
+    within `factor` of the worst error of the reference's op sequence differentiated in
+    fp32 (ref32) against the same float64 oracle: sums over tokens of products whose
+    softmax part cancels (G.x_s - G.out) carry fp32 errors above the fixed bar.  Over
+    186 fp32 gradient checks of a 100-seed sweep the kernels' worst error was 1.0x the
+    fp32 reference's at the median, 2.0x at the 99th percentile and 4.2x at most, and
+    one check exceeded the contract bar (1.14x)."""
+    got = np64(got)
+    tol = 1e-4 * np.abs(ref) + 1e-5 * np.abs(ref).max()
+
+    def ratio(err):  # err / tol, 0 where both are 0 (e.g. all-zero query gradients at S = 1)
+        return float(np.where(err == 0, 0.0, err / np.maximum(tol, 1e-300)).max())
+
+    e, e32 = ratio(np.abs(got - ref)), ratio(np.abs(ref32 - ref))
+    print(f"[f32 grad] {label}: {e:.2f}x the bar (fp32 reference op sequence {e32:.2f}x)", flush=True)
+    assert e <= max(1.0, factor * e32), f"{label}: {e:.2f}x the fp32 bar; the fp32 reference op sequence {e32:.2f}x"
+
+
+def _route_f32_grads(x, query, gain, eps, G):
+    """Gradients (sources, query, gain) of the reference's op sequence (llama.py:640-644) in
+    fp32 on the CPU, through torch autograd; the gain fold is an fp32 product."""
+    xt = torch.tensor(x, dtype=torch.float32).unsqueeze(1).requires_grad_(True)
+    q = torch.tensor(query, dtype=torch.float32).requires_grad_(True)
+    g = torch.tensor(gain, dtype=torch.float32).requires_grad_(True)
+    mask = torch.ones(x.shape[0], dtype=torch.bool)
+    out = TP.route_static_cpu(xt, q * g, eps, mask)
+    (out * torch.tensor(G, dtype=torch.float32)).sum().backward()
+    return xt.grad[:, 0].double().numpy(), q.grad.double().numpy(), g.grad.double().numpy()
 
 
 def _policy(rng):
@@ -43,7 +97,7 @@ def _with_policy(pol, fn):
         _capi.set_kernel_policy(prev)
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(SEEDS or 12))
 def test_random_route_forward_backward(gpu, seed):
     rng = np.random.default_rng(1000 + seed)
     dtype = [torch.bfloat16, torch.float32][int(rng.integers(2))]
@@ -83,15 +137,27 @@ def test_random_route_forward_backward(gpu, seed):
     if out.dtype == torch.bfloat16:
         check_bf16(out.reshape(N, D), ref, f"seed {seed} out")
     else:
-        check_f32(out.reshape(N, D), ref, f"seed {seed} out")
+        r = O.route(x, qw, 1e-5)
+        check_f32_logits(out.reshape(N, D), ref, x, r["weights"][0], r["logits"][0], f"seed {seed} out")
     b = O.route_backward(x, qw, 1e-5, np64(G).reshape(N, D), None)
-    check_grad(buf.grad.reshape(S, N, D), b["dx"], dtype, f"seed {seed} dsources")
-    check_grad(query.grad, b["dqw"] * np64(norm.weight), pdt, f"seed {seed} dquery")
-    if with_gain:
-        check_grad(norm.weight.grad, b["dqw"] * np64(query), pdt, f"seed {seed} dgain")
+    f32 = None
+    if torch.float32 in (dtype, pdt):
+        f32 = _route_f32_grads(x, np64(query), np64(norm.weight), 1e-5, np64(G).reshape(N, D))
+    if dtype == torch.float32:
+        check_grad_f32(buf.grad.reshape(S, N, D), b["dx"], f32[0], f"seed {seed} dsources")
+    else:
+        check_grad(buf.grad.reshape(S, N, D), b["dx"], dtype, f"seed {seed} dsources")
+    if pdt == torch.float32:
+        check_grad_f32(query.grad, b["dqw"] * np64(norm.weight), f32[1], f"seed {seed} dquery")
+        if with_gain:
+            check_grad_f32(norm.weight.grad, b["dqw"] * np64(query), f32[2], f"seed {seed} dgain")
+    else:
+        check_grad(query.grad, b["dqw"] * np64(norm.weight), pdt, f"seed {seed} dquery")
+        if with_gain:
+            check_grad(norm.weight.grad, b["dqw"] * np64(query), pdt, f"seed {seed} dgain")
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(SEEDS or 8))
 def test_random_merge_forward_backward(gpu, seed):
     rng = np.random.default_rng(3000 + seed)
     pdt = [torch.bfloat16, torch.float32][int(rng.integers(2))]
@@ -132,7 +198,7 @@ def test_random_merge_forward_backward(gpu, seed):
     check_grad(q.grad, b["dq"], qdt, f"seed {seed} dquery")
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(SEEDS or 8))
 def test_random_batched_queries_forward_backward(gpu, seed):
     # the serving engine's phase-1 call: Q queries over one stack, bf16
     # output and fp32 lse, and its batched backward (matrix-core kernels for
@@ -172,7 +238,7 @@ def test_random_batched_queries_forward_backward(gpu, seed):
         check_grad(gain.grad, dgain, torch.bfloat16, f"seed {seed} dgain")
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(SEEDS or 8))
 def test_random_block_arena_forward(gpu, seed):
     # the stack-free caller (fused block steps over one arena): random layer
     # count and boundary set (with or without layer 0), arena dtype, width,
@@ -218,16 +284,31 @@ def test_random_block_arena_forward(gpu, seed):
     pd = "bf16" if dtype == torch.bfloat16 else "f32"
     qws = [O.fold_query(np64(q[j]), np64(gn[j]) if with_gain else None, pd) for j in range(P)]
     ref = O.block_forward(np64(embed), [np64(deltas[j]) for j in range(2 * L)], qws, 1e-5, L, set(bounds), dtype=pd)
-    check = check_bf16 if dtype == torch.bfloat16 else check_f32
     assert len(outs) == P and arena.n_committed == len(bounds)
-    for j in range(P):
-        check(outs[j], ref["outs"][j], f"seed {seed} point {j}")
+    if dtype == torch.bfloat16:
+        for j in range(P):
+            check_bf16(outs[j], ref["outs"][j], f"seed {seed} point {j}")
+    else:
+        # the sources of every point (the partial sums are fp32 additions, as
+        # in the arena) for the fp32 bar's sensitivity term
+        partial, committed = np64(embed), []
+        for j in range(P):
+            i, pre_mlp = divmod(j, 2)
+            if j < P - 1 and pre_mlp and i in set(bounds):
+                committed, partial = committed + [partial], np.zeros_like(partial)
+            if j < P - 1 and pre_mlp:
+                partial = (partial.astype(np.float32) + np64(deltas[2 * i]).astype(np.float32)).astype(np.float64)
+            srcs = np.stack(committed + [partial])
+            r = O.route(srcs, qws[j], 1e-5)
+            check_f32_logits(outs[j], ref["outs"][j], srcs, r["weights"][0], r["logits"][0], f"seed {seed} point {j}")
+            if j < P - 1 and pre_mlp:
+                partial = (partial.astype(np.float32) + np64(deltas[2 * i + 1]).astype(np.float32)).astype(np.float64)
     for b in range(len(bounds)):
         assert np.array_equal(np64(arena.committed[b]), ref["committed"][b]), f"seed {seed} committed {b}"
     assert np.array_equal(np64(arena.partial), ref["partial"]), f"seed {seed} partial"
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(SEEDS or 8))
 def test_random_list_routing_weights_and_backward(gpu, seed):
     # list routing over separate allocations in a random order (the pointer-
     # table kernel instance when they are not equally spaced), with the
