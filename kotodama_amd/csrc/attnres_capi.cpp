@@ -1163,8 +1163,9 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   hipFunction_t f = nullptr;
   int bpc = 1;
   // dynamic LDS (S >= 5): each thread's qw chunks and, with one chunk per
-  // thread, its query-gradient sums (fp32), in blocks of 16 chunks
-  const size_t lds = num_sources >= 5 ? (size_t)(v == 1 ? 2 : 1) * round16(nchunk) * vec * sizeof(float) : 0;
+  // thread, its query-gradient sums (fp32), a slot for every chunk index the
+  // block touches (v * block of them; those past the row end hold zeros)
+  const size_t lds = num_sources >= 5 ? (size_t)(v == 1 ? 2 : 1) * (size_t)(v * block) * vec * sizeof(float) : 0;
   if (lds + kBwdStaticLds > (size_t)st->max_lds)
     return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d needs %zu bytes of LDS per workgroup (device limit %d)", hidden,
                 lds + kBwdStaticLds, st->max_lds);

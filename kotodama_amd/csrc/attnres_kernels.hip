@@ -1740,17 +1740,20 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
 
   // Where registers are tight (S >= 5) each thread's chunks of qw and, for
   // V == 1, of its running query-gradient sum live in (dynamic) LDS instead,
-  // nchunk * VEC floats each; the LDS is thread-private, so no barrier.
+  // VEC floats per chunk; the LDS is thread-private, so no barrier.
   // Layout [chunk / 16][h][chunk % 16] (float4 h of a chunk's VEC floats):
   // sixteen consecutive lanes touch 256 contiguous bytes per access, so the
   // 128-bit LDS accesses are free of bank conflicts, and h is an immediate
-  // offset.  Each array holds round16(nchunk) * VEC / 4 float4s.
+  // offset.  Each array has a slot for every chunk index the block touches
+  // (V * blockDim of them, a multiple of 16); the slots of chunks past the
+  // row end hold zeros, so the dot loop reads them without a branch (stale
+  // LDS there can be Inf or NaN, which 0 * x would carry into the row).
   constexpr bool QW_LDS = S >= 5;
   constexpr bool DQW_LDS = QW_LDS && V == 1;
   constexpr int NPL = VEC / 4;
   extern __shared__ float4 bwd_lds[];
   float4* s_qw = bwd_lds;
-  float4* s_dqw = bwd_lds + ((P.nchunk + 15) & ~15) * NPL;
+  float4* s_dqw = bwd_lds + (int)(V * blockDim.x) * NPL;
   auto lds_at = [](int c, int h) { return (c & ~15) * NPL + h * 16 + (c & 15); };
   float qw_reg[QW_LDS ? 1 : V][VEC];
   float dqw_reg[DQW_LDS ? 1 : V][VEC];
@@ -1766,7 +1769,13 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
   for (int k = 0; k < V; ++k) {
     chunk[k] = tid + k * (int)blockDim.x;
     ok[k] = chunk[k] < P.nchunk;
-    if (!ok[k]) continue;
+    if (!ok[k]) {
+      if constexpr (QW_LDS) {
+#pragma unroll
+        for (int h = 0; h < VEC / 4; ++h) s_qw[lds_at(chunk[k], h)] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      continue;
+    }
     const int64_t off = (int64_t)chunk[k] * VEC;
     float q[VEC];
     load_param<VEC>(P.query, off, P.param_bf16, q);
@@ -1790,17 +1799,8 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
       for (int e = 0; e < VEC; ++e) qw_reg[QW_LDS ? 0 : k][e] = q[e];
     }
   }
-  // Chunks past the row end get zeros: their LDS slots were never written
-  // (and lie past the array where the block has more threads than 16-chunk
-  // groups), and stale contents there can be Inf or NaN, which 0 * x would
-  // carry into the row's dot products.
   auto qw_chunk = [&](int k, float (&q)[VEC]) {
     if constexpr (QW_LDS) {
-      if (!ok[k]) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) q[e] = 0.f;
-        return;
-      }
 #pragma unroll
       for (int h = 0; h < VEC / 4; ++h) {
         const float4 t = s_qw[lds_at(chunk[k], h)];
