@@ -1880,7 +1880,9 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
     const float wl = el * (1.0f / seg_sum<SEG>(el));
     const float go = seg_sum<SEG>(wl * t_gx);  // G . out = sum_s w_s (G . x_s)
     const float glse = P.grad_lse != nullptr ? P.grad_lse[tok] : 0.f;
-    const float c1l = wl * (glse + t_gx - go) * rl;
+    // glse is added after G.x_s - G.out cancels: added to G.x_s first it would
+    // be rounded to the ulp of that (much larger) dot product
+    const float c1l = wl * (glse + (t_gx - go)) * rl;
     const float c2l = -c1l * ll * rl * P.inv_d;
     // The coefficients are the same in every lane: scalar registers.
     float c1[S], c2[S], wgt[S];
@@ -2164,7 +2166,7 @@ __device__ __forceinline__ void route_bwd_mq_body(const attnres_route_bwd_mq_par
       const float wl = el * (1.0f / seg_sum<SEG>(el));
       const float go = seg_sum<SEG>(wl * t_gx);  // G_q . out_q
       const float glse = P.grad_lse != nullptr ? P.grad_lse[(int64_t)q * P.n_tokens + tok] : 0.f;
-      const float c1l = slot ? wl * (glse + t_gx - go) * rl : 0.f;
+      const float c1l = slot ? wl * (glse + (t_gx - go)) * rl : 0.f;  // cancel first, then add glse
       c2sum += slot ? -c1l * ll * rl * P.inv_d : 0.f;
       if (wave == 0 && lane < S) P.c1[(tok * nq + q) * S + lane] = c1l;
       float wgt[S], c1[S];
@@ -2391,7 +2393,7 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
       const float wl = slot ? el * (1.0f / sum) : 0.f;
       const float go = seg_sum<SEG>(wl * t_gx);  // G_q . out_q
       const float glse = slot && P.grad_lse != nullptr ? P.grad_lse[(int64_t)q * P.n_tokens + tok] : 0.f;
-      const float c1l = slot ? wl * (glse + t_gx - go) * rl : 0.f;
+      const float c1l = slot ? wl * (glse + (t_gx - go)) * rl : 0.f;  // cancel first, then add glse
       c2acc += slot ? -c1l * ll * rl * P.inv_d : 0.f;
       if (wave == 0 && slot) P.c1[(tok * nq + q) * S + ss] = c1l;
 

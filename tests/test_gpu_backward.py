@@ -166,6 +166,32 @@ def test_narrow_rows_backward_ignores_stale_lds(gpu, dtype, S, D, B, T):
     check_grad(norm.weight.grad, dg, dtype, "dgain")
 
 
+def test_lse_gradient_kept_next_to_large_dot_products(gpu):
+    # dL/dlogit_s = w_s (g_lse + G.x_s - G.out): g_lse (~0.1) must be added after
+    # G.x_s - G.out cancels; added to G.x_s (~100) first it is rounded to that
+    # number's ulp, a relative error of ~4e-5 in g_lse.  fp32 throughout; with one
+    # source the query gradient is exactly sum_n g_lse_n r_n x_n, which fp32
+    # sums to ~1e-6 of its largest value.
+    S, D, N = 1, 2928, 341
+    g = torch.Generator(device="cpu").manual_seed(41)
+    x = (torch.randn(S, N, D, generator=g) * 2.0).to(gpu)
+    q = (torch.randn(D, generator=g) * 0.05).to(gpu)
+    G = torch.randn(N, D, generator=g).to(gpu)
+    glse = (torch.randn(N, generator=g) * 0.1).to(gpu)
+    dx = torch.empty(S, N, D, device=gpu)
+    ws = torch.empty(_capi.route_bwd_workspace_size(N, D) // 4, device=gpu)
+    dq = torch.empty(D, device=gpu)
+    _capi.route_bwd(_capi.pointer_array([x[s].data_ptr() for s in range(S)]), S, N, D, D, _capi.DTYPE_F32,
+                    q.data_ptr(), None, _capi.DTYPE_F32, 1e-5, G.data_ptr(), _capi.DTYPE_F32, D, glse.data_ptr(),
+                    _capi.pointer_array([dx[s].data_ptr() for s in range(S)]), D, ws.data_ptr(), ws.numel() * 4,
+                    dq.data_ptr(), None, torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize()
+    b = O.route_backward(np64(x), np64(q), 1e-5, np64(G), np64(glse))
+    err = np.abs(np64(dq) - b["dqw"]).max()
+    assert err <= 2e-6 * np.abs(b["dqw"]).max(), f"query gradient worst err {err:.3e}"
+    assert np.abs(np64(dx) - b["dx"]).max() <= 1e-6 * np.abs(b["dx"]).max()
+
+
 def test_padded_stack_backward_like_the_training_loop(gpu):
     # llama.py:690-699: committed blocks + partial + zero padding stacked, then
     # routed; the padding does not require grad, so its gradient rows are not

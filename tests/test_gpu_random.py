@@ -27,7 +27,7 @@ from oracle import attnres_oracle as O
 from oracle import torch_cpu_path as TP
 
 from .test_gpu_backward import Norm, check_grad, np64
-from .test_gpu_parity import check_bf16
+from .test_gpu_parity import check_bf16, check_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -373,3 +373,89 @@ def test_random_list_routing_weights_and_backward(gpu, seed):
         check_grad(t.grad, b["dx"][k], dtype, f"seed {seed} dsource {k}")
     check_grad(query.grad, b["dqw"] * np64(gain), dtype, f"seed {seed} dquery")
     check_grad(gain.grad, b["dqw"] * np64(query), dtype, f"seed {seed} dgain")
+
+
+CANARY = 7.0  # exact in bf16 and fp32; no routed value here equals it
+
+
+def _code(dtype):
+    return _capi.DTYPE_BF16 if dtype == torch.bfloat16 else _capi.DTYPE_F32
+
+
+@pytest.mark.parametrize("seed", range(SEEDS or 8))
+def test_random_row_strides_through_the_c_abi(gpu, seed):
+    # attnres_route_fwd / attnres_route_bwd called directly on rows of wider,
+    # canary-filled buffers with random strides (16-byte aligned): sources,
+    # outputs, query planes, output gradient and gradients; forward with 1-9
+    # queries, backward with one; nothing outside the rows may be written
+    rng = np.random.default_rng(11000 + seed)
+    sdt = [torch.bfloat16, torch.float32][int(rng.integers(2))]
+    qdt = [torch.bfloat16, torch.float32][int(rng.integers(2))]
+    odt = [torch.bfloat16, torch.float32][int(rng.integers(2))]
+    vec = 8 if sdt == torch.bfloat16 else 4
+    ovec = 8 if odt == torch.bfloat16 else 4
+    S = int(rng.integers(1, 13))
+    Q = 1 if rng.integers(2) else int(rng.integers(2, 10))
+    D = vec * int(rng.integers(8, (8192 if sdt == torch.bfloat16 else 4096) // vec + 1))
+    N = _rows(rng, (S + Q) * D)
+    src_ld = D + vec * int(rng.integers(0, 9))
+    out_ld = D + ovec * int(rng.integers(0, 9))
+    qstride = N * out_ld + ovec * int(rng.integers(0, 9))
+    pol = _policy(rng)
+    print(f"random strides seed={seed}: src {sdt} q {qdt} out {odt} S={S} Q={Q} D={D} N={N} src_ld={src_ld} "
+          f"out_ld={out_ld} policy={pol}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(12000 + seed)
+    big = torch.full((S, N, src_ld), CANARY, dtype=sdt)
+    for s in range(S):
+        big[s, :, :D] = (torch.randn(N, D, generator=g) * float(np.exp(rng.uniform(np.log(0.25), np.log(4.0))))).to(sdt)
+    big = big.to(gpu)
+    qs = (torch.randn(Q, D, generator=g) * 0.05).to(qdt).to(gpu)
+    obuf = torch.full(((Q - 1) * qstride + N * out_ld,), CANARY, dtype=odt, device=gpu)
+    weights = torch.full((Q, S, N), CANARY, device=gpu)
+    lse = torch.full((Q, N), CANARY, device=gpu)
+    before = big.clone()
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    prev = _capi.set_kernel_policy(pol)
+    try:
+        _capi.route_fwd(_capi.pointer_array([big[s].data_ptr() for s in range(S)]), S, N, D, src_ld, _code(sdt),
+                        qs.data_ptr(), None, Q, _code(qdt), 1e-5, obuf.data_ptr(), _code(odt), out_ld, qstride,
+                        weights.data_ptr(), lse.data_ptr(), None, None, stream)
+    finally:
+        _capi.set_kernel_policy(prev)
+    torch.cuda.synchronize()
+    x = np64(big[:, :, :D])
+    ref = O.route(x, np64(qs), 1e-5)
+    for q in range(Q):
+        view = obuf[q * qstride: q * qstride + N * out_ld].view(N, out_ld)
+        if odt == torch.bfloat16:
+            check_bf16(view[:, :D], ref["out"][q], f"seed {seed} out[{q}]")
+        else:
+            check_f32(view[:, :D], ref["out"][q], f"seed {seed} out[{q}]")
+        assert torch.all(view[:, D:] == CANARY), f"seed {seed}: output row padding written"
+        if q + 1 < Q:
+            assert torch.all(obuf[q * qstride + N * out_ld: (q + 1) * qstride] == CANARY), f"seed {seed}: gap written"
+        assert np.abs(np64(weights[q]) - ref["weights"][q]).max() <= 1e-5, f"seed {seed} weights[{q}]"
+        np.testing.assert_allclose(np64(lse[q]), ref["lse"][q], rtol=1e-5, atol=1e-5)
+    assert torch.equal(big, before), f"seed {seed}: a source was modified"
+    if Q > 1:
+        return
+    gvec = 8 if sdt == torch.bfloat16 else 4
+    gout_ld = D + gvec * int(rng.integers(0, 9))
+    grad_ld = D + vec * int(rng.integers(0, 9))
+    gbuf = torch.full((N, gout_ld), CANARY, dtype=sdt)
+    gbuf[:, :D] = torch.randn(N, D, generator=g).to(sdt)
+    gbuf = gbuf.to(gpu)
+    glse = (torch.randn(N, generator=g) * 0.1).to(gpu) if rng.integers(2) else None
+    dbig = torch.full((S, N, grad_ld), CANARY, dtype=sdt, device=gpu)
+    ws = torch.empty(_capi.route_bwd_workspace_size(N, D) // 4, device=gpu)
+    dq = torch.full((D,), CANARY, dtype=qdt, device=gpu)
+    _capi.route_bwd(_capi.pointer_array([big[s].data_ptr() for s in range(S)]), S, N, D, src_ld, _code(sdt),
+                    qs.data_ptr(), None, _code(qdt), 1e-5, gbuf.data_ptr(), _code(sdt), gout_ld,
+                    None if glse is None else glse.data_ptr(),
+                    _capi.pointer_array([dbig[s].data_ptr() for s in range(S)]), grad_ld, ws.data_ptr(),
+                    ws.numel() * 4, dq.data_ptr(), None, stream)
+    torch.cuda.synchronize()
+    b = O.route_backward(x, np64(qs[0]), 1e-5, np64(gbuf[:, :D]), None if glse is None else np64(glse))
+    check_grad(dbig[:, :, :D], b["dx"], sdt, f"seed {seed} dsources")
+    assert torch.all(dbig[:, :, D:] == CANARY), f"seed {seed}: gradient row padding written"
+    check_grad(dq, b["dqw"], qdt, f"seed {seed} dquery")
