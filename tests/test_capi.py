@@ -32,6 +32,34 @@ def test_library_exports_every_declared_symbol():
     assert lib.attnres_max_sources() == _capi.MAX_SOURCES == 16
 
 
+# C parameter types of the header and the ctypes type each must be bound with
+C_TO_CTYPES = {
+    "int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float, "char*": ctypes.c_char_p,
+    "const void*": ctypes.c_void_p, "void*": ctypes.c_void_p, "const float*": ctypes.c_void_p,
+    "float*": ctypes.c_void_p, "const void* const*": ctypes.POINTER(ctypes.c_void_p),
+    "void* const*": ctypes.POINTER(ctypes.c_void_p), "int64_t*": ctypes.POINTER(ctypes.c_int64),
+}
+
+
+def test_binding_signatures_match_the_header_prototypes():
+    # a parameter bound with the wrong width (int against int64_t, say) would
+    # pass wrong values through the ABI without any error
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    protos = re.findall(r"^\s*((?:const\s+)?\w+\**)\s+(attnres_\w+)\s*\((.*?)\);", text, flags=re.M | re.S)
+    assert [p[1] for p in protos] == list(_capi.EXPORTS)
+    for ret, name, params in protos:
+        ptypes = []
+        for p in params.split(","):
+            p = " ".join(p.split())
+            if p in ("", "void"):
+                continue
+            ptypes.append(C_TO_CTYPES[re.sub(r"\s*\w+$", "", p)])
+        argtypes, restype = _capi._SIGNATURES[name]
+        assert list(argtypes) == ptypes, f"{name}: binding argtypes differ from the header"
+        assert restype == {"int": ctypes.c_int, "const char*": ctypes.c_char_p}[ret], f"{name}: return type"
+
+
 FAKE = 0x7F0000000000  # never dereferenced: argument checks run first
 
 
