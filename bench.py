@@ -28,6 +28,8 @@ backward of the same routing calls instead (attnres_route_bwd on preallocated
 gradient buffers: (2S+1) * B*T*D * 2 algorithmic bytes per call — sources and
 dL/dout read, source gradients written; for cfg2serve the batched-query
 backward of each phase-1 call, (3S+Q) rows, and the merge backward, 5 rows).
+``cfg2arena`` runs the stack-free caller's prefill at the 3B shape (fused block
+steps over one arena: (S+3) rows per point, S+2 right after a commit).
 ``--workload mall`` checks what the 256 MB last-level cache serves of a call's
 bytes (the dominant calls back to back vs after other memory traffic).
 ``--gpus`` above 1 exits: this build measures one GPU.
@@ -54,6 +56,8 @@ WORKLOAD_TEXT = {
     "cfg4": "8B decode step: T=1, B=256, D=4096, 65 fused block steps (S=1..9) in one HIP graph, bf16",
     "cfg5": "3B data-driven blocks {0,3,7,12,18,23}: D=3072, B=2, T=4096, 57 calls S=1..7 (sum S=267), BOS x20, bf16",
     "copy": "calibration: torch device copy of 1 GiB (bf16), the plain copy kernel that scales rocprof byte counters",
+    "cfg2arena": "3B stack-free prefill (llama.py:680-716): 57 fused block steps over one arena (partial update, "
+    "commit, route), D=3072, B=8, T=4096, bf16",
     "mall": "cache check: the dominant cfg2 (S=8) and cfg3 (S=9) calls back to back vs after a 512 MiB write, "
     "a 512 MiB read, or a call on a second pool",
     "cfg2serve": "3B serving two-phase routing (serve.py:113-164): 7 blocks of 8 sublayers, one batched phase-1 call "
@@ -89,8 +93,10 @@ def load_traffic(kernel_tag: str):
         return None, None
 
 
-def kernel_name(s: int, tokens: int, hidden: int, dtype, queries: int = 1) -> str:
-    """The kernel symbol the library launches for one routing call of this shape."""
+def kernel_name(s: int, tokens: int, hidden: int, dtype, queries: int = 1, mode: int = 0) -> str:
+    """The kernel symbol the library launches for one routing call of this shape
+    (mode: 0 a routing call, 1 a block step accumulating into the partial, 2 a
+    block step with a commit)."""
     import ctypes
 
     from kotodama_amd import _capi, ops
@@ -98,7 +104,7 @@ def kernel_name(s: int, tokens: int, hidden: int, dtype, queries: int = 1) -> st
     buf = ctypes.create_string_buffer(128)
     code = ops.dtype_code(dtype)
     _capi.check("attnres_route_kernel_name",
-                _capi.lib().attnres_route_kernel_name(s, tokens, hidden, code, code, code, queries, 0, 1, buf,
+                _capi.lib().attnres_route_kernel_name(s, tokens, hidden, code, code, code, queries, mode, 1, buf,
                                                       len(buf)))
     return buf.value.decode()
 
@@ -461,6 +467,16 @@ def bench_serve_backward(steps: int, warmup: int, dev):
     return elapsed, step_bytes, deepest_ms, (3 * deepest + (ranges[-1][1] - ranges[-1][0])) * row
 
 
+def arena_step_rows(sched) -> int:
+    """Algorithmic rows moved by one pass of fused block steps over an arena:
+    the first point reads the partial and writes its output (2 rows); a point
+    that updates the partial reads S sources and the delta and writes the
+    partial and its output (S + 3); a point right after a block commit starts
+    the new partial from the delta, so it reads S - 1 committed blocks and the
+    delta (S + 2)."""
+    return 2 + sum(s + (2 if commit else 3) for s, commit in zip(sched.active_counts[1:], sched.commit_before[1:]))
+
+
 def bench_decode(w, steps: int, warmup: int, dev):
     """cfg4: one decode step = 65 fused block steps, captured in a HIP graph."""
     import torch
@@ -503,10 +519,56 @@ def bench_decode(w, steps: int, warmup: int, dev):
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
     step_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in events)
-    # algorithmic bytes of one decode step: (S+3) rows per fused point
-    # (S sources + delta read, partial + out written), 2 rows for the first point
-    rows = 2 + sum(s + 3 for s in sched.active_counts[1:])
-    return elapsed, rows * w.batch * w.hidden * w.elem_bytes, step_ms
+    return elapsed, arena_step_rows(sched) * w.batch * w.hidden * w.elem_bytes, step_ms
+
+
+def bench_arena(w, steps: int, warmup: int, dev):
+    """cfg2arena: the stack-free caller's prefill at the 3B shape (llama.py:680-716
+    without the per-call stacked copy): the 57 routing points as fused block
+    steps over one arena, each updating the partial from a sublayer output
+    (four distinct outputs, reused).  Events around the S = 8 points give the
+    dominant kernel's time."""
+    import torch
+
+    from kotodama_amd import workloads
+    from kotodama_amd.engine import AttnResRouter
+
+    sched = w.schedule
+    embed = torch.randn((w.batch, w.seq, w.hidden), device=dev).to(w.dtype)
+    deltas = workloads.make_deltas(w, dev, 5, 4)
+    q, gn = workloads.make_params(w, dev, 5, sched.num_points)
+    router = AttnResRouter(sched, list(q), list(gn), w.eps)
+    arena = router.new_arena((w.batch, w.seq), w.hidden, w.dtype, dev)
+    top = max(sched.active_counts)
+
+    def step(events=None):
+        arena.start(embed)
+        delta = None
+        for j in range(sched.num_points):
+            timed = events is not None and sched.active_counts[j] == top and not sched.commit_before[j]
+            if timed:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+            arena.step(q[j], gn[j], w.eps, delta=delta, commit=sched.commit_before[j])
+            if timed:
+                e1.record()
+                events.append((e0, e1))
+            delta = deltas[j % 4]
+
+    with torch.inference_mode():
+        for _ in range(warmup):
+            step([])
+        torch.cuda.synchronize()
+        events: list = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(events)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    dom_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in events)
+    row = w.tokens * w.hidden * w.elem_bytes
+    return elapsed, arena_step_rows(sched) * row, top, dom_ms, (top + 3) * row
 
 
 def bench_copy(steps: int, warmup: int, dev):
@@ -625,6 +687,25 @@ def main() -> int:
         ms = elapsed * 1e3 / args.steps
         print(json.dumps({"workload": WORKLOAD_TEXT["copy"], "bytes_read": nbytes // 2, "bytes_written": nbytes // 2,
                           "ms_per_copy": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return 0
+    if args.workload == "cfg2arena":
+        w2 = workloads.get("cfg2")
+        elapsed, step_bytes, top, dom_ms, dom_bytes = bench_arena(w2, args.steps, args.warmup, dev)
+        ms_per_step = elapsed * 1e3 / args.steps
+        gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+        ach = dom_bytes / (dom_ms * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": "AttnRes stack-free prefill (fused block steps over an arena) achieved HBM GB/s",
+            "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16", "data": "synthetic (seeded embedding, sublayer outputs and routing weights, in HBM)",
+            "config": {"workload": WORKLOAD_TEXT["cfg2arena"], "algorithmic_bytes_per_step": step_bytes},
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(w2.tokens / (ms_per_step * 1e-3), 1),
+            "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": kernel_name(top, w2.tokens, w2.hidden, w2.dtype, mode=1) + f" (S={top} points)",
+                         "algorithmic_bytes": dom_bytes, "avg_ms": round(dom_ms, 4)},
+        }), flush=True)
         return 0
     if args.workload == "mall":
         print(json.dumps({"workload": WORKLOAD_TEXT["mall"], "steps": args.steps, "warmup": args.warmup,
