@@ -97,6 +97,7 @@ struct DeviceState {
   int merge_bpc[kMergeFuncs] = {};
   int merge_bpc_block[kMergeFuncs] = {};
   hipFunction_t bwd[kBwdFuncs] = {};
+  hipFunction_t bwd_stream[2 * 9] = {};  // row-per-wave backward: rows of 6 / 8 KiB x S
   int bwd_bpc[kBwdFuncs] = {};
   int bwd_bpc_block[kBwdFuncs] = {};
   ReduceFns reduce;
@@ -390,6 +391,36 @@ int get_bwd(DeviceState& st, bool bf, bool gbf, int s, int v, int block, size_t 
   }
   *f = st.bwd[idx];
   *bpc = st.bwd_bpc[idx];
+  return ATTNRES_OK;
+}
+
+// Row-per-wave backward (code-object part 4): bf16 sources and output
+// gradients, rows of 6 or 8 KiB (hidden 3072 / 4096), S * (row KiB) <= 48 so
+// the kept source rows fit the registers; a grid of one 4-wave workgroup per
+// CU.  Chosen like the forward streaming kernel: by the kernel policy, and
+// under AUTO for calls of at least the streaming threshold's rows.
+constexpr int kBwdStreamWaves = 4;
+int bwd_stream_nch(bool bf, bool gbf, int num_sources, int hidden, int64_t num_tokens) {
+  if (!bf || !gbf || hidden % 512 != 0) return 0;
+  const int nch = hidden / 512;
+  if ((nch != 6 && nch != 8) || num_sources < 1 || num_sources * nch > 48) return 0;
+  if (num_tokens >= (int64_t)1 << 31) return 0;  // 32-bit row counters
+  const int policy = g_policy.load(std::memory_order_relaxed);
+  const int want = policy == ATTNRES_POLICY_STREAM ? 1 : policy == ATTNRES_POLICY_WORKGROUP ? 0 : tuning().stream;
+  return want == 1 || (want < 0 && num_tokens >= tuning().stream_min_tokens) ? nch : 0;
+}
+size_t bwd_stream_lds(int nch) { return (size_t)kBwdStreamWaves * (size_t)nch * 2048; }
+
+int get_bwd_stream(DeviceState& st, int nch, int s, hipFunction_t* f) {
+  const int idx = (nch == 8 ? 9 : 0) + s;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (st.bwd_stream[idx] == nullptr) {
+    char name[96];
+    snprintf(name, sizeof(name), "attnres_route_bwd_stream_c%d_s%d", nch, s);
+    int rc = find_function(st, 4, name, &st.bwd_stream[idx]);
+    if (rc != ATTNRES_OK) return rc;
+  }
+  *f = st.bwd_stream[idx];
   return ATTNRES_OK;
 }
 
@@ -951,6 +982,11 @@ int attnres_route_bwd_kernel_name(int num_sources, int64_t num_tokens, int hidde
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
+  const int nch = bwd_stream_nch(bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, hidden, num_tokens);
+  if (nch > 0) {
+    snprintf(buf, (size_t)buf_len, "attnres_route_bwd_stream_c%d_s%d", nch, num_sources);
+    return ATTNRES_OK;
+  }
   const int v = bwd_chunks_per_thread(hidden / vec, num_sources, num_tokens, st->num_cus);
   snprintf(buf, (size_t)buf_len, "attnres_route_bwd_%s_g%s_s%d_v%d", bf ? "bf" : "f32",
            grad_out_dtype == ATTNRES_DTYPE_BF16 ? "bf" : "f32", num_sources, v);
@@ -1113,6 +1149,54 @@ int attnres_route_bwd_workspace_size(int64_t num_tokens, int hidden, int64_t* by
   return ATTNRES_OK;
 }
 
+// The launch of a routing backward kernel (either family) over `grid`
+// workgroups, each writing one query-gradient partial row to the workspace,
+// then the column reduction of those rows into grad_query / grad_gain.
+static int route_bwd_finish(hipFunction_t f, int grid, int block, size_t lds, DeviceState& st, int nchunk,
+                     const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
+                     const void* query, const void* gain, int param_dtype, float eps, const void* grad_out,
+                     int grad_out_dtype, int64_t grad_out_ld, const float* grad_lse, void* const* grad_sources,
+                     int64_t grad_ld, void* workspace, int64_t workspace_bytes, void* grad_query, void* grad_gain,
+                     void* stream) {
+  int rc = ATTNRES_OK;
+  const int64_t need = (int64_t)grid * (int64_t)hidden * (int64_t)sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(ATTNRES_ERR_ARG, "workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
+                (long long)need);
+  if (!aligned16(workspace)) return fail(ATTNRES_ERR_ALIGN, "workspace not 16-byte aligned");
+  const ReduceFns* red = nullptr;
+  if (grad_query != nullptr || grad_gain != nullptr) {
+    rc = get_reduce(st, &red);
+    if (rc != ATTNRES_OK) return rc;
+  }
+
+  attnres_route_bwd_params P;
+  std::memset(&P, 0, sizeof(P));
+  for (int s = 0; s < num_sources; ++s) {
+    P.src[s] = sources[s];
+    P.dsrc[s] = grad_sources[s];
+  }
+  P.query = query;
+  P.gain = gain;
+  P.grad_out = grad_out;
+  P.grad_lse = grad_lse;
+  P.dqw_part = static_cast<float*>(workspace);
+  P.n_tokens = num_tokens;
+  P.src_ld = src_ld;
+  P.dsrc_ld = grad_ld;
+  P.gout_ld = grad_out_ld;
+  P.d = hidden;
+  P.nchunk = nchunk;
+  P.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
+  P.gout_bf16 = grad_out_dtype == ATTNRES_DTYPE_BF16;
+  P.eps = eps;
+  P.inv_d = 1.0f / (float)hidden;
+  rc = launch(f, (int)grid, block, P, stream, 1, lds);
+  if (rc != ATTNRES_OK || red == nullptr) return rc;
+
+  return reduce_launch(*red, workspace, (int)grid, hidden, query, gain, param_dtype, grad_query, grad_gain, stream);
+}
+
 int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
                       int src_dtype, const void* query, const void* gain, int param_dtype, float eps,
                       const void* grad_out, int grad_out_dtype, int64_t grad_out_ld, const float* grad_lse,
@@ -1158,6 +1242,19 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
+  const int snch = bwd_stream_nch(bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, hidden, num_tokens);
+  if (snch > 0) {
+    hipFunction_t f = nullptr;
+    rc = get_bwd_stream(*st, snch, num_sources, &f);
+    if (rc != ATTNRES_OK) return rc;
+    const int64_t need_wg = (num_tokens + kBwdStreamWaves - 1) / kBwdStreamWaves;
+    const int64_t cap = (int64_t)st->num_cus * (tuning().bwd_per_cu > 0 ? tuning().bwd_per_cu : 1);
+    const int grid = (int)(need_wg < cap ? need_wg : cap);
+    return route_bwd_finish(f, grid, 64 * kBwdStreamWaves, bwd_stream_lds(snch), *st, nchunk, sources, num_sources,
+                            num_tokens, hidden, src_ld, query, gain, param_dtype, eps, grad_out, grad_out_dtype,
+                            grad_out_ld, grad_lse, grad_sources, grad_ld, workspace, workspace_bytes, grad_query,
+                            grad_gain, stream);
+  }
   const int v = bwd_chunks_per_thread(nchunk, num_sources, num_tokens, st->num_cus);
   const int block = v == 1 ? round64(nchunk) : round64((nchunk + 1) / 2);
   hipFunction_t f = nullptr;
@@ -1177,42 +1274,9 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   const int per_cu = tuning().bwd_per_cu > 0 ? tuning().bwd_per_cu : num_sources == 1 ? 3 : 2;
   int64_t grid = (int64_t)st->num_cus * (bpc < per_cu ? bpc : per_cu);
   if (grid > num_tokens) grid = num_tokens;
-  const int64_t need = grid * (int64_t)hidden * (int64_t)sizeof(float);
-  if (workspace == nullptr || workspace_bytes < need)
-    return fail(ATTNRES_ERR_ARG, "workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
-                (long long)need);
-  if (!aligned16(workspace)) return fail(ATTNRES_ERR_ALIGN, "workspace not 16-byte aligned");
-  const ReduceFns* red = nullptr;
-  if (grad_query != nullptr || grad_gain != nullptr) {
-    rc = get_reduce(*st, &red);
-    if (rc != ATTNRES_OK) return rc;
-  }
-
-  attnres_route_bwd_params P;
-  std::memset(&P, 0, sizeof(P));
-  for (int s = 0; s < num_sources; ++s) {
-    P.src[s] = sources[s];
-    P.dsrc[s] = grad_sources[s];
-  }
-  P.query = query;
-  P.gain = gain;
-  P.grad_out = grad_out;
-  P.grad_lse = grad_lse;
-  P.dqw_part = static_cast<float*>(workspace);
-  P.n_tokens = num_tokens;
-  P.src_ld = src_ld;
-  P.dsrc_ld = grad_ld;
-  P.gout_ld = grad_out_ld;
-  P.d = hidden;
-  P.nchunk = nchunk;
-  P.param_bf16 = param_dtype == ATTNRES_DTYPE_BF16;
-  P.gout_bf16 = grad_out_dtype == ATTNRES_DTYPE_BF16;
-  P.eps = eps;
-  P.inv_d = 1.0f / (float)hidden;
-  rc = launch(f, (int)grid, block, P, stream, 1, lds);
-  if (rc != ATTNRES_OK || red == nullptr) return rc;
-
-  return reduce_launch(*red, workspace, (int)grid, hidden, query, gain, param_dtype, grad_query, grad_gain, stream);
+  return route_bwd_finish(f, (int)grid, block, lds, *st, nchunk, sources, num_sources, num_tokens, hidden, src_ld, query,
+                          gain, param_dtype, eps, grad_out, grad_out_dtype, grad_out_ld, grad_lse, grad_sources,
+                          grad_ld, workspace, workspace_bytes, grad_query, grad_gain, stream);
 }
 
 // Workspace of the batched-query backward: c1 coefficients (num_tokens, Q, S)

@@ -1974,6 +1974,226 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
   }
 }
 
+// ------------------------------------------ row-per-wave routing backward --
+//
+// The routing backward with one wave per token row, for bf16 sources and
+// output gradients and rows of NCH KiB (hidden = 512 * NCH): a resident grid
+// of one workgroup per CU whose waves take rows grid-stride.  A row's items
+// stream through the two-slot pipeline of the forward streaming kernel (the
+// next item is requested as soon as the current one has arrived): G, then
+// x_0 .. x_{S-1}.  Per source the lane forms sum(x^2) and x.G (v_dot2 on the
+// packed words) and x.qw (fp32 qw from LDS) over its chunks, three DPP wave
+// sums give the row's values, and the packed source row is kept in registers
+// (S * NCH * 4 of them, which at one wave per SIMD the compiler places in the
+// accumulation half of the register file).  After the last source the softmax
+// and the coefficients are formed wave-uniformly, and each gradient row
+//   dx_s = w_s G + c1_s qw + c2_s x_s,
+//   c1_s = dl_s r_s,  c2_s = -dl_s l_s r_s^2 / D,  dl_s = w_s (g_lse + G.x_s - G.out),
+// is stored whole, source after source, while the next row's G is in flight.
+// The query gradient sum_s c1_s x_s accumulates per lane over the wave's
+// rows; at the end the workgroup's waves add theirs through LDS in a fixed
+// order and write one fp32 partial row per workgroup, as route_bwd_body does.
+template <int S, int NCH>
+__device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_params& P) {
+  // Dynamic LDS in float4 slots [chunk][half][lane] (consecutive lanes 16
+  // bytes apart): the folded query in fp32, then at the end one such row of
+  // query-gradient sums per wave.
+  extern __shared__ float4 bws_lds[];
+  constexpr int ROW4 = NCH * 2 * 64;  // float4 slots of one row
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nwv = (int)(blockDim.x >> 6);
+  auto slot = [&](int c, int h) { return (c * 2 + h) * 64 + lane; };
+
+  // ---- folded query (query * gain, rounded to the parameter dtype) ----
+  for (int i = tid; i < NCH * 64; i += (int)blockDim.x) {
+    float q[8];
+    load_param<8>(P.query, (int64_t)i * 8, P.param_bf16, q);
+    if (P.gain != nullptr) {
+      float gn[8];
+      load_param<8>(P.gain, (int64_t)i * 8, P.param_bf16, gn);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float prod = q[e] * gn[e];
+        q[e] = P.param_bf16 ? round_bf16(prod) : prod;
+      }
+    }
+    const int c = i >> 6, l = i & 63;
+    bws_lds[(c * 2) * 64 + l] = make_float4(q[0], q[1], q[2], q[3]);
+    bws_lds[(c * 2 + 1) * 64 + l] = make_float4(q[4], q[5], q[6], q[7]);
+  }
+  __syncthreads();
+  // The query is read from LDS at each use (an opaque index): hoisted out of
+  // the row loop it would hold 8 * NCH more registers.
+  auto qw_chunk = [&](int c, float (&q)[8]) {
+    int i0 = slot(c, 0);
+    asm volatile("" : "+v"(i0));
+    const float4 qa = bws_lds[i0], qb = bws_lds[i0 + 64];
+    q[0] = qa.x, q[1] = qa.y, q[2] = qa.z, q[3] = qa.w;
+    q[4] = qb.x, q[5] = qb.y, q[6] = qb.z, q[7] = qb.w;
+  };
+  auto lane63 = [](float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+  };
+
+  float dq[NCH][8];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dq[c][e] = 0.f;
+  }
+  // 32-bit wave-uniform row counters (scalar loop control, as in stream_body)
+  const uint32_t n_tok = (uint32_t)P.n_tokens;
+  const uint32_t nw = gridDim.x * (uint32_t)nwv;
+  const uint32_t tok0 = blockIdx.x * (uint32_t)nwv + (uint32_t)wave;
+  if (tok0 < n_tok) {  // no barrier inside: waves without rows go straight to the partial sums
+    const uint64_t row_bytes = (uint64_t)P.src_ld * 2;
+    const uint64_t grow_bytes = (uint64_t)P.gout_ld * 2;
+    const uint64_t drow_bytes = (uint64_t)P.dsrc_ld * 2;
+    const uint64_t gout0 = reinterpret_cast<uint64_t>(P.grad_out);
+    const uint32_t lane_off = (uint32_t)lane * 16;
+    // z: an arrival_zero() of the previous item, added to the lane offsets
+    auto load_row = [&](u32x4(&buf)[NCH], uint64_t addr, uint32_t z) {
+      const char* row = uniform_ptr(addr);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) buf[c] = ldg_global<u32x4>(row + (lane_off + (uint32_t)(c * 1024) + z));
+      // keep the prefetch ahead of the work on the current row
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    u32x4 gnext[NCH], g[NCH], xa[NCH], xb[NCH], keep[S][NCH];
+    const uint32_t rows = (n_tok - tok0 - 1) / nw + 1;
+    uint32_t t = tok0;
+    load_row(gnext, gout0 + (uint64_t)t * grow_bytes, 0u);
+    for (uint32_t r = 0; r < rows; ++r) {
+      t = __builtin_amdgcn_readfirstlane(t);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) g[c] = gnext[c];
+      load_row(xa, reinterpret_cast<uint64_t>(P.src[0]) + (uint64_t)t * row_bytes, arrival_zero(g[NCH - 1][3]));
+      float lg[S], ri[S], gx[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        u32x4(&cur)[NCH] = (s & 1) ? xb : xa;
+        u32x4(&nxt)[NCH] = (s & 1) ? xa : xb;
+        const uint32_t z = arrival_zero(cur[NCH - 1][3]);
+        if (s + 1 < S) {
+          load_row(nxt, reinterpret_cast<uint64_t>(P.src[s + 1]) + (uint64_t)t * row_bytes, z);
+        } else {
+          // the next row's G (past the wave's last row, this row's G again)
+          const uint32_t tn = r + 1 < rows ? t + nw : t;
+          load_row(gnext, gout0 + (uint64_t)tn * grow_bytes, z);
+        }
+        // ---- sum(x^2), x.G and x.qw over this lane's chunks (two chains each) ----
+        float ss0 = 0.f, ss1 = 0.f, gx0 = 0.f, gx1 = 0.f, dt0 = 0.f, dt1 = 0.f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          float q[8];
+          qw_chunk(c, q);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t xw = cur[c][w];
+            if (w & 1) {
+              ss1 = dot2_bf16(xw, xw, ss1);
+              gx1 = dot2_bf16(xw, g[c][w], gx1);
+            } else {
+              ss0 = dot2_bf16(xw, xw, ss0);
+              gx0 = dot2_bf16(xw, g[c][w], gx0);
+            }
+            dt0 = __builtin_fmaf(bf_lo(xw), q[2 * w], dt0);
+            dt1 = __builtin_fmaf(bf_hi(xw), q[2 * w + 1], dt1);
+          }
+          keep[s][c] = cur[c];
+        }
+        const float ss = lane63(wave_sum_to_lane63(ss0 + ss1));
+        const float dt = lane63(wave_sum_to_lane63(dt0 + dt1));
+        gx[s] = lane63(wave_sum_to_lane63(gx0 + gx1));
+        ri[s] = __builtin_amdgcn_rsqf(ss * P.inv_d + P.eps);
+        lg[s] = dt * ri[s];
+      }
+
+      // ---- softmax over the sources and the coefficients (wave-uniform) ----
+      float m = lg[0];
+#pragma unroll
+      for (int s = 1; s < S; ++s) m = lg[s] > m ? lg[s] : m;
+      float ex[S], sum = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        ex[s] = __expf(lg[s] - m);
+        sum += ex[s];
+      }
+      const float rsum = 1.0f / sum;
+      float wgt[S], go = 0.f;  // go = G . out = sum_s w_s (G . x_s)
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        wgt[s] = ex[s] * rsum;
+        go = __builtin_fmaf(wgt[s], gx[s], go);
+      }
+      const float glse = P.grad_lse != nullptr ? P.grad_lse[t] : 0.f;
+      float c1[S], c2[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        // glse is added after G.x_s - G.out cancels (added to G.x_s first it
+        // would be rounded to the ulp of that much larger dot product)
+        c1[s] = wgt[s] * (glse + (gx[s] - go)) * ri[s];
+        c2[s] = -c1[s] * lg[s] * ri[s] * P.inv_d;
+      }
+
+      // ---- the gradient rows, one whole row per source ----
+      // The kept rows are re-expanded here (opaque copies) rather than kept
+      // unpacked from the first pass, which would double their registers.
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) asm volatile("" : "+v"(keep[s][c]));
+        char* drow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.dsrc[s]) + (uint64_t)t * drow_bytes));
+        const __amdgpu_buffer_rsrc_t dr = row_rsrc(drow, (uint32_t)(NCH * 1024));
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          float q[8];
+          qw_chunk(c, q);
+          u32x4 pk;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t xw = keep[s][c][w], gw = g[c][w];
+            const float x0 = bf_lo(xw), x1 = bf_hi(xw);
+            const float d0 = __builtin_fmaf(c2[s], x0, __builtin_fmaf(c1[s], q[2 * w], wgt[s] * bf_lo(gw)));
+            const float d1 = __builtin_fmaf(c2[s], x1, __builtin_fmaf(c1[s], q[2 * w + 1], wgt[s] * bf_hi(gw)));
+            dq[c][2 * w] = __builtin_fmaf(c1[s], x0, dq[c][2 * w]);
+            dq[c][2 * w + 1] = __builtin_fmaf(c1[s], x1, dq[c][2 * w + 1]);
+            pk[w] = pack_bf16(d0, d1);
+          }
+          st_row(dr, lane_off + (uint32_t)(c * 1024), pk);
+        }
+      }
+      t += nw;
+    }
+  }
+
+  // ---- this workgroup's query-gradient partial: the waves' sums through LDS ----
+  __syncthreads();  // every wave is done with the query in LDS
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      bws_lds[wave * ROW4 + slot(c, h)] =
+          make_float4(dq[c][4 * h], dq[c][4 * h + 1], dq[c][4 * h + 2], dq[c][4 * h + 3]);
+  }
+  __syncthreads();
+  float4* prow = reinterpret_cast<float4*>(P.dqw_part + (int64_t)blockIdx.x * P.d);
+  for (int j = tid; j < ROW4; j += (int)blockDim.x) {
+    float4 a = bws_lds[j];
+    for (int w = 1; w < nwv; ++w) {
+      const float4 b = bws_lds[w * ROW4 + j];
+      a.x += b.x;
+      a.y += b.y;
+      a.z += b.z;
+      a.w += b.w;
+    }
+    const int c = j >> 7, h = (j >> 6) & 1, l = j & 63;
+    prow[(c * 64 + l) * 2 + h] = a;
+  }
+}
+
 
 // ------------------------------------------- batched-query backward body --
 //
@@ -3231,7 +3451,20 @@ STREAM_TYPES(8)
   BWD_TYPES(S, 1) \
   BWD_TYPES(S, 2)
 
+// Row-per-wave backward: attnres_route_bwd_stream_c<NCH>_s<S> (bf16 sources
+// and output gradients, rows of NCH KiB), built where the kept source rows
+// (S * NCH * 4 registers) fit the accumulation registers: S * NCH <= 48.
+#define BWD_STREAM_ONE(S, NCH)                                                                          \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))            \
+      attnres_route_bwd_stream_c##NCH##_s##S(attnres_route_bwd_params P) {                               \
+    route_bwd_stream_body<S, NCH>(P);                                                                   \
+  }
+
 #if ATTNRES_PART == 4 || defined(ATTNRES_ALL_PARTS)
+BWD_STREAM_ONE(1, 6) BWD_STREAM_ONE(2, 6) BWD_STREAM_ONE(3, 6) BWD_STREAM_ONE(4, 6)
+BWD_STREAM_ONE(5, 6) BWD_STREAM_ONE(6, 6) BWD_STREAM_ONE(7, 6) BWD_STREAM_ONE(8, 6)
+BWD_STREAM_ONE(1, 8) BWD_STREAM_ONE(2, 8) BWD_STREAM_ONE(3, 8) BWD_STREAM_ONE(4, 8)
+BWD_STREAM_ONE(5, 8) BWD_STREAM_ONE(6, 8)
 BWD_S(1)
 BWD_S(2)
 BWD_S(3)

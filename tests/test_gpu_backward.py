@@ -368,17 +368,27 @@ def test_batched_query_backward_matches_oracle(gpu, monkeypatch, dtype, S, D, B,
         check_grad(gain.grad, dgain, dtype, "dgain (sum over queries)")
 
 
-def test_backward_chunks_per_thread_policy(gpu):
-    # two chunks per thread for 5 <= S <= 8 over many rows of at most 384
-    # chunks (3B prefill shape), one elsewhere (fewer rows, wider rows, S <= 4
-    # or S >= 9, whose two-chunk instances spill from S = 12)
+def _bwd_kernel_name(s, n, d, policy=None):
     import ctypes
 
+    buf = ctypes.create_string_buffer(128)
+    code = _capi.DTYPE_BF16
+    prev = _capi.set_kernel_policy(policy) if policy is not None else None
+    try:
+        _capi.check("attnres_route_bwd_kernel_name",
+                    _capi.lib().attnres_route_bwd_kernel_name(s, n, d, code, code, buf, 128))
+    finally:
+        if prev is not None:
+            _capi.set_kernel_policy(prev)
+    return buf.value.decode()
+
+
+def test_backward_chunks_per_thread_policy(gpu):
+    # row-per-workgroup kernel: two chunks per thread for 5 <= S <= 8 over many
+    # rows of at most 384 chunks (3B prefill shape), one elsewhere (fewer rows,
+    # wider rows, S <= 4 or S >= 9, whose two-chunk instances spill from S = 12)
     def name(s, n, d):
-        buf = ctypes.create_string_buffer(128)
-        code = _capi.DTYPE_BF16
-        _capi.check("attnres_route_bwd_kernel_name", _capi.lib().attnres_route_bwd_kernel_name(s, n, d, code, code, buf, 128))
-        return buf.value.decode()
+        return _bwd_kernel_name(s, n, d, _capi.POLICY_WORKGROUP)
 
     assert name(7, 32768, 3072).endswith("_s7_v2")
     assert name(4, 32768, 3072).endswith("_s4_v1")
@@ -386,6 +396,75 @@ def test_backward_chunks_per_thread_policy(gpu):
     assert name(7, 8192, 3072).endswith("_s7_v1")
     assert name(7, 32768, 4096).endswith("_s7_v1")
     assert name(3, 64, 8192).endswith("_s3_v2")  # rows above 512 chunks: always two
+
+
+def test_backward_row_per_wave_policy(gpu):
+    # under AUTO the row-per-wave kernel takes bf16 calls of >= 2048 rows with
+    # rows of 6 or 8 KiB while the kept rows fit (S * row KiB <= 48)
+    auto = _capi.POLICY_AUTO
+    assert _bwd_kernel_name(7, 32768, 3072, auto) == "attnres_route_bwd_stream_c6_s7"
+    assert _bwd_kernel_name(8, 32768, 3072, auto) == "attnres_route_bwd_stream_c6_s8"
+    assert _bwd_kernel_name(1, 8192, 3072, auto) == "attnres_route_bwd_stream_c6_s1"
+    assert _bwd_kernel_name(6, 16384, 4096, auto) == "attnres_route_bwd_stream_c8_s6"
+    assert _bwd_kernel_name(7, 16384, 4096, auto).endswith("_s7_v1")  # 56 KiB of kept rows
+    assert _bwd_kernel_name(9, 32768, 3072, auto).endswith("_s9_v1")
+    assert _bwd_kernel_name(7, 1000, 3072, auto).endswith("_s7_v1")  # below the row threshold
+    assert _bwd_kernel_name(4, 32768, 2048, auto).endswith("_s4_v1")  # 4 KiB rows
+    assert _bwd_kernel_name(7, 100, 3072, _capi.POLICY_STREAM) == "attnres_route_bwd_stream_c6_s7"
+
+
+# The row-per-wave backward against the oracle: every instance (rows of 6 KiB
+# at S = 1..8, 8 KiB at S = 1..6), row counts that leave waves of the last
+# workgroups without a row or with one row fewer, fewer rows than one
+# workgroup's waves, and fp32 parameters.
+STREAM_BWD = [(3072, s, 1, 3001, None) for s in range(1, 9)] + [(4096, s, 1, 2003, None) for s in range(1, 7)] + \
+    [(3072, 8, 1, 3, None), (3072, 4, 2, 1500, torch.float32), (4096, 6, 1, 5, torch.float32)]
+
+
+@pytest.mark.parametrize("D,S,B,T,pd", STREAM_BWD,
+                         ids=[f"D{c[0]}-S{c[1]}-N{c[2] * c[3]}{'-pf32' if c[4] else ''}" for c in STREAM_BWD])
+def test_row_per_wave_backward_matches_oracle(gpu, D, S, B, T, pd):
+    print(f"row-per-wave backward D={D} S={S} B={B} T={T} param={pd}", flush=True)
+    assert _bwd_kernel_name(S, B * T, D, _capi.POLICY_STREAM) == f"attnres_route_bwd_stream_c{D // 512}_s{S}"
+    buf, query, gain, G = make_case(gpu, S, 1, B, T, D, torch.bfloat16, seed=300 + S + D + T, param_dtype=pd)
+    buf.requires_grad_(True)
+    query.requires_grad_(True)
+    norm = Norm(gain.clone(), 1e-5)
+    mask = torch.zeros(S + 1, dtype=torch.bool, device=gpu)
+    mask[:S] = True
+    prev = _capi.set_kernel_policy(_capi.POLICY_STREAM)
+    try:
+        out = kotodama_amd.route_static(buf, query, norm, mask, S)
+        (out.float() * G).sum().backward()
+        torch.cuda.synchronize()
+    finally:
+        _capi.set_kernel_policy(prev)
+    dx, dq, dg = oracle_grads(buf, S, query, norm.weight, G, 1e-5, pd or torch.bfloat16)
+    check_grad(buf.grad[:S].reshape(S, -1, D), dx, torch.bfloat16, "dsources")
+    assert torch.all(buf.grad[S:] == 0), "inactive slot must get zero gradient"
+    check_grad(query.grad, dq, query.dtype, "dquery")
+    check_grad(norm.weight.grad, dg, query.dtype, "dgain")
+
+
+@pytest.mark.parametrize("S", [1, 5, 8])
+def test_row_per_wave_backward_with_lse_gradient(gpu, S):
+    print(f"row-per-wave backward with dL/dlse S={S}", flush=True)
+    buf, query, gain, G = make_case(gpu, S, 0, 2, 1100, 3072, torch.bfloat16, seed=77 + S)
+    buf.requires_grad_(True)
+    query.requires_grad_(True)
+    norm = Norm(gain.clone(), 1e-5)
+    gl = torch.randn(2, 1100, device=gpu)
+    prev = _capi.set_kernel_policy(_capi.POLICY_STREAM)
+    try:
+        res = ops.route(buf, S, query, norm.weight, 1e-5, torch.bfloat16, True, False)
+        (res[0][0].float() * G).sum().add_((res[2][0] * gl).sum()).backward()
+        torch.cuda.synchronize()
+    finally:
+        _capi.set_kernel_policy(prev)
+    dx, dq, dg = oracle_grads(buf, S, query, norm.weight, G, 1e-5, torch.bfloat16, grad_lse=gl)
+    check_grad(buf.grad.reshape(S, -1, 3072), dx, torch.bfloat16, "dsources")
+    check_grad(query.grad, dq, torch.bfloat16, "dquery")
+    check_grad(norm.weight.grad, dg, torch.bfloat16, "dgain")
 
 
 def test_batched_query_backward_without_lse_gradient(gpu):
@@ -525,8 +604,9 @@ def test_mixed_param_dtypes_backward(gpu):
     check_grad(query.grad, b["dqw"] * np64(norm.weight), torch.float32, "dquery")
 
 
-def test_query_gradient_is_deterministic(gpu):
-    S, B, T, D = 8, 4, 512, 4096
+@pytest.mark.parametrize("D", [4096, 3072], ids=["workgroup", "row_per_wave"])
+def test_query_gradient_is_deterministic(gpu, D):
+    S, B, T = 8, 4, 512
     buf, query, gain, G = make_case(gpu, S, 0, B, T, D, torch.bfloat16, seed=5)
     res = []
     for _ in range(2):
@@ -562,16 +642,23 @@ def test_capi_backward_argument_errors(gpu):
 
 
 @pytest.mark.parametrize("S", [5, 8])
-def test_full_size_3b_backward_properties(gpu, S):
-    # the 3B prefill shape (B=8, T=4096, D=3072), bf16, at two source counts that run
-    # the two-chunks-per-thread kernel (checked through the kernel-name query)
-    import ctypes
-
+@pytest.mark.parametrize("kernel", ["row_per_wave", "workgroup"])
+def test_full_size_3b_backward_properties(gpu, S, kernel):
+    # the 3B prefill shape (B=8, T=4096, D=3072), bf16, at two source counts, through
+    # the row-per-wave kernel (AUTO) and the two-chunks-per-thread workgroup kernel
+    # (checked through the kernel-name query)
     w = workloads.get("cfg2")
-    kn = ctypes.create_string_buffer(128)
-    _capi.check("attnres_route_bwd_kernel_name", _capi.lib().attnres_route_bwd_kernel_name(
-        S, w.tokens, w.hidden, _capi.DTYPE_BF16, _capi.DTYPE_BF16, kn, 128))
-    assert kn.value.decode().endswith(f"_s{S}_v2")
+    policy = _capi.POLICY_AUTO if kernel == "row_per_wave" else _capi.POLICY_WORKGROUP
+    want = f"attnres_route_bwd_stream_c6_s{S}" if kernel == "row_per_wave" else f"attnres_route_bwd_bf_gbf_s{S}_v2"
+    assert _bwd_kernel_name(S, w.tokens, w.hidden, policy) == want
+    prev = _capi.set_kernel_policy(policy)
+    try:
+        _full_size_3b_backward(gpu, w, S)
+    finally:
+        _capi.set_kernel_policy(prev)
+
+
+def _full_size_3b_backward(gpu, w, S):
     pool = workloads.make_pool(w, gpu, 3)
     q, gn = workloads.make_params(w, gpu, 3, 1)
     eps = w.eps

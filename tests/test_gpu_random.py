@@ -166,6 +166,53 @@ def test_random_route_forward_backward(gpu, seed):
 
 
 @pytest.mark.parametrize("seed", range(SEEDS or 8))
+def test_random_row_per_wave_backward(gpu, seed):
+    # the row-per-wave backward's shapes (bf16, rows of 6 or 8 KiB, S * row KiB <= 48)
+    # with random row counts, parameter dtype, gain, softmax peakedness and dL/dlse
+    rng = np.random.default_rng(9000 + seed)
+    D = [3072, 4096][int(rng.integers(2))]
+    S = int(rng.integers(1, 48 // (D // 512) + 1))
+    N = _rows(rng, S * D)
+    pdt = [torch.bfloat16, torch.float32][int(rng.integers(2))]
+    with_gain = bool(rng.integers(2))
+    # dL/dlse with bf16 parameters only (the fp32 comparator below has no lse term)
+    with_lse = bool(rng.integers(2)) and pdt == torch.bfloat16
+    qscale = [0.05, 0.5][int(rng.integers(2))]
+    print(f"random row-per-wave backward seed={seed}: S={S} D={D} N={N} param={pdt} gain={with_gain} "
+          f"lse={with_lse} qscale={qscale}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(9500 + seed)
+    scales = torch.exp(torch.empty(S).uniform_(np.log(0.25), np.log(4.0), generator=g))
+    buf = (torch.randn(S, 1, N, D, generator=g) * scales[:, None, None, None]).to(torch.bfloat16).to(gpu)
+    buf.requires_grad_(True)
+    query = (torch.randn(D, generator=g) * qscale).to(pdt).to(gpu).requires_grad_(True)
+    gain = (1 + 0.1 * torch.randn(D, generator=g)).to(pdt).to(gpu) if with_gain else torch.ones(D, dtype=pdt).to(gpu)
+    norm = Norm(gain.clone(), 1e-5)
+    norm.weight.requires_grad_(with_gain)
+    G = torch.randn(1, N, D, generator=g).to(torch.bfloat16).float().to(gpu)
+    gl = (torch.randn(1, N, generator=g) * 0.3).to(gpu) if with_lse else None
+
+    def run():
+        res = ops.route(buf, S, query, norm.weight, 1e-5, torch.bfloat16, True, False)
+        loss = (res[0][0].float() * G).sum()
+        if gl is not None:
+            loss = loss + (res[2][0] * gl).sum()
+        loss.backward()
+        torch.cuda.synchronize()
+
+    _with_policy(_capi.POLICY_STREAM, run)
+    pd = "bf16" if pdt == torch.bfloat16 else "f32"
+    qw = O.fold_query(np64(query), np64(norm.weight), pd)
+    x = np64(buf).reshape(S, N, D)
+    b = O.route_backward(x, qw, 1e-5, np64(G).reshape(N, D), None if gl is None else np64(gl).reshape(N))
+    check_grad(buf.grad.reshape(S, N, D), b["dx"], torch.bfloat16, f"seed {seed} dsources")
+    if pdt == torch.float32:
+        f32 = _route_f32_grads(x, np64(query), np64(norm.weight), 1e-5, np64(G).reshape(N, D))
+        check_grad_f32(query.grad, b["dqw"] * np64(norm.weight), f32[1], f"seed {seed} dquery")
+    else:
+        check_grad(query.grad, b["dqw"] * np64(norm.weight), pdt, f"seed {seed} dquery")
+
+
+@pytest.mark.parametrize("seed", range(SEEDS or 8))
 def test_random_merge_forward_backward(gpu, seed):
     rng = np.random.default_rng(3000 + seed)
     pdt = [torch.bfloat16, torch.float32][int(rng.integers(2))]

@@ -109,7 +109,26 @@ def test_route_fwd_row_strides(gpu, label, S, n, d, sdt, qdt, Q, separate, suffi
 @pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
 @pytest.mark.parametrize("S", [3, 6])
 def test_route_bwd_row_strides(gpu, sdt, S):
-    n, d = 300, 2048
+    _route_bwd_strided(gpu, sdt, S, 300, 2048)
+
+
+@pytest.mark.parametrize("S,n", [(2, 777), (8, 1029)])
+def test_route_bwd_row_per_wave_row_strides(gpu, S, n):
+    # the row-per-wave backward (bf16, rows of 6 KiB) over padded rows and
+    # separate gradient rows: its whole-row loads and stores stay inside each row
+    kn = ctypes.create_string_buffer(128)
+    prev = _capi.set_kernel_policy(_capi.POLICY_STREAM)
+    try:
+        _capi.check("attnres_route_bwd_kernel_name", _capi.lib().attnres_route_bwd_kernel_name(
+            S, n, 3072, _capi.DTYPE_BF16, _capi.DTYPE_BF16, kn, 128))
+        assert kn.value.decode() == f"attnres_route_bwd_stream_c6_s{S}"
+        _route_bwd_strided(gpu, torch.bfloat16, S, n, 3072)
+    finally:
+        _capi.set_kernel_policy(prev)
+
+
+def _route_bwd_strided(gpu, sdt, S, n, d):
+    print(f"route_bwd strided {sdt} S={S} n={n} d={d}", flush=True)
     src_ld, gout_ld, grad_ld = d + 64, d + 128, d + 32
     g = torch.Generator(device=gpu).manual_seed(S * 7 + (sdt == torch.float32))
     big = torch.full((S, n, src_ld), CANARY, device=gpu, dtype=sdt)
