@@ -52,13 +52,15 @@ int attnres_max_sources(void);
 /* Message for the last failed call on this thread ("" if none). */
 const char* attnres_last_error(void);
 
-/* Kernel family used by attnres_route_fwd / attnres_block_step (process-wide). */
+/* Kernel family used by attnres_route_fwd / attnres_block_step / attnres_merge_fwd /
+ * attnres_route_bwd (process-wide). */
 #define ATTNRES_POLICY_AUTO 0      /* streaming kernel for large launches, else workgroup kernel */
 #define ATTNRES_POLICY_WORKGROUP 1 /* one workgroup per token row, sources held in registers */
 #define ATTNRES_POLICY_STREAM 2    /* one wave per token row, sources streamed (where the shape allows) */
 
 /*
- * Select the kernel family of routing and merge calls; returns the previous
+ * Select the kernel family of routing, merge and single-query routing
+ * backward calls (row per workgroup or row per wave); returns the previous
  * policy (or ATTNRES_ERR_ARG).  Both families compute the same function; AUTO
  * picks by launch size.  A tuning and testing switch with no counterpart in
  * the reference.
