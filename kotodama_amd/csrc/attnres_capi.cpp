@@ -97,7 +97,7 @@ struct DeviceState {
   int merge_bpc[kMergeFuncs] = {};
   int merge_bpc_block[kMergeFuncs] = {};
   hipFunction_t bwd[kBwdFuncs] = {};
-  hipFunction_t bwd_stream[2 * 9] = {};  // row-per-wave backward: rows of 6 / 8 KiB x S
+  hipFunction_t bwd_stream[2 * 10] = {};  // row-per-wave backward: rows of 6 / 8 KiB x S (1..9)
   int bwd_bpc[kBwdFuncs] = {};
   int bwd_bpc_block[kBwdFuncs] = {};
   ReduceFns reduce;
@@ -395,24 +395,33 @@ int get_bwd(DeviceState& st, bool bf, bool gbf, int s, int v, int block, size_t 
 }
 
 // Row-per-wave backward (code-object part 4): bf16 sources and output
-// gradients, rows of 6 or 8 KiB (hidden 3072 / 4096), S * (row KiB) <= 48 so
-// the kept source rows fit the registers; a grid of one 4-wave workgroup per
-// CU.  Chosen like the forward streaming kernel: by the kernel policy, and
-// under AUTO for calls of at least the streaming threshold's rows.
+// gradients, rows of 6 KiB (hidden 3072, S <= 8, source rows kept in
+// registers) or 8 KiB (hidden 4096, S <= 9; from S = 7 the first S - 6 rows
+// kept in LDS); a grid of one 4-wave workgroup per CU.  Chosen by the kernel
+// policy; under AUTO for 6 KiB rows and calls of at least the streaming
+// threshold's rows (1-7% faster than the row-per-workgroup kernel at every S
+// of the 3B shape; at 8 KiB rows it measured the same within 1-2%, and 19%
+// slower at S = 2, so AUTO keeps the workgroup kernel there).
 constexpr int kBwdStreamWaves = 4;
 int bwd_stream_nch(bool bf, bool gbf, int num_sources, int hidden, int64_t num_tokens) {
   if (!bf || !gbf || hidden % 512 != 0) return 0;
   const int nch = hidden / 512;
-  if ((nch != 6 && nch != 8) || num_sources < 1 || num_sources * nch > 48) return 0;
+  if ((nch != 6 && nch != 8) || num_sources < 1 || num_sources > (nch == 6 ? 8 : 9)) return 0;
   if (num_tokens >= (int64_t)1 << 31) return 0;  // 32-bit row counters
   const int policy = g_policy.load(std::memory_order_relaxed);
   const int want = policy == ATTNRES_POLICY_STREAM ? 1 : policy == ATTNRES_POLICY_WORKGROUP ? 0 : tuning().stream;
-  return want == 1 || (want < 0 && num_tokens >= tuning().stream_min_tokens) ? nch : 0;
+  return want == 1 || (want < 0 && nch == 6 && num_tokens >= tuning().stream_min_tokens) ? nch : 0;
 }
-size_t bwd_stream_lds(int nch) { return (size_t)kBwdStreamWaves * (size_t)nch * 2048; }
+// the query (nch * 2 KiB) and the LDS-kept rows, or at the end the waves' query-gradient rows
+size_t bwd_stream_lds(int nch, int num_sources) {
+  const size_t kl = num_sources > 48 / nch ? (size_t)(num_sources - 48 / nch) : 0;
+  const size_t run = (size_t)nch * 2048 + (size_t)kBwdStreamWaves * kl * (size_t)nch * 1024;
+  const size_t end = (size_t)kBwdStreamWaves * (size_t)nch * 2048;
+  return run > end ? run : end;
+}
 
 int get_bwd_stream(DeviceState& st, int nch, int s, hipFunction_t* f) {
-  const int idx = (nch == 8 ? 9 : 0) + s;
+  const int idx = (nch == 8 ? 10 : 0) + s;
   std::lock_guard<std::mutex> lk(g_mu);
   if (st.bwd_stream[idx] == nullptr) {
     char name[96];
@@ -1250,10 +1259,10 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
     const int64_t need_wg = (num_tokens + kBwdStreamWaves - 1) / kBwdStreamWaves;
     const int64_t cap = (int64_t)st->num_cus * (tuning().bwd_per_cu > 0 ? tuning().bwd_per_cu : 1);
     const int grid = (int)(need_wg < cap ? need_wg : cap);
-    return route_bwd_finish(f, grid, 64 * kBwdStreamWaves, bwd_stream_lds(snch), *st, nchunk, sources, num_sources,
-                            num_tokens, hidden, src_ld, query, gain, param_dtype, eps, grad_out, grad_out_dtype,
-                            grad_out_ld, grad_lse, grad_sources, grad_ld, workspace, workspace_bytes, grad_query,
-                            grad_gain, stream);
+    return route_bwd_finish(f, grid, 64 * kBwdStreamWaves, bwd_stream_lds(snch, num_sources), *st, nchunk, sources,
+                            num_sources, num_tokens, hidden, src_ld, query, gain, param_dtype, eps, grad_out,
+                            grad_out_dtype, grad_out_ld, grad_lse, grad_sources, grad_ld, workspace, workspace_bytes,
+                            grad_query, grad_gain, stream);
   }
   const int v = bwd_chunks_per_thread(nchunk, num_sources, num_tokens, st->num_cus);
   const int block = v == 1 ? round64(nchunk) : round64((nchunk + 1) / 2);

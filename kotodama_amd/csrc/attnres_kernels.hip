@@ -1984,8 +1984,9 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
 // x_0 .. x_{S-1}.  Per source the lane forms sum(x^2) and x.G (v_dot2 on the
 // packed words) and x.qw (fp32 qw from LDS) over its chunks, three DPP wave
 // sums give the row's values, and the packed source row is kept in registers
-// (S * NCH * 4 of them, which at one wave per SIMD the compiler places in the
-// accumulation half of the register file).  After the last source the softmax
+// ((S - KL) * NCH * 4 of them, which at one wave per SIMD the compiler places
+// partly in the accumulation half of the register file) or, for the first KL
+// sources, in the wave's part of the LDS.  After the last source the softmax
 // and the coefficients are formed wave-uniformly, and each gradient row
 //   dx_s = w_s G + c1_s qw + c2_s x_s,
 //   c1_s = dl_s r_s,  c2_s = -dl_s l_s r_s^2 / D,  dl_s = w_s (g_lse + G.x_s - G.out),
@@ -1993,11 +1994,15 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
 // The query gradient sum_s c1_s x_s accumulates per lane over the wave's
 // rows; at the end the workgroup's waves add theirs through LDS in a fixed
 // order and write one fp32 partial row per workgroup, as route_bwd_body does.
-template <int S, int NCH>
+// KL > 0: the first KL source rows are kept in the wave's part of the
+// dynamic LDS instead of registers (more sources than the registers hold).
+template <int S, int NCH, int KL>
 __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_params& P) {
+  static_assert(KL >= 0 && KL < S, "at least one source row is kept in registers");
   // Dynamic LDS in float4 slots [chunk][half][lane] (consecutive lanes 16
-  // bytes apart): the folded query in fp32, then at the end one such row of
-  // query-gradient sums per wave.
+  // bytes apart): the folded query in fp32 and, past it, each wave's KL kept
+  // rows ([wave][row][chunk][lane], 16-byte slots); at the end one row of
+  // query-gradient sums per wave from the start.
   extern __shared__ float4 bws_lds[];
   constexpr int ROW4 = NCH * 2 * 64;  // float4 slots of one row
   const int tid = threadIdx.x;
@@ -2061,7 +2066,8 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
       // keep the prefetch ahead of the work on the current row
       __builtin_amdgcn_sched_barrier(0);
     };
-    u32x4 gnext[NCH], g[NCH], xa[NCH], xb[NCH], keep[S][NCH];
+    u32x4 gnext[NCH], g[NCH], xa[NCH], xb[NCH], keep[S - KL][NCH];
+    u32x4* kept_lds = reinterpret_cast<u32x4*>(bws_lds) + ROW4 + (wave * KL) * NCH * 64 + lane;
     const uint32_t rows = (n_tok - tok0 - 1) / nw + 1;
     uint32_t t = tok0;
     load_row(gnext, gout0 + (uint64_t)t * grow_bytes, 0u);
@@ -2102,7 +2108,8 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
             dt0 = __builtin_fmaf(bf_lo(xw), q[2 * w], dt0);
             dt1 = __builtin_fmaf(bf_hi(xw), q[2 * w + 1], dt1);
           }
-          keep[s][c] = cur[c];
+          if (s < KL) kept_lds[(s * NCH + c) * 64] = cur[c];
+          else keep[s >= KL ? s - KL : 0][c] = cur[c];
         }
         const float ss = lane63(wave_sum_to_lane63(ss0 + ss1));
         const float dt = lane63(wave_sum_to_lane63(dt0 + dt1));
@@ -2143,8 +2150,16 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
       // unpacked from the first pass, which would double their registers.
 #pragma unroll
       for (int s = 0; s < S; ++s) {
+        u32x4 xk[NCH];
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) asm volatile("" : "+v"(keep[s][c]));
+        for (int c = 0; c < NCH; ++c) {
+          if (s < KL) {
+            xk[c] = kept_lds[(s * NCH + c) * 64];
+          } else {
+            xk[c] = keep[s >= KL ? s - KL : 0][c];
+            asm volatile("" : "+v"(xk[c]));
+          }
+        }
         char* drow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.dsrc[s]) + (uint64_t)t * drow_bytes));
         const __amdgpu_buffer_rsrc_t dr = row_rsrc(drow, (uint32_t)(NCH * 1024));
 #pragma unroll
@@ -2154,7 +2169,7 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
           u32x4 pk;
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
-            const uint32_t xw = keep[s][c][w], gw = g[c][w];
+            const uint32_t xw = xk[c][w], gw = g[c][w];
             const float x0 = bf_lo(xw), x1 = bf_hi(xw);
             const float d0 = __builtin_fmaf(c2[s], x0, __builtin_fmaf(c1[s], q[2 * w], wgt[s] * bf_lo(gw)));
             const float d1 = __builtin_fmaf(c2[s], x1, __builtin_fmaf(c1[s], q[2 * w + 1], wgt[s] * bf_hi(gw)));
@@ -3452,19 +3467,22 @@ STREAM_TYPES(8)
   BWD_TYPES(S, 2)
 
 // Row-per-wave backward: attnres_route_bwd_stream_c<NCH>_s<S> (bf16 sources
-// and output gradients, rows of NCH KiB), built where the kept source rows
-// (S * NCH * 4 registers) fit the accumulation registers: S * NCH <= 48.
-#define BWD_STREAM_ONE(S, NCH)                                                                          \
+// and output gradients, rows of NCH KiB).  Up to 48 / NCH source rows are
+// kept in registers (S * NCH * 4 of them, partly in the accumulation
+// registers); the 8 KiB instances with S = 7..9 keep their first KL = S - 6
+// rows in LDS (KL * 8 KiB per wave).
+#define BWD_STREAM_ONE(S, NCH, KL)                                                                      \
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))            \
       attnres_route_bwd_stream_c##NCH##_s##S(attnres_route_bwd_params P) {                               \
-    route_bwd_stream_body<S, NCH>(P);                                                                   \
+    route_bwd_stream_body<S, NCH, KL>(P);                                                               \
   }
 
 #if ATTNRES_PART == 4 || defined(ATTNRES_ALL_PARTS)
-BWD_STREAM_ONE(1, 6) BWD_STREAM_ONE(2, 6) BWD_STREAM_ONE(3, 6) BWD_STREAM_ONE(4, 6)
-BWD_STREAM_ONE(5, 6) BWD_STREAM_ONE(6, 6) BWD_STREAM_ONE(7, 6) BWD_STREAM_ONE(8, 6)
-BWD_STREAM_ONE(1, 8) BWD_STREAM_ONE(2, 8) BWD_STREAM_ONE(3, 8) BWD_STREAM_ONE(4, 8)
-BWD_STREAM_ONE(5, 8) BWD_STREAM_ONE(6, 8)
+BWD_STREAM_ONE(1, 6, 0) BWD_STREAM_ONE(2, 6, 0) BWD_STREAM_ONE(3, 6, 0) BWD_STREAM_ONE(4, 6, 0)
+BWD_STREAM_ONE(5, 6, 0) BWD_STREAM_ONE(6, 6, 0) BWD_STREAM_ONE(7, 6, 0) BWD_STREAM_ONE(8, 6, 0)
+BWD_STREAM_ONE(1, 8, 0) BWD_STREAM_ONE(2, 8, 0) BWD_STREAM_ONE(3, 8, 0) BWD_STREAM_ONE(4, 8, 0)
+BWD_STREAM_ONE(5, 8, 0) BWD_STREAM_ONE(6, 8, 0) BWD_STREAM_ONE(7, 8, 1) BWD_STREAM_ONE(8, 8, 2)
+BWD_STREAM_ONE(9, 8, 3)
 BWD_S(1)
 BWD_S(2)
 BWD_S(3)

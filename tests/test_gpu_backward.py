@@ -399,14 +399,16 @@ def test_backward_chunks_per_thread_policy(gpu):
 
 
 def test_backward_row_per_wave_policy(gpu):
-    # under AUTO the row-per-wave kernel takes bf16 calls of >= 2048 rows with
-    # rows of 6 or 8 KiB while the kept rows fit (S * row KiB <= 48)
-    auto = _capi.POLICY_AUTO
+    # under AUTO the row-per-wave kernel takes bf16 calls of >= 2048 rows of 6 KiB
+    # with S <= 8; its 8 KiB instances (S <= 9) run under the STREAM policy
+    auto, stream = _capi.POLICY_AUTO, _capi.POLICY_STREAM
     assert _bwd_kernel_name(7, 32768, 3072, auto) == "attnres_route_bwd_stream_c6_s7"
     assert _bwd_kernel_name(8, 32768, 3072, auto) == "attnres_route_bwd_stream_c6_s8"
     assert _bwd_kernel_name(1, 8192, 3072, auto) == "attnres_route_bwd_stream_c6_s1"
-    assert _bwd_kernel_name(6, 16384, 4096, auto) == "attnres_route_bwd_stream_c8_s6"
-    assert _bwd_kernel_name(7, 16384, 4096, auto).endswith("_s7_v1")  # 56 KiB of kept rows
+    assert _bwd_kernel_name(6, 16384, 4096, auto).endswith("_s6_v1")
+    assert _bwd_kernel_name(6, 16384, 4096, stream) == "attnres_route_bwd_stream_c8_s6"
+    assert _bwd_kernel_name(9, 16384, 4096, stream) == "attnres_route_bwd_stream_c8_s9"
+    assert _bwd_kernel_name(10, 16384, 4096, stream).endswith("_s10_v1")
     assert _bwd_kernel_name(9, 32768, 3072, auto).endswith("_s9_v1")
     assert _bwd_kernel_name(7, 1000, 3072, auto).endswith("_s7_v1")  # below the row threshold
     assert _bwd_kernel_name(4, 32768, 2048, auto).endswith("_s4_v1")  # 4 KiB rows
@@ -414,11 +416,13 @@ def test_backward_row_per_wave_policy(gpu):
 
 
 # The row-per-wave backward against the oracle: every instance (rows of 6 KiB
-# at S = 1..8, 8 KiB at S = 1..6), row counts that leave waves of the last
-# workgroups without a row or with one row fewer, fewer rows than one
-# workgroup's waves, and fp32 parameters.
+# at S = 1..8, 8 KiB at S = 1..9, the last three with rows kept in LDS), row
+# counts that leave waves of the last workgroups without a row or with one row
+# fewer, fewer rows than one workgroup's waves, and fp32 parameters.
 STREAM_BWD = [(3072, s, 1, 3001, None) for s in range(1, 9)] + [(4096, s, 1, 2003, None) for s in range(1, 7)] + \
-    [(3072, 8, 1, 3, None), (3072, 4, 2, 1500, torch.float32), (4096, 6, 1, 5, torch.float32)]
+    [(4096, s, 1, 1500, None) for s in range(7, 10)] + \
+    [(3072, 8, 1, 3, None), (3072, 4, 2, 1500, torch.float32), (4096, 6, 1, 5, torch.float32),
+     (4096, 9, 1, 7, torch.float32)]
 
 
 @pytest.mark.parametrize("D,S,B,T,pd", STREAM_BWD,

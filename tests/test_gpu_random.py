@@ -167,11 +167,11 @@ def test_random_route_forward_backward(gpu, seed):
 
 @pytest.mark.parametrize("seed", range(SEEDS or 8))
 def test_random_row_per_wave_backward(gpu, seed):
-    # the row-per-wave backward's shapes (bf16, rows of 6 or 8 KiB, S * row KiB <= 48)
-    # with random row counts, parameter dtype, gain, softmax peakedness and dL/dlse
+    # the row-per-wave backward's shapes (bf16, rows of 6 KiB with S <= 8 or 8 KiB with
+    # S <= 9) with random row counts, parameter dtype, gain, softmax peakedness and dL/dlse
     rng = np.random.default_rng(9000 + seed)
     D = [3072, 4096][int(rng.integers(2))]
-    S = int(rng.integers(1, 48 // (D // 512) + 1))
+    S = int(rng.integers(1, (8 if D == 3072 else 9) + 1))
     N = _rows(rng, S * D)
     pdt = [torch.bfloat16, torch.float32][int(rng.integers(2))]
     with_gain = bool(rng.integers(2))
