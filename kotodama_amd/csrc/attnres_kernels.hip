@@ -37,7 +37,11 @@
 //   * attnres_route_bwd_* / _mq_ / _mqg_ / _dqw* / merge_bwd / reduce_dqw*:
 //     the backward of routing and merge (source, query and gain gradients;
 //     the query gradient summed over rows in a fixed order), the batched-
-//     query forms again on the matrix cores.
+//     query forms again on the matrix cores.  attnres_route_bwd_stream_* is
+//     the routing backward with one wave per token row (the training shapes'
+//     bf16 rows of 6 KiB): the row's G and source rows stream through the
+//     same two-slot pipeline, the source rows are kept in registers, and the
+//     gradient rows are stored whole after the row's softmax.
 //
 // S is a template parameter of the row-per-workgroup kernels (register arrays
 // stay in VGPRs) and a runtime argument of the streaming ones; the last slot
