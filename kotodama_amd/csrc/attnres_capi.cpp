@@ -398,19 +398,21 @@ int get_bwd(DeviceState& st, bool bf, bool gbf, int s, int v, int block, size_t 
 // gradients, rows of 6 KiB (hidden 3072, S <= 8, source rows kept in
 // registers) or 8 KiB (hidden 4096, S <= 9; from S = 7 the first S - 6 rows
 // kept in LDS); a grid of one 4-wave workgroup per CU.  Chosen by the kernel
-// policy; under AUTO for 6 KiB rows and calls of at least the streaming
-// threshold's rows (1-7% faster than the row-per-workgroup kernel at every S
-// of the 3B shape; at 8 KiB rows it measured the same within 1-2%, and 19%
-// slower at S = 2, so AUTO keeps the workgroup kernel there).
+// policy; under AUTO for 6 KiB rows and at least 64 rows per CU (16 per
+// wave).  Against the row-per-workgroup kernel it measured 1-7% faster at
+// every S at 128 rows per CU (the 3B prefill shape), even to 3.5% faster at
+// 64, mixed at 32 (up to 5% slower at S <= 5) and up to 6% slower at 16; at
+// 8 KiB rows the same within 1-2% and 19% slower at S = 2, so AUTO keeps the
+// workgroup kernel there.
 constexpr int kBwdStreamWaves = 4;
-int bwd_stream_nch(bool bf, bool gbf, int num_sources, int hidden, int64_t num_tokens) {
+int bwd_stream_nch(bool bf, bool gbf, int num_sources, int hidden, int64_t num_tokens, int num_cus) {
   if (!bf || !gbf || hidden % 512 != 0) return 0;
   const int nch = hidden / 512;
   if ((nch != 6 && nch != 8) || num_sources < 1 || num_sources > (nch == 6 ? 8 : 9)) return 0;
   if (num_tokens >= (int64_t)1 << 31) return 0;  // 32-bit row counters
   const int policy = g_policy.load(std::memory_order_relaxed);
   const int want = policy == ATTNRES_POLICY_STREAM ? 1 : policy == ATTNRES_POLICY_WORKGROUP ? 0 : tuning().stream;
-  return want == 1 || (want < 0 && nch == 6 && num_tokens >= tuning().stream_min_tokens) ? nch : 0;
+  return want == 1 || (want < 0 && nch == 6 && num_tokens >= 64LL * num_cus) ? nch : 0;
 }
 // the query (nch * 2 KiB) and the LDS-kept rows, or at the end the waves' query-gradient rows
 size_t bwd_stream_lds(int nch, int num_sources) {
@@ -991,7 +993,8 @@ int attnres_route_bwd_kernel_name(int num_sources, int64_t num_tokens, int hidde
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
-  const int nch = bwd_stream_nch(bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, hidden, num_tokens);
+  const int nch =
+      bwd_stream_nch(bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, hidden, num_tokens, st->num_cus);
   if (nch > 0) {
     snprintf(buf, (size_t)buf_len, "attnres_route_bwd_stream_c%d_s%d", nch, num_sources);
     return ATTNRES_OK;
@@ -1251,7 +1254,8 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
-  const int snch = bwd_stream_nch(bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, hidden, num_tokens);
+  const int snch =
+      bwd_stream_nch(bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, hidden, num_tokens, st->num_cus);
   if (snch > 0) {
     hipFunction_t f = nullptr;
     rc = get_bwd_stream(*st, snch, num_sources, &f);

@@ -399,12 +399,14 @@ def test_backward_chunks_per_thread_policy(gpu):
 
 
 def test_backward_row_per_wave_policy(gpu):
-    # under AUTO the row-per-wave kernel takes bf16 calls of >= 2048 rows of 6 KiB
-    # with S <= 8; its 8 KiB instances (S <= 9) run under the STREAM policy
+    # under AUTO the row-per-wave kernel takes bf16 calls of >= 64 rows per CU of
+    # 6 KiB with S <= 8; its 8 KiB instances (S <= 9) run under the STREAM policy
     auto, stream = _capi.POLICY_AUTO, _capi.POLICY_STREAM
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
     assert _bwd_kernel_name(7, 32768, 3072, auto) == "attnres_route_bwd_stream_c6_s7"
     assert _bwd_kernel_name(8, 32768, 3072, auto) == "attnres_route_bwd_stream_c6_s8"
-    assert _bwd_kernel_name(1, 8192, 3072, auto) == "attnres_route_bwd_stream_c6_s1"
+    assert _bwd_kernel_name(1, 64 * cus, 3072, auto) == "attnres_route_bwd_stream_c6_s1"
+    assert _bwd_kernel_name(5, 64 * cus - 1, 3072, auto).endswith("_s5_v1")
     assert _bwd_kernel_name(6, 16384, 4096, auto).endswith("_s6_v1")
     assert _bwd_kernel_name(6, 16384, 4096, stream) == "attnres_route_bwd_stream_c8_s6"
     assert _bwd_kernel_name(9, 16384, 4096, stream) == "attnres_route_bwd_stream_c8_s9"
@@ -611,13 +613,21 @@ def test_mixed_param_dtypes_backward(gpu):
 @pytest.mark.parametrize("D", [4096, 3072], ids=["workgroup", "row_per_wave"])
 def test_query_gradient_is_deterministic(gpu, D):
     S, B, T = 8, 4, 512
+    policy = _capi.POLICY_STREAM if D == 3072 else _capi.POLICY_WORKGROUP
+    want = "attnres_route_bwd_stream_c6_s8" if D == 3072 else "attnres_route_bwd_bf_gbf_s8_v1"
+    assert _bwd_kernel_name(S, B * T, D, policy) == want
     buf, query, gain, G = make_case(gpu, S, 0, B, T, D, torch.bfloat16, seed=5)
     res = []
-    for _ in range(2):
-        q = query.clone().requires_grad_(True)
-        out = kotodama_amd.route_static(buf, q, Norm(gain.clone(), 1e-5), torch.ones(S, dtype=torch.bool, device=gpu), S)
-        (out.float() * G).sum().backward()
-        res.append(q.grad.clone())
+    prev = _capi.set_kernel_policy(policy)
+    try:
+        for _ in range(2):
+            q = query.clone().requires_grad_(True)
+            out = kotodama_amd.route_static(buf, q, Norm(gain.clone(), 1e-5),
+                                            torch.ones(S, dtype=torch.bool, device=gpu), S)
+            (out.float() * G).sum().backward()
+            res.append(q.grad.clone())
+    finally:
+        _capi.set_kernel_policy(prev)
     assert torch.equal(res[0], res[1])
 
 
