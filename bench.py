@@ -14,11 +14,14 @@ Also on the JSON line:
 * ``cfg3`` — the 8B prefill shape (S=9, D=4096, B=4, T=4096, 8 calls),
   measured in the same run with the same steps: step time, GB/s and its own
   ``roofline`` block for the S=9 kernel.
+* ``cfg5`` — the 3B data-driven blocks (57 calls, S=1..7, B=2), the same way.
+* ``cfg2_bwd`` — the backward of cfg2's 57 routing calls (the training path):
+  (2S+1) rows per call, with a ``roofline`` block for the S=8 backward.
 * ``cpu_baseline`` — the reference's CPU routing path (oracle/torch_cpu_path:
   the einsum-branch op sequence over the padded buffer, fp32) timed on this
-  host on a bounded sample (one call per distinct S at 2048 tokens),
-  extrapolated to the full step; with the threads used, the host's logical
-  CPUs, the CPUs this process may use and the CPU model.
+  host on a bounded sample (the whole call schedule over 4096 token rows, at
+  least 5 passes, the median), extrapolated to the full step; with the threads
+  used, the host's logical CPUs, the CPUs this process may use and the CPU model.
 
 ``--workload cfg3|cfg4|cfg5`` measures the other shapes (cfg4 = 8B decode step,
 65 fused block steps captured in one HIP graph); ``cfg2serve`` the serving
@@ -30,6 +33,9 @@ dL/dout read, source gradients written; for cfg2serve the batched-query
 backward of each phase-1 call, (3S+Q) rows, and the merge backward, 5 rows).
 ``cfg2arena`` runs the stack-free caller's prefill at the 3B shape (fused block
 steps over one arena: (S+3) rows per point, S+2 right after a commit).
+``cfg2train`` times the reference's training step on the routing path at the
+3B shape (forward under autograd + backward; ``--variant list|stack``,
+``--compile`` for torch.compile with inductor).
 ``--workload mall`` checks what the 256 MB last-level cache serves of a call's
 bytes (the dominant calls back to back vs after other memory traffic).
 ``--gpus`` above 1 exits: this build measures one GPU.
@@ -62,6 +68,8 @@ WORKLOAD_TEXT = {
     "a 512 MiB read, or a call on a second pool",
     "cfg2serve": "3B serving two-phase routing (serve.py:113-164): 7 blocks of 8 sublayers, one batched phase-1 call "
     "(Q=8, S=1..7) + 7 phase-2 merges per block, final phase 1 (S=8); D=3072, B=8, T=4096, bf16",
+    "cfg2train": "3B training step (train.py:610-614 on llama.py:666-716): forward of the 57-point routing loop "
+    "under autograd + backward, D=3072, B=8, T=4096, bf16 model; sublayers x*0.5 (no GEMMs)",
 }
 
 
@@ -73,6 +81,11 @@ def parse_args():
     ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOAD_TEXT))
     ap.add_argument("--pass", dest="pass_", default="fwd", choices=("fwd", "bwd"),
                     help="time the routing forward (default) or its backward")
+    ap.add_argument("--variant", default="list", choices=("list", "stack"),
+                    help="cfg2train: forward_attn_res under autograd (list) or the reference loop with "
+                         "route_static and its per-call stacks (stack)")
+    ap.add_argument("--compile", action="store_true",
+                    help="cfg2train: run the forward under torch.compile(fullgraph=True, backend='inductor')")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-tokens", type=int, default=4096, help="tokens per CPU-baseline sample call")
     return ap.parse_args()
@@ -142,8 +155,8 @@ def cpu_baseline(w, tokens: int) -> dict:
         masks[s][:s] = True
         TP.route_static_cpu(buf, qw, w.eps, masks[s])  # warm-up
     passes: list = []
-    # the whole call schedule, in order, per pass; at least 3 passes and ~10 s of CPU work
-    while len(passes) < 3 or (sum(passes) < 10.0 and len(passes) < 15):
+    # the whole call schedule, in order, per pass; at least 5 passes and ~10 s of CPU work
+    while len(passes) < 5 or (sum(passes) < 10.0 and len(passes) < 15):
         t0 = time.perf_counter()
         for s in w.calls:
             TP.route_static_cpu(buf, qw, w.eps, masks[s])
@@ -648,25 +661,117 @@ def bench_mall(steps: int, warmup: int, dev) -> dict:
     return out
 
 
-def secondary_cfg3(steps: int, warmup: int, dev) -> dict:
-    """The 8B prefill shape (cfg3: S=9, D=4096, B=4, T=4096, 8 calls) measured in the same run as cfg2."""
+def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool) -> dict:
+    """cfg2train: the reference's training step on the routing path at the 3B shape.
+
+    A model with the reference's AttnRes attributes (workloads.TrainingModel:
+    bf16 queries and gains, trainable; sublayers ``x * 0.5``) runs the forward
+    under autograd on a bf16 embedding that requires grad, then
+    ``out.backward(G)`` (train.py:610-614: ``model(...)`` then
+    ``loss.backward()``).  ``variant`` "list": ``forward_attn_res`` (the
+    stack-free caller, list-based routing calls); "stack": the reference's loop
+    with only ``_route_static`` swapped (per-call pad + stack, clones at
+    commits).  HIP events split each step into forward and backward.
+    """
+    import torch
+
+    from kotodama_amd import engine, routing, workloads
+
+    w = workloads.get("cfg2")
+    model = workloads.TrainingModel(w, dev, seed=8)
+    gen = torch.Generator(device=dev).manual_seed(9)
+    embed = torch.randn((w.batch, w.seq, w.hidden), generator=gen, device=dev).to(w.dtype).requires_grad_(True)
+    G = torch.randn((w.batch, w.seq, w.hidden), generator=gen, device=dev).to(w.dtype)
+    if variant == "stack":
+        def fwd(m, x):
+            return workloads.stacked_training_forward(m, x, routing.route_static)
+    else:
+        def fwd(m, x):
+            return engine.forward_attn_res(m, x)
+    if compiled:
+        torch._dynamo.reset()
+        fwd = torch.compile(fwd, fullgraph=True, backend="inductor")
+
+    def step(events):
+        model.zero_grad(set_to_none=True)
+        embed.grad = None
+        e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        e0.record()
+        out = fwd(model, embed)
+        e1.record()
+        out.backward(G)
+        e2.record()
+        events.append((e0, e1, e2))
+
+    t_first = time.perf_counter()
+    for i in range(warmup):
+        print(f"cfg2train {variant}{' compiled' if compiled else ''}: warm-up step {i}", flush=True)
+        step([])
+        torch.cuda.synchronize()
+    first_s = time.perf_counter() - t_first
+    torch.cuda.reset_peak_memory_stats(dev)
+    events: list = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(events)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    fwd_ms = statistics.mean(a.elapsed_time(b) for a, b, _ in events)
+    bwd_ms = statistics.mean(b.elapsed_time(c) for _, b, c in events)
+    row = w.tokens * w.hidden * w.elem_bytes
+    fwd_rows = sum(s + 1 for s in w.calls)
+    bwd_rows = sum(2 * s + 1 for s in w.calls)
+    ms = elapsed * 1e3 / steps
+    return {"ms_per_step": round(ms, 4), "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
+            "routing_kernel_bytes": {"fwd": fwd_rows * row, "bwd": bwd_rows * row},
+            "routing_kernel_bytes_per_ms": round((fwd_rows + bwd_rows) * row / ms / 1e6, 1),
+            "tokens_per_s": round(w.tokens / (ms * 1e-3), 1),
+            "peak_allocated_GiB": round(torch.cuda.max_memory_allocated(dev) / 2**30, 2),
+            "warmup_s": round(first_s, 2)}
+
+
+def secondary_sweep(name: str, steps: int, warmup: int, dev) -> dict:
+    """Another sweep workload (cfg3: the 8B prefill shape, S=9, 8 calls; cfg5: the 3B data-driven
+    blocks, 57 calls) measured in the same run as cfg2, with its own roofline block."""
     from kotodama_amd import workloads
 
-    w = workloads.get("cfg3")
+    w = workloads.get(name)
     elapsed, dominant, dom_ms, dom_bytes = bench_sweep(w, steps, warmup, dev)
     ms = elapsed * 1e3 / steps
     gbs = w.step_bytes() / (ms * 1e-3) / 1e9
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-    traffic, traffic_src = load_traffic(f"cfg3_s{dominant}")
+    traffic, traffic_src = load_traffic(f"{name}_s{dominant}")
     roof = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "kernel": kernel_name(dominant, w.tokens, w.hidden, w.dtype), "algorithmic_bytes": dom_bytes,
             "avg_ms": round(dom_ms, 4)}
     if traffic_src:
         roof["traffic_source"] = traffic_src
-    return {"workload": WORKLOAD_TEXT["cfg3"], "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+    return {"workload": WORKLOAD_TEXT[name], "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
             "value": round(gbs, 2), "unit": "GB/s", "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "tokens_per_s": round(w.tokens / (ms * 1e-3), 1), "algorithmic_bytes_per_step": w.step_bytes(),
+            "roofline": roof}
+
+
+def secondary_backward(name: str, steps: int, warmup: int, dev) -> dict:
+    """The backward of a sweep workload's routing calls (the training path), measured in the same run."""
+    from kotodama_amd import workloads
+
+    w = workloads.get(name)
+    elapsed, dominant, dom_ms, dom_bytes, step_bytes = bench_backward(w, steps, warmup, dev)
+    ms = elapsed * 1e3 / steps
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    traffic, traffic_src = load_traffic(f"bwd_{name}_s{dominant}")
+    roof = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": bwd_kernel_name(dominant, w.tokens, w.hidden, w.dtype) + " (+ attnres_reduce_dqw_cols)",
+            "algorithmic_bytes": dom_bytes, "avg_ms": round(dom_ms, 4)}
+    if traffic_src:
+        roof["traffic_source"] = traffic_src
+    return {"workload": "backward of: " + WORKLOAD_TEXT[name], "steps": steps, "warmup": warmup,
+            "ms_per_step": round(ms, 4), "value": round(gbs, 2), "unit": "GB/s", "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(w.tokens / (ms * 1e-3), 1), "algorithmic_bytes_per_step": step_bytes,
             "roofline": roof}
 
 
@@ -707,6 +812,23 @@ def main() -> int:
                          "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                          "kernel": kernel_name(top, w2.tokens, w2.hidden, w2.dtype, mode=1) + f" (S={top} points)",
                          "algorithmic_bytes": dom_bytes, "avg_ms": round(dom_ms, 4)},
+        }), flush=True)
+        return 0
+    if args.workload == "cfg2train":
+        rec = bench_train(args.steps, args.warmup, dev, args.variant, args.compile)
+        ms = rec["ms_per_step"]
+        rb = rec["routing_kernel_bytes"]
+        gbs = (rb["fwd"] + rb["bwd"]) / (ms * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": "AttnRes training step (routing caller loop forward + backward): tokens/s and the routing "
+                      "kernels' algorithmic bytes per step time",
+            "value": rec["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded embedding, output gradient and routing parameters, resident in HBM)",
+            "config": {"workload": WORKLOAD_TEXT["cfg2train"], "variant": args.variant,
+                       "compiled": bool(args.compile)},
+            "routing_GB/s_over_step": round(gbs, 2), "hbm_frac_routing_bytes": round(gbs / HBM_PEAK_GBS, 4),
+            **rec,
         }), flush=True)
         return 0
     if args.workload == "mall":
@@ -872,7 +994,9 @@ def main() -> int:
         "roofline": roofline,
     }
     if args.workload == "cfg2":
-        line["cfg3"] = secondary_cfg3(args.steps, args.warmup, dev)
+        line["cfg3"] = secondary_sweep("cfg3", args.steps, args.warmup, dev)
+        line["cfg5"] = secondary_sweep("cfg5", args.steps, args.warmup, dev)
+        line["cfg2_bwd"] = secondary_backward("cfg2", args.steps, args.warmup, dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, min(args.cpu_tokens, w.tokens)) if args.workload != "cfg4" else \
             cpu_baseline(w, w.tokens)

@@ -145,8 +145,8 @@ int attnres_merge_fwd(const void* partial, int64_t num_tokens, int hidden, int p
  * Symbol name of the kernel attnres_merge_fwd launches for these arguments
  * (the row-per-wave attnres_merge_stream_* or the row-per-workgroup
  * attnres_merge_*), for matching profiler output; written NUL-terminated into
- * buf.  Loads the code object on the current device.  No counterpart in the
- * reference.
+ * buf (empty for num_tokens == 0, where nothing is launched).  Loads the code
+ * object on the current device.  No counterpart in the reference.
  */
 int attnres_merge_kernel_name(int64_t num_tokens, int hidden, int partial_dtype, int param_dtype, int inter_dtype,
                               char* buf, int buf_len);
@@ -228,7 +228,9 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
  * the library holds on every device it runs on until the process ends.  The
  * call allocates nothing (no hipMalloc, no allocating library routine); the
  * array's device address is resolved at set-up (attnres_init(), or the first
- * call on a device).  Shapes whose workspace would exceed the array return
+ * call on a device).  Under HIP graph capture, call attnres_init() on the
+ * device first: a call on a capturing stream before set-up returns
+ * ATTNRES_ERR_ARG.  Shapes whose workspace would exceed the array return
  * ATTNRES_ERR_UNSUPPORTED.  Every call on a device shares that device's
  * array: calls that overlap on one device (concurrent streams or threads)
  * race and must be ordered by the caller.  Results are bit-identical to

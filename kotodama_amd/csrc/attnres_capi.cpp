@@ -69,6 +69,20 @@ constexpr size_t kBwdStaticLds = 2 * ATTNRES_KMAX_WAVES * 48 * sizeof(float);  /
 constexpr size_t kQgStaticLds = 2 * ATTNRES_KMAX_WAVES * 72 * sizeof(float);   // batched-query reduction buffer
 constexpr size_t kMqgStaticLds = 2 * ATTNRES_KMAX_WAVES * 72 * sizeof(float);  // its backward's (S <= 8)
 
+// One kernel on one device.  Its handle is looked up once, under g_mu, and
+// published with a release store; it never changes afterwards, so finding it
+// again is one acquire load and no lock.  `static_lds` is written before the
+// handle is published.  The resident-workgroup count depends on the launch's
+// block size and dynamic LDS; it is cached in one packed word (valid bit,
+// block, LDS bytes, workgroups per CU), read without a lock by launches of
+// the same shape and recomputed for another shape (the value is a function
+// of the shape, so two threads racing on it store the same word).
+struct KernelSlot {
+  std::atomic<hipFunction_t> fn{nullptr};
+  std::atomic<uint64_t> occ{0};
+  int static_lds = 0;
+};
+
 // Query-gradient reduction kernels: one launch (`cols`), or two (`stage`
 // then `fin`) where the one-launch form's 32-bit offsets would not fit.
 struct ReduceFns {
@@ -82,38 +96,18 @@ struct DeviceState {
   hipModule_t mods[kParts] = {};
   int num_cus = 0;
   int max_lds = 0;  // bytes of LDS one workgroup may use
-  hipFunction_t route[kRouteFuncs] = {};
-  int route_bpc[kRouteFuncs] = {};  // resident workgroups per CU, for the launch block size used
-  int route_bpc_block[kRouteFuncs] = {};
-  hipFunction_t route_qg[kNumS * 2] = {};  // batched-query kernels: S x V
-  int route_qg_bpc[kNumS * 2] = {};
-  int route_qg_block[kNumS * 2] = {};
-  size_t route_qg_lds[kNumS * 2] = {};
-  hipFunction_t stream[kStreamFuncs] = {};
-  int stream_bpc[kStreamFuncs] = {};
-  int stream_slds[kStreamFuncs] = {};  // static LDS bytes of each streaming kernel
-  hipFunction_t merge[kMergeFuncs] = {};
-  hipFunction_t merge_stream[2 * kStreamMaxChunks] = {};  // row-per-wave merge: query path x row KiB
-  int merge_bpc[kMergeFuncs] = {};
-  int merge_bpc_block[kMergeFuncs] = {};
-  hipFunction_t bwd[kBwdFuncs] = {};
-  hipFunction_t bwd_stream[2 * 10] = {};  // row-per-wave backward: rows of 6 / 8 KiB x S (1..9)
-  int bwd_bpc[kBwdFuncs] = {};
-  int bwd_bpc_block[kBwdFuncs] = {};
-  ReduceFns reduce;
-  hipFunction_t merge_bwd[kMergeFuncs] = {};
-  int merge_bwd_bpc[kMergeFuncs] = {};
-  int merge_bwd_bpc_block[kMergeFuncs] = {};
-  hipFunction_t bwd_mq[kBwdFuncs] = {};  // batched-query backward: (source, grad_out) dtypes x S x V
-  int bwd_mq_bpc[kBwdFuncs] = {};
-  int bwd_mq_bpc_block[kBwdFuncs] = {};
-  hipFunction_t bwd_dqw[4] = {};  // source dtype x V
-  int bwd_dqw_bpc[4] = {};
-  int bwd_dqw_bpc_block[4] = {};
-  hipFunction_t bwd_mqg[2 * 9] = {};  // batched-query backward on the matrix cores: query groups x S
-  int bwd_mqg_bpc[2 * 9] = {};
-  int bwd_mqg_block[2 * 9] = {};
-  size_t bwd_mqg_lds[2 * 9] = {};
+  KernelSlot route[kRouteFuncs];
+  KernelSlot route_qg[kNumS * 2];  // batched-query kernels: S x V
+  KernelSlot stream[kStreamFuncs];
+  KernelSlot merge[kMergeFuncs];
+  KernelSlot merge_stream[2 * kStreamMaxChunks];  // row-per-wave merge: query path x row KiB
+  KernelSlot bwd[kBwdFuncs];
+  KernelSlot bwd_stream[2 * 10];  // row-per-wave backward: rows of 6 / 8 KiB x S (1..9)
+  KernelSlot reduce_stage, reduce_cols, reduce_fin;
+  KernelSlot merge_bwd[kMergeFuncs];
+  KernelSlot bwd_mq[kBwdFuncs];  // batched-query backward: (source, grad_out) dtypes x S x V
+  KernelSlot bwd_dqw[4];         // source dtype x V
+  KernelSlot bwd_mqg[2 * 9];     // batched-query backward on the matrix cores: query groups x S
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -235,6 +229,53 @@ int find_function(DeviceState& st, int part, const char* name, hipFunction_t* f)
   return ATTNRES_OK;
 }
 
+// The slot's kernel handle, looked up by `name` in code-object `part` on first use.
+int slot_function(DeviceState& st, KernelSlot& k, int part, const char* name, hipFunction_t* f) {
+  hipFunction_t fn = k.fn.load(std::memory_order_acquire);
+  if (fn == nullptr) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    fn = k.fn.load(std::memory_order_relaxed);
+    if (fn == nullptr) {
+      int rc = find_function(st, part, name, &fn);
+      if (rc != ATTNRES_OK) return rc;
+      int slds = 0;
+      hipError_t e = hipFuncGetAttribute(&slds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, fn);
+      if (e != hipSuccess) return hip_fail(e, "hipFuncGetAttribute(SHARED_SIZE_BYTES)");
+      k.static_lds = slds;
+      k.fn.store(fn, std::memory_order_release);
+    }
+  }
+  *f = fn;
+  return ATTNRES_OK;
+}
+
+// Resident workgroups per CU of the slot's kernel for `block` threads and
+// `lds` bytes of dynamic LDS (at least 1).
+int slot_occupancy(KernelSlot& k, hipFunction_t fn, int block, size_t lds, int* bpc) {
+  const uint64_t key = ((uint64_t)1 << 63) | ((uint64_t)(block & 0x7fff) << 48) | ((uint64_t)(lds & 0xffffffffu) << 16);
+  const uint64_t o = k.occ.load(std::memory_order_acquire);
+  if ((o & ~(uint64_t)0xffff) == key) {
+    *bpc = (int)(o & 0xffff);
+    return ATTNRES_OK;
+  }
+  int nb = 0;
+  hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, block, lds);
+  if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+  if (nb < 1) nb = 1;
+  if (nb > 0xffff) nb = 0xffff;
+  k.occ.store(key | (uint64_t)nb, std::memory_order_release);
+  *bpc = nb;
+  return ATTNRES_OK;
+}
+
+// Handle and occupancy together.
+int slot_get(DeviceState& st, KernelSlot& k, int part, const char* name, int block, size_t lds, hipFunction_t* f,
+             int* bpc) {
+  int rc = slot_function(st, k, part, name, f);
+  if (rc != ATTNRES_OK) return rc;
+  return slot_occupancy(k, *f, block, lds, bpc);
+}
+
 int part_of_stream(int nch) { return nch <= 4 ? 2 : 1; }
 
 enum StreamVariant { kStreamPlain = 0, kStreamTable = 1, kStreamFused = 2 };
@@ -243,26 +284,14 @@ const char* const kStreamVariantNames[3] = {"plain", "table", "fused"};
 int get_stream(DeviceState& st, int combo, bool out_bf, int nch, int variant, hipFunction_t* f, int* bpc,
                int* static_lds) {
   const int idx = ((combo * 2 + (out_bf ? 0 : 1)) * kStreamMaxChunks + (nch - 1)) * 3 + variant;
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (!st.stream[idx]) {
-    static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
-    char name[96];
-    snprintf(name, sizeof(name), "attnres_stream_%s_o%s_c%d_%s", combo_names[combo], out_bf ? "bf" : "f32", nch,
-             kStreamVariantNames[variant]);
-    int rc = find_function(st, part_of_stream(nch), name, &st.stream[idx]);
-    if (rc != ATTNRES_OK) return rc;
-    int nb = 0;
-    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.stream[idx], 64 * kStreamWaves, 0);
-    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
-    st.stream_bpc[idx] = nb > 0 ? nb : 1;
-    int slds = 0;
-    e = hipFuncGetAttribute(&slds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, st.stream[idx]);
-    if (e != hipSuccess) return hip_fail(e, "hipFuncGetAttribute(SHARED_SIZE_BYTES)");
-    st.stream_slds[idx] = slds;
-  }
-  *f = st.stream[idx];
-  *bpc = st.stream_bpc[idx];
-  *static_lds = st.stream_slds[idx];
+  static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_stream_%s_o%s_c%d_%s", combo_names[combo], out_bf ? "bf" : "f32", nch,
+           kStreamVariantNames[variant]);
+  KernelSlot& k = st.stream[idx];
+  int rc = slot_get(st, k, part_of_stream(nch), name, 64 * kStreamWaves, 0, f, bpc);
+  if (rc != ATTNRES_OK) return rc;
+  *static_lds = k.static_lds;
   return ATTNRES_OK;
 }
 
@@ -288,85 +317,32 @@ int stream_out_batch(int num_sources, int64_t out_row_bytes, int static_lds, int
 int route_index(int combo, int s, int v, bool multiq) { return ((combo * kNumS + s) * 2 + (v - 1)) * 2 + (multiq ? 1 : 0); }
 
 int get_route(DeviceState& st, int combo, int s, int v, bool multiq, int block, hipFunction_t* f, int* bpc) {
-  const int idx = route_index(combo, s, v, multiq);
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (!st.route[idx]) {
-    static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
-    char name[96];
-    snprintf(name, sizeof(name), "attnres_route_%s_s%d_v%d_%s", combo_names[combo], s, v, multiq ? "qn" : "q1");
-    int rc = find_function(st, part_of_route(s), name, &st.route[idx]);
-    if (rc != ATTNRES_OK) return rc;
-  }
-  if (st.route_bpc_block[idx] != block) {
-    int nb = 0;
-    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.route[idx], block, 0);
-    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
-    st.route_bpc[idx] = nb > 0 ? nb : 1;
-    st.route_bpc_block[idx] = block;
-  }
-  *f = st.route[idx];
-  *bpc = st.route_bpc[idx];
-  return ATTNRES_OK;
+  static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_route_%s_s%d_v%d_%s", combo_names[combo], s, v, multiq ? "qn" : "q1");
+  return slot_get(st, st.route[route_index(combo, s, v, multiq)], part_of_route(s), name, block, 0, f, bpc);
 }
 
 // Batched-query kernel (bf16 sources and parameters, Q >= 2) with `lds` bytes
 // of dynamic LDS for the staged queries.
 int get_route_qg(DeviceState& st, int s, int v, int block, size_t lds, hipFunction_t* f, int* bpc) {
-  const int idx = s * 2 + (v - 1);
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (!st.route_qg[idx]) {
-    char name[96];
-    snprintf(name, sizeof(name), "attnres_route_bf_d2_s%d_v%d_qg", s, v);
-    int rc = find_function(st, part_of_route(s), name, &st.route_qg[idx]);
-    if (rc != ATTNRES_OK) return rc;
-  }
-  if (st.route_qg_block[idx] != block || st.route_qg_lds[idx] != lds) {
-    int nb = 0;
-    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.route_qg[idx], block, lds);
-    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
-    st.route_qg_bpc[idx] = nb > 0 ? nb : 1;
-    st.route_qg_block[idx] = block;
-    st.route_qg_lds[idx] = lds;
-  }
-  *f = st.route_qg[idx];
-  *bpc = st.route_qg_bpc[idx];
-  return ATTNRES_OK;
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_route_bf_d2_s%d_v%d_qg", s, v);
+  return slot_get(st, st.route_qg[s * 2 + (v - 1)], part_of_route(s), name, block, lds, f, bpc);
 }
 
 // Row-per-wave merge (code-object part 3): bf16 rows of nch KiB, the query on
 // the v_dot2 path (bf16 parameter) or in fp32.
 int get_merge_stream(DeviceState& st, bool d2, int nch, hipFunction_t* f) {
-  const int idx = (d2 ? 0 : kStreamMaxChunks) + (nch - 1);
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (!st.merge_stream[idx]) {
-    char name[96];
-    snprintf(name, sizeof(name), "attnres_merge_stream_%s_c%d", d2 ? "d2" : "fm", nch);
-    int rc = find_function(st, kMergePart, name, &st.merge_stream[idx]);
-    if (rc != ATTNRES_OK) return rc;
-  }
-  *f = st.merge_stream[idx];
-  return ATTNRES_OK;
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_merge_stream_%s_c%d", d2 ? "d2" : "fm", nch);
+  return slot_function(st, st.merge_stream[(d2 ? 0 : kStreamMaxChunks) + (nch - 1)], kMergePart, name, f);
 }
 
 int get_merge(DeviceState& st, bool pbf, bool ibf, int v, int block, hipFunction_t* f, int* bpc) {
-  const int idx = ((pbf ? 0 : 2) + (ibf ? 0 : 1)) * 2 + (v - 1);
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (!st.merge[idx]) {
-    char name[96];
-    snprintf(name, sizeof(name), "attnres_merge_%s_%s_v%d", pbf ? "bf" : "f32", ibf ? "bf" : "f32", v);
-    int rc = find_function(st, kMergePart, name, &st.merge[idx]);
-    if (rc != ATTNRES_OK) return rc;
-  }
-  if (st.merge_bpc_block[idx] != block) {
-    int nb = 0;
-    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.merge[idx], block, 0);
-    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
-    st.merge_bpc[idx] = nb > 0 ? nb : 1;
-    st.merge_bpc_block[idx] = block;
-  }
-  *f = st.merge[idx];
-  *bpc = st.merge_bpc[idx];
-  return ATTNRES_OK;
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_merge_%s_%s_v%d", pbf ? "bf" : "f32", ibf ? "bf" : "f32", v);
+  return slot_get(st, st.merge[((pbf ? 0 : 2) + (ibf ? 0 : 1)) * 2 + (v - 1)], kMergePart, name, block, 0, f, bpc);
 }
 
 // Backward kernels: S <= 8 and the column reduce in part 4, S >= 9 in part 5.
@@ -375,23 +351,9 @@ constexpr int kReducePart = 4;
 
 int get_bwd(DeviceState& st, bool bf, bool gbf, int s, int v, int block, size_t lds, hipFunction_t* f, int* bpc) {
   const int idx = (((bf ? 0 : 2) + (gbf ? 0 : 1)) * kNumS + s) * 2 + (v - 1);
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (st.bwd[idx] == nullptr) {
-    char name[96];
-    snprintf(name, sizeof(name), "attnres_route_bwd_%s_g%s_s%d_v%d", bf ? "bf" : "f32", gbf ? "bf" : "f32", s, v);
-    int rc = find_function(st, part_of_bwd(s), name, &st.bwd[idx]);
-    if (rc != ATTNRES_OK) return rc;
-  }
-  if (st.bwd_bpc_block[idx] != block) {
-    int nb = 0;
-    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.bwd[idx], block, lds);
-    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
-    st.bwd_bpc[idx] = nb > 0 ? nb : 1;
-    st.bwd_bpc_block[idx] = block;
-  }
-  *f = st.bwd[idx];
-  *bpc = st.bwd_bpc[idx];
-  return ATTNRES_OK;
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_route_bwd_%s_g%s_s%d_v%d", bf ? "bf" : "f32", gbf ? "bf" : "f32", s, v);
+  return slot_get(st, st.bwd[idx], part_of_bwd(s), name, block, lds, f, bpc);
 }
 
 // Row-per-wave backward (code-object part 4): bf16 sources and output
@@ -405,15 +367,6 @@ int get_bwd(DeviceState& st, bool bf, bool gbf, int s, int v, int block, size_t 
 // 8 KiB rows the same within 1-2% and 19% slower at S = 2, so AUTO keeps the
 // workgroup kernel there.
 constexpr int kBwdStreamWaves = 4;
-int bwd_stream_nch(bool bf, bool gbf, int num_sources, int hidden, int64_t num_tokens, int num_cus) {
-  if (!bf || !gbf || hidden % 512 != 0) return 0;
-  const int nch = hidden / 512;
-  if ((nch != 6 && nch != 8) || num_sources < 1 || num_sources > (nch == 6 ? 8 : 9)) return 0;
-  if (num_tokens >= (int64_t)1 << 31) return 0;  // 32-bit row counters
-  const int policy = g_policy.load(std::memory_order_relaxed);
-  const int want = policy == ATTNRES_POLICY_STREAM ? 1 : policy == ATTNRES_POLICY_WORKGROUP ? 0 : tuning().stream;
-  return want == 1 || (want < 0 && nch == 6 && num_tokens >= 64LL * num_cus) ? nch : 0;
-}
 // the query (nch * 2 KiB) and the LDS-kept rows, or at the end the waves' query-gradient rows
 size_t bwd_stream_lds(int nch, int num_sources) {
   const size_t kl = num_sources > 48 / nch ? (size_t)(num_sources - 48 / nch) : 0;
@@ -421,18 +374,24 @@ size_t bwd_stream_lds(int nch, int num_sources) {
   const size_t end = (size_t)kBwdStreamWaves * (size_t)nch * 2048;
   return run > end ? run : end;
 }
+// Row KiB of the row-per-wave backward for this call, or 0 for the
+// row-per-workgroup kernel (also when its dynamic LDS exceeds the device's
+// per-workgroup limit, so that the launch and the kernel-name query agree).
+int bwd_stream_nch(bool bf, bool gbf, int num_sources, int hidden, int64_t num_tokens, int num_cus, int max_lds) {
+  if (!bf || !gbf || hidden % 512 != 0) return 0;
+  const int nch = hidden / 512;
+  if ((nch != 6 && nch != 8) || num_sources < 1 || num_sources > (nch == 6 ? 8 : 9)) return 0;
+  if (num_tokens >= (int64_t)1 << 31) return 0;  // 32-bit row counters
+  if (bwd_stream_lds(nch, num_sources) > (size_t)max_lds) return 0;
+  const int policy = g_policy.load(std::memory_order_relaxed);
+  const int want = policy == ATTNRES_POLICY_STREAM ? 1 : policy == ATTNRES_POLICY_WORKGROUP ? 0 : tuning().stream;
+  return want == 1 || (want < 0 && nch == 6 && num_tokens >= 64LL * num_cus) ? nch : 0;
+}
 
 int get_bwd_stream(DeviceState& st, int nch, int s, hipFunction_t* f) {
-  const int idx = (nch == 8 ? 10 : 0) + s;
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (st.bwd_stream[idx] == nullptr) {
-    char name[96];
-    snprintf(name, sizeof(name), "attnres_route_bwd_stream_c%d_s%d", nch, s);
-    int rc = find_function(st, 4, name, &st.bwd_stream[idx]);
-    if (rc != ATTNRES_OK) return rc;
-  }
-  *f = st.bwd_stream[idx];
-  return ATTNRES_OK;
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_route_bwd_stream_c%d_s%d", nch, s);
+  return slot_function(st, st.bwd_stream[(nch == 8 ? 10 : 0) + s], 4, name, f);
 }
 
 // Batched-query backward kernels (code-object part 6).  Source-gradient
@@ -447,50 +406,21 @@ bool bwd_mq_available(bool bf, int s, int v) {
 
 int get_bwd_mq(DeviceState& st, bool bf, bool gbf, int s, int v, int block, hipFunction_t* f, int* bpc) {
   const int idx = (((bf ? 0 : 2) + (gbf ? 0 : 1)) * kNumS + s) * 2 + (v - 1);
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (st.bwd_mq[idx] == nullptr) {
-    char name[96];
-    snprintf(name, sizeof(name), "attnres_route_bwd_mq_%s_g%s_s%d_v%d", bf ? "bf" : "f32", gbf ? "bf" : "f32", s, v);
-    int rc = find_function(st, kBwdMqPart, name, &st.bwd_mq[idx]);
-    if (rc != ATTNRES_OK) return rc;
-  }
-  if (st.bwd_mq_bpc_block[idx] != block) {
-    int nb = 0;
-    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.bwd_mq[idx], block, 0);
-    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
-    st.bwd_mq_bpc[idx] = nb > 0 ? nb : 1;
-    st.bwd_mq_bpc_block[idx] = block;
-  }
-  *f = st.bwd_mq[idx];
-  *bpc = st.bwd_mq_bpc[idx];
-  return ATTNRES_OK;
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_route_bwd_mq_%s_g%s_s%d_v%d", bf ? "bf" : "f32", gbf ? "bf" : "f32", s, v);
+  return slot_get(st, st.bwd_mq[idx], kBwdMqPart, name, block, 0, f, bpc);
 }
 
 // bf16 sources: the matrix-core variant (part 7) unless ATTNRES_MQG=0.
 int get_bwd_dqw(DeviceState& st, bool bf, int v, int block, hipFunction_t* f, int* bpc) {
-  const int idx = (bf ? 0 : 2) + (v - 1);
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (st.bwd_dqw[idx] == nullptr) {
-    char name[96];
-    const bool mfma = bf && tuning().mqg != 0;
-    if (mfma) {
-      snprintf(name, sizeof(name), "attnres_route_bwd_dqwm_bf_v%d", v);
-    } else {
-      snprintf(name, sizeof(name), "attnres_route_bwd_dqw_%s_v%d", bf ? "bf" : "f32", v);
-    }
-    int rc = find_function(st, mfma ? kBwdMqgPart : kBwdMqPart, name, &st.bwd_dqw[idx]);
-    if (rc != ATTNRES_OK) return rc;
+  char name[96];
+  const bool mfma = bf && tuning().mqg != 0;
+  if (mfma) {
+    snprintf(name, sizeof(name), "attnres_route_bwd_dqwm_bf_v%d", v);
+  } else {
+    snprintf(name, sizeof(name), "attnres_route_bwd_dqw_%s_v%d", bf ? "bf" : "f32", v);
   }
-  if (st.bwd_dqw_bpc_block[idx] != block) {
-    int nb = 0;
-    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.bwd_dqw[idx], block, 0);
-    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
-    st.bwd_dqw_bpc[idx] = nb > 0 ? nb : 1;
-    st.bwd_dqw_bpc_block[idx] = block;
-  }
-  *f = st.bwd_dqw[idx];
-  *bpc = st.bwd_dqw_bpc[idx];
-  return ATTNRES_OK;
+  return slot_get(st, st.bwd_dqw[(bf ? 0 : 2) + (v - 1)], mfma ? kBwdMqgPart : kBwdMqPart, name, block, 0, f, bpc);
 }
 
 // Batched-query backward on the matrix cores (code-object part 7): bf16
@@ -504,60 +434,23 @@ bool bwd_mqg_shape(bool bf, bool gbf, bool pbf, int s, int nq, int nchunk) {
 }
 
 int get_bwd_mqg(DeviceState& st, int s, int nq4, int block, size_t lds, hipFunction_t* f, int* bpc) {
-  const int idx = (nq4 - 1) * 9 + s;
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (st.bwd_mqg[idx] == nullptr) {
-    char name[96];
-    snprintf(name, sizeof(name), "attnres_route_bwd_mqg_s%d_q%d", s, nq4);
-    int rc = find_function(st, kBwdMqgPart, name, &st.bwd_mqg[idx]);
-    if (rc != ATTNRES_OK) return rc;
-  }
-  if (st.bwd_mqg_block[idx] != block || st.bwd_mqg_lds[idx] != lds) {
-    int nb = 0;
-    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.bwd_mqg[idx], block, lds);
-    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
-    st.bwd_mqg_bpc[idx] = nb > 0 ? nb : 1;
-    st.bwd_mqg_block[idx] = block;
-    st.bwd_mqg_lds[idx] = lds;
-  }
-  *f = st.bwd_mqg[idx];
-  *bpc = st.bwd_mqg_bpc[idx];
-  return ATTNRES_OK;
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_route_bwd_mqg_s%d_q%d", s, nq4);
+  return slot_get(st, st.bwd_mqg[(nq4 - 1) * 9 + s], kBwdMqgPart, name, block, lds, f, bpc);
 }
 
 int get_merge_bwd(DeviceState& st, bool pbf, bool ibf, int v, int block, hipFunction_t* f, int* bpc) {
-  const int idx = ((pbf ? 0 : 2) + (ibf ? 0 : 1)) * 2 + (v - 1);
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (!st.merge_bwd[idx]) {
-    char name[96];
-    snprintf(name, sizeof(name), "attnres_merge_bwd_%s_%s_v%d", pbf ? "bf" : "f32", ibf ? "bf" : "f32", v);
-    int rc = find_function(st, kReducePart, name, &st.merge_bwd[idx]);
-    if (rc != ATTNRES_OK) return rc;
-  }
-  if (st.merge_bwd_bpc_block[idx] != block) {
-    int nb = 0;
-    hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, st.merge_bwd[idx], block, 0);
-    if (e != hipSuccess) return hip_fail(e, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
-    st.merge_bwd_bpc[idx] = nb > 0 ? nb : 1;
-    st.merge_bwd_bpc_block[idx] = block;
-  }
-  *f = st.merge_bwd[idx];
-  *bpc = st.merge_bwd_bpc[idx];
-  return ATTNRES_OK;
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_merge_bwd_%s_%s_v%d", pbf ? "bf" : "f32", ibf ? "bf" : "f32", v);
+  return slot_get(st, st.merge_bwd[((pbf ? 0 : 2) + (ibf ? 0 : 1)) * 2 + (v - 1)], kReducePart, name, block, 0, f,
+                  bpc);
 }
 
-int get_reduce(DeviceState& st, const ReduceFns** out) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (st.reduce.fin == nullptr) {
-    int rc = find_function(st, kReducePart, "attnres_reduce_dqw_stage", &st.reduce.stage);
-    if (rc != ATTNRES_OK) return rc;
-    rc = find_function(st, kReducePart, "attnres_reduce_dqw_cols", &st.reduce.cols);
-    if (rc != ATTNRES_OK) return rc;
-    rc = find_function(st, kReducePart, "attnres_reduce_dqw", &st.reduce.fin);
-    if (rc != ATTNRES_OK) return rc;
-  }
-  *out = &st.reduce;
-  return ATTNRES_OK;
+int get_reduce(DeviceState& st, ReduceFns* out) {
+  int rc = slot_function(st, st.reduce_stage, kReducePart, "attnres_reduce_dqw_stage", &out->stage);
+  if (rc == ATTNRES_OK) rc = slot_function(st, st.reduce_cols, kReducePart, "attnres_reduce_dqw_cols", &out->cols);
+  if (rc == ATTNRES_OK) rc = slot_function(st, st.reduce_fin, kReducePart, "attnres_reduce_dqw", &out->fin);
+  return rc;
 }
 
 inline int round64(int64_t t) { return (int)(((t + 63) / 64) * 64); }
@@ -962,9 +855,13 @@ int attnres_merge_kernel_name(int64_t num_tokens, int hidden, int partial_dtype,
   if (buf == nullptr || buf_len < 1) return fail(ATTNRES_ERR_ARG, "no output buffer");
   if (!valid_dtype(partial_dtype) || !valid_dtype(param_dtype) || !valid_dtype(inter_dtype))
     return fail(ATTNRES_ERR_ARG, "unknown dtype code");
-  if (num_tokens < 1 || hidden <= 0) return fail(ATTNRES_ERR_ARG, "bad shape");
+  if (num_tokens < 0 || hidden <= 0) return fail(ATTNRES_ERR_ARG, "bad shape");
   const int vec = partial_dtype == ATTNRES_DTYPE_BF16 ? 8 : 4;
   if (hidden % vec != 0) return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d is not a multiple of %d", hidden, vec);
+  if (num_tokens == 0) {  // attnres_merge_fwd launches nothing
+    buf[0] = '\0';
+    return ATTNRES_OK;
+  }
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
@@ -994,7 +891,8 @@ int attnres_route_bwd_kernel_name(int num_sources, int64_t num_tokens, int hidde
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
   const int nch =
-      bwd_stream_nch(bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, hidden, num_tokens, st->num_cus);
+      bwd_stream_nch(bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, hidden, num_tokens, st->num_cus,
+                     st->max_lds);
   if (nch > 0) {
     snprintf(buf, (size_t)buf_len, "attnres_route_bwd_stream_c%d_s%d", nch, num_sources);
     return ATTNRES_OK;
@@ -1176,9 +1074,11 @@ static int route_bwd_finish(hipFunction_t f, int grid, int block, size_t lds, De
     return fail(ATTNRES_ERR_ARG, "workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
                 (long long)need);
   if (!aligned16(workspace)) return fail(ATTNRES_ERR_ALIGN, "workspace not 16-byte aligned");
+  ReduceFns redfns;
   const ReduceFns* red = nullptr;
   if (grad_query != nullptr || grad_gain != nullptr) {
-    rc = get_reduce(st, &red);
+    rc = get_reduce(st, &redfns);
+    red = &redfns;
     if (rc != ATTNRES_OK) return rc;
   }
 
@@ -1255,7 +1155,8 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
   const int snch =
-      bwd_stream_nch(bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, hidden, num_tokens, st->num_cus);
+      bwd_stream_nch(bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, hidden, num_tokens, st->num_cus,
+                     st->max_lds);
   if (snch > 0) {
     hipFunction_t f = nullptr;
     rc = get_bwd_stream(*st, snch, num_sources, &f);
@@ -1295,7 +1196,7 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
 // Workspace of the batched-query backward: c1 coefficients (num_tokens, Q, S)
 // fp32, then the per-workgroup query-gradient partials (grid, Q, hidden).
 constexpr int kBwdDqwPerCu = 2;
-int64_t bwd_mq_c1_bytes(int64_t num_tokens, int num_sources, int num_queries) {
+static int64_t bwd_mq_c1_bytes(int64_t num_tokens, int num_sources, int num_queries) {
   const int64_t b = num_tokens * (int64_t)num_queries * num_sources * (int64_t)sizeof(float);
   return (b + 255) / 256 * 256;
 }
@@ -1390,12 +1291,14 @@ int attnres_route_bwd_queries(const void* const* sources, int num_sources, int64
   }
   if (rc != ATTNRES_OK) return rc;
   const bool want_q = grad_query != nullptr || grad_gain != nullptr;
+  ReduceFns redfns;
   const ReduceFns* red = nullptr;
   int64_t grid_q = 0;
   if (want_q) {
     rc = get_bwd_dqw(*st, bf, v, block, &fq, &bpcq);
     if (rc != ATTNRES_OK) return rc;
-    rc = get_reduce(*st, &red);
+    rc = get_reduce(*st, &redfns);
+    red = &redfns;
     if (rc != ATTNRES_OK) return rc;
     grid_q = (int64_t)st->num_cus * (bpcq < kBwdDqwPerCu ? bpcq : kBwdDqwPerCu);
     if (grid_q > num_tokens) grid_q = num_tokens;
@@ -1510,9 +1413,11 @@ int attnres_merge_bwd(const void* partial, int64_t num_tokens, int hidden, int p
     return fail(ATTNRES_ERR_ARG, "workspace of %lld bytes is smaller than the %lld needed", (long long)workspace_bytes,
                 (long long)need);
   if (!aligned16(workspace)) return fail(ATTNRES_ERR_ALIGN, "workspace not 16-byte aligned");
+  ReduceFns redfns;
   const ReduceFns* red = nullptr;
   if (grad_query != nullptr) {
-    rc = get_reduce(*st, &red);
+    rc = get_reduce(*st, &redfns);
+    red = &redfns;
     if (rc != ATTNRES_OK) return rc;
   }
 

@@ -42,12 +42,27 @@ std::atomic<void*> g_scratch[kMaxDevices];
 std::mutex g_scratch_mu;
 
 // Device address of `scratch` on the current device, resolved once per device.
-int scratch_for_current_device(void** out) {
+// The first resolution may load the code object that holds the array (and so
+// place the array in device memory); that must not happen inside a stream
+// capture, so a call on a capturing `stream` before set-up is an error.
+int scratch_for_current_device(void** out, hipStream_t stream = nullptr, bool check_capture = false) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return attnres_internal_fail(ATTNRES_ERR_HIP, "hipGetDevice failed");
   if (dev < 0 || dev >= kMaxDevices) return attnres_internal_fail(ATTNRES_ERR_HIP, "device ordinal out of range");
   void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr && check_capture) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &status);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return attnres_internal_fail(ATTNRES_ERR_HIP, "hipStreamIsCapturing failed");
+    }
+    if (status != hipStreamCaptureStatusNone)
+      return attnres_internal_fail(ATTNRES_ERR_ARG,
+                                   "attnres_route_bwd_noalloc called under stream capture before set-up: call "
+                                   "attnres_init() on this device before capturing");
+  }
   if (p == nullptr) {
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     p = g_scratch[dev].load(std::memory_order_relaxed);
@@ -92,7 +107,7 @@ extern "C" int attnres_route_bwd_noalloc(const void* const* sources, int num_sou
                                  "the backward needs more workspace than the fixed scratch array "
                                  "(ATTNRES_NOALLOC_SCRATCH_BYTES); use attnres_route_bwd");
   void* ws = nullptr;
-  rc = scratch_for_current_device(&ws);
+  rc = scratch_for_current_device(&ws, static_cast<hipStream_t>(stream), true);
   if (rc != ATTNRES_OK) return rc;
   return attnres_route_bwd(sources, num_sources, num_tokens, hidden, src_ld, src_dtype, query, gain, param_dtype, eps,
                            grad_out, grad_out_dtype, grad_out_ld, grad_lse, grad_sources, grad_ld, ws,

@@ -142,3 +142,108 @@ def make_deltas(w: Workload, device, seed: int, count: int, tokens: Optional[tup
     b, t = tokens if tokens is not None else (w.batch, w.seq)
     g = _gen(device, seed + 2000)
     return torch.randn((count, b, t, w.hidden), generator=g, device=device, dtype=torch.float32).to(w.dtype)
+
+
+# ------------------------------------------------------------ training step --
+
+
+class _HalfSublayer(torch.nn.Module):
+    """Stand-in for attention / the MLP in the training-step workload: ``x * 0.5``,
+    one elementwise kernel each way, so the step's time is the routing side."""
+
+    def forward(self, x: torch.Tensor, *args, **kwargs) -> torch.Tensor:
+        return x * 0.5
+
+
+class _RoutingNorm(torch.nn.Module):
+    """The routing points' RMSNorm as the routing path uses it (llama.py:143-153):
+    a gain parameter and ``eps``; its ``forward`` is never called on the path."""
+
+    def __init__(self, gain: torch.Tensor, eps: float) -> None:
+        super().__init__()
+        self.weight = torch.nn.Parameter(gain)
+        self.eps = eps
+
+
+class _TrainingLayer(torch.nn.Module):
+    def __init__(self, q_attn, g_attn, q_mlp, g_mlp, eps: float) -> None:
+        super().__init__()
+        self.attn_norm = torch.nn.Identity()
+        self.attn = _HalfSublayer()
+        self.ffn_norm = torch.nn.Identity()
+        self.ffn = _HalfSublayer()
+        self.attn_res_query = torch.nn.Parameter(q_attn)
+        self.attn_res_norm = _RoutingNorm(g_attn, eps)
+        self.mlp_res_query = torch.nn.Parameter(q_mlp)
+        self.mlp_res_norm = _RoutingNorm(g_mlp, eps)
+
+
+class _Cfg:
+    def __init__(self, num_layers: int, norm_eps: float) -> None:
+        self.num_layers = num_layers
+        self.norm_eps = norm_eps
+
+
+class TrainingModel(torch.nn.Module):
+    """A model with the attributes the reference's AttnRes forward reads
+    (llama.py:446-551, 545-571): ``layers[i].{attn_norm, attn, ffn_norm, ffn,
+    attn_res_query, attn_res_norm, mlp_res_query, mlp_res_norm}``,
+    ``final_res_query`` / ``final_res_norm``, ``norm``, ``rope_cos/sin``,
+    ``_attn_res_boundary_set`` and the schedule tables (``_attn_res_max_sources``,
+    ``_attn_res_masks``, ``_attn_res_active_counts``).  The routing queries and
+    gains are the workload's (``make_params``), in its dtype and trainable; the
+    sublayers are ``x * 0.5`` and the norms around them identities, so a
+    training step of it is the routing calls, the caller loop's own tensor
+    traffic (stacks, partial sums, commits) and autograd's gradient sums."""
+
+    def __init__(self, w: Workload, device, seed: int) -> None:
+        super().__init__()
+        sched = w.schedule
+        L = sched.num_layers
+        q, gain = make_params(w, device, seed, sched.num_points)
+        self.config = _Cfg(L, w.eps)
+        self.layers = torch.nn.ModuleList(
+            [_TrainingLayer(q[2 * i].clone(), gain[2 * i].clone(), q[2 * i + 1].clone(), gain[2 * i + 1].clone(), w.eps)
+             for i in range(L)])
+        self.final_res_query = torch.nn.Parameter(q[-1].clone())
+        self.final_res_norm = _RoutingNorm(gain[-1].clone(), w.eps)
+        self.norm = torch.nn.Identity()
+        self._attn_res_boundary_set = frozenset(sched.boundary_set)
+        self._attn_res_max_sources = sched.max_sources
+        self._attn_res_active_counts = list(sched.active_counts)
+        self.register_buffer("_attn_res_masks", sched.masks().to(device), persistent=False)
+        self.register_buffer("rope_cos", torch.zeros(1, device=device))
+        self.register_buffer("rope_sin", torch.zeros(1, device=device))
+
+
+def stacked_training_forward(model, embed: torch.Tensor, route_fn) -> torch.Tensor:
+    """The reference's training forward (llama.py:666-716) as it runs after the
+    routing function alone is swapped: before every routing call the committed
+    blocks and the partial are zero-padded to max_S and stacked (llama.py:690-695),
+    a commit clones the partial and restarts from a cloned zero block
+    (llama.py:701-703), and sublayer outputs are added out of place
+    (llama.py:706, 712).  ``route_fn(buf, query, norm, mask, num_active)``."""
+    masks = model._attn_res_masks
+    counts = model._attn_res_active_counts
+    max_s = model._attn_res_max_sources
+    boundaries = model._attn_res_boundary_set
+    committed: list = []
+    partial = embed
+    zero = torch.zeros_like(embed)
+
+    def stacked():
+        srcs = committed + [partial]
+        srcs += [zero] * (max_s - len(srcs))
+        return torch.stack(srcs, dim=0)
+
+    for i, layer in enumerate(model.layers):
+        h = route_fn(stacked(), layer.attn_res_query, layer.attn_res_norm, masks[2 * i], counts[2 * i])
+        if i in boundaries:
+            committed.append(partial.clone())
+            partial = zero.clone()
+        partial = partial + layer.attn(layer.attn_norm(h), model.rope_cos, model.rope_sin, None)
+        h = route_fn(stacked(), layer.mlp_res_query, layer.mlp_res_norm, masks[2 * i + 1], counts[2 * i + 1])
+        partial = partial + layer.ffn(layer.ffn_norm(h))
+    L = len(model.layers)
+    x = route_fn(stacked(), model.final_res_query, model.final_res_norm, masks[2 * L], counts[2 * L])
+    return model.norm(x)

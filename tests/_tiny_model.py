@@ -55,13 +55,29 @@ class TinyFFN(nn.Module):
         return torch.sin(self.proj(x)) * 0.5
 
 
+class TinyElementwise(nn.Module):
+    """A sublayer without matrix products: tanh(x * a + b) / 2 with (D,) parameters a, b
+    (for bf16 models: no batched bf16 products anywhere in the step)."""
+
+    def __init__(self, d):
+        super().__init__()
+        self.a = nn.Parameter(torch.ones(d))
+        self.b = nn.Parameter(torch.zeros(d))
+
+    def forward(self, x, rope_cos=None, rope_sin=None, mask=None, layer_past=None, use_cache=False):
+        y = torch.tanh(x * self.a + self.b) * 0.5
+        if use_cache:
+            return y, (x, x)
+        return y
+
+
 class TinyLayer(nn.Module):
-    def __init__(self, d, eps):
+    def __init__(self, d, eps, elementwise=False):
         super().__init__()
         self.attn_norm = TinyNorm(d, eps)
-        self.attn = TinyAttn(d)
+        self.attn = TinyElementwise(d) if elementwise else TinyAttn(d)
         self.ffn_norm = TinyNorm(d, eps)
-        self.ffn = TinyFFN(d)
+        self.ffn = TinyElementwise(d) if elementwise else TinyFFN(d)
         self.attn_res_query = nn.Parameter(torch.zeros(d))
         self.attn_res_norm = TinyNorm(d, eps)
         self.mlp_res_query = nn.Parameter(torch.zeros(d))
@@ -75,11 +91,11 @@ class Cfg:
 
 
 class TinyModel(nn.Module):
-    def __init__(self, d=512, num_layers=4, boundaries=(0, 2), eps=1e-5, seed=0):
+    def __init__(self, d=512, num_layers=4, boundaries=(0, 2), eps=1e-5, seed=0, elementwise=False):
         super().__init__()
         g = torch.Generator().manual_seed(seed)
         self.config = Cfg(num_layers, eps)
-        self.layers = nn.ModuleList([TinyLayer(d, eps) for _ in range(num_layers)])
+        self.layers = nn.ModuleList([TinyLayer(d, eps, elementwise) for _ in range(num_layers)])
         self.final_res_query = nn.Parameter(torch.zeros(d))
         self.final_res_norm = TinyNorm(d, eps)
         self.norm = TinyNorm(d, eps)
@@ -98,6 +114,10 @@ class TinyModel(nn.Module):
                 if p.dim() == 2:
                     p.copy_(torch.randn(p.shape, generator=g) / math.sqrt(p.shape[1]))
             for layer in self.layers:
+                for sub in (layer.attn, layer.ffn):
+                    if isinstance(sub, TinyElementwise):
+                        sub.a.copy_(1 + 0.2 * torch.randn(d, generator=g))
+                        sub.b.copy_(0.1 * torch.randn(d, generator=g))
                 for q in (layer.attn_res_query, layer.mlp_res_query):
                     q.copy_(torch.randn(d, generator=g) * 0.1)
                 for n in (layer.attn_res_norm, layer.mlp_res_norm):

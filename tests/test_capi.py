@@ -209,5 +209,7 @@ def test_kernel_name_argument_errors():
     assert lib.attnres_route_kernel_name(17, 16, 64, 1, 1, 1, 1, 0, 1, buf, 8) == _capi.ERR_ARG
     assert lib.attnres_merge_kernel_name(16, 512, 1, 1, 1, None, 0) == _capi.ERR_ARG
     assert lib.attnres_merge_kernel_name(16, 512, 1, 7, 1, buf, 8) == _capi.ERR_ARG  # param dtype
-    assert lib.attnres_merge_kernel_name(0, 512, 1, 1, 1, buf, 8) == _capi.ERR_ARG  # no rows
+    assert lib.attnres_merge_kernel_name(-1, 512, 1, 1, 1, buf, 8) == _capi.ERR_ARG  # negative rows
+    # no rows: attnres_merge_fwd launches nothing, and the name is empty (no device needed)
+    assert lib.attnres_merge_kernel_name(0, 512, 1, 1, 1, buf, 8) == _capi.OK and buf.value == b""
     assert lib.attnres_merge_kernel_name(16, 500, 1, 1, 1, buf, 8) == _capi.ERR_UNSUPPORTED  # not 16-byte chunks

@@ -657,7 +657,7 @@ def test_capi_backward_argument_errors(gpu):
 
 @pytest.mark.parametrize("S", [5, 8])
 @pytest.mark.parametrize("kernel", ["row_per_wave", "workgroup"])
-def test_full_size_3b_backward_properties(gpu, S, kernel):
+def test_full_size_backward_properties(gpu, S, kernel):
     # the 3B prefill shape (B=8, T=4096, D=3072), bf16, at two source counts, through
     # the row-per-wave kernel (AUTO) and the two-chunks-per-thread workgroup kernel
     # (checked through the kernel-name query)
@@ -667,12 +667,26 @@ def test_full_size_3b_backward_properties(gpu, S, kernel):
     assert _bwd_kernel_name(S, w.tokens, w.hidden, policy) == want
     prev = _capi.set_kernel_policy(policy)
     try:
-        _full_size_3b_backward(gpu, w, S)
+        _full_size_backward(gpu, w, S)
     finally:
         _capi.set_kernel_policy(prev)
 
 
-def _full_size_3b_backward(gpu, w, S):
+def test_full_size_8b_backward(gpu):
+    # config 3's training backward at full size (B=4, T=4096, D=4096, S=9, bf16,
+    # peaky queries and source scales from log-uniform[0.1, 10]) through the kernel
+    # AUTO launches for it: the one-chunk row-per-workgroup S = 9 instance, the only
+    # hot instance compiled under a register cap that spills a few dwords
+    w = workloads.get("cfg3")
+    assert _bwd_kernel_name(9, w.tokens, w.hidden, _capi.POLICY_AUTO) == "attnres_route_bwd_bf_gbf_s9_v1"
+    prev = _capi.set_kernel_policy(_capi.POLICY_AUTO)
+    try:
+        _full_size_backward(gpu, w, 9)
+    finally:
+        _capi.set_kernel_policy(prev)
+
+
+def _full_size_backward(gpu, w, S):
     pool = workloads.make_pool(w, gpu, 3)
     q, gn = workloads.make_params(w, gpu, 3, 1)
     eps = w.eps
@@ -709,7 +723,7 @@ def _full_size_3b_backward(gpu, w, S):
         rel = ((lhs - rhs).abs() / scale).max().item()
         del dx
     assert rel < 1e-2, f"scale identity violated: rel {rel:.3e}"
-    # the query and gain gradients (sums over all 32768 rows)
+    # the query and gain gradients (sums over all rows)
     for got, ref, label in ((query.grad, dqw * norm.weight.detach().float(), "dquery"),
                             (norm.weight.grad, dqw * query.detach().float(), "dgain")):
         g64, r64 = np64(got), ref.double().cpu().numpy()

@@ -236,3 +236,66 @@ def test_eager_calls_skip_the_dispatcher_only_when_nothing_is_recorded(gpu, monk
     with torch.no_grad(), PassThrough():
         h3 = routing.route_static(buf, query, norm, mask, 3)
     assert calls == ["route"] and torch.equal(h3, via_op)
+
+
+@pytest.mark.parametrize("path", ["stack_free", "stacked"])
+def test_bf16_training_loop_sixteen_layers(gpu, path):
+    # a bf16 model (the reference trains in bf16, train.py:237) of 16 layers in 4
+    # blocks (S = 1..5), sublayers without matrix products: loss, output and every
+    # parameter gradient (routing queries and gains, sublayer parameters, the
+    # embedding) against the reference loop in float64.  Bar per tensor: the
+    # worst error within 2x that of the reference's own op sequence
+    # (llama.py:640-644, the einsum branch) evaluated in bf16 on the same bf16
+    # model, plus 2^-9 of the largest reference magnitude (sublayer roundings
+    # alone move bf16 values by that much).  path: forward_attn_res under
+    # autograd (list routing) or the pad-and-stack loop with route_static.
+    from kotodama_amd import route_static
+    from oracle.torch_cpu_path import route_static_cpu
+
+    L, bounds, d = 16, (0, 4, 8, 12), 1024
+    model = TinyModel(d=d, num_layers=L, boundaries=bounds, seed=51, elementwise=True)
+    model = model.to(torch.bfloat16).float()  # bf16-exact parameters shared by every run
+    assert model._attn_res_max_sources == 5
+    gen = torch.Generator().manual_seed(52)
+    embed = (torch.randn((2, 32, d), generator=gen) * 2).to(torch.bfloat16).float()
+    G = torch.randn((2, 32, d), generator=gen).to(torch.bfloat16).float()
+
+    def einsum(buf, q, norm, mask, n):
+        return route_static_cpu(buf, q * norm.weight, norm.eps, mask)
+
+    def run(m, e, fwd):
+        e = e.clone().requires_grad_(True)
+        out = fwd(m, e)
+        loss = (out.float() * G.to(e.device)).sum()
+        loss.backward()
+        grads = {n: p.grad.double().cpu() for n, p in m.named_parameters()}
+        grads["embed"] = e.grad.double().cpu()
+        return loss.item(), out.detach().double().cpu(), grads
+
+    ref = run(copy.deepcopy(model).double(), embed.double(), lambda m, e: training_forward(m, e, einsum))
+    tb = run(copy.deepcopy(model).to(gpu).to(torch.bfloat16), embed.to(gpu).to(torch.bfloat16),
+             lambda m, e: training_forward(m, e, einsum))
+    if path == "stack_free":
+        fwd = forward_attn_res
+    else:
+        def fwd(m, e):
+            return training_forward(m, e, route_static)
+    ours = run(copy.deepcopy(model).to(gpu).to(torch.bfloat16), embed.to(gpu).to(torch.bfloat16), fwd)
+    torch.cuda.synchronize()
+
+    def worst(a, b):
+        return (a - b).abs().max().item()
+
+    loss_bar = 2 * abs(tb[0] - ref[0]) + 2.0**-9 * abs(ref[0])
+    print(f"bf16 L=16 {path}: loss err {abs(ours[0] - ref[0]):.3e} (torch bf16 {abs(tb[0] - ref[0]):.3e})", flush=True)
+    assert abs(ours[0] - ref[0]) <= loss_bar
+    floor = 2.0**-9 * ref[1].abs().max().item()
+    assert worst(ours[1], ref[1]) <= 2 * worst(tb[1], ref[1]) + floor, "output"
+    ratios = []
+    for name, want in ref[2].items():
+        e_ours, e_tb = worst(ours[2][name], want), worst(tb[2][name], want)
+        bar = 2 * e_tb + 2.0**-9 * want.abs().max().item()
+        ratios.append(e_ours / max(e_tb, 1e-30))
+        assert e_ours <= bar, f"{name}: err {e_ours:.3e}, torch bf16 op sequence {e_tb:.3e}"
+    print(f"bf16 L=16 {path}: {len(ratios)} gradients, error / torch-bf16 error: median "
+          f"{float(np.median(ratios)):.2f}, max {max(ratios):.2f}", flush=True)

@@ -113,3 +113,47 @@ def test_compiled_training_loop_matches_eager_and_float64(gpu, backend):
             tol_e = 2e-4 * pe.grad.abs().max().item() + 1e-7
             assert (p.grad - pe.grad).abs().max().item() <= tol_e, f"{backend} it={it} {name}: vs eager"
         torch.testing.assert_close(out.detach().double().cpu(), out_ref.detach(), rtol=2e-4, atol=2e-4)
+
+
+def test_compiled_stack_free_training_matches_eager_and_float64(gpu):
+    # the stack-free caller (forward_attn_res under autograd: route_list with a
+    # list of block tensors per routing point, INTEGRATION's training drop-in)
+    # compiled as one graph with the reference's default backend, forward and
+    # backward, against the eager run and the reference's pad-and-stack loop in
+    # float64; two calls (the second runs the cached graph)
+    from oracle.torch_cpu_path import route_static_cpu
+
+    torch._dynamo.reset()
+    model = TinyModel(d=512, num_layers=4, boundaries=(0, 2), seed=25)
+    ref_model = copy.deepcopy(model).double()
+    g = torch.Generator().manual_seed(26)
+    embed = torch.randn((2, 16, 512), generator=g)
+    G = torch.randn((2, 16, 512), generator=g)
+    out_ref = training_forward(ref_model, embed.double(),
+                                lambda buf, q, norm, mask, n: route_static_cpu(buf, q * norm.weight, norm.eps, mask))
+    loss_ref = (out_ref * G.double()).sum()
+    loss_ref.backward()
+
+    m_eager = model.to(gpu)
+    m_comp = copy.deepcopy(m_eager)
+    e, Gg = embed.to(gpu), G.to(gpu)
+    (kotodama_amd.forward_attn_res(m_eager, e) * Gg).sum().backward()
+    step = torch.compile(lambda m, x: kotodama_amd.forward_attn_res(m, x), backend="inductor", fullgraph=True)
+    for it in range(2):
+        m_comp.zero_grad(set_to_none=True)
+        out = step(m_comp, e)
+        loss = (out * Gg).sum()
+        loss.backward()
+        torch.cuda.synchronize()
+        assert abs(loss.item() - loss_ref.item()) <= 1e-4 * abs(loss_ref.item()) + 1e-3, f"it={it}: loss"
+        torch.testing.assert_close(out.detach().double().cpu(), out_ref.detach(), rtol=2e-4, atol=2e-4)
+        checked = 0
+        for (name, p), (_, pe), (_, pr) in zip(m_comp.named_parameters(), m_eager.named_parameters(),
+                                               ref_model.named_parameters()):
+            want = pr.grad
+            tol = 2e-4 * want.abs().max().item() + 1e-7
+            assert (p.grad.double().cpu() - want).abs().max().item() <= tol, f"it={it} {name}: vs float64"
+            tol_e = 2e-4 * pe.grad.abs().max().item() + 1e-7
+            assert (p.grad - pe.grad).abs().max().item() <= tol_e, f"it={it} {name}: vs eager"
+            checked += 1
+        assert checked == len(list(m_comp.parameters()))

@@ -379,6 +379,33 @@ def test_merge_backward_keeps_small_one_minus_pi():
         assert np.all(b["dinter"] != 0.0)
 
 
+def test_merge_backward_saturated_rows_reference_form_within_bar():
+    # The reference takes dinter = (1.0 - pi) G in fp32 (kernels/phase_2.py:141);
+    # this build takes 1 - pi = 1 / (1 + e^z).  On saturated rows (z >~ 17, where fp32
+    # pi rounds to 1) the reference's form gives 0 and this one ~e^-z G: the two
+    # differ by less than e^-z |G| per element, which stays inside the bf16 gradient
+    # bar (1 bf16 ulp + 1e-3 max|ref|) of a tensor that also holds unsaturated rows.
+    rng = np.random.default_rng(65)
+    N, D, eps = 8, 64, 1e-6
+    p = rng.standard_normal((N, D))
+    q = rng.standard_normal(D)
+    it = rng.standard_normal((N, D))
+    G = rng.standard_normal((N, D))
+    logit = O.merge(p, q, it, np.zeros(N), eps)["logit"]
+    z = np.array([-2.0, 0.0, 1.5, 5.0, 17.0, 25.0, 40.0, 80.0])
+    lse = logit - z
+    b = O.merge_backward(p, q, it, lse, eps, G)
+    pi32 = (np.float32(1.0) / (np.float32(1.0) + np.exp(-z.astype(np.float32)))).astype(np.float32)
+    ref_form = ((np.float32(1.0) - pi32)[:, None] * G.astype(np.float32)).astype(np.float64)
+    assert np.all(ref_form[z >= 17.0] == 0.0)  # the reference's fp32 form vanishes on saturated rows
+    diff = np.abs(b["dinter"] - ref_form)
+    # (z is recovered as logit - lse, so to float64 rounding)
+    assert np.all(diff[z >= 17.0] <= (1 + 1e-9) * np.exp(-z[z >= 17.0])[:, None] * np.abs(G[z >= 17.0]))
+    e = np.floor(np.log2(np.maximum(np.abs(b["dinter"]), 2.0**-126)))
+    bar = 2.0 ** (e - 7) + 1e-3 * np.abs(b["dinter"]).max()
+    assert np.all(diff <= bar)
+
+
 def test_merge_backward_equals_routing_backward_over_one_more_source():
     # merge(p, phase1(C)) == route(C + [p]), so the gradients w.r.t. p and the
     # query agree with the routing backward's (the sources C enter through inter/lse)

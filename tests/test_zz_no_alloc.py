@@ -110,3 +110,78 @@ def test_noalloc_rejects_bad_arguments(gpu):
     bad = list(args)
     bad[3] = 0
     assert lib.attnres_route_bwd_noalloc(*bad) == _capi.ERR_ARG  # hidden = 0
+
+
+def _bwd_name(S, n, d, dt):
+    import ctypes
+
+    buf = ctypes.create_string_buffer(128)
+    _capi.check("attnres_route_bwd_kernel_name",
+                _capi.lib().attnres_route_bwd_kernel_name(S, n, d, code(dt), code(dt), buf, 128))
+    return buf.value.decode()
+
+
+# the row-per-wave backward (one 4-wave workgroup per CU: a different grid, so a
+# different share of the scratch array), at 6 KiB rows with the source rows in
+# registers and at 8 KiB rows with the first S - 6 rows kept in LDS
+STREAM_CASES = [(8, 4096, 3072, 21, "attnres_route_bwd_stream_c6_s8"), (9, 2048, 4096, 22, "attnres_route_bwd_stream_c8_s9")]
+
+
+def test_noalloc_row_per_wave_backward(gpu):
+    assert _capi.lib().attnres_init() == _capi.OK
+    prev = _capi.set_kernel_policy(_capi.POLICY_STREAM)
+    try:
+        for S, n, d, seed, kernel in STREAM_CASES:
+            print(f"noalloc row-per-wave S={S} n={n} d={d}", flush=True)
+            assert _bwd_name(S, n, d, torch.bfloat16) == kernel
+            case = make_case(gpu, S, n, d, torch.bfloat16, seed)
+            want = run(gpu, *case, noalloc=False)
+            got = run(gpu, *case, noalloc=True)
+            for a, b, name in zip(got, want, ("dsources", "dquery", "dgain")):
+                assert torch.equal(a, b), f"S={S} d={d}: {name} differs from attnres_route_bwd"
+            check_oracle(*case, *got)
+    finally:
+        _capi.set_kernel_policy(prev)
+
+
+def test_noalloc_under_graph_capture(gpu):
+    # after attnres_init(), one noalloc call captured in a HIP graph: every
+    # replay (with eager work between them, including another noalloc call of a
+    # different shape that overwrites the shared scratch array) equals the
+    # workspace entry point's result
+    assert _capi.lib().attnres_init() == _capi.OK
+    S, n, d = 4, 2048, 3072
+    case = make_case(gpu, S, n, d, torch.bfloat16, 31)
+    want = run(gpu, *case, noalloc=False)
+    src, q, gain, gout, glse = case
+    dsrc = torch.empty_like(src)
+    dq = torch.empty((d,), device=gpu, dtype=src.dtype)
+    dg = torch.empty((d,), device=gpu, dtype=src.dtype)
+    srcs = _capi.pointer_array([src[s].data_ptr() for s in range(S)])
+    dsrcs = _capi.pointer_array([dsrc[s].data_ptr() for s in range(S)])
+
+    def call(stream):
+        return _capi.lib().attnres_route_bwd_noalloc(
+            srcs, S, n, d, d, code(src.dtype), q.data_ptr(), gain.data_ptr(), code(src.dtype), 1e-5,
+            gout.data_ptr(), code(src.dtype), d, glse.data_ptr(), dsrcs, d, dq.data_ptr(), dg.data_ptr(), stream)
+
+    side = torch.cuda.Stream(gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):  # warm-up on the capture's kind of stream: kernel lookups happen here
+        assert call(side.cuda_stream) == _capi.OK
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = call(torch.cuda.current_stream(gpu).cuda_stream)
+    assert rc == _capi.OK
+    other = make_case(gpu, 2, 300, 1024, torch.float32, 32)
+    for rep in range(3):
+        print(f"noalloc graph replay {rep}", flush=True)
+        for t in (dsrc, dq, dg):
+            t.fill_(3.0)
+        run(gpu, *other, noalloc=True)  # leaves other values in the scratch array
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b, name in zip((dsrc, dq, dg), want, ("dsources", "dquery", "dgain")):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs from attnres_route_bwd"
