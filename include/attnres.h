@@ -217,6 +217,29 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
                       void* const* grad_sources, int64_t grad_ld, void* workspace, int64_t workspace_bytes,
                       void* grad_query, void* grad_gain, void* stream);
 
+/*
+ * attnres_route_bwd with addend rows: grad_sources[s] = dL/dsource_s +
+ * grad_addend[s], summed in fp32 and rounded once, for every s whose
+ * grad_addend[s] is non-NULL (rows of grad_ld, the gradient layout).
+ * grad_addend[s] may equal grad_sources[s]: the call then accumulates into
+ * that gradient in place.  No two sources may share gradient or addend rows.
+ * Addend rows need grad_out in the source dtype (bf16 with bf16, fp32 with
+ * fp32; ATTNRES_ERR_UNSUPPORTED otherwise).  grad_addend == NULL or all-NULL
+ * is attnres_route_bwd.
+ *
+ * Replaces autograd's summation of the gradients of a tensor that several
+ * routing calls read (a committed block is a source of every later routing
+ * point of the caller loop, src/model/llama.py:690-715; torch accumulates
+ * each use's gradient with a separate add): with it each use's gradient is
+ * added to the block's gradient inside the backward kernel.
+ */
+int attnres_route_bwd_add(const void* const* sources, int num_sources, int64_t num_tokens, int hidden,
+                          int64_t src_ld, int src_dtype, const void* query, const void* gain, int param_dtype,
+                          float eps, const void* grad_out, int grad_out_dtype, int64_t grad_out_ld,
+                          const float* grad_lse, void* const* grad_sources, const void* const* grad_addend,
+                          int64_t grad_ld, void* workspace, int64_t workspace_bytes, void* grad_query,
+                          void* grad_gain, void* stream);
+
 /* Size of the device scratch array attnres_route_bwd_noalloc uses (32 MiB:
  * 256 CUs x 4 workgroups x 8192 fp32 columns, the largest workspace
  * attnres_route_bwd_workspace_size() reports on an MI355X). */

@@ -53,6 +53,7 @@ EXPORTS = (
     "attnres_block_step",
     "attnres_route_bwd_workspace_size",
     "attnres_route_bwd",
+    "attnres_route_bwd_add",
     "attnres_route_bwd_noalloc",
     "attnres_route_bwd_kernel_name",
     "attnres_route_bwd_queries_workspace_size",
@@ -160,6 +161,33 @@ _SIGNATURES = {
             _c_i64,  # grad_out_ld
             _c_vp,  # grad_lse
             ctypes.POINTER(_c_vp),  # grad_sources
+            _c_i64,  # grad_ld
+            _c_vp,  # workspace
+            _c_i64,  # workspace_bytes
+            _c_vp,  # grad_query
+            _c_vp,  # grad_gain
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
+    "attnres_route_bwd_add": (
+        [
+            ctypes.POINTER(_c_vp),  # sources
+            _c_int,  # num_sources
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_i64,  # src_ld
+            _c_int,  # src_dtype
+            _c_vp,  # query
+            _c_vp,  # gain
+            _c_int,  # param_dtype
+            _c_float,  # eps
+            _c_vp,  # grad_out
+            _c_int,  # grad_out_dtype
+            _c_i64,  # grad_out_ld
+            _c_vp,  # grad_lse
+            ctypes.POINTER(_c_vp),  # grad_sources
+            ctypes.POINTER(_c_vp),  # grad_addend
             _c_i64,  # grad_ld
             _c_vp,  # workspace
             _c_i64,  # workspace_bytes
@@ -327,6 +355,11 @@ def route_bwd_workspace_size(num_tokens: int, hidden: int) -> int:
 
 def route_bwd(*args) -> None:
     check("attnres_route_bwd", lib().attnres_route_bwd(*args))
+
+
+def route_bwd_add(*args) -> None:
+    """attnres_route_bwd with addend rows (grad_sources[s] += grad_addend[s] where non-NULL)."""
+    check("attnres_route_bwd_add", lib().attnres_route_bwd_add(*args))
 
 
 def route_bwd_noalloc(*args) -> None:

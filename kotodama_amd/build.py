@@ -30,7 +30,7 @@ INCLUDE = PKG.parent / "include"
 LIB_NAME = "libattnres_hip.so"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
-NUM_PARTS = 8
+NUM_PARTS = 10
 
 # Packed-fp32 VALU ops are disabled for every HIP compile (the kernels are
 # written with scalar fp32 arithmetic).

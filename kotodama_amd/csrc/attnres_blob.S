@@ -1,4 +1,4 @@
-/* The eight gfx950 code-object parts, linked into libattnres_hip.so as bytes
+/* The ten gfx950 code-object parts, linked into libattnres_hip.so as bytes
  * and loaded with hipModuleLoadData.  The build passes -I<dir of the .hsaco>. */
     .section .rodata
     .balign 4096
@@ -33,4 +33,12 @@ attnres_hsaco_part6:
     .global attnres_hsaco_part7
 attnres_hsaco_part7:
     .incbin "attnres_gfx950_part7.hsaco"
+    .balign 4096
+    .global attnres_hsaco_part8
+attnres_hsaco_part8:
+    .incbin "attnres_gfx950_part8.hsaco"
+    .balign 4096
+    .global attnres_hsaco_part9
+attnres_hsaco_part9:
+    .incbin "attnres_gfx950_part9.hsaco"
     .section .note.GNU-stack,"",@progbits

@@ -31,10 +31,12 @@ extern "C" const unsigned char attnres_hsaco_part4[];
 extern "C" const unsigned char attnres_hsaco_part5[];
 extern "C" const unsigned char attnres_hsaco_part6[];
 extern "C" const unsigned char attnres_hsaco_part7[];
+extern "C" const unsigned char attnres_hsaco_part8[];
+extern "C" const unsigned char attnres_hsaco_part9[];
 
 namespace {
 
-constexpr int kParts = 8;
+constexpr int kParts = 10;
 constexpr int kMaxDevices = 64;
 constexpr int kMaxThreads = 512;  // __launch_bounds__ of every kernel
 
@@ -103,6 +105,8 @@ struct DeviceState {
   KernelSlot merge_stream[2 * kStreamMaxChunks];  // row-per-wave merge: query path x row KiB
   KernelSlot bwd[kBwdFuncs];
   KernelSlot bwd_stream[2 * 10];  // row-per-wave backward: rows of 6 / 8 KiB x S (1..9)
+  KernelSlot bwd_add[kBwdFuncs];   // the same with addend rows (_add)
+  KernelSlot bwd_stream_add[2 * 10];
   KernelSlot reduce_stage, reduce_cols, reduce_fin;
   KernelSlot merge_bwd[kMergeFuncs];
   KernelSlot bwd_mq[kBwdFuncs];  // batched-query backward: (source, grad_out) dtypes x S x V
@@ -186,7 +190,8 @@ int ensure_loaded(DeviceState** out) {
     if (!st.loaded.load(std::memory_order_relaxed)) {
       const unsigned char* blobs[kParts] = {attnres_hsaco_part0, attnres_hsaco_part1, attnres_hsaco_part2,
                                             attnres_hsaco_part3, attnres_hsaco_part4, attnres_hsaco_part5,
-                                            attnres_hsaco_part6, attnres_hsaco_part7};
+                                            attnres_hsaco_part6, attnres_hsaco_part7, attnres_hsaco_part8,
+                                            attnres_hsaco_part9};
       // On a failure nothing stays half-loaded: the next call starts over.
       auto unload = [&st](int n) {
         for (int j = 0; j < n; ++j) {
@@ -349,11 +354,18 @@ int get_merge(DeviceState& st, bool pbf, bool ibf, int v, int block, hipFunction
 int part_of_bwd(int s) { return s <= 8 ? 4 : 5; }
 constexpr int kReducePart = 4;
 
-int get_bwd(DeviceState& st, bool bf, bool gbf, int s, int v, int block, size_t lds, hipFunction_t* f, int* bpc) {
+// Kernels with addend rows (_add): parts 8 (S <= 4 and the row-per-wave ones) and 9.
+int part_of_bwd_add(int s) { return s <= 4 ? 8 : 9; }
+constexpr int kBwdStreamAddPart = 8;
+
+int get_bwd(DeviceState& st, bool bf, bool gbf, int s, int v, int block, size_t lds, hipFunction_t* f, int* bpc,
+            bool add = false) {
   const int idx = (((bf ? 0 : 2) + (gbf ? 0 : 1)) * kNumS + s) * 2 + (v - 1);
   char name[96];
-  snprintf(name, sizeof(name), "attnres_route_bwd_%s_g%s_s%d_v%d", bf ? "bf" : "f32", gbf ? "bf" : "f32", s, v);
-  return slot_get(st, st.bwd[idx], part_of_bwd(s), name, block, lds, f, bpc);
+  snprintf(name, sizeof(name), "attnres_route_bwd_%s_g%s_s%d_v%d%s", bf ? "bf" : "f32", gbf ? "bf" : "f32", s, v,
+           add ? "_add" : "");
+  return slot_get(st, add ? st.bwd_add[idx] : st.bwd[idx], add ? part_of_bwd_add(s) : part_of_bwd(s), name, block,
+                  lds, f, bpc);
 }
 
 // Row-per-wave backward (code-object part 4): bf16 sources and output
@@ -388,10 +400,11 @@ int bwd_stream_nch(bool bf, bool gbf, int num_sources, int hidden, int64_t num_t
   return want == 1 || (want < 0 && nch == 6 && num_tokens >= 64LL * num_cus) ? nch : 0;
 }
 
-int get_bwd_stream(DeviceState& st, int nch, int s, hipFunction_t* f) {
+int get_bwd_stream(DeviceState& st, int nch, int s, hipFunction_t* f, bool add = false) {
   char name[96];
-  snprintf(name, sizeof(name), "attnres_route_bwd_stream_c%d_s%d", nch, s);
-  return slot_function(st, st.bwd_stream[(nch == 8 ? 10 : 0) + s], 4, name, f);
+  snprintf(name, sizeof(name), "attnres_route_bwd_stream_c%d_s%d%s", nch, s, add ? "_add" : "");
+  const int idx = (nch == 8 ? 10 : 0) + s;
+  return slot_function(st, add ? st.bwd_stream_add[idx] : st.bwd_stream[idx], add ? kBwdStreamAddPart : 4, name, f);
 }
 
 // Batched-query backward kernels (code-object part 6).  Source-gradient
@@ -1067,7 +1080,7 @@ static int route_bwd_finish(hipFunction_t f, int grid, int block, size_t lds, De
                      const void* query, const void* gain, int param_dtype, float eps, const void* grad_out,
                      int grad_out_dtype, int64_t grad_out_ld, const float* grad_lse, void* const* grad_sources,
                      int64_t grad_ld, void* workspace, int64_t workspace_bytes, void* grad_query, void* grad_gain,
-                     void* stream) {
+                     void* stream, const void* const* grad_addend) {
   int rc = ATTNRES_OK;
   const int64_t need = (int64_t)grid * (int64_t)hidden * (int64_t)sizeof(float);
   if (workspace == nullptr || workspace_bytes < need)
@@ -1087,6 +1100,7 @@ static int route_bwd_finish(hipFunction_t f, int grid, int block, size_t lds, De
   for (int s = 0; s < num_sources; ++s) {
     P.src[s] = sources[s];
     P.dsrc[s] = grad_sources[s];
+    P.dadd[s] = grad_addend != nullptr ? grad_addend[s] : nullptr;
   }
   P.query = query;
   P.gain = gain;
@@ -1109,11 +1123,12 @@ static int route_bwd_finish(hipFunction_t f, int grid, int block, size_t lds, De
   return reduce_launch(*red, workspace, (int)grid, hidden, query, gain, param_dtype, grad_query, grad_gain, stream);
 }
 
-int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
-                      int src_dtype, const void* query, const void* gain, int param_dtype, float eps,
-                      const void* grad_out, int grad_out_dtype, int64_t grad_out_ld, const float* grad_lse,
-                      void* const* grad_sources, int64_t grad_ld, void* workspace, int64_t workspace_bytes,
-                      void* grad_query, void* grad_gain, void* stream) {
+static int route_bwd_impl(const void* const* sources, int num_sources, int64_t num_tokens, int hidden,
+                          int64_t src_ld, int src_dtype, const void* query, const void* gain, int param_dtype,
+                          float eps, const void* grad_out, int grad_out_dtype, int64_t grad_out_ld,
+                          const float* grad_lse, void* const* grad_sources, int64_t grad_ld, void* workspace,
+                          int64_t workspace_bytes, void* grad_query, void* grad_gain, void* stream,
+                          const void* const* grad_addend) {
   if (num_sources < 1 || num_sources > ATTNRES_MAX_SOURCES)
     return fail(ATTNRES_ERR_UNSUPPORTED, "backward: num_sources=%d outside [1, %d]", num_sources,
                 ATTNRES_MAX_SOURCES);
@@ -1149,17 +1164,28 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
     if (!aligned16(sources[s]) || !aligned16(grad_sources[s]))
       return fail(ATTNRES_ERR_ALIGN, "sources[%d] or grad_sources[%d] not 16-byte aligned", s, s);
   }
+  bool add = false;
+  if (grad_addend != nullptr) {
+    for (int s = 0; s < num_sources; ++s) {
+      if (grad_addend[s] == nullptr) continue;
+      if (!aligned16(grad_addend[s])) return fail(ATTNRES_ERR_ALIGN, "grad_addend[%d] not 16-byte aligned", s);
+      add = true;
+    }
+    if (add && bf != (grad_out_dtype == ATTNRES_DTYPE_BF16))
+      return fail(ATTNRES_ERR_UNSUPPORTED, "addend rows need grad_out in the source dtype");
+  }
   if (num_tokens == 0) return ATTNRES_OK;  // no tokens: the query gradients are not written
 
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
+  const void* const* addend = add ? grad_addend : nullptr;
   const int snch =
       bwd_stream_nch(bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, hidden, num_tokens, st->num_cus,
                      st->max_lds);
   if (snch > 0) {
     hipFunction_t f = nullptr;
-    rc = get_bwd_stream(*st, snch, num_sources, &f);
+    rc = get_bwd_stream(*st, snch, num_sources, &f, add);
     if (rc != ATTNRES_OK) return rc;
     const int64_t need_wg = (num_tokens + kBwdStreamWaves - 1) / kBwdStreamWaves;
     const int64_t cap = (int64_t)st->num_cus * (tuning().bwd_per_cu > 0 ? tuning().bwd_per_cu : 1);
@@ -1167,7 +1193,7 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
     return route_bwd_finish(f, grid, 64 * kBwdStreamWaves, bwd_stream_lds(snch, num_sources), *st, nchunk, sources,
                             num_sources, num_tokens, hidden, src_ld, query, gain, param_dtype, eps, grad_out,
                             grad_out_dtype, grad_out_ld, grad_lse, grad_sources, grad_ld, workspace, workspace_bytes,
-                            grad_query, grad_gain, stream);
+                            grad_query, grad_gain, stream, addend);
   }
   const int v = bwd_chunks_per_thread(nchunk, num_sources, num_tokens, st->num_cus);
   const int block = v == 1 ? round64(nchunk) : round64((nchunk + 1) / 2);
@@ -1180,7 +1206,7 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   if (lds + kBwdStaticLds > (size_t)st->max_lds)
     return fail(ATTNRES_ERR_UNSUPPORTED, "hidden=%d needs %zu bytes of LDS per workgroup (device limit %d)", hidden,
                 lds + kBwdStaticLds, st->max_lds);
-  rc = get_bwd(*st, bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, v, block, lds, &f, &bpc);
+  rc = get_bwd(*st, bf, grad_out_dtype == ATTNRES_DTYPE_BF16, num_sources, v, block, lds, &f, &bpc, add);
   if (rc != ATTNRES_OK) return rc;
   // Resident workgroups per CU: more than two (where registers allow three or
   // four) measured 4-12% slower for S >= 2 at the 3B shapes; S = 1 gains
@@ -1190,7 +1216,28 @@ int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_t
   if (grid > num_tokens) grid = num_tokens;
   return route_bwd_finish(f, (int)grid, block, lds, *st, nchunk, sources, num_sources, num_tokens, hidden, src_ld, query,
                           gain, param_dtype, eps, grad_out, grad_out_dtype, grad_out_ld, grad_lse, grad_sources,
-                          grad_ld, workspace, workspace_bytes, grad_query, grad_gain, stream);
+                          grad_ld, workspace, workspace_bytes, grad_query, grad_gain, stream, addend);
+}
+
+int attnres_route_bwd(const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
+                      int src_dtype, const void* query, const void* gain, int param_dtype, float eps,
+                      const void* grad_out, int grad_out_dtype, int64_t grad_out_ld, const float* grad_lse,
+                      void* const* grad_sources, int64_t grad_ld, void* workspace, int64_t workspace_bytes,
+                      void* grad_query, void* grad_gain, void* stream) {
+  return route_bwd_impl(sources, num_sources, num_tokens, hidden, src_ld, src_dtype, query, gain, param_dtype, eps,
+                        grad_out, grad_out_dtype, grad_out_ld, grad_lse, grad_sources, grad_ld, workspace,
+                        workspace_bytes, grad_query, grad_gain, stream, nullptr);
+}
+
+int attnres_route_bwd_add(const void* const* sources, int num_sources, int64_t num_tokens, int hidden,
+                          int64_t src_ld, int src_dtype, const void* query, const void* gain, int param_dtype,
+                          float eps, const void* grad_out, int grad_out_dtype, int64_t grad_out_ld,
+                          const float* grad_lse, void* const* grad_sources, const void* const* grad_addend,
+                          int64_t grad_ld, void* workspace, int64_t workspace_bytes, void* grad_query,
+                          void* grad_gain, void* stream) {
+  return route_bwd_impl(sources, num_sources, num_tokens, hidden, src_ld, src_dtype, query, gain, param_dtype, eps,
+                        grad_out, grad_out_dtype, grad_out_ld, grad_lse, grad_sources, grad_ld, workspace,
+                        workspace_bytes, grad_query, grad_gain, stream, grad_addend);
 }
 
 // Workspace of the batched-query backward: c1 coefficients (num_tokens, Q, S)

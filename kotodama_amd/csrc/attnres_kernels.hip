@@ -1723,9 +1723,12 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
 // are stored, so a workgroup's loads overlap its own stores.  The query
 // gradient sum_s c1_s x_s is accumulated in registers over all rows the
 // workgroup handles and written once as this workgroup's partial.
+// ADD: sources with a non-NULL P.dadd[s] get dx_s + dadd[s] (the addend chunk
+// is requested before the chunk's products and added in fp32, one rounding;
+// a source without an addend adds the 0 that an empty buffer resource reads).
 
 
-template <int S, int V, bool BF16, bool GBF>
+template <int S, int V, bool BF16, bool GBF, bool ADD = false>
 __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P) {
   constexpr bool PF = S <= ATTNRES_BWD_PREFETCH_MAX_S;
   using C = Chunk<BF16>;
@@ -1928,12 +1931,25 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
       for (int s = 0; s < S; ++s) {
         char* drow = reinterpret_cast<char*>(P.dsrc[s]) + tok * P.dsrc_ld * C::BYTES;
         const __amdgpu_buffer_rsrc_t drsrc = row_rsrc(drow, (uint32_t)(P.d * C::BYTES));
+        // ADD: the addend chunk through a buffer resource over its row, empty
+        // (loads return 0, no memory access) when the source has no addend,
+        // so the code has no branch
+        u32x4 ad = u32x4{0, 0, 0, 0};
+        if constexpr (ADD) {
+          const void* abase = P.dadd[s];
+          char* arow = reinterpret_cast<char*>(const_cast<void*>(abase)) + tok * P.dsrc_ld * C::BYTES;
+          ad = ld_row(row_rsrc(arow, abase != nullptr ? (uint32_t)(P.d * C::BYTES) : 0u), (uint32_t)chunk[k] * 16);
+        }
         float dx[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
           const float v = C::elem(xc[s][k], e);
           dx[e] = __builtin_fmaf(c2[s], v, __builtin_fmaf(c1[s], q[e], wgt[s] * gc[k].elem(e)));
           acc[e] = __builtin_fmaf(c1[s], v, acc[e]);
+        }
+        if constexpr (ADD) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) dx[e] += C::elem(ad, e);
         }
         if constexpr (BF16) {
           st_row(drsrc, (uint32_t)chunk[k] * 16,
@@ -2000,7 +2016,10 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
 // order and write one fp32 partial row per workgroup, as route_bwd_body does.
 // KL > 0: the first KL source rows are kept in the wave's part of the
 // dynamic LDS instead of registers (more sources than the registers hold).
-template <int S, int NCH, int KL>
+// ADD: sources with a non-NULL P.dadd[s] get dx_s + dadd[s]; the addend row
+// of source s + 1 is requested before the gradient of source s is formed, so
+// one addend row per wave is in flight behind the row being stored.
+template <int S, int NCH, int KL, bool ADD = false>
 __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_params& P) {
   static_assert(KL >= 0 && KL < S, "at least one source row is kept in registers");
   // Dynamic LDS in float4 slots [chunk][half][lane] (consecutive lanes 16
@@ -2152,8 +2171,25 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
       // ---- the gradient rows, one whole row per source ----
       // The kept rows are re-expanded here (opaque copies) rather than kept
       // unpacked from the first pass, which would double their registers.
+      // Addend rows through a buffer resource over the row, empty (loads
+      // return 0 without a memory access) for a source without an addend, so
+      // the loop has no branch.
+      u32x4 adA[ADD ? NCH : 1], adB[ADD ? NCH : 1];
+      auto load_add = [&](u32x4(&buf)[ADD ? NCH : 1], int s) {
+        const void* abase = P.dadd[s];
+        char* row = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(abase) + (uint64_t)t * drow_bytes));
+        const __amdgpu_buffer_rsrc_t ar = row_rsrc(row, abase != nullptr ? (uint32_t)(NCH * 1024) : 0u);
+#pragma unroll
+        for (int c = 0; c < (ADD ? NCH : 1); ++c) buf[c] = ld_row(ar, lane_off + (uint32_t)(c * 1024));
+      };
+      if constexpr (ADD) load_add(adA, 0);
 #pragma unroll
       for (int s = 0; s < S; ++s) {
+        u32x4(&ad_cur)[ADD ? NCH : 1] = (s & 1) ? adB : adA;
+        u32x4(&ad_nxt)[ADD ? NCH : 1] = (s & 1) ? adA : adB;
+        if constexpr (ADD) {
+          if (s + 1 < S) load_add(ad_nxt, s + 1 < S ? s + 1 : 0);
+        }
         u32x4 xk[NCH];
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
@@ -2175,10 +2211,14 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
           for (int w = 0; w < 4; ++w) {
             const uint32_t xw = xk[c][w], gw = g[c][w];
             const float x0 = bf_lo(xw), x1 = bf_hi(xw);
-            const float d0 = __builtin_fmaf(c2[s], x0, __builtin_fmaf(c1[s], q[2 * w], wgt[s] * bf_lo(gw)));
-            const float d1 = __builtin_fmaf(c2[s], x1, __builtin_fmaf(c1[s], q[2 * w + 1], wgt[s] * bf_hi(gw)));
+            float d0 = __builtin_fmaf(c2[s], x0, __builtin_fmaf(c1[s], q[2 * w], wgt[s] * bf_lo(gw)));
+            float d1 = __builtin_fmaf(c2[s], x1, __builtin_fmaf(c1[s], q[2 * w + 1], wgt[s] * bf_hi(gw)));
             dq[c][2 * w] = __builtin_fmaf(c1[s], x0, dq[c][2 * w]);
             dq[c][2 * w + 1] = __builtin_fmaf(c1[s], x1, dq[c][2 * w + 1]);
+            if constexpr (ADD) {
+              d0 += bf_lo(ad_cur[c][w]);
+              d1 += bf_hi(ad_cur[c][w]);
+            }
             pk[w] = pack_bf16(d0, d1);
           }
           st_row(dr, lane_off + (uint32_t)(c * 1024), pk);
@@ -3335,7 +3375,7 @@ __device__ __forceinline__ void reduce_dqw_body(const attnres_reduce_params& P) 
   ROUTE_TYPES(S, 1) \
   ROUTE_TYPES(S, 2)
 
-// The build compiles this file once per module part (ATTNRES_PART = 0..7)
+// The build compiles this file once per module part (ATTNRES_PART = 0..9)
 // so the parts build in parallel; the host maps each symbol to its part.
 #ifndef ATTNRES_PART
 #define ATTNRES_PART 0
@@ -3578,4 +3618,51 @@ BWD_DQW(bf, true, 1) BWD_DQW(bf, true, 2) BWD_DQW(f32, false, 1) BWD_DQW(f32, fa
 BWD_DQWM(1) BWD_DQWM(2)
 BWD_MQG(1, 1) BWD_MQG(2, 1) BWD_MQG(3, 1) BWD_MQG(4, 1) BWD_MQG(5, 1) BWD_MQG(6, 1) BWD_MQG(7, 1) BWD_MQG(8, 1)
 BWD_MQG(1, 2) BWD_MQG(2, 2) BWD_MQG(3, 2) BWD_MQG(4, 2) BWD_MQG(5, 2) BWD_MQG(6, 2) BWD_MQG(7, 2) BWD_MQG(8, 2)
+#endif
+
+// Backward with addend rows (dsrc[s] = dx_s + dadd[s]; in place when dadd[s] is
+// dsrc[s]): attnres_route_bwd_<in>_g<grad_out>_s<S>_v<V>_add for bf16 sources
+// with bf16 output gradients and fp32 with fp32, and
+// attnres_route_bwd_stream_c<NCH>_s<S>_add.  The same register targets as
+// the kernels without addends.
+#define BWD_ONE_ADD(INNAME, BF, GNAME, GBF, S, V)                                                      \
+  extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(BWD_WAVES_PER_EU(S, V)))) \
+  attnres_route_bwd_##INNAME##_g##GNAME##_s##S##_v##V##_add(attnres_route_bwd_params P) {              \
+    route_bwd_body<S, V, BF, GBF, true>(P);                                                            \
+  }
+#define BWD_S_ADD(S)                          \
+  BWD_ONE_ADD(bf, true, bf, true, S, 1)       \
+  BWD_ONE_ADD(bf, true, bf, true, S, 2)       \
+  BWD_ONE_ADD(f32, false, f32, false, S, 1)   \
+  BWD_ONE_ADD(f32, false, f32, false, S, 2)
+#define BWD_STREAM_ONE_ADD(S, NCH, KL)                                                                  \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))            \
+      attnres_route_bwd_stream_c##NCH##_s##S##_add(attnres_route_bwd_params P) {                         \
+    route_bwd_stream_body<S, NCH, KL, true>(P);                                                         \
+  }
+
+#if ATTNRES_PART == 8 || defined(ATTNRES_ALL_PARTS)
+BWD_STREAM_ONE_ADD(1, 6, 0) BWD_STREAM_ONE_ADD(2, 6, 0) BWD_STREAM_ONE_ADD(3, 6, 0) BWD_STREAM_ONE_ADD(4, 6, 0)
+BWD_STREAM_ONE_ADD(5, 6, 0) BWD_STREAM_ONE_ADD(6, 6, 0) BWD_STREAM_ONE_ADD(7, 6, 0) BWD_STREAM_ONE_ADD(8, 6, 0)
+BWD_STREAM_ONE_ADD(1, 8, 0) BWD_STREAM_ONE_ADD(2, 8, 0) BWD_STREAM_ONE_ADD(3, 8, 0) BWD_STREAM_ONE_ADD(4, 8, 0)
+BWD_STREAM_ONE_ADD(5, 8, 0) BWD_STREAM_ONE_ADD(6, 8, 0) BWD_STREAM_ONE_ADD(7, 8, 1) BWD_STREAM_ONE_ADD(8, 8, 2)
+BWD_STREAM_ONE_ADD(9, 8, 3)
+BWD_S_ADD(1)
+BWD_S_ADD(2)
+BWD_S_ADD(3)
+BWD_S_ADD(4)
+#endif
+#if ATTNRES_PART == 9 || defined(ATTNRES_ALL_PARTS)
+BWD_S_ADD(5)
+BWD_S_ADD(6)
+BWD_S_ADD(7)
+BWD_S_ADD(8)
+BWD_S_ADD(9)
+BWD_S_ADD(10)
+BWD_S_ADD(11)
+BWD_S_ADD(12)
+BWD_S_ADD(13)
+BWD_S_ADD(14)
+BWD_S_ADD(15)
+BWD_S_ADD(16)
 #endif

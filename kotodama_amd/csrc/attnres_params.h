@@ -69,11 +69,14 @@ typedef struct attnres_route_params {
  *   dx_s = w_s G + c1_s qw + c2_s x_s,  c1_s = dl_s r_s,  c2_s = -dl_s l_s r_s^2 / d,
  *   dl_s = w_s (G.x_s - G.out);  dqw += sum_s c1_s x_s
  * Every workgroup writes its dqw partial sum to dqw_part[blockIdx.x * d ...];
- * a reduce kernel then sums the partials in a fixed order.
+ * a reduce kernel then sums the partials in a fixed order.  The `_add`
+ * kernels store dsrc[s] = dx_s + dadd[s] (rounded once) for every source with
+ * a non-NULL dadd[s], which may be dsrc[s] itself (in-place accumulation).
  */
 typedef struct attnres_route_bwd_params {
   const void* src[ATTNRES_KMAX_SOURCES];
-  void* dsrc[ATTNRES_KMAX_SOURCES];  /* gradient rows of each source, src dtype */
+  void* dsrc[ATTNRES_KMAX_SOURCES];        /* gradient rows of each source, src dtype */
+  const void* dadd[ATTNRES_KMAX_SOURCES];  /* rows added to them (row stride dsrc_ld), or NULL */
   const void* query;
   const void* gain;
   const void* grad_out;  /* (n_tokens, d) */

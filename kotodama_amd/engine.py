@@ -149,25 +149,41 @@ def _route_points_autograd(model, embed: Tensor, sublayer: Callable[[int, Tensor
     """The caller loop of llama.py:697-715 under autograd, without the stacks.
 
     Every routing point passes the committed blocks and the partial as a list
-    of tensors (``attnres_hip::route_list``: one pointer per source, no
-    padded ``(max_S, B, T, D)`` copy, differentiable through the backward
-    kernels).  A commit appends the partial itself (nothing mutates it later)
-    and the new partial starts as the next sublayer output, which is what
-    ``zero.clone() + attn_out`` gives.
+    of tensors (one pointer per source, no padded ``(max_S, B, T, D)`` copy,
+    differentiable through the backward kernels).  A commit appends the
+    partial itself (nothing mutates it later) and the new partial starts as
+    the next sublayer output, which is what ``zero.clone() + attn_out`` gives.
+
+    In eager mode the committed blocks' gradients are summed inside the
+    routing backward kernels (``ops.route_accumulate`` with one
+    ``ops.GradSlot`` per block, handed back by the block's commit node)
+    instead of by one autograd add per use; under torch.compile (and where a
+    routing point's output dtype differs from the blocks') the calls are
+    ``attnres_hip::route_list`` and autograd sums them.
     """
     committed: list[Tensor] = []
+    slots: list[ops.GradSlot] = []
     partial: Optional[Tensor] = embed
+    accumulate = ops.accumulating_path_ok(embed)
 
     def route(query: Tensor, norm) -> Tensor:
         gain = norm.weight
         out_dtype = torch.promote_types(embed.dtype, torch.promote_types(query.dtype, gain.dtype))
-        return ops.route_list_call(committed + [partial], query, gain, float(norm.eps), out_dtype)[0][0]
+        srcs = committed + [partial]
+        if accumulate and out_dtype == embed.dtype and ops.accumulating_path_ok(query, gain, partial):
+            return ops.route_accumulate(srcs, slots + [None], query, gain, float(norm.eps), out_dtype)
+        return ops.route_list_call(srcs, query, gain, float(norm.eps), out_dtype)[0].squeeze(0)
 
     boundaries = model._attn_res_boundary_set
     for i, layer in enumerate(model.layers):
         h = route(layer.attn_res_query, layer.attn_res_norm)
         if i in boundaries:
-            committed.append(partial)
+            if accumulate:
+                slot = ops.GradSlot()
+                committed.append(ops.commit_block(partial, slot))
+                slots.append(slot)
+            else:
+                committed.append(partial)
             partial = None
         d = sublayer(2 * i, h)
         partial = d.to(torch.promote_types(embed.dtype, d.dtype)) if partial is None else partial + d

@@ -304,8 +304,11 @@ def _launch_route_bwd(
     eps: float,
     grad_out: Tensor,
     grad_lse: Optional[Tensor],
+    add_ptrs: Optional[list] = None,
 ) -> tuple[Tensor, Optional[Tensor]]:
-    """Launch attnres_route_bwd; returns (grad_query, grad_gain) in the parameter dtype.
+    """Launch attnres_route_bwd (attnres_route_bwd_add when ``add_ptrs`` holds
+    addend rows: ``None`` entries for none, the gradient's own pointer to add in
+    place); returns (grad_query, grad_gain) in the parameter dtype.
 
     ``query``/``gain`` are the op's inputs; when their dtypes differ the fold
     is taken here (as in the forward) and the product rule applied in torch.
@@ -320,29 +323,15 @@ def _launch_route_bwd(
         grad_lse = grad_lse.reshape(n).to(torch.float32).contiguous()
     with _DeviceStream(device) as stream:
         ws = torch.empty(max(1, _capi.route_bwd_workspace_size(n, d) // 4), device=device, dtype=torch.float32)
-        _capi.route_bwd(
-            _capi.pointer_array(ptrs),
-            len(ptrs),
-            n,
-            d,
-            d,
-            dtype_code(src_dtype),
-            kq.data_ptr(),
-            kg.data_ptr() if kg is not None else None,
-            pcode,
-            float(eps),
-            grad_out.data_ptr(),
-            dtype_code(grad_out.dtype),
-            d,
-            grad_lse.data_ptr() if grad_lse is not None else None,
-            _capi.pointer_array(grad_ptrs),
-            d,
-            ws.data_ptr(),
-            ws.numel() * 4,
-            dq.data_ptr(),
-            dg.data_ptr() if dg is not None else None,
-            stream,
-        )
+        head = (_capi.pointer_array(ptrs), len(ptrs), n, d, d, dtype_code(src_dtype), kq.data_ptr(),
+                kg.data_ptr() if kg is not None else None, pcode, float(eps), grad_out.data_ptr(),
+                dtype_code(grad_out.dtype), d, grad_lse.data_ptr() if grad_lse is not None else None,
+                _capi.pointer_array(grad_ptrs))
+        tail = (d, ws.data_ptr(), ws.numel() * 4, dq.data_ptr(), dg.data_ptr() if dg is not None else None, stream)
+        if add_ptrs is not None and any(a is not None for a in add_ptrs):
+            _capi.route_bwd_add(*head, _capi.pointer_array(add_ptrs), *tail)
+        else:
+            _capi.route_bwd(*head, *tail)
     if mixed:
         # dq is dL/dqw for qw = query * gain taken in the promoted dtype
         return (dq * gain).to(query.dtype).reshape(query.shape), (dq * q).to(gain.dtype)
@@ -619,6 +608,147 @@ def _route_list_backward(ctx, g_out, g_w, g_lse, g_inv, g_logits):
 
 
 route_list.register_autograd(_route_list_backward, setup_context=_route_list_setup_context)
+
+
+# ------------------------------------------------- summed block gradients --
+#
+# In the reference's training loop (llama.py:666-716) a committed block is a
+# source of every later routing point, and autograd sums the gradients those
+# calls return with one add kernel per use after the first (two rows read,
+# one written).  On the accumulating path each routing call's gradient of a
+# committed block is added into that block's gradient buffer inside the
+# backward kernel (attnres_route_bwd_add: one row read more), and the block's
+# commit node hands the sum to autograd once every routing call that read the
+# block has run its backward (autograd runs a node after all of its
+# consumers).  Eager only: under torch.compile the loop keeps the op path.
+
+
+class GradSlot:
+    """The gradient of one committed block, summed over the routing calls that
+    read it during one backward pass."""
+
+    __slots__ = ("buf", "task")
+
+    def __init__(self) -> None:
+        self.buf: Optional[Tensor] = None
+        self.task: Optional[int] = None
+
+    def target(self, like: Tensor) -> tuple[Tensor, bool]:
+        """The buffer for one more call's gradient and whether to add to it.
+        The first call of a backward pass (autograd graph task) writes a fresh
+        buffer; what an earlier pass left (one that did not reach the commit
+        node) is not added to."""
+        task = torch._C._current_graph_task_id()
+        if self.buf is None or self.task != task:
+            self.buf = torch.empty(like.shape, device=like.device, dtype=like.dtype)
+            self.task = task
+            return self.buf, False
+        return self.buf, True
+
+    def take(self) -> Optional[Tensor]:
+        buf = self.buf
+        self.buf, self.task = None, None
+        return buf
+
+
+class _Commit(torch.autograd.Function):
+    """A block becoming committed (llama.py:701-702): the identity forward; the
+    backward returns the gradient summed in the block's GradSlot, plus what
+    autograd delivered from uses outside the accumulating calls."""
+
+    @staticmethod
+    def forward(ctx, block, slot):
+        ctx.slot = slot
+        ctx.set_materialize_grads(False)
+        return block.view_as(block)
+
+    @staticmethod
+    def backward(ctx, grad):
+        acc = ctx.slot.take()
+        if acc is None:
+            return grad, None
+        if grad is not None:
+            acc.add_(grad)
+        return acc, None
+
+
+def commit_block(block: Tensor, slot: GradSlot) -> Tensor:
+    """``block`` as a committed source whose routing gradients accumulate in ``slot``."""
+    return _Commit.apply(block, slot)
+
+
+def _route_rows_forward(sources, query, gain, eps, out_dtype) -> Tensor:
+    out = _route_list_impl(list(sources), query, gain, eps, out_dtype, False, False, placeholders=False)[0]
+    return out.view(out.shape[1:])
+
+
+def _route_rows_backward(sources, grads, adds, query, gain, eps, grad_out) -> tuple[Tensor, Optional[Tensor]]:
+    """attnres_route_bwd(_add) into ``grads``; ``adds[s]`` is None or the row block added to source s's gradient."""
+    device = sources[0].device
+    d = sources[0].shape[-1]
+    n = sources[0].numel() // d
+    return _launch_route_bwd(
+        [t.data_ptr() for t in sources], [g.data_ptr() for g in grads], sources[0].dtype, n, d, device, query, gain,
+        eps, grad_out, None, add_ptrs=[a.data_ptr() if a is not None else None for a in adds],
+    )
+
+
+class _RouteAccumulate(torch.autograd.Function):
+    """route_list whose backward adds the gradients of the sources that have a
+    GradSlot into it instead of returning them (the others are returned)."""
+
+    @staticmethod
+    def forward(ctx, slots, eps, out_dtype, query, gain, *sources):
+        ctx.slots = slots
+        ctx.eps = eps
+        ctx.save_for_backward(query, gain, *sources)
+        ctx.set_materialize_grads(False)
+        return _route_rows_forward(sources, query, gain, eps, out_dtype)
+
+    @staticmethod
+    def backward(ctx, g_out):
+        n_src = len(ctx.slots)
+        if g_out is None:
+            return (None,) * (5 + n_src)
+        query, gain, *sources = ctx.saved_tensors
+        sources = [t if t.is_contiguous() else t.contiguous() for t in sources]
+        need = ctx.needs_input_grad
+        grads, adds = [], []
+        for src, slot, nd in zip(sources, ctx.slots, need[5:]):
+            if slot is None or not nd:
+                grads.append(torch.empty(src.shape, device=src.device, dtype=src.dtype))
+                adds.append(None)
+            else:
+                buf, acc = slot.target(src)
+                grads.append(buf)
+                adds.append(buf if acc else None)
+        dq, dg = _route_rows_backward(sources, grads, adds, query, gain, ctx.eps, g_out)
+        res = [None, None, None, dq if need[3] else None, dg if (gain is not None and need[4]) else None]
+        for g, slot, nd in zip(grads, ctx.slots, need[5:]):
+            res.append(g if (slot is None and nd) else None)
+        return tuple(res)
+
+
+def accumulating_path_ok(*tensors: Optional[Tensor]) -> bool:
+    """Whether the accumulating calls may run: eager autograd (no compile
+    tracing, no dispatch or function modes, no functorch transforms) on plain
+    tensors."""
+    if (
+        torch.compiler.is_compiling()
+        or torch._C._len_torch_dispatch_stack()
+        or torch._C._is_torch_function_mode_enabled()
+        or torch._C._are_functorch_transforms_active()
+    ):
+        return False
+    return all(t is None or type(t) in _PLAIN_TYPES for t in tensors)
+
+
+def route_accumulate(sources: Sequence[Tensor], slots: Sequence[Optional[GradSlot]], query: Tensor,
+                     gain: Optional[Tensor], eps: float, out_dtype: torch.dtype) -> Tensor:
+    """The routed ``(*batch, D)`` rows of ``sources`` (the first S-1 committed,
+    the last the partial); under autograd the gradients of the sources with a
+    slot are added into it (their dtype must equal ``out_dtype``)."""
+    return _RouteAccumulate.apply(tuple(slots), float(eps), out_dtype, query, gain, *sources)
 
 
 # ------------------------------------------------------------------ merge --

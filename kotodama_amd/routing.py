@@ -50,13 +50,13 @@ def route_static(
     if num_active:
         n = int(num_active)
         res = ops.route_call(buf, n, query, gain, float(norm.eps), out_dtype)
-        return res[0][0]
+        return res[0].squeeze(0)
     idx = [i for i, a in enumerate(active_mask.reshape(-1).tolist()) if a]
     if idx == list(range(len(idx))):
         res = ops.route_call(buf, len(idx), query, gain, float(norm.eps), out_dtype)
     else:
         res = ops.route_list_call([buf[i] for i in idx], query, gain, float(norm.eps), out_dtype)
-    return res[0][0]
+    return res[0].squeeze(0)
 
 
 def block_attn_res_from_list(sources: Sequence[Tensor], query: Tensor, norm) -> Tensor:
@@ -69,7 +69,7 @@ def block_attn_res_from_list(sources: Sequence[Tensor], query: Tensor, norm) -> 
     gain = norm.weight
     out_dtype = _out_dtype(sources[0].dtype, query, gain)
     res = ops.route_list_call(list(sources), query, gain, float(norm.eps), out_dtype)
-    return res[0][0]
+    return res[0].squeeze(0)
 
 
 def route_weights(buf: Tensor, num_active: int, query: Tensor, norm) -> tuple[Tensor, Tensor, Tensor]:
