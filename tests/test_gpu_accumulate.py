@@ -80,7 +80,7 @@ CASES = [
     (8, 4096, 3072, torch.bfloat16, _capi.POLICY_STREAM, "attnres_route_bwd_stream_c6_s8"),
     (9, 1024, 4096, torch.bfloat16, _capi.POLICY_STREAM, "attnres_route_bwd_stream_c8_s9"),
     (3, 700, 3072, torch.bfloat16, _capi.POLICY_WORKGROUP, "attnres_route_bwd_bf_gbf_s3_v"),
-    (8, 8192, 3072, torch.bfloat16, _capi.POLICY_WORKGROUP, "attnres_route_bwd_bf_gbf_s8_v2"),
+    (8, 64, 8184, torch.bfloat16, _capi.POLICY_WORKGROUP, "attnres_route_bwd_bf_gbf_s8_v2"),
     (9, 600, 4096, torch.bfloat16, _capi.POLICY_WORKGROUP, "attnres_route_bwd_bf_gbf_s9_v1"),
     (12, 300, 1024, torch.bfloat16, _capi.POLICY_WORKGROUP, "attnres_route_bwd_bf_gbf_s12_v"),
     (4, 500, 2048, torch.float32, _capi.POLICY_AUTO, "attnres_route_bwd_f32_gf32_s4_v"),
