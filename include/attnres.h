@@ -71,8 +71,9 @@ int attnres_set_kernel_policy(int policy);
  * Symbol name of the kernel a routing call launches for these arguments under
  * the current policy, for matching profiler output; written NUL-terminated
  * into buf.  fused: 0 = attnres_route_fwd (or attnres_block_step with no
- * delta and no commit), 1 = attnres_block_step accumulating a delta into the
- * partial, 2 = attnres_block_step with a commit.  equally_spaced: nonzero when
+ * delta and no commit), 1 = attnres_block_step or attnres_route_step
+ * accumulating a delta into the partial, 2 = attnres_block_step with a
+ * commit.  equally_spaced: nonzero when
  * the source pointers are equally spaced (a stacked buffer, an arena), zero
  * for arbitrary pointers (a list of separate tensors).  The same function
  * chooses the kernel here and at launch.  Loads the code object on the
@@ -174,6 +175,28 @@ int attnres_merge_kernel_name(int64_t num_tokens, int hidden, int partial_dtype,
  */
 int attnres_block_step(void* arena, int num_slots, int64_t slot_stride, int n_committed, int commit,
                        const void* delta, int64_t num_tokens, int hidden, int dtype, const void* query,
+                       const void* gain, int param_dtype, float eps, void* out, float* weights, float* lse,
+                       void* stream);
+
+/*
+ * One routing point of the training loop over separate block tensors, with
+ * the partial-block update fused in and written to a new buffer:
+ *   partial_out := partial + delta       (rounded to dtype)
+ *   out         := route over committed[0 .. num_committed-1] + partial_out
+ * Every row block is (num_tokens, hidden) contiguous rows of `dtype`, 16-byte
+ * aligned; `partial` and `delta` are read, partial_out (which must not
+ * overlap any input) and out are written; weights / lse as in
+ * attnres_route_fwd, or NULL.  Unlike attnres_block_step nothing is updated in
+ * place, so the partial block before the update stays valid (autograd keeps
+ * it for the backward of the previous routing point).
+ *
+ * Replaces one iteration step of the training loop _forward_attn_res
+ * (src/model/llama.py:706 or 712 `partial = partial + out`, then
+ * `_pad_and_stack` + `_route_static` at 709 or 715) without the stacked copy
+ * and without a separate add.
+ */
+int attnres_route_step(const void* const* committed, int num_committed, const void* partial, const void* delta,
+                       void* partial_out, int64_t num_tokens, int hidden, int dtype, const void* query,
                        const void* gain, int param_dtype, float eps, void* out, float* weights, float* lse,
                        void* stream);
 

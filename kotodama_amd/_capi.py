@@ -51,6 +51,7 @@ EXPORTS = (
     "attnres_merge_fwd",
     "attnres_merge_kernel_name",
     "attnres_block_step",
+    "attnres_route_step",
     "attnres_route_bwd_workspace_size",
     "attnres_route_bwd",
     "attnres_route_bwd_add",
@@ -166,6 +167,27 @@ _SIGNATURES = {
             _c_i64,  # workspace_bytes
             _c_vp,  # grad_query
             _c_vp,  # grad_gain
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
+    "attnres_route_step": (
+        [
+            ctypes.POINTER(_c_vp),  # committed
+            _c_int,  # num_committed
+            _c_vp,  # partial
+            _c_vp,  # delta
+            _c_vp,  # partial_out
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_int,  # dtype
+            _c_vp,  # query
+            _c_vp,  # gain
+            _c_int,  # param_dtype
+            _c_float,  # eps
+            _c_vp,  # out
+            _c_vp,  # weights
+            _c_vp,  # lse
             _c_vp,  # stream
         ],
         _c_int,
@@ -355,6 +377,11 @@ def route_bwd_workspace_size(num_tokens: int, hidden: int) -> int:
 
 def route_bwd(*args) -> None:
     check("attnres_route_bwd", lib().attnres_route_bwd(*args))
+
+
+def route_step(*args) -> None:
+    """attnres_route_step: the partial update into a new buffer, then the routing over committed + it."""
+    check("attnres_route_step", lib().attnres_route_step(*args))
 
 
 def route_bwd_add(*args) -> None:

@@ -63,8 +63,8 @@ constexpr int kRouteFuncs = kTypeCombos * kNumS * 2 * 2;
 constexpr int kMergeFuncs = 4 * 2;
 constexpr int kStreamMaxChunks = 8;  // rows of up to 8 KiB
 constexpr int kStreamWaves = 4;      // waves per workgroup of the streaming kernels
-// combo x out dtype x KiB x variant (plain / pointer table / fused)
-constexpr int kStreamFuncs = kTypeCombos * 2 * kStreamMaxChunks * 3;
+// combo x out dtype x KiB x variant (plain / pointer table / fused / fused with the pointer table)
+constexpr int kStreamFuncs = kTypeCombos * 2 * kStreamMaxChunks * 4;
 constexpr int kBwdFuncs = 4 * kNumS * 2;  // (source, grad_out) dtype pairs x S x V
 constexpr int kBwdMaxPerCu = 4;           // workgroups per CU the backward grid may use (workspace bound)
 constexpr size_t kBwdStaticLds = 2 * ATTNRES_KMAX_WAVES * 48 * sizeof(float);  // reduction buffer, S = 16
@@ -283,12 +283,13 @@ int slot_get(DeviceState& st, KernelSlot& k, int part, const char* name, int blo
 
 int part_of_stream(int nch) { return nch <= 4 ? 2 : 1; }
 
-enum StreamVariant { kStreamPlain = 0, kStreamTable = 1, kStreamFused = 2 };
-const char* const kStreamVariantNames[3] = {"plain", "table", "fused"};
+enum StreamVariant { kStreamPlain = 0, kStreamTable = 1, kStreamFused = 2, kStreamFusedTable = 3 };
+constexpr int kStreamVariants = 4;
+const char* const kStreamVariantNames[kStreamVariants] = {"plain", "table", "fused", "fusedtable"};
 
 int get_stream(DeviceState& st, int combo, bool out_bf, int nch, int variant, hipFunction_t* f, int* bpc,
                int* static_lds) {
-  const int idx = ((combo * 2 + (out_bf ? 0 : 1)) * kStreamMaxChunks + (nch - 1)) * 3 + variant;
+  const int idx = ((combo * 2 + (out_bf ? 0 : 1)) * kStreamMaxChunks + (nch - 1)) * kStreamVariants + variant;
   static const char* combo_names[kTypeCombos] = {"bf_d2", "bf_fm", "f32_fm"};
   char name[96];
   snprintf(name, sizeof(name), "attnres_stream_%s_o%s_c%d_%s", combo_names[combo], out_bf ? "bf" : "f32", nch,
@@ -610,9 +611,10 @@ RouteChoice plan_route(int num_sources, int64_t num_tokens, int hidden, int src_
   RouteChoice ch = choose_route(num_sources, num_tokens, hidden, src_dtype, param_dtype, num_queries, st.num_cus,
                                 stream_ok, mode != ATTNRES_MODE_PLAIN);
   if (ch.stream) {
-    ch.variant = mode != ATTNRES_MODE_PLAIN ? kStreamFused
-                 : (equally_spaced || num_sources < 2) ? kStreamPlain
-                                                       : kStreamTable;
+    const bool spaced = equally_spaced || num_sources < 2;
+    ch.variant = mode != ATTNRES_MODE_PLAIN ? (spaced ? kStreamFused : kStreamFusedTable)
+                 : spaced ? kStreamPlain
+                          : kStreamTable;
   } else if (ch.v != 0) {
     choose_qg(ch, num_sources, num_queries, hidden, out_dtype, mode, st.max_lds);
   }
@@ -665,7 +667,8 @@ MergeChoice plan_merge(int64_t num_tokens, int hidden, int partial_dtype, int in
 int route_launch(const void* const* sources, int num_sources, int64_t num_tokens, int hidden, int64_t src_ld,
                  int src_dtype, const void* query, const void* gain, int num_queries, int param_dtype, float eps,
                  void* out, int out_dtype, int64_t out_ld, int64_t out_qstride, float* weights, float* lse,
-                 float* inv_rms, float* logits, int mode, const void* delta, int64_t delta_ld, void* stream) {
+                 float* inv_rms, float* logits, int mode, const void* delta, int64_t delta_ld, void* stream,
+                 void* partial_out = nullptr) {
   if (num_sources < 0 || num_sources > ATTNRES_MAX_SOURCES)
     return fail(ATTNRES_ERR_UNSUPPORTED, "num_sources=%d outside [0, %d]", num_sources, ATTNRES_MAX_SOURCES);
   if (num_sources > 0 && sources == nullptr) return fail(ATTNRES_ERR_ARG, "sources is NULL");
@@ -707,6 +710,8 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
     if (delta == nullptr) return fail(ATTNRES_ERR_ARG, "delta is NULL");
     if (!aligned16(delta) || (delta_ld * esize(src_dtype)) % 16 != 0)
       return fail(ATTNRES_ERR_ALIGN, "delta rows not 16-byte aligned");
+    if (partial_out != nullptr && !aligned16(partial_out))
+      return fail(ATTNRES_ERR_ALIGN, "partial_out not 16-byte aligned");
   }
   if (num_tokens == 0) return ATTNRES_OK;
 
@@ -741,7 +746,9 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
     const int64_t out_row_bytes = (int64_t)hidden * esize(out_dtype);
     // the fused variants write their partial rows back as they go: batching
     // the output rows alone measured 1-2% slower there
-    out_batch = ch.variant == kStreamFused ? 1 : stream_out_batch(num_sources, out_row_bytes, slds, st->max_lds, waves);
+    out_batch = (ch.variant == kStreamFused || ch.variant == kStreamFusedTable)
+                    ? 1
+                    : stream_out_batch(num_sources, out_row_bytes, slds, st->max_lds, waves);
     if (out_batch > 1) stream_lds = (size_t)waves * out_batch * out_row_bytes;
   } else if (ch.qg_lds > 0) {
     rc = get_route_qg(*st, num_sources, ch.v, block, ch.qg_lds, &f, &bpc);
@@ -757,6 +764,7 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   P.query = query;
   P.gain = gain;
   P.delta = delta;
+  P.partial_out = partial_out;
   P.out = out;
   P.weights = weights;
   P.lse = lse;
@@ -1058,6 +1066,39 @@ int attnres_block_step(void* arena, int num_slots, int64_t slot_stride, int n_co
   return route_launch(srcs, S, num_tokens, hidden, hidden, dtype, query, gain, 1, param_dtype, eps, out, dtype,
                       hidden, (int64_t)num_tokens * hidden, weights, lse, nullptr, nullptr, mode, delta, hidden,
                       stream);
+}
+
+int attnres_route_step(const void* const* committed, int num_committed, const void* partial, const void* delta,
+                       void* partial_out, int64_t num_tokens, int hidden, int dtype, const void* query,
+                       const void* gain, int param_dtype, float eps, void* out, float* weights, float* lse,
+                       void* stream) {
+  if (num_committed < 0) return fail(ATTNRES_ERR_ARG, "num_committed=%d < 0", num_committed);
+  if (num_committed > 0 && committed == nullptr) return fail(ATTNRES_ERR_ARG, "committed is NULL");
+  if (partial == nullptr || delta == nullptr || partial_out == nullptr)
+    return fail(ATTNRES_ERR_ARG, "partial/delta/partial_out is NULL");
+  const int S = num_committed + 1;
+  if (S > ATTNRES_MAX_SOURCES)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "%d sources exceed the maximum %d", S, ATTNRES_MAX_SOURCES);
+  if (!valid_dtype(dtype)) return fail(ATTNRES_ERR_ARG, "unknown dtype code %d", dtype);
+  if (num_tokens < 0 || hidden <= 0) return fail(ATTNRES_ERR_ARG, "bad num_tokens/hidden");
+  const char* po = static_cast<const char*>(partial_out);
+  const int64_t bytes = num_tokens * (int64_t)hidden * esize(dtype);
+  auto overlaps = [&](const void* p) {
+    const char* q = static_cast<const char*>(p);
+    return q < po + bytes && po < q + bytes;
+  };
+  const void* srcs[ATTNRES_MAX_SOURCES];
+  for (int s = 0; s < num_committed; ++s) {
+    srcs[s] = committed[s];
+    if (srcs[s] != nullptr && bytes > 0 && overlaps(srcs[s]))
+      return fail(ATTNRES_ERR_ARG, "partial_out overlaps committed[%d]", s);
+  }
+  if (bytes > 0 && (overlaps(partial) || overlaps(delta)))
+    return fail(ATTNRES_ERR_ARG, "partial_out overlaps partial or delta");
+  srcs[num_committed] = partial;
+  return route_launch(srcs, S, num_tokens, hidden, hidden, dtype, query, gain, 1, param_dtype, eps, out, dtype, hidden,
+                      (int64_t)num_tokens * hidden, weights, lse, nullptr, nullptr, ATTNRES_MODE_ACCUM, delta, hidden,
+                      stream, partial_out);
 }
 
 int attnres_route_bwd_workspace_size(int64_t num_tokens, int hidden, int64_t* bytes) {

@@ -684,10 +684,12 @@ __device__ __forceinline__ void route_body(const attnres_route_params& P) {
           }
         }
       }
-      // The updated partial row is written back after the output row: a store
-      // issued before the dot products would be waited for with the loads.
+      // The updated partial row is written back (or to partial_out) after the
+      // output row: a store issued before the dot products would be waited for
+      // with the loads.
       if (P.mode != ATTNRES_MODE_PLAIN) {
-        char* prow = reinterpret_cast<char*>(const_cast<void*>(P.src[S - 1])) + tok * row_bytes_ld;
+        void* pdst = P.partial_out != nullptr ? P.partial_out : const_cast<void*>(P.src[S - 1]);
+        char* prow = reinterpret_cast<char*>(pdst) + tok * row_bytes_ld;
         const __amdgpu_buffer_rsrc_t prsrc = row_rsrc(prow, (uint32_t)(P.d * C::BYTES));
 #pragma unroll
         for (int k = 0; k < V; ++k) {
@@ -1497,9 +1499,11 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
             }
           }
         }
-        // the updated partial row is written back (in a branch: an unconditional
-        // write-back through an empty resource made these kernels spill)
-        const uint64_t pbase = TBL ? src_tbl[S - 1] : src0 + (uint64_t)(S - 1) * src_stride;
+        // the updated partial row is written back, or to partial_out (in a
+        // branch: an unconditional write-back through an empty resource made
+        // these kernels spill)
+        const uint64_t pout = reinterpret_cast<uint64_t>(P.partial_out);
+        const uint64_t pbase = pout != 0 ? pout : TBL ? src_tbl[S - 1] : src0 + (uint64_t)(S - 1) * src_stride;
         char* prow = const_cast<char*>(uniform_ptr(pbase + (uint64_t)t * row_bytes));
         const __amdgpu_buffer_rsrc_t prsrc = row_rsrc(prow, (uint32_t)(NCH * 1024));
 #pragma unroll
@@ -3440,7 +3444,7 @@ MERGE_STREAM(7)
 MERGE_STREAM(8)
 #endif
 
-// Streaming kernels: attnres_stream_<in>_<qw>_c<NCH>_<plain|fused>, row = NCH KiB.
+// Streaming kernels: attnres_stream_<in>_<qw>_c<NCH>_<plain|table|fused|fusedtable>, row = NCH KiB.
 // Occupancy target (waves per SIMD): the plain and table kernels run one
 // wave per SIMD (one workgroup per CU), so their register budget also holds
 // the staged output rows past the LDS slots.
@@ -3463,6 +3467,11 @@ MERGE_STREAM(8)
       __attribute__((amdgpu_waves_per_eu(STREAM_FUSED_WAVES_PER_EU(NCH))))                              \
       attnres_stream_##INNAME##_##QNAME##_o##ONAME##_c##NCH##_fused(attnres_route_params P) {           \
     stream_body<NCH, BF, QD2, true, OBF, false>(P);                                                     \
+  }                                                                                                     \
+  extern "C" __global__ void __launch_bounds__(64 * ATTNRES_STREAM_WAVES)                               \
+      __attribute__((amdgpu_waves_per_eu(STREAM_FUSED_WAVES_PER_EU(NCH))))                              \
+      attnres_stream_##INNAME##_##QNAME##_o##ONAME##_c##NCH##_fusedtable(attnres_route_params P) {      \
+    stream_body<NCH, BF, QD2, true, OBF, true>(P);                                                      \
   }
 #define STREAM_ONE(INNAME, BF, QNAME, QD2, NCH)             \
   STREAM_ONE_OUT(INNAME, BF, QNAME, QD2, bf, true, NCH)     \

@@ -26,6 +26,8 @@
  *   query       (num_queries, d) pseudo-queries, param dtype
  *   gain        (d,) RMSNorm gain folded into every query, or NULL (pre-folded)
  *   delta       (n_tokens, d) sublayer output for MODE_ACCUM / MODE_SET, else NULL
+ *   partial_out where MODE_ACCUM / MODE_SET write the updated partial rows (same row
+ *               stride as the sources), or NULL to write them back over src[S-1]
  *   out         (num_queries, n_tokens, d): query q, token t at
  *               out + q*out_qstride + t*out_ld elements
  *   weights     (num_queries, S, n_tokens) fp32 softmax weights, or NULL
@@ -38,6 +40,7 @@ typedef struct attnres_route_params {
   const void* query;
   const void* gain;
   const void* delta;
+  void* partial_out;
   void* out;
   float* weights;
   float* lse;

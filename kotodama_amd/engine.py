@@ -148,37 +148,49 @@ def _grad_needed(model, embed: Tensor) -> bool:
 def _route_points_autograd(model, embed: Tensor, sublayer: Callable[[int, Tensor], Tensor]) -> Tensor:
     """The caller loop of llama.py:697-715 under autograd, without the stacks.
 
-    Every routing point passes the committed blocks and the partial as a list
-    of tensors (one pointer per source, no padded ``(max_S, B, T, D)`` copy,
-    differentiable through the backward kernels).  A commit appends the
+    Every routing point passes the committed blocks and the partial as
+    separate tensors (one pointer per source, no padded ``(max_S, B, T, D)``
+    copy, differentiable through the backward kernels).  A commit appends the
     partial itself (nothing mutates it later) and the new partial starts as
     the next sublayer output, which is what ``zero.clone() + attn_out`` gives.
 
-    In eager mode the committed blocks' gradients are summed inside the
-    routing backward kernels (``ops.route_accumulate`` with one
-    ``ops.GradSlot`` per block, handed back by the block's commit node)
-    instead of by one autograd add per use; under torch.compile (and where a
-    routing point's output dtype differs from the blocks') the calls are
-    ``attnres_hip::route_list`` and autograd sums them.
+    In eager mode each point is one ``ops.route_point``: the partial's update
+    ``partial + sublayer output`` is formed by the routing kernel into a new
+    tensor (attnres_route_step), and in the backward the gradients are summed
+    inside the routing backward kernel — each committed block's over the
+    points that read it (``ops.GradSlot``, handed back by the block's commit
+    node) and the partial's routing gradient with the gradient of the partial
+    that the next point routes — so autograd adds no gradients and the loop
+    launches no adds.  Under torch.compile, and at points whose output dtype
+    or sublayer output dtype differs from the blocks', the point is an
+    ``attnres_hip::route_list`` call with torch adds, and autograd sums.
     """
     committed: list[Tensor] = []
     slots: list[ops.GradSlot] = []
+    dt = embed.dtype
+    fused = ops.accumulating_path_ok(embed)
     partial: Optional[Tensor] = embed
-    accumulate = ops.accumulating_path_ok(embed)
+    pending: Optional[Tensor] = None  # the sublayer output not yet added to the partial
 
-    def route(query: Tensor, norm) -> Tensor:
+    def point(query: Tensor, norm) -> Tensor:
+        nonlocal partial, pending
         gain = norm.weight
-        out_dtype = torch.promote_types(embed.dtype, torch.promote_types(query.dtype, gain.dtype))
-        srcs = committed + [partial]
-        if accumulate and out_dtype == embed.dtype and ops.accumulating_path_ok(query, gain, partial):
-            return ops.route_accumulate(srcs, slots + [None], query, gain, float(norm.eps), out_dtype)
-        return ops.route_list_call(srcs, query, gain, float(norm.eps), out_dtype)[0].squeeze(0)
+        out_dtype = torch.promote_types(dt, torch.promote_types(query.dtype, gain.dtype))
+        if (fused and out_dtype == dt and (pending is None or pending.dtype == dt)
+                and ops.accumulating_path_ok(query, gain, partial, pending)):
+            h, partial = ops.route_point(committed, slots, partial, pending, query, gain, float(norm.eps), out_dtype)
+        else:
+            if pending is not None:
+                partial = partial + pending
+            h = ops.route_list_call(committed + [partial], query, gain, float(norm.eps), out_dtype)[0].squeeze(0)
+        pending = None
+        return h
 
     boundaries = model._attn_res_boundary_set
     for i, layer in enumerate(model.layers):
-        h = route(layer.attn_res_query, layer.attn_res_norm)
+        h = point(layer.attn_res_query, layer.attn_res_norm)
         if i in boundaries:
-            if accumulate:
+            if fused:
                 slot = ops.GradSlot()
                 committed.append(ops.commit_block(partial, slot))
                 slots.append(slot)
@@ -186,10 +198,13 @@ def _route_points_autograd(model, embed: Tensor, sublayer: Callable[[int, Tensor
                 committed.append(partial)
             partial = None
         d = sublayer(2 * i, h)
-        partial = d.to(torch.promote_types(embed.dtype, d.dtype)) if partial is None else partial + d
-        h = route(layer.mlp_res_query, layer.mlp_res_norm)
-        partial = partial + sublayer(2 * i + 1, h)
-    return route(model.final_res_query, model.final_res_norm)
+        if partial is None:
+            partial = d.to(torch.promote_types(dt, d.dtype))
+        else:
+            pending = d
+        h = point(layer.mlp_res_query, layer.mlp_res_norm)
+        pending = sublayer(2 * i + 1, h)
+    return point(model.final_res_query, model.final_res_norm)
 
 
 def forward_attn_res(model, embed: Tensor, mask: Optional[Tensor] = None) -> Tensor:

@@ -693,28 +693,76 @@ def _route_rows_backward(sources, grads, adds, query, gain, eps, grad_out) -> tu
     )
 
 
-class _RouteAccumulate(torch.autograd.Function):
-    """route_list whose backward adds the gradients of the sources that have a
-    GradSlot into it instead of returning them (the others are returned)."""
+def _route_rows_step(committed, partial, delta, query, gain, eps, out_dtype) -> tuple[Tensor, Tensor]:
+    """attnres_route_step: (routed rows, partial + delta in a new tensor)."""
+    device = _require_device(*committed, partial, delta, query, gain)
+    ref = partial
+    for t in (*committed, delta):
+        if t.shape != ref.shape or t.dtype != ref.dtype:
+            raise ValueError("attnres_hip: blocks, partial and delta must share shape and dtype")
+    d = ref.shape[-1]
+    n = ref.numel() // d
+    q = query.reshape(1, -1) if query.dim() == 1 else query
+    kq, kg, pcode = _fold_query(q, gain)
+    srcs = [t if t.is_contiguous() else t.contiguous() for t in committed]
+    partial = partial if partial.is_contiguous() else partial.contiguous()
+    delta = delta if delta.is_contiguous() else delta.contiguous()
+    new_partial = torch.empty(ref.shape, device=device, dtype=ref.dtype)
+    out = torch.empty(ref.shape, device=device, dtype=out_dtype)
+    with _DeviceStream(device) as stream:
+        _capi.route_step(
+            _capi.pointer_array([t.data_ptr() for t in srcs]), len(srcs), partial.data_ptr(), delta.data_ptr(),
+            new_partial.data_ptr(), n, d, dtype_code(ref.dtype), kq.data_ptr(),
+            kg.data_ptr() if kg is not None else None, pcode, float(eps), out.data_ptr(), None, None, stream,
+        )
+    return out, new_partial
+
+
+class _RoutePoint(torch.autograd.Function):
+    """One routing point of the training loop, with the blocks' gradient sums
+    inside the backward kernel.
+
+    Inputs: the committed blocks (``slots[s]`` holds the GradSlot of block s,
+    into which its gradient is added instead of being returned), the partial
+    block before this point's update and ``delta``, the previous sublayer's
+    output, or None when the partial is routed as it is.  Outputs: the routed
+    rows and the partial block this point routed (``partial + delta`` in a new
+    tensor, attnres_route_step; or the partial itself, as a view).  The
+    backward forms the routed partial's gradient as the routing gradient plus
+    the gradient of the partial output (attnres_route_bwd_add with that
+    gradient as the addend), which is also the gradient of ``partial`` and of
+    ``delta``: autograd adds nothing."""
 
     @staticmethod
-    def forward(ctx, slots, eps, out_dtype, query, gain, *sources):
+    def forward(ctx, slots, eps, out_dtype, query, gain, delta, *sources):
+        committed, partial = sources[:-1], sources[-1]
+        if delta is None:
+            out = _route_rows_forward(sources, query, gain, eps, out_dtype)
+            routed = partial
+            new_partial = partial.view_as(partial)
+        else:
+            out, new_partial = _route_rows_step(committed, partial, delta, query, gain, eps, out_dtype)
+            routed = new_partial
         ctx.slots = slots
         ctx.eps = eps
-        ctx.save_for_backward(query, gain, *sources)
+        ctx.has_delta = delta is not None
+        ctx.save_for_backward(query, gain, routed, *committed)
         ctx.set_materialize_grads(False)
-        return _route_rows_forward(sources, query, gain, eps, out_dtype)
+        return out, new_partial
 
     @staticmethod
-    def backward(ctx, g_out):
-        n_src = len(ctx.slots)
-        if g_out is None:
-            return (None,) * (5 + n_src)
-        query, gain, *sources = ctx.saved_tensors
-        sources = [t if t.is_contiguous() else t.contiguous() for t in sources]
+    def backward(ctx, g_out, g_partial):
+        n_com = len(ctx.slots)
         need = ctx.needs_input_grad
+        if g_out is None:
+            # only the partial output is used downstream: its gradient passes through
+            gp = g_partial
+            return (None,) * 5 + (gp if ctx.has_delta and need[5] else None,) + (None,) * n_com + (
+                gp if need[6 + n_com] else None,)
+        query, gain, routed, *committed = ctx.saved_tensors
+        sources = [t if t.is_contiguous() else t.contiguous() for t in (*committed, routed)]
         grads, adds = [], []
-        for src, slot, nd in zip(sources, ctx.slots, need[5:]):
+        for src, slot, nd in zip(sources[:-1], ctx.slots, need[6:6 + n_com]):
             if slot is None or not nd:
                 grads.append(torch.empty(src.shape, device=src.device, dtype=src.dtype))
                 adds.append(None)
@@ -722,10 +770,18 @@ class _RouteAccumulate(torch.autograd.Function):
                 buf, acc = slot.target(src)
                 grads.append(buf)
                 adds.append(buf if acc else None)
+        p = sources[-1]
+        gp = torch.empty(p.shape, device=p.device, dtype=p.dtype)
+        grads.append(gp)
+        if g_partial is not None and not g_partial.is_contiguous():
+            g_partial = g_partial.contiguous()
+        adds.append(g_partial)
         dq, dg = _route_rows_backward(sources, grads, adds, query, gain, ctx.eps, g_out)
-        res = [None, None, None, dq if need[3] else None, dg if (gain is not None and need[4]) else None]
-        for g, slot, nd in zip(grads, ctx.slots, need[5:]):
+        res = [None, None, None, dq if need[3] else None, dg if (gain is not None and need[4]) else None,
+               gp if ctx.has_delta and need[5] else None]
+        for g, slot, nd in zip(grads[:-1], ctx.slots, need[6:6 + n_com]):
             res.append(g if (slot is None and nd) else None)
+        res.append(gp if need[6 + n_com] else None)
         return tuple(res)
 
 
@@ -743,12 +799,15 @@ def accumulating_path_ok(*tensors: Optional[Tensor]) -> bool:
     return all(t is None or type(t) in _PLAIN_TYPES for t in tensors)
 
 
-def route_accumulate(sources: Sequence[Tensor], slots: Sequence[Optional[GradSlot]], query: Tensor,
-                     gain: Optional[Tensor], eps: float, out_dtype: torch.dtype) -> Tensor:
-    """The routed ``(*batch, D)`` rows of ``sources`` (the first S-1 committed,
-    the last the partial); under autograd the gradients of the sources with a
-    slot are added into it (their dtype must equal ``out_dtype``)."""
-    return _RouteAccumulate.apply(tuple(slots), float(eps), out_dtype, query, gain, *sources)
+def route_point(committed: Sequence[Tensor], slots: Sequence[Optional[GradSlot]], partial: Tensor,
+                delta: Optional[Tensor], query: Tensor, gain: Optional[Tensor], eps: float,
+                out_dtype: torch.dtype) -> tuple[Tensor, Tensor]:
+    """One routing point of the training loop: (routed ``(*batch, D)`` rows, the
+    partial block it routed).  The partial routed is ``partial + delta`` (a new
+    tensor) or, with ``delta`` None, ``partial`` itself.  Under autograd the
+    gradient of committed block s is added into ``slots[s]`` (blocks, partial,
+    delta and ``out_dtype`` share one dtype)."""
+    return _RoutePoint.apply(tuple(slots), float(eps), out_dtype, query, gain, delta, *committed, partial)
 
 
 # ------------------------------------------------------------------ merge --

@@ -2,8 +2,8 @@
 
 ``forward_attn_res`` under autograd sums each committed block's gradient over
 the routing calls that read it inside the backward kernel
-(``ops.route_accumulate`` + ``ops.GradSlot`` + the commit node).  Here the
-two kernel launches (``ops._route_rows_forward`` / ``_route_rows_backward``)
+(``ops.route_point`` + ``ops.GradSlot`` + the commit node).  Here the
+kernel launches (``ops._route_rows_forward`` / ``_route_rows_step`` / ``_route_rows_backward``)
 are replaced by float64 torch restatements of the reference op sequence
 (llama.py:640-644) that honour the same contract — ``grads[s]`` receives
 dL/dsource_s plus ``adds[s]`` when that is given — so the test checks what
@@ -53,7 +53,12 @@ def cpu_kernels(monkeypatch):
         calls.append([("add" if a is not None else "write") for a in adds])
         return q.grad.to(query.dtype), (g.grad.to(gain.dtype) if g is not None else None)
 
+    def step(committed, partial, delta, query, gain, eps, out_dtype):
+        new_partial = partial.detach() + delta.detach()
+        return fwd(list(committed) + [new_partial], query, gain, eps, out_dtype), new_partial
+
     monkeypatch.setattr(ops, "_route_rows_forward", fwd)
+    monkeypatch.setattr(ops, "_route_rows_step", step)
     monkeypatch.setattr(ops, "_route_rows_backward", bwd)
     return calls
 
@@ -89,10 +94,14 @@ def test_accumulated_gradients_equal_plain_autograd(cpu_kernels, boundaries):
     for c in cpu_kernels:
         for b, kind in enumerate(c[:-1]):
             (writes if kind == "write" else adds)[b] += 1
-        assert c[-1] == "write"  # the partial's gradient is returned to autograd
     assert writes == [1] * n_blocks
     uses = [sum(1 for c in cpu_kernels if len(c) - 1 > b) for b in range(n_blocks)]
     assert adds == [u - 1 for u in uses]
+    # the routed partial's gradient: the final point's (first backward call) is
+    # its routing gradient alone; every other point adds the gradient of the
+    # partial the next point routes (or, at a commit, the block's summed gradient)
+    assert len(cpu_kernels) == 2 * len(model.layers) + 1
+    assert cpu_kernels[0][-1] == "write" and all(c[-1] == "add" for c in cpu_kernels[1:])
 
 
 def test_retained_graph_and_partial_backward_start_over(cpu_kernels):

@@ -1,4 +1,4 @@
-"""Gradient accumulation inside the routing backward (GPU).
+"""Gradient sums inside the routing backward, and the fused training step (GPU).
 
 ``attnres_route_bwd_add`` writes grad_sources[s] = dL/dsource_s + grad_addend[s]
 (fp32 sum, one rounding) for the sources given an addend, in place when the
@@ -11,9 +11,13 @@ sources with and without addends:
 * sources without an addend bit-identical to attnres_route_bwd (zeros compare
   equal to negative zeros), and the query / gain gradients bit-identical too;
 * in place (addend == gradient) bit-identical to a separate addend buffer.
-Then the training loop that uses it (forward_attn_res under autograd) against
-the same loop with the accumulation switched off (autograd sums the blocks'
-gradients), fp32 and bf16.
+``attnres_route_step`` (partial + delta into a new buffer, then routing over
+the committed blocks and it): the new partial exactly the rounded sum, the
+inputs untouched, the routed rows at the forward bars against the oracle and
+bit-identical to the arena's fused step on the same values.  Then the
+training loop that uses both (forward_attn_res under autograd) against the
+same loop with them switched off (route_list calls and torch adds; autograd
+sums the gradients), fp32 and bf16.
 """
 
 import copy
@@ -168,13 +172,13 @@ def test_training_loop_accumulating_equals_autograd_sums(gpu, dtype, monkeypatch
         return out
 
     calls = []
-    real = ops.route_accumulate
+    real = ops.route_point
 
     def counting(*a, **k):
         calls.append(1)
         return real(*a, **k)
 
-    monkeypatch.setattr(ops, "route_accumulate", counting)
+    monkeypatch.setattr(ops, "route_point", counting)
     m1 = copy.deepcopy(model)
     got = run(m1)
     assert len(calls) == 17  # every routing point took the accumulating path
@@ -188,3 +192,67 @@ def test_training_loop_accumulating_equals_autograd_sums(gpu, dtype, monkeypatch
         worst = max(worst, err / max(scale, 1e-30))
         assert err <= tol, f"{k}: err {err:.3e}, max|grad| {scale:.3e}"
     print(f"accumulating vs autograd sums ({dtype}): worst err {worst:.2e} of max|grad|", flush=True)
+
+
+# (committed blocks, rows, hidden, dtype, policy, kernel suffix)
+STEP_CASES = [
+    (0, 700, 3072, torch.bfloat16, _capi.POLICY_AUTO, "_s1_v2_q1"),
+    (2, 4096, 3072, torch.bfloat16, _capi.POLICY_STREAM, "_c6_fusedtable"),
+    (7, 4096, 3072, torch.bfloat16, _capi.POLICY_STREAM, "_c6_fusedtable"),
+    (8, 2048, 4096, torch.bfloat16, _capi.POLICY_STREAM, "_c8_fusedtable"),
+    (4, 500, 2048, torch.bfloat16, _capi.POLICY_WORKGROUP, "_s5_v1_q1"),
+    (3, 300, 1024, torch.float32, _capi.POLICY_AUTO, "_s4_v1_q1"),
+    (5, 300, 1024, torch.float32, _capi.POLICY_STREAM, "_c4_fusedtable"),
+]
+
+
+@pytest.mark.parametrize("nc,n,d,dt,policy,suffix", STEP_CASES, ids=[f"c{c[0]}-{c[5][1:]}" for c in STEP_CASES])
+def test_route_step_matches_oracle_and_arena_step(gpu, nc, n, d, dt, policy, suffix):
+    from .test_gpu_parity import check_bf16, check_f32
+
+    print(f"route_step committed={nc} n={n} d={d} {dt}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(200 + nc)
+    arena = torch.stack([torch.randn((n, d), generator=g, device=gpu) * (0.5 + 0.3 * s) for s in range(nc + 1)]).to(dt)
+    delta = torch.randn((n, d), generator=g, device=gpu).to(dt)
+    q = (torch.randn(d, generator=g, device=gpu) * 0.05).to(dt)
+    gain = (1 + 0.1 * torch.randn(d, generator=g, device=gpu)).to(dt)
+    committed = [arena[s].clone() for s in range(nc)]  # separate allocations (not equally spaced)
+    partial = arena[nc].clone()
+    before = [t.clone() for t in (*committed, partial, delta)]
+    prev = _capi.set_kernel_policy(policy)
+    try:
+        buf = ctypes.create_string_buffer(128)
+        _capi.check("attnres_route_kernel_name", _capi.lib().attnres_route_kernel_name(
+            nc + 1, n, d, code(dt), code(dt), code(dt), 1, 1, 0, buf, 128))
+        assert buf.value.decode().endswith(suffix), buf.value.decode()
+        out, new_partial = ops._route_rows_step(committed, partial, delta, q, gain, 1e-5, dt)
+        # the arena's fused step on the same values (updates its partial slot in place)
+        ref_arena = arena.clone()
+        out2, _, _ = ops.block_step(ref_arena, nc, False, delta, q, gain, 1e-5, False)
+        torch.cuda.synchronize()
+    finally:
+        _capi.set_kernel_policy(prev)
+    for a, b in zip(before, (*committed, partial, delta)):
+        assert torch.equal(a, b), "an input was modified"
+    assert torch.equal(new_partial, (partial.float() + delta.float()).to(dt)), "partial + delta not rounded once"
+    assert torch.equal(new_partial, ref_arena[nc]) and torch.equal(out, out2.reshape(out.shape))
+    pd = "bf16" if dt == torch.bfloat16 else "f32"
+    x = np.stack([np64(t) for t in (*committed, new_partial)])
+    ref = O.route(x, O.fold_query(np64(q), np64(gain), pd), 1e-5)["out"][0]
+    if dt == torch.bfloat16:
+        check_bf16(out, ref, "route_step")
+    else:
+        check_f32(out, ref, "route_step")
+
+
+def test_route_step_rejects_overlapping_output(gpu):
+    n, d = 64, 512
+    t = torch.randn((3, n, d), device=gpu).to(torch.bfloat16)
+    q = torch.zeros(d, device=gpu, dtype=torch.bfloat16)
+    out = torch.empty((n, d), device=gpu, dtype=torch.bfloat16)
+    lib = _capi.lib()
+    args = (_capi.pointer_array([t[0].data_ptr()]), 1, t[1].data_ptr(), t[2].data_ptr())
+    tail = (n, d, _capi.DTYPE_BF16, q.data_ptr(), None, _capi.DTYPE_BF16, 1e-5, out.data_ptr(), None, None, None)
+    assert lib.attnres_route_step(*args, t[1].data_ptr(), *tail) == _capi.ERR_ARG  # over the partial
+    assert lib.attnres_route_step(*args, t[0].data_ptr(), *tail) == _capi.ERR_ARG  # over a committed block
+    assert lib.attnres_route_step(*args, None, *tail) == _capi.ERR_ARG
