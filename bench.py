@@ -17,6 +17,9 @@ Also on the JSON line:
 * ``cfg5`` — the 3B data-driven blocks (57 calls, S=1..7, B=2), the same way.
 * ``cfg2_bwd`` — the backward of cfg2's 57 routing calls (the training path):
   (2S+1) rows per call, with a ``roofline`` block for the S=8 backward.
+* ``cfg4`` (the 8B decode step), ``cfg2arena`` (the stack-free prefill) and
+  ``cfg2train`` (the 3B training step, at most 5 steps) — as their own
+  ``--workload`` runs report them.
 * ``cpu_baseline`` — the reference's CPU routing path (oracle/torch_cpu_path:
   the einsum-branch op sequence over the padded buffer, fp32) timed on this
   host on a bounded sample (the whole call schedule over 4096 token rows, at
@@ -775,6 +778,52 @@ def secondary_backward(name: str, steps: int, warmup: int, dev) -> dict:
             "roofline": roof}
 
 
+def secondary_decode(steps: int, warmup: int, dev) -> dict:
+    """cfg4 (the 8B decode step: 65 fused block steps in one HIP graph), measured in the same run."""
+    from kotodama_amd import workloads
+
+    w = workloads.get("cfg4")
+    elapsed, step_bytes, graph_ms = bench_decode(w, steps, warmup, dev)
+    ms = elapsed * 1e3 / steps
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    ach = step_bytes / (graph_ms * 1e-3) / 1e9
+    return {"workload": WORKLOAD_TEXT["cfg4"], "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+            "value": round(gbs, 2), "unit": "GB/s", "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(w.batch / (ms * 1e-3), 1), "algorithmic_bytes_per_step": step_bytes,
+            "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "one decode step (65 fused attnres_route_bf_d2_s*_v1_q1 launches, HIP graph)",
+                         "avg_ms": round(graph_ms, 4)}}
+
+
+def secondary_arena(steps: int, warmup: int, dev) -> dict:
+    """cfg2arena (the stack-free prefill: 57 fused block steps over one arena), measured in the same run."""
+    from kotodama_amd import workloads
+
+    w = workloads.get("cfg2")
+    elapsed, step_bytes, top, dom_ms, dom_bytes = bench_arena(w, steps, warmup, dev)
+    ms = elapsed * 1e3 / steps
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    ach = dom_bytes / (dom_ms * 1e-3) / 1e9
+    return {"workload": WORKLOAD_TEXT["cfg2arena"], "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+            "value": round(gbs, 2), "unit": "GB/s", "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(w.tokens / (ms * 1e-3), 1), "algorithmic_bytes_per_step": step_bytes,
+            "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": kernel_name(top, w.tokens, w.hidden, w.dtype, mode=1) + f" (S={top} points)",
+                         "algorithmic_bytes": dom_bytes, "avg_ms": round(dom_ms, 4)}}
+
+
+def secondary_train(steps: int, warmup: int, dev) -> dict:
+    """cfg2train (the 3B training step on the routing path, stack-free drop-in, eager), measured in the same run."""
+    rec = bench_train(steps, warmup, dev, "list", False)
+    rb = rec["routing_kernel_bytes"]
+    gbs = (rb["fwd"] + rb["bwd"]) / (rec["ms_per_step"] * 1e-3) / 1e9
+    return {"workload": WORKLOAD_TEXT["cfg2train"], "variant": "list (forward_attn_res under autograd)",
+            "steps": steps, "warmup": warmup, "value": rec["tokens_per_s"], "unit": "tokens/s",
+            "routing_GB/s_over_step": round(gbs, 2), **rec}
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -997,6 +1046,9 @@ def main() -> int:
         line["cfg3"] = secondary_sweep("cfg3", args.steps, args.warmup, dev)
         line["cfg5"] = secondary_sweep("cfg5", args.steps, args.warmup, dev)
         line["cfg2_bwd"] = secondary_backward("cfg2", args.steps, args.warmup, dev)
+        line["cfg4"] = secondary_decode(args.steps, args.warmup, dev)
+        line["cfg2arena"] = secondary_arena(args.steps, args.warmup, dev)
+        line["cfg2train"] = secondary_train(min(args.steps, 5), min(args.warmup, 2), dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, min(args.cpu_tokens, w.tokens)) if args.workload != "cfg4" else \
             cpu_baseline(w, w.tokens)
