@@ -213,3 +213,49 @@ def test_kernel_name_argument_errors():
     # no rows: attnres_merge_fwd launches nothing, and the name is empty (no device needed)
     assert lib.attnres_merge_kernel_name(0, 512, 1, 1, 1, buf, 8) == _capi.OK and buf.value == b""
     assert lib.attnres_merge_kernel_name(16, 500, 1, 1, 1, buf, 8) == _capi.ERR_UNSUPPORTED  # not 16-byte chunks
+
+
+def test_route_step_argument_errors():
+    lib = _capi.lib()
+    N, D = 16, 64
+    blk = N * D * 2  # bytes of one bf16 row block
+    com = _capi.pointer_array([FAKE, FAKE + blk])
+
+    def step(committed=com, nc=2, partial=FAKE + 2 * blk, delta=FAKE + 3 * blk, pout=FAKE + 4 * blk, n=N, d=D,
+             dt=_capi.DTYPE_BF16, query=FAKE, out=FAKE + 5 * blk):
+        return lib.attnres_route_step(committed, nc, partial, delta, pout, n, d, dt, query, None, _capi.DTYPE_BF16,
+                                      1e-5, out, None, None, None)
+
+    assert step(n=0) == _capi.OK  # nothing to do: returns before any HIP call
+    assert step(partial=None) == _capi.ERR_ARG
+    assert step(delta=None) == _capi.ERR_ARG
+    assert step(pout=None) == _capi.ERR_ARG
+    assert step(nc=-1) == _capi.ERR_ARG
+    assert step(committed=None) == _capi.ERR_ARG
+    assert step(nc=16) == _capi.ERR_UNSUPPORTED  # 17 sources
+    assert step(dt=7) == _capi.ERR_ARG
+    # the new partial may not overlap an input: it would be read while written
+    assert step(pout=FAKE + 2 * blk) == _capi.ERR_ARG
+    assert step(pout=FAKE + 3 * blk + 64) == _capi.ERR_ARG
+    assert step(pout=FAKE + blk // 2) == _capi.ERR_ARG
+    assert step(pout=FAKE + 4 * blk + 8) == _capi.ERR_ALIGN  # route_launch's alignment check of partial_out
+    assert step(query=None) == _capi.ERR_ARG
+
+
+def test_route_bwd_add_argument_errors():
+    lib = _capi.lib()
+    N, D, S = 16, 64, 2
+    srcs = _capi.pointer_array([FAKE, FAKE + 4096])
+    grads = _capi.pointer_array([FAKE + 8192, FAKE + 12288])
+
+    def call(adds, gdt=_capi.DTYPE_BF16, n=N):
+        return lib.attnres_route_bwd_add(srcs, S, n, D, D, _capi.DTYPE_BF16, FAKE, None, _capi.DTYPE_BF16, 1e-5,
+                                         FAKE, gdt, D, None, grads, adds, D, FAKE, 1 << 20, None, None, None)
+
+    assert call(_capi.pointer_array([FAKE + 8192, None]), n=0) == _capi.OK
+    assert call(_capi.pointer_array([FAKE + 8200, None]), n=0) == _capi.ERR_ALIGN
+    # an addend needs grad_out in the source dtype (bf16 sources, fp32 dL/dout: no kernel)
+    assert call(_capi.pointer_array([FAKE + 8192, None]), gdt=_capi.DTYPE_F32, n=0) == _capi.ERR_UNSUPPORTED
+    # without any addend the call is attnres_route_bwd
+    assert call(_capi.pointer_array([None, None]), gdt=_capi.DTYPE_F32, n=0) == _capi.OK
+    assert call(None, gdt=_capi.DTYPE_F32, n=0) == _capi.OK
