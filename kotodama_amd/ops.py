@@ -663,6 +663,7 @@ class _Commit(torch.autograd.Function):
         return block.view_as(block)
 
     @staticmethod
+    @torch.autograd.function.once_differentiable
     def backward(ctx, grad):
         acc = ctx.slot.take()
         if acc is None:
@@ -751,6 +752,7 @@ class _RoutePoint(torch.autograd.Function):
         return out, new_partial
 
     @staticmethod
+    @torch.autograd.function.once_differentiable
     def backward(ctx, g_out, g_partial):
         n_com = len(ctx.slots)
         need = ctx.needs_input_grad
