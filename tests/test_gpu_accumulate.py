@@ -148,8 +148,14 @@ def test_route_bwd_add_rejects_mixed_dtypes(gpu):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-def test_training_loop_accumulating_equals_autograd_sums(gpu, dtype, monkeypatch):
+# (dtype, width, kernel policy): the row-per-workgroup kernels, and under POLICY_STREAM
+# the row-per-wave ones (the `_fusedtable` forward and `_stream_c6_*_add` backward)
+LOOP_CASES = [(torch.float32, 1024, _capi.POLICY_AUTO), (torch.bfloat16, 1024, _capi.POLICY_AUTO),
+              (torch.bfloat16, 3072, _capi.POLICY_STREAM)]
+
+
+@pytest.mark.parametrize("dtype,d,policy", LOOP_CASES, ids=["f32", "bf16", "bf16-row-per-wave"])
+def test_training_loop_accumulating_equals_autograd_sums(gpu, dtype, d, policy, monkeypatch):
     # forward_attn_res under autograd: the blocks' gradients summed in the
     # backward kernels, against the same loop with that switched off (route_list
     # calls; autograd adds each use's gradient): every gradient.  fp32: to 1e-5
@@ -158,15 +164,19 @@ def test_training_loop_accumulating_equals_autograd_sums(gpu, dtype, monkeypatch
     # kernel rounds each partial sum once, over up to 16 uses of a block, and
     # the differences travel upstream through the bf16 sublayers: within 4 bf16
     # ulps (2^-5) of each tensor's largest magnitude
-    model = TinyModel(d=1024, num_layers=8, boundaries=(0, 2, 4, 6), seed=61, elementwise=True).to(gpu).to(dtype)
+    model = TinyModel(d=d, num_layers=8, boundaries=(0, 2, 4, 6), seed=61, elementwise=True).to(gpu).to(dtype)
     g = torch.Generator(device=gpu).manual_seed(62)
-    embed = torch.randn((2, 64, 1024), generator=g, device=gpu).to(dtype)
-    G = torch.randn((2, 64, 1024), generator=g, device=gpu).to(dtype)
+    embed = torch.randn((2, 64, d), generator=g, device=gpu).to(dtype)
+    G = torch.randn((2, 64, d), generator=g, device=gpu).to(dtype)
 
     def run(m):
         e = embed.clone().requires_grad_(True)
-        (kotodama_amd.forward_attn_res(m, e).float() * G.float()).sum().backward()
-        torch.cuda.synchronize()
+        prev = _capi.set_kernel_policy(policy)
+        try:
+            (kotodama_amd.forward_attn_res(m, e).float() * G.float()).sum().backward()
+            torch.cuda.synchronize()
+        finally:
+            _capi.set_kernel_policy(prev)
         out = {n: p.grad.float() for n, p in m.named_parameters()}
         out["embed"] = e.grad.float()
         return out

@@ -506,3 +506,115 @@ def test_random_row_strides_through_the_c_abi(gpu, seed):
     check_grad(dbig[:, :, :D], b["dx"], sdt, f"seed {seed} dsources")
     assert torch.all(dbig[:, :, D:] == CANARY), f"seed {seed}: gradient row padding written"
     check_grad(dq, b["dqw"], qdt, f"seed {seed} dquery")
+
+
+def _check_grad_sum(got, ref, dtype, label):
+    """A gradient summed over two routing calls inside the backward kernels: bf16 takes one
+    rounding per call (the first call's gradient is rounded, the second is added to it in fp32
+    and rounded again), so the bar is the backward bar of check_grad, one ulp of |ref| plus
+    1e-3 max|ref|, with >= 50% of the elements equal to the correctly rounded sum; fp32 as
+    check_grad."""
+    if dtype == torch.float32:
+        check_grad(got, ref, dtype, label)
+        return
+    g = np64(got)
+    err = np.abs(g - ref)
+    e = np.floor(np.log2(np.maximum(np.abs(ref), 2.0**-126)))
+    tol = 2.0 ** (e - 7) + 1e-3 * np.abs(ref).max()
+    assert (err <= tol).all(), f"{label}: worst err {err.max():.3e}"
+    counted = np.abs(ref) >= 1e-30
+    if counted.any():
+        assert np.mean(g[counted] == O.bf16_round(ref[counted])) >= 0.5, f"{label}: too few correctly rounded"
+
+
+@pytest.mark.parametrize("seed", range(SEEDS or 8))
+def test_random_training_points(gpu, seed):
+    # two routing points of the training loop (ops.route_point: the fused partial
+    # update and the in-kernel gradient sums) over the same committed blocks, the
+    # second routing the first's partial as it is, with random block count,
+    # width, rows, dtype, gains, peakedness, with or without a pending sublayer
+    # output and kernel policy:
+    #   X = partial (+ delta);  h1 = route(C + [X], q1);  h2 = route(C + [X], q2)
+    #   loss = <h1, G1> + <h2, G2> + <X, Gp>
+    # routed rows against the oracle; dC_k = dx1_k + dx2_k (summed in the GradSlot),
+    # dX = dx1_X + dx2_X + Gp (the second call's gradient of the partial output
+    # is the first's addend), returned for both partial and delta; query and gain
+    # gradients of each call
+    rng = np.random.default_rng(11000 + seed)
+    dtype = [torch.bfloat16, torch.float32][int(rng.integers(2))]
+    K = int(rng.integers(0, 9))
+    vec = 8 if dtype == torch.bfloat16 else 4
+    D = vec * int(rng.integers(8, (4096 if dtype == torch.bfloat16 else 2048) // vec + 1))
+    if rng.integers(2):  # half the cases on widths the row-per-wave kernels take
+        D = (512 if dtype == torch.bfloat16 else 256) * int(rng.integers(1, 9))
+    N = _rows(rng, (K + 3) * D)
+    with_delta = bool(rng.integers(2))
+    with_gain = bool(rng.integers(2))
+    qscale = 0.05 if dtype == torch.float32 else [0.05, 0.5][int(rng.integers(2))]
+    pol = _policy(rng)
+    print(f"random training points seed={seed}: {dtype} K={K} D={D} N={N} delta={with_delta} gain={with_gain} "
+          f"qscale={qscale} policy={pol}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(12000 + seed)
+
+    def t(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(dtype).to(gpu)
+
+    blocks = [t(N, D, scale=float(np.exp(rng.uniform(np.log(0.25), np.log(4.0))))).requires_grad_(True)
+              for _ in range(K)]
+    partial = t(N, D).requires_grad_(True)
+    delta = t(N, D, scale=0.5).requires_grad_(True) if with_delta else None
+    q = [t(D, scale=qscale).requires_grad_(True) for _ in range(2)]
+    gn = [(1 + 0.1 * torch.randn(D, generator=g)).to(dtype).to(gpu).requires_grad_(True) if with_gain else None
+          for _ in range(2)]
+    G1, G2, Gp = (torch.randn(N, D, generator=g).to(dtype).to(gpu) for _ in range(3))
+
+    def run():
+        slots = [ops.GradSlot() for _ in range(K)]
+        committed = [ops.commit_block(b, s) for b, s in zip(blocks, slots)]
+        h1, X = ops.route_point(committed, slots, partial, delta, q[0], gn[0], 1e-5, dtype)
+        h2, X2 = ops.route_point(committed, slots, X, None, q[1], gn[1], 1e-5, dtype)
+        loss = (h1.float() * G1.float()).sum() + (h2.float() * G2.float()).sum() + (X2.float() * Gp.float()).sum()
+        loss.backward()
+        torch.cuda.synchronize()
+        return h1, h2, X
+
+    h1, h2, X = _with_policy(pol, run)
+    pd = "bf16" if dtype == torch.bfloat16 else "f32"
+    Xref = np64(partial) + np64(delta) if with_delta else np64(partial)
+    Xref = O.bf16_round(Xref).astype(np.float64) if dtype == torch.bfloat16 else Xref.astype(np.float32).astype(np.float64)
+    assert np.array_equal(np64(X), Xref), f"seed {seed}: partial + delta not rounded once"
+    srcs = np.stack([np64(b) for b in blocks] + [Xref])
+    res, f32 = [], []
+    for j, (h, G) in enumerate(((h1, G1), (h2, G2))):
+        qw = O.fold_query(np64(q[j]), np64(gn[j]) if with_gain else None, pd)
+        ref = O.route(srcs, qw, 1e-5)["out"][0]
+        if dtype == torch.bfloat16:
+            check_bf16(h, ref, f"seed {seed} h{j + 1}")
+        else:
+            sens, lmax = route_sensitivity(srcs, qw, ref, O.route(srcs, qw, 1e-5))
+            check_f32_logits(h, ref, sens, lmax, f"seed {seed} h{j + 1}")
+        res.append(O.route_backward(srcs, qw, 1e-5, np64(G), None))
+        gq = res[-1]["dqw"] * (np64(gn[j]) if with_gain else 1.0)
+        if dtype == torch.float32:
+            # fp32: against the reference op sequence differentiated in fp32, as the route family does
+            gains = np64(gn[j]) if with_gain else np.ones(D)
+            f32.append(_route_f32_grads(srcs, np64(q[j]), gains, 1e-5, np64(G)))
+            check_grad_f32(q[j].grad, gq, f32[-1][1], f"seed {seed} dquery{j + 1}")
+            if with_gain:
+                check_grad_f32(gn[j].grad, res[-1]["dqw"] * np64(q[j]), f32[-1][2], f"seed {seed} dgain{j + 1}")
+        else:
+            check_grad(q[j].grad, gq, dtype, f"seed {seed} dquery{j + 1}")
+            if with_gain:
+                check_grad(gn[j].grad, res[-1]["dqw"] * np64(q[j]), dtype, f"seed {seed} dgain{j + 1}")
+    dX = res[0]["dx"][K] + res[1]["dx"][K] + np64(Gp)
+    if dtype == torch.float32:
+        for k in range(K):
+            check_grad_f32(blocks[k].grad, res[0]["dx"][k] + res[1]["dx"][k], f32[0][0][k] + f32[1][0][k],
+                           f"seed {seed} dblock{k}")
+        check_grad_f32(partial.grad, dX, f32[0][0][K] + f32[1][0][K] + np64(Gp), f"seed {seed} dpartial")
+    else:
+        for k in range(K):
+            _check_grad_sum(blocks[k].grad, res[0]["dx"][k] + res[1]["dx"][k], dtype, f"seed {seed} dblock{k}")
+        _check_grad_sum(partial.grad, dX, dtype, f"seed {seed} dpartial")
+    if with_delta:
+        assert torch.equal(delta.grad, partial.grad), f"seed {seed}: d(partial + delta) differs between its inputs"
