@@ -90,6 +90,8 @@ def parse_args():
     ap.add_argument("--compile", action="store_true",
                     help="cfg2train: run the forward under torch.compile(fullgraph=True, backend='inductor')")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", action="store_true",
+                    help="cfg2: measure the sweep alone, without the other workloads' records (for profiling)")
     ap.add_argument("--cpu-tokens", type=int, default=4096, help="tokens per CPU-baseline sample call")
     return ap.parse_args()
 
@@ -1042,7 +1044,7 @@ def main() -> int:
         "tokens_per_s": round(tokens / (ms_per_step * 1e-3), 1),
         "roofline": roofline,
     }
-    if args.workload == "cfg2":
+    if args.workload == "cfg2" and not args.only:
         line["cfg3"] = secondary_sweep("cfg3", args.steps, args.warmup, dev)
         line["cfg5"] = secondary_sweep("cfg5", args.steps, args.warmup, dev)
         line["cfg2_bwd"] = secondary_backward("cfg2", args.steps, args.warmup, dev)
