@@ -263,6 +263,53 @@ int attnres_route_bwd_add(const void* const* sources, int num_sources, int64_t n
                           int64_t grad_ld, void* workspace, int64_t workspace_bytes, void* grad_query,
                           void* grad_gain, void* stream);
 
+/*
+ * attnres_route_bwd_add for a routing point whose committed sources'
+ * gradients are summed later, over every call that read them
+ * (attnres_route_bwd_gather), instead of being read, added to and written
+ * back at each call.  Only the gradient of the last source (the partial
+ * block) is written: grad_partial = dL/dsource_{S-1} + grad_partial_addend
+ * (NULL for none; may be grad_partial).  For sources s = 0 .. S-2 the call
+ * stores, per token t, coef[(t*(S-1) + s)*4 + 0..3] = (w_s, c1_s, c2_s, 0)
+ * (fp32; coef holds num_tokens*(S-1)*4 floats) and writes the folded query
+ * query * gain (bf16, hidden values) to qfold, so that
+ *   dL/dsource_s = w_s grad_out + c1_s qfold + c2_s source_s.
+ * grad_query / grad_gain and the workspace as attnres_route_bwd.  Kernels
+ * exist for bf16 sources, grad_out and parameters with hidden 3072 (2..8
+ * sources) or 4096 (2..9 sources); other calls return
+ * ATTNRES_ERR_UNSUPPORTED and write nothing.
+ *
+ * Replaces, with attnres_route_bwd_gather, autograd's summation of a
+ * committed block's gradient over the routing points that read it
+ * (src/model/llama.py:690-715; each use's gradient is a separate tensor that
+ * torch adds): the sum is formed once per block from each point's output
+ * gradient and these coefficients.
+ */
+int attnres_route_bwd_defer(const void* const* sources, int num_sources, int64_t num_tokens, int hidden,
+                            int64_t src_ld, int src_dtype, const void* query, const void* gain, int param_dtype,
+                            float eps, const void* grad_out, int grad_out_dtype, int64_t grad_out_ld,
+                            const float* grad_lse, void* grad_partial, const void* grad_partial_addend,
+                            int64_t grad_ld, float* coef, void* qfold, void* workspace, int64_t workspace_bytes,
+                            void* grad_query, void* grad_gain, void* stream);
+
+/*
+ * A source's gradient summed over the num_terms calls of
+ * attnres_route_bwd_defer that read it, for every token t:
+ *   out = addend + sum_j (w_j grad_outs[j] + c1_j qfolds[j]) + (sum_j c2_j) x
+ * with (w_j, c1_j, c2_j) = coefs[j][t*coef_lds[j] + 0..2]: for a call over
+ * S_j sources that read x as source s_j, coefs[j] = its coef + 4*s_j and
+ * coef_lds[j] = 4*(S_j - 1).  bf16 rows of hidden 3072 or 4096 (x rows x_ld
+ * apart, grad_outs[j] rows grad_out_ld, out and addend rows out_ld); addend
+ * may be NULL or out (in place).  fp32 sums rounded once per group of up to
+ * 48 terms (more terms: later groups add to out).
+ *
+ * See attnres_route_bwd_defer for the reference code this replaces.
+ */
+int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int64_t x_ld, int dtype, int num_terms,
+                             const void* const* grad_outs, int64_t grad_out_ld, const float* const* coefs,
+                             const int64_t* coef_lds, const void* const* qfolds, const void* addend, void* out,
+                             int64_t out_ld, void* stream);
+
 /* Size of the device scratch array attnres_route_bwd_noalloc uses (32 MiB:
  * 256 CUs x 4 workgroups x 8192 fp32 columns, the largest workspace
  * attnres_route_bwd_workspace_size() reports on an MI355X). */

@@ -55,6 +55,8 @@ EXPORTS = (
     "attnres_route_bwd_workspace_size",
     "attnres_route_bwd",
     "attnres_route_bwd_add",
+    "attnres_route_bwd_defer",
+    "attnres_route_bwd_gather",
     "attnres_route_bwd_noalloc",
     "attnres_route_bwd_kernel_name",
     "attnres_route_bwd_queries_workspace_size",
@@ -219,6 +221,55 @@ _SIGNATURES = {
         ],
         _c_int,
     ),
+    "attnres_route_bwd_defer": (
+        [
+            ctypes.POINTER(_c_vp),  # sources
+            _c_int,  # num_sources
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_i64,  # src_ld
+            _c_int,  # src_dtype
+            _c_vp,  # query
+            _c_vp,  # gain
+            _c_int,  # param_dtype
+            _c_float,  # eps
+            _c_vp,  # grad_out
+            _c_int,  # grad_out_dtype
+            _c_i64,  # grad_out_ld
+            _c_vp,  # grad_lse
+            _c_vp,  # grad_partial
+            _c_vp,  # grad_partial_addend
+            _c_i64,  # grad_ld
+            _c_vp,  # coef
+            _c_vp,  # qfold
+            _c_vp,  # workspace
+            _c_i64,  # workspace_bytes
+            _c_vp,  # grad_query
+            _c_vp,  # grad_gain
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
+    "attnres_route_bwd_gather": (
+        [
+            _c_vp,  # x
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_i64,  # x_ld
+            _c_int,  # dtype
+            _c_int,  # num_terms
+            ctypes.POINTER(_c_vp),  # grad_outs
+            _c_i64,  # grad_out_ld
+            ctypes.POINTER(_c_vp),  # coefs
+            ctypes.POINTER(_c_i64),  # coef_lds
+            ctypes.POINTER(_c_vp),  # qfolds
+            _c_vp,  # addend
+            _c_vp,  # out
+            _c_i64,  # out_ld
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
     "attnres_route_bwd_noalloc": (
         [
             ctypes.POINTER(_c_vp),  # sources
@@ -356,6 +407,13 @@ def pointer_array(ptrs: list[int]):
     return arr
 
 
+def int64_array(vals: list[int]):
+    arr = (_c_i64 * max(1, len(vals)))()
+    for i, v in enumerate(vals):
+        arr[i] = v
+    return arr
+
+
 def route_fwd(*args) -> None:
     check("attnres_route_fwd", lib().attnres_route_fwd(*args))
 
@@ -387,6 +445,19 @@ def route_step(*args) -> None:
 def route_bwd_add(*args) -> None:
     """attnres_route_bwd with addend rows (grad_sources[s] += grad_addend[s] where non-NULL)."""
     check("attnres_route_bwd_add", lib().attnres_route_bwd_add(*args))
+
+
+def route_bwd_defer(*args) -> int:
+    """attnres_route_bwd_defer; returns its code (ERR_UNSUPPORTED: no deferred kernel for the call, nothing written)."""
+    code = lib().attnres_route_bwd_defer(*args)
+    if code not in (OK, ERR_UNSUPPORTED):
+        check("attnres_route_bwd_defer", code)
+    return code
+
+
+def route_bwd_gather(*args) -> None:
+    """attnres_route_bwd_gather: one source's gradient summed from the deferred terms of the calls that read it."""
+    check("attnres_route_bwd_gather", lib().attnres_route_bwd_gather(*args))
 
 
 def route_bwd_noalloc(*args) -> None:

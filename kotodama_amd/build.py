@@ -3,7 +3,7 @@
 Steps (all outputs under ``kotodama_amd/lib/``):
 
 1. ``hipcc --genco --offload-arch=gfx950`` compiles ``csrc/attnres_kernels.hip``
-   once per code-object part (``-DATTNRES_PART=0..7``, in parallel).
+   once per code-object part (``-DATTNRES_PART=0..10``, in parallel).
 2. ``gcc`` assembles ``csrc/attnres_blob.S``, which ``.incbin``s the parts.
 3. ``hipcc -c -fPIC`` compiles ``csrc/attnres_noalloc.hip`` (the no-alloc
    entry point; its device array needs HIP device code of its own).
@@ -30,7 +30,7 @@ INCLUDE = PKG.parent / "include"
 LIB_NAME = "libattnres_hip.so"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
-NUM_PARTS = 10
+NUM_PARTS = 11
 
 # Packed-fp32 VALU ops are disabled for every HIP compile (the kernels are
 # written with scalar fp32 arithmetic).

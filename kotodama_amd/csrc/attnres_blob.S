@@ -1,4 +1,4 @@
-/* The ten gfx950 code-object parts, linked into libattnres_hip.so as bytes
+/* The eleven gfx950 code-object parts, linked into libattnres_hip.so as bytes
  * and loaded with hipModuleLoadData.  The build passes -I<dir of the .hsaco>. */
     .section .rodata
     .balign 4096
@@ -41,4 +41,8 @@ attnres_hsaco_part8:
     .global attnres_hsaco_part9
 attnres_hsaco_part9:
     .incbin "attnres_gfx950_part9.hsaco"
+    .balign 4096
+    .global attnres_hsaco_part10
+attnres_hsaco_part10:
+    .incbin "attnres_gfx950_part10.hsaco"
     .section .note.GNU-stack,"",@progbits

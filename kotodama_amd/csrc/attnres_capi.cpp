@@ -33,10 +33,11 @@ extern "C" const unsigned char attnres_hsaco_part6[];
 extern "C" const unsigned char attnres_hsaco_part7[];
 extern "C" const unsigned char attnres_hsaco_part8[];
 extern "C" const unsigned char attnres_hsaco_part9[];
+extern "C" const unsigned char attnres_hsaco_part10[];
 
 namespace {
 
-constexpr int kParts = 10;
+constexpr int kParts = 11;
 constexpr int kMaxDevices = 64;
 constexpr int kMaxThreads = 512;  // __launch_bounds__ of every kernel
 
@@ -112,6 +113,8 @@ struct DeviceState {
   KernelSlot bwd_mq[kBwdFuncs];  // batched-query backward: (source, grad_out) dtypes x S x V
   KernelSlot bwd_dqw[4];         // source dtype x V
   KernelSlot bwd_mqg[2 * 9];     // batched-query backward on the matrix cores: query groups x S
+  KernelSlot bwd_defer[2 * 10];  // row-per-wave backward with deferred block gradients: row KiB x S
+  KernelSlot gather[2];          // their per-block sums: rows of 6 / 8 KiB
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -191,7 +194,7 @@ int ensure_loaded(DeviceState** out) {
       const unsigned char* blobs[kParts] = {attnres_hsaco_part0, attnres_hsaco_part1, attnres_hsaco_part2,
                                             attnres_hsaco_part3, attnres_hsaco_part4, attnres_hsaco_part5,
                                             attnres_hsaco_part6, attnres_hsaco_part7, attnres_hsaco_part8,
-                                            attnres_hsaco_part9};
+                                            attnres_hsaco_part9, attnres_hsaco_part10};
       // On a failure nothing stays half-loaded: the next call starts over.
       auto unload = [&st](int n) {
         for (int j = 0; j < n; ++j) {
@@ -406,6 +409,34 @@ int get_bwd_stream(DeviceState& st, int nch, int s, hipFunction_t* f, bool add =
   snprintf(name, sizeof(name), "attnres_route_bwd_stream_c%d_s%d%s", nch, s, add ? "_add" : "");
   const int idx = (nch == 8 ? 10 : 0) + s;
   return slot_function(st, add ? st.bwd_stream_add[idx] : st.bwd_stream[idx], add ? kBwdStreamAddPart : 4, name, f);
+}
+
+// Deferred block gradients (code-object part 10): the row-per-wave backward
+// forming only the partial's gradient (attnres_route_bwd_stream_c<NCH>_s<S>_defer,
+// S >= 2) and the per-block sum (attnres_route_bwd_gather_c<NCH>).
+constexpr int kDeferPart = 10;
+int get_bwd_defer(DeviceState& st, int nch, int s, hipFunction_t* f) {
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_route_bwd_stream_c%d_s%d_defer", nch, s);
+  return slot_function(st, st.bwd_defer[(nch == 8 ? 10 : 0) + s], kDeferPart, name, f);
+}
+int get_gather(DeviceState& st, int nch, hipFunction_t* f) {
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_route_bwd_gather_c%d", nch);
+  return slot_function(st, st.gather[nch == 8 ? 1 : 0], kDeferPart, name, f);
+}
+// Row KiB of the deferred backward for this call, or 0 when it has no kernel
+// (bf16 sources, output gradients and parameters; rows of 6 KiB with S <= 8
+// or 8 KiB with S <= 9; at least one committed source).
+int bwd_defer_nch(int src_dtype, int grad_out_dtype, int param_dtype, int num_sources, int hidden,
+                  int64_t num_tokens) {
+  if (src_dtype != ATTNRES_DTYPE_BF16 || grad_out_dtype != ATTNRES_DTYPE_BF16 || param_dtype != ATTNRES_DTYPE_BF16)
+    return 0;
+  if (hidden != 3072 && hidden != 4096) return 0;
+  const int nch = hidden / 512;
+  if (num_sources < 2 || num_sources > (nch == 6 ? 8 : 9)) return 0;
+  if (num_tokens >= (int64_t)1 << 31) return 0;
+  return nch;
 }
 
 // Batched-query backward kernels (code-object part 6).  Source-gradient
@@ -1121,7 +1152,8 @@ static int route_bwd_finish(hipFunction_t f, int grid, int block, size_t lds, De
                      const void* query, const void* gain, int param_dtype, float eps, const void* grad_out,
                      int grad_out_dtype, int64_t grad_out_ld, const float* grad_lse, void* const* grad_sources,
                      int64_t grad_ld, void* workspace, int64_t workspace_bytes, void* grad_query, void* grad_gain,
-                     void* stream, const void* const* grad_addend) {
+                     void* stream, const void* const* grad_addend, float* coef = nullptr,
+                     void* qfold = nullptr) {
   int rc = ATTNRES_OK;
   const int64_t need = (int64_t)grid * (int64_t)hidden * (int64_t)sizeof(float);
   if (workspace == nullptr || workspace_bytes < need)
@@ -1148,6 +1180,8 @@ static int route_bwd_finish(hipFunction_t f, int grid, int block, size_t lds, De
   P.grad_out = grad_out;
   P.grad_lse = grad_lse;
   P.dqw_part = static_cast<float*>(workspace);
+  P.coef = coef;
+  P.qfold = qfold;
   P.n_tokens = num_tokens;
   P.src_ld = src_ld;
   P.dsrc_ld = grad_ld;
@@ -1279,6 +1313,134 @@ int attnres_route_bwd_add(const void* const* sources, int num_sources, int64_t n
   return route_bwd_impl(sources, num_sources, num_tokens, hidden, src_ld, src_dtype, query, gain, param_dtype, eps,
                         grad_out, grad_out_dtype, grad_out_ld, grad_lse, grad_sources, grad_ld, workspace,
                         workspace_bytes, grad_query, grad_gain, stream, grad_addend);
+}
+
+int attnres_route_bwd_defer(const void* const* sources, int num_sources, int64_t num_tokens, int hidden,
+                            int64_t src_ld, int src_dtype, const void* query, const void* gain, int param_dtype,
+                            float eps, const void* grad_out, int grad_out_dtype, int64_t grad_out_ld,
+                            const float* grad_lse, void* grad_partial, const void* grad_partial_addend,
+                            int64_t grad_ld, float* coef, void* qfold, void* workspace, int64_t workspace_bytes,
+                            void* grad_query, void* grad_gain, void* stream) {
+  if (num_sources < 1 || num_sources > ATTNRES_MAX_SOURCES)
+    return fail(ATTNRES_ERR_ARG, "deferred backward: num_sources=%d outside [1, %d]", num_sources,
+                ATTNRES_MAX_SOURCES);
+  if (sources == nullptr || grad_partial == nullptr || coef == nullptr || qfold == nullptr)
+    return fail(ATTNRES_ERR_ARG, "sources, grad_partial, coef or qfold is NULL");
+  if (num_tokens < 0) return fail(ATTNRES_ERR_ARG, "num_tokens=%lld < 0", (long long)num_tokens);
+  if (hidden <= 0) return fail(ATTNRES_ERR_ARG, "hidden=%d <= 0", hidden);
+  if (!valid_dtype(src_dtype) || !valid_dtype(param_dtype) || !valid_dtype(grad_out_dtype))
+    return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (query == nullptr || grad_out == nullptr) return fail(ATTNRES_ERR_ARG, "query/grad_out is NULL");
+  if (gain == nullptr && grad_gain != nullptr) return fail(ATTNRES_ERR_ARG, "grad_gain given without gain");
+  if (!std::isfinite(eps)) return fail(ATTNRES_ERR_ARG, "eps is not finite");
+  const int nch = bwd_defer_nch(src_dtype, grad_out_dtype, param_dtype, num_sources, hidden, num_tokens);
+  if (nch == 0)
+    return fail(ATTNRES_ERR_UNSUPPORTED,
+                "deferred backward: no kernel for %d sources, hidden=%d and these dtypes (bf16, hidden 3072 with "
+                "2..8 sources or 4096 with 2..9)",
+                num_sources, hidden);
+  if (src_ld < hidden || grad_ld < hidden || grad_out_ld < hidden)
+    return fail(ATTNRES_ERR_ARG, "a row stride is smaller than hidden=%d", hidden);
+  if ((src_ld * 2) % 16 != 0 || (grad_ld * 2) % 16 != 0 || (grad_out_ld * 2) % 16 != 0)
+    return fail(ATTNRES_ERR_ALIGN, "row strides not 16-byte aligned");
+  if (!aligned16(grad_out) || !aligned16(grad_partial) || !aligned16(coef) || !aligned16(qfold) ||
+      (grad_partial_addend != nullptr && !aligned16(grad_partial_addend)))
+    return fail(ATTNRES_ERR_ALIGN, "grad_out, grad_partial, its addend, coef or qfold not 16-byte aligned");
+  for (int s = 0; s < num_sources; ++s) {
+    if (sources[s] == nullptr) return fail(ATTNRES_ERR_ARG, "sources[%d] is NULL", s);
+    if (!aligned16(sources[s])) return fail(ATTNRES_ERR_ALIGN, "sources[%d] not 16-byte aligned", s);
+  }
+  if (num_tokens == 0) return ATTNRES_OK;
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  if (bwd_stream_lds(nch, num_sources) > (size_t)st->max_lds)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "deferred backward: %zu bytes of LDS exceed the device's %d",
+                bwd_stream_lds(nch, num_sources), st->max_lds);
+  hipFunction_t f = nullptr;
+  rc = get_bwd_defer(*st, nch, num_sources, &f);
+  if (rc != ATTNRES_OK) return rc;
+  void* grads[ATTNRES_MAX_SOURCES] = {};
+  const void* adds[ATTNRES_MAX_SOURCES] = {};
+  grads[num_sources - 1] = grad_partial;
+  adds[num_sources - 1] = grad_partial_addend;
+  const int64_t need_wg = (num_tokens + kBwdStreamWaves - 1) / kBwdStreamWaves;
+  const int64_t cap = (int64_t)st->num_cus * (tuning().bwd_per_cu > 0 ? tuning().bwd_per_cu : 1);
+  const int grid = (int)(need_wg < cap ? need_wg : cap);
+  return route_bwd_finish(f, grid, 64 * kBwdStreamWaves, bwd_stream_lds(nch, num_sources), *st, hidden / 8, sources,
+                          num_sources, num_tokens, hidden, src_ld, query, gain, param_dtype, eps, grad_out,
+                          grad_out_dtype, grad_out_ld, grad_lse, grads, grad_ld, workspace, workspace_bytes,
+                          grad_query, grad_gain, stream, adds, coef, qfold);
+}
+
+// Sum of deferred gradient terms: one launch per ATTNRES_GATHER_MAX_TERMS
+// terms, the later ones adding to `out`.  Grid: one 4-wave workgroup per CU.
+constexpr int kGatherWaves = 4;
+int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int64_t x_ld, int dtype, int num_terms,
+                             const void* const* grad_outs, int64_t grad_out_ld, const float* const* coefs,
+                             const int64_t* coef_lds, const void* const* qfolds, const void* addend, void* out,
+                             int64_t out_ld, void* stream) {
+  if (x == nullptr || out == nullptr) return fail(ATTNRES_ERR_ARG, "x/out is NULL");
+  if (num_tokens < 0 || hidden <= 0) return fail(ATTNRES_ERR_ARG, "bad num_tokens/hidden");
+  if (num_terms < 0) return fail(ATTNRES_ERR_ARG, "num_terms=%d < 0", num_terms);
+  if (num_terms > 0 && (grad_outs == nullptr || coefs == nullptr || coef_lds == nullptr || qfolds == nullptr))
+    return fail(ATTNRES_ERR_ARG, "term arrays are NULL");
+  if (!valid_dtype(dtype)) return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (dtype != ATTNRES_DTYPE_BF16 || (hidden != 3072 && hidden != 4096))
+    return fail(ATTNRES_ERR_UNSUPPORTED, "gather: bf16 rows of hidden 3072 or 4096 only (hidden=%d)", hidden);
+  if (x_ld < hidden || out_ld < hidden || (num_terms > 0 && grad_out_ld < hidden))
+    return fail(ATTNRES_ERR_ARG, "a row stride is smaller than hidden=%d", hidden);
+  if ((x_ld * 2) % 16 != 0 || (out_ld * 2) % 16 != 0 || (num_terms > 0 && (grad_out_ld * 2) % 16 != 0))
+    return fail(ATTNRES_ERR_ALIGN, "row strides not 16-byte aligned");
+  if (!aligned16(x) || !aligned16(out) || (addend != nullptr && !aligned16(addend)))
+    return fail(ATTNRES_ERR_ALIGN, "x, out or addend not 16-byte aligned");
+  for (int j = 0; j < num_terms; ++j) {
+    if (grad_outs[j] == nullptr || coefs[j] == nullptr || qfolds[j] == nullptr)
+      return fail(ATTNRES_ERR_ARG, "term %d has a NULL pointer", j);
+    if (!aligned16(grad_outs[j]) || !aligned16(coefs[j]) || !aligned16(qfolds[j]))
+      return fail(ATTNRES_ERR_ALIGN, "term %d: grad_out, coef or qfold not 16-byte aligned", j);
+    if (coef_lds[j] < 4 || coef_lds[j] % 4 != 0)
+      return fail(ATTNRES_ERR_ARG, "term %d: coef_ld=%lld is not a positive multiple of 4", j,
+                  (long long)coef_lds[j]);
+  }
+  if (num_tokens == 0) return ATTNRES_OK;
+  if (num_tokens >= (int64_t)1 << 31) return fail(ATTNRES_ERR_UNSUPPORTED, "num_tokens >= 2^31");
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  const int nch = hidden / 512;
+  hipFunction_t f = nullptr;
+  rc = get_gather(*st, nch, &f);
+  if (rc != ATTNRES_OK) return rc;
+  const int64_t need_wg = (num_tokens + kGatherWaves - 1) / kGatherWaves;
+  const int64_t cap = (int64_t)st->num_cus;
+  const int grid = (int)(need_wg < cap ? need_wg : cap);
+  attnres_route_bwd_gather_params P;
+  int j0 = 0;
+  do {
+    const int nt = num_terms - j0 < ATTNRES_GATHER_MAX_TERMS ? num_terms - j0 : ATTNRES_GATHER_MAX_TERMS;
+    std::memset(&P, 0, sizeof(P));
+    P.x = x;
+    P.addend = j0 == 0 ? addend : out;
+    P.out = out;
+    P.n_tokens = num_tokens;
+    P.x_ld = x_ld;
+    P.gout_ld = grad_out_ld;
+    P.out_ld = out_ld;
+    P.d = hidden;
+    P.num_terms = nt;
+    P.block = 64 * kGatherWaves;
+    for (int j = 0; j < nt; ++j) {
+      P.term[j].grad_out = grad_outs[j0 + j];
+      P.term[j].coef = coefs[j0 + j];
+      P.term[j].qfold = qfolds[j0 + j];
+      P.term[j].coef_ld = coef_lds[j0 + j];
+    }
+    rc = launch(f, grid, 64 * kGatherWaves, P, stream, 1, 0);
+    if (rc != ATTNRES_OK) return rc;
+    j0 += nt;
+  } while (j0 < num_terms);
+  return ATTNRES_OK;
 }
 
 // Workspace of the batched-query backward: c1 coefficients (num_tokens, Q, S)

@@ -2023,9 +2023,16 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
 // ADD: sources with a non-NULL P.dadd[s] get dx_s + dadd[s]; the addend row
 // of source s + 1 is requested before the gradient of source s is formed, so
 // one addend row per wave is in flight behind the row being stored.
-template <int S, int NCH, int KL, bool ADD = false>
+// DEFER (with ADD): only the last source's gradient row is formed (plus
+// dadd[S-1], requested before the second pass); for sources 0 .. S-2 lane s
+// stores the token's (w_s, c1_s, c2_s, 0) to P.coef, and workgroup 0 writes
+// the folded query to P.qfold (bf16 parameters), so that the sum of a
+// block's gradients over the points that read it is formed once, later
+// (route_bwd_gather_body), from the points' output gradients.
+template <int S, int NCH, int KL, bool ADD = false, bool DEFER = false>
 __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_params& P) {
   static_assert(KL >= 0 && KL < S, "at least one source row is kept in registers");
+  static_assert(!DEFER || (ADD && S >= 2), "deferred gradients need a committed source and the addend path");
   // Dynamic LDS in float4 slots [chunk][half][lane] (consecutive lanes 16
   // bytes apart): the folded query in fp32 and, past it, each wave's KL kept
   // rows ([wave][row][chunk][lane], 16-byte slots); at the end one row of
@@ -2054,6 +2061,12 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
     const int c = i >> 6, l = i & 63;
     bws_lds[(c * 2) * 64 + l] = make_float4(q[0], q[1], q[2], q[3]);
     bws_lds[(c * 2 + 1) * 64 + l] = make_float4(q[4], q[5], q[6], q[7]);
+    if constexpr (DEFER) {
+      if (blockIdx.x == 0) {
+        const u32x4 pk = {pack_bf16(q[0], q[1]), pack_bf16(q[2], q[3]), pack_bf16(q[4], q[5]), pack_bf16(q[6], q[7])};
+        stg<u32x4>(static_cast<char*>(P.qfold) + (size_t)i * 16, pk);
+      }
+    }
   }
   __syncthreads();
   // The query is read from LDS at each use (an opaque index): hoisted out of
@@ -2171,6 +2184,15 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
         c1[s] = wgt[s] * (glse + (gx[s] - go)) * ri[s];
         c2[s] = -c1[s] * lg[s] * ri[s] * P.inv_d;
       }
+      if constexpr (DEFER) {
+        // the committed sources' coefficients: lane s holds source s's record
+        float4 rec = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int s = 0; s < S - 1; ++s) {
+          if (lane == s) rec = make_float4(wgt[s], c1[s], c2[s], 0.f);
+        }
+        if (lane < S - 1) stg<float4>(P.coef + ((uint64_t)t * (S - 1) + (uint32_t)lane) * 4, rec);
+      }
 
       // ---- the gradient rows, one whole row per source ----
       // The kept rows are re-expanded here (opaque copies) rather than kept
@@ -2186,12 +2208,12 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
 #pragma unroll
         for (int c = 0; c < (ADD ? NCH : 1); ++c) buf[c] = ld_row(ar, lane_off + (uint32_t)(c * 1024));
       };
-      if constexpr (ADD) load_add(adA, 0);
+      if constexpr (ADD) load_add(adA, DEFER ? S - 1 : 0);
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        u32x4(&ad_cur)[ADD ? NCH : 1] = (s & 1) ? adB : adA;
+        u32x4(&ad_cur)[ADD ? NCH : 1] = (DEFER || !(s & 1)) ? adA : adB;
         u32x4(&ad_nxt)[ADD ? NCH : 1] = (s & 1) ? adA : adB;
-        if constexpr (ADD) {
+        if constexpr (ADD && !DEFER) {
           if (s + 1 < S) load_add(ad_nxt, s + 1 < S ? s + 1 : 0);
         }
         u32x4 xk[NCH];
@@ -2203,6 +2225,18 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
             xk[c] = keep[s >= KL ? s - KL : 0][c];
             asm volatile("" : "+v"(xk[c]));
           }
+        }
+        if (DEFER && s < S - 1) {
+          // a committed source: its query-gradient term only
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              dq[c][2 * w] = __builtin_fmaf(c1[s], bf_lo(xk[c][w]), dq[c][2 * w]);
+              dq[c][2 * w + 1] = __builtin_fmaf(c1[s], bf_hi(xk[c][w]), dq[c][2 * w + 1]);
+            }
+          }
+          continue;
         }
         char* drow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.dsrc[s]) + (uint64_t)t * drow_bytes));
         const __amdgpu_buffer_rsrc_t dr = row_rsrc(drow, (uint32_t)(NCH * 1024));
@@ -2257,6 +2291,143 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
   }
 }
 
+
+// ---------------------------------------------- deferred-gradient sum --
+//
+// One committed block's gradient from the coefficients the `_defer`
+// backward kernels stored, one wave per token row (grid-stride; a resident
+// grid of 4-wave workgroups), bf16 rows of NCH KiB:
+//   out = addend + sum_j (w_j G_j + c1_j q_j) + (sum_j c2_j) x
+// A row's items stream through a two-slot pipeline (the next item is
+// requested once the current one has arrived, as in stream_body): per term j
+// its coefficient record, its folded query q_j (read by every row: it stays
+// in L2) and its output-gradient row G_j; then the block's row x; then the
+// addend row (an empty buffer resource when there is none: its loads return
+// 0 without a memory access).  fp32 accumulators, one rounding at the store.
+__device__ __forceinline__ u32x4 ld_row_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);  // nt: read once
+}
+
+template <int NCH>
+__device__ __forceinline__ void route_bwd_gather_body(const attnres_route_bwd_gather_params& P) {
+  constexpr uint32_t RB = NCH * 1024;
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t nwv = (uint32_t)P.block >> 6;
+  const uint32_t n_tok = (uint32_t)P.n_tokens;
+  const uint32_t nw = gridDim.x * nwv;
+  const uint32_t tok0 = blockIdx.x * nwv + wave;
+  if (tok0 >= n_tok) return;
+  const uint32_t rows = (n_tok - tok0 - 1) / nw + 1;
+  const uint32_t nt = (uint32_t)P.num_terms;
+  const uint32_t per = nt + 2;
+  const uint32_t lane_off = (uint32_t)lane * 16;
+
+  // item r of the wave's row j; past the wave's last item, that item again
+  auto issue = [&](u32x4(&row)[NCH], u32x4(&q)[NCH], u32x4& cf, uint32_t j, uint32_t r, uint32_t z) {
+    if (j >= rows) {
+      j = rows - 1;
+      r = per - 1;
+    }
+    j = __builtin_amdgcn_readfirstlane(j);
+    r = __builtin_amdgcn_readfirstlane(r);
+    const uint64_t t = tok0 + (uint64_t)j * nw;
+    char* rbase;
+    uint32_t rbytes = RB;
+    char* qbase = nullptr;
+    char* cbase = nullptr;
+    if (r < nt) {
+      const attnres_gather_term& T = P.term[r];
+      rbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(T.grad_out) + t * (uint64_t)P.gout_ld * 2));
+      qbase = const_cast<char*>(static_cast<const char*>(T.qfold));
+      cbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(T.coef) + t * (uint64_t)T.coef_ld * 4));
+    } else if (r == nt) {
+      rbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.x) + t * (uint64_t)P.x_ld * 2));
+    } else {
+      rbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.addend) + t * (uint64_t)P.out_ld * 2));
+      rbytes = P.addend != nullptr ? RB : 0u;
+    }
+    const __amdgpu_buffer_rsrc_t rc = row_rsrc(cbase, cbase != nullptr ? 16u : 0u);
+    const __amdgpu_buffer_rsrc_t rq = row_rsrc(qbase, qbase != nullptr ? RB : 0u);
+    const __amdgpu_buffer_rsrc_t rr = row_rsrc(rbase, rbytes);
+    // record and query first: rows return in order, so the row's arrival implies theirs
+    cf = __builtin_amdgcn_raw_buffer_load_b128(rc, z, 0, 0);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) q[c] = __builtin_amdgcn_raw_buffer_load_b128(rq, lane_off + (uint32_t)(c * 1024) + z, 0, 0);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) row[c] = ld_row_nt(rr, lane_off + (uint32_t)(c * 1024) + z);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  float acc[NCH][8];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
+  }
+  float csum = 0.f;
+  // item (j, r) of the wave's rows; (j, r) wave-uniform, passed by value
+  auto process = [&](u32x4(&row)[NCH], u32x4(&q)[NCH], const u32x4& cf, uint32_t j, uint32_t r) {
+    float a, b;
+    if (r < nt) {
+      a = as_f32(cf[0]);
+      b = as_f32(cf[1]);
+      csum += as_f32(cf[2]);
+    } else {
+      a = r == nt ? csum : 1.0f;
+      b = 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        acc[c][2 * w] = __builtin_fmaf(a, bf_lo(row[c][w]), __builtin_fmaf(b, bf_lo(q[c][w]), acc[c][2 * w]));
+        acc[c][2 * w + 1] = __builtin_fmaf(a, bf_hi(row[c][w]), __builtin_fmaf(b, bf_hi(q[c][w]), acc[c][2 * w + 1]));
+      }
+    }
+    if (r == per - 1) {
+      const uint64_t t = tok0 + (uint64_t)j * nw;
+      char* orow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.out) + t * (uint64_t)P.out_ld * 2));
+      const __amdgpu_buffer_rsrc_t ro = row_rsrc(orow, RB);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        u32x4 pk;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) pk[w] = pack_bf16(acc[c][2 * w], acc[c][2 * w + 1]);
+        st_row(ro, lane_off + (uint32_t)(c * 1024), pk);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
+      }
+      csum = 0.f;
+    }
+  };
+  // the item after (j, r), wave-uniform
+  auto after = [per](uint32_t& j, uint32_t& r) {
+    const uint32_t r1 = r + 1;
+    const bool wrap = r1 == per;
+    r = __builtin_amdgcn_readfirstlane(wrap ? 0u : r1);
+    j = __builtin_amdgcn_readfirstlane(wrap ? j + 1 : j);
+  };
+
+  u32x4 ra[NCH], qa[NCH], rb2[NCH], qb[NCH], ca, cb;
+  uint32_t ji = 0, ri = 0;  // the item issued next
+  uint32_t jp = 0, rp = 0;  // the item processed next
+  issue(ra, qa, ca, ji, ri, 0u);
+  after(ji, ri);
+  const uint32_t items = rows * per;
+  for (uint32_t i = 0; i < items; i += 2) {
+    issue(rb2, qb, cb, ji, ri, arrival_zero(ra[NCH - 1][3]));
+    after(ji, ri);
+    process(ra, qa, ca, jp, rp);
+    after(jp, rp);
+    issue(ra, qa, ca, ji, ri, arrival_zero(rb2[NCH - 1][3]));
+    after(ji, ri);
+    if (i + 1 < items) {
+      process(rb2, qb, cb, jp, rp);
+      after(jp, rp);
+    }
+  }
+}
 
 // ------------------------------------------- batched-query backward body --
 //
@@ -3379,7 +3550,7 @@ __device__ __forceinline__ void reduce_dqw_body(const attnres_reduce_params& P) 
   ROUTE_TYPES(S, 1) \
   ROUTE_TYPES(S, 2)
 
-// The build compiles this file once per module part (ATTNRES_PART = 0..9)
+// The build compiles this file once per module part (ATTNRES_PART = 0..10)
 // so the parts build in parallel; the host maps each symbol to its part.
 #ifndef ATTNRES_PART
 #define ATTNRES_PART 0
@@ -3674,4 +3845,30 @@ BWD_S_ADD(13)
 BWD_S_ADD(14)
 BWD_S_ADD(15)
 BWD_S_ADD(16)
+#endif
+
+// Deferred block gradients (the training loop's routing points):
+// attnres_route_bwd_stream_c<NCH>_s<S>_defer, the row-per-wave backward that
+// forms only the last source's gradient and stores the committed sources'
+// coefficients, and attnres_route_bwd_gather_c<NCH>, which sums one block's
+// gradient from them.
+#define BWD_STREAM_ONE_DEFER(S, NCH, KL)                                                                \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))            \
+      attnres_route_bwd_stream_c##NCH##_s##S##_defer(attnres_route_bwd_params P) {                       \
+    route_bwd_stream_body<S, NCH, KL, true, true>(P);                                                   \
+  }
+#define GATHER_ONE(NCH)                                                                                 \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))            \
+      attnres_route_bwd_gather_c##NCH(attnres_route_bwd_gather_params P) {                               \
+    route_bwd_gather_body<NCH>(P);                                                                      \
+  }
+
+#if ATTNRES_PART == 10 || defined(ATTNRES_ALL_PARTS)
+BWD_STREAM_ONE_DEFER(2, 6, 0) BWD_STREAM_ONE_DEFER(3, 6, 0) BWD_STREAM_ONE_DEFER(4, 6, 0)
+BWD_STREAM_ONE_DEFER(5, 6, 0) BWD_STREAM_ONE_DEFER(6, 6, 0) BWD_STREAM_ONE_DEFER(7, 6, 0)
+BWD_STREAM_ONE_DEFER(8, 6, 0)
+BWD_STREAM_ONE_DEFER(2, 8, 0) BWD_STREAM_ONE_DEFER(3, 8, 0) BWD_STREAM_ONE_DEFER(4, 8, 0)
+BWD_STREAM_ONE_DEFER(5, 8, 0) BWD_STREAM_ONE_DEFER(6, 8, 0) BWD_STREAM_ONE_DEFER(7, 8, 1)
+BWD_STREAM_ONE_DEFER(8, 8, 2) BWD_STREAM_ONE_DEFER(9, 8, 3)
+GATHER_ONE(6) GATHER_ONE(8)
 #endif

@@ -85,6 +85,12 @@ typedef struct attnres_route_bwd_params {
   const void* grad_out;  /* (n_tokens, d) */
   const float* grad_lse; /* (n_tokens,) or NULL */
   float* dqw_part;       /* (gridDim.x, d) fp32 */
+  /* The `_defer` kernels: the gradients of sources 0 .. S-2 are not formed;
+   * token t's coefficients of source s go to coef[(t*(S-1) + s)*4 ...] as
+   * (w_s, c1_s, c2_s, 0), and workgroup 0 writes the folded query (d values,
+   * param dtype) to qfold.  Only dsrc[S-1] (with dadd[S-1]) is written. */
+  float* coef;
+  void* qfold;
   int64_t n_tokens;
   int64_t src_ld;
   int64_t dsrc_ld;
@@ -96,6 +102,36 @@ typedef struct attnres_route_bwd_params {
   float eps;
   float inv_d;
 } attnres_route_bwd_params;
+
+/*
+ * One block's gradient from the coefficients the `_defer` kernels left, for
+ * every token t:
+ *   out = addend + sum_j (w_j G_j + c1_j qfold_j) + (sum_j c2_j) x
+ * with (w_j, c1_j, c2_j) at term[j].coef + t*coef_ld floats.  bf16 rows and
+ * folded queries; out may be addend (in place).
+ */
+#define ATTNRES_GATHER_MAX_TERMS 48
+typedef struct attnres_gather_term {
+  const void* grad_out;  /* (n_tokens, d), row stride gout_ld */
+  const float* coef;     /* token 0's (w, c1, c2, -) */
+  const void* qfold;     /* (d,) */
+  int64_t coef_ld;       /* floats from one token's record to the next */
+} attnres_gather_term;
+
+typedef struct attnres_route_bwd_gather_params {
+  const void* x;       /* (n_tokens, d), row stride x_ld */
+  const void* addend;  /* (n_tokens, d), row stride out_ld, or NULL */
+  void* out;           /* (n_tokens, d), row stride out_ld */
+  int64_t n_tokens;
+  int64_t x_ld;
+  int64_t gout_ld;
+  int64_t out_ld;
+  int32_t d;
+  int32_t num_terms;   /* 1 .. ATTNRES_GATHER_MAX_TERMS */
+  int32_t block;       /* threads per workgroup */
+  int32_t pad;
+  attnres_gather_term term[ATTNRES_GATHER_MAX_TERMS];
+} attnres_route_bwd_gather_params;
 
 /*
  * Backward of Q >= 2 queries over one set of sources (the batched phase-1

@@ -625,30 +625,60 @@ route_list.register_autograd(_route_list_backward, setup_context=_route_list_set
 
 class GradSlot:
     """The gradient of one committed block, summed over the routing calls that
-    read it during one backward pass."""
+    read it during one backward pass: rows accumulated in place (``buf``,
+    attnres_route_bwd_add) and deferred terms (``terms``: per call its output
+    gradient, coefficient records and folded query, attnres_route_bwd_defer),
+    which the block's commit node sums in one pass (attnres_route_bwd_gather)."""
 
-    __slots__ = ("buf", "task")
+    __slots__ = ("buf", "task", "terms")
 
     def __init__(self) -> None:
         self.buf: Optional[Tensor] = None
         self.task: Optional[int] = None
+        self.terms: list = []
+
+    def _join(self) -> None:
+        """Start over when this is a new backward pass (autograd graph task):
+        what an earlier pass left (one that did not reach the commit node) is
+        not added to."""
+        task = torch._C._current_graph_task_id()
+        if self.task != task:
+            self.buf, self.terms, self.task = None, [], task
 
     def target(self, like: Tensor) -> tuple[Tensor, bool]:
-        """The buffer for one more call's gradient and whether to add to it.
-        The first call of a backward pass (autograd graph task) writes a fresh
-        buffer; what an earlier pass left (one that did not reach the commit
-        node) is not added to."""
-        task = torch._C._current_graph_task_id()
-        if self.buf is None or self.task != task:
+        """The buffer for one more call's gradient and whether to add to it."""
+        self._join()
+        if self.buf is None:
             self.buf = torch.empty(like.shape, device=like.device, dtype=like.dtype)
-            self.task = task
             return self.buf, False
         return self.buf, True
 
-    def take(self) -> Optional[Tensor]:
-        buf = self.buf
-        self.buf, self.task = None, None
-        return buf
+    def defer(self, grad_out: Tensor, coef: Tensor, index: int, qfold: Tensor) -> None:
+        """Record one call's term: ``grad_out`` (n, D) rows, the call's
+        (n, S-1, 4) coefficient records, this block's source index in the
+        call and the call's folded query."""
+        self._join()
+        self.terms.append((grad_out, coef, index, qfold))
+
+    def take(self) -> tuple[Optional[Tensor], list]:
+        buf, terms = self.buf, self.terms
+        self.buf, self.terms, self.task = None, [], None
+        return buf, terms
+
+
+def _gather_terms(x: Tensor, terms: list, addend: Optional[Tensor], out: Tensor) -> None:
+    """attnres_route_bwd_gather: out = addend + the deferred terms' sum."""
+    d = x.shape[-1]
+    n = x.numel() // d
+    with _DeviceStream(x.device) as stream:
+        _capi.route_bwd_gather(
+            x.data_ptr(), n, d, d, dtype_code(x.dtype), len(terms),
+            _capi.pointer_array([g.data_ptr() for g, _, _, _ in terms]), d,
+            _capi.pointer_array([c.data_ptr() + 16 * k for _, c, k, _ in terms]),
+            _capi.int64_array([4 * c.shape[1] for _, c, _, _ in terms]),
+            _capi.pointer_array([q.data_ptr() for _, _, _, q in terms]),
+            addend.data_ptr() if addend is not None else None, out.data_ptr(), d, stream,
+        )
 
 
 class _Commit(torch.autograd.Function):
@@ -660,17 +690,27 @@ class _Commit(torch.autograd.Function):
     def forward(ctx, block, slot):
         ctx.slot = slot
         ctx.set_materialize_grads(False)
+        ctx.save_for_backward(block)
         return block.view_as(block)
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, grad):
-        acc = ctx.slot.take()
-        if acc is None:
-            return grad, None
-        if grad is not None:
+        acc, terms = ctx.slot.take()
+        if acc is not None and grad is not None:
             acc.add_(grad)
-        return acc, None
+        elif acc is None:
+            acc = grad
+        if not terms:
+            return acc, None
+        (x,) = ctx.saved_tensors
+        x = x if x.is_contiguous() else x.contiguous()
+        if acc is not None and not acc.is_contiguous():
+            acc = acc.contiguous()
+        # in place into our own buffer; a fresh tensor when the addend is autograd's
+        out = acc if (acc is not None and acc is not grad) else torch.empty(x.shape, device=x.device, dtype=x.dtype)
+        _gather_terms(x, terms, acc, out)
+        return out, None
 
 
 def commit_block(block: Tensor, slot: GradSlot) -> Tensor:
@@ -692,6 +732,38 @@ def _route_rows_backward(sources, grads, adds, query, gain, eps, grad_out) -> tu
         [t.data_ptr() for t in sources], [g.data_ptr() for g in grads], sources[0].dtype, n, d, device, query, gain,
         eps, grad_out, None, add_ptrs=[a.data_ptr() if a is not None else None for a in adds],
     )
+
+
+def _route_rows_backward_defer(sources, query, gain, eps, grad_out, grad_add):
+    """attnres_route_bwd_defer: (partial's gradient, (n, S-1, 4) coefficient
+    records, folded query, grad_out as (n, D) rows, grad_query, grad_gain),
+    or None when the library has no deferred kernel for the call."""
+    p = sources[-1]
+    device = p.device
+    d = p.shape[-1]
+    n = p.numel() // d
+    q = query.reshape(-1)
+    if p.dtype != torch.bfloat16 or d not in (3072, 4096) or (gain is not None and gain.dtype != q.dtype):
+        return None  # no deferred kernel (the library decides the rest)
+    kq, kg, pcode = _fold_query(q, gain)
+    grad_out = grad_out.reshape(n, d).contiguous()
+    gp = torch.empty(p.shape, device=device, dtype=p.dtype)
+    coef = torch.empty((n, len(sources) - 1, 4), device=device, dtype=torch.float32)
+    qfold = torch.empty(d, device=device, dtype=kq.dtype)
+    dq = torch.empty(d, device=device, dtype=kq.dtype)
+    dg = torch.empty(d, device=device, dtype=kg.dtype) if kg is not None else None
+    with _DeviceStream(device) as stream:
+        ws = torch.empty(max(1, _capi.route_bwd_workspace_size(n, d) // 4), device=device, dtype=torch.float32)
+        code = _capi.route_bwd_defer(
+            _capi.pointer_array([t.data_ptr() for t in sources]), len(sources), n, d, d, dtype_code(p.dtype),
+            kq.data_ptr(), kg.data_ptr() if kg is not None else None, pcode, float(eps), grad_out.data_ptr(),
+            dtype_code(grad_out.dtype), d, None, gp.data_ptr(), grad_add.data_ptr() if grad_add is not None else None,
+            d, coef.data_ptr(), qfold.data_ptr(), ws.data_ptr(), ws.numel() * 4, dq.data_ptr(),
+            dg.data_ptr() if dg is not None else None, stream,
+        )
+    if code != _capi.OK:
+        return None
+    return gp, coef, qfold, grad_out, dq.reshape(query.shape), dg
 
 
 def _route_rows_step(committed, partial, delta, query, gain, eps, out_dtype) -> tuple[Tensor, Tensor]:
@@ -730,9 +802,14 @@ class _RoutePoint(torch.autograd.Function):
     rows and the partial block this point routed (``partial + delta`` in a new
     tensor, attnres_route_step; or the partial itself, as a view).  The
     backward forms the routed partial's gradient as the routing gradient plus
-    the gradient of the partial output (attnres_route_bwd_add with that
-    gradient as the addend), which is also the gradient of ``partial`` and of
-    ``delta``: autograd adds nothing."""
+    the gradient of the partial output (that gradient as the kernel's addend),
+    which is also the gradient of ``partial`` and of ``delta``: autograd adds
+    nothing.  Where the library has a deferred kernel for the call
+    (attnres_route_bwd_defer: bf16, hidden 3072 / 4096) the committed blocks'
+    gradients are not formed here: the call's output gradient and
+    coefficients go to each block's GradSlot, and the block's commit node sums
+    them once (attnres_route_bwd_gather); otherwise each block's gradient is
+    added into its slot's rows (attnres_route_bwd_add)."""
 
     @staticmethod
     def forward(ctx, slots, eps, out_dtype, query, gain, delta, *sources):
@@ -763,6 +840,20 @@ class _RoutePoint(torch.autograd.Function):
                 gp if need[6 + n_com] else None,)
         query, gain, routed, *committed = ctx.saved_tensors
         sources = [t if t.is_contiguous() else t.contiguous() for t in (*committed, routed)]
+        if g_partial is not None and not g_partial.is_contiguous():
+            g_partial = g_partial.contiguous()
+        com_need = need[6:6 + n_com]
+        if n_com and any(com_need) and all(slot is not None or not nd for slot, nd in zip(ctx.slots, com_need)):
+            # the committed blocks' gradients deferred to their commit nodes
+            res = _route_rows_backward_defer(sources, query, gain, ctx.eps, g_out, g_partial)
+            if res is not None:
+                gp, coef, qfold, g_rows, dq, dg = res
+                for s_idx, (slot, nd) in enumerate(zip(ctx.slots, com_need)):
+                    if nd:
+                        slot.defer(g_rows, coef, s_idx, qfold)
+                return ((None, None, None, dq if need[3] else None, dg if (gain is not None and need[4]) else None,
+                         gp if ctx.has_delta and need[5] else None) + (None,) * n_com
+                        + (gp if need[6 + n_com] else None,))
         grads, adds = [], []
         for src, slot, nd in zip(sources[:-1], ctx.slots, need[6:6 + n_com]):
             if slot is None or not nd:
@@ -775,8 +866,6 @@ class _RoutePoint(torch.autograd.Function):
         p = sources[-1]
         gp = torch.empty(p.shape, device=p.device, dtype=p.dtype)
         grads.append(gp)
-        if g_partial is not None and not g_partial.is_contiguous():
-            g_partial = g_partial.contiguous()
         adds.append(g_partial)
         dq, dg = _route_rows_backward(sources, grads, adds, query, gain, ctx.eps, g_out)
         res = [None, None, None, dq if need[3] else None, dg if (gain is not None and need[4]) else None,

@@ -38,6 +38,7 @@ C_TO_CTYPES = {
     "const void*": ctypes.c_void_p, "void*": ctypes.c_void_p, "const float*": ctypes.c_void_p,
     "float*": ctypes.c_void_p, "const void* const*": ctypes.POINTER(ctypes.c_void_p),
     "void* const*": ctypes.POINTER(ctypes.c_void_p), "int64_t*": ctypes.POINTER(ctypes.c_int64),
+    "const float* const*": ctypes.POINTER(ctypes.c_void_p), "const int64_t*": ctypes.POINTER(ctypes.c_int64),
 }
 
 
@@ -259,3 +260,50 @@ def test_route_bwd_add_argument_errors():
     # without any addend the call is attnres_route_bwd
     assert call(_capi.pointer_array([None, None]), gdt=_capi.DTYPE_F32, n=0) == _capi.OK
     assert call(None, gdt=_capi.DTYPE_F32, n=0) == _capi.OK
+
+
+def test_route_bwd_defer_argument_errors():
+    lib = _capi.lib()
+    bf, f32 = _capi.DTYPE_BF16, _capi.DTYPE_F32
+
+    def call(S=3, D=3072, n=0, sdt=bf, gdt=bf, pdt=bf, gp=FAKE + 65536, coef=FAKE + 131072, qfold=FAKE + 196608,
+             add=None):
+        srcs = _capi.pointer_array([FAKE + 4096 * s for s in range(S)])
+        return lib.attnres_route_bwd_defer(srcs, S, n, D, D, sdt, FAKE, None, pdt, 1e-5, FAKE, gdt, D, None, gp, add,
+                                           D, coef, qfold, FAKE, 1 << 20, None, None, None)
+
+    # kernels: bf16 everywhere, hidden 3072 (2..8 sources) or 4096 (2..9); n = 0 returns before any HIP call
+    assert call() == _capi.OK
+    assert call(S=8) == _capi.OK and call(S=9, D=4096) == _capi.OK
+    assert call(S=9) == _capi.ERR_UNSUPPORTED
+    assert call(S=1) == _capi.ERR_UNSUPPORTED  # no committed source to defer
+    assert call(D=2048) == _capi.ERR_UNSUPPORTED
+    assert call(sdt=f32) == _capi.ERR_UNSUPPORTED and call(gdt=f32) == _capi.ERR_UNSUPPORTED
+    assert call(pdt=f32) == _capi.ERR_UNSUPPORTED
+    assert call(S=17) == _capi.ERR_ARG
+    assert call(gp=None) == _capi.ERR_ARG and call(coef=None) == _capi.ERR_ARG and call(qfold=None) == _capi.ERR_ARG
+    assert call(coef=FAKE + 8) == _capi.ERR_ALIGN and call(add=FAKE + 4) == _capi.ERR_ALIGN
+    assert call(add=FAKE + 65536) == _capi.OK  # the addend may be the gradient itself
+
+
+def test_route_bwd_gather_argument_errors():
+    lib = _capi.lib()
+    bf = _capi.DTYPE_BF16
+
+    def call(nt=2, D=3072, n=0, dt=bf, gouts=None, coefs=None, lds=None, qfs=None, x=FAKE, out=FAKE + 65536,
+             add=None):
+        gouts = gouts if gouts is not None else [FAKE + 4096 * j for j in range(nt)]
+        coefs = coefs if coefs is not None else [FAKE + 1024 * j for j in range(nt)]
+        lds = lds if lds is not None else [8] * nt
+        qfs = qfs if qfs is not None else [FAKE] * nt
+        return lib.attnres_route_bwd_gather(x, n, D, D, dt, nt, _capi.pointer_array(gouts), D,
+                                            _capi.pointer_array(coefs), _capi.int64_array(lds),
+                                            _capi.pointer_array(qfs), add, out, D, None)
+
+    assert call() == _capi.OK and call(nt=0) == _capi.OK and call(D=4096, nt=60) == _capi.OK
+    assert call(D=2048) == _capi.ERR_UNSUPPORTED and call(dt=_capi.DTYPE_F32) == _capi.ERR_UNSUPPORTED
+    assert call(nt=-1) == _capi.ERR_ARG and call(x=None) == _capi.ERR_ARG and call(out=None) == _capi.ERR_ARG
+    assert call(gouts=[FAKE, None]) == _capi.ERR_ARG
+    assert call(lds=[8, 6]) == _capi.ERR_ARG and call(lds=[0, 8]) == _capi.ERR_ARG
+    assert call(coefs=[FAKE, FAKE + 4]) == _capi.ERR_ALIGN and call(add=FAKE + 2) == _capi.ERR_ALIGN
+    assert call(out=FAKE + 8) == _capi.ERR_ALIGN
