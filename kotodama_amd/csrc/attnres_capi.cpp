@@ -135,7 +135,8 @@ std::atomic<int> g_policy{ATTNRES_POLICY_AUTO};
 // (1: store each row at once), ATTNRES_OUT_BATCH_MIN_S sets the source count
 // from which they stage, ATTNRES_REDUCE_TWO_STAGE=1 reduces the query
 // gradients in two launches always, ATTNRES_MERGE_STREAM=0 keeps the merge on
-// its row-per-workgroup kernel.
+// its row-per-workgroup kernel, ATTNRES_GATHER_PER_CU and ATTNRES_GATHER_BATCH set
+// the deferred-gradient sum's workgroups per CU (1..4) and staged rows per wave.
 struct Tuning {
   int force_v = 0;
   int qg = 1;
@@ -150,6 +151,8 @@ struct Tuning {
   int stream_waves = 0;        // > 0: waves per workgroup of the streaming kernels (1..4); 0: by S
   int reduce_two_stage = 0;    // 1: the query-gradient reduction in two launches
   int merge_stream = 1;        // 0: the merge never uses the row-per-wave kernel
+  int gather_per_cu = 0;       // > 0: workgroups per CU of the deferred-gradient sum
+  int gather_batch = 0;        // > 0: its staged output rows per wave (1: none)
   Tuning() {
     const char* on = std::getenv("ATTNRES_TUNING");
     if (on == nullptr || std::strcmp(on, "1") != 0) return;
@@ -167,6 +170,16 @@ struct Tuning {
       if (bwd_per_cu > kBwdMaxPerCu) bwd_per_cu = kBwdMaxPerCu;
     }
     if (const char* v = std::getenv("ATTNRES_STREAM_PER_CU")) stream_per_cu = std::atof(v);
+    if (const char* v = std::getenv("ATTNRES_GATHER_PER_CU")) {
+      gather_per_cu = std::atoi(v);
+      if (gather_per_cu < 1) gather_per_cu = 1;
+      if (gather_per_cu > 4) gather_per_cu = 4;
+    }
+    if (const char* v = std::getenv("ATTNRES_GATHER_BATCH")) {
+      gather_batch = std::atoi(v);
+      if (gather_batch < 1) gather_batch = 1;
+      if (gather_batch > 8) gather_batch = 8;
+    }
     if (const char* v = std::getenv("ATTNRES_V")) force_v = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_QG")) qg = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_STREAM")) stream = std::atoi(v);
@@ -1357,6 +1370,7 @@ int attnres_route_bwd_defer(const void* const* sources, int num_sources, int64_t
   if (bwd_stream_lds(nch, num_sources) > (size_t)st->max_lds)
     return fail(ATTNRES_ERR_UNSUPPORTED, "deferred backward: %zu bytes of LDS exceed the device's %d",
                 bwd_stream_lds(nch, num_sources), st->max_lds);
+  const size_t lds = bwd_stream_lds(nch, num_sources);
   hipFunction_t f = nullptr;
   rc = get_bwd_defer(*st, nch, num_sources, &f);
   if (rc != ATTNRES_OK) return rc;
@@ -1367,15 +1381,19 @@ int attnres_route_bwd_defer(const void* const* sources, int num_sources, int64_t
   const int64_t need_wg = (num_tokens + kBwdStreamWaves - 1) / kBwdStreamWaves;
   const int64_t cap = (int64_t)st->num_cus * (tuning().bwd_per_cu > 0 ? tuning().bwd_per_cu : 1);
   const int grid = (int)(need_wg < cap ? need_wg : cap);
-  return route_bwd_finish(f, grid, 64 * kBwdStreamWaves, bwd_stream_lds(nch, num_sources), *st, hidden / 8, sources,
-                          num_sources, num_tokens, hidden, src_ld, query, gain, param_dtype, eps, grad_out,
-                          grad_out_dtype, grad_out_ld, grad_lse, grads, grad_ld, workspace, workspace_bytes,
-                          grad_query, grad_gain, stream, adds, coef, qfold);
+  return route_bwd_finish(f, grid, 64 * kBwdStreamWaves, lds, *st, hidden / 8, sources, num_sources, num_tokens,
+                          hidden, src_ld, query, gain, param_dtype, eps, grad_out, grad_out_dtype, grad_out_ld,
+                          grad_lse, grads, grad_ld, workspace, workspace_bytes, grad_query, grad_gain, stream, adds,
+                          coef, qfold);
 }
 
 // Sum of deferred gradient terms: one launch per ATTNRES_GATHER_MAX_TERMS
-// terms, the later ones adding to `out`.  Grid: one 4-wave workgroup per CU.
+// terms, the later ones adding to `out`.  Grid: kGatherPerCu 4-wave
+// workgroups per CU, each wave staging kGatherBatch finished rows in LDS
+// (fewer where the LDS does not hold them).
 constexpr int kGatherWaves = 4;
+constexpr int kGatherPerCu = 2;
+constexpr int kGatherBatch = 3;
 int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int64_t x_ld, int dtype, int num_terms,
                              const void* const* grad_outs, int64_t grad_out_ld, const float* const* coefs,
                              const int64_t* coef_lds, const void* const* qfolds, const void* addend, void* out,
@@ -1412,9 +1430,17 @@ int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int6
   hipFunction_t f = nullptr;
   rc = get_gather(*st, nch, &f);
   if (rc != ATTNRES_OK) return rc;
+  const int per_cu = tuning().gather_per_cu > 0 ? tuning().gather_per_cu : kGatherPerCu;
   const int64_t need_wg = (num_tokens + kGatherWaves - 1) / kGatherWaves;
-  const int64_t cap = (int64_t)st->num_cus;
+  const int64_t cap = (int64_t)st->num_cus * per_cu;
   const int grid = (int)(need_wg < cap ? need_wg : cap);
+  // staged rows: as many as the LDS holds for per_cu workgroups, at most the default
+  const int64_t row_bytes = (int64_t)hidden * 2;
+  int batch = tuning().gather_batch > 0 ? tuning().gather_batch : kGatherBatch;
+  const int64_t fit = (int64_t)st->max_lds / per_cu / (kGatherWaves * row_bytes);
+  if (batch > fit) batch = (int)fit;
+  if (batch < 1) batch = 1;
+  const size_t lds = batch > 1 ? (size_t)kGatherWaves * batch * row_bytes : 0;
   attnres_route_bwd_gather_params P;
   int j0 = 0;
   do {
@@ -1430,13 +1456,14 @@ int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int6
     P.d = hidden;
     P.num_terms = nt;
     P.block = 64 * kGatherWaves;
+    P.out_batch = batch;
     for (int j = 0; j < nt; ++j) {
       P.term[j].grad_out = grad_outs[j0 + j];
       P.term[j].coef = coefs[j0 + j];
       P.term[j].qfold = qfolds[j0 + j];
       P.term[j].coef_ld = coef_lds[j0 + j];
     }
-    rc = launch(f, grid, 64 * kGatherWaves, P, stream, 1, 0);
+    rc = launch(f, grid, 64 * kGatherWaves, P, stream, 1, lds);
     if (rc != ATTNRES_OK) return rc;
     j0 += nt;
   } while (j0 < num_terms);

@@ -140,6 +140,12 @@ __device__ __forceinline__ T ldg(const void* p) {
 #define ATTNRES_LOAD_CPOL -1  // -1: global loads (nt per ATTNRES_NT_LOADS); >= 0: buffer loads with this policy
 #endif
 
+// A wave-uniform fp32 read through the scalar data cache (s_load): its wait
+// counts with the LDS operations, not with the vector loads in flight.
+__device__ __forceinline__ float ld_scalar_f32(const float* p) {
+  return *(const __attribute__((address_space(4))) float*)(p);
+}
+
 // Zero that the compiler cannot fold, computed from v: adding it to the next
 // load's offset makes that load wait until v has arrived.  The streaming
 // kernels pass the last register of the row just loaded, so a wave requests
@@ -182,6 +188,12 @@ __device__ __forceinline__ void st_row(__amdgpu_buffer_rsrc_t r, uint32_t off, u
 }
 __device__ __forceinline__ void st_row(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, ATTNRES_STORE_CPOL);
+}
+// Non-temporal stores: the deferred backward and its gradient sums, whose
+// stores come one row per token between many reads, ran 2-3% faster with
+// them in the training step (the routing forward kernels 1.5-9% slower).
+__device__ __forceinline__ void st_row_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 2);
 }
 
 template <typename T>
@@ -2059,13 +2071,14 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
       }
     }
     const int c = i >> 6, l = i & 63;
-    bws_lds[(c * 2) * 64 + l] = make_float4(q[0], q[1], q[2], q[3]);
-    bws_lds[(c * 2 + 1) * 64 + l] = make_float4(q[4], q[5], q[6], q[7]);
     if constexpr (DEFER) {
-      if (blockIdx.x == 0) {
-        const u32x4 pk = {pack_bf16(q[0], q[1]), pack_bf16(q[2], q[3]), pack_bf16(q[4], q[5]), pack_bf16(q[6], q[7])};
-        stg<u32x4>(static_cast<char*>(P.qfold) + (size_t)i * 16, pk);
-      }
+      // bf16 parameters: the folded query is bf16-exact and kept packed
+      const u32x4 pk = {pack_bf16(q[0], q[1]), pack_bf16(q[2], q[3]), pack_bf16(q[4], q[5]), pack_bf16(q[6], q[7])};
+      reinterpret_cast<u32x4*>(bws_lds)[c * 64 + l] = pk;
+      if (blockIdx.x == 0) stg<u32x4>(static_cast<char*>(P.qfold) + (size_t)i * 16, pk);
+    } else {
+      bws_lds[(c * 2) * 64 + l] = make_float4(q[0], q[1], q[2], q[3]);
+      bws_lds[(c * 2 + 1) * 64 + l] = make_float4(q[4], q[5], q[6], q[7]);
     }
   }
   __syncthreads();
@@ -2077,6 +2090,12 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
     const float4 qa = bws_lds[i0], qb = bws_lds[i0 + 64];
     q[0] = qa.x, q[1] = qa.y, q[2] = qa.z, q[3] = qa.w;
     q[4] = qb.x, q[5] = qb.y, q[6] = qb.z, q[7] = qb.w;
+  };
+  // DEFER: the packed chunk (x.qw then on v_dot2 like the x.x and x.G sums)
+  auto qp_chunk = [&](int c) {
+    int i0 = c * 64 + lane;
+    asm volatile("" : "+v"(i0));
+    return reinterpret_cast<const u32x4*>(bws_lds)[i0];
   };
   auto lane63 = [](float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
@@ -2133,20 +2152,37 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
         float ss0 = 0.f, ss1 = 0.f, gx0 = 0.f, gx1 = 0.f, dt0 = 0.f, dt1 = 0.f;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
-          float q[8];
-          qw_chunk(c, q);
+          if constexpr (DEFER) {
+            const u32x4 qp = qp_chunk(c);
 #pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const uint32_t xw = cur[c][w];
-            if (w & 1) {
-              ss1 = dot2_bf16(xw, xw, ss1);
-              gx1 = dot2_bf16(xw, g[c][w], gx1);
-            } else {
-              ss0 = dot2_bf16(xw, xw, ss0);
-              gx0 = dot2_bf16(xw, g[c][w], gx0);
+            for (int w = 0; w < 4; ++w) {
+              const uint32_t xw = cur[c][w];
+              if (w & 1) {
+                ss1 = dot2_bf16(xw, xw, ss1);
+                gx1 = dot2_bf16(xw, g[c][w], gx1);
+                dt1 = dot2_bf16(xw, qp[w], dt1);
+              } else {
+                ss0 = dot2_bf16(xw, xw, ss0);
+                gx0 = dot2_bf16(xw, g[c][w], gx0);
+                dt0 = dot2_bf16(xw, qp[w], dt0);
+              }
             }
-            dt0 = __builtin_fmaf(bf_lo(xw), q[2 * w], dt0);
-            dt1 = __builtin_fmaf(bf_hi(xw), q[2 * w + 1], dt1);
+          } else {
+            float q[8];
+            qw_chunk(c, q);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const uint32_t xw = cur[c][w];
+              if (w & 1) {
+                ss1 = dot2_bf16(xw, xw, ss1);
+                gx1 = dot2_bf16(xw, g[c][w], gx1);
+              } else {
+                ss0 = dot2_bf16(xw, xw, ss0);
+                gx0 = dot2_bf16(xw, g[c][w], gx0);
+              }
+              dt0 = __builtin_fmaf(bf_lo(xw), q[2 * w], dt0);
+              dt1 = __builtin_fmaf(bf_hi(xw), q[2 * w + 1], dt1);
+            }
           }
           if (s < KL) kept_lds[(s * NCH + c) * 64] = cur[c];
           else keep[s >= KL ? s - KL : 0][c] = cur[c];
@@ -2175,7 +2211,10 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
         wgt[s] = ex[s] * rsum;
         go = __builtin_fmaf(wgt[s], gx[s], go);
       }
-      const float glse = P.grad_lse != nullptr ? P.grad_lse[t] : 0.f;
+      // dL/dlse through the scalar cache (a wave-uniform read-only value): a
+      // vector load here would be waited for with the next row's G, which is
+      // in flight behind it, and put G's round trip into every row's chain
+      const float glse = P.grad_lse != nullptr ? ld_scalar_f32(P.grad_lse + t) : 0.f;
       float c1[S], c2[S];
 #pragma unroll
       for (int s = 0; s < S; ++s) {
@@ -2191,7 +2230,10 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
         for (int s = 0; s < S - 1; ++s) {
           if (lane == s) rec = make_float4(wgt[s], c1[s], c2[s], 0.f);
         }
-        if (lane < S - 1) stg<float4>(P.coef + ((uint64_t)t * (S - 1) + (uint32_t)lane) * 4, rec);
+        char* crow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.coef) + (uint64_t)t * ((S - 1) * 16)));
+        // lanes >= S-1 fall outside the resource's range: their stores are dropped
+        st_row_nt(row_rsrc(crow, (uint32_t)((S - 1) * 16)), lane_off,
+                  u32x4{as_u32(rec.x), as_u32(rec.y), as_u32(rec.z), as_u32(rec.w)});
       }
 
       // ---- the gradient rows, one whole row per source ----
@@ -2243,7 +2285,13 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
           float q[8];
-          qw_chunk(c, q);
+          if constexpr (DEFER) {
+            const u32x4 qp = qp_chunk(c);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) q[2 * w] = bf_lo(qp[w]), q[2 * w + 1] = bf_hi(qp[w]);
+          } else {
+            qw_chunk(c, q);
+          }
           u32x4 pk;
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
@@ -2259,7 +2307,8 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
             }
             pk[w] = pack_bf16(d0, d1);
           }
-          st_row(dr, lane_off + (uint32_t)(c * 1024), pk);
+          if constexpr (DEFER) st_row_nt(dr, lane_off + (uint32_t)(c * 1024), pk);
+          else st_row(dr, lane_off + (uint32_t)(c * 1024), pk);
         }
       }
       t += nw;
@@ -2303,7 +2352,8 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
 // its coefficient record, its folded query q_j (read by every row: it stays
 // in L2) and its output-gradient row G_j; then the block's row x; then the
 // addend row (an empty buffer resource when there is none: its loads return
-// 0 without a memory access).  fp32 accumulators, one rounding at the store.
+// 0 without a memory access).  fp32 accumulators, one rounding at the store;
+// finished rows are stored at once or staged in LDS and stored in bursts.
 __device__ __forceinline__ u32x4 ld_row_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);  // nt: read once
 }
@@ -2366,6 +2416,13 @@ __device__ __forceinline__ void route_bwd_gather_body(const attnres_route_bwd_ga
     for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
   }
   float csum = 0.f;
+  // Finished rows staged in dynamic LDS, P.out_batch per wave ([row][chunk][lane],
+  // 16 bytes per lane: no bank conflicts; a wave reads back only what its own
+  // lanes wrote, so no barrier), stored in bursts between the reads.
+  extern __shared__ u32x4 gather_stage[];
+  const uint32_t batch = (uint32_t)P.out_batch;
+  u32x4* my_stage = gather_stage + (size_t)wave * batch * NCH * 64 + lane;
+  uint32_t nheld = 0, jfirst = 0;
   // item (j, r) of the wave's rows; (j, r) wave-uniform, passed by value
   auto process = [&](u32x4(&row)[NCH], u32x4(&q)[NCH], const u32x4& cf, uint32_t j, uint32_t r) {
     float a, b;
@@ -2386,15 +2443,42 @@ __device__ __forceinline__ void route_bwd_gather_body(const attnres_route_bwd_ga
       }
     }
     if (r == per - 1) {
-      const uint64_t t = tok0 + (uint64_t)j * nw;
-      char* orow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.out) + t * (uint64_t)P.out_ld * 2));
-      const __amdgpu_buffer_rsrc_t ro = row_rsrc(orow, RB);
+      if (batch > 1) {
+        // stage the row; the wave's rows are stored together when `batch`
+        // are held or at its last row
+        if (nheld == 0) jfirst = j;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          u32x4 pk;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) pk[w] = pack_bf16(acc[c][2 * w], acc[c][2 * w + 1]);
+          my_stage[(nheld * NCH + c) * 64] = pk;
+        }
+        nheld = __builtin_amdgcn_readfirstlane(nheld + 1);
+        if (nheld == batch || j + 1 == rows) {
+          for (uint32_t h = 0; h < nheld; ++h) {
+            const uint64_t t = tok0 + (uint64_t)(jfirst + h) * nw;
+            char* orow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.out) + t * (uint64_t)P.out_ld * 2));
+            const __amdgpu_buffer_rsrc_t ro = row_rsrc(orow, RB);
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) st_row_nt(ro, lane_off + (uint32_t)(c * 1024), my_stage[(h * NCH + c) * 64]);
+          }
+          nheld = 0;
+        }
+      } else {
+        const uint64_t t = tok0 + (uint64_t)j * nw;
+        char* orow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.out) + t * (uint64_t)P.out_ld * 2));
+        const __amdgpu_buffer_rsrc_t ro = row_rsrc(orow, RB);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          u32x4 pk;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) pk[w] = pack_bf16(acc[c][2 * w], acc[c][2 * w + 1]);
+          st_row_nt(ro, lane_off + (uint32_t)(c * 1024), pk);
+        }
+      }
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
-        u32x4 pk;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) pk[w] = pack_bf16(acc[c][2 * w], acc[c][2 * w + 1]);
-        st_row(ro, lane_off + (uint32_t)(c * 1024), pk);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
       }

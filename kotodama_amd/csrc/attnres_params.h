@@ -127,9 +127,10 @@ typedef struct attnres_route_bwd_gather_params {
   int64_t gout_ld;
   int64_t out_ld;
   int32_t d;
-  int32_t num_terms;   /* 1 .. ATTNRES_GATHER_MAX_TERMS */
+  int32_t num_terms;   /* 0 .. ATTNRES_GATHER_MAX_TERMS */
   int32_t block;       /* threads per workgroup */
-  int32_t pad;
+  int32_t out_batch;   /* finished rows each wave stages in (dynamic) LDS and stores
+                          together; 1 = store each row at once */
   attnres_gather_term term[ATTNRES_GATHER_MAX_TERMS];
 } attnres_route_bwd_gather_params;
 

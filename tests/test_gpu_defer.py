@@ -6,9 +6,9 @@ and committed source s, the record (w_s, c1_s, c2_s, 0) with which
 dL/dsource_s = w_s G + c1_s qfold + c2_s x_s, plus the folded query.
 ``attnres_route_bwd_gather`` sums one block's gradient over the calls that
 read it from those records.  Checked through the C ABI:
-* the partial's gradient, the query and gain gradients bit-identical to the
-  ``_add`` row-per-wave kernel on the same inputs, and the partial's gradient
-  at the backward bar against the float64 oracle;
+* the partial's gradient and the query and gain gradients at the backward
+  bar against the float64 oracle, and within a bf16 ulp of the ``_add``
+  row-per-wave kernel on the same inputs;
 * the folded query equal to the oracle's fold; each committed source's
   gradient rebuilt in float64 from its records against the oracle's;
 * the gather of several calls' terms (different source counts and source
@@ -85,12 +85,17 @@ def test_defer_matches_add_kernel_and_oracle(gpu, S, n, d):
         dq1, dg1 = _call(gpu, src, q, gain, gout, grads, [None] * (S - 1) + [addend[S - 1]])
     finally:
         _capi.set_kernel_policy(prev)
-    assert torch.equal(gp, grads[S - 1]), "partial's gradient differs from the _add kernel"
-    assert torch.equal(dq, dq1) and torch.equal(dg, dg1), "query / gain gradients differ from the _add kernel"
     qw = O.fold_query(np64(q), np64(gain), "bf16")
     assert np.array_equal(np64(qfold), qw), "folded query"
     ref = O.route_backward(np64(src), qw, 1e-5, np64(gout), None)
     check_grad(gp, ref["dx"][S - 1] + np64(addend[S - 1]), torch.bfloat16, "partial + addend")
+    check_grad(dq, ref["dqw"] * np64(gain), torch.bfloat16, "dquery")
+    check_grad(dg, ref["dqw"] * np64(q), torch.bfloat16, "dgain")
+    # the _add kernel forms x.qw with fp32 products, this one on v_dot2: the
+    # two agree to a bf16 ulp on the partial's gradient and the parameter ones
+    for a, b, name in ((gp, grads[S - 1], "partial"), (dq, dq1, "dquery"), (dg, dg1, "dgain")):
+        diff = (a.float() - b.float()).abs()
+        assert (diff <= b.float().abs() * 2.0**-7 + 1e-3 * b.float().abs().max()).all(), f"{name} vs the _add kernel"
     c = coef.double().cpu().numpy()
     assert (c[..., 3] == 0).all(), "record padding"
     G = np64(gout)
