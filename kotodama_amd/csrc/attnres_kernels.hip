@@ -189,9 +189,9 @@ __device__ __forceinline__ void st_row(__amdgpu_buffer_rsrc_t r, uint32_t off, u
 __device__ __forceinline__ void st_row(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, ATTNRES_STORE_CPOL);
 }
-// Non-temporal stores: the deferred backward and its gradient sums, whose
-// stores come one row per token between many reads, ran 2-3% faster with
-// them in the training step (the routing forward kernels 1.5-9% slower).
+// Non-temporal stores: the routing backward kernels (the 3B backward sweep
+// 2.4% faster, the 8B one 0.5%) and the deferred gradient sums (2-3% in the
+// training step) measured faster with them; the forward kernels 1.5-9% slower.
 __device__ __forceinline__ void st_row_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 2);
 }
@@ -1968,11 +1968,12 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
           for (int e = 0; e < VEC; ++e) dx[e] += C::elem(ad, e);
         }
         if constexpr (BF16) {
-          st_row(drsrc, (uint32_t)chunk[k] * 16,
-                 u32x4{pack_bf16(dx[0], dx[1]), pack_bf16(dx[2], dx[3]), pack_bf16(dx[4], dx[5]),
-                       pack_bf16(dx[6], dx[7])});
+          st_row_nt(drsrc, (uint32_t)chunk[k] * 16,
+                    u32x4{pack_bf16(dx[0], dx[1]), pack_bf16(dx[2], dx[3]), pack_bf16(dx[4], dx[5]),
+                          pack_bf16(dx[6], dx[7])});
         } else {
-          st_row(drsrc, (uint32_t)chunk[k] * 16, u32x4{as_u32(dx[0]), as_u32(dx[1]), as_u32(dx[2]), as_u32(dx[3])});
+          st_row_nt(drsrc, (uint32_t)chunk[k] * 16,
+                    u32x4{as_u32(dx[0]), as_u32(dx[1]), as_u32(dx[2]), as_u32(dx[3])});
         }
       }
       if constexpr (DQW_LDS) {
@@ -2307,8 +2308,7 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
             }
             pk[w] = pack_bf16(d0, d1);
           }
-          if constexpr (DEFER) st_row_nt(dr, lane_off + (uint32_t)(c * 1024), pk);
-          else st_row(dr, lane_off + (uint32_t)(c * 1024), pk);
+          st_row_nt(dr, lane_off + (uint32_t)(c * 1024), pk);
         }
       }
       t += nw;
