@@ -190,10 +190,16 @@ __device__ __forceinline__ void st_row(__amdgpu_buffer_rsrc_t r, uint32_t off, u
   __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, ATTNRES_STORE_CPOL);
 }
 // Non-temporal stores: the routing backward kernels (the 3B backward sweep
-// 2.4% faster, the 8B one 0.5%) and the deferred gradient sums (2-3% in the
-// training step) measured faster with them; the forward kernels 1.5-9% slower.
+// 2.4% faster, the 8B one 0.5%), the serving backward (merge and batched
+// backward, 2.4%), the arena's fused block steps (2%) and the deferred
+// gradient sums (2-3% in the training step) measured faster with them; the
+// list and batched-query forward kernels and the fused step writing its
+// partial to a new buffer 1.5-9% slower.
 __device__ __forceinline__ void st_row_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 2);
+}
+__device__ __forceinline__ void st_row_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 2);
 }
 
 template <typename T>
@@ -1439,6 +1445,9 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
   // partial write-back is a second write stream; staging measured slower
   // there) and carry no staging code.
   const uint32_t batch = (uint32_t)P.out_batch;
+  // the arena's fused block steps (the partial written back in place) store
+  // non-temporally; a fused step writing its partial to a new buffer does not
+  const bool nt_st = FUSED && P.partial_out == nullptr;
   extern __shared__ u32x4 stream_stage[];
   constexpr uint32_t STAGE_ROW = NCH * OPC * 64 * OPB;     // bytes of one staged row
   auto stage_row = [&](uint32_t b) {
@@ -1519,7 +1528,10 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
         char* prow = const_cast<char*>(uniform_ptr(pbase + (uint64_t)t * row_bytes));
         const __amdgpu_buffer_rsrc_t prsrc = row_rsrc(prow, (uint32_t)(NCH * 1024));
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) st_row(prsrc, (uint32_t)(c * 1024 + lane * 16), x[c]);
+        for (int c = 0; c < NCH; ++c) {
+          if (nt_st) st_row_nt(prsrc, (uint32_t)(c * 1024 + lane * 16), x[c]);
+          else st_row(prsrc, (uint32_t)(c * 1024 + lane * 16), x[c]);
+        }
       }
     }
 
@@ -1652,8 +1664,13 @@ __device__ __forceinline__ void stream_body(const attnres_route_params& P) {
 #pragma unroll
           for (int h = 0; h < OPC; ++h) {
             const uint32_t off = lane_ob + (uint32_t)(c * 64 * VEC * OES + 16 * h);
-            if constexpr (OPB == 16) st_row(orsrc, off, pk[c][h]);
-            else st_row(orsrc, off, u32x2{pk[c][h][0], pk[c][h][1]});
+            if (nt_st) {
+              if constexpr (OPB == 16) st_row_nt(orsrc, off, pk[c][h]);
+              else st_row_nt(orsrc, off, u32x2{pk[c][h][0], pk[c][h][1]});
+            } else {
+              if constexpr (OPB == 16) st_row(orsrc, off, pk[c][h]);
+              else st_row(orsrc, off, u32x2{pk[c][h][0], pk[c][h][1]});
+            }
           }
         }
       }
@@ -2736,11 +2753,11 @@ __device__ __forceinline__ void route_bwd_mq_body(const attnres_route_bwd_mq_par
 #pragma unroll
         for (int e = 0; e < VEC; ++e) dx[e] = __builtin_fmaf(c2, C::elem(x[s][k], e), acc[s][k][e]);
         if constexpr (BF16) {
-          st_row(drs, (uint32_t)chunk[k] * 16,
+          st_row_nt(drs, (uint32_t)chunk[k] * 16,
                  u32x4{pack_bf16(dx[0], dx[1]), pack_bf16(dx[2], dx[3]), pack_bf16(dx[4], dx[5]),
                        pack_bf16(dx[6], dx[7])});
         } else {
-          st_row(drs, (uint32_t)chunk[k] * 16, u32x4{as_u32(dx[0]), as_u32(dx[1]), as_u32(dx[2]), as_u32(dx[3])});
+          st_row_nt(drs, (uint32_t)chunk[k] * 16, u32x4{as_u32(dx[0]), as_u32(dx[1]), as_u32(dx[2]), as_u32(dx[3])});
         }
       }
     }
@@ -3018,7 +3035,7 @@ __device__ __forceinline__ void route_bwd_mqg_body(const attnres_route_bwd_mq_pa
           const int s = 4 * ks + i;
           if (s >= S) break;
           char* drow = reinterpret_cast<char*>(P.dsrc[s]) + tok * P.dsrc_ld * 2;
-          st_row(row_rsrc(drow, row_bytes), (uint32_t)chunk[k] * 16,
+          st_row_nt(row_rsrc(drow, row_bytes), (uint32_t)chunk[k] * 16,
                  u32x4{packed[i][0], packed[i][1], packed[i][2], packed[i][3]});
         }
       }
@@ -3267,16 +3284,16 @@ template <bool BF, int VEC>
 __device__ __forceinline__ void store_f32_chunk(__amdgpu_buffer_rsrc_t r, int chunk, const float (&o)[VEC]) {
   if constexpr (BF) {
     if constexpr (VEC == 8) {
-      st_row(r, (uint32_t)chunk * 16,
-             u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])});
+      st_row_nt(r, (uint32_t)chunk * 16,
+                u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])});
     } else {
-      st_row(r, (uint32_t)chunk * 8, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
+      st_row_nt(r, (uint32_t)chunk * 8, u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])});
     }
   } else {
 #pragma unroll
     for (int h = 0; h < VEC / 4; ++h)
-      st_row(r, (uint32_t)(chunk * VEC + 4 * h) * 4,
-             u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]), as_u32(o[4 * h + 2]), as_u32(o[4 * h + 3])});
+      st_row_nt(r, (uint32_t)(chunk * VEC + 4 * h) * 4,
+                u32x4{as_u32(o[4 * h]), as_u32(o[4 * h + 1]), as_u32(o[4 * h + 2]), as_u32(o[4 * h + 3])});
   }
 }
 
