@@ -544,13 +544,29 @@ def test_random_training_points(gpu, seed):
     # dX = dx1_X + dx2_X + Gp (the second call's gradient of the partial output
     # is the first's addend), returned for both partial and delta; query and gain
     # gradients of each call
-    rng = np.random.default_rng(11000 + seed)
-    dtype = [torch.bfloat16, torch.float32][int(rng.integers(2))]
-    K = int(rng.integers(0, 9))
-    vec = 8 if dtype == torch.bfloat16 else 4
-    D = vec * int(rng.integers(8, (4096 if dtype == torch.bfloat16 else 2048) // vec + 1))
-    if rng.integers(2):  # half the cases on widths the row-per-wave kernels take
-        D = (512 if dtype == torch.bfloat16 else 256) * int(rng.integers(1, 9))
+    _training_points_case(gpu, seed, deferred=False)
+
+
+@pytest.mark.parametrize("seed", range(SEEDS or 8))
+def test_random_deferred_training_points(gpu, seed):
+    # the same two points where the committed blocks' gradients are deferred
+    # (attnres_route_bwd_defer per point, attnres_route_bwd_gather at each
+    # block's commit node): bf16 at hidden 3072 (1..7 blocks) or 4096 (1..8)
+    _training_points_case(gpu, seed, deferred=True)
+
+
+def _training_points_case(gpu, seed, deferred):
+    rng = np.random.default_rng((21000 if deferred else 11000) + seed)
+    dtype = torch.bfloat16 if deferred else [torch.bfloat16, torch.float32][int(rng.integers(2))]
+    if deferred:
+        D = [3072, 4096][int(rng.integers(2))]
+        K = int(rng.integers(1, 8 if D == 3072 else 9))
+    else:
+        K = int(rng.integers(0, 9))
+        vec = 8 if dtype == torch.bfloat16 else 4
+        D = vec * int(rng.integers(8, (4096 if dtype == torch.bfloat16 else 2048) // vec + 1))
+        if rng.integers(2):  # half the cases on widths the row-per-wave kernels take
+            D = (512 if dtype == torch.bfloat16 else 256) * int(rng.integers(1, 9))
     N = _rows(rng, (K + 3) * D)
     with_delta = bool(rng.integers(2))
     with_gain = bool(rng.integers(2))
@@ -582,7 +598,21 @@ def test_random_training_points(gpu, seed):
         torch.cuda.synchronize()
         return h1, h2, X
 
-    h1, h2, X = _with_policy(pol, run)
+    deferred_calls = []
+    real = ops._route_rows_backward_defer
+
+    def counting(*a, **k):
+        r = real(*a, **k)
+        deferred_calls.append(r is not None)
+        return r
+
+    ops._route_rows_backward_defer = counting
+    try:
+        h1, h2, X = _with_policy(pol, run)
+    finally:
+        ops._route_rows_backward_defer = real
+    if deferred:
+        assert deferred_calls == [True, True], f"seed {seed}: the points did not defer ({deferred_calls})"
     pd = "bf16" if dtype == torch.bfloat16 else "f32"
     Xref = np64(partial) + np64(delta) if with_delta else np64(partial)
     Xref = O.bf16_round(Xref).astype(np.float64) if dtype == torch.bfloat16 else Xref.astype(np.float32).astype(np.float64)
