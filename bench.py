@@ -666,6 +666,35 @@ def bench_mall(steps: int, warmup: int, dev) -> dict:
     return out
 
 
+def train_path_bytes(w) -> tuple[int, int]:
+    """Algorithmic bytes per step of the kernels the eager training loop runs at
+    ``w``'s schedule (bf16, hidden 3072 / 4096: the deferred backward), in rows of
+    tokens * hidden * 2 bytes and 16-byte coefficient records per token and
+    committed source.  Forward: a point that updates the partial reads S - 1
+    blocks, the partial and the sublayer output and writes the new partial and
+    the routed row; the first point and a point after a commit read S and write
+    one.  Backward: a point with committed blocks reads its S sources, dL/dout
+    and the next point's partial gradient (none at the last point), writes the
+    partial's gradient and its records; the first point (S = 1) the same with
+    its one gradient row; each block's sum reads the dL/dout rows and records of
+    its P readers and the block's row, and writes its gradient."""
+    sched = w.schedule
+    S, C = list(sched.active_counts), list(sched.commit_before)
+    P = len(S)
+    row = w.tokens * w.hidden * w.elem_bytes
+    rec = w.tokens * 16
+    fwd = bwd = 0
+    for j in range(P):
+        fwd += (S[j] + 1) * row if (j == 0 or C[j]) else (S[j] + 3) * row
+        add = 1 if j < P - 1 else 0
+        bwd += (S[j] + 2 + add) * row + ((S[j] - 1) * rec if S[j] >= 2 else 0)
+    for j in range(P):
+        if C[j]:
+            terms = P - j
+            bwd += (terms + 2) * row + terms * rec
+    return fwd, bwd
+
+
 def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool) -> dict:
     """cfg2train: the reference's training step on the routing path at the 3B shape.
 
@@ -727,9 +756,16 @@ def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool) -> d
     fwd_rows = sum(s + 1 for s in w.calls)
     bwd_rows = sum(2 * s + 1 for s in w.calls)
     ms = elapsed * 1e3 / steps
+    extra = {}
+    if variant == "list" and not compiled:
+        # what the eager list path's kernels move (fused forward points, deferred backward + per-block sums)
+        fb, bb = train_path_bytes(w)
+        extra = {"path_kernel_bytes": {"fwd": fb, "bwd": bb},
+                 "path_kernel_GB/s": {"fwd": round(fb / (fwd_ms * 1e-3) / 1e9, 1),
+                                      "bwd": round(bb / (bwd_ms * 1e-3) / 1e9, 1)}}
     return {"ms_per_step": round(ms, 4), "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
             "routing_kernel_bytes": {"fwd": fwd_rows * row, "bwd": bwd_rows * row},
-            "routing_kernel_bytes_per_ms": round((fwd_rows + bwd_rows) * row / ms / 1e6, 1),
+            "routing_kernel_bytes_per_ms": round((fwd_rows + bwd_rows) * row / ms / 1e6, 1), **extra,
             "tokens_per_s": round(w.tokens / (ms * 1e-3), 1),
             "peak_allocated_GiB": round(torch.cuda.max_memory_allocated(dev) / 2**30, 2),
             "warmup_s": round(first_s, 2)}
