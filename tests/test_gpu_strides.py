@@ -8,7 +8,8 @@ float64 oracle and that no byte outside the rows was written.  The cases cover
 every kernel family the host can pick: the row-per-workgroup kernel (few rows),
 the streaming kernel (both its base+stride and pointer-table addressing), the
 batched-query kernel (bf16 queries) and the per-query kernel (fp32 queries),
-bf16 and fp32.  Tolerances as in test_gpu_parity / test_gpu_backward.
+bf16 and fp32; and the training loop's deferred backward and per-block sum.
+Tolerances as in test_gpu_parity / test_gpu_backward.
 """
 
 import ctypes
@@ -161,3 +162,58 @@ def _route_bwd_strided(gpu, sdt, S, n, d):
     tq = 1e-4 * np.abs(dqr) + 1e-5 * np.abs(dqr).max() if qdt == torch.float32 else \
         bf16_ulp(dqr) + 1e-3 * np.abs(dqr).max()
     assert (np.abs(np64(dq) - dqr) <= tq).all(), "query gradient"
+
+
+@pytest.mark.parametrize("S,n,d", [(3, 777, 3072), (9, 515, 4096)])
+def test_route_bwd_defer_and_gather_row_strides(gpu, S, n, d):
+    # attnres_route_bwd_defer over padded source, dL/dout and gradient rows, with
+    # dL/dlse; then attnres_route_bwd_gather of source 0's gradient from that
+    # call's records over a padded block row and padded output rows: every
+    # result against the oracle, no byte of the padding written
+    print(f"route_bwd_defer + gather strided S={S} n={n} d={d}", flush=True)
+    bf = torch.bfloat16
+    src_ld, gout_ld, grad_ld = d + 64, d + 128, d + 32
+    g = torch.Generator(device=gpu).manual_seed(S * 13 + n)
+    big = torch.full((S, n, src_ld), CANARY, device=gpu, dtype=bf)
+    for s in range(S):
+        big[s, :, :d] = (torch.randn((n, d), generator=g, device=gpu) * (0.5 + 0.3 * s)).to(bf)
+    q = (torch.randn(d, generator=g, device=gpu) * 0.05).to(bf)
+    gain = (1 + 0.1 * torch.randn(d, generator=g, device=gpu)).to(bf)
+    gbuf = torch.full((n, gout_ld), CANARY, device=gpu, dtype=bf)
+    gbuf[:, :d] = torch.randn((n, d), generator=g, device=gpu).to(bf)
+    glse = torch.randn(n, generator=g, device=gpu) * 0.1
+    gpart = torch.full((n, grad_ld), CANARY, device=gpu, dtype=bf)
+    add = torch.full((n, grad_ld), CANARY, device=gpu, dtype=bf)
+    add[:, :d] = (torch.randn((n, d), generator=g, device=gpu) * 0.01).to(bf)
+    coef = torch.full((n, S - 1, 4), float("nan"), device=gpu)
+    qfold = torch.empty(d, device=gpu, dtype=bf)
+    ws = torch.empty(_capi.route_bwd_workspace_size(n, d) // 4, device=gpu)
+    dq = torch.empty(d, device=gpu, dtype=bf)
+    st = torch.cuda.current_stream(gpu).cuda_stream
+    rc = _capi.route_bwd_defer(
+        _capi.pointer_array([big[s].data_ptr() for s in range(S)]), S, n, d, src_ld, _capi.DTYPE_BF16, q.data_ptr(),
+        gain.data_ptr(), _capi.DTYPE_BF16, 1e-5, gbuf.data_ptr(), _capi.DTYPE_BF16, gout_ld, glse.data_ptr(),
+        gpart.data_ptr(), add.data_ptr(), grad_ld, coef.data_ptr(), qfold.data_ptr(), ws.data_ptr(), ws.numel() * 4,
+        dq.data_ptr(), None, st)
+    _capi.check("attnres_route_bwd_defer", rc)
+    torch.cuda.synchronize()
+    qw = O.fold_query(np64(q), np64(gain), "bf16")
+    ref = O.route_backward(np64(big[:, :, :d]), qw, 1e-5, np64(gbuf[:, :d]), np64(glse))
+    want = ref["dx"][S - 1] + np64(add[:, :d])
+    err = np.abs(np64(gpart[:, :d]) - want)
+    assert (err <= bf16_ulp(want) + 1e-3 * np.abs(want).max()).all(), f"partial gradient worst err {err.max():.3e}"
+    assert torch.all(gpart[:, d:] == CANARY), "partial gradient row padding written"
+    dqr = ref["dqw"] * np64(gain)
+    assert (np.abs(np64(dq) - dqr) <= bf16_ulp(dqr) + 1e-3 * np.abs(dqr).max()).all(), "query gradient"
+    assert not torch.isnan(coef).any(), "a record was not written"
+    # gather source 0's gradient from this call (one term) onto padded output rows
+    out = torch.full((n, grad_ld), CANARY, device=gpu, dtype=bf)
+    _capi.route_bwd_gather(
+        big[0].data_ptr(), n, d, src_ld, _capi.DTYPE_BF16, 1, _capi.pointer_array([gbuf.data_ptr()]), gout_ld,
+        _capi.pointer_array([coef.data_ptr()]), _capi.int64_array([4 * (S - 1)]),
+        _capi.pointer_array([qfold.data_ptr()]), add.data_ptr(), out.data_ptr(), grad_ld, st)
+    torch.cuda.synchronize()
+    want0 = ref["dx"][0] + np64(add[:, :d])
+    err = np.abs(np64(out[:, :d]) - want0)
+    assert (err <= bf16_ulp(want0) + 1e-3 * np.abs(want0).max()).all(), f"gathered gradient worst err {err.max():.3e}"
+    assert torch.all(out[:, d:] == CANARY), "gathered gradient row padding written"
