@@ -310,6 +310,34 @@ int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int6
                              const int64_t* coef_lds, const void* const* qfolds, const void* addend, void* out,
                              int64_t out_ld, void* stream);
 
+/*
+ * The gradients of blocks 0 .. num_blocks-1 summed over one segment of the
+ * training loop: the num_terms calls of attnres_route_bwd_defer that read
+ * them all as sources 0 .. num_blocks-1 (every routing point between two
+ * commits), each call's grad_out row read once for all blocks.  For every
+ * token t and block k, with (w, c1, c2) = coefs[j][t*coef_lds[j] + 4*k + 0..2]
+ * (coefs[j] = call j's coef, coef_lds[j] = 4*(S_j - 1) >= 4*num_blocks):
+ *   sum_k  = part_in[k] + sum_j (w grad_outs[j] + c1 qfolds[j])   (bf16 rows)
+ *   csum_k = csum_in[k] + sum_j c2                                (fp32)
+ * Blocks k < num_blocks-1 store sum_k to part_out[k] and csum_k to
+ * csum_out[k] (their running sums for the next segment); the last block, the
+ * one whose commit ends the segment, stores its gradient
+ *   part_out[last] = sum + csum x + addend
+ * (x: its rows; addend NULL or rows of out_ld, may equal part_out[last]).
+ * part_in / csum_in (the arrays or entries) may be NULL for a block's first
+ * segment, or equal part_out / csum_out (in place).  More than 16 terms are
+ * launched in groups, the later ones continuing from part_out / csum_out
+ * (csum_out[last] is then needed as scratch).  bf16 rows of hidden 3072 or
+ * 4096, up to 8 blocks; other calls return ATTNRES_ERR_UNSUPPORTED.
+ *
+ * See attnres_route_bwd_defer for the reference code this replaces.
+ */
+int attnres_route_bwd_gather_seg(int num_blocks, int64_t num_tokens, int hidden, int dtype, int num_terms,
+                                 const void* const* grad_outs, int64_t grad_out_ld, const float* const* coefs,
+                                 const int64_t* coef_lds, const void* const* qfolds, const void* const* part_in,
+                                 const float* const* csum_in, void* const* part_out, float* const* csum_out,
+                                 const void* x, int64_t x_ld, const void* addend, int64_t out_ld, void* stream);
+
 /* Size of the device scratch array attnres_route_bwd_noalloc uses (32 MiB:
  * 256 CUs x 4 workgroups x 8192 fp32 columns, the largest workspace
  * attnres_route_bwd_workspace_size() reports on an MI355X). */

@@ -57,6 +57,7 @@ EXPORTS = (
     "attnres_route_bwd_add",
     "attnres_route_bwd_defer",
     "attnres_route_bwd_gather",
+    "attnres_route_bwd_gather_seg",
     "attnres_route_bwd_noalloc",
     "attnres_route_bwd_kernel_name",
     "attnres_route_bwd_queries_workspace_size",
@@ -270,6 +271,30 @@ _SIGNATURES = {
         ],
         _c_int,
     ),
+    "attnres_route_bwd_gather_seg": (
+        [
+            _c_int,  # num_blocks
+            _c_i64,  # num_tokens
+            _c_int,  # hidden
+            _c_int,  # dtype
+            _c_int,  # num_terms
+            ctypes.POINTER(_c_vp),  # grad_outs
+            _c_i64,  # grad_out_ld
+            ctypes.POINTER(_c_vp),  # coefs
+            ctypes.POINTER(_c_i64),  # coef_lds
+            ctypes.POINTER(_c_vp),  # qfolds
+            ctypes.POINTER(_c_vp),  # part_in
+            ctypes.POINTER(_c_vp),  # csum_in
+            ctypes.POINTER(_c_vp),  # part_out
+            ctypes.POINTER(_c_vp),  # csum_out
+            _c_vp,  # x
+            _c_i64,  # x_ld
+            _c_vp,  # addend
+            _c_i64,  # out_ld
+            _c_vp,  # stream
+        ],
+        _c_int,
+    ),
     "attnres_route_bwd_noalloc": (
         [
             ctypes.POINTER(_c_vp),  # sources
@@ -460,12 +485,19 @@ def route_bwd_gather(*args) -> None:
     check("attnres_route_bwd_gather", lib().attnres_route_bwd_gather(*args))
 
 
+def route_bwd_gather_seg(*args) -> None:
+    """attnres_route_bwd_gather_seg: one segment's terms summed into blocks 0 .. num_blocks-1."""
+    check("attnres_route_bwd_gather_seg", lib().attnres_route_bwd_gather_seg(*args))
+
+
 def route_bwd_noalloc(*args) -> None:
     """attnres_route_bwd without a workspace (the library's fixed scratch array)."""
     check("attnres_route_bwd_noalloc", lib().attnres_route_bwd_noalloc(*args))
 
 
 NOALLOC_SCRATCH_BYTES = 32 << 20  # ATTNRES_NOALLOC_SCRATCH_BYTES
+SEG_MAX_BLOCKS = 8  # ATTNRES_SEG_MAX_BLOCKS
+SEG_MAX_TERMS = 16  # ATTNRES_SEG_MAX_TERMS
 
 
 def route_bwd_queries_workspace_size(num_tokens: int, hidden: int, num_sources: int, num_queries: int) -> int:

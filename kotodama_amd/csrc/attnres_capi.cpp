@@ -115,6 +115,7 @@ struct DeviceState {
   KernelSlot bwd_mqg[2 * 9];     // batched-query backward on the matrix cores: query groups x S
   KernelSlot bwd_defer[2 * 10];  // row-per-wave backward with deferred block gradients: row KiB x S
   KernelSlot gather[2];          // their per-block sums: rows of 6 / 8 KiB
+  KernelSlot gather_seg[2 * ATTNRES_SEG_MAX_BLOCKS];  // segment sums: row KiB x blocks
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -437,6 +438,24 @@ int get_gather(DeviceState& st, int nch, hipFunction_t* f) {
   char name[96];
   snprintf(name, sizeof(name), "attnres_route_bwd_gather_c%d", nch);
   return slot_function(st, st.gather[nch == 8 ? 1 : 0], kDeferPart, name, f);
+}
+int get_gather_seg(DeviceState& st, int nch, int nb, hipFunction_t* f) {
+  char name[96];
+  snprintf(name, sizeof(name), "attnres_route_bwd_gather_seg_c%d_b%d", nch, nb);
+  return slot_function(st, st.gather_seg[(nch == 8 ? ATTNRES_SEG_MAX_BLOCKS : 0) + nb - 1], kDeferPart, name, f);
+}
+// Row parts per token of the segment kernel (each wave takes one) and the
+// waves per SIMD each instance is compiled for (workgroups per CU), as the
+// instances in attnres_kernels.hip.
+int gather_seg_parts(int nch, int nb) {
+  static const int cpw6[ATTNRES_SEG_MAX_BLOCKS] = {6, 3, 2, 2, 3, 1, 1, 1};
+  static const int cpw8[ATTNRES_SEG_MAX_BLOCKS] = {8, 4, 2, 2, 1, 1, 1, 1};
+  return nch / (nch == 8 ? cpw8[nb - 1] : cpw6[nb - 1]);
+}
+int gather_seg_per_cu(int nch, int nb) {
+  static const int wpe6[ATTNRES_SEG_MAX_BLOCKS] = {2, 2, 2, 2, 1, 2, 2, 2};
+  static const int wpe8[ATTNRES_SEG_MAX_BLOCKS] = {1, 1, 2, 2, 2, 2, 2, 1};
+  return nch == 8 ? wpe8[nb - 1] : wpe6[nb - 1];
 }
 // Row KiB of the deferred backward for this call, or 0 when it has no kernel
 // (bf16 sources, output gradients and parameters; rows of 6 KiB with S <= 8
@@ -1464,6 +1483,96 @@ int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int6
       P.term[j].coef_ld = coef_lds[j0 + j];
     }
     rc = launch(f, grid, 64 * kGatherWaves, P, stream, 1, lds);
+    if (rc != ATTNRES_OK) return rc;
+    j0 += nt;
+  } while (j0 < num_terms);
+  return ATTNRES_OK;
+}
+
+int attnres_route_bwd_gather_seg(int num_blocks, int64_t num_tokens, int hidden, int dtype, int num_terms,
+                                 const void* const* grad_outs, int64_t grad_out_ld, const float* const* coefs,
+                                 const int64_t* coef_lds, const void* const* qfolds, const void* const* part_in,
+                                 const float* const* csum_in, void* const* part_out, float* const* csum_out,
+                                 const void* x, int64_t x_ld, const void* addend, int64_t out_ld, void* stream) {
+  if (num_blocks < 1 || num_blocks > ATTNRES_SEG_MAX_BLOCKS)
+    return fail(ATTNRES_ERR_UNSUPPORTED, "segment sum: num_blocks=%d outside [1, %d]", num_blocks,
+                ATTNRES_SEG_MAX_BLOCKS);
+  if (num_terms < 1) return fail(ATTNRES_ERR_ARG, "segment sum: num_terms=%d < 1", num_terms);
+  if (grad_outs == nullptr || coefs == nullptr || coef_lds == nullptr || qfolds == nullptr || part_out == nullptr ||
+      x == nullptr)
+    return fail(ATTNRES_ERR_ARG, "segment sum: a required pointer array or x is NULL");
+  if (num_tokens < 0 || hidden <= 0) return fail(ATTNRES_ERR_ARG, "bad num_tokens/hidden");
+  if (!valid_dtype(dtype)) return fail(ATTNRES_ERR_ARG, "unknown dtype code");
+  if (dtype != ATTNRES_DTYPE_BF16 || (hidden != 3072 && hidden != 4096))
+    return fail(ATTNRES_ERR_UNSUPPORTED, "segment sum: bf16 rows of hidden 3072 or 4096 only (hidden=%d)", hidden);
+  if (x_ld < hidden || out_ld < hidden || grad_out_ld < hidden)
+    return fail(ATTNRES_ERR_ARG, "a row stride is smaller than hidden=%d", hidden);
+  if ((x_ld * 2) % 16 != 0 || (out_ld * 2) % 16 != 0 || (grad_out_ld * 2) % 16 != 0)
+    return fail(ATTNRES_ERR_ALIGN, "row strides not 16-byte aligned");
+  if (!aligned16(x) || (addend != nullptr && !aligned16(addend)))
+    return fail(ATTNRES_ERR_ALIGN, "x or addend not 16-byte aligned");
+  for (int j = 0; j < num_terms; ++j) {
+    if (grad_outs[j] == nullptr || coefs[j] == nullptr || qfolds[j] == nullptr)
+      return fail(ATTNRES_ERR_ARG, "term %d has a NULL pointer", j);
+    if (!aligned16(grad_outs[j]) || !aligned16(coefs[j]) || !aligned16(qfolds[j]))
+      return fail(ATTNRES_ERR_ALIGN, "term %d: grad_out, coef or qfold not 16-byte aligned", j);
+    if (coef_lds[j] < 4 * (int64_t)num_blocks || coef_lds[j] % 4 != 0)
+      return fail(ATTNRES_ERR_ARG, "term %d: coef_ld=%lld holds fewer than %d records", j, (long long)coef_lds[j],
+                  num_blocks);
+  }
+  for (int k = 0; k < num_blocks; ++k) {
+    if (part_out[k] == nullptr) return fail(ATTNRES_ERR_ARG, "part_out[%d] is NULL", k);
+    if (!aligned16(part_out[k]) || (part_in != nullptr && part_in[k] != nullptr && !aligned16(part_in[k])))
+      return fail(ATTNRES_ERR_ALIGN, "block %d: running sum rows not 16-byte aligned", k);
+    // the last block's csum_out carries its sum between launches of more than ATTNRES_SEG_MAX_TERMS terms
+    const bool need = k < num_blocks - 1 || num_terms > ATTNRES_SEG_MAX_TERMS;
+    if (need && (csum_out == nullptr || csum_out[k] == nullptr))
+      return fail(ATTNRES_ERR_ARG, "csum_out[%d] is NULL", k);
+  }
+  if (num_tokens == 0) return ATTNRES_OK;
+  const int nch = hidden / 512;
+  const int parts = gather_seg_parts(nch, num_blocks);
+  if (num_tokens * parts >= ((int64_t)1 << 31)) return fail(ATTNRES_ERR_UNSUPPORTED, "num_tokens too large");
+  DeviceState* st = nullptr;
+  int rc = ensure_loaded(&st);
+  if (rc != ATTNRES_OK) return rc;
+  hipFunction_t f = nullptr;
+  rc = get_gather_seg(*st, nch, num_blocks, &f);
+  if (rc != ATTNRES_OK) return rc;
+  const int per_cu = tuning().gather_per_cu > 0 ? tuning().gather_per_cu : gather_seg_per_cu(nch, num_blocks);
+  const int64_t need_wg = (num_tokens * parts + kGatherWaves - 1) / kGatherWaves;
+  const int64_t cap = (int64_t)st->num_cus * per_cu;
+  const int grid = (int)(need_wg < cap ? need_wg : cap);
+  attnres_route_bwd_gather_seg_params P;
+  int j0 = 0;
+  do {
+    const int nt = num_terms - j0 < ATTNRES_SEG_MAX_TERMS ? num_terms - j0 : ATTNRES_SEG_MAX_TERMS;
+    const bool last = j0 + nt == num_terms;
+    std::memset(&P, 0, sizeof(P));
+    P.x = x;
+    P.addend = addend;
+    P.n_tokens = num_tokens;
+    P.x_ld = x_ld;
+    P.gout_ld = grad_out_ld;
+    P.out_ld = out_ld;
+    P.d = hidden;
+    P.num_terms = nt;
+    P.block = 64 * kGatherWaves;
+    P.final_block = last ? 1 : 0;
+    for (int j = 0; j < nt; ++j) {
+      P.term[j].grad_out = grad_outs[j0 + j];
+      P.term[j].coef = coefs[j0 + j];
+      P.term[j].qfold = qfolds[j0 + j];
+      P.term[j].coef_ld = coef_lds[j0 + j];
+    }
+    for (int k = 0; k < num_blocks; ++k) {
+      // later launches continue from the running sums the earlier ones stored
+      P.blk[k].part_in = j0 == 0 ? (part_in != nullptr ? part_in[k] : nullptr) : part_out[k];
+      P.blk[k].csum_in = j0 == 0 ? (csum_in != nullptr ? csum_in[k] : nullptr) : csum_out[k];
+      P.blk[k].part_out = part_out[k];
+      P.blk[k].csum_out = csum_out != nullptr ? csum_out[k] : nullptr;
+    }
+    rc = launch(f, grid, 64 * kGatherWaves, P, stream, 1, 0);
     if (rc != ATTNRES_OK) return rc;
     j0 += nt;
   } while (j0 < num_terms);

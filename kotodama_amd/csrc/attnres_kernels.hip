@@ -2530,6 +2530,212 @@ __device__ __forceinline__ void route_bwd_gather_body(const attnres_route_bwd_ga
   }
 }
 
+// ------------------------------------------- segment of deferred sums --
+//
+// The gradients of blocks 0 .. NB-1 from the terms of the points that read
+// them all (the points between two commits), each point's dL/dout row read
+// once: a wave takes one part of a token row (CPW KiB of the NCH KiB; NB*CPW*8
+// fp32 accumulators per lane) and streams, through a two-slot pipeline (the
+// next item requested once the current one has arrived), per term its record
+// row (lane j: block j's (w, c1, c2)), its folded query part and its dL/dout
+// part, accumulating
+//   acc_j += w_pj G_p + c1_pj q_p,   cs_j += c2_pj   (cs wave-uniform)
+// for every block j; then per block its running sum part (empty buffer
+// resource without one), the block's sum stored (bf16, non-temporal) with
+// cs_j to csum_out; with P.final_block the last block instead takes its row
+// x and the addend in one more item and stores acc + cs x + addend.
+template <int NB, int NCH, int CPW>
+__device__ __forceinline__ void route_bwd_gather_seg_body(const attnres_route_bwd_gather_seg_params& P) {
+  static_assert(NCH % CPW == 0, "a row splits into whole parts");
+  constexpr uint32_t PARTS = NCH / CPW;
+  constexpr uint32_t PB = CPW * 1024;  // bytes of one part of a row
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t nwv = (uint32_t)P.block >> 6;
+  const uint32_t n_items = (uint32_t)P.n_tokens * PARTS;
+  const uint32_t nw = gridDim.x * nwv;
+  const uint32_t item0 = blockIdx.x * nwv + wave;
+  if (item0 >= n_items) return;
+  const uint32_t rows = (n_items - item0 - 1) / nw + 1;  // items of this wave
+  const uint32_t nt = (uint32_t)P.num_terms;
+  const bool fin = P.final_block != 0;
+  // terms, then one slot per block, then (final) the last block's x and addend
+  const uint32_t per = nt + NB + (fin ? 1u : 0u);
+  const uint32_t lane_off = (uint32_t)lane * 16;
+
+  // slot (j, r) of the wave's items: A and B row parts and a record row
+  auto issue = [&](u32x4(&a)[CPW], u32x4(&b)[CPW], u32x4& rec, uint32_t j, uint32_t r, uint32_t z) {
+    if (j >= rows) {
+      j = rows - 1;
+      r = per - 1;
+    }
+    j = __builtin_amdgcn_readfirstlane(j);
+    r = __builtin_amdgcn_readfirstlane(r);
+    const uint32_t item = item0 + j * nw;
+    const uint64_t t = item / PARTS;
+    const uint32_t h = item % PARTS;
+    char* abase = nullptr;
+    char* bbase = nullptr;
+    char* cbase = nullptr;
+    uint32_t abytes = 0, bbytes = 0;
+    if (r < nt) {
+      const attnres_gather_term& T = P.term[r];
+      abase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(T.grad_out) + t * (uint64_t)P.gout_ld * 2 + h * PB));
+      bbase = const_cast<char*>(static_cast<const char*>(T.qfold)) + h * PB;
+      cbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(T.coef) + t * (uint64_t)T.coef_ld * 4));
+      abytes = bbytes = PB;
+    } else if (r < nt + NB) {
+      // the block's running sum part and (in the record slot) its x-coefficient sum
+      const void* pin = P.blk[r - nt].part_in;
+      const float* cin = P.blk[r - nt].csum_in;
+      abase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(pin) + t * (uint64_t)P.out_ld * 2 + h * PB));
+      abytes = pin != nullptr ? PB : 0u;
+      char* cs_at = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(cin) + t * 4));
+      const __amdgpu_buffer_rsrc_t rcs = row_rsrc(cs_at, cin != nullptr ? 4u : 0u);
+      rec = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rcs, z, 0, 0), 0u, 0u, 0u};
+    } else {
+      abase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.x) + t * (uint64_t)P.x_ld * 2 + h * PB));
+      bbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.addend) + t * (uint64_t)P.out_ld * 2 + h * PB));
+      abytes = PB;
+      bbytes = P.addend != nullptr ? PB : 0u;
+    }
+    const __amdgpu_buffer_rsrc_t rc = row_rsrc(cbase, cbase != nullptr ? (uint32_t)(NB * 16) : 0u);
+    const __amdgpu_buffer_rsrc_t rb = row_rsrc(bbase, bbytes);
+    const __amdgpu_buffer_rsrc_t ra = row_rsrc(abase, abytes);
+    // records and the folded query first: rows return in order, so the A part's arrival implies theirs
+    if (r < nt) rec = __builtin_amdgcn_raw_buffer_load_b128(rc, lane_off + z, 0, 0);
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) b[c] = __builtin_amdgcn_raw_buffer_load_b128(rb, lane_off + (uint32_t)(c * 1024) + z, 0, 0);
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) a[c] = ld_row_nt(ra, lane_off + (uint32_t)(c * 1024) + z);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  float acc[NB][CPW][8];
+  float cs[NB];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    cs[k] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[k][c][e] = 0.f;
+    }
+  }
+  auto lane_f = [](uint32_t v, int l) { return as_f32(__builtin_amdgcn_readlane(v, l)); };
+  auto process = [&](u32x4(&a)[CPW], u32x4(&b)[CPW], const u32x4& rec, uint32_t j, uint32_t r) {
+    const uint32_t item = item0 + j * nw;
+    const uint64_t t = item / PARTS;
+    const uint32_t h = item % PARTS;
+    if (r < nt) {
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        const float w = lane_f(rec[0], k), c1 = lane_f(rec[1], k);
+        cs[k] += lane_f(rec[2], k);
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[k][c][2 * q] = __builtin_fmaf(w, bf_lo(a[c][q]), __builtin_fmaf(c1, bf_lo(b[c][q]), acc[k][c][2 * q]));
+            acc[k][c][2 * q + 1] =
+                __builtin_fmaf(w, bf_hi(a[c][q]), __builtin_fmaf(c1, bf_hi(b[c][q]), acc[k][c][2 * q + 1]));
+          }
+        }
+      }
+      return;
+    }
+    if (r < nt + NB) {
+      // block k's running sum from earlier segments (zeros without one)
+      const uint32_t kb = r - nt;
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        if ((uint32_t)k != kb) continue;
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[k][c][2 * q] += bf_lo(a[c][q]);
+            acc[k][c][2 * q + 1] += bf_hi(a[c][q]);
+          }
+        }
+        cs[k] += as_f32(__builtin_amdgcn_readfirstlane(rec[0]));  // 0 without a running sum
+        if (k < NB - 1 || !fin) {
+          char* orow = const_cast<char*>(
+              uniform_ptr(reinterpret_cast<uint64_t>(P.blk[k].part_out) + t * (uint64_t)P.out_ld * 2 + h * PB));
+          const __amdgpu_buffer_rsrc_t ro = row_rsrc(orow, PB);
+#pragma unroll
+          for (int c = 0; c < CPW; ++c) {
+            u32x4 pk;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) pk[q] = pack_bf16(acc[k][c][2 * q], acc[k][c][2 * q + 1]);
+            st_row_nt(ro, lane_off + (uint32_t)(c * 1024), pk);
+          }
+          if (h == 0 && lane == 0) P.blk[k].csum_out[t] = cs[k];
+#pragma unroll
+          for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[k][c][e] = 0.f;
+          }
+          cs[k] = 0.f;
+        }
+      }
+      return;
+    }
+    // the last block: + cs x + addend, stored as its gradient
+    constexpr int L = NB - 1;
+    const float cst = cs[L];
+    char* orow = const_cast<char*>(
+        uniform_ptr(reinterpret_cast<uint64_t>(P.blk[L].part_out) + t * (uint64_t)P.out_ld * 2 + h * PB));
+    const __amdgpu_buffer_rsrc_t ro = row_rsrc(orow, PB);
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      u32x4 pk;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float lo = __builtin_fmaf(cst, bf_lo(a[c][q]), acc[L][c][2 * q]) + bf_lo(b[c][q]);
+        const float hi = __builtin_fmaf(cst, bf_hi(a[c][q]), acc[L][c][2 * q + 1]) + bf_hi(b[c][q]);
+        pk[q] = pack_bf16(lo, hi);
+      }
+      st_row_nt(ro, lane_off + (uint32_t)(c * 1024), pk);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[L][c][e] = 0.f;
+    }
+    cs[L] = 0.f;
+  };
+  auto after = [per](uint32_t& j, uint32_t& r) {
+    const uint32_t r1 = r + 1;
+    const bool wrap = r1 == per;
+    r = __builtin_amdgcn_readfirstlane(wrap ? 0u : r1);
+    j = __builtin_amdgcn_readfirstlane(wrap ? j + 1 : j);
+  };
+
+  // A ring of DEPTH = PARTS + 1 slots: PARTS items in flight behind the one
+  // being processed, so a wave keeps about one whole row (NCH KiB) in flight
+  // whatever its part size (the next item is requested once the oldest in
+  // flight has arrived).
+  constexpr int DEPTH = (int)PARTS + 1;
+  u32x4 A[DEPTH][CPW], B[DEPTH][CPW], R[DEPTH];
+  uint32_t ji = 0, ri = 0, jp = 0, rp = 0;
+#pragma unroll
+  for (int u = 0; u < DEPTH - 1; ++u) {
+    issue(A[u], B[u], R[u], ji, ri, 0u);
+    after(ji, ri);
+  }
+  const uint32_t items = rows * per;
+  for (uint32_t i = 0; i < items; i += DEPTH) {
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) {
+      if (i + (uint32_t)u < items) {
+        const int nx = (u + DEPTH - 1) % DEPTH;  // the slot processed last, refilled now
+        issue(A[nx], B[nx], R[nx], ji, ri, arrival_zero(A[u][CPW - 1][3]));
+        after(ji, ri);
+        process(A[u], B[u], R[u], jp, rp);
+        after(jp, rp);
+      }
+    }
+  }
+}
+
 // ------------------------------------------- batched-query backward body --
 //
 // Backward of Q >= 2 queries over one set of sources (the batched phase-1
@@ -3972,4 +4178,23 @@ BWD_STREAM_ONE_DEFER(2, 8, 0) BWD_STREAM_ONE_DEFER(3, 8, 0) BWD_STREAM_ONE_DEFER
 BWD_STREAM_ONE_DEFER(5, 8, 0) BWD_STREAM_ONE_DEFER(6, 8, 0) BWD_STREAM_ONE_DEFER(7, 8, 1)
 BWD_STREAM_ONE_DEFER(8, 8, 2) BWD_STREAM_ONE_DEFER(9, 8, 3)
 GATHER_ONE(6) GATHER_ONE(8)
+#endif
+
+// Segments of deferred sums: attnres_route_bwd_gather_seg_c<NCH>_b<NB>, a wave
+// per CPW KiB part of a row, compiled for WPE waves per SIMD (the host runs
+// WPE workgroups per CU).  The kernels are bound by their NB*2 FMAs per
+// element and term: smaller parts at two waves per SIMD measured faster
+// (3 blocks: 0.79 -> 0.65 ms, 7 blocks: 1.52 -> 1.47 ms at the 3B shape)
+// except at 5 blocks (3 KiB parts, one wave: 1.09 against 1.23 ms); two-KiB
+// parts at two waves per SIMD spill from 5 blocks on.
+#define GATHER_SEG_ONE(NCH, NB, CPW, WPE)                                                               \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))          \
+      attnres_route_bwd_gather_seg_c##NCH##_b##NB(attnres_route_bwd_gather_seg_params P) {              \
+    route_bwd_gather_seg_body<NB, NCH, CPW>(P);                                                         \
+  }
+#if ATTNRES_PART == 10 || defined(ATTNRES_ALL_PARTS)
+GATHER_SEG_ONE(6, 1, 6, 2) GATHER_SEG_ONE(6, 2, 3, 2) GATHER_SEG_ONE(6, 3, 2, 2) GATHER_SEG_ONE(6, 4, 2, 2)
+GATHER_SEG_ONE(6, 5, 3, 1) GATHER_SEG_ONE(6, 6, 1, 2) GATHER_SEG_ONE(6, 7, 1, 2) GATHER_SEG_ONE(6, 8, 1, 2)
+GATHER_SEG_ONE(8, 1, 8, 1) GATHER_SEG_ONE(8, 2, 4, 1) GATHER_SEG_ONE(8, 3, 2, 2) GATHER_SEG_ONE(8, 4, 2, 2)
+GATHER_SEG_ONE(8, 5, 1, 2) GATHER_SEG_ONE(8, 6, 1, 2) GATHER_SEG_ONE(8, 7, 1, 2) GATHER_SEG_ONE(8, 8, 1, 1)
 #endif

@@ -135,6 +135,45 @@ typedef struct attnres_route_bwd_gather_params {
 } attnres_route_bwd_gather_params;
 
 /*
+ * One segment of the training loop's deferred gradients: the terms of the
+ * points that read blocks 0 .. NB-1 (every point between two commits), summed
+ * into each block's running gradient at once, so each point's dL/dout row is
+ * read once however many blocks it read.  For every token t and block j:
+ *   acc_j = part_in_j + sum_p (w_pj G_p + c1_pj qfold_p)      (bf16 rows)
+ *   cs_j  = csum_in_j + sum_p c2_pj                           (fp32 per token)
+ * with (w_pj, c1_pj, c2_pj) at term[p].coef + t*coef_ld + 4*j floats.  Blocks
+ * j < NB-1 store acc_j to part_out_j and cs_j to csum_out_j; the last block
+ * (the one whose commit this is) stores its gradient
+ *   part_out = acc + cs x + addend.
+ * part_in / csum_in may be NULL (no earlier segment) or equal part_out /
+ * csum_out (in place).
+ */
+#define ATTNRES_SEG_MAX_BLOCKS 8
+#define ATTNRES_SEG_MAX_TERMS 16
+typedef struct attnres_seg_block {
+  const void* part_in;   /* (n_tokens, d), row stride out_ld, or NULL */
+  const float* csum_in;  /* (n_tokens,), or NULL */
+  void* part_out;        /* (n_tokens, d), row stride out_ld */
+  float* csum_out;       /* (n_tokens,); unused for the last block */
+} attnres_seg_block;
+
+typedef struct attnres_route_bwd_gather_seg_params {
+  const void* x;       /* (n_tokens, d) rows of the last block, stride x_ld */
+  const void* addend;  /* (n_tokens, d), stride out_ld, or NULL: added to the last block's gradient */
+  int64_t n_tokens;
+  int64_t x_ld;
+  int64_t gout_ld;
+  int64_t out_ld;
+  int32_t d;
+  int32_t num_terms;   /* 1 .. ATTNRES_SEG_MAX_TERMS */
+  int32_t block;       /* threads per workgroup */
+  int32_t final_block; /* 1: the last block takes x and the addend and stores its gradient;
+                          0: it is stored like the others (running sum + csum_out) */
+  attnres_gather_term term[ATTNRES_SEG_MAX_TERMS];
+  attnres_seg_block blk[ATTNRES_SEG_MAX_BLOCKS];
+} attnres_route_bwd_gather_seg_params;
+
+/*
  * Backward of Q >= 2 queries over one set of sources (the batched phase-1
  * call), source gradients in one pass:
  *   dx_s = sum_q (w_qs G_q + c1_qs qw_q) + (sum_q c2_qs) x_s

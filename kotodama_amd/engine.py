@@ -167,6 +167,7 @@ def _route_points_autograd(model, embed: Tensor, sublayer: Callable[[int, Tensor
     """
     committed: list[Tensor] = []
     slots: list[ops.GradSlot] = []
+    segments = ops.GradSegments()  # the blocks' deferred gradients, summed segment by segment
     dt = embed.dtype
     fused = ops.accumulating_path_ok(embed)
     partial: Optional[Tensor] = embed
@@ -191,7 +192,7 @@ def _route_points_autograd(model, embed: Tensor, sublayer: Callable[[int, Tensor
         h = point(layer.attn_res_query, layer.attn_res_norm)
         if i in boundaries:
             if fused:
-                slot = ops.GradSlot()
+                slot = ops.GradSlot(segments)
                 committed.append(ops.commit_block(partial, slot))
                 slots.append(slot)
             else:

@@ -628,14 +628,19 @@ class GradSlot:
     read it during one backward pass: rows accumulated in place (``buf``,
     attnres_route_bwd_add) and deferred terms (``terms``: per call its output
     gradient, coefficient records and folded query, attnres_route_bwd_defer),
-    which the block's commit node sums in one pass (attnres_route_bwd_gather)."""
+    which the block's commit node sums in one pass (attnres_route_bwd_gather).
+    A slot that belongs to a ``GradSegments`` (the training loop's blocks in
+    commit order) has its deferred terms summed segment by segment there."""
 
-    __slots__ = ("buf", "task", "terms")
+    __slots__ = ("buf", "task", "terms", "seg")
 
-    def __init__(self) -> None:
+    def __init__(self, seg: Optional["GradSegments"] = None) -> None:
         self.buf: Optional[Tensor] = None
         self.task: Optional[int] = None
         self.terms: list = []
+        self.seg = seg
+        if seg is not None:
+            seg.slots.append(self)
 
     def _join(self) -> None:
         """Start over when this is a new backward pass (autograd graph task):
@@ -661,9 +666,105 @@ class GradSlot:
         self.terms.append((grad_out, coef, index, qfold))
 
     def take(self) -> tuple[Optional[Tensor], list]:
+        self._join()
         buf, terms = self.buf, self.terms
         self.buf, self.terms, self.task = None, [], None
         return buf, terms
+
+
+class GradSegments:
+    """The committed blocks of one training loop (their GradSlots in commit
+    order) and the deferred terms of the routing points whose backward ran
+    since the last commit node.  Those points read exactly the blocks committed
+    before them, 0 .. k, where k is the block whose commit node runs next; that
+    node sums their terms into every one of those blocks in one pass
+    (attnres_route_bwd_gather_seg: each point's dL/dout row read once), keeping
+    the running sums of blocks 0 .. k-1 (bf16 rows, fp32 per-token sums of the
+    x coefficient) for the later segments and finishing block k's gradient."""
+
+    __slots__ = ("slots", "task", "pending", "part", "csum")
+
+    def __init__(self) -> None:
+        self.slots: list[GradSlot] = []
+        self.task: Optional[int] = None
+        self.pending: list = []
+        self.part: dict = {}
+        self.csum: dict = {}
+
+    def _join(self) -> None:
+        task = torch._C._current_graph_task_id()
+        if self.task != task:
+            self.pending, self.part, self.csum, self.task = [], {}, {}, task
+
+    def add(self, slots: Sequence[Optional[GradSlot]], grad_out: Tensor, coef: Tensor, qfold: Tensor) -> bool:
+        """Keep one point's deferred term if it read blocks 0 .. len(slots)-1 of
+        this loop in order; False (nothing kept) otherwise."""
+        k = len(slots)
+        if k == 0 or k > len(self.slots) or any(a is not b for a, b in zip(slots, self.slots)):
+            return False
+        self._join()
+        self.pending.append((grad_out, coef, qfold, k))
+        return True
+
+    def flush(self, slot: GradSlot, x: Tensor, addend: Optional[Tensor]) -> Optional[Tensor]:
+        """At ``slot``'s commit node: the block's gradient (plus ``addend``) with
+        the pending terms summed into it and into the earlier blocks' running
+        sums; None when no term is pending for it (nothing done)."""
+        self._join()
+        if not self.pending:
+            return self._finish(slot, x, addend)
+        k = next(i for i, s in enumerate(self.slots) if s is slot)
+        terms, self.pending = self.pending, []
+        if any(n != k + 1 for _, _, _, n in terms) or k + 1 > _capi.SEG_MAX_BLOCKS:
+            # not one segment over blocks 0 .. k: per-block sums instead
+            for g, coef, qfold, n in terms:
+                for j in range(n):
+                    self.slots[j].defer(g, coef, j, qfold)
+            return self._finish(slot, x, addend)
+        d = x.shape[-1]
+        n_tok = x.numel() // d
+        nb = k + 1
+        part_in = [self.part.get(j) for j in range(nb)]
+        csum_in = [self.csum.get(j) for j in range(nb)]
+        part_out = [p if p is not None else torch.empty((n_tok, d), device=x.device, dtype=x.dtype)
+                    for p in part_in[:k]]
+        csum_out = [c if c is not None else torch.empty(n_tok, device=x.device, dtype=torch.float32)
+                    for c in csum_in[:k]]
+        out = addend if addend is not None else torch.empty(x.shape, device=x.device, dtype=x.dtype)
+        last_csum = torch.empty(n_tok, device=x.device, dtype=torch.float32) if len(terms) > _capi.SEG_MAX_TERMS \
+            else None
+        with _DeviceStream(x.device) as stream:
+            _capi.route_bwd_gather_seg(
+                nb, n_tok, d, dtype_code(x.dtype), len(terms),
+                _capi.pointer_array([g.data_ptr() for g, _, _, _ in terms]), d,
+                _capi.pointer_array([c.data_ptr() for _, c, _, _ in terms]),
+                _capi.int64_array([4 * c.shape[1] for _, c, _, _ in terms]),
+                _capi.pointer_array([q.data_ptr() for _, _, q, _ in terms]),
+                _capi.pointer_array([p.data_ptr() if p is not None else None for p in part_in]),
+                _capi.pointer_array([c.data_ptr() if c is not None else None for c in csum_in]),
+                _capi.pointer_array([p.data_ptr() for p in part_out] + [out.data_ptr()]),
+                _capi.pointer_array([c.data_ptr() for c in csum_out] + [last_csum.data_ptr() if last_csum is not None
+                                                                        else None]),
+                x.data_ptr(), d, addend.data_ptr() if addend is not None else None, d, stream,
+            )
+        for j in range(k):
+            self.part[j], self.csum[j] = part_out[j], csum_out[j]
+        self.part.pop(k, None)
+        self.csum.pop(k, None)
+        return out
+
+    def _finish(self, slot: GradSlot, x: Tensor, addend: Optional[Tensor]) -> Optional[Tensor]:
+        """A block whose last segment had no pending term: its running sum (if
+        any) plus ``addend``; None when it has neither."""
+        k = next(i for i, s in enumerate(self.slots) if s is slot)
+        part, csum = self.part.pop(k, None), self.csum.pop(k, None)
+        if part is None:
+            return None
+        # the running sum still lacks its x term: csum * x
+        out = part.float() + csum.view(*x.shape[:-1], 1) * x.float()
+        if addend is not None:
+            out += addend.float()
+        return out.to(x.dtype)
 
 
 def _gather_terms(x: Tensor, terms: list, addend: Optional[Tensor], out: Tensor) -> None:
@@ -701,14 +802,23 @@ class _Commit(torch.autograd.Function):
             acc.add_(grad)
         elif acc is None:
             acc = grad
-        if not terms:
+        seg = ctx.slot.seg
+        if not terms and (seg is None or (not seg.pending and not seg.part)):
             return acc, None
         (x,) = ctx.saved_tensors
         x = x if x.is_contiguous() else x.contiguous()
         if acc is not None and not acc.is_contiguous():
             acc = acc.contiguous()
-        # in place into our own buffer; a fresh tensor when the addend is autograd's
-        out = acc if (acc is not None and acc is not grad) else torch.empty(x.shape, device=x.device, dtype=x.dtype)
+        if acc is grad and acc is not None:
+            acc = acc.clone()  # written in place below; autograd's own gradient is left as it is
+        if seg is not None:
+            out = seg.flush(ctx.slot, x, acc)
+            if out is not None:
+                acc = out
+                _, terms = ctx.slot.take()  # a segment that fell back to per-block sums
+        if not terms:
+            return acc, None
+        out = acc if acc is not None else torch.empty(x.shape, device=x.device, dtype=x.dtype)
         _gather_terms(x, terms, acc, out)
         return out, None
 
@@ -848,9 +958,11 @@ class _RoutePoint(torch.autograd.Function):
             res = _route_rows_backward_defer(sources, query, gain, ctx.eps, g_out, g_partial)
             if res is not None:
                 gp, coef, qfold, g_rows, dq, dg = res
-                for s_idx, (slot, nd) in enumerate(zip(ctx.slots, com_need)):
-                    if nd:
-                        slot.defer(g_rows, coef, s_idx, qfold)
+                seg = ctx.slots[0].seg if ctx.slots[0] is not None else None
+                if not (seg is not None and all(com_need) and seg.add(ctx.slots, g_rows, coef, qfold)):
+                    for s_idx, (slot, nd) in enumerate(zip(ctx.slots, com_need)):
+                        if nd:
+                            slot.defer(g_rows, coef, s_idx, qfold)
                 return ((None, None, None, dq if need[3] else None, dg if (gain is not None and need[4]) else None,
                          gp if ctx.has_delta and need[5] else None) + (None,) * n_com
                         + (gp if need[6 + n_com] else None,))

@@ -39,6 +39,7 @@ C_TO_CTYPES = {
     "float*": ctypes.c_void_p, "const void* const*": ctypes.POINTER(ctypes.c_void_p),
     "void* const*": ctypes.POINTER(ctypes.c_void_p), "int64_t*": ctypes.POINTER(ctypes.c_int64),
     "const float* const*": ctypes.POINTER(ctypes.c_void_p), "const int64_t*": ctypes.POINTER(ctypes.c_int64),
+    "float* const*": ctypes.POINTER(ctypes.c_void_p),
 }
 
 

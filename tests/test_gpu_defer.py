@@ -256,3 +256,110 @@ def test_bf16_training_loop_with_deferred_gradients(gpu, d, bounds, max_s, monke
         assert e_ours <= bar, f"{name}: err {e_ours:.3e}, torch bf16 op sequence {e_tb:.3e}"
     print(f"deferred training loop d={d} S<={max_s}: {len(ratios)} gradients, error / torch-bf16 error: median "
           f"{float(np.median(ratios)):.2f}, max {max(ratios):.2f}", flush=True)
+
+
+def _gather_seg(gpu, nb, terms, part_in, csum_in, part_out, csum_out, x, addend, out):
+    """attnres_route_bwd_gather_seg over blocks 0 .. nb-1; terms: (grad_out, coef, qfold)."""
+    n, d = x.shape
+    _capi.route_bwd_gather_seg(
+        nb, n, d, BF, len(terms), _capi.pointer_array([g.data_ptr() for g, _, _ in terms]), d,
+        _capi.pointer_array([c.data_ptr() for _, c, _ in terms]), _capi.int64_array([4 * c.shape[1] for _, c, _ in terms]),
+        _capi.pointer_array([q.data_ptr() for _, _, q in terms]),
+        _capi.pointer_array([p.data_ptr() if p is not None else None for p in part_in]),
+        _capi.pointer_array([c.data_ptr() if c is not None else None for c in csum_in]),
+        _capi.pointer_array([p.data_ptr() for p in part_out] + [out.data_ptr()]),
+        _capi.pointer_array([c.data_ptr() for c in csum_out] + [None]),
+        x.data_ptr(), d, addend.data_ptr() if addend is not None else None, d,
+        torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize()
+
+
+# (blocks, points in the segment, rows, hidden)
+SEG_CASES = [(1, 3, 700, 3072), (3, 8, 1000, 3072), (7, 8, 513, 3072), (4, 5, 800, 4096), (8, 8, 300, 4096)]
+
+
+@pytest.mark.parametrize("nb,P,n,d", SEG_CASES, ids=[f"b{c[0]}-p{c[1]}-n{c[2]}-d{c[3]}" for c in SEG_CASES])
+def test_gather_seg_sums_a_segment(gpu, nb, P, n, d):
+    # P points, each routing blocks 0 .. nb-1 and a partial of its own
+    # (attnres_route_bwd_defer), then one attnres_route_bwd_gather_seg: blocks
+    # j < nb-1 continue from running sums (some with none), the last one is
+    # finished with its x term and an addend.  Each block's running sum and
+    # x-coefficient sum against the same sums formed in float64 from the
+    # records; the last block's gradient against the oracle
+    print(f"route_bwd_gather_seg blocks={nb} points={P} n={n} d={d}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(700 + nb * 10 + P)
+    blocks = [(torch.randn((n, d), generator=g, device=gpu) * (0.5 + 0.2 * j)).to(torch.bfloat16) for j in range(nb)]
+    terms, recs, grads = [], [], []
+    for p in range(P):
+        own = torch.randn((n, d), generator=g, device=gpu).to(torch.bfloat16)
+        q = (torch.randn(d, generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+        gain = (1 + 0.1 * torch.randn(d, generator=g, device=gpu)).to(torch.bfloat16)
+        gout = torch.randn((n, d), generator=g, device=gpu).to(torch.bfloat16)
+        _, coef, qfold, _, _ = _defer(gpu, blocks + [own], q, gain, gout)
+        terms.append((gout, coef, qfold))
+        ref = O.route_backward(np.stack([np64(t) for t in blocks + [own]]), O.fold_query(np64(q), np64(gain), "bf16"),
+                               1e-5, np64(gout), None)
+        grads.append(ref["dx"][:nb])
+        recs.append((coef.double().cpu().numpy(), np64(gout), np64(qfold)))
+    part_in = [None if j % 2 else (torch.randn((n, d), generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+               for j in range(nb)]
+    csum_in = [None if j % 2 else torch.randn(n, generator=g, device=gpu) * 0.01 for j in range(nb)]
+    part_out = [torch.full((n, d), 3.0, device=gpu, dtype=torch.bfloat16) for _ in range(nb - 1)]
+    csum_out = [torch.full((n,), float("nan"), device=gpu) for _ in range(nb - 1)]
+    addend = (torch.randn((n, d), generator=g, device=gpu) * 0.01).to(torch.bfloat16)
+    out = torch.full((n, d), 3.0, device=gpu, dtype=torch.bfloat16)
+    _gather_seg(gpu, nb, terms, part_in, csum_in, part_out, csum_out, blocks[-1], addend, out)
+    for j in range(nb - 1):
+        want = np.zeros((n, d)) if part_in[j] is None else np64(part_in[j])
+        wc = np.zeros(n) if csum_in[j] is None else np64(csum_in[j])
+        for c, G, qf in recs:
+            want = want + c[:, j, 0:1] * G + c[:, j, 1:2] * qf[None, :]
+            wc = wc + c[:, j, 2]
+        check_grad(part_out[j], want, torch.bfloat16, f"block {j} running sum")
+        err = np.abs(np64(csum_out[j]) - wc)
+        assert (err <= 1e-5 * np.abs(wc) + 1e-6 * np.abs(wc).max() + 1e-30).all(), f"block {j} x-coefficient sum"
+    last = nb - 1
+    want = sum(gr[last] for gr in grads) + np64(addend)
+    if part_in[last] is not None:
+        want = want + np64(part_in[last]) + np64(csum_in[last])[:, None] * np64(blocks[last])
+    check_grad(out, want, torch.bfloat16, "last block's gradient")
+
+
+def test_gather_seg_more_terms_than_one_launch(gpu):
+    # 20 points over 2 blocks: two launches, the second continuing from the
+    # first's running sums (the last block's x-coefficient sum in the scratch
+    # csum_out[last]); the last block's gradient against the oracle's sum, the
+    # bar widened by half an ulp of the running sum the first launch rounds
+    from .test_gpu_backward import bf16_ulp
+
+    n, d, nb, P = 256, 3072, 2, 20
+    g = torch.Generator(device=gpu).manual_seed(91)
+    blocks = [torch.randn((n, d), generator=g, device=gpu).to(torch.bfloat16) for _ in range(nb)]
+    terms, dx, first = [], [], np.zeros((n, d))
+    for p in range(P):
+        own = torch.randn((n, d), generator=g, device=gpu).to(torch.bfloat16)
+        q = (torch.randn(d, generator=g, device=gpu) * 0.05).to(torch.bfloat16)
+        gout = torch.randn((n, d), generator=g, device=gpu).to(torch.bfloat16)
+        gain = torch.ones(d, device=gpu, dtype=torch.bfloat16)
+        _, coef, qfold, _, _ = _defer(gpu, blocks + [own], q, gain, gout)
+        terms.append((gout, coef, qfold))
+        if p < 16:  # the running sum the first launch rounds (without its x term)
+            c = coef.double().cpu().numpy()
+            first += c[:, 1, 0:1] * np64(gout) + c[:, 1, 1:2] * np64(qfold)[None, :]
+        dx.append(O.route_backward(np.stack([np64(t) for t in blocks + [own]]),
+                                   O.fold_query(np64(q), np64(gain), "bf16"), 1e-5, np64(gout), None)["dx"])
+    part_out = [torch.empty((n, d), device=gpu, dtype=torch.bfloat16)]
+    csum_out = [torch.empty(n, device=gpu), torch.empty(n, device=gpu)]
+    out = torch.empty((n, d), device=gpu, dtype=torch.bfloat16)
+    _capi.route_bwd_gather_seg(
+        nb, n, d, BF, P, _capi.pointer_array([t[0].data_ptr() for t in terms]), d,
+        _capi.pointer_array([t[1].data_ptr() for t in terms]), _capi.int64_array([4 * t[1].shape[1] for t in terms]),
+        _capi.pointer_array([t[2].data_ptr() for t in terms]), _capi.pointer_array([None, None]),
+        _capi.pointer_array([None, None]), _capi.pointer_array([part_out[0].data_ptr(), out.data_ptr()]),
+        _capi.pointer_array([c.data_ptr() for c in csum_out]), blocks[1].data_ptr(), d, None, d,
+        torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize()
+    want = sum(x[1] for x in dx)
+    err = np.abs(np64(out) - want)
+    bar = bf16_ulp(want) + 0.5 * bf16_ulp(first) + 1e-3 * np.abs(want).max()
+    assert (err <= bar).all(), f"20 terms: worst err {err.max():.3e}"
