@@ -668,30 +668,37 @@ def bench_mall(steps: int, warmup: int, dev) -> dict:
 
 def train_path_bytes(w) -> tuple[int, int]:
     """Algorithmic bytes per step of the kernels the eager training loop runs at
-    ``w``'s schedule (bf16, hidden 3072 / 4096: the deferred backward), in rows of
-    tokens * hidden * 2 bytes and 16-byte coefficient records per token and
-    committed source.  Forward: a point that updates the partial reads S - 1
-    blocks, the partial and the sublayer output and writes the new partial and
-    the routed row; the first point and a point after a commit read S and write
-    one.  Backward: a point with committed blocks reads its S sources, dL/dout
-    and the next point's partial gradient (none at the last point), writes the
-    partial's gradient and its records; the first point (S = 1) the same with
-    its one gradient row; each block's sum reads the dL/dout rows and records of
-    its P readers and the block's row, and writes its gradient."""
+    ``w``'s schedule (bf16, hidden 3072 / 4096: the deferred backward and the
+    segment sums), in rows of tokens * hidden * 2 bytes, 16-byte coefficient
+    records per token and block, and 4-byte per-token sums.  Forward: a point
+    that updates the partial reads S - 1 blocks, the partial and the sublayer
+    output and writes the new partial and the routed row; the first point and
+    a point after a commit read S and write one.  Backward: a point with
+    committed blocks reads its S sources, dL/dout and the next point's partial
+    gradient (none at the last point), writes the partial's gradient and its
+    records; the first point (S = 1) the same with its one gradient row; at
+    the commit of block k the segment sum reads the dL/dout rows of the points
+    since the previous commit and their records of blocks 0 .. k, the running
+    sums those blocks carry from later segments and block k's row, and writes
+    the blocks' running sums (block k's gradient)."""
     sched = w.schedule
     S, C = list(sched.active_counts), list(sched.commit_before)
     P = len(S)
     row = w.tokens * w.hidden * w.elem_bytes
     rec = w.tokens * 16
+    tsum = w.tokens * 4
     fwd = bwd = 0
     for j in range(P):
         fwd += (S[j] + 1) * row if (j == 0 or C[j]) else (S[j] + 3) * row
         add = 1 if j < P - 1 else 0
         bwd += (S[j] + 2 + add) * row + ((S[j] - 1) * rec if S[j] >= 2 else 0)
-    for j in range(P):
-        if C[j]:
-            terms = P - j
-            bwd += (terms + 2) * row + terms * rec
+    commits = [j for j in range(P) if C[j]]
+    for i in range(len(commits) - 1, -1, -1):
+        j0 = commits[i]
+        j1 = commits[i + 1] if i + 1 < len(commits) else P
+        nb, terms = i + 1, j1 - j0
+        carried = nb if i + 1 < len(commits) else 0  # running sums from later segments
+        bwd += (terms + carried + 1 + nb) * row + terms * nb * rec + (carried + nb - 1) * tsum
     return fwd, bwd
 
 
