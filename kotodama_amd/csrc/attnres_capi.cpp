@@ -447,15 +447,21 @@ int get_gather_seg(DeviceState& st, int nch, int nb, hipFunction_t* f) {
 // Row parts per token of the segment kernel (each wave takes one) and the
 // waves per SIMD each instance is compiled for (workgroups per CU), as the
 // instances in attnres_kernels.hip.
+// Parts per row and workgroups per CU of the segment kernel for (nch, nb),
+// from the instance table the kernels are compiled from.
 int gather_seg_parts(int nch, int nb) {
-  static const int cpw6[ATTNRES_SEG_MAX_BLOCKS] = {6, 3, 2, 2, 3, 1, 1, 1};
-  static const int cpw8[ATTNRES_SEG_MAX_BLOCKS] = {8, 4, 2, 2, 1, 1, 1, 1};
-  return nch / (nch == 8 ? cpw8[nb - 1] : cpw6[nb - 1]);
+#define ATTNRES_SEG_PARTS(NCH, NB, CPW, DEPTH, WPE) \
+  if (nch == NCH && nb == NB) return NCH / CPW;
+  ATTNRES_SEG_INSTANCES(ATTNRES_SEG_PARTS)
+#undef ATTNRES_SEG_PARTS
+  return 0;
 }
 int gather_seg_per_cu(int nch, int nb) {
-  static const int wpe6[ATTNRES_SEG_MAX_BLOCKS] = {2, 2, 2, 2, 1, 2, 2, 2};
-  static const int wpe8[ATTNRES_SEG_MAX_BLOCKS] = {1, 1, 2, 2, 2, 2, 2, 1};
-  return nch == 8 ? wpe8[nb - 1] : wpe6[nb - 1];
+#define ATTNRES_SEG_WPE(NCH, NB, CPW, DEPTH, WPE) \
+  if (nch == NCH && nb == NB) return WPE;
+  ATTNRES_SEG_INSTANCES(ATTNRES_SEG_WPE)
+#undef ATTNRES_SEG_WPE
+  return 1;
 }
 // Row KiB of the deferred backward for this call, or 0 when it has no kernel
 // (bf16 sources, output gradients and parameters; rows of 6 KiB with S <= 8

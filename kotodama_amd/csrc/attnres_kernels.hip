@@ -57,6 +57,7 @@
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 namespace {
@@ -200,6 +201,24 @@ __device__ __forceinline__ void st_row_nt(__amdgpu_buffer_rsrc_t r, uint32_t off
 }
 __device__ __forceinline__ void st_row_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 2);
+}
+
+// Stores hidden from the compiler's wait-count model.  One counter (vmcnt)
+// covers vector loads and stores, and the compiler, which cannot order a
+// pending store against a pending load, waits for a loaded register with
+// vmcnt(0) whenever one of its stores may be in flight: every prefetched row
+// drains.  Loads complete in issue order, so a wait until no more loads are
+// outstanding than were issued after the one awaited proves that load
+// complete whatever stores are in flight as well (they only lengthen the
+// wait); with the stores issued from inline assembly the compiler counts
+// loads alone and its waits keep the later loads in flight (kernels that
+// keep several loads in flight across their stores).  The s_nop covers the
+// store-data hazard of a VALU write right after the store.
+__device__ __forceinline__ void st_row_nt_hidden(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
+  asm volatile("buffer_store_dwordx4 %0, %1, %2, 0 offen nt\n\ts_nop 1" : : "v"(v), "v"(off), "s"(r) : "memory");
+}
+__device__ __forceinline__ void st_f32_hidden(float* p, float v) {
+  asm volatile("global_store_dword %0, %1, off\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
 }
 
 template <typename T>
@@ -2534,21 +2553,37 @@ __device__ __forceinline__ void route_bwd_gather_body(const attnres_route_bwd_ga
 //
 // The gradients of blocks 0 .. NB-1 from the terms of the points that read
 // them all (the points between two commits), each point's dL/dout row read
-// once: a wave takes one part of a token row (CPW KiB of the NCH KiB; NB*CPW*8
-// fp32 accumulators per lane) and streams, through a two-slot pipeline (the
-// next item requested once the current one has arrived), per term its record
-// row (lane j: block j's (w, c1, c2)), its folded query part and its dL/dout
-// part, accumulating
-//   acc_j += w_pj G_p + c1_pj q_p,   cs_j += c2_pj   (cs wave-uniform)
-// for every block j; then per block its running sum part (empty buffer
-// resource without one), the block's sum stored (bf16, non-temporal) with
-// cs_j to csum_out; with P.final_block the last block instead takes its row
-// x and the addend in one more item and stores acc + cs x + addend.
-template <int NB, int NCH, int CPW>
+// once.  A wave takes one part of a token row (CPW KiB of the NCH KiB) at a
+// time, a unit, and streams its items through a ring of DEPTH slots (the
+// next item requested once the oldest in flight has arrived): per term its
+// record row (lane j: block j's (w, c1, c2)), its dL/dout part and its
+// folded query part; per block its running sum part and x-coefficient sum;
+// with P.final_block the last block's x and addend parts.  Every item is
+// one accumulation on the matrix cores (v_mfma_f32_4x4x4_16b_bf16) into the
+// blocks' fp32 sums of the unit,
+//   acc_j += a_j G + b_j Q
+// (per element and group of four blocks one product: lane 4b+i of A carries
+// block 4s+i's (a hi, b hi, a lo, b lo), the coefficients split into bf16
+// hi + lo parts, hi + lo equal to the fp32 value to about 2^-17 of it; lane
+// 4b+j's B column its own element (G, Q, G, Q); D element i is block 4s+i
+// at that element):
+//   term p:      G = dL/dout_p, Q = q_p,  a_j = w_pj,  b_j = c1_pj,
+//                cs_j += c2_pj (lane j);
+//   block k:     G = its running sum, a_k = 1, cs_k += its x-coefficient sum;
+//   final:       G = x, Q = addend,  a_L = cs_L, b_L = 1  (L = NB - 1),
+// so the accumulation runs the same code for every item.  After the unit's
+// last item the blocks' sums are stored (bf16, non-temporal; with
+// P.final_block the last one as the block's gradient) and, for the blocks
+// that carry on, cs_j to csum_out.
+template <int NB, int NCH, int CPW, int DEPTH>
 __device__ __forceinline__ void route_bwd_gather_seg_body(const attnres_route_bwd_gather_seg_params& P) {
   static_assert(NCH % CPW == 0, "a row splits into whole parts");
+  static_assert(NB >= 1 && NB <= 8, "blocks of one segment");
+  static_assert(DEPTH >= 2, "one item in flight behind the one processed");
   constexpr uint32_t PARTS = NCH / CPW;
   constexpr uint32_t PB = CPW * 1024;  // bytes of one part of a row
+  constexpr int R = (NB + 3) / 4;      // groups of four blocks
+  constexpr int L = NB - 1;
   const int lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t nwv = (uint32_t)P.block >> 6;
@@ -2556,15 +2591,20 @@ __device__ __forceinline__ void route_bwd_gather_seg_body(const attnres_route_bw
   const uint32_t nw = gridDim.x * nwv;
   const uint32_t item0 = blockIdx.x * nwv + wave;
   if (item0 >= n_items) return;
-  const uint32_t rows = (n_items - item0 - 1) / nw + 1;  // items of this wave
+  const uint32_t rows = (n_items - item0 - 1) / nw + 1;  // units of this wave
   const uint32_t nt = (uint32_t)P.num_terms;
   const bool fin = P.final_block != 0;
-  // terms, then one slot per block, then (final) the last block's x and addend
+  // terms, then one item per block, then (final) the last block's x and addend
   const uint32_t per = nt + NB + (fin ? 1u : 0u);
   const uint32_t lane_off = (uint32_t)lane * 16;
 
-  // slot (j, r) of the wave's items: A and B row parts and a record row
-  auto issue = [&](u32x4(&a)[CPW], u32x4(&b)[CPW], u32x4& rec, uint32_t j, uint32_t r, uint32_t z) {
+  // item (j, r) of the wave's units into a slot: every item issues the same
+  // loads into the same registers (one record load, CPW B and CPW A parts;
+  // empty resources read zeros), so the wait for a slot counts exactly the
+  // loads issued after it.  The record load takes 12 bytes (w, c1, c2): a
+  // loaded register left unused would be reused while its load is in flight,
+  // and overwriting it waits for that load.
+  auto issue = [&](u32x4(&a)[CPW], u32x4(&b)[CPW], u32x3& rec, uint32_t j, uint32_t r, uint32_t z) {
     if (j >= rows) {
       j = rows - 1;
       r = per - 1;
@@ -2577,33 +2617,34 @@ __device__ __forceinline__ void route_bwd_gather_seg_body(const attnres_route_bw
     char* abase = nullptr;
     char* bbase = nullptr;
     char* cbase = nullptr;
-    uint32_t abytes = 0, bbytes = 0;
+    uint32_t abytes = 0, bbytes = 0, cbytes = 0, coff = 0;
     if (r < nt) {
       const attnres_gather_term& T = P.term[r];
       abase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(T.grad_out) + t * (uint64_t)P.gout_ld * 2 + h * PB));
       bbase = const_cast<char*>(static_cast<const char*>(T.qfold)) + h * PB;
       cbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(T.coef) + t * (uint64_t)T.coef_ld * 4));
       abytes = bbytes = PB;
+      cbytes = NB * 16;  // lane j: block j's record
+      coff = lane_off;
     } else if (r < nt + NB) {
-      // the block's running sum part and (in the record slot) its x-coefficient sum
+      // the block's running sum part and (record word 0, every lane) its x-coefficient sum
       const void* pin = P.blk[r - nt].part_in;
       const float* cin = P.blk[r - nt].csum_in;
       abase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(pin) + t * (uint64_t)P.out_ld * 2 + h * PB));
       abytes = pin != nullptr ? PB : 0u;
-      char* cs_at = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(cin) + t * 4));
-      const __amdgpu_buffer_rsrc_t rcs = row_rsrc(cs_at, cin != nullptr ? 4u : 0u);
-      rec = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rcs, z, 0, 0), 0u, 0u, 0u};
+      cbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(cin) + t * 4));
+      cbytes = cin != nullptr ? 4u : 0u;
     } else {
       abase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.x) + t * (uint64_t)P.x_ld * 2 + h * PB));
       bbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.addend) + t * (uint64_t)P.out_ld * 2 + h * PB));
       abytes = PB;
       bbytes = P.addend != nullptr ? PB : 0u;
     }
-    const __amdgpu_buffer_rsrc_t rc = row_rsrc(cbase, cbase != nullptr ? (uint32_t)(NB * 16) : 0u);
+    const __amdgpu_buffer_rsrc_t rc = row_rsrc(cbase, cbytes);
     const __amdgpu_buffer_rsrc_t rb = row_rsrc(bbase, bbytes);
     const __amdgpu_buffer_rsrc_t ra = row_rsrc(abase, abytes);
-    // records and the folded query first: rows return in order, so the A part's arrival implies theirs
-    if (r < nt) rec = __builtin_amdgcn_raw_buffer_load_b128(rc, lane_off + z, 0, 0);
+    // records and the B part first: loads return in order, so the A part's arrival implies theirs
+    rec = __builtin_amdgcn_raw_buffer_load_b96(rc, coff + z, 0, 0);
 #pragma unroll
     for (int c = 0; c < CPW; ++c) b[c] = __builtin_amdgcn_raw_buffer_load_b128(rb, lane_off + (uint32_t)(c * 1024) + z, 0, 0);
 #pragma unroll
@@ -2611,96 +2652,92 @@ __device__ __forceinline__ void route_bwd_gather_seg_body(const attnres_route_bw
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  float acc[NB][CPW][8];
-  float cs[NB];
+  // block k's sum at element e of chunk c: element k % 4 of acc[k / 4][c][e]
+  f32x4 acc[R][CPW][8];
 #pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    cs[k] = 0.f;
+  for (int g = 0; g < R; ++g) {
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[k][c][e] = 0.f;
+      for (int e = 0; e < 8; ++e) acc[g][c][e] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
+  float csl = 0.f;  // lane k: block k's x-coefficient sum
   auto lane_f = [](uint32_t v, int l) { return as_f32(__builtin_amdgcn_readlane(v, l)); };
-  auto process = [&](u32x4(&a)[CPW], u32x4(&b)[CPW], const u32x4& rec, uint32_t j, uint32_t r) {
+  auto process = [&](u32x4(&a)[CPW], u32x4(&b)[CPW], const u32x3& rec, uint32_t j, uint32_t r) {
+    // the A operands: (a, b) of block 4g + (lane & 3), split hi + lo
+    float av[R], bv[R];
+    if (r < nt) {
+#pragma unroll
+      for (int g = 0; g < R; ++g) {
+        const int src = (4 * g + (lane & 3)) << 2;
+        av[g] = as_f32(__builtin_amdgcn_ds_bpermute(src, (int)rec[0]));
+        bv[g] = as_f32(__builtin_amdgcn_ds_bpermute(src, (int)rec[1]));
+      }
+      csl += as_f32(rec[2]);
+    } else {
+      const bool blk = r < nt + NB;
+      const uint32_t kb = blk ? r - nt : (uint32_t)L;
+      const float ka = blk ? 1.f : lane_f(as_u32(csl), L);
+      const float kq = blk ? 0.f : 1.f;
+#pragma unroll
+      for (int g = 0; g < R; ++g) {
+        const bool mine = (uint32_t)(4 * g + (lane & 3)) == kb;
+        av[g] = mine ? ka : 0.f;
+        bv[g] = mine ? kq : 0.f;
+      }
+      if (blk) csl += (uint32_t)lane == kb ? as_f32(rec[0]) : 0.f;
+    }
+    u32x2 am[R];
+#pragma unroll
+    for (int g = 0; g < R; ++g) {
+      const uint32_t hi = pack_bf16(av[g], bv[g]);
+      am[g] = u32x2{hi, pack_bf16(av[g] - bf_lo(hi), bv[g] - bf_hi(hi))};
+    }
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t pl = __builtin_amdgcn_perm(b[c][q], a[c][q], 0x05040100u);  // (G, Q) of element 2q
+        const uint32_t ph = __builtin_amdgcn_perm(b[c][q], a[c][q], 0x07060302u);  // of element 2q + 1
+#pragma unroll
+        for (int g = 0; g < R; ++g) {
+          acc[g][c][2 * q] = mfma_4x4x4(am[g], u32x2{pl, pl}, acc[g][c][2 * q]);
+          acc[g][c][2 * q + 1] = mfma_4x4x4(am[g], u32x2{ph, ph}, acc[g][c][2 * q + 1]);
+        }
+      }
+    }
+    if (r != per - 1) return;
+    // the unit's last item: store every block's sum, clear them
     const uint32_t item = item0 + j * nw;
     const uint64_t t = item / PARTS;
     const uint32_t h = item % PARTS;
-    if (r < nt) {
 #pragma unroll
-      for (int k = 0; k < NB; ++k) {
-        const float w = lane_f(rec[0], k), c1 = lane_f(rec[1], k);
-        cs[k] += lane_f(rec[2], k);
+    for (int k = 0; k < NB; ++k) {
+      char* orow = const_cast<char*>(
+          uniform_ptr(reinterpret_cast<uint64_t>(P.blk[k].part_out) + t * (uint64_t)P.out_ld * 2 + h * PB));
+      const __amdgpu_buffer_rsrc_t ro = row_rsrc(orow, PB);
 #pragma unroll
-        for (int c = 0; c < CPW; ++c) {
+      for (int c = 0; c < CPW; ++c) {
+        u32x4 pk;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            acc[k][c][2 * q] = __builtin_fmaf(w, bf_lo(a[c][q]), __builtin_fmaf(c1, bf_lo(b[c][q]), acc[k][c][2 * q]));
-            acc[k][c][2 * q + 1] =
-                __builtin_fmaf(w, bf_hi(a[c][q]), __builtin_fmaf(c1, bf_hi(b[c][q]), acc[k][c][2 * q + 1]));
-          }
-        }
+        for (int q = 0; q < 4; ++q) pk[q] = pack_bf16(acc[k / 4][c][2 * q][k % 4], acc[k / 4][c][2 * q + 1][k % 4]);
+        st_row_nt_hidden(ro, lane_off + (uint32_t)(c * 1024), pk);
       }
-      return;
-    }
-    if (r < nt + NB) {
-      // block k's running sum from earlier segments (zeros without one)
-      const uint32_t kb = r - nt;
-#pragma unroll
-      for (int k = 0; k < NB; ++k) {
-        if ((uint32_t)k != kb) continue;
-#pragma unroll
-        for (int c = 0; c < CPW; ++c) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            acc[k][c][2 * q] += bf_lo(a[c][q]);
-            acc[k][c][2 * q + 1] += bf_hi(a[c][q]);
-          }
-        }
-        cs[k] += as_f32(__builtin_amdgcn_readfirstlane(rec[0]));  // 0 without a running sum
-        if (k < NB - 1 || !fin) {
-          char* orow = const_cast<char*>(
-              uniform_ptr(reinterpret_cast<uint64_t>(P.blk[k].part_out) + t * (uint64_t)P.out_ld * 2 + h * PB));
-          const __amdgpu_buffer_rsrc_t ro = row_rsrc(orow, PB);
-#pragma unroll
-          for (int c = 0; c < CPW; ++c) {
-            u32x4 pk;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) pk[q] = pack_bf16(acc[k][c][2 * q], acc[k][c][2 * q + 1]);
-            st_row_nt(ro, lane_off + (uint32_t)(c * 1024), pk);
-          }
-          if (h == 0 && lane == 0) P.blk[k].csum_out[t] = cs[k];
-#pragma unroll
-          for (int c = 0; c < CPW; ++c) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[k][c][e] = 0.f;
-          }
-          cs[k] = 0.f;
-        }
+      if (k < L || !fin) {
+        const float csk = lane_f(as_u32(csl), k);
+        if (h == 0 && lane == 0) st_f32_hidden(P.blk[k].csum_out + t, csk);
       }
-      return;
     }
-    // the last block: + cs x + addend, stored as its gradient
-    constexpr int L = NB - 1;
-    const float cst = cs[L];
-    char* orow = const_cast<char*>(
-        uniform_ptr(reinterpret_cast<uint64_t>(P.blk[L].part_out) + t * (uint64_t)P.out_ld * 2 + h * PB));
-    const __amdgpu_buffer_rsrc_t ro = row_rsrc(orow, PB);
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      u32x4 pk;
+    for (int g = 0; g < R; ++g) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float lo = __builtin_fmaf(cst, bf_lo(a[c][q]), acc[L][c][2 * q]) + bf_lo(b[c][q]);
-        const float hi = __builtin_fmaf(cst, bf_hi(a[c][q]), acc[L][c][2 * q + 1]) + bf_hi(b[c][q]);
-        pk[q] = pack_bf16(lo, hi);
+      for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][c][e] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-      st_row_nt(ro, lane_off + (uint32_t)(c * 1024), pk);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[L][c][e] = 0.f;
     }
-    cs[L] = 0.f;
+    csl = 0.f;
   };
   auto after = [per](uint32_t& j, uint32_t& r) {
     const uint32_t r1 = r + 1;
@@ -2709,29 +2746,34 @@ __device__ __forceinline__ void route_bwd_gather_seg_body(const attnres_route_bw
     j = __builtin_amdgcn_readfirstlane(wrap ? j + 1 : j);
   };
 
-  // A ring of DEPTH = PARTS + 1 slots: PARTS items in flight behind the one
-  // being processed, so a wave keeps about one whole row (NCH KiB) in flight
-  // whatever its part size (the next item is requested once the oldest in
-  // flight has arrived).
-  constexpr int DEPTH = (int)PARTS + 1;
-  u32x4 A[DEPTH][CPW], B[DEPTH][CPW], R[DEPTH];
+  u32x4 A[DEPTH][CPW], B[DEPTH][CPW];
+  u32x3 Rc[DEPTH];
   uint32_t ji = 0, ri = 0, jp = 0, rp = 0;
 #pragma unroll
   for (int u = 0; u < DEPTH - 1; ++u) {
-    issue(A[u], B[u], R[u], ji, ri, 0u);
+    issue(A[u], B[u], Rc[u], ji, ri, 0u);
     after(ji, ri);
   }
   const uint32_t items = rows * per;
-  for (uint32_t i = 0; i < items; i += DEPTH) {
+  // whole rounds of the ring without conditions (each wait then counts the
+  // loads issued after it across the loop's back edge), then the last,
+  // partial round
+  uint32_t i = 0;
+  for (; i + DEPTH <= items; i += DEPTH) {
 #pragma unroll
     for (int u = 0; u < DEPTH; ++u) {
-      if (i + (uint32_t)u < items) {
-        const int nx = (u + DEPTH - 1) % DEPTH;  // the slot processed last, refilled now
-        issue(A[nx], B[nx], R[nx], ji, ri, arrival_zero(A[u][CPW - 1][3]));
-        after(ji, ri);
-        process(A[u], B[u], R[u], jp, rp);
-        after(jp, rp);
-      }
+      const int nx = (u + DEPTH - 1) % DEPTH;  // the slot processed last, refilled now
+      issue(A[nx], B[nx], Rc[nx], ji, ri, arrival_zero(A[u][CPW - 1][3]));
+      after(ji, ri);
+      process(A[u], B[u], Rc[u], jp, rp);
+      after(jp, rp);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < DEPTH - 1; ++u) {
+    if (i + (uint32_t)u < items) {
+      process(A[u], B[u], Rc[u], jp, rp);
+      after(jp, rp);
     }
   }
 }
@@ -4180,21 +4222,21 @@ BWD_STREAM_ONE_DEFER(8, 8, 2) BWD_STREAM_ONE_DEFER(9, 8, 3)
 GATHER_ONE(6) GATHER_ONE(8)
 #endif
 
-// Segments of deferred sums: attnres_route_bwd_gather_seg_c<NCH>_b<NB>, a wave
-// per CPW KiB part of a row, compiled for WPE waves per SIMD (the host runs
-// WPE workgroups per CU).  The kernels are bound by their NB*2 FMAs per
-// element and term: smaller parts at two waves per SIMD measured faster
-// (3 blocks: 0.79 -> 0.65 ms, 7 blocks: 1.52 -> 1.47 ms at the 3B shape)
-// except at 5 blocks (3 KiB parts, one wave: 1.09 against 1.23 ms); two-KiB
-// parts at two waves per SIMD spill from 5 blocks on.
-#define GATHER_SEG_ONE(NCH, NB, CPW, WPE)                                                               \
+// Segments of deferred sums (the instances in ATTNRES_SEG_INSTANCES), a wave
+// per CPW KiB part of a row with a ring of DEPTH items, compiled for WPE
+// waves per SIMD.  Measured at the 3B and 8B shapes (8 terms, 32768 and 16384
+// rows): the kernels are bound by their loads and stores, not the matrix
+// cores (removing the MFMAs or the A operands' construction changed nothing,
+// removing the stores took 15-30% off); larger parts read faster, so up to
+// four blocks (one group, 32 fp32 sums per KiB and lane) take 3 KiB (6 KiB
+// rows) or 4 KiB parts (8 KiB rows), five to eight blocks (two groups) 2 KiB
+// parts with a shallow ring, where 1 KiB parts ran 5-8% slower at 6 KiB
+// rows.  Non-temporal stores beat sc1 and default ones by 5-15%.
+#define GATHER_SEG_ONE(NCH, NB, CPW, DEPTH, WPE)                                                        \
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))          \
       attnres_route_bwd_gather_seg_c##NCH##_b##NB(attnres_route_bwd_gather_seg_params P) {              \
-    route_bwd_gather_seg_body<NB, NCH, CPW>(P);                                                         \
+    route_bwd_gather_seg_body<NB, NCH, CPW, DEPTH>(P);                                                  \
   }
 #if ATTNRES_PART == 10 || defined(ATTNRES_ALL_PARTS)
-GATHER_SEG_ONE(6, 1, 6, 2) GATHER_SEG_ONE(6, 2, 3, 2) GATHER_SEG_ONE(6, 3, 2, 2) GATHER_SEG_ONE(6, 4, 2, 2)
-GATHER_SEG_ONE(6, 5, 3, 1) GATHER_SEG_ONE(6, 6, 1, 2) GATHER_SEG_ONE(6, 7, 1, 2) GATHER_SEG_ONE(6, 8, 1, 2)
-GATHER_SEG_ONE(8, 1, 8, 1) GATHER_SEG_ONE(8, 2, 4, 1) GATHER_SEG_ONE(8, 3, 2, 2) GATHER_SEG_ONE(8, 4, 2, 2)
-GATHER_SEG_ONE(8, 5, 1, 2) GATHER_SEG_ONE(8, 6, 1, 2) GATHER_SEG_ONE(8, 7, 1, 2) GATHER_SEG_ONE(8, 8, 1, 1)
+ATTNRES_SEG_INSTANCES(GATHER_SEG_ONE)
 #endif

@@ -150,6 +150,19 @@ typedef struct attnres_route_bwd_gather_params {
  */
 #define ATTNRES_SEG_MAX_BLOCKS 8
 #define ATTNRES_SEG_MAX_TERMS 16
+/*
+ * The compiled segment kernels, attnres_route_bwd_gather_seg_c<NCH>_b<NB>:
+ * X(NCH row KiB, NB blocks, CPW KiB per wave part, DEPTH ring slots, WPE waves
+ * per SIMD; the host runs WPE workgroups of four waves per CU).  Shared by the
+ * kernels and the host, which sizes the grid from the same parts.
+ */
+#ifndef ATTNRES_SEG_INSTANCES
+#define ATTNRES_SEG_INSTANCES(X)                                                                        \
+  X(6, 1, 3, 4, 2) X(6, 2, 3, 4, 2) X(6, 3, 3, 4, 2) X(6, 4, 3, 4, 2)                                   \
+  X(6, 5, 2, 2, 2) X(6, 6, 2, 2, 2) X(6, 7, 2, 2, 2) X(6, 8, 2, 2, 2)                                   \
+  X(8, 1, 4, 2, 2) X(8, 2, 4, 2, 2) X(8, 3, 4, 2, 2) X(8, 4, 4, 2, 2)                                   \
+  X(8, 5, 2, 3, 2) X(8, 6, 2, 3, 2) X(8, 7, 2, 3, 2) X(8, 8, 2, 3, 2)
+#endif
 typedef struct attnres_seg_block {
   const void* part_in;   /* (n_tokens, d), row stride out_ld, or NULL */
   const float* csum_in;  /* (n_tokens,), or NULL */
