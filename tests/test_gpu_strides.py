@@ -217,3 +217,75 @@ def test_route_bwd_defer_and_gather_row_strides(gpu, S, n, d):
     err = np.abs(np64(out[:, :d]) - want0)
     assert (err <= bf16_ulp(want0) + 1e-3 * np.abs(want0).max()).all(), f"gathered gradient worst err {err.max():.3e}"
     assert torch.all(out[:, d:] == CANARY), "gathered gradient row padding written"
+
+
+@pytest.mark.parametrize("nb,P,n,d", [(3, 5, 700, 3072), (6, 4, 513, 4096), (8, 3, 301, 4096)])
+def test_route_bwd_gather_seg_row_strides_in_place(gpu, nb, P, n, d):
+    # P calls of attnres_route_bwd_defer over nb padded block rows and a
+    # partial of their own, then one attnres_route_bwd_gather_seg with padded
+    # dL/dout, block and output rows: blocks 0 .. nb-2 continue their running
+    # sums in place (part_in = part_out, csum_in = csum_out), the last block
+    # takes its addend in place (addend = its output).  The carried sums against
+    # float64 sums of the records, the last block against the oracle; no byte
+    # of the padding written
+    print(f"route_bwd_gather_seg strided in place nb={nb} P={P} n={n} d={d}", flush=True)
+    bf = torch.bfloat16
+    src_ld, gout_ld, out_ld = d + 64, d + 128, d + 32
+    g = torch.Generator(device=gpu).manual_seed(nb * 31 + P)
+    big = torch.full((nb, n, src_ld), CANARY, device=gpu, dtype=bf)
+    for j in range(nb):
+        big[j, :, :d] = (torch.randn((n, d), generator=g, device=gpu) * (0.5 + 0.2 * j)).to(bf)
+    ws = torch.empty(_capi.route_bwd_workspace_size(n, d) // 4, device=gpu)
+    st = torch.cuda.current_stream(gpu).cuda_stream
+    gouts, coefs, qfolds, dx = [], [], [], []
+    for p in range(P):
+        own = torch.full((n, src_ld), CANARY, device=gpu, dtype=bf)
+        own[:, :d] = torch.randn((n, d), generator=g, device=gpu).to(bf)
+        q = (torch.randn(d, generator=g, device=gpu) * 0.05).to(bf)
+        gain = (1 + 0.1 * torch.randn(d, generator=g, device=gpu)).to(bf)
+        gbuf = torch.full((n, gout_ld), CANARY, device=gpu, dtype=bf)
+        gbuf[:, :d] = torch.randn((n, d), generator=g, device=gpu).to(bf)
+        gpart = torch.empty((n, d), device=gpu, dtype=bf)
+        coef = torch.full((n, nb, 4), float("nan"), device=gpu)
+        qfold = torch.empty(d, device=gpu, dtype=bf)
+        dq = torch.empty(d, device=gpu, dtype=bf)
+        srcs = [big[j].data_ptr() for j in range(nb)] + [own.data_ptr()]
+        rc = _capi.route_bwd_defer(
+            _capi.pointer_array(srcs), nb + 1, n, d, src_ld, _capi.DTYPE_BF16, q.data_ptr(), gain.data_ptr(),
+            _capi.DTYPE_BF16, 1e-5, gbuf.data_ptr(), _capi.DTYPE_BF16, gout_ld, None, gpart.data_ptr(), None, d,
+            coef.data_ptr(), qfold.data_ptr(), ws.data_ptr(), ws.numel() * 4, dq.data_ptr(), None, st)
+        _capi.check("attnres_route_bwd_defer", rc)
+        torch.cuda.synchronize()
+        srcs64 = np.concatenate([np64(big[:, :, :d]), np64(own[:, :d])[None]])
+        dx.append(O.route_backward(srcs64, O.fold_query(np64(q), np64(gain), "bf16"), 1e-5, np64(gbuf[:, :d]),
+                                   None)["dx"])
+        gouts.append(gbuf), coefs.append(coef), qfolds.append(qfold)
+    # running sums of blocks 0 .. nb-2 from a later segment, updated in place
+    part = torch.full((nb, n, out_ld), CANARY, device=gpu, dtype=bf)
+    for j in range(nb - 1):
+        part[j, :, :d] = (torch.randn((n, d), generator=g, device=gpu) * 0.1).to(bf)
+    csum = torch.randn((nb, n), generator=g, device=gpu) * 0.01
+    part[nb - 1, :, :d] = (torch.randn((n, d), generator=g, device=gpu) * 0.01).to(bf)  # the addend
+    prev = np64(part[:, :, :d])
+    prev_cs = np64(csum)
+    rows = [part[j].data_ptr() for j in range(nb)]
+    cs = [csum[j].data_ptr() for j in range(nb - 1)] + [None]
+    _capi.route_bwd_gather_seg(
+        nb, n, d, _capi.DTYPE_BF16, P, _capi.pointer_array([t.data_ptr() for t in gouts]), gout_ld,
+        _capi.pointer_array([c.data_ptr() for c in coefs]), _capi.int64_array([4 * nb] * P),
+        _capi.pointer_array([q.data_ptr() for q in qfolds]), _capi.pointer_array(rows[:-1] + [None]),
+        _capi.pointer_array(cs), _capi.pointer_array(rows), _capi.pointer_array(cs), big[nb - 1].data_ptr(), src_ld,
+        rows[-1], out_ld, st)
+    torch.cuda.synchronize()
+    recs = [(np64(c), np64(t[:, :d]), np64(q)) for c, t, q in zip(coefs, gouts, qfolds)]
+    for j in range(nb - 1):
+        want = prev[j] + sum(c[:, j, 0:1] * G + c[:, j, 1:2] * q[None, :] for c, G, q in recs)
+        err = np.abs(np64(part[j, :, :d]) - want)
+        assert (err <= bf16_ulp(want) + 1e-3 * np.abs(want).max()).all(), f"block {j} running sum worst err {err.max():.3e}"
+        wc = prev_cs[j] + sum(c[:, j, 2] for c, _, _ in recs)
+        assert (np.abs(np64(csum[j]) - wc) <= 1e-5 * np.abs(wc) + 1e-6 * np.abs(wc).max()).all(), f"block {j} csum"
+    want = sum(x[nb - 1] for x in dx) + prev[nb - 1]
+    err = np.abs(np64(part[nb - 1, :, :d]) - want)
+    assert (err <= bf16_ulp(want) + 1e-3 * np.abs(want).max()).all(), f"last block worst err {err.max():.3e}"
+    assert torch.all(part[:, :, d:] == CANARY), "output row padding written"
+    assert torch.all(big[:, :, d:] == CANARY), "block row padding written"
