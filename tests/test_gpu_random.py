@@ -550,8 +550,10 @@ def test_random_training_points(gpu, seed):
 @pytest.mark.parametrize("seed", range(SEEDS or 8))
 def test_random_deferred_training_points(gpu, seed):
     # the same two points where the committed blocks' gradients are deferred
-    # (attnres_route_bwd_defer per point, attnres_route_bwd_gather at each
-    # block's commit node): bf16 at hidden 3072 (1..7 blocks) or 4096 (1..8)
+    # (attnres_route_bwd_defer per point; at each block's commit node one
+    # attnres_route_bwd_gather, or for odd seeds one attnres_route_bwd_gather_seg
+    # over all blocks at the last block's commit): bf16 at hidden 3072 (1..7
+    # blocks) or 4096 (1..8)
     _training_points_case(gpu, seed, deferred=True)
 
 
@@ -572,8 +574,11 @@ def _training_points_case(gpu, seed, deferred):
     with_gain = bool(rng.integers(2))
     qscale = 0.05 if dtype == torch.float32 else [0.05, 0.5][int(rng.integers(2))]
     pol = _policy(rng)
+    # deferred, odd seeds: the slots share a GradSegments, so the last block's commit sums both points
+    # into every block in one attnres_route_bwd_gather_seg (the others finish from its running sums)
+    seg_mode = deferred and seed % 2 == 1
     print(f"random training points seed={seed}: {dtype} K={K} D={D} N={N} delta={with_delta} gain={with_gain} "
-          f"qscale={qscale} policy={pol}", flush=True)
+          f"qscale={qscale} policy={pol} segments={seg_mode}", flush=True)
     g = torch.Generator(device="cpu").manual_seed(12000 + seed)
 
     def t(*shape, scale=1.0):
@@ -589,7 +594,8 @@ def _training_points_case(gpu, seed, deferred):
     G1, G2, Gp = (torch.randn(N, D, generator=g).to(dtype).to(gpu) for _ in range(3))
 
     def run():
-        slots = [ops.GradSlot() for _ in range(K)]
+        segs = ops.GradSegments() if seg_mode else None
+        slots = [ops.GradSlot(segs) for _ in range(K)]
         committed = [ops.commit_block(b, s) for b, s in zip(blocks, slots)]
         h1, X = ops.route_point(committed, slots, partial, delta, q[0], gn[0], 1e-5, dtype)
         h2, X2 = ops.route_point(committed, slots, X, None, q[1], gn[1], 1e-5, dtype)
@@ -598,12 +604,14 @@ def _training_points_case(gpu, seed, deferred):
         torch.cuda.synchronize()
         return h1, h2, X
 
-    deferred_calls = []
+    deferred_calls, records = [], []
     real = ops._route_rows_backward_defer
 
     def counting(*a, **k):
         r = real(*a, **k)
         deferred_calls.append(r is not None)
+        if r is not None:
+            records.append((np64(r[1]), np64(r[3]), np64(r[2])))  # (w, c1, c2) records, dL/dout rows, qfold
         return r
 
     ops._route_rows_backward_defer = counting
@@ -648,7 +656,14 @@ def _training_points_case(gpu, seed, deferred):
         check_grad_f32(partial.grad, dX, f32[0][0][K] + f32[1][0][K] + np64(Gp), f"seed {seed} dpartial")
     else:
         for k in range(K):
-            _check_grad_sum(blocks[k].grad, res[0]["dx"][k] + res[1]["dx"][k], res[1]["dx"][k], dtype,
+            if seg_mode:
+                # block K-1 is finished in the kernel (one rounding); the others from their running sums,
+                # rounded to bf16 (both points' w G + c1 qfold) before their x terms are added
+                first = np.zeros((N, D)) if k == K - 1 else \
+                    sum(c[:, k, 0:1] * Gr + c[:, k, 1:2] * qf[None, :] for c, Gr, qf in records)
+            else:
+                first = res[1]["dx"][k]
+            _check_grad_sum(blocks[k].grad, res[0]["dx"][k] + res[1]["dx"][k], first, dtype,
                             f"seed {seed} dblock{k}")
         _check_grad_sum(partial.grad, dX, res[1]["dx"][K] + np64(Gp), dtype, f"seed {seed} dpartial")
     if with_delta:
