@@ -301,7 +301,8 @@ int attnres_route_bwd_defer(const void* const* sources, int num_sources, int64_t
  * coef_lds[j] = 4*(S_j - 1).  bf16 rows of hidden 3072 or 4096 (x rows x_ld
  * apart, grad_outs[j] rows grad_out_ld, out and addend rows out_ld); addend
  * may be NULL or out (in place).  fp32 sums rounded once per group of up to
- * 48 terms (more terms: later groups add to out).
+ * 48 terms (more terms: later groups add to out).  Runs the one-block
+ * instance of the attnres_route_bwd_gather_seg kernels.
  *
  * See attnres_route_bwd_defer for the reference code this replaces.
  */
@@ -325,7 +326,7 @@ int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int6
  *   part_out[last] = sum + csum x + addend
  * (x: its rows; addend NULL or rows of out_ld, may equal part_out[last]).
  * part_in / csum_in (the arrays or entries) may be NULL for a block's first
- * segment, or equal part_out / csum_out (in place).  More than 16 terms are
+ * segment, or equal part_out / csum_out (in place).  More than 48 terms are
  * launched in groups, the later ones continuing from part_out / csum_out
  * (csum_out[last] is then needed as scratch).  bf16 rows of hidden 3072 or
  * 4096, up to 8 blocks; other calls return ATTNRES_ERR_UNSUPPORTED.

@@ -497,7 +497,7 @@ def route_bwd_noalloc(*args) -> None:
 
 NOALLOC_SCRATCH_BYTES = 32 << 20  # ATTNRES_NOALLOC_SCRATCH_BYTES
 SEG_MAX_BLOCKS = 8  # ATTNRES_SEG_MAX_BLOCKS
-SEG_MAX_TERMS = 16  # ATTNRES_SEG_MAX_TERMS
+SEG_MAX_TERMS = 48  # ATTNRES_SEG_MAX_TERMS
 
 
 def route_bwd_queries_workspace_size(num_tokens: int, hidden: int, num_sources: int, num_queries: int) -> int:

@@ -114,7 +114,6 @@ struct DeviceState {
   KernelSlot bwd_dqw[4];         // source dtype x V
   KernelSlot bwd_mqg[2 * 9];     // batched-query backward on the matrix cores: query groups x S
   KernelSlot bwd_defer[2 * 10];  // row-per-wave backward with deferred block gradients: row KiB x S
-  KernelSlot gather[2];          // their per-block sums: rows of 6 / 8 KiB
   KernelSlot gather_seg[2 * ATTNRES_SEG_MAX_BLOCKS];  // segment sums: row KiB x blocks
 };
 
@@ -136,8 +135,8 @@ std::atomic<int> g_policy{ATTNRES_POLICY_AUTO};
 // (1: store each row at once), ATTNRES_OUT_BATCH_MIN_S sets the source count
 // from which they stage, ATTNRES_REDUCE_TWO_STAGE=1 reduces the query
 // gradients in two launches always, ATTNRES_MERGE_STREAM=0 keeps the merge on
-// its row-per-workgroup kernel, ATTNRES_GATHER_PER_CU and ATTNRES_GATHER_BATCH set
-// the deferred-gradient sum's workgroups per CU (1..4) and staged rows per wave.
+// its row-per-workgroup kernel, ATTNRES_GATHER_PER_CU sets the deferred-gradient
+// sums' workgroups per CU (1..4).
 struct Tuning {
   int force_v = 0;
   int qg = 1;
@@ -152,8 +151,7 @@ struct Tuning {
   int stream_waves = 0;        // > 0: waves per workgroup of the streaming kernels (1..4); 0: by S
   int reduce_two_stage = 0;    // 1: the query-gradient reduction in two launches
   int merge_stream = 1;        // 0: the merge never uses the row-per-wave kernel
-  int gather_per_cu = 0;       // > 0: workgroups per CU of the deferred-gradient sum
-  int gather_batch = 0;        // > 0: its staged output rows per wave (1: none)
+  int gather_per_cu = 0;       // > 0: workgroups per CU of the deferred-gradient sums
   Tuning() {
     const char* on = std::getenv("ATTNRES_TUNING");
     if (on == nullptr || std::strcmp(on, "1") != 0) return;
@@ -175,11 +173,6 @@ struct Tuning {
       gather_per_cu = std::atoi(v);
       if (gather_per_cu < 1) gather_per_cu = 1;
       if (gather_per_cu > 4) gather_per_cu = 4;
-    }
-    if (const char* v = std::getenv("ATTNRES_GATHER_BATCH")) {
-      gather_batch = std::atoi(v);
-      if (gather_batch < 1) gather_batch = 1;
-      if (gather_batch > 8) gather_batch = 8;
     }
     if (const char* v = std::getenv("ATTNRES_V")) force_v = std::atoi(v);
     if (const char* v = std::getenv("ATTNRES_QG")) qg = std::atoi(v);
@@ -427,17 +420,13 @@ int get_bwd_stream(DeviceState& st, int nch, int s, hipFunction_t* f, bool add =
 
 // Deferred block gradients (code-object part 10): the row-per-wave backward
 // forming only the partial's gradient (attnres_route_bwd_stream_c<NCH>_s<S>_defer,
-// S >= 2) and the per-block sum (attnres_route_bwd_gather_c<NCH>).
+// S >= 2) and the sums of the blocks' terms
+// (attnres_route_bwd_gather_seg_c<NCH>_b<NB>).
 constexpr int kDeferPart = 10;
 int get_bwd_defer(DeviceState& st, int nch, int s, hipFunction_t* f) {
   char name[96];
   snprintf(name, sizeof(name), "attnres_route_bwd_stream_c%d_s%d_defer", nch, s);
   return slot_function(st, st.bwd_defer[(nch == 8 ? 10 : 0) + s], kDeferPart, name, f);
-}
-int get_gather(DeviceState& st, int nch, hipFunction_t* f) {
-  char name[96];
-  snprintf(name, sizeof(name), "attnres_route_bwd_gather_c%d", nch);
-  return slot_function(st, st.gather[nch == 8 ? 1 : 0], kDeferPart, name, f);
 }
 int get_gather_seg(DeviceState& st, int nch, int nb, hipFunction_t* f) {
   char name[96];
@@ -1412,13 +1401,33 @@ int attnres_route_bwd_defer(const void* const* sources, int num_sources, int64_t
                           coef, qfold);
 }
 
-// Sum of deferred gradient terms: one launch per ATTNRES_GATHER_MAX_TERMS
-// terms, the later ones adding to `out`.  Grid: kGatherPerCu 4-wave
-// workgroups per CU, each wave staging kGatherBatch finished rows in LDS
-// (fewer where the LDS does not hold them).
-constexpr int kGatherWaves = 4;
-constexpr int kGatherPerCu = 2;
-constexpr int kGatherBatch = 3;
+constexpr int kGatherWaves = 4;  // waves per workgroup of the segment kernels
+
+// Fill the launch parameters of the segment kernel for terms [j0, j0 + nt).
+static void seg_terms(attnres_route_bwd_gather_seg_params& P, int j0, int nt, const void* const* grad_outs,
+                      const float* const* coefs, const int64_t* coef_lds, const void* const* qfolds) {
+  P.num_terms = nt;
+  for (int j = 0; j < nt; ++j) {
+    P.term[j].grad_out = grad_outs[j0 + j];
+    P.term[j].coef = coefs[j0 + j];
+    P.term[j].qfold = qfolds[j0 + j];
+    P.term[j].coef_ld = coef_lds[j0 + j];
+  }
+}
+
+// Grid of the segment kernel for (nch, nb): its workgroups per CU, at most one
+// wave per row part.
+static int seg_grid(const DeviceState& st, int nch, int nb, int64_t num_tokens) {
+  const int per_cu = tuning().gather_per_cu > 0 ? tuning().gather_per_cu : gather_seg_per_cu(nch, nb);
+  const int64_t need_wg = (num_tokens * gather_seg_parts(nch, nb) + kGatherWaves - 1) / kGatherWaves;
+  const int64_t cap = (int64_t)st.num_cus * per_cu;
+  return (int)(need_wg < cap ? need_wg : cap);
+}
+
+// One block's sum of deferred gradient terms: the segment kernel with one
+// block (no running sum in), one launch per ATTNRES_SEG_MAX_TERMS terms, each
+// finishing the block (its own c2 sum times x) onto the one before (the
+// caller's addend for the first).
 int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int64_t x_ld, int dtype, int num_terms,
                              const void* const* grad_outs, int64_t grad_out_ld, const float* const* coefs,
                              const int64_t* coef_lds, const void* const* qfolds, const void* addend, void* out,
@@ -1447,48 +1456,33 @@ int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int6
                   (long long)coef_lds[j]);
   }
   if (num_tokens == 0) return ATTNRES_OK;
-  if (num_tokens >= (int64_t)1 << 31) return fail(ATTNRES_ERR_UNSUPPORTED, "num_tokens >= 2^31");
+  const int nch = hidden / 512;
+  if (num_tokens * gather_seg_parts(nch, 1) >= ((int64_t)1 << 31))
+    return fail(ATTNRES_ERR_UNSUPPORTED, "num_tokens too large");
   DeviceState* st = nullptr;
   int rc = ensure_loaded(&st);
   if (rc != ATTNRES_OK) return rc;
-  const int nch = hidden / 512;
   hipFunction_t f = nullptr;
-  rc = get_gather(*st, nch, &f);
+  rc = get_gather_seg(*st, nch, 1, &f);
   if (rc != ATTNRES_OK) return rc;
-  const int per_cu = tuning().gather_per_cu > 0 ? tuning().gather_per_cu : kGatherPerCu;
-  const int64_t need_wg = (num_tokens + kGatherWaves - 1) / kGatherWaves;
-  const int64_t cap = (int64_t)st->num_cus * per_cu;
-  const int grid = (int)(need_wg < cap ? need_wg : cap);
-  // staged rows: as many as the LDS holds for per_cu workgroups, at most the default
-  const int64_t row_bytes = (int64_t)hidden * 2;
-  int batch = tuning().gather_batch > 0 ? tuning().gather_batch : kGatherBatch;
-  const int64_t fit = (int64_t)st->max_lds / per_cu / (kGatherWaves * row_bytes);
-  if (batch > fit) batch = (int)fit;
-  if (batch < 1) batch = 1;
-  const size_t lds = batch > 1 ? (size_t)kGatherWaves * batch * row_bytes : 0;
-  attnres_route_bwd_gather_params P;
+  const int grid = seg_grid(*st, nch, 1, num_tokens);
+  attnres_route_bwd_gather_seg_params P;
   int j0 = 0;
   do {
-    const int nt = num_terms - j0 < ATTNRES_GATHER_MAX_TERMS ? num_terms - j0 : ATTNRES_GATHER_MAX_TERMS;
+    const int nt = num_terms - j0 < ATTNRES_SEG_MAX_TERMS ? num_terms - j0 : ATTNRES_SEG_MAX_TERMS;
     std::memset(&P, 0, sizeof(P));
     P.x = x;
     P.addend = j0 == 0 ? addend : out;
-    P.out = out;
     P.n_tokens = num_tokens;
     P.x_ld = x_ld;
     P.gout_ld = grad_out_ld;
     P.out_ld = out_ld;
     P.d = hidden;
-    P.num_terms = nt;
     P.block = 64 * kGatherWaves;
-    P.out_batch = batch;
-    for (int j = 0; j < nt; ++j) {
-      P.term[j].grad_out = grad_outs[j0 + j];
-      P.term[j].coef = coefs[j0 + j];
-      P.term[j].qfold = qfolds[j0 + j];
-      P.term[j].coef_ld = coef_lds[j0 + j];
-    }
-    rc = launch(f, grid, 64 * kGatherWaves, P, stream, 1, lds);
+    P.final_block = 1;
+    seg_terms(P, j0, nt, grad_outs, coefs, coef_lds, qfolds);
+    P.blk[0].part_out = out;
+    rc = launch(f, grid, 64 * kGatherWaves, P, stream, 1, 0);
     if (rc != ATTNRES_OK) return rc;
     j0 += nt;
   } while (j0 < num_terms);
@@ -1545,10 +1539,7 @@ int attnres_route_bwd_gather_seg(int num_blocks, int64_t num_tokens, int hidden,
   hipFunction_t f = nullptr;
   rc = get_gather_seg(*st, nch, num_blocks, &f);
   if (rc != ATTNRES_OK) return rc;
-  const int per_cu = tuning().gather_per_cu > 0 ? tuning().gather_per_cu : gather_seg_per_cu(nch, num_blocks);
-  const int64_t need_wg = (num_tokens * parts + kGatherWaves - 1) / kGatherWaves;
-  const int64_t cap = (int64_t)st->num_cus * per_cu;
-  const int grid = (int)(need_wg < cap ? need_wg : cap);
+  const int grid = seg_grid(*st, nch, num_blocks, num_tokens);
   attnres_route_bwd_gather_seg_params P;
   int j0 = 0;
   do {
@@ -1562,15 +1553,9 @@ int attnres_route_bwd_gather_seg(int num_blocks, int64_t num_tokens, int hidden,
     P.gout_ld = grad_out_ld;
     P.out_ld = out_ld;
     P.d = hidden;
-    P.num_terms = nt;
     P.block = 64 * kGatherWaves;
     P.final_block = last ? 1 : 0;
-    for (int j = 0; j < nt; ++j) {
-      P.term[j].grad_out = grad_outs[j0 + j];
-      P.term[j].coef = coefs[j0 + j];
-      P.term[j].qfold = qfolds[j0 + j];
-      P.term[j].coef_ld = coef_lds[j0 + j];
-    }
+    seg_terms(P, j0, nt, grad_outs, coefs, coef_lds, qfolds);
     for (int k = 0; k < num_blocks; ++k) {
       // later launches continue from the running sums the earlier ones stored
       P.blk[k].part_in = j0 == 0 ? (part_in != nullptr ? part_in[k] : nullptr) : part_out[k];

@@ -2377,176 +2377,9 @@ __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_pa
 }
 
 
-// ---------------------------------------------- deferred-gradient sum --
-//
-// One committed block's gradient from the coefficients the `_defer`
-// backward kernels stored, one wave per token row (grid-stride; a resident
-// grid of 4-wave workgroups), bf16 rows of NCH KiB:
-//   out = addend + sum_j (w_j G_j + c1_j q_j) + (sum_j c2_j) x
-// A row's items stream through a two-slot pipeline (the next item is
-// requested once the current one has arrived, as in stream_body): per term j
-// its coefficient record, its folded query q_j (read by every row: it stays
-// in L2) and its output-gradient row G_j; then the block's row x; then the
-// addend row (an empty buffer resource when there is none: its loads return
-// 0 without a memory access).  fp32 accumulators, one rounding at the store;
-// finished rows are stored at once or staged in LDS and stored in bursts.
+// Non-temporal row load: a row read once.
 __device__ __forceinline__ u32x4 ld_row_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);  // nt: read once
-}
-
-template <int NCH>
-__device__ __forceinline__ void route_bwd_gather_body(const attnres_route_bwd_gather_params& P) {
-  constexpr uint32_t RB = NCH * 1024;
-  const int lane = threadIdx.x & 63;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t nwv = (uint32_t)P.block >> 6;
-  const uint32_t n_tok = (uint32_t)P.n_tokens;
-  const uint32_t nw = gridDim.x * nwv;
-  const uint32_t tok0 = blockIdx.x * nwv + wave;
-  if (tok0 >= n_tok) return;
-  const uint32_t rows = (n_tok - tok0 - 1) / nw + 1;
-  const uint32_t nt = (uint32_t)P.num_terms;
-  const uint32_t per = nt + 2;
-  const uint32_t lane_off = (uint32_t)lane * 16;
-
-  // item r of the wave's row j; past the wave's last item, that item again
-  auto issue = [&](u32x4(&row)[NCH], u32x4(&q)[NCH], u32x4& cf, uint32_t j, uint32_t r, uint32_t z) {
-    if (j >= rows) {
-      j = rows - 1;
-      r = per - 1;
-    }
-    j = __builtin_amdgcn_readfirstlane(j);
-    r = __builtin_amdgcn_readfirstlane(r);
-    const uint64_t t = tok0 + (uint64_t)j * nw;
-    char* rbase;
-    uint32_t rbytes = RB;
-    char* qbase = nullptr;
-    char* cbase = nullptr;
-    if (r < nt) {
-      const attnres_gather_term& T = P.term[r];
-      rbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(T.grad_out) + t * (uint64_t)P.gout_ld * 2));
-      qbase = const_cast<char*>(static_cast<const char*>(T.qfold));
-      cbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(T.coef) + t * (uint64_t)T.coef_ld * 4));
-    } else if (r == nt) {
-      rbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.x) + t * (uint64_t)P.x_ld * 2));
-    } else {
-      rbase = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.addend) + t * (uint64_t)P.out_ld * 2));
-      rbytes = P.addend != nullptr ? RB : 0u;
-    }
-    const __amdgpu_buffer_rsrc_t rc = row_rsrc(cbase, cbase != nullptr ? 16u : 0u);
-    const __amdgpu_buffer_rsrc_t rq = row_rsrc(qbase, qbase != nullptr ? RB : 0u);
-    const __amdgpu_buffer_rsrc_t rr = row_rsrc(rbase, rbytes);
-    // record and query first: rows return in order, so the row's arrival implies theirs
-    cf = __builtin_amdgcn_raw_buffer_load_b128(rc, z, 0, 0);
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) q[c] = __builtin_amdgcn_raw_buffer_load_b128(rq, lane_off + (uint32_t)(c * 1024) + z, 0, 0);
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) row[c] = ld_row_nt(rr, lane_off + (uint32_t)(c * 1024) + z);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  float acc[NCH][8];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
-  }
-  float csum = 0.f;
-  // Finished rows staged in dynamic LDS, P.out_batch per wave ([row][chunk][lane],
-  // 16 bytes per lane: no bank conflicts; a wave reads back only what its own
-  // lanes wrote, so no barrier), stored in bursts between the reads.
-  extern __shared__ u32x4 gather_stage[];
-  const uint32_t batch = (uint32_t)P.out_batch;
-  u32x4* my_stage = gather_stage + (size_t)wave * batch * NCH * 64 + lane;
-  uint32_t nheld = 0, jfirst = 0;
-  // item (j, r) of the wave's rows; (j, r) wave-uniform, passed by value
-  auto process = [&](u32x4(&row)[NCH], u32x4(&q)[NCH], const u32x4& cf, uint32_t j, uint32_t r) {
-    float a, b;
-    if (r < nt) {
-      a = as_f32(cf[0]);
-      b = as_f32(cf[1]);
-      csum += as_f32(cf[2]);
-    } else {
-      a = r == nt ? csum : 1.0f;
-      b = 0.f;
-    }
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        acc[c][2 * w] = __builtin_fmaf(a, bf_lo(row[c][w]), __builtin_fmaf(b, bf_lo(q[c][w]), acc[c][2 * w]));
-        acc[c][2 * w + 1] = __builtin_fmaf(a, bf_hi(row[c][w]), __builtin_fmaf(b, bf_hi(q[c][w]), acc[c][2 * w + 1]));
-      }
-    }
-    if (r == per - 1) {
-      if (batch > 1) {
-        // stage the row; the wave's rows are stored together when `batch`
-        // are held or at its last row
-        if (nheld == 0) jfirst = j;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          u32x4 pk;
-#pragma unroll
-          for (int w = 0; w < 4; ++w) pk[w] = pack_bf16(acc[c][2 * w], acc[c][2 * w + 1]);
-          my_stage[(nheld * NCH + c) * 64] = pk;
-        }
-        nheld = __builtin_amdgcn_readfirstlane(nheld + 1);
-        if (nheld == batch || j + 1 == rows) {
-          for (uint32_t h = 0; h < nheld; ++h) {
-            const uint64_t t = tok0 + (uint64_t)(jfirst + h) * nw;
-            char* orow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.out) + t * (uint64_t)P.out_ld * 2));
-            const __amdgpu_buffer_rsrc_t ro = row_rsrc(orow, RB);
-#pragma unroll
-            for (int c = 0; c < NCH; ++c) st_row_nt(ro, lane_off + (uint32_t)(c * 1024), my_stage[(h * NCH + c) * 64]);
-          }
-          nheld = 0;
-        }
-      } else {
-        const uint64_t t = tok0 + (uint64_t)j * nw;
-        char* orow = const_cast<char*>(uniform_ptr(reinterpret_cast<uint64_t>(P.out) + t * (uint64_t)P.out_ld * 2));
-        const __amdgpu_buffer_rsrc_t ro = row_rsrc(orow, RB);
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          u32x4 pk;
-#pragma unroll
-          for (int w = 0; w < 4; ++w) pk[w] = pack_bf16(acc[c][2 * w], acc[c][2 * w + 1]);
-          st_row_nt(ro, lane_off + (uint32_t)(c * 1024), pk);
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
-      }
-      csum = 0.f;
-    }
-  };
-  // the item after (j, r), wave-uniform
-  auto after = [per](uint32_t& j, uint32_t& r) {
-    const uint32_t r1 = r + 1;
-    const bool wrap = r1 == per;
-    r = __builtin_amdgcn_readfirstlane(wrap ? 0u : r1);
-    j = __builtin_amdgcn_readfirstlane(wrap ? j + 1 : j);
-  };
-
-  u32x4 ra[NCH], qa[NCH], rb2[NCH], qb[NCH], ca, cb;
-  uint32_t ji = 0, ri = 0;  // the item issued next
-  uint32_t jp = 0, rp = 0;  // the item processed next
-  issue(ra, qa, ca, ji, ri, 0u);
-  after(ji, ri);
-  const uint32_t items = rows * per;
-  for (uint32_t i = 0; i < items; i += 2) {
-    issue(rb2, qb, cb, ji, ri, arrival_zero(ra[NCH - 1][3]));
-    after(ji, ri);
-    process(ra, qa, ca, jp, rp);
-    after(jp, rp);
-    issue(ra, qa, ca, ji, ri, arrival_zero(rb2[NCH - 1][3]));
-    after(ji, ri);
-    if (i + 1 < items) {
-      process(rb2, qb, cb, jp, rp);
-      after(jp, rp);
-    }
-  }
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
 }
 
 // ------------------------------------------- segment of deferred sums --
@@ -4199,17 +4032,11 @@ BWD_S_ADD(16)
 // Deferred block gradients (the training loop's routing points):
 // attnres_route_bwd_stream_c<NCH>_s<S>_defer, the row-per-wave backward that
 // forms only the last source's gradient and stores the committed sources'
-// coefficients, and attnres_route_bwd_gather_c<NCH>, which sums one block's
-// gradient from them.
+// coefficients (summed by the segment kernels below).
 #define BWD_STREAM_ONE_DEFER(S, NCH, KL)                                                                \
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))            \
       attnres_route_bwd_stream_c##NCH##_s##S##_defer(attnres_route_bwd_params P) {                       \
     route_bwd_stream_body<S, NCH, KL, true, true>(P);                                                   \
-  }
-#define GATHER_ONE(NCH)                                                                                 \
-  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))            \
-      attnres_route_bwd_gather_c##NCH(attnres_route_bwd_gather_params P) {                               \
-    route_bwd_gather_body<NCH>(P);                                                                      \
   }
 
 #if ATTNRES_PART == 10 || defined(ATTNRES_ALL_PARTS)
@@ -4219,7 +4046,6 @@ BWD_STREAM_ONE_DEFER(8, 6, 0)
 BWD_STREAM_ONE_DEFER(2, 8, 0) BWD_STREAM_ONE_DEFER(3, 8, 0) BWD_STREAM_ONE_DEFER(4, 8, 0)
 BWD_STREAM_ONE_DEFER(5, 8, 0) BWD_STREAM_ONE_DEFER(6, 8, 0) BWD_STREAM_ONE_DEFER(7, 8, 1)
 BWD_STREAM_ONE_DEFER(8, 8, 2) BWD_STREAM_ONE_DEFER(9, 8, 3)
-GATHER_ONE(6) GATHER_ONE(8)
 #endif
 
 // Segments of deferred sums (the instances in ATTNRES_SEG_INSTANCES), a wave

@@ -103,36 +103,14 @@ typedef struct attnres_route_bwd_params {
   float inv_d;
 } attnres_route_bwd_params;
 
-/*
- * One block's gradient from the coefficients the `_defer` kernels left, for
- * every token t:
- *   out = addend + sum_j (w_j G_j + c1_j qfold_j) + (sum_j c2_j) x
- * with (w_j, c1_j, c2_j) at term[j].coef + t*coef_ld floats.  bf16 rows and
- * folded queries; out may be addend (in place).
- */
-#define ATTNRES_GATHER_MAX_TERMS 48
+/* One point's deferred gradient terms: its dL/dout rows, the coefficient
+ * records its `_defer` backward stored and its folded query. */
 typedef struct attnres_gather_term {
   const void* grad_out;  /* (n_tokens, d), row stride gout_ld */
-  const float* coef;     /* token 0's (w, c1, c2, -) */
+  const float* coef;     /* token 0's (w, c1, c2, -) of the first block */
   const void* qfold;     /* (d,) */
-  int64_t coef_ld;       /* floats from one token's record to the next */
+  int64_t coef_ld;       /* floats from one token's records to the next */
 } attnres_gather_term;
-
-typedef struct attnres_route_bwd_gather_params {
-  const void* x;       /* (n_tokens, d), row stride x_ld */
-  const void* addend;  /* (n_tokens, d), row stride out_ld, or NULL */
-  void* out;           /* (n_tokens, d), row stride out_ld */
-  int64_t n_tokens;
-  int64_t x_ld;
-  int64_t gout_ld;
-  int64_t out_ld;
-  int32_t d;
-  int32_t num_terms;   /* 0 .. ATTNRES_GATHER_MAX_TERMS */
-  int32_t block;       /* threads per workgroup */
-  int32_t out_batch;   /* finished rows each wave stages in (dynamic) LDS and stores
-                          together; 1 = store each row at once */
-  attnres_gather_term term[ATTNRES_GATHER_MAX_TERMS];
-} attnres_route_bwd_gather_params;
 
 /*
  * One segment of the training loop's deferred gradients: the terms of the
@@ -149,7 +127,7 @@ typedef struct attnres_route_bwd_gather_params {
  * csum_out (in place).
  */
 #define ATTNRES_SEG_MAX_BLOCKS 8
-#define ATTNRES_SEG_MAX_TERMS 16
+#define ATTNRES_SEG_MAX_TERMS 48
 /*
  * The compiled segment kernels, attnres_route_bwd_gather_seg_c<NCH>_b<NB>:
  * X(NCH row KiB, NB blocks, CPW KiB per wave part, DEPTH ring slots, WPE waves
@@ -178,7 +156,7 @@ typedef struct attnres_route_bwd_gather_seg_params {
   int64_t gout_ld;
   int64_t out_ld;
   int32_t d;
-  int32_t num_terms;   /* 1 .. ATTNRES_SEG_MAX_TERMS */
+  int32_t num_terms;   /* 0 .. ATTNRES_SEG_MAX_TERMS */
   int32_t block;       /* threads per workgroup */
   int32_t final_block; /* 1: the last block takes x and the addend and stores its gradient;
                           0: it is stored like the others (running sum + csum_out) */

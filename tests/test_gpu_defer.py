@@ -326,13 +326,13 @@ def test_gather_seg_sums_a_segment(gpu, nb, P, n, d):
 
 
 def test_gather_seg_more_terms_than_one_launch(gpu):
-    # 20 points over 2 blocks: two launches, the second continuing from the
+    # 52 points over 2 blocks: two launches, the second continuing from the
     # first's running sums (the last block's x-coefficient sum in the scratch
     # csum_out[last]); the last block's gradient against the oracle's sum, the
     # bar widened by half an ulp of the running sum the first launch rounds
     from .test_gpu_backward import bf16_ulp
 
-    n, d, nb, P = 256, 3072, 2, 20
+    n, d, nb, P = 256, 3072, 2, 52
     g = torch.Generator(device=gpu).manual_seed(91)
     blocks = [torch.randn((n, d), generator=g, device=gpu).to(torch.bfloat16) for _ in range(nb)]
     terms, dx, first = [], [], np.zeros((n, d))
@@ -343,7 +343,7 @@ def test_gather_seg_more_terms_than_one_launch(gpu):
         gain = torch.ones(d, device=gpu, dtype=torch.bfloat16)
         _, coef, qfold, _, _ = _defer(gpu, blocks + [own], q, gain, gout)
         terms.append((gout, coef, qfold))
-        if p < 16:  # the running sum the first launch rounds (without its x term)
+        if p < _capi.SEG_MAX_TERMS:  # the running sum the first launch rounds (without its x term)
             c = coef.double().cpu().numpy()
             first += c[:, 1, 0:1] * np64(gout) + c[:, 1, 1:2] * np64(qfold)[None, :]
         dx.append(O.route_backward(np.stack([np64(t) for t in blocks + [own]]),
@@ -362,4 +362,4 @@ def test_gather_seg_more_terms_than_one_launch(gpu):
     want = sum(x[1] for x in dx)
     err = np.abs(np64(out) - want)
     bar = bf16_ulp(want) + 0.5 * bf16_ulp(first) + 1e-3 * np.abs(want).max()
-    assert (err <= bar).all(), f"20 terms: worst err {err.max():.3e}"
+    assert (err <= bar).all(), f"{P} terms: worst err {err.max():.3e}"
