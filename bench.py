@@ -39,6 +39,8 @@ steps over one arena: (S+3) rows per point, S+2 right after a commit).
 ``cfg2train`` times the reference's training step on the routing path at the
 3B shape (forward under autograd + backward; ``--variant list|stack``,
 ``--compile`` for torch.compile with inductor).
+``--workload segsum`` times the training step's deferred-gradient segment sums
+(attnres_route_bwd_gather_seg) per block count at the 3B and 8B shapes.
 ``--workload mall`` checks what the 256 MB last-level cache serves of a call's
 bytes (the dominant calls back to back vs after other memory traffic).
 ``--gpus`` above 1 exits: this build measures one GPU.
@@ -73,6 +75,8 @@ WORKLOAD_TEXT = {
     "(Q=8, S=1..7) + 7 phase-2 merges per block, final phase 1 (S=8); D=3072, B=8, T=4096, bf16",
     "cfg2train": "3B training step (train.py:610-614 on llama.py:666-716): forward of the 57-point routing loop "
     "under autograd + backward, D=3072, B=8, T=4096, bf16 model; sublayers x*0.5 (no GEMMs)",
+    "segsum": "the training step's deferred-gradient segment sums alone: 8 points' terms into 1..8 blocks, "
+    "D=3072 x 32768 rows and D=4096 x 16384 rows, bf16",
 }
 
 
@@ -702,6 +706,63 @@ def train_path_bytes(w) -> tuple[int, int]:
     return fwd, bwd
 
 
+def bench_segsum(steps: int, warmup: int, dev) -> dict:
+    """attnres_route_bwd_gather_seg, the training loop's deferred-gradient sums, per block count:
+    8 points' terms summed into blocks 0..NB-1 (blocks 0..NB-2 continuing running sums, the last one
+    finished with x and an addend), at the 3B (D=3072, 32768 rows) and 8B (D=4096, 16384 rows)
+    shapes; HIP events around each launch, median over the steps."""
+    import torch
+
+    from kotodama_amd import _capi
+
+    P = 8
+    out = {}
+    for d, n in ((3072, 32768), (4096, 16384)):
+        g = torch.Generator(device=dev).manual_seed(d)
+        gouts = [torch.randn((n, d), generator=g, device=dev).to(torch.bfloat16) for _ in range(P)]
+        qfolds = [(torch.randn(d, generator=g, device=dev) * 0.05).to(torch.bfloat16) for _ in range(P)]
+        coefs = [torch.randn((n, 8, 4), generator=g, device=dev) * 0.1 for _ in range(P)]
+        x = torch.randn((n, d), generator=g, device=dev).to(torch.bfloat16)
+        addend = torch.randn((n, d), generator=g, device=dev).to(torch.bfloat16)
+        part_in = [torch.randn((n, d), generator=g, device=dev).to(torch.bfloat16) for _ in range(7)]
+        csum_in = [torch.randn(n, generator=g, device=dev) for _ in range(7)]
+        part_out = [torch.empty((n, d), device=dev, dtype=torch.bfloat16) for _ in range(8)]
+        csum_out = [torch.empty(n, device=dev) for _ in range(8)]
+        row = n * d * 2
+        rows = {}
+        for nb in range(1, 9):
+            args = (nb, n, d, _capi.DTYPE_BF16, P, _capi.pointer_array([t.data_ptr() for t in gouts]), d,
+                    _capi.pointer_array([c.data_ptr() for c in coefs]), _capi.int64_array([32] * P),
+                    _capi.pointer_array([q.data_ptr() for q in qfolds]),
+                    _capi.pointer_array([part_in[k].data_ptr() if k < nb - 1 else None for k in range(nb)]),
+                    _capi.pointer_array([csum_in[k].data_ptr() if k < nb - 1 else None for k in range(nb)]),
+                    _capi.pointer_array([part_out[k].data_ptr() for k in range(nb)]),
+                    _capi.pointer_array([csum_out[k].data_ptr() if k < nb - 1 else None for k in range(nb)]),
+                    x.data_ptr(), d, addend.data_ptr(), d, torch.cuda.current_stream(dev).cuda_stream)
+            for _ in range(warmup):
+                _capi.route_bwd_gather_seg(*args)
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(steps):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                _capi.route_bwd_gather_seg(*args)
+                b.record()
+                b.synchronize()
+                ts.append(a.elapsed_time(b))
+            ms = statistics.median(ts)
+            # read: the P dL/dout rows, NB-1 running sums, x, the addend, the P x NB records and NB-1
+            # x-coefficient sums; written: NB rows and NB-1 coefficient sums
+            nbytes = (P + (nb - 1) + 2 + nb) * row + P * n * nb * 16 + 2 * (nb - 1) * n * 4
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            rows[f"b{nb}"] = {"us": round(ms * 1e3, 1), "algorithmic_bytes": nbytes, "GB/s": round(gbs, 1),
+                              "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        out[f"d{d}"] = rows
+        del gouts, qfolds, coefs, x, addend, part_in, csum_in, part_out, csum_out
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool) -> dict:
     """cfg2train: the reference's training step on the routing path at the 3B shape.
 
@@ -924,6 +985,10 @@ def main() -> int:
             "routing_GB/s_over_step": round(gbs, 2), "hbm_frac_routing_bytes": round(gbs / HBM_PEAK_GBS, 4),
             **rec,
         }), flush=True)
+        return 0
+    if args.workload == "segsum":
+        print(json.dumps({"workload": WORKLOAD_TEXT["segsum"], "steps": args.steps, "warmup": args.warmup,
+                          **bench_segsum(args.steps, args.warmup, dev)}), flush=True)
         return 0
     if args.workload == "mall":
         print(json.dumps({"workload": WORKLOAD_TEXT["mall"], "steps": args.steps, "warmup": args.warmup,
