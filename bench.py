@@ -18,8 +18,8 @@ Also on the JSON line:
 * ``cfg2_bwd`` — the backward of cfg2's 57 routing calls (the training path):
   (2S+1) rows per call, with a ``roofline`` block for the S=8 backward.
 * ``cfg4`` (the 8B decode step), ``cfg2arena`` (the stack-free prefill) and
-  ``cfg2train`` (the 3B training step, at most 5 steps) — as their own
-  ``--workload`` runs report them.
+  ``cfg2train`` / ``cfg3train`` (the 3B and 8B training steps, at most 5 steps)
+  — as their own ``--workload`` runs report them.
 * ``cpu_baseline`` — the reference's CPU routing path (oracle/torch_cpu_path:
   the einsum-branch op sequence over the padded buffer, fp32) timed on this
   host on a bounded sample (the whole call schedule over 4096 token rows, at
@@ -38,7 +38,8 @@ backward of each phase-1 call, (3S+Q) rows, and the merge backward, 5 rows).
 steps over one arena: (S+3) rows per point, S+2 right after a commit).
 ``cfg2train`` times the reference's training step on the routing path at the
 3B shape (forward under autograd + backward; ``--variant list|stack``,
-``--compile`` for torch.compile with inductor).
+``--compile`` for torch.compile with inductor), ``cfg3train`` the same at the
+8B model's schedule (32 layers, 65 points, S up to 9; D=4096, B=4, T=4096).
 ``--workload segsum`` times the training step's deferred-gradient segment sums
 (attnres_route_bwd_gather_seg) per block count at the 3B and 8B shapes.
 ``--workload mall`` checks what the 256 MB last-level cache serves of a call's
@@ -75,6 +76,8 @@ WORKLOAD_TEXT = {
     "(Q=8, S=1..7) + 7 phase-2 merges per block, final phase 1 (S=8); D=3072, B=8, T=4096, bf16",
     "cfg2train": "3B training step (train.py:610-614 on llama.py:666-716): forward of the 57-point routing loop "
     "under autograd + backward, D=3072, B=8, T=4096, bf16 model; sublayers x*0.5 (no GEMMs)",
+    "cfg3train": "8B training step (train.py:610-614 on llama.py:666-716): forward of the 65-point routing loop "
+    "(32 layers / 8 blocks, S up to 9) under autograd + backward, D=4096, B=4, T=4096, bf16 model; sublayers x*0.5",
     "segsum": "the training step's deferred-gradient segment sums alone: 8 points' terms into 1..8 blocks, "
     "D=3072 x 32768 rows and D=4096 x 16384 rows, bf16",
 }
@@ -89,10 +92,10 @@ def parse_args():
     ap.add_argument("--pass", dest="pass_", default="fwd", choices=("fwd", "bwd"),
                     help="time the routing forward (default) or its backward")
     ap.add_argument("--variant", default="list", choices=("list", "stack"),
-                    help="cfg2train: forward_attn_res under autograd (list) or the reference loop with "
+                    help="cfg2train / cfg3train: forward_attn_res under autograd (list) or the reference loop with "
                          "route_static and its per-call stacks (stack)")
     ap.add_argument("--compile", action="store_true",
-                    help="cfg2train: run the forward under torch.compile(fullgraph=True, backend='inductor')")
+                    help="cfg2train / cfg3train: run the forward under torch.compile(fullgraph=True, backend='inductor')")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", action="store_true",
                     help="cfg2: measure the sweep alone, without the other workloads' records (for profiling)")
@@ -763,8 +766,8 @@ def bench_segsum(steps: int, warmup: int, dev) -> dict:
     return out
 
 
-def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool) -> dict:
-    """cfg2train: the reference's training step on the routing path at the 3B shape.
+def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool, name: str = "cfg2train") -> dict:
+    """cfg2train / cfg3train: the reference's training step on the routing path at the 3B / 8B shape.
 
     A model with the reference's AttnRes attributes (workloads.TrainingModel:
     bf16 queries and gains, trainable; sublayers ``x * 0.5``) runs the forward
@@ -779,7 +782,7 @@ def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool) -> d
 
     from kotodama_amd import engine, routing, workloads
 
-    w = workloads.get("cfg2")
+    w = workloads.get("cfg3train" if name == "cfg3train" else "cfg2")
     model = workloads.TrainingModel(w, dev, seed=8)
     gen = torch.Generator(device=dev).manual_seed(9)
     embed = torch.randn((w.batch, w.seq, w.hidden), generator=gen, device=dev).to(w.dtype).requires_grad_(True)
@@ -807,7 +810,7 @@ def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool) -> d
 
     t_first = time.perf_counter()
     for i in range(warmup):
-        print(f"cfg2train {variant}{' compiled' if compiled else ''}: warm-up step {i}", flush=True)
+        print(f"{name} {variant}{' compiled' if compiled else ''}: warm-up step {i}", flush=True)
         step([])
         torch.cuda.synchronize()
     first_s = time.perf_counter() - t_first
@@ -920,12 +923,13 @@ def secondary_arena(steps: int, warmup: int, dev) -> dict:
                          "algorithmic_bytes": dom_bytes, "avg_ms": round(dom_ms, 4)}}
 
 
-def secondary_train(steps: int, warmup: int, dev) -> dict:
-    """cfg2train (the 3B training step on the routing path, stack-free drop-in, eager), measured in the same run."""
-    rec = bench_train(steps, warmup, dev, "list", False)
+def secondary_train(steps: int, warmup: int, dev, name: str = "cfg2train") -> dict:
+    """cfg2train / cfg3train (the 3B / 8B training step on the routing path, stack-free drop-in, eager),
+    measured in the same run."""
+    rec = bench_train(steps, warmup, dev, "list", False, name)
     rb = rec["routing_kernel_bytes"]
     gbs = (rb["fwd"] + rb["bwd"]) / (rec["ms_per_step"] * 1e-3) / 1e9
-    return {"workload": WORKLOAD_TEXT["cfg2train"], "variant": "list (forward_attn_res under autograd)",
+    return {"workload": WORKLOAD_TEXT[name], "variant": "list (forward_attn_res under autograd)",
             "steps": steps, "warmup": warmup, "value": rec["tokens_per_s"], "unit": "tokens/s",
             "routing_GB/s_over_step": round(gbs, 2), **rec}
 
@@ -969,8 +973,8 @@ def main() -> int:
                          "algorithmic_bytes": dom_bytes, "avg_ms": round(dom_ms, 4)},
         }), flush=True)
         return 0
-    if args.workload == "cfg2train":
-        rec = bench_train(args.steps, args.warmup, dev, args.variant, args.compile)
+    if args.workload in ("cfg2train", "cfg3train"):
+        rec = bench_train(args.steps, args.warmup, dev, args.variant, args.compile, args.workload)
         ms = rec["ms_per_step"]
         rb = rec["routing_kernel_bytes"]
         gbs = (rb["fwd"] + rb["bwd"]) / (ms * 1e-3) / 1e9
@@ -980,7 +984,7 @@ def main() -> int:
             "value": rec["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
             "data": "synthetic (seeded embedding, output gradient and routing parameters, resident in HBM)",
-            "config": {"workload": WORKLOAD_TEXT["cfg2train"], "variant": args.variant,
+            "config": {"workload": WORKLOAD_TEXT[args.workload], "variant": args.variant,
                        "compiled": bool(args.compile)},
             "routing_GB/s_over_step": round(gbs, 2), "hbm_frac_routing_bytes": round(gbs / HBM_PEAK_GBS, 4),
             **rec,
@@ -1159,6 +1163,7 @@ def main() -> int:
         line["cfg4"] = secondary_decode(args.steps, args.warmup, dev)
         line["cfg2arena"] = secondary_arena(args.steps, args.warmup, dev)
         line["cfg2train"] = secondary_train(min(args.steps, 5), min(args.warmup, 2), dev)
+        line["cfg3train"] = secondary_train(min(args.steps, 5), min(args.warmup, 2), dev, "cfg3train")
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, min(args.cpu_tokens, w.tokens)) if args.workload != "cfg4" else \
             cpu_baseline(w, w.tokens)

@@ -88,6 +88,11 @@ def get(name: str) -> Workload:
     if name == "cfg4":
         s = _sched_8b()
         return Workload("cfg4", 4096, 256, 1, torch.bfloat16, s, s.max_sources, s.active_counts, 1.0, 1.0, 0.1, 0.1, 1e-5)
+    if name == "cfg3train":
+        # the 8B model's whole routing loop (32 layers, 8 blocks, 65 points, S up to 9) at config 3's shape
+        s = _sched_8b()
+        return Workload("cfg3train", 4096, 4, 4096, torch.bfloat16, s, s.max_sources, s.active_counts, 0.1, 10.0, 0.1,
+                        0.1, 1e-5)
     if name == "cfg5":
         s = _sched_dd()
         return Workload(
