@@ -73,6 +73,20 @@ def route(sources, S=None, N=16, D=64, ld=None, sdt=_capi.DTYPE_BF16, query=FAKE
         out_ld if out_ld is not None else D, N * D, None, None, None, None, None)
 
 
+def test_python_constants_match_the_kernel_parameters():
+    # the ops layer chunks segment sums by these limits; they must be the C side's
+    params = (ROOT / "kotodama_amd" / "csrc" / "attnres_params.h").read_text()
+    for name, value in (("ATTNRES_SEG_MAX_BLOCKS", _capi.SEG_MAX_BLOCKS), ("ATTNRES_SEG_MAX_TERMS", _capi.SEG_MAX_TERMS)):
+        m = re.search(rf"#define {name} (\d+)", params)
+        assert m is not None and int(m.group(1)) == value, name
+    # every (row KiB, block count) the host can ask for has a compiled segment kernel
+    inst = re.findall(r"X\((\d+), (\d+), (\d+), (\d+), (\d+)\)", params)
+    have = {(int(a), int(b)) for a, b, *_ in inst}
+    assert have == {(nch, nb) for nch in (6, 8) for nb in range(1, _capi.SEG_MAX_BLOCKS + 1)}
+    for nch, nb, cpw, depth, wpe in ((int(v) for v in t) for t in inst):
+        assert nch % cpw == 0 and depth >= 2 and 1 <= wpe <= 4, (nch, nb)
+
+
 def test_route_argument_errors():
     ok_src = [FAKE + 4096 * i for i in range(3)]
     assert route(ok_src, N=0) == _capi.OK  # empty launch: returns before any HIP call
