@@ -96,6 +96,9 @@ def parse_args():
                          "route_static and its per-call stacks (stack)")
     ap.add_argument("--compile", action="store_true",
                     help="cfg2train / cfg3train: run the forward under torch.compile(fullgraph=True, backend='inductor')")
+    ap.add_argument("--compile-breaks", action="store_true",
+                    help="cfg2train / cfg3train: torch.compile(backend='inductor') without fullgraph, the routing "
+                         "points run eagerly as graph breaks (kotodama_amd.engine.defer_under_compile)")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", action="store_true",
                     help="cfg2: measure the sweep alone, without the other workloads' records (for profiling)")
@@ -766,7 +769,8 @@ def bench_segsum(steps: int, warmup: int, dev) -> dict:
     return out
 
 
-def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool, name: str = "cfg2train") -> dict:
+def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool, name: str = "cfg2train",
+                breaks: bool = False) -> dict:
     """cfg2train / cfg3train: the reference's training step on the routing path at the 3B / 8B shape.
 
     A model with the reference's AttnRes attributes (workloads.TrainingModel:
@@ -793,9 +797,10 @@ def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool, name
     else:
         def fwd(m, x):
             return engine.forward_attn_res(m, x)
-    if compiled:
+    engine.defer_under_compile(breaks)
+    if compiled or breaks:
         torch._dynamo.reset()
-        fwd = torch.compile(fwd, fullgraph=True, backend="inductor")
+        fwd = torch.compile(fwd, fullgraph=not breaks, backend="inductor")
 
     def step(events):
         model.zero_grad(set_to_none=True)
@@ -810,7 +815,8 @@ def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool, name
 
     t_first = time.perf_counter()
     for i in range(warmup):
-        print(f"{name} {variant}{' compiled' if compiled else ''}: warm-up step {i}", flush=True)
+        print(f"{name} {variant}{' compiled' if compiled else ''}{' compiled (graph breaks)' if breaks else ''}: "
+              f"warm-up step {i}", flush=True)
         step([])
         torch.cuda.synchronize()
     first_s = time.perf_counter() - t_first
@@ -828,7 +834,7 @@ def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool, name
     bwd_rows = sum(2 * s + 1 for s in w.calls)
     ms = elapsed * 1e3 / steps
     extra = {}
-    if variant == "list" and not compiled:
+    if variant == "list" and not compiled and not breaks:
         # what the eager list path's kernels move (fused forward points, deferred backward + per-block sums)
         fb, bb = train_path_bytes(w)
         extra = {"path_kernel_bytes": {"fwd": fb, "bwd": bb},
@@ -974,7 +980,7 @@ def main() -> int:
         }), flush=True)
         return 0
     if args.workload in ("cfg2train", "cfg3train"):
-        rec = bench_train(args.steps, args.warmup, dev, args.variant, args.compile, args.workload)
+        rec = bench_train(args.steps, args.warmup, dev, args.variant, args.compile, args.workload, args.compile_breaks)
         ms = rec["ms_per_step"]
         rb = rec["routing_kernel_bytes"]
         gbs = (rb["fwd"] + rb["bwd"]) / (ms * 1e-3) / 1e9
@@ -985,7 +991,8 @@ def main() -> int:
             "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
             "data": "synthetic (seeded embedding, output gradient and routing parameters, resident in HBM)",
             "config": {"workload": WORKLOAD_TEXT[args.workload], "variant": args.variant,
-                       "compiled": bool(args.compile)},
+                       "compiled": "fullgraph" if args.compile else ("graph breaks at the routing points"
+                                                                      if args.compile_breaks else False)},
             "routing_GB/s_over_step": round(gbs, 2), "hbm_frac_routing_bytes": round(gbs / HBM_PEAK_GBS, 4),
             **rec,
         }), flush=True)

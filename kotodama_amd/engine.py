@@ -145,8 +145,25 @@ def _grad_needed(model, embed: Tensor) -> bool:
     return torch.is_grad_enabled() and (embed.requires_grad or any(p.requires_grad for p in model.parameters()))
 
 
-def _route_points_autograd(model, embed: Tensor, sublayer: Callable[[int, Tensor], Tensor]) -> Tensor:
-    """The caller loop of llama.py:697-715 under autograd, without the stacks.
+_DEFER_UNDER_COMPILE = False
+
+
+def defer_under_compile(enabled: bool = True) -> None:
+    """Under ``torch.compile`` without ``fullgraph`` (the reference compiles its
+    model with ``torch.compile(model)``, train.py:314-324), run each routing
+    point of the training loop eagerly, as a graph break, so that the blocks'
+    gradients are deferred and summed in the segment kernels as in eager mode;
+    the sublayers between the points are still compiled.  Off by default: with
+    ``fullgraph=True`` a graph break is an error, and the points are then
+    ``attnres_hip::route_list`` calls with torch adds that inductor fuses."""
+    global _DEFER_UNDER_COMPILE
+    _DEFER_UNDER_COMPILE = bool(enabled)
+
+
+class _PointLoop:
+    """The routing side of the caller loop of llama.py:697-715 under autograd:
+    the committed blocks, their gradient slots, the partial block and the
+    sublayer output not yet added to it.
 
     Every routing point passes the committed blocks and the partial as
     separate tensors (one pointer per source, no padded ``(max_S, B, T, D)``
@@ -157,55 +174,100 @@ def _route_points_autograd(model, embed: Tensor, sublayer: Callable[[int, Tensor
     In eager mode each point is one ``ops.route_point``: the partial's update
     ``partial + sublayer output`` is formed by the routing kernel into a new
     tensor (attnres_route_step), and in the backward the gradients are summed
-    inside the routing backward kernel — each committed block's over the
+    inside the routing backward kernels — each committed block's over the
     points that read it (``ops.GradSlot``, handed back by the block's commit
-    node) and the partial's routing gradient with the gradient of the partial
-    that the next point routes — so autograd adds no gradients and the loop
-    launches no adds.  Under torch.compile, and at points whose output dtype
-    or sublayer output dtype differs from the blocks', the point is an
-    ``attnres_hip::route_list`` call with torch adds, and autograd sums.
+    node; the points between two commits summed into all their blocks at
+    once, ``ops.GradSegments``) and the partial's routing gradient with the
+    gradient of the partial that the next point routes — so autograd adds no
+    gradients and the loop launches no adds.  Under torch.compile (unless the
+    points run eagerly, :func:`defer_under_compile`), and at points whose
+    output dtype or sublayer output dtype differs from the blocks', the point
+    is an ``attnres_hip::route_list`` call with torch adds, and autograd sums.
     """
-    committed: list[Tensor] = []
-    slots: list[ops.GradSlot] = []
-    segments = ops.GradSegments()  # the blocks' deferred gradients, summed segment by segment
-    dt = embed.dtype
-    fused = ops.accumulating_path_ok(embed)
-    partial: Optional[Tensor] = embed
-    pending: Optional[Tensor] = None  # the sublayer output not yet added to the partial
 
-    def point(query: Tensor, norm) -> Tensor:
-        nonlocal partial, pending
+    def __init__(self, embed: Tensor) -> None:
+        self.committed: list[Tensor] = []
+        self.slots: list[ops.GradSlot] = []
+        self.segments = ops.GradSegments()  # the blocks' deferred gradients, summed segment by segment
+        self.dt = embed.dtype
+        self.fused = ops.accumulating_path_ok(embed)
+        self.partial: Optional[Tensor] = embed
+        self.pending: Optional[Tensor] = None  # the sublayer output not yet added to the partial
+
+    def point(self, query: Tensor, norm) -> Tensor:
         gain = norm.weight
+        dt = self.dt
         out_dtype = torch.promote_types(dt, torch.promote_types(query.dtype, gain.dtype))
-        if (fused and out_dtype == dt and (pending is None or pending.dtype == dt)
-                and ops.accumulating_path_ok(query, gain, partial, pending)):
-            h, partial = ops.route_point(committed, slots, partial, pending, query, gain, float(norm.eps), out_dtype)
+        pending = self.pending
+        if (self.fused and out_dtype == dt and (pending is None or pending.dtype == dt)
+                and ops.accumulating_path_ok(query, gain, self.partial, pending)):
+            h, self.partial = ops.route_point(self.committed, self.slots, self.partial, pending, query, gain,
+                                              float(norm.eps), out_dtype)
         else:
             if pending is not None:
-                partial = partial + pending
-            h = ops.route_list_call(committed + [partial], query, gain, float(norm.eps), out_dtype)[0].squeeze(0)
-        pending = None
+                self.partial = self.partial + pending
+            h = ops.route_list_call(self.committed + [self.partial], query, gain, float(norm.eps), out_dtype)[0]
+            h = h.squeeze(0)
+        self.pending = None
         return h
 
+    def commit(self) -> None:
+        if self.fused:
+            slot = ops.GradSlot(self.segments)
+            self.committed.append(ops.commit_block(self.partial, slot))
+            self.slots.append(slot)
+        else:
+            self.committed.append(self.partial)
+        self.partial = None
+
+    def add(self, d: Tensor) -> None:
+        """The sublayer output ``d``: the new partial right after a commit, else pending."""
+        if self.partial is None:
+            self.partial = d.to(torch.promote_types(self.dt, d.dtype))
+        else:
+            self.pending = d
+
+
+# The same steps as graph breaks: torch.compile runs them eagerly.
+@torch.compiler.disable
+def _eager_loop(embed: Tensor) -> _PointLoop:
+    return _PointLoop(embed)
+
+
+@torch.compiler.disable
+def _eager_point(loop: _PointLoop, query: Tensor, norm) -> Tensor:
+    return loop.point(query, norm)
+
+
+@torch.compiler.disable
+def _eager_commit(loop: _PointLoop) -> None:
+    loop.commit()
+
+
+@torch.compiler.disable
+def _eager_add(loop: _PointLoop, d: Tensor) -> None:
+    loop.add(d)
+
+
+def _route_points_autograd(model, embed: Tensor, sublayer: Callable[[int, Tensor], Tensor]) -> Tensor:
+    """The caller loop of llama.py:697-715 under autograd, without the stacks
+    (:class:`_PointLoop`); under torch.compile with :func:`defer_under_compile`
+    its routing steps run eagerly between the compiled sublayers."""
+    if torch.compiler.is_compiling() and _DEFER_UNDER_COMPILE:
+        loop = _eager_loop(embed)
+        point, commit, add = _eager_point, _eager_commit, _eager_add
+    else:
+        loop = _PointLoop(embed)
+        point, commit, add = _PointLoop.point, _PointLoop.commit, _PointLoop.add
     boundaries = model._attn_res_boundary_set
     for i, layer in enumerate(model.layers):
-        h = point(layer.attn_res_query, layer.attn_res_norm)
+        h = point(loop, layer.attn_res_query, layer.attn_res_norm)
         if i in boundaries:
-            if fused:
-                slot = ops.GradSlot(segments)
-                committed.append(ops.commit_block(partial, slot))
-                slots.append(slot)
-            else:
-                committed.append(partial)
-            partial = None
-        d = sublayer(2 * i, h)
-        if partial is None:
-            partial = d.to(torch.promote_types(dt, d.dtype))
-        else:
-            pending = d
-        h = point(layer.mlp_res_query, layer.mlp_res_norm)
-        pending = sublayer(2 * i + 1, h)
-    return point(model.final_res_query, model.final_res_norm)
+            commit(loop)
+        add(loop, sublayer(2 * i, h))
+        h = point(loop, layer.mlp_res_query, layer.mlp_res_norm)
+        add(loop, sublayer(2 * i + 1, h))
+    return point(loop, model.final_res_query, model.final_res_norm)
 
 
 def forward_attn_res(model, embed: Tensor, mask: Optional[Tensor] = None) -> Tensor:

@@ -160,3 +160,41 @@ def test_blocks_without_grad_and_plain_calls_mix(cpu_kernels, monkeypatch):
     torch.testing.assert_close(loss, loss_ref, rtol=1e-12, atol=1e-12)
     for (n, p), (_, pr) in zip(model.named_parameters(), ref.named_parameters()):
         torch.testing.assert_close(p.grad, pr.grad, rtol=1e-10, atol=1e-12, msg=lambda m, n=n: f"{n}: {m}")
+
+
+@pytest.mark.parametrize("backend", ["eager", "aot_eager"])
+def test_points_run_eagerly_under_compile(cpu_kernels, backend):
+    # engine.defer_under_compile: under torch.compile (no fullgraph) each routing
+    # point, commit and sublayer-output step is a graph break run eagerly, so the
+    # accumulating path (its slots and commit nodes) is the one that runs, with
+    # the sublayers between the points compiled; gradients as plain autograd,
+    # the same write / add pattern as in eager mode, on two compiled calls
+    model = TinyModel(d=32, num_layers=4, boundaries=(0, 2), seed=7).double()
+    ref = copy.deepcopy(model)
+    g = torch.Generator().manual_seed(8)
+    embed = torch.randn((2, 3, 32), generator=g, dtype=torch.float64)
+    G = torch.randn((2, 3, 32), generator=g, dtype=torch.float64)
+    torch._dynamo.reset()
+    fwd = torch.compile(lambda m, e: engine.forward_attn_res(m, e), backend=backend, fullgraph=False)
+    engine.defer_under_compile(True)
+    try:
+        for rep in range(2):
+            cpu_kernels.clear()
+            model.zero_grad(set_to_none=True)
+            e1 = embed.clone().requires_grad_(True)
+            loss = (fwd(model, e1) * G).sum()
+            loss.backward()
+            ref.zero_grad(set_to_none=True)
+            e2 = embed.clone().requires_grad_(True)
+            loss_ref = (training_forward(ref, e2, _ref_route) * G).sum()
+            loss_ref.backward()
+            torch.testing.assert_close(loss, loss_ref, rtol=1e-12, atol=1e-12)
+            got, want = _grads(model, e1), _grads(ref, e2)
+            for k in want:
+                torch.testing.assert_close(got[k], want[k], rtol=1e-10, atol=1e-12,
+                                           msg=lambda m, k=k, rep=rep: f"call {rep} {k}: {m}")
+            assert len(cpu_kernels) == 2 * len(model.layers) + 1, f"call {rep}: the accumulating path did not run"
+            assert cpu_kernels[0][-1] == "write" and all(c[-1] == "add" for c in cpu_kernels[1:])
+    finally:
+        engine.defer_under_compile(False)
+        torch._dynamo.reset()

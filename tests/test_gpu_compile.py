@@ -157,3 +157,71 @@ def test_compiled_stack_free_training_matches_eager_and_float64(gpu):
             assert (p.grad - pe.grad).abs().max().item() <= tol_e, f"it={it} {name}: vs eager"
             checked += 1
         assert checked == len(list(m_comp.parameters()))
+
+
+def test_compiled_training_with_eager_points_defers(gpu, monkeypatch):
+    # kotodama_amd.engine.defer_under_compile: the reference's torch.compile(model)
+    # (no fullgraph) with the routing points run eagerly as graph breaks, so the
+    # blocks' gradients are deferred (attnres_route_bwd_defer per point, segment
+    # sums at the commits) while the sublayers are compiled by inductor; bf16 at
+    # hidden 3072 over 8 layers, two calls, against the reference loop in float64
+    # at the bar of the eager deferred loop test (2x the error of the reference's
+    # own op sequence evaluated in bf16, plus 2^-9 of the largest magnitude)
+    from kotodama_amd import engine
+    from oracle.torch_cpu_path import route_static_cpu
+
+    d = 3072
+    model = TinyModel(d=d, num_layers=8, boundaries=(0, 2, 4, 6), seed=31, elementwise=True)
+    model = model.to(torch.bfloat16).float()
+    gen = torch.Generator().manual_seed(32)
+    embed = (torch.randn((2, 32, d), generator=gen) * 2).to(torch.bfloat16).float()
+    G = torch.randn((2, 32, d), generator=gen).to(torch.bfloat16).float()
+
+    def einsum(buf, q, norm, mask, n):
+        return route_static_cpu(buf, q * norm.weight, norm.eps, mask)
+
+    def run(m, e, fwd):
+        e = e.clone().requires_grad_(True)
+        out = fwd(m, e)
+        (out.float() * G.to(e.device)).sum().backward()
+        grads = {n: p.grad.double().cpu() for n, p in m.named_parameters()}
+        grads["embed"] = e.grad.double().cpu()
+        return out.detach().double().cpu(), grads
+
+    ref = run(copy.deepcopy(model).double(), embed.double(), lambda m, e: training_forward(m, e, einsum))
+    tb = run(copy.deepcopy(model).to(gpu).to(torch.bfloat16), embed.to(gpu).to(torch.bfloat16),
+             lambda m, e: training_forward(m, e, einsum))
+    deferred = []
+    real = ops._route_rows_backward_defer
+
+    def counting(*a, **k):
+        r = real(*a, **k)
+        deferred.append(r is not None)
+        return r
+
+    monkeypatch.setattr(ops, "_route_rows_backward_defer", counting)
+    torch._dynamo.reset()
+    step = torch.compile(lambda m, x: kotodama_amd.forward_attn_res(m, x), backend="inductor", fullgraph=False)
+    m_comp = copy.deepcopy(model).to(gpu).to(torch.bfloat16)
+    engine.defer_under_compile(True)
+    try:
+        for it in range(2):
+            deferred.clear()
+            m_comp.zero_grad(set_to_none=True)
+            ours = run(m_comp, embed.to(gpu).to(torch.bfloat16), step)
+            torch.cuda.synchronize()
+            # every point with a committed block deferred its blocks' gradients
+            assert deferred and all(deferred), f"it={it}: the points did not defer ({deferred})"
+
+            def worst(a, b):
+                return (a - b).abs().max().item()
+
+            assert worst(ours[0], ref[0]) <= 2 * worst(tb[0], ref[0]) + 2.0**-9 * ref[0].abs().max().item(), \
+                f"it={it}: output"
+            for name, want in ref[1].items():
+                e_ours, e_tb = worst(ours[1][name], want), worst(tb[1][name], want)
+                assert e_ours <= 2 * e_tb + 2.0**-9 * want.abs().max().item(), \
+                    f"it={it} {name}: err {e_ours:.3e}, torch bf16 op sequence {e_tb:.3e}"
+    finally:
+        engine.defer_under_compile(False)
+        torch._dynamo.reset()
