@@ -41,7 +41,10 @@
 //     the routing backward with one wave per token row (the training shapes'
 //     bf16 rows of 6 KiB): the row's G and source rows stream through the
 //     same two-slot pipeline, the source rows are kept in registers, and the
-//     gradient rows are stored whole after the row's softmax.
+//     gradient rows are stored whole after the row's softmax; its _defer
+//     instances leave the committed blocks' gradients as per-token
+//     coefficients, which attnres_route_bwd_gather_seg_* sum over the
+//     training loop's points on the matrix cores.
 //
 // S is a template parameter of the row-per-workgroup kernels (register arrays
 // stay in VGPRs) and a runtime argument of the streaming ones; the last slot
@@ -2077,7 +2080,7 @@ __device__ __forceinline__ void route_bwd_body(const attnres_route_bwd_params& P
 // stores the token's (w_s, c1_s, c2_s, 0) to P.coef, and workgroup 0 writes
 // the folded query to P.qfold (bf16 parameters), so that the sum of a
 // block's gradients over the points that read it is formed once, later
-// (route_bwd_gather_body), from the points' output gradients.
+// (route_bwd_gather_seg_body), from the points' output gradients.
 template <int S, int NCH, int KL, bool ADD = false, bool DEFER = false>
 __device__ __forceinline__ void route_bwd_stream_body(const attnres_route_bwd_params& P) {
   static_assert(KL >= 0 && KL < S, "at least one source row is kept in registers");
