@@ -668,3 +668,115 @@ def _training_points_case(gpu, seed, deferred):
         _check_grad_sum(partial.grad, dX, res[1]["dx"][K] + np64(Gp), dtype, f"seed {seed} dpartial")
     if with_delta:
         assert torch.equal(delta.grad, partial.grad), f"seed {seed}: d(partial + delta) differs between its inputs"
+
+
+@pytest.mark.parametrize("seed", range(SEEDS or 12))
+def test_random_gather_seg(gpu, seed):
+    # attnres_route_bwd_gather_seg over random segments: width 3072 or 4096, 1..8
+    # blocks, 1..48 terms (one launch), ragged row counts, padded row strides,
+    # records wider than the blocks summed, running sums and x-coefficient sums
+    # present or absent per block and updated in place or into separate
+    # buffers, the addend absent, separate or in place.  The sums are those of
+    # the kernel's contract (the defer tests pin the records' meaning): float64
+    # sums of the records' terms, each within one bf16 ulp plus 2^-15 of the
+    # sum of the products' magnitudes |w G| + |c1 q| (fp32 accumulation, the
+    # coefficients split into bf16 hi + lo parts: 2^-18 of each product); the
+    # x-coefficient sums within 1e-5 relative; no byte of the padding written
+    rng = np.random.default_rng(31000 + seed)
+    d = [3072, 4096][int(rng.integers(2))]
+    nb = int(rng.integers(1, 9))
+    P = int(rng.integers(1, 49)) if rng.integers(4) == 0 else int(rng.integers(1, 17))
+    n = int(np.exp(rng.uniform(0, np.log(1200))))
+    pad = [8 * int(rng.integers(0, 5)) for _ in range(3)]
+    gout_ld, x_ld, out_ld = d + pad[0], d + pad[1], d + pad[2]
+    extra = int(rng.integers(0, 3))  # records per token beyond the nb summed
+    addend_mode = ["none", "separate", "in_place"][int(rng.integers(3))]
+    print(f"random gather_seg seed={seed}: d={d} nb={nb} P={P} n={n} lds={gout_ld},{x_ld},{out_ld} "
+          f"extra={extra} addend={addend_mode}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(32000 + seed)
+    bf = torch.bfloat16
+    CAN = 7.0
+
+    def rows(ld, scale=1.0):
+        t = torch.full((n, ld), CAN, device=gpu, dtype=bf)
+        t[:, :d] = (torch.randn((n, d), generator=g, device=gpu) * scale).to(bf)
+        return t
+
+    gouts = [rows(gout_ld) for _ in range(P)]
+    qfolds = [(torch.randn(d, generator=g, device=gpu) * 0.1).to(bf) for _ in range(P)]
+    coefs = []
+    for _ in range(P):
+        c = torch.randn((n, nb + extra, 4), generator=g, device=gpu)
+        c[:, :, 2] *= 0.1
+        coefs.append(c)
+    x = rows(x_ld, 2.0)
+    part_out = [torch.full((n, out_ld), CAN, device=gpu, dtype=bf) for _ in range(nb)]
+    csum_out = [torch.full((n,), float("nan"), device=gpu) for _ in range(nb)]
+    part_in, csum_in, prev, prev_cs = [], [], [], []
+    for k in range(nb):
+        has = bool(rng.integers(2)) and k < nb - 1 or (k == nb - 1 and rng.integers(4) == 0)
+        in_place = bool(rng.integers(2))
+        if has:
+            src = part_out[k] if in_place else torch.full((n, out_ld), CAN, device=gpu, dtype=bf)
+            src[:, :d] = (torch.randn((n, d), generator=g, device=gpu) * 0.5).to(bf)
+            cs = csum_out[k] if in_place else torch.empty(n, device=gpu)
+            cs.copy_(torch.randn(n, generator=g, device=gpu) * 0.1)
+            prev.append(np64(src[:, :d]))
+            prev_cs.append(np64(cs))
+            part_in.append(src)
+            csum_in.append(cs)
+        else:
+            prev.append(np.zeros((n, d)))
+            prev_cs.append(np.zeros(n))
+            part_in.append(None)
+            csum_in.append(None)
+    if addend_mode == "none":
+        addend, add64 = None, np.zeros((n, d))
+    else:
+        addend = part_out[nb - 1] if addend_mode == "in_place" else torch.full((n, out_ld), CAN, device=gpu, dtype=bf)
+        if addend_mode == "in_place" and part_in[nb - 1] is not None:
+            addend = torch.full((n, out_ld), CAN, device=gpu, dtype=bf)  # the last block's part_in took that buffer
+        addend[:, :d] = (torch.randn((n, d), generator=g, device=gpu) * 0.1).to(bf)
+        add64 = np64(addend[:, :d])
+    torch.cuda.synchronize()
+    _capi.route_bwd_gather_seg(
+        nb, n, d, _capi.DTYPE_BF16, P, _capi.pointer_array([t.data_ptr() for t in gouts]), gout_ld,
+        _capi.pointer_array([c.data_ptr() for c in coefs]), _capi.int64_array([4 * (nb + extra)] * P),
+        _capi.pointer_array([q.data_ptr() for q in qfolds]),
+        _capi.pointer_array([t.data_ptr() if t is not None else None for t in part_in]),
+        _capi.pointer_array([t.data_ptr() if t is not None else None for t in csum_in]),
+        _capi.pointer_array([t.data_ptr() for t in part_out]),
+        _capi.pointer_array([t.data_ptr() for t in csum_out[:-1]] + [None]),
+        x.data_ptr(), x_ld, addend.data_ptr() if addend is not None else None, out_ld,
+        torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize()
+    C = [np64(c) for c in coefs]
+    Gs = [np64(t[:, :d]) for t in gouts]
+    Q = [np64(q) for q in qfolds]
+
+    def ulp(v):
+        return 2.0 ** (np.floor(np.log2(np.maximum(np.abs(v), 2.0**-126))) - 7)
+
+    for k in range(nb):
+        terms = [c[:, k, 0:1] * Gk + c[:, k, 1:2] * q[None, :] for c, Gk, q in zip(C, Gs, Q)]
+        want = prev[k] + sum(terms)
+        # the products' magnitudes: w G and c1 q enter separately, each coefficient as bf16 hi + lo
+        mag = np.abs(prev[k]) + sum(np.abs(c[:, k, 0:1] * Gk) + np.abs(c[:, k, 1:2] * q[None, :])
+                                    for c, Gk, q in zip(C, Gs, Q))
+        cs = prev_cs[k] + sum(c[:, k, 2] for c in C)
+        if k == nb - 1:
+            xt = cs[:, None] * np64(x[:, :d])
+            want = want + xt + add64
+            mag = mag + np.abs(xt) + np.abs(add64)
+        got = np64(part_out[k][:, :d])
+        err = np.abs(got - want)
+        bar = ulp(want) + 2.0**-15 * mag + 1e-30
+        if not (err <= bar).all():
+            i = np.unravel_index(np.argmax(err / bar), err.shape)
+            raise AssertionError(f"seed {seed} block {k}: worst err/bar {(err / bar)[i]:.2f} at {i}: got {got[i]:.6e} "
+                                 f"want {want[i]:.6e} |terms| {mag[i]:.3e} prev {prev[k][i]:.4e}")
+        if k < nb - 1:
+            e = np.abs(np64(csum_out[k]) - cs)
+            assert (e <= 1e-5 * np.abs(cs) + 1e-6 * np.abs(cs).max() + 1e-30).all(), f"seed {seed} block {k} csum"
+    for t in part_out + gouts + [x] + ([addend] if addend is not None else []):
+        assert torch.all(t[:, d:] == CAN), f"seed {seed}: padding written"
