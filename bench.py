@@ -18,8 +18,8 @@ Also on the JSON line:
 * ``cfg2_bwd`` — the backward of cfg2's 57 routing calls (the training path):
   (2S+1) rows per call, with a ``roofline`` block for the S=8 backward.
 * ``cfg4`` (the 8B decode step), ``cfg2arena`` (the stack-free prefill) and
-  ``cfg2train`` / ``cfg3train`` (the 3B and 8B training steps, at most 5 steps)
-  — as their own ``--workload`` runs report them.
+  ``cfg2train`` / ``cfg3train`` / ``cfg1btrain`` (the 3B, 8B and 1B training
+  steps) — as their own ``--workload`` runs report them.
 * ``cpu_baseline`` — the reference's CPU routing path (oracle/torch_cpu_path:
   the einsum-branch op sequence over the padded buffer, fp32) timed on this
   host on a bounded sample (the whole call schedule over 4096 token rows, at
@@ -39,7 +39,8 @@ steps over one arena: (S+3) rows per point, S+2 right after a commit).
 ``cfg2train`` times the reference's training step on the routing path at the
 3B shape (forward under autograd + backward; ``--variant list|stack``,
 ``--compile`` for torch.compile with inductor), ``cfg3train`` the same at the
-8B model's schedule (32 layers, 65 points, S up to 9; D=4096, B=4, T=4096).
+8B model's schedule (32 layers, 65 points, S up to 9; D=4096, B=4, T=4096) and
+``cfg1btrain`` at the 1B intermediate model's (D=1024, B=4, T=2048).
 ``--workload segsum`` times the training step's deferred-gradient segment sums
 (attnres_route_bwd_gather_seg) per block count at the 3B and 8B shapes.
 ``--workload mall`` checks what the 256 MB last-level cache serves of a call's
@@ -76,6 +77,9 @@ WORKLOAD_TEXT = {
     "(Q=8, S=1..7) + 7 phase-2 merges per block, final phase 1 (S=8); D=3072, B=8, T=4096, bf16",
     "cfg2train": "3B training step (train.py:610-614 on llama.py:666-716): forward of the 57-point routing loop "
     "under autograd + backward, D=3072, B=8, T=4096, bf16 model; sublayers x*0.5 (no GEMMs)",
+    "cfg1btrain": "1B intermediate training step (configs/1b-intermediate.yaml on llama.py:666-716): forward of the "
+    "57-point routing loop (28 layers, DD-v1 boundaries 0,3,7,12,21,25, S up to 7) under autograd + backward, D=1024, "
+    "B=4, T=2048, bf16 model; sublayers x*0.5",
     "cfg3train": "8B training step (train.py:610-614 on llama.py:666-716): forward of the 65-point routing loop "
     "(32 layers / 8 blocks, S up to 9) under autograd + backward, D=4096, B=4, T=4096, bf16 model; sublayers x*0.5",
     "segsum": "the training step's deferred-gradient segment sums alone: 8 points' terms into 1..8 blocks, "
@@ -786,7 +790,7 @@ def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool, name
 
     from kotodama_amd import engine, routing, workloads
 
-    w = workloads.get("cfg3train" if name == "cfg3train" else "cfg2")
+    w = workloads.get(name if name in ("cfg3train", "cfg1btrain") else "cfg2")
     model = workloads.TrainingModel(w, dev, seed=8)
     gen = torch.Generator(device=dev).manual_seed(9)
     embed = torch.randn((w.batch, w.seq, w.hidden), generator=gen, device=dev).to(w.dtype).requires_grad_(True)
@@ -979,7 +983,7 @@ def main() -> int:
                          "algorithmic_bytes": dom_bytes, "avg_ms": round(dom_ms, 4)},
         }), flush=True)
         return 0
-    if args.workload in ("cfg2train", "cfg3train"):
+    if args.workload in ("cfg2train", "cfg3train", "cfg1btrain"):
         rec = bench_train(args.steps, args.warmup, dev, args.variant, args.compile, args.workload, args.compile_breaks)
         ms = rec["ms_per_step"]
         rb = rec["routing_kernel_bytes"]
@@ -1171,6 +1175,7 @@ def main() -> int:
         line["cfg2arena"] = secondary_arena(args.steps, args.warmup, dev)
         line["cfg2train"] = secondary_train(min(args.steps, 5), min(args.warmup, 2), dev)
         line["cfg3train"] = secondary_train(min(args.steps, 5), min(args.warmup, 2), dev, "cfg3train")
+        line["cfg1btrain"] = secondary_train(min(args.steps, 10), min(args.warmup, 3), dev, "cfg1btrain")
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, min(args.cpu_tokens, w.tokens)) if args.workload != "cfg4" else \
             cpu_baseline(w, w.tokens)

@@ -275,8 +275,8 @@ int attnres_route_bwd_add(const void* const* sources, int num_sources, int64_t n
  * query * gain (bf16, hidden values) to qfold, so that
  *   dL/dsource_s = w_s grad_out + c1_s qfold + c2_s source_s.
  * grad_query / grad_gain and the workspace as attnres_route_bwd.  Kernels
- * exist for bf16 sources, grad_out and parameters with hidden 3072 (2..8
- * sources) or 4096 (2..9 sources); other calls return
+ * exist for bf16 sources, grad_out and parameters with hidden 512, 1024 or
+ * 3072 (2..8 sources) or 4096 (2..9 sources); other calls return
  * ATTNRES_ERR_UNSUPPORTED and write nothing.
  *
  * Replaces, with attnres_route_bwd_gather, autograd's summation of a
@@ -298,7 +298,7 @@ int attnres_route_bwd_defer(const void* const* sources, int num_sources, int64_t
  *   out = addend + sum_j (w_j grad_outs[j] + c1_j qfolds[j]) + (sum_j c2_j) x
  * with (w_j, c1_j, c2_j) = coefs[j][t*coef_lds[j] + 0..2]: for a call over
  * S_j sources that read x as source s_j, coefs[j] = its coef + 4*s_j and
- * coef_lds[j] = 4*(S_j - 1).  bf16 rows of hidden 3072 or 4096 (x rows x_ld
+ * coef_lds[j] = 4*(S_j - 1).  bf16 rows of hidden 512, 1024, 3072 or 4096 (x rows x_ld
  * apart, grad_outs[j] rows grad_out_ld, out and addend rows out_ld); addend
  * may be NULL or out (in place).  fp32 sums rounded once per group of up to
  * 48 terms (more terms: later groups add to out).  Runs the one-block
@@ -328,8 +328,9 @@ int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int6
  * part_in / csum_in (the arrays or entries) may be NULL for a block's first
  * segment, or equal part_out / csum_out (in place).  More than 48 terms are
  * launched in groups, the later ones continuing from part_out / csum_out
- * (csum_out[last] is then needed as scratch).  bf16 rows of hidden 3072 or
- * 4096, up to 8 blocks; other calls return ATTNRES_ERR_UNSUPPORTED.
+ * (csum_out[last] is then needed as scratch).  bf16 rows of hidden 512,
+ * 1024, 3072 or 4096, up to 8 blocks; other calls return
+ * ATTNRES_ERR_UNSUPPORTED.
  *
  * See attnres_route_bwd_defer for the reference code this replaces.
  */

@@ -113,8 +113,8 @@ struct DeviceState {
   KernelSlot bwd_mq[kBwdFuncs];  // batched-query backward: (source, grad_out) dtypes x S x V
   KernelSlot bwd_dqw[4];         // source dtype x V
   KernelSlot bwd_mqg[2 * 9];     // batched-query backward on the matrix cores: query groups x S
-  KernelSlot bwd_defer[2 * 10];  // row-per-wave backward with deferred block gradients: row KiB x S
-  KernelSlot gather_seg[2 * ATTNRES_SEG_MAX_BLOCKS];  // segment sums: row KiB x blocks
+  KernelSlot bwd_defer[4 * 10];  // row-per-wave backward with deferred block gradients: row width x S
+  KernelSlot gather_seg[4 * ATTNRES_SEG_MAX_BLOCKS];  // segment sums: row width x blocks
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -423,15 +423,19 @@ int get_bwd_stream(DeviceState& st, int nch, int s, hipFunction_t* f, bool add =
 // S >= 2) and the sums of the blocks' terms
 // (attnres_route_bwd_gather_seg_c<NCH>_b<NB>).
 constexpr int kDeferPart = 10;
+// The row widths of the deferred path: hidden 3072, 4096, 1024 and 512 (rows of
+// 6, 8, 2 and 1 KiB), the reference's 3B, 8B, 1B and proxy models.
+bool defer_hidden(int hidden) { return hidden == 3072 || hidden == 4096 || hidden == 1024 || hidden == 512; }
+int defer_width(int nch) { return nch == 6 ? 0 : nch == 8 ? 1 : nch == 2 ? 2 : 3; }
 int get_bwd_defer(DeviceState& st, int nch, int s, hipFunction_t* f) {
   char name[96];
   snprintf(name, sizeof(name), "attnres_route_bwd_stream_c%d_s%d_defer", nch, s);
-  return slot_function(st, st.bwd_defer[(nch == 8 ? 10 : 0) + s], kDeferPart, name, f);
+  return slot_function(st, st.bwd_defer[defer_width(nch) * 10 + s], kDeferPart, name, f);
 }
 int get_gather_seg(DeviceState& st, int nch, int nb, hipFunction_t* f) {
   char name[96];
   snprintf(name, sizeof(name), "attnres_route_bwd_gather_seg_c%d_b%d", nch, nb);
-  return slot_function(st, st.gather_seg[(nch == 8 ? ATTNRES_SEG_MAX_BLOCKS : 0) + nb - 1], kDeferPart, name, f);
+  return slot_function(st, st.gather_seg[defer_width(nch) * ATTNRES_SEG_MAX_BLOCKS + nb - 1], kDeferPart, name, f);
 }
 // Row parts per token of the segment kernel (each wave takes one) and the
 // waves per SIMD each instance is compiled for (workgroups per CU), as the
@@ -459,9 +463,9 @@ int bwd_defer_nch(int src_dtype, int grad_out_dtype, int param_dtype, int num_so
                   int64_t num_tokens) {
   if (src_dtype != ATTNRES_DTYPE_BF16 || grad_out_dtype != ATTNRES_DTYPE_BF16 || param_dtype != ATTNRES_DTYPE_BF16)
     return 0;
-  if (hidden != 3072 && hidden != 4096) return 0;
+  if (!defer_hidden(hidden)) return 0;
   const int nch = hidden / 512;
-  if (num_sources < 2 || num_sources > (nch == 6 ? 8 : 9)) return 0;
+  if (num_sources < 2 || num_sources > (nch == 8 ? 9 : 8)) return 0;
   if (num_tokens >= (int64_t)1 << 31) return 0;
   return nch;
 }
@@ -1363,8 +1367,8 @@ int attnres_route_bwd_defer(const void* const* sources, int num_sources, int64_t
   const int nch = bwd_defer_nch(src_dtype, grad_out_dtype, param_dtype, num_sources, hidden, num_tokens);
   if (nch == 0)
     return fail(ATTNRES_ERR_UNSUPPORTED,
-                "deferred backward: no kernel for %d sources, hidden=%d and these dtypes (bf16, hidden 3072 with "
-                "2..8 sources or 4096 with 2..9)",
+                "deferred backward: no kernel for %d sources, hidden=%d and these dtypes (bf16, hidden 512, 1024 "
+                "or 3072 with 2..8 sources, 4096 with 2..9)",
                 num_sources, hidden);
   if (src_ld < hidden || grad_ld < hidden || grad_out_ld < hidden)
     return fail(ATTNRES_ERR_ARG, "a row stride is smaller than hidden=%d", hidden);
@@ -1393,7 +1397,9 @@ int attnres_route_bwd_defer(const void* const* sources, int num_sources, int64_t
   grads[num_sources - 1] = grad_partial;
   adds[num_sources - 1] = grad_partial_addend;
   const int64_t need_wg = (num_tokens + kBwdStreamWaves - 1) / kBwdStreamWaves;
-  const int64_t cap = (int64_t)st->num_cus * (tuning().bwd_per_cu > 0 ? tuning().bwd_per_cu : 1);
+  // rows of 1-2 KiB: more waves per CU to keep the memory system busy
+  const int per_cu = tuning().bwd_per_cu > 0 ? tuning().bwd_per_cu : nch <= 2 ? kBwdMaxPerCu : 1;
+  const int64_t cap = (int64_t)st->num_cus * per_cu;
   const int grid = (int)(need_wg < cap ? need_wg : cap);
   return route_bwd_finish(f, grid, 64 * kBwdStreamWaves, lds, *st, hidden / 8, sources, num_sources, num_tokens,
                           hidden, src_ld, query, gain, param_dtype, eps, grad_out, grad_out_dtype, grad_out_ld,
@@ -1438,8 +1444,9 @@ int attnres_route_bwd_gather(const void* x, int64_t num_tokens, int hidden, int6
   if (num_terms > 0 && (grad_outs == nullptr || coefs == nullptr || coef_lds == nullptr || qfolds == nullptr))
     return fail(ATTNRES_ERR_ARG, "term arrays are NULL");
   if (!valid_dtype(dtype)) return fail(ATTNRES_ERR_ARG, "unknown dtype code");
-  if (dtype != ATTNRES_DTYPE_BF16 || (hidden != 3072 && hidden != 4096))
-    return fail(ATTNRES_ERR_UNSUPPORTED, "gather: bf16 rows of hidden 3072 or 4096 only (hidden=%d)", hidden);
+  if (dtype != ATTNRES_DTYPE_BF16 || !defer_hidden(hidden))
+    return fail(ATTNRES_ERR_UNSUPPORTED, "gather: bf16 rows of hidden 512, 1024, 3072 or 4096 only (hidden=%d)",
+                hidden);
   if (x_ld < hidden || out_ld < hidden || (num_terms > 0 && grad_out_ld < hidden))
     return fail(ATTNRES_ERR_ARG, "a row stride is smaller than hidden=%d", hidden);
   if ((x_ld * 2) % 16 != 0 || (out_ld * 2) % 16 != 0 || (num_terms > 0 && (grad_out_ld * 2) % 16 != 0))
@@ -1503,8 +1510,9 @@ int attnres_route_bwd_gather_seg(int num_blocks, int64_t num_tokens, int hidden,
     return fail(ATTNRES_ERR_ARG, "segment sum: a required pointer array or x is NULL");
   if (num_tokens < 0 || hidden <= 0) return fail(ATTNRES_ERR_ARG, "bad num_tokens/hidden");
   if (!valid_dtype(dtype)) return fail(ATTNRES_ERR_ARG, "unknown dtype code");
-  if (dtype != ATTNRES_DTYPE_BF16 || (hidden != 3072 && hidden != 4096))
-    return fail(ATTNRES_ERR_UNSUPPORTED, "segment sum: bf16 rows of hidden 3072 or 4096 only (hidden=%d)", hidden);
+  if (dtype != ATTNRES_DTYPE_BF16 || !defer_hidden(hidden))
+    return fail(ATTNRES_ERR_UNSUPPORTED,
+                "segment sum: bf16 rows of hidden 512, 1024, 3072 or 4096 only (hidden=%d)", hidden);
   if (x_ld < hidden || out_ld < hidden || grad_out_ld < hidden)
     return fail(ATTNRES_ERR_ARG, "a row stride is smaller than hidden=%d", hidden);
   if ((x_ld * 2) % 16 != 0 || (out_ld * 2) % 16 != 0 || (grad_out_ld * 2) % 16 != 0)

@@ -4049,6 +4049,12 @@ BWD_STREAM_ONE_DEFER(8, 6, 0)
 BWD_STREAM_ONE_DEFER(2, 8, 0) BWD_STREAM_ONE_DEFER(3, 8, 0) BWD_STREAM_ONE_DEFER(4, 8, 0)
 BWD_STREAM_ONE_DEFER(5, 8, 0) BWD_STREAM_ONE_DEFER(6, 8, 0) BWD_STREAM_ONE_DEFER(7, 8, 1)
 BWD_STREAM_ONE_DEFER(8, 8, 2) BWD_STREAM_ONE_DEFER(9, 8, 3)
+BWD_STREAM_ONE_DEFER(2, 2, 0) BWD_STREAM_ONE_DEFER(3, 2, 0) BWD_STREAM_ONE_DEFER(4, 2, 0)
+BWD_STREAM_ONE_DEFER(5, 2, 0) BWD_STREAM_ONE_DEFER(6, 2, 0) BWD_STREAM_ONE_DEFER(7, 2, 0)
+BWD_STREAM_ONE_DEFER(8, 2, 0)
+BWD_STREAM_ONE_DEFER(2, 1, 0) BWD_STREAM_ONE_DEFER(3, 1, 0) BWD_STREAM_ONE_DEFER(4, 1, 0)
+BWD_STREAM_ONE_DEFER(5, 1, 0) BWD_STREAM_ONE_DEFER(6, 1, 0) BWD_STREAM_ONE_DEFER(7, 1, 0)
+BWD_STREAM_ONE_DEFER(8, 1, 0)
 #endif
 
 // Segments of deferred sums (the instances in ATTNRES_SEG_INSTANCES), a wave

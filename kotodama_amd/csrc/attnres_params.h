@@ -139,7 +139,11 @@ typedef struct attnres_gather_term {
   X(6, 1, 3, 4, 2) X(6, 2, 3, 4, 2) X(6, 3, 3, 4, 2) X(6, 4, 3, 4, 2)                                   \
   X(6, 5, 2, 2, 2) X(6, 6, 2, 2, 2) X(6, 7, 2, 2, 2) X(6, 8, 2, 2, 2)                                   \
   X(8, 1, 4, 2, 2) X(8, 2, 4, 2, 2) X(8, 3, 4, 2, 2) X(8, 4, 4, 2, 2)                                   \
-  X(8, 5, 2, 3, 2) X(8, 6, 2, 3, 2) X(8, 7, 2, 3, 2) X(8, 8, 2, 3, 2)
+  X(8, 5, 2, 3, 2) X(8, 6, 2, 3, 2) X(8, 7, 2, 3, 2) X(8, 8, 2, 3, 2)                                   \
+  X(2, 1, 2, 4, 2) X(2, 2, 2, 4, 2) X(2, 3, 2, 4, 2) X(2, 4, 2, 4, 2)                                   \
+  X(2, 5, 2, 2, 2) X(2, 6, 2, 2, 2) X(2, 7, 2, 2, 2) X(2, 8, 2, 2, 2)                                   \
+  X(1, 1, 1, 8, 2) X(1, 2, 1, 8, 2) X(1, 3, 1, 8, 2) X(1, 4, 1, 8, 2)                                   \
+  X(1, 5, 1, 8, 2) X(1, 6, 1, 8, 2) X(1, 7, 1, 8, 2) X(1, 8, 1, 8, 2)
 #endif
 typedef struct attnres_seg_block {
   const void* part_in;   /* (n_tokens, d), row stride out_ld, or NULL */

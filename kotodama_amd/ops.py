@@ -853,7 +853,7 @@ def _route_rows_backward_defer(sources, query, gain, eps, grad_out, grad_add):
     d = p.shape[-1]
     n = p.numel() // d
     q = query.reshape(-1)
-    if p.dtype != torch.bfloat16 or d not in (3072, 4096) or (gain is not None and gain.dtype != q.dtype):
+    if p.dtype != torch.bfloat16 or d not in (512, 1024, 3072, 4096) or (gain is not None and gain.dtype != q.dtype):
         return None  # no deferred kernel (the library decides the rest)
     kq, kg, pcode = _fold_query(q, gain)
     grad_out = grad_out.reshape(n, d).contiguous()
@@ -915,10 +915,11 @@ class _RoutePoint(torch.autograd.Function):
     the gradient of the partial output (that gradient as the kernel's addend),
     which is also the gradient of ``partial`` and of ``delta``: autograd adds
     nothing.  Where the library has a deferred kernel for the call
-    (attnres_route_bwd_defer: bf16, hidden 3072 / 4096) the committed blocks'
+    (attnres_route_bwd_defer: bf16, hidden 512 / 1024 / 3072 / 4096) the committed blocks'
     gradients are not formed here: the call's output gradient and
-    coefficients go to each block's GradSlot, and the block's commit node sums
-    them once (attnres_route_bwd_gather); otherwise each block's gradient is
+    coefficients go to the blocks' GradSlots (their GradSegments), and the
+    commit nodes sum them once (attnres_route_bwd_gather_seg, or
+    attnres_route_bwd_gather per block); otherwise each block's gradient is
     added into its slot's rows (attnres_route_bwd_add)."""
 
     @staticmethod

@@ -88,6 +88,12 @@ def get(name: str) -> Workload:
     if name == "cfg4":
         s = _sched_8b()
         return Workload("cfg4", 4096, 256, 1, torch.bfloat16, s, s.max_sources, s.active_counts, 1.0, 1.0, 0.1, 0.1, 1e-5)
+    if name == "cfg1btrain":
+        # the reference's 1B intermediate model (configs/1b-intermediate.yaml: hidden 1024, 28 layers,
+        # DD-v1 boundaries 0,3,7,12,21,25, sequence 2048, micro-batch 4)
+        s = AttnResSchedule.build(28, boundaries=[0, 3, 7, 12, 21, 25])
+        return Workload("cfg1btrain", 1024, 4, 2048, torch.bfloat16, s, s.max_sources, s.active_counts, 0.5, 4.0, 0.05,
+                        0.1, 1e-5)
     if name == "cfg3train":
         # the 8B model's whole routing loop (32 layers, 8 blocks, 65 points, S up to 9) at config 3's shape
         s = _sched_8b()

@@ -82,7 +82,7 @@ def test_python_constants_match_the_kernel_parameters():
     # every (row KiB, block count) the host can ask for has a compiled segment kernel
     inst = re.findall(r"X\((\d+), (\d+), (\d+), (\d+), (\d+)\)", params)
     have = {(int(a), int(b)) for a, b, *_ in inst}
-    assert have == {(nch, nb) for nch in (6, 8) for nb in range(1, _capi.SEG_MAX_BLOCKS + 1)}
+    assert have == {(nch, nb) for nch in (1, 2, 6, 8) for nb in range(1, _capi.SEG_MAX_BLOCKS + 1)}
     for nch, nb, cpw, depth, wpe in ((int(v) for v in t) for t in inst):
         assert nch % cpw == 0 and depth >= 2 and 1 <= wpe <= 4, (nch, nb)
 
@@ -287,10 +287,12 @@ def test_route_bwd_defer_argument_errors():
         return lib.attnres_route_bwd_defer(srcs, S, n, D, D, sdt, FAKE, None, pdt, 1e-5, FAKE, gdt, D, None, gp, add,
                                            D, coef, qfold, FAKE, 1 << 20, None, None, None)
 
-    # kernels: bf16 everywhere, hidden 3072 (2..8 sources) or 4096 (2..9); n = 0 returns before any HIP call
+    # kernels: bf16 everywhere, hidden 512, 1024 or 3072 (2..8 sources) or 4096 (2..9); n = 0 returns
+    # before any HIP call
     assert call() == _capi.OK
     assert call(S=8) == _capi.OK and call(S=9, D=4096) == _capi.OK
-    assert call(S=9) == _capi.ERR_UNSUPPORTED
+    assert call(S=8, D=1024) == _capi.OK and call(S=8, D=512) == _capi.OK
+    assert call(S=9) == _capi.ERR_UNSUPPORTED and call(S=9, D=1024) == _capi.ERR_UNSUPPORTED
     assert call(S=1) == _capi.ERR_UNSUPPORTED  # no committed source to defer
     assert call(D=2048) == _capi.ERR_UNSUPPORTED
     assert call(sdt=f32) == _capi.ERR_UNSUPPORTED and call(gdt=f32) == _capi.ERR_UNSUPPORTED
@@ -316,6 +318,7 @@ def test_route_bwd_gather_argument_errors():
                                             _capi.pointer_array(qfs), add, out, D, None)
 
     assert call() == _capi.OK and call(nt=0) == _capi.OK and call(D=4096, nt=60) == _capi.OK
+    assert call(D=1024) == _capi.OK and call(D=512) == _capi.OK
     assert call(D=2048) == _capi.ERR_UNSUPPORTED and call(dt=_capi.DTYPE_F32) == _capi.ERR_UNSUPPORTED
     assert call(nt=-1) == _capi.ERR_ARG and call(x=None) == _capi.ERR_ARG and call(out=None) == _capi.ERR_ARG
     assert call(gouts=[FAKE, None]) == _capi.ERR_ARG

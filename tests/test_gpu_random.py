@@ -561,8 +561,8 @@ def _training_points_case(gpu, seed, deferred):
     rng = np.random.default_rng((21000 if deferred else 11000) + seed)
     dtype = torch.bfloat16 if deferred else [torch.bfloat16, torch.float32][int(rng.integers(2))]
     if deferred:
-        D = [3072, 4096][int(rng.integers(2))]
-        K = int(rng.integers(1, 8 if D == 3072 else 9))
+        D = [3072, 4096, 1024, 512][int(rng.integers(4))]
+        K = int(rng.integers(1, 9 if D == 4096 else 8))
     else:
         K = int(rng.integers(0, 9))
         vec = 8 if dtype == torch.bfloat16 else 4
@@ -672,7 +672,7 @@ def _training_points_case(gpu, seed, deferred):
 
 @pytest.mark.parametrize("seed", range(SEEDS or 12))
 def test_random_gather_seg(gpu, seed):
-    # attnres_route_bwd_gather_seg over random segments: width 3072 or 4096, 1..8
+    # attnres_route_bwd_gather_seg over random segments: width 512, 1024, 3072 or 4096, 1..8
     # blocks, 1..48 terms (one launch), ragged row counts, padded row strides,
     # records wider than the blocks summed, running sums and x-coefficient sums
     # present or absent per block and updated in place or into separate
@@ -683,7 +683,7 @@ def test_random_gather_seg(gpu, seed):
     # coefficients split into bf16 hi + lo parts: 2^-18 of each product); the
     # x-coefficient sums within 1e-5 relative; no byte of the padding written
     rng = np.random.default_rng(31000 + seed)
-    d = [3072, 4096][int(rng.integers(2))]
+    d = [3072, 4096, 1024, 512][int(rng.integers(4))]
     nb = int(rng.integers(1, 9))
     P = int(rng.integers(1, 49)) if rng.integers(4) == 0 else int(rng.integers(1, 17))
     n = int(np.exp(rng.uniform(0, np.log(1200))))
