@@ -20,6 +20,11 @@ Also on the JSON line:
 * ``cfg4`` (the 8B decode step), ``cfg2arena`` (the stack-free prefill) and
   ``cfg2train`` / ``cfg3train`` / ``cfg1btrain`` (the 3B, 8B and 1B training
   steps) — as their own ``--workload`` runs report them.
+* ``lmstep_proxy`` / ``lmstep_3b`` — a whole training step of the reference's
+  model (kotodama_amd.lmstep) at the proxy and 3B shapes with the standard
+  residual stream, AttnRes through this package's kernels and AttnRes through
+  the reference's routing ops compiled by inductor, as ``--workload lmstep``
+  reports them.
 * ``cpu_baseline`` — the reference's CPU routing path (oracle/torch_cpu_path:
   the einsum-branch op sequence over the padded buffer, fp32) timed on this
   host on a bounded sample (the whole call schedule over 4096 token rows, at
@@ -41,6 +46,9 @@ steps over one arena: (S+3) rows per point, S+2 right after a commit).
 ``--compile`` for torch.compile with inductor), ``cfg3train`` the same at the
 8B model's schedule (32 layers, 65 points, S up to 9; D=4096, B=4, T=4096) and
 ``cfg1btrain`` at the 1B intermediate model's (D=1024, B=4, T=2048).
+``--workload lmstep --lm proxy|1b|3b|8b`` times a whole training step of the
+reference's Llama-family model (attention, SwiGLU, loss, AdamW; sublayers
+compiled by inductor) with each residual stream of ``--residuals``.
 ``--workload segsum`` times the training step's deferred-gradient segment sums
 (attnres_route_bwd_gather_seg) per block count at the 3B and 8B shapes.
 ``--workload mall`` checks what the 256 MB last-level cache serves of a call's
@@ -82,6 +90,9 @@ WORKLOAD_TEXT = {
     "B=4, T=2048, bf16 model; sublayers x*0.5",
     "cfg3train": "8B training step (train.py:610-614 on llama.py:666-716): forward of the 65-point routing loop "
     "(32 layers / 8 blocks, S up to 9) under autograd + backward, D=4096, B=4, T=4096, bf16 model; sublayers x*0.5",
+    "lmstep": "whole training step of the reference's Llama-family model (configs/model.yaml; forward, CE + z-loss, "
+    "backward, AdamW; bf16) with the standard residual stream, AttnRes through this package's kernels, and AttnRes "
+    "through the reference's routing ops compiled by inductor",
     "segsum": "the training step's deferred-gradient segment sums alone: 8 points' terms into 1..8 blocks, "
     "D=3072 x 32768 rows and D=4096 x 16384 rows, bf16",
 }
@@ -103,6 +114,11 @@ def parse_args():
     ap.add_argument("--compile-breaks", action="store_true",
                     help="cfg2train / cfg3train: torch.compile(backend='inductor') without fullgraph, the routing "
                          "points run eagerly as graph breaks (kotodama_amd.engine.defer_under_compile)")
+    ap.add_argument("--lm", default="proxy", choices=("proxy", "1b", "3b", "8b"),
+                    help="lmstep: the model (configs/model.yaml) and its benchmark batch")
+    ap.add_argument("--residuals", default="standard,attnres,torch",
+                    help="lmstep: comma-separated residual streams to time (standard, attnres, torch)")
+    ap.add_argument("--eager-sublayers", action="store_true", help="lmstep: run the dense sublayers uncompiled")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", action="store_true",
                     help="cfg2: measure the sweep alone, without the other workloads' records (for profiling)")
@@ -852,6 +868,120 @@ def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool, name
             "warmup_s": round(first_s, 2)}
 
 
+def reference_routing_loop():
+    """A comparator for the whole-step timing, not part of the package: the
+    reference's training caller (llama.py:666-716) with its own routing ops
+    (``_route_static``'s PyTorch path, llama.py:630-644), compiled by inductor
+    for the fixed max_S shape as the reference intends (llama.py:615-616).  The
+    padded source list is stacked inside the compiled function, so inductor may
+    fuse the stack into the routing reductions as a whole-model compile would;
+    the commits' clones (llama.py:701-702) are left out for the same reason
+    (a compiled graph drops them); the partial's adds stay eager adds."""
+    import torch
+
+    def route(srcs, query, gain, eps: float, mask):
+        buf = torch.stack(srcs, 0)
+        rsqrt = torch.rsqrt(buf.pow(2).mean(-1) + eps)
+        logits = (buf * (query * gain)).sum(-1) * rsqrt
+        logits = logits.masked_fill(~mask.view(-1, 1, 1), float("-inf"))
+        return (torch.softmax(logits, dim=0).unsqueeze(-1) * buf).sum(0)
+
+    croute = torch.compile(route, dynamic=False)
+
+    def loop(model, embed):
+        masks, max_s, bset = model._attn_res_masks, model._attn_res_max_sources, model._attn_res_boundary_set
+        committed: list = []
+        zero = torch.zeros_like(embed)
+
+        def point(j, partial, query, norm):
+            srcs = committed + [partial] + [zero] * (max_s - len(committed) - 1)
+            return croute(srcs, query, norm.weight, norm.eps, masks[j])
+
+        partial = embed
+        for i, layer in enumerate(model.layers):
+            h = point(2 * i, partial, layer.attn_res_query, layer.attn_res_norm)
+            if i in bset:
+                committed.append(partial)
+                partial = zero
+            partial = partial + layer.attn(layer.attn_norm(h), model.rope_cos, model.rope_sin, None)
+            h = point(2 * i + 1, partial, layer.mlp_res_query, layer.mlp_res_norm)
+            partial = partial + layer.ffn(layer.ffn_norm(h))
+        return point(2 * len(model.layers), partial, model.final_res_query, model.final_res_norm)
+
+    return loop
+
+
+def bench_lmstep(steps: int, warmup: int, dev, lm: str, residuals, compiled: bool = True) -> dict:
+    """lmstep: one training step of the reference's Llama-family model
+    (kotodama_amd.lmstep: forward, cross-entropy + z-loss, backward, AdamW step;
+    train.py:610-640) with each residual stream in ``residuals``: "standard"
+    (x + f(norm(x))), "attnres" (this package's routing kernels) and "torch"
+    (the reference's routing ops compiled by inductor, :func:`reference_routing_loop`).
+    The dense sublayers are the same torch functions in every variant, compiled
+    by inductor unless ``compiled`` is false.  HIP events split each step into
+    forward (with the loss), backward and optimizer step."""
+    import torch
+
+    from kotodama_amd import lmstep
+
+    c = lmstep.PRESETS[lm]
+    torch.backends.cuda.enable_math_sdp(False)  # SDPA runs a fused kernel or raises
+    torch._dynamo.reset()
+    lmstep.compile_sublayers(compiled)
+    ids, labels = lmstep.make_batch(c, dev)
+    loops = {"standard": "standard", "attnres": "attnres", "torch": reference_routing_loop()}
+    out = {"model": c.name, "hidden": c.hidden_size, "layers": c.num_layers, "batch": c.batch, "seq": c.seq,
+           "vocab": c.vocab_size, "routing_points": 2 * c.num_layers + 1, "sublayers_compiled": compiled}
+    for name in residuals:
+        residual = loops[name]
+        model = lmstep.LanguageModel(c, dev, seed=3)  # every variant starts from the same weights
+        opt = lmstep.optimizer(model)
+        out.setdefault("params_M", round(sum(p.numel() for p in model.parameters()) / 1e6, 1))
+        out.setdefault("blocks", len(model._attn_res_boundary_set))
+
+        def step(events):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            opt.zero_grad(set_to_none=True)
+            e[0].record()
+            loss = model(ids, labels, residual)
+            e[1].record()
+            loss.backward()
+            e[2].record()
+            opt.step()
+            e[3].record()
+            events.append(e)
+            return loss
+
+        t_first = time.perf_counter()
+        for i in range(warmup):
+            print(f"lmstep {lm} {name}: warm-up step {i}", flush=True)
+            step([])
+            torch.cuda.synchronize()
+        first_s = time.perf_counter() - t_first
+        torch.cuda.reset_peak_memory_stats(dev)
+        events: list = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = step(events)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        split = [statistics.mean(e[k].elapsed_time(e[k + 1]) for e in events) for k in range(3)]
+        out[name] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(c.tokens / (ms * 1e-3), 1),
+                     "fwd_ms": round(split[0], 3), "bwd_ms": round(split[1], 3), "opt_ms": round(split[2], 3),
+                     "loss": round(float(loss), 4),
+                     "peak_allocated_GiB": round(torch.cuda.max_memory_allocated(dev) / 2**30, 2),
+                     "warmup_s": round(first_s, 1)}
+        print(f"lmstep {lm} {name}: {json.dumps(out[name])}", flush=True)
+        del model, opt
+        torch.cuda.empty_cache()
+    base = out.get("standard", {}).get("ms_per_step")
+    if base:
+        for name in residuals:
+            if name != "standard":
+                out[name]["overhead_vs_standard"] = round(out[name]["ms_per_step"] / base - 1.0, 4)
+    return out
+
+
 def secondary_sweep(name: str, steps: int, warmup: int, dev) -> dict:
     """Another sweep workload (cfg3: the 8B prefill shape, S=9, 8 calls; cfg5: the 3B data-driven
     blocks, 57 calls) measured in the same run as cfg2, with its own roofline block."""
@@ -999,6 +1129,17 @@ def main() -> int:
                                                                       if args.compile_breaks else False)},
             "routing_GB/s_over_step": round(gbs, 2), "hbm_frac_routing_bytes": round(gbs / HBM_PEAK_GBS, 4),
             **rec,
+        }), flush=True)
+        return 0
+    if args.workload == "lmstep":
+        rec = bench_lmstep(args.steps, args.warmup, dev, args.lm, args.residuals.split(","), not args.eager_sublayers)
+        head = rec.get("attnres") or next(rec[k] for k in args.residuals.split(","))
+        print(json.dumps({
+            "metric": "whole training step tokens/s with AttnRes routing (and the standard residual stream beside it)",
+            "value": head["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random token ids, random-init weights)",
+            "config": {"workload": WORKLOAD_TEXT["lmstep"], "lm": args.lm}, **rec,
         }), flush=True)
         return 0
     if args.workload == "segsum":
@@ -1176,6 +1317,13 @@ def main() -> int:
         line["cfg2train"] = secondary_train(min(args.steps, 5), min(args.warmup, 2), dev)
         line["cfg3train"] = secondary_train(min(args.steps, 5), min(args.warmup, 2), dev, "cfg3train")
         line["cfg1btrain"] = secondary_train(min(args.steps, 10), min(args.warmup, 3), dev, "cfg1btrain")
+        # whole training steps of the reference's model: AttnRes against the standard residual stream
+        line["lmstep_proxy"] = {"workload": WORKLOAD_TEXT["lmstep"] + ": proxy model (D=512, 28 layers, B=4, T=2048)",
+                                **bench_lmstep(min(args.steps, 10), min(args.warmup, 3), dev, "proxy",
+                                               ("standard", "attnres", "torch"))}
+        line["lmstep_3b"] = {"workload": WORKLOAD_TEXT["lmstep"] + ": 3B model (D=3072, 28 layers, B=4, T=4096)",
+                             **bench_lmstep(min(args.steps, 5), min(args.warmup, 2), dev, "3b",
+                                            ("standard", "attnres", "torch"))}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, min(args.cpu_tokens, w.tokens)) if args.workload != "cfg4" else \
             cpu_baseline(w, w.tokens)
