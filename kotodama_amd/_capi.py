@@ -426,10 +426,7 @@ def check(fn: str, code: int) -> None:
 
 
 def pointer_array(ptrs: list[int]):
-    arr = (_c_vp * max(1, len(ptrs)))()
-    for i, p in enumerate(ptrs):
-        arr[i] = p
-    return arr
+    return (_c_vp * max(1, len(ptrs)))(*ptrs)
 
 
 def int64_array(vals: list[int]):

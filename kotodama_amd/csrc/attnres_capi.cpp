@@ -128,7 +128,7 @@ std::atomic<int> g_policy{ATTNRES_POLICY_AUTO};
 // ATTNRES_STREAM_MIN_TOKENS choose when the row-per-wave streaming kernels
 // run, ATTNRES_GRID_MULT scales the resident-workgroup grid,
 // ATTNRES_STREAM_PER_CU sets the streaming kernels' workgroups per CU (0: the
-// occupancy limit), ATTNRES_BWD_PER_CU caps the backward kernels' (at most
+// occupancy limit; by default by row width), ATTNRES_BWD_PER_CU caps the backward kernels' (at most
 // kBwdMaxPerCu, the bound its workspace size assumes), ATTNRES_QG=0 turns off
 // the batched-query kernel, ATTNRES_MQG=0 the matrix-core batched backward,
 // ATTNRES_OUT_BATCH caps the streaming kernels' staged output rows per wave
@@ -143,7 +143,7 @@ struct Tuning {
   int stream = -1;  // -1: by size, 0: never, 1: whenever the shape allows
   int64_t stream_min_tokens = 2048;
   double grid_mult = 1.0;
-  double stream_per_cu = 1.0;  // workgroups per CU of the streaming kernels
+  double stream_per_cu = -1.0;  // workgroups per CU of the streaming kernels (< 0: by row width)
   int bwd_per_cu = 0;          // > 0: resident workgroups per CU of the routing backward
   int mqg = 1;                 // 0: the batched-query backward never uses the matrix-core kernel
   int out_batch = 0;           // > 0: at most this many staged output rows per streaming wave (1: none)
@@ -636,6 +636,22 @@ int stream_waves_for(int row_kib, bool fused) {
   return !fused && row_kib >= 8 ? 3 : kStreamWaves;
 }
 
+// Workgroups per CU of a streaming launch (0: the occupancy limit).  One
+// 4-wave workgroup per CU is best from 6 KiB rows (above), but a wave of a
+// narrow row keeps too few bytes in flight: bf16 routing steps (S = 2 and 8,
+// 8192-131072 rows) ran at 2.3-2.7 TB/s with one workgroup per CU at 1 KiB
+// rows and 5.0-6.6 TB/s with eight; at 2 KiB rows 3.8-4.3 TB/s against
+// 5.3-6.3 with two to four (four best for the fused steps at 8192-32768
+// rows, two for the others); at 3-4 KiB rows the fused steps gained 5-35%
+// with two, while the routing calls that stage their output rows lost 1-6%.
+double stream_per_cu_for(int row_kib, bool fused) {
+  if (tuning().stream_per_cu >= 0.0) return tuning().stream_per_cu;
+  if (row_kib <= 1) return 8.0;
+  if (row_kib == 2) return fused ? 4.0 : 2.0;
+  if (row_kib <= 4) return fused ? 2.0 : 1.0;
+  return 1.0;
+}
+
 RouteChoice choose_route(int num_sources, int64_t num_tokens, int hidden, int src_dtype, int param_dtype,
                          int num_queries, int num_cus, bool stream_ok, bool fused) {
   RouteChoice ch;
@@ -849,12 +865,15 @@ int route_launch(const void* const* sources, int num_sources, int64_t num_tokens
   P.out_batch = out_batch;
   P.eps = eps;
   P.inv_d = 1.0f / (float)hidden;
-  // The streaming kernels run one 4-wave workgroup per CU: at the occupancy
-  // limit (up to four per CU) four times the requests are in flight and the
-  // same traffic measured 4-6% slower.
+  // The streaming kernels run one 4-wave workgroup per CU from 6 KiB rows: at
+  // the occupancy limit (up to four per CU) four times the requests are in
+  // flight and the same traffic measured 4-6% slower; narrower rows run more
+  // (stream_per_cu_for).
   int grid = grid_for(work_units, st->num_cus, bpc);
-  if (ch.stream && tuning().stream_per_cu > 0.0) {
-    int64_t g = (int64_t)(st->num_cus * (tuning().stream_per_cu < bpc ? tuning().stream_per_cu : (double)bpc));
+  const double per_cu =
+      ch.stream ? stream_per_cu_for(ch.nch, ch.variant == kStreamFused || ch.variant == kStreamFusedTable) : 0.0;
+  if (per_cu > 0.0) {
+    int64_t g = (int64_t)(st->num_cus * (per_cu < bpc ? per_cu : (double)bpc));
     if (g < 1) g = 1;
     if (g > work_units) g = work_units;
     grid = (int)g;

@@ -303,5 +303,8 @@ def make_batch(c: LMConfig, device, seed: int = 1) -> tuple[Tensor, Tensor]:
 
 def optimizer(model: nn.Module) -> torch.optim.Optimizer:
     """AdamW with the reference's AdamW settings (configs/proxy-benchmark.yaml: lr 6e-4,
-    betas 0.9/0.95, weight decay 0.1), over every parameter."""
-    return torch.optim.AdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1, foreach=True)
+    betas 0.9/0.95, weight decay 0.1), over every parameter; the fused
+    implementation (a few launches for all parameters) on the GPU."""
+    fused = next(model.parameters()).is_cuda
+    return torch.optim.AdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1,
+                             foreach=None if fused else True, fused=fused or None)

@@ -55,20 +55,35 @@ def dtype_code(dt: torch.dtype) -> int:
 
 
 def _require_device(*tensors: Optional[Tensor]) -> torch.device:
-    dev = None
+    first = None
+    idx = -1
     for t in tensors:
         if t is None:
             continue
-        if t.device.type != "cuda":
+        if not t.is_cuda:
             raise RuntimeError(
                 f"attnres_hip runs on ROCm device tensors only (got a {t.device.type} tensor); there is no CPU path"
             )
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise RuntimeError(f"attnres_hip: tensors on different devices ({dev} vs {t.device})")
-    assert dev is not None
-    return dev
+        if first is None:
+            first, idx = t, t.get_device()
+        elif t.get_device() != idx:
+            raise RuntimeError(f"attnres_hip: tensors on different devices ({first.device} vs {t.device})")
+    assert first is not None
+    return first.device
+
+
+_WS_BYTES: dict = {}
+
+
+def _bwd_workspace(device: torch.device, n: int, d: int) -> Tensor:
+    """The routing backward's workspace for ``n`` rows of ``d`` on ``device``
+    (the current device; its size, which depends on the device's CU count,
+    asked of the library once per shape)."""
+    key = (device.index, n, d)
+    nbytes = _WS_BYTES.get(key)
+    if nbytes is None:
+        nbytes = _WS_BYTES[key] = _capi.route_bwd_workspace_size(n, d)
+    return torch.empty(max(1, nbytes // 4), device=device, dtype=torch.float32)
 
 
 def _no_grad_needed(*tensors: Optional[Tensor]) -> None:
@@ -322,7 +337,7 @@ def _launch_route_bwd(
     if grad_lse is not None:
         grad_lse = grad_lse.reshape(n).to(torch.float32).contiguous()
     with _DeviceStream(device) as stream:
-        ws = torch.empty(max(1, _capi.route_bwd_workspace_size(n, d) // 4), device=device, dtype=torch.float32)
+        ws = _bwd_workspace(device, n, d)
         head = (_capi.pointer_array(ptrs), len(ptrs), n, d, d, dtype_code(src_dtype), kq.data_ptr(),
                 kg.data_ptr() if kg is not None else None, pcode, float(eps), grad_out.data_ptr(),
                 dtype_code(grad_out.dtype), d, grad_lse.data_ptr() if grad_lse is not None else None,
@@ -863,7 +878,7 @@ def _route_rows_backward_defer(sources, query, gain, eps, grad_out, grad_add):
     dq = torch.empty(d, device=device, dtype=kq.dtype)
     dg = torch.empty(d, device=device, dtype=kg.dtype) if kg is not None else None
     with _DeviceStream(device) as stream:
-        ws = torch.empty(max(1, _capi.route_bwd_workspace_size(n, d) // 4), device=device, dtype=torch.float32)
+        ws = _bwd_workspace(device, n, d)
         code = _capi.route_bwd_defer(
             _capi.pointer_array([t.data_ptr() for t in sources]), len(sources), n, d, d, dtype_code(p.dtype),
             kq.data_ptr(), kg.data_ptr() if kg is not None else None, pcode, float(eps), grad_out.data_ptr(),
@@ -1149,7 +1164,7 @@ def merge_bwd(
     if n == 0:
         return gp, gq, gi, gl
     with _DeviceStream(device) as stream:
-        ws = torch.empty(max(1, _capi.route_bwd_workspace_size(n, d) // 4), device=device, dtype=torch.float32)
+        ws = _bwd_workspace(device, n, d)
         _capi.merge_bwd(
             partial.data_ptr(),
             n,
