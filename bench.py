@@ -1320,7 +1320,13 @@ def main() -> int:
         # whole training steps of the reference's model: AttnRes against the standard residual stream
         line["lmstep_proxy"] = {"workload": WORKLOAD_TEXT["lmstep"] + ": proxy model (D=512, 28 layers, B=4, T=2048)",
                                 **bench_lmstep(min(args.steps, 10), min(args.warmup, 3), dev, "proxy",
-                                               ("standard", "attnres", "torch"))}
+                                               ("standard", "attnres", "torch")),
+                                # the reference's published figures for this comparison (another GPU, another
+                                # variant): docs/attnres-performance-brief.md:53-59
+                                "reference_published": {"standard_tokens_per_s": 256000, "attnres_tokens_per_s": 117000,
+                                                        "overhead": 0.54, "hardware": "1x B200",
+                                                        "variant": "once-per-layer routing (29 calls), whole model "
+                                                                   "under torch.compile"}}
         line["lmstep_3b"] = {"workload": WORKLOAD_TEXT["lmstep"] + ": 3B model (D=3072, 28 layers, B=4, T=4096)",
                              **bench_lmstep(min(args.steps, 5), min(args.warmup, 2), dev, "3b",
                                             ("standard", "attnres", "torch"))}
