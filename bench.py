@@ -49,6 +49,7 @@ steps over one arena: (S+3) rows per point, S+2 right after a commit).
 ``--workload lmstep --lm proxy|1b|3b|8b`` times a whole training step of the
 reference's Llama-family model (attention, SwiGLU, loss, AdamW; sublayers
 compiled by inductor) with each residual stream of ``--residuals``.
+``--workload narrow`` times routing steps and calls at hidden 512 / 1024.
 ``--workload segsum`` times the training step's deferred-gradient segment sums
 (attnres_route_bwd_gather_seg) per block count at the 3B and 8B shapes.
 ``--workload mall`` checks what the 256 MB last-level cache serves of a call's
@@ -93,6 +94,8 @@ WORKLOAD_TEXT = {
     "lmstep": "whole training step of the reference's Llama-family model (configs/model.yaml; forward, CE + z-loss, "
     "backward, AdamW; bf16) with the standard residual stream, AttnRes through this package's kernels, and AttnRes "
     "through the reference's routing ops compiled by inductor",
+    "narrow": "routing steps and calls at hidden 512 / 1024 (the proxy and 1B models), S = 2 and 8, 8192-131072 "
+    "rows, bf16",
     "segsum": "the training step's deferred-gradient segment sums alone: 8 points' terms into 1..8 blocks, "
     "D=3072 x 32768 rows and D=4096 x 16384 rows, bf16",
 }
@@ -868,6 +871,47 @@ def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool, name
             "warmup_s": round(first_s, 2)}
 
 
+def bench_narrow(steps: int, warmup: int, dev) -> dict:
+    """narrow: single training-path routing steps (attnres_route_step, the fused
+    forward of a routing point: S - 1 committed blocks, the partial and the
+    sublayer output read, the routed row and the updated partial written; (S+3)
+    rows) and routing calls over S sources ((S+1) rows) at the narrow widths of
+    the proxy and 1B models (hidden 512 / 1024, bf16), S = 2 and 8, 8192-131072
+    rows: HIP events over ``steps`` back-to-back calls per case."""
+    import torch
+
+    from kotodama_amd import ops
+
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(21)
+    with torch.no_grad():
+        for d in (512, 1024):
+            for n in (8192, 32768, 131072):
+                for S in (2, 8):
+                    com = [torch.randn((n, d), generator=g, device=dev).to(torch.bfloat16) for _ in range(S - 1)]
+                    part = torch.randn((n, d), generator=g, device=dev).to(torch.bfloat16)
+                    delta = torch.randn((n, d), generator=g, device=dev).to(torch.bfloat16)
+                    q = (torch.randn(d, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+                    gain = torch.ones(d, device=dev, dtype=torch.bfloat16)
+                    calls = {"step": lambda: ops._route_rows_step(com, part, delta, q, gain, 1e-5, torch.bfloat16),
+                             "route": lambda: ops._route_rows_forward(com + [part], q, gain, 1e-5, torch.bfloat16)}
+                    for kind, fn in calls.items():
+                        for _ in range(warmup):
+                            fn()
+                        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                        for _ in range(steps):
+                            fn()
+                        e1.record()
+                        torch.cuda.synchronize()
+                        us = e0.elapsed_time(e1) * 1e3 / steps
+                        rows = S + 3 if kind == "step" else S + 1
+                        out[f"{kind}_d{d}_n{n}_s{S}"] = {"us": round(us, 2),
+                                                         "GB/s": round(rows * n * d * 2 / (us * 1e-6) / 1e9, 1)}
+                    del com, part, delta
+    return out
+
+
 def reference_routing_loop():
     """A comparator for the whole-step timing, not part of the package: the
     reference's training caller (llama.py:666-716) with its own routing ops
@@ -1141,6 +1185,10 @@ def main() -> int:
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random token ids, random-init weights)",
             "config": {"workload": WORKLOAD_TEXT["lmstep"], "lm": args.lm}, **rec,
         }), flush=True)
+        return 0
+    if args.workload == "narrow":
+        print(json.dumps({"workload": WORKLOAD_TEXT["narrow"], "steps": args.steps, "warmup": args.warmup,
+                          **bench_narrow(args.steps, args.warmup, dev)}), flush=True)
         return 0
     if args.workload == "segsum":
         print(json.dumps({"workload": WORKLOAD_TEXT["segsum"], "steps": args.steps, "warmup": args.warmup,
