@@ -167,20 +167,20 @@ class _PreNorm(_Norm):
         return x
 
 
-def _linear(n_in: int, n_out: int, device, dtype) -> nn.Parameter:
-    return nn.Parameter(torch.empty((n_out, n_in), device=device, dtype=dtype).normal_(0.0, 0.02))
+def _linear(n_in: int, n_out: int, device, dtype, gen: torch.Generator) -> nn.Parameter:
+    return nn.Parameter(torch.empty((n_out, n_in), device=device, dtype=dtype).normal_(0.0, 0.02, generator=gen))
 
 
 class _Attention(nn.Module):
-    def __init__(self, c: LMConfig, pre_norm: _PreNorm, device, dtype) -> None:
+    def __init__(self, c: LMConfig, pre_norm: _PreNorm, device, dtype, gen: torch.Generator) -> None:
         super().__init__()
         self.c = c
         object.__setattr__(self, "pre_norm", pre_norm)  # owned (and registered) by the layer
         inner, kv = c.num_attention_heads * c.head_dim, c.num_kv_heads * c.head_dim
-        self.wq = _linear(c.hidden_size, inner, device, dtype)
-        self.wk = _linear(c.hidden_size, kv, device, dtype)
-        self.wv = _linear(c.hidden_size, kv, device, dtype)
-        self.wo = _linear(inner, c.hidden_size, device, dtype)
+        self.wq = _linear(c.hidden_size, inner, device, dtype, gen)
+        self.wk = _linear(c.hidden_size, kv, device, dtype, gen)
+        self.wv = _linear(c.hidden_size, kv, device, dtype, gen)
+        self.wo = _linear(inner, c.hidden_size, device, dtype, gen)
         self.q_norm = _Norm(c.head_dim, c.norm_eps, device, dtype)
         self.k_norm = _Norm(c.head_dim, c.norm_eps, device, dtype)
 
@@ -194,25 +194,25 @@ class _Attention(nn.Module):
 
 
 class _SwiGLU(nn.Module):
-    def __init__(self, c: LMConfig, pre_norm: _PreNorm, device, dtype) -> None:
+    def __init__(self, c: LMConfig, pre_norm: _PreNorm, device, dtype, gen: torch.Generator) -> None:
         super().__init__()
         self.eps = c.norm_eps
         object.__setattr__(self, "pre_norm", pre_norm)  # owned (and registered) by the layer
-        self.wg = _linear(c.hidden_size, c.intermediate_size, device, dtype)
-        self.wu = _linear(c.hidden_size, c.intermediate_size, device, dtype)
-        self.wd = _linear(c.intermediate_size, c.hidden_size, device, dtype)
+        self.wg = _linear(c.hidden_size, c.intermediate_size, device, dtype, gen)
+        self.wu = _linear(c.hidden_size, c.intermediate_size, device, dtype, gen)
+        self.wd = _linear(c.intermediate_size, c.hidden_size, device, dtype, gen)
 
     def forward(self, x: Tensor) -> Tensor:
         return _FN["swiglu"](x, self.pre_norm.weight, self.wg, self.wu, self.wd, self.eps)
 
 
 class _Layer(nn.Module):
-    def __init__(self, c: LMConfig, device, dtype) -> None:
+    def __init__(self, c: LMConfig, device, dtype, gen: torch.Generator) -> None:
         super().__init__()
         self.attn_norm = _PreNorm(c.hidden_size, c.norm_eps, device, dtype)
-        self.attn = _Attention(c, self.attn_norm, device, dtype)
+        self.attn = _Attention(c, self.attn_norm, device, dtype, gen)
         self.ffn_norm = _PreNorm(c.hidden_size, c.norm_eps, device, dtype)
-        self.ffn = _SwiGLU(c, self.ffn_norm, device, dtype)
+        self.ffn = _SwiGLU(c, self.ffn_norm, device, dtype, gen)
         self.attn_res_query = nn.Parameter(torch.zeros(c.hidden_size, device=device, dtype=dtype))
         self.attn_res_norm = _Norm(c.hidden_size, c.norm_eps, device, dtype)
         self.mlp_res_query = nn.Parameter(torch.zeros(c.hidden_size, device=device, dtype=dtype))
@@ -244,11 +244,11 @@ class LanguageModel(nn.Module):
 
     def __init__(self, c: LMConfig, device, dtype=torch.bfloat16, seed: int = 0) -> None:
         super().__init__()
-        torch.manual_seed(seed)
+        gen = torch.Generator(device=device).manual_seed(seed)
         self.config = c
         self.embed = nn.Parameter(torch.empty((c.vocab_size, c.hidden_size), device=device,
-                                              dtype=dtype).normal_(0.0, 0.02))
-        self.layers = nn.ModuleList([_Layer(c, device, dtype) for _ in range(c.num_layers)])
+                                              dtype=dtype).normal_(0.0, 0.02, generator=gen))
+        self.layers = nn.ModuleList([_Layer(c, device, dtype, gen) for _ in range(c.num_layers)])
         self.norm = _FinalNorm(c.hidden_size, c.norm_eps, device, dtype)
         self.final_res_query = nn.Parameter(torch.zeros(c.hidden_size, device=device, dtype=dtype))
         self.final_res_norm = _Norm(c.hidden_size, c.norm_eps, device, dtype)
