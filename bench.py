@@ -88,7 +88,7 @@ WORKLOAD_TEXT = {
     "under autograd + backward, D=3072, B=8, T=4096, bf16 model; sublayers x*0.5 (no GEMMs)",
     "cfg1btrain": "1B intermediate training step (configs/1b-intermediate.yaml on llama.py:666-716): forward of the "
     "57-point routing loop (28 layers, DD-v1 boundaries 0,3,7,12,21,25, S up to 7) under autograd + backward, D=1024, "
-    "B=4, T=2048, bf16 model; sublayers x*0.5",
+    "B=4, T=2048, bf16 model; sublayers x*0.5 (at this size bound by the host's launches: 4.2 ms of kernels per step)",
     "cfg3train": "8B training step (train.py:610-614 on llama.py:666-716): forward of the 65-point routing loop "
     "(32 layers / 8 blocks, S up to 9) under autograd + backward, D=4096, B=4, T=4096, bf16 model; sublayers x*0.5",
     "lmstep": "whole training step of the reference's Llama-family model (configs/model.yaml; forward, CE + z-loss, "
