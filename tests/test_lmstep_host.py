@@ -4,7 +4,8 @@ The routing schedule the model carries must be the reference's (llama.py:545-571
 boundaries from ``attn_res_n_blocks`` or an explicit list, per-point masks and
 source counts), the presets must be configs/model.yaml's shapes, and the standard
 residual stream and the reference caller loop must run (forward, loss, backward)
-on a tiny model.  The AttnRes stream through this package's kernels needs the GPU
+on a tiny model, and bench.py's compiled comparator loop must equal the reference
+loop.  The AttnRes stream through this package's kernels needs the GPU
 (tests/test_gpu_lmstep.py).
 """
 
@@ -112,3 +113,33 @@ def test_pre_norms_run_inside_the_sublayer_functions():
     normed = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + c.norm_eps) * layer.ffn_norm.weight
     want = F.linear(F.silu(F.linear(normed, layer.ffn.wg)) * F.linear(normed, layer.ffn.wu), layer.ffn.wd)
     torch.testing.assert_close(f, want, rtol=1e-12, atol=1e-12)
+
+
+def test_bench_comparator_loop_is_the_reference_loop():
+    # bench.py's comparator (the reference's loop and routing ops, compiled by inductor with the
+    # padded stack inside the compiled function) gives the reference loop's loss and gradients
+    import copy
+    import sys
+    from pathlib import Path
+
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    import bench
+
+    lmstep.compile_sublayers(False)
+    c = lmstep.LMConfig("t", 64, 3, 4, 2, 16, 96, vocab_size=128, attn_res_n_blocks=2, batch=2, seq=16)
+    model = lmstep.LanguageModel(c, "cpu", torch.float64, seed=3)
+    with torch.no_grad():  # routing away from uniform
+        for name, p in model.named_parameters():
+            if "res_query" in name:
+                p.normal_(0.0, 0.3)
+    ids, labels = lmstep.make_batch(c, "cpu", seed=4)
+    other = copy.deepcopy(model)
+    loss = model(ids, labels, bench.reference_routing_loop())
+    loss.backward()
+    ref = other(ids, labels, lambda m, x: workloads.stacked_training_forward(m, x, _route_reference))
+    ref.backward()
+    torch.testing.assert_close(loss, ref, rtol=1e-12, atol=1e-12)
+    for (name, p), q in zip(model.named_parameters(), other.parameters()):
+        assert (p.grad is None) == (q.grad is None), name
+        if p.grad is not None:
+            torch.testing.assert_close(p.grad, q.grad, rtol=1e-9, atol=1e-12, msg=name)
