@@ -19,7 +19,8 @@ Also on the JSON line:
   (2S+1) rows per call, with a ``roofline`` block for the S=8 backward.
 * ``cfg4`` (the 8B decode step), ``cfg2arena`` (the stack-free prefill) and
   ``cfg2train`` / ``cfg3train`` / ``cfg1btrain`` (the 3B, 8B and 1B training
-  steps) — as their own ``--workload`` runs report them.
+  steps) — as their own ``--workload`` runs report them, each also recorded in
+  a HIP graph and replayed (``hip_graph``: the step without its host launches).
 * ``lmstep_proxy`` / ``lmstep_3b`` — a whole training step of the reference's
   model (kotodama_amd.lmstep) at the proxy and 3B shapes with the standard
   residual stream, AttnRes through this package's kernels and AttnRes through
@@ -122,6 +123,8 @@ def parse_args():
     ap.add_argument("--residuals", default="standard,attnres,torch",
                     help="lmstep: comma-separated residual streams to time (standard, attnres, torch)")
     ap.add_argument("--eager-sublayers", action="store_true", help="lmstep: run the dense sublayers uncompiled")
+    ap.add_argument("--graph", action="store_true",
+                    help="cfg2train / cfg3train / cfg1btrain (list, eager): also time the step recorded in a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", action="store_true",
                     help="cfg2: measure the sweep alone, without the other workloads' records (for profiling)")
@@ -793,7 +796,7 @@ def bench_segsum(steps: int, warmup: int, dev) -> dict:
 
 
 def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool, name: str = "cfg2train",
-                breaks: bool = False) -> dict:
+                breaks: bool = False, graph: bool = False) -> dict:
     """cfg2train / cfg3train: the reference's training step on the routing path at the 3B / 8B shape.
 
     A model with the reference's AttnRes attributes (workloads.TrainingModel:
@@ -863,6 +866,30 @@ def bench_train(steps: int, warmup: int, dev, variant: str, compiled: bool, name
         extra = {"path_kernel_bytes": {"fwd": fb, "bwd": bb},
                  "path_kernel_GB/s": {"fwd": round(fb / (fwd_ms * 1e-3) / 1e9, 1),
                                       "bwd": round(bb / (bwd_ms * 1e-3) / 1e9, 1)}}
+    if graph and variant == "list" and not compiled and not breaks:
+        # the same step recorded in a HIP graph (no host synchronisation or memset in it) and replayed
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            model.zero_grad(set_to_none=True)
+            embed.grad = None
+            fwd(model, embed).backward(G)
+        torch.cuda.current_stream().wait_stream(side)
+        model.zero_grad(set_to_none=True)
+        embed.grad = None
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fwd(model, embed).backward(G)
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        torch.cuda.synchronize()
+        gms = (time.perf_counter() - t0) * 1e3 / steps
+        extra["hip_graph"] = {"ms_per_step": round(gms, 4), "tokens_per_s": round(w.tokens / (gms * 1e-3), 1)}
+        del g
     return {"ms_per_step": round(ms, 4), "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
             "routing_kernel_bytes": {"fwd": fwd_rows * row, "bwd": bwd_rows * row},
             "routing_kernel_bytes_per_ms": round((fwd_rows + bwd_rows) * row / ms / 1e6, 1), **extra,
@@ -1107,10 +1134,10 @@ def secondary_arena(steps: int, warmup: int, dev) -> dict:
                          "algorithmic_bytes": dom_bytes, "avg_ms": round(dom_ms, 4)}}
 
 
-def secondary_train(steps: int, warmup: int, dev, name: str = "cfg2train") -> dict:
-    """cfg2train / cfg3train (the 3B / 8B training step on the routing path, stack-free drop-in, eager),
-    measured in the same run."""
-    rec = bench_train(steps, warmup, dev, "list", False, name)
+def secondary_train(steps: int, warmup: int, dev, name: str = "cfg2train", graph: bool = False) -> dict:
+    """cfg2train / cfg3train / cfg1btrain (the 3B / 8B / 1B training step on the routing path, stack-free
+    drop-in, eager; with ``graph`` also recorded in a HIP graph), measured in the same run."""
+    rec = bench_train(steps, warmup, dev, "list", False, name, graph=graph)
     rb = rec["routing_kernel_bytes"]
     gbs = (rb["fwd"] + rb["bwd"]) / (rec["ms_per_step"] * 1e-3) / 1e9
     return {"workload": WORKLOAD_TEXT[name], "variant": "list (forward_attn_res under autograd)",
@@ -1158,7 +1185,8 @@ def main() -> int:
         }), flush=True)
         return 0
     if args.workload in ("cfg2train", "cfg3train", "cfg1btrain"):
-        rec = bench_train(args.steps, args.warmup, dev, args.variant, args.compile, args.workload, args.compile_breaks)
+        rec = bench_train(args.steps, args.warmup, dev, args.variant, args.compile, args.workload, args.compile_breaks,
+                          args.graph)
         ms = rec["ms_per_step"]
         rb = rec["routing_kernel_bytes"]
         gbs = (rb["fwd"] + rb["bwd"]) / (ms * 1e-3) / 1e9
@@ -1362,9 +1390,9 @@ def main() -> int:
         line["cfg2_bwd"] = secondary_backward("cfg2", args.steps, args.warmup, dev)
         line["cfg4"] = secondary_decode(args.steps, args.warmup, dev)
         line["cfg2arena"] = secondary_arena(args.steps, args.warmup, dev)
-        line["cfg2train"] = secondary_train(min(args.steps, 5), min(args.warmup, 2), dev)
-        line["cfg3train"] = secondary_train(min(args.steps, 5), min(args.warmup, 2), dev, "cfg3train")
-        line["cfg1btrain"] = secondary_train(min(args.steps, 10), min(args.warmup, 3), dev, "cfg1btrain")
+        line["cfg2train"] = secondary_train(min(args.steps, 5), min(args.warmup, 2), dev, graph=True)
+        line["cfg3train"] = secondary_train(min(args.steps, 5), min(args.warmup, 2), dev, "cfg3train", graph=True)
+        line["cfg1btrain"] = secondary_train(min(args.steps, 10), min(args.warmup, 3), dev, "cfg1btrain", graph=True)
         # whole training steps of the reference's model: AttnRes against the standard residual stream
         line["lmstep_proxy"] = {"workload": WORKLOAD_TEXT["lmstep"] + ": proxy model (D=512, 28 layers, B=4, T=2048)",
                                 **bench_lmstep(min(args.steps, 10), min(args.warmup, 3), dev, "proxy",
