@@ -1,9 +1,10 @@
 """The training step of the routing path recorded in a HIP graph.
 
 forward_attn_res under autograd plus its backward (the fused routing steps, the
-deferred block gradients with their segment sums, the query-gradient
-reductions; torch's elementwise stand-in sublayers) issues no host
-synchronisation and no memset, so torch.cuda.graph can record the whole step.
+deferred block gradients with their segment sums or, in fp32, the in-place
+block sums, the query-gradient reductions; torch's elementwise stand-in
+sublayers) issues no host synchronisation and no memset, so torch.cuda.graph
+can record the whole step.
 Each replay, with the program's own eager work and synchronisations between the
 replays, must give the eager step's gradients bit for bit (every kernel of the
 step is deterministic).
@@ -27,16 +28,19 @@ def _grads(model, embed):
     return out
 
 
-@pytest.mark.parametrize("name,hidden,seq", [("cfg1btrain", 1024, 256), ("cfg2train", 3072, 128),
-                                             ("cfg1btrain", 512, 384)], ids=["d1024-dd", "d3072-uniform", "d512-dd"])
-def test_captured_training_step_replays_bit_exact(name, hidden, seq):
+@pytest.mark.parametrize("name,hidden,seq,dtype", [
+    ("cfg1btrain", 1024, 256, torch.bfloat16), ("cfg2train", 3072, 128, torch.bfloat16),
+    ("cfg1btrain", 512, 384, torch.bfloat16),
+    ("cfg1btrain", 512, 192, torch.float32),  # fp32: the in-place sums (attnres_route_bwd_add) instead of deferral
+], ids=["d1024-dd", "d3072-uniform", "d512-dd", "d512-fp32"])
+def test_captured_training_step_replays_bit_exact(name, hidden, seq, dtype):
     base = workloads.get("cfg2" if name == "cfg2train" else name)
-    w = dataclasses.replace(base, hidden=hidden, batch=2, seq=seq)
+    w = dataclasses.replace(base, hidden=hidden, batch=2, seq=seq, dtype=dtype)
     model = workloads.TrainingModel(w, DEV, seed=12)
     g = torch.Generator(device=DEV).manual_seed(13)
     embed = torch.randn((w.batch, w.seq, w.hidden), generator=g, device=DEV).to(w.dtype).requires_grad_(True)
     G = torch.randn((w.batch, w.seq, w.hidden), generator=g, device=DEV).to(w.dtype)
-    print(f"graph training {name} D={hidden} T={seq}", flush=True)
+    print(f"graph training {name} D={hidden} T={seq} {dtype}", flush=True)
 
     def step():
         engine.forward_attn_res(model, embed).backward(G)
